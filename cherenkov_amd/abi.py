@@ -1,0 +1,167 @@
+"""ctypes view of the C ABI in include/cherenkov/{types,engine,kernels}.h.
+
+The engine, its kernels and its runner are native (libcherenkov.so); this
+module only loads the library and declares signatures so that tests and
+bench.py can drive it.  Loading fails loudly when the library is missing:
+there is no Python or CPU fallback for any engine call.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+LIB_PATH = PKG / "libcherenkov.so"
+
+u32, u64, f32, f64, i32 = C.c_uint32, C.c_uint64, C.c_float, C.c_double, C.c_int
+P = C.c_void_p
+
+
+class ChkConfig(C.Structure):
+    _fields_ = [
+        ("hidden_size", u32),
+        ("num_hidden_layers", u32),
+        ("full_attention_interval", u32),
+        ("vocab_size", u32),
+        ("num_attention_heads", u32),
+        ("num_key_value_heads", u32),
+        ("head_dim", u32),
+        ("linear_num_key_heads", u32),
+        ("linear_num_value_heads", u32),
+        ("linear_key_head_dim", u32),
+        ("linear_value_head_dim", u32),
+        ("linear_conv_kernel_dim", u32),
+        ("hc_count", u32),
+        ("hc_lowrank", u32),
+        ("num_experts", u32),
+        ("num_experts_per_tok", u32),
+        ("moe_intermediate_size", u32),
+        ("shared_expert_intermediate_size", u32),
+        ("norm_topk_prob", u32),
+        ("indexer_n_heads", u32),
+        ("indexer_head_dim", u32),
+        ("indexer_budget", u32),
+        ("indexer_compress_ratio", u32),
+        ("mtp_num_hidden_layers", u32),
+        ("eos_token_id", u32),
+        ("ple_layer", u32),
+        ("rms_norm_eps", f64),
+        ("partial_rotary_factor", f64),
+        ("rope_theta", f64),
+        ("seed", u64),
+    ]
+
+    def as_dict(self) -> dict:
+        return {k: getattr(self, k) for k, _ in self._fields_}
+
+
+class ChkOptions(C.Structure):
+    _fields_ = [("experts", u32), ("drafts", u32), ("max_t", u32), ("no_eos", u32)]
+
+
+class ChkMemoryStats(C.Structure):
+    _fields_ = [
+        ("dense", u64),
+        ("experts", u64),
+        ("experts_low_bit", u64),
+        ("state", u64),
+        ("kv_cache", u64),
+        ("scratch", u64),
+        ("total", u64),
+    ]
+
+
+def make_config(**kw) -> ChkConfig:
+    c = ChkConfig()
+    for k, v in kw.items():
+        if not hasattr(c, k):
+            raise KeyError(k)
+        setattr(c, k, v)
+    return c
+
+
+# (name, restype, argtypes) of every exported symbol, in header order.
+SIGNATURES = [
+    # engine.h
+    ("chk_last_error", C.c_char_p, []),
+    ("chk_engine_load", i32, [C.POINTER(ChkConfig), C.POINTER(ChkOptions), C.POINTER(P)]),
+    ("chk_engine_free", None, [P]),
+    ("chk_step_rows", i32, [P, C.POINTER(u32), u32, i32, i32, C.POINTER(u32)]),
+    ("chk_step", i32, [P, u32, C.POINTER(u32)]),
+    ("chk_commit", i32, [P, u32]),
+    ("chk_reset", i32, [P]),
+    ("chk_mtp_draft", i32, [P, C.POINTER(u32), u32, u32, C.POINTER(u32), C.POINTER(u32)]),
+    ("chk_mtp_chain", i32, [P, u32, C.POINTER(u32)]),
+    ("chk_prefill_chunk", i32, [P, C.POINTER(u32), u32, C.POINTER(u32), C.POINTER(u32)]),
+    ("chk_logits_row", C.POINTER(f32), [P, u32]),
+    ("chk_mtp_logits_row", C.POINTER(f32), [P, u32]),
+    ("chk_pos", u32, [P]),
+    ("chk_eos_token", u32, [P]),
+    ("chk_max_t", u32, [P]),
+    ("chk_trunk_rows", u32, [P]),
+    ("chk_has_mtp", i32, [P]),
+    ("chk_memory_stats", i32, [P, C.POINTER(ChkMemoryStats)]),
+    ("chk_pool_slots", u32, [P]),
+    ("chk_pool_resident", u32, [P]),
+    ("chk_pool_is_member", i32, [P, u32]),
+    ("chk_pool_acquire", u32, [P, C.POINTER(u32), u32, C.POINTER(u32)]),
+    ("chk_pool_addr", u64, [P, u32]),
+    ("chk_pool_kind", u32, [P, u32]),
+    ("chk_pool_bytes", u64, [P]),
+    ("chk_last_routes", i32, [P, u32, u32, C.POINTER(u32), C.POINTER(f32)]),
+    # kernels.h
+    ("chk_q4_matvec", i32, [P, P, P, u32, u32, P, P, u32, P]),
+    ("chk_moe_block", i32, [P, u32, P, u32, P, P, P, P]),
+    ("chk_deltanet_block", i32, [P, u32, P, u32, i32, P]),
+    ("chk_deltanet_state", i32, [P, u32, P, P]),
+    ("chk_deltanet_rollback", i32, [P, u32, u32]),
+    ("chk_attention_block", i32, [P, u32, P, u32, u32, P]),
+    ("chk_kv_fill", i32, [P, u32, u32, P, P, u32]),
+    ("chk_attention_block2", i32, [P, u32, P, C.POINTER(u32), P]),
+    ("chk_hc_read", i32, [P, u32, u32, P, u32, P, P]),
+    ("chk_expert_record", i32, [P, u32, u32, u32, P, u64]),
+    ("chk_record_stride", u64, [P, u32]),
+    ("chk_trace_enable", i32, [P, i32]),
+    ("chk_layer_hyper", i32, [P, u32, u32, P]),
+    ("chk_profile_kernel", i32, [P, i32]),
+    ("chk_profile_read", i32, [P, C.POINTER(f64), C.POINTER(u64), C.POINTER(u64)]),
+    ("chk_time_decode", i32, [P, u32, u32, C.POINTER(f32), C.POINTER(u32)]),
+    # runner (decode loop)
+    ("chk_decode_new", i32, [P, u32, C.POINTER(u32), u32, u32, u32, u32, C.POINTER(P)]),
+    ("chk_decode_free", None, [P]),
+    ("chk_decode_step", i32, [P, C.POINTER(u32), C.POINTER(u32)]),
+    ("chk_decode_finished", i32, [P]),
+    ("chk_decode_stats", i32, [P, C.POINTER(u32), C.POINTER(u32)]),
+    ("chk_decode_error", C.c_char_p, []),
+]
+
+_lib = None
+
+
+class EngineError(RuntimeError):
+    pass
+
+
+def lib() -> C.CDLL:
+    """Load libcherenkov.so (built by cherenkov_amd.build); raise if absent."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise EngineError(
+                f"{LIB_PATH} is missing: build it with `python -m cherenkov_amd.build` "
+                "(there is no CPU fallback)"
+            )
+        L = C.CDLL(str(LIB_PATH), mode=os.RTLD_NOW | C.RTLD_GLOBAL)
+        for name, res, args in SIGNATURES:
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        raise EngineError(lib().chk_last_error().decode())

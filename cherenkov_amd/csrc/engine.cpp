@@ -1,0 +1,1242 @@
+// The qwen4_exp engine on one MI355X: HBM-resident store, state, step
+// orchestration, and the C ABI of include/cherenkov/{engine,kernels}.h.
+//
+// Restates the reference engine's behaviour (src/qwen4_exp/gpu.rs and
+// gpu/{load,decode,state,mtp,experts,deltanet,attention}.rs) without its
+// Metal structure: no command-buffer encoding, no CPU<->GPU handshake per
+// MoE block (every expert record is resident, so expert addresses are
+// computed on the device from the router's ids), no expert streaming.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "cherenkov/engine.h"
+#include "cherenkov/kernels.h"
+#include "kernels_internal.h"
+
+namespace chk {
+
+thread_local std::string g_err;
+
+struct Error : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+#define HIPCHK(x)                                                                                   \
+    do {                                                                                            \
+        hipError_t e_ = (x);                                                                        \
+        if (e_ != hipSuccess)                                                                       \
+            throw Error(std::string("HIP error ") + hipGetErrorString(e_) + " at " #x);             \
+    } while (0)
+
+static void ensure(bool ok, const std::string& msg) {
+    if (!ok) throw Error(msg);
+}
+
+RecordLayout record_layout(uint32_t bits, uint32_t hidden, uint32_t inter) {
+    RecordLayout L{};
+    const uint64_t page = 16384;
+    uint64_t codes = (uint64_t)inter * hidden;
+    L.bits = bits;
+    L.scale_up = (uint64_t)inter * (hidden / 64) * 2;
+    L.scale_down = (uint64_t)hidden * (inter / 64) * 2;
+    if (bits == 4) {
+        uint64_t off = 0;
+        auto take = [&](uint64_t n) { uint64_t o = off; off += n; return o; };
+        L.mat = codes / 2;
+        L.gate_w = take(codes / 2); L.up_w = take(codes / 2); L.down_w = take(codes / 2);
+        L.gate_s = take(L.scale_up); L.gate_b = take(L.scale_up);
+        L.up_s = take(L.scale_up); L.up_b = take(L.scale_up);
+        L.down_s = take(L.scale_down); L.down_b = take(L.scale_down);
+        L.bytes = off;
+    } else {
+        // lowbit::Layout::new (lowbit.rs:81-115): 3 matrices then 6
+        // scale/bias blocks of scale_bytes each.
+        uint64_t mat = codes * bits / 8, sb = L.scale_up;
+        L.mat = mat;
+        L.gate_w = 0; L.up_w = mat; L.down_w = 2 * mat;
+        L.gate_s = 3 * mat; L.gate_b = 3 * mat + sb; L.up_s = 3 * mat + 2 * sb; L.up_b = 3 * mat + 3 * sb;
+        L.down_s = 3 * mat + 4 * sb; L.down_b = 3 * mat + 5 * sb;
+        L.bytes = 3 * mat + 6 * sb;
+    }
+    L.stride = (L.bytes + page - 1) / page * page;
+    return L;
+}
+
+// Bump allocator over one HBM block; a dry run (base == 0) sizes it.
+struct Bump {
+    uint8_t* base = nullptr;
+    uint64_t off = 0;
+    bool gen = false;
+    template <class T>
+    T* take(uint64_t n) {
+        off = (off + 255) & ~(uint64_t)255;
+        T* p = reinterpret_cast<T*>(base + off);
+        off += n * sizeof(T);
+        return p;
+    }
+};
+
+struct LayerDev {
+    bool linear = false;
+    int dn_idx = -1, at_idx = -1;
+    HcDev attn_hc{}, mlp_hc{};
+    DnDev dn{};
+    AtDev at{};
+    MoeDev moe{};
+};
+
+enum { PROF_NONE = 0, PROF_MOE = 1, PROF_DN_PROJ = 2, PROF_LM_HEAD = 3 };
+
+struct Scratch {
+    uint32_t* tokens;
+    float *hyper, *hc_d, *hc_inv, *inj_a, *inj_m, *mixed;
+    float *dn_conv, *dn_z, *dn_decay, *dn_beta, *dn_y;
+    float *q_raw, *k_raw, *v_raw, *idx_raw, *q_ready, *attn_out, *part;
+    float *router_logits, *router_probs, *sg, *route_w, *act, *mix_out;
+    uint32_t *route_ids, *counter;
+    float *logits, *pv;
+    uint32_t *pi, *out_tok;
+    // MTP
+    float *mtp_hyper, *mtp_hn, *mtp_fe, *mtp_fh, *mtp_src, *mtp_logits;
+    uint32_t* mtp_out;
+    float* trace;  // [L][MAX_NB][hh] when tracing
+};
+
+}  // namespace chk
+
+using namespace chk;
+
+struct ChkEngine {
+    ChkConfig c{};
+    ChkOptions o{};
+    Dims D{};
+    hipStream_t st = nullptr;
+    std::vector<void*> allocs;
+    uint8_t* dense = nullptr;
+    uint64_t dense_bytes = 0;
+    RecordLayout rl4{}, rllo{};
+    uint8_t* experts4 = nullptr;
+    uint8_t* experts_lo = nullptr;
+    uint32_t record_layers = 0;
+    uint64_t state_bytes = 0, kv_bytes = 0, scratch_bytes = 0;
+    Q4Mat embed{}, lm_head{};
+    std::vector<LayerDev> layers;
+    HcDev final_mixer{};
+    bool has_mtp = false;
+    LayerDev mtp_layer{};
+    HcDev mtp_mixer{};
+    const uint16_t* mtp_enorm = nullptr;
+    const uint16_t* mtp_hnorm = nullptr;
+    Q4Mat fc_e{}, fc_h{};
+    // state
+    std::vector<float*> dn_state, dn_hist, dn_snap_state, dn_snap_hist;
+    std::vector<KvDev> kv, kv2;
+    KvDev mtp_kv{};
+    Scratch s{};
+    uint32_t max_chunks = 1, lm_parts = 1024;
+    // sequence
+    uint32_t pos = 0, batch_pos = 0, batch_nb = 0, max_t = 0, trunk_rows = 1;
+    bool batch_snap = false;
+    uint32_t mtp_len = 0;
+    std::vector<uint32_t> tokens;
+    std::vector<float> host_logits, host_mtp_logits;
+    uint32_t last_mtp_rows = 0;
+    bool tracing = false;
+    // folded MTP pass results of the last step (one draft per row)
+    bool folded_valid = false;
+    std::vector<uint32_t> folded;
+    // live profiler: HIP events around one kernel class on the engine stream
+    int prof_kind = 0;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> prof_events;
+    size_t prof_used = 0;
+    uint64_t prof_bytes = 0, prof_launches = 0;
+    double prof_ms = 0.0;
+
+    void prof_begin(int kind) {
+        if (prof_kind != kind) return;
+        if (prof_used == prof_events.size()) {
+            hipEvent_t a, b;
+            HIPCHK(hipEventCreate(&a));
+            HIPCHK(hipEventCreate(&b));
+            prof_events.push_back({a, b});
+        }
+        HIPCHK(hipEventRecord(prof_events[prof_used].first, st));
+    }
+    void prof_end(int kind, uint64_t bytes) {
+        if (prof_kind != kind) return;
+        HIPCHK(hipEventRecord(prof_events[prof_used].second, st));
+        ++prof_used;
+        prof_bytes += bytes;
+        ++prof_launches;
+    }
+    void prof_collect() {
+        if (!prof_used) return;
+        HIPCHK(hipStreamSynchronize(st));
+        for (size_t i = 0; i < prof_used; ++i) {
+            float ms = 0;
+            HIPCHK(hipEventElapsedTime(&ms, prof_events[i].first, prof_events[i].second));
+            prof_ms += ms;
+        }
+        prof_used = 0;
+    }
+    uint64_t q4_bytes(const Q4Mat& m) const { return (uint64_t)m.out * m.in / 2 + 4ull * (m.out * (m.in / 64)); }
+    uint64_t expert_mat_bytes() const {
+        uint64_t codes = (uint64_t)D.I * D.H;
+        if (o.experts == 4) return codes / 2 + 4 * (codes / 64);
+        return codes * o.experts / 8 + 4 * (codes / 64);
+    }
+
+    ~ChkEngine() {
+        if (st) hipStreamSynchronize(st);
+        for (void* p : allocs) hipFree(p);
+        if (st) hipStreamDestroy(st);
+    }
+
+    template <class T>
+    T* dalloc(uint64_t n) {
+        void* p = nullptr;
+        HIPCHK(hipMalloc(&p, std::max<uint64_t>(n * sizeof(T), 256)));
+        allocs.push_back(p);
+        return reinterpret_cast<T*>(p);
+    }
+
+    bool is_linear(uint32_t l) const { return (l + 1) % c.full_attention_interval != 0; }
+
+    // ------------------------------------------------------ store build
+    Q4Mat q4(Bump& B, uint32_t kind, uint32_t slot, uint32_t part, uint32_t out, uint32_t in) {
+        Q4Mat m{};
+        m.out = out;
+        m.in = in;
+        uint32_t* w = B.take<uint32_t>((uint64_t)out * in / 8);
+        uint16_t* s = B.take<uint16_t>((uint64_t)out * in / 64);
+        uint16_t* b = B.take<uint16_t>((uint64_t)out * in / 64);
+        m.w = w; m.s = s; m.b = b;
+        if (B.gen) gen_q4(w, s, b, out, in, c.seed, chk_tensor_id(kind, slot, 0, part), st);
+        return m;
+    }
+    const uint16_t* bf(Bump& B, uint32_t kind, uint32_t slot, uint32_t part, uint64_t n) {
+        uint16_t* p = B.take<uint16_t>(n);
+        if (B.gen) gen_bf16(p, n, c.seed, chk_tensor_id(kind, slot, 0, part), kind, st);
+        return p;
+    }
+    HcDev hc(Bump& B, uint32_t slot, uint32_t part, bool inject) {
+        HcDev w{};
+        uint32_t hh = D.hh;
+        w.norm = bf(B, CHK_T_HC_NORM, slot, part, hh);
+        w.down = q4(B, CHK_T_HC_DOWN, slot, part, c.hc_lowrank, hh);
+        w.up = q4(B, CHK_T_HC_UP, slot, part, hh, c.hc_lowrank);
+        w.has_inject = inject;
+        if (inject) w.inject = q4(B, CHK_T_HC_INJECT, slot, part, c.hc_count, hh);
+        return w;
+    }
+    void layer(Bump& B, LayerDev& L, uint32_t slot, bool linear, uint32_t record_layer) {
+        uint32_t H = D.H;
+        L.linear = linear;
+        L.attn_hc = hc(B, slot, CHK_HC_ATTN, true);
+        L.mlp_hc = hc(B, slot, CHK_HC_MLP, true);
+        if (linear) {
+            L.dn.qkv = q4(B, CHK_T_DN_QKV, slot, 0, D.conv_dim, H);
+            L.dn.z = q4(B, CHK_T_DN_Z, slot, 0, D.v_dim, H);
+            L.dn.a = q4(B, CHK_T_DN_A, slot, 0, D.nv, H);
+            L.dn.b = q4(B, CHK_T_DN_B, slot, 0, D.nv, H);
+            L.dn.out = q4(B, CHK_T_DN_OUT, slot, 0, H, D.v_dim);
+            L.dn.conv = bf(B, CHK_T_DN_CONV, slot, 0, (uint64_t)D.conv_dim * D.ck);
+            L.dn.a_log = bf(B, CHK_T_DN_ALOG, slot, 0, D.nv);
+            L.dn.dt_bias = bf(B, CHK_T_DN_DTBIAS, slot, 0, D.nv);
+            L.dn.norm = bf(B, CHK_T_DN_NORM, slot, 0, D.dv);
+        } else {
+            L.at.q = q4(B, CHK_T_AT_Q, slot, 0, 2 * D.nh * D.hd, H);
+            L.at.k = q4(B, CHK_T_AT_K, slot, 0, D.nkv * D.hd, H);
+            L.at.v = q4(B, CHK_T_AT_V, slot, 0, D.nkv * D.hd, H);
+            L.at.o = q4(B, CHK_T_AT_O, slot, 0, H, D.nh * D.hd);
+            L.at.idx = q4(B, CHK_T_AT_IDX, slot, 0, D.idx_out, H);
+            L.at.q_norm = bf(B, CHK_T_AT_QNORM, slot, 0, D.hd);
+            L.at.k_norm = bf(B, CHK_T_AT_KNORM, slot, 0, D.hd);
+            L.at.idx_q_norm = bf(B, CHK_T_AT_IDX_QNORM, slot, 0, D.ihd);
+            L.at.idx_k_norm = bf(B, CHK_T_AT_IDX_KNORM, slot, 0, D.ihd);
+        }
+        L.moe.router = bf(B, CHK_T_MOE_ROUTER, slot, 0, (uint64_t)D.E * H);
+        L.moe.shared_gate = bf(B, CHK_T_MOE_SHARED_GATE, slot, 0, H);
+        L.moe.sh_gate = q4(B, CHK_T_MOE_SH_GATE_PROJ, slot, 0, D.SI, H);
+        L.moe.sh_up = q4(B, CHK_T_MOE_SH_UP, slot, 0, D.SI, H);
+        L.moe.sh_down = q4(B, CHK_T_MOE_SH_DOWN, slot, 0, H, D.SI);
+        L.moe.record_layer = record_layer;
+    }
+    void build_dense(Bump& B) {
+        uint32_t H = D.H, L = c.num_hidden_layers;
+        embed = q4(B, CHK_T_EMBED, 0, 0, D.V, H);
+        lm_head = q4(B, CHK_T_LM_HEAD, 0, 0, D.V, H);
+        layers.assign(L, LayerDev{});
+        int dn_i = 0, at_i = 0;
+        for (uint32_t l = 0; l < L; ++l) {
+            layer(B, layers[l], l, is_linear(l), l);
+            if (layers[l].linear) layers[l].dn_idx = dn_i++;
+            else layers[l].at_idx = at_i++;
+        }
+        final_mixer = hc(B, 0, CHK_HC_FINAL, false);
+        if (has_mtp) {
+            mtp_enorm = bf(B, CHK_T_MTP_ENORM, L, 0, H);
+            mtp_hnorm = bf(B, CHK_T_MTP_HNORM, L, 0, D.hh);
+            fc_e = q4(B, CHK_T_MTP_FC_E, L, 0, H, H);
+            fc_h = q4(B, CHK_T_MTP_FC_H, L, 0, H, H);
+            layer(B, mtp_layer, L, false, L);
+            mtp_mixer = hc(B, L, CHK_HC_MTP, false);
+        }
+    }
+
+    ExpertsDev experts_dev() const {
+        ExpertsDev X{};
+        const RecordLayout& R = o.experts == 4 ? rl4 : rllo;
+        X.base = o.experts == 4 ? experts4 : experts_lo;
+        X.stride = R.stride;
+        X.bits = o.experts;
+        X.experts = D.E;
+        X.gate_w = R.gate_w; X.up_w = R.up_w; X.down_w = R.down_w;
+        X.gate_s = R.gate_s; X.gate_b = R.gate_b; X.up_s = R.up_s; X.up_b = R.up_b;
+        X.down_s = R.down_s; X.down_b = R.down_b;
+        return X;
+    }
+
+    KvDev alloc_kv() {
+        KvDev k{};
+        k.k = dalloc<int8_t>((uint64_t)max_t * D.kv_row);
+        k.v = dalloc<int8_t>((uint64_t)max_t * D.kv_row);
+        k.ks = dalloc<uint16_t>((uint64_t)max_t * D.kv_row / 32);
+        k.vs = dalloc<uint16_t>((uint64_t)max_t * D.kv_row / 32);
+        k.index_k = dalloc<float>((uint64_t)max_t * D.ihd);
+        kv_bytes += (uint64_t)max_t * (2 * D.kv_row + D.kv_row / 8 + 4 * D.ihd);
+        return k;
+    }
+
+    void load(const ChkConfig* cfg, const ChkOptions* opt) {
+        c = *cfg;
+        o = *opt;
+        ensure(o.experts == 4 || o.experts == 3 || o.experts == 2, "expert precision must be 4, 3 or 2 bits");
+        ensure(o.drafts <= 3, "drafts must be 0..=3");
+        ensure(o.max_t >= 1, "max_t must be positive");
+        ensure(c.full_attention_interval >= 1 && c.num_hidden_layers >= 1, "layer pattern");
+        ensure(c.hc_count >= 2 && c.hc_count <= 8, "hc_count must be 2..=8");
+        ensure(c.hidden_size % 256 == 0, "hidden % 256 == 0 (gpu/load.rs:25-28)");
+        ensure(c.hc_lowrank % 32 == 0 && c.hc_lowrank <= 2048, "hc_lowrank must be a multiple of 32");
+        ensure(c.moe_intermediate_size % 64 == 0, "expert width must be a multiple of 64 (gpu/load.rs:37-40)");
+        ensure(c.shared_expert_intermediate_size == c.moe_intermediate_size,
+               "shared expert width must equal the routed expert width");
+        ensure(c.linear_key_head_dim == 128, "DeltaNet key head dim must be 128");
+        ensure(c.linear_value_head_dim * 4 <= 1024, "DeltaNet value head dim too wide");
+        ensure(c.linear_num_value_heads % c.linear_num_key_heads == 0, "value heads must group key heads");
+        ensure(c.head_dim <= 256 && c.head_dim % 64 == 0, "head_dim must be 64..256");
+        ensure(c.indexer_head_dim <= 256 && c.indexer_head_dim % 32 == 0,
+               "indexer head dim must be a multiple of 32 up to 256 (gpu/load.rs:29-32)");
+        ensure(c.indexer_budget % c.indexer_compress_ratio == 0,
+               "indexer budget must be a multiple of the block size (gpu/load.rs:33-36)");
+        ensure(c.num_experts <= 1024 && c.num_experts_per_tok <= 64 && c.num_experts_per_tok <= c.num_experts,
+               "experts per token");
+        ensure(c.ple_layer == 0, "PLE layers are not supported");
+        ensure(c.linear_conv_kernel_dim >= 2 && c.linear_conv_kernel_dim <= 9, "conv kernel 2..=9");
+        // QSA selection only matters once complete blocks exceed the budget
+        // (cpu.rs:651-662); this engine runs the dense case.
+        ensure(o.max_t / c.indexer_compress_ratio <= c.indexer_budget / c.indexer_compress_ratio,
+               "contexts beyond indexer_budget need QSA selective attention, which this engine does not implement");
+        D.H = c.hidden_size;
+        D.hc = c.hc_count;
+        D.hh = D.H * D.hc;
+        D.lowrank = c.hc_lowrank;
+        D.nk = c.linear_num_key_heads;
+        D.nv = c.linear_num_value_heads;
+        D.dk = c.linear_key_head_dim;
+        D.dv = c.linear_value_head_dim;
+        D.qk_dim = D.nk * D.dk;
+        D.v_dim = D.nv * D.dv;
+        D.conv_dim = 2 * D.qk_dim + D.v_dim;
+        D.ck = c.linear_conv_kernel_dim;
+        D.nh = c.num_attention_heads;
+        D.nkv = c.num_key_value_heads;
+        D.hd = c.head_dim;
+        D.rot = (uint32_t)((double)D.hd * c.partial_rotary_factor);
+        D.kv_row = D.nkv * D.hd;
+        D.inh = c.indexer_n_heads;
+        D.ihd = c.indexer_head_dim;
+        D.idx_out = (D.inh + 1) * D.ihd;
+        D.E = c.num_experts;
+        D.topk = c.num_experts_per_tok;
+        D.I = c.moe_intermediate_size;
+        D.SI = c.shared_expert_intermediate_size;
+        D.V = c.vocab_size;
+        D.eps = (float)c.rms_norm_eps;
+        D.theta = (float)c.rope_theta;
+        D.attn_scale = powf((float)D.hd, -0.5f);
+        D.qscale = powf((float)D.dk, -0.5f);
+        D.norm_topk = c.norm_topk_prob != 0;
+        has_mtp = c.mtp_num_hidden_layers > 0;
+        ensure(o.drafts == 0 || has_mtp, "drafts need an MTP head");
+        max_t = o.max_t;
+        trunk_rows = 1 + o.drafts;
+        HIPCHK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+
+        // dense store: dry run for the size, then allocate and generate
+        Bump dry;
+        build_dense(dry);
+        dense_bytes = dry.off;
+        dense = dalloc<uint8_t>(dense_bytes);
+        Bump B;
+        B.base = dense;
+        B.gen = true;
+        build_dense(B);
+
+        // routed-expert store: all records resident, main layers then MTP
+        record_layers = c.num_hidden_layers + (has_mtp ? 1 : 0);
+        rl4 = record_layout(4, D.H, D.I);
+        uint64_t n_rec = (uint64_t)record_layers * D.E;
+        experts4 = dalloc<uint8_t>(n_rec * rl4.stride);
+        gen_records(experts4, rl4, c.seed, D.E, 0, record_layers, D.H, D.I, st);
+        if (o.experts != 4) {
+            rllo = record_layout(o.experts, D.H, D.I);
+            experts_lo = dalloc<uint8_t>(n_rec * rllo.stride);
+            repack_lowbit(experts4, rl4, experts_lo, rllo, (uint32_t)n_rec, (uint64_t)D.I * D.H, st);
+        }
+
+        // recurrent state, snapshots, KV
+        for (uint32_t l = 0; l < c.num_hidden_layers; ++l) {
+            if (layers[l].linear) {
+                uint64_t sn = (uint64_t)D.nv * D.dv * D.dk, hn = (uint64_t)D.conv_dim * (D.ck - 1);
+                dn_state.push_back(dalloc<float>(sn));
+                dn_hist.push_back(dalloc<float>(hn));
+                dn_snap_state.push_back(dalloc<float>(sn * MAX_SNAP));
+                dn_snap_hist.push_back(dalloc<float>(hn * MAX_SNAP));
+                state_bytes += (sn + hn) * 4 * (1 + MAX_SNAP);
+            } else {
+                kv.push_back(alloc_kv());
+            }
+        }
+        if (has_mtp) mtp_kv = alloc_kv();
+        max_chunks = (max_t + ATTN_CHUNK - 1) / ATTN_CHUNK;
+
+        // scratch
+        const uint32_t NB = MAX_NB;
+        s.tokens = dalloc<uint32_t>(NB);
+        s.hyper = dalloc<float>(NB * D.hh);
+        s.hc_d = dalloc<float>(NB * D.lowrank);
+        s.hc_inv = dalloc<float>(NB * D.hc);
+        s.inj_a = dalloc<float>(NB * D.hc);
+        s.inj_m = dalloc<float>(NB * D.hc);
+        s.mixed = dalloc<float>(NB * D.H);
+        s.dn_conv = dalloc<float>(NB * D.conv_dim);
+        s.dn_z = dalloc<float>(NB * D.v_dim);
+        s.dn_decay = dalloc<float>(NB * D.nv);
+        s.dn_beta = dalloc<float>(NB * D.nv);
+        s.dn_y = dalloc<float>(NB * D.v_dim);
+        s.q_raw = dalloc<float>(NB * 2 * D.nh * D.hd);
+        s.k_raw = dalloc<float>(NB * D.kv_row);
+        s.v_raw = dalloc<float>(NB * D.kv_row);
+        s.idx_raw = dalloc<float>(NB * D.idx_out);
+        s.q_ready = dalloc<float>(NB * D.nh * D.hd);
+        s.attn_out = dalloc<float>(NB * D.nh * D.hd);
+        s.part = dalloc<float>((uint64_t)NB * D.nh * max_chunks * (D.hd + 2));
+        s.router_logits = dalloc<float>(NB * D.E);
+        uint32_t LR = record_layers;
+        s.router_probs = dalloc<float>((uint64_t)LR * NB * D.E);
+        s.route_ids = dalloc<uint32_t>((uint64_t)LR * NB * D.topk);
+        s.route_w = dalloc<float>((uint64_t)LR * NB * D.topk);
+        s.sg = dalloc<float>(NB);
+        s.act = dalloc<float>((uint64_t)NB * (D.topk + 1) * D.I);
+        s.mix_out = dalloc<float>(NB * D.H);
+        s.counter = dalloc<uint32_t>(64);
+        HIPCHK(hipMemsetAsync(s.counter, 0, 256, st));
+        s.logits = dalloc<float>((uint64_t)NB * D.V);
+        s.pv = dalloc<float>((uint64_t)NB * lm_parts);
+        s.pi = dalloc<uint32_t>((uint64_t)NB * lm_parts);
+        s.out_tok = dalloc<uint32_t>(NB);
+        s.mtp_hyper = dalloc<float>(NB * D.hh);
+        s.mtp_hn = dalloc<float>((uint64_t)NB * (D.H + D.hh));
+        s.mtp_src = dalloc<float>((uint64_t)D.hh);
+        s.mtp_fe = dalloc<float>(NB * D.H);
+        s.mtp_fh = dalloc<float>((uint64_t)NB * D.hh);
+        s.mtp_logits = dalloc<float>((uint64_t)NB * D.V);
+        s.mtp_out = dalloc<uint32_t>(NB);
+        s.trace = nullptr;
+        scratch_bytes = 4ull * (NB * (3 * D.hh + 4 * D.H + D.conv_dim + 3 * D.v_dim + 4 * D.nh * D.hd) +
+                                 (uint64_t)NB * D.nh * max_chunks * (D.hd + 2) + 2ull * NB * D.V);
+        host_logits.resize((size_t)NB * D.V);
+        host_mtp_logits.resize((size_t)NB * D.V);
+        reset_state();
+        HIPCHK(hipStreamSynchronize(st));
+        HIPCHK(hipGetLastError());
+    }
+
+    void reset_state() {
+        for (size_t i = 0; i < dn_state.size(); ++i) {
+            launch_zero_f32(dn_state[i], (uint64_t)D.nv * D.dv * D.dk, st);
+            launch_zero_f32(dn_hist[i], (uint64_t)D.conv_dim * (D.ck - 1), st);
+        }
+        pos = 0;
+        batch_pos = 0;
+        batch_nb = 0;
+        mtp_len = 0;
+        tokens.clear();
+        folded_valid = false;
+    }
+
+    // ----------------------------------------------------------- blocks
+    void hc_read(const HcDev& w, const float* hyper, float* inj, int nb) {
+        launch_hc_down(w, hyper, s.hc_d, inj, s.hc_inv, D.H, D.hc, D.eps, nb, st);
+        launch_hc_up_mix(w, hyper, s.hc_inv, s.hc_d, s.mixed, D.H, D.hc, nb, st);
+    }
+
+    void deltanet(const LayerDev& L, const float* x, int nb, bool snap, float* hyper, const float* inj,
+                  float* raw_out) {
+        const int di = L.dn_idx;
+        SegArgs a{};
+        a.nseg = 4;
+        uint32_t r0 = 0;
+        a.seg[0] = Seg{L.dn.qkv, x, s.dn_conv, D.H, D.conv_dim, r0, EPI_DN_CONV};
+        r0 += D.conv_dim;
+        a.seg[1] = Seg{L.dn.z, x, s.dn_z, D.H, D.v_dim, r0, EPI_RAW};
+        r0 += D.v_dim;
+        a.seg[2] = Seg{L.dn.a, x, s.dn_decay, D.H, D.nv, r0, EPI_DN_DECAY};
+        r0 += D.nv;
+        a.seg[3] = Seg{L.dn.b, x, s.dn_beta, D.H, D.nv, r0, EPI_DN_BETA};
+        r0 += D.nv;
+        a.total = r0;
+        a.conv_w = L.dn.conv;
+        a.hist = dn_hist[di];
+        a.snap_hist = dn_snap_hist[di];
+        a.ck = D.ck;
+        a.conv_dim = D.conv_dim;
+        a.snap = snap;
+        a.a_log = L.dn.a_log;
+        a.dt_bias = L.dn.dt_bias;
+        uint64_t bytes = q4_bytes(L.dn.qkv) + q4_bytes(L.dn.z) + q4_bytes(L.dn.a) + q4_bytes(L.dn.b) +
+                         (uint64_t)D.conv_dim * D.ck * 2 + 2ull * D.conv_dim * (D.ck - 1) * 4 +
+                         (uint64_t)nb * (D.H * 4 + (D.conv_dim + D.v_dim + 2 * D.nv) * 4);
+        prof_begin(PROF_DN_PROJ);
+        launch_qmv(a, nb, st);
+        prof_end(PROF_DN_PROJ, bytes);
+        DnScanArgs sa{};
+        sa.state = dn_state[di];
+        sa.snap_state = dn_snap_state[di];
+        sa.conv_out = s.dn_conv;
+        sa.decay = s.dn_decay;
+        sa.beta = s.dn_beta;
+        sa.z = s.dn_z;
+        sa.norm = L.dn.norm;
+        sa.y = s.dn_y;
+        sa.nk = D.nk;
+        sa.nv = D.nv;
+        sa.dv = D.dv;
+        sa.qk_dim = D.qk_dim;
+        sa.conv_dim = D.conv_dim;
+        sa.qscale = D.qscale;
+        sa.snap = snap;
+        launch_dn_scan(sa, nb, st);
+        launch_qmv_inject(L.dn.out, s.dn_y, D.v_dim, hyper, inj, D.hc, raw_out, nb, st);
+    }
+
+    void attention(const LayerDev& L, const float* x, int nb, const KvDev* kvs, const uint32_t* rows_pos,
+                   float* hyper, const float* inj, float* raw_out) {
+        SegArgs a{};
+        a.nseg = 4;
+        uint32_t r0 = 0;
+        a.seg[0] = Seg{L.at.q, x, s.q_raw, D.H, 2 * D.nh * D.hd, r0, EPI_RAW};
+        r0 += 2 * D.nh * D.hd;
+        a.seg[1] = Seg{L.at.k, x, s.k_raw, D.H, D.kv_row, r0, EPI_RAW};
+        r0 += D.kv_row;
+        a.seg[2] = Seg{L.at.v, x, s.v_raw, D.H, D.kv_row, r0, EPI_RAW};
+        r0 += D.kv_row;
+        a.seg[3] = Seg{L.at.idx, x, s.idx_raw, D.H, D.idx_out, r0, EPI_RAW};
+        r0 += D.idx_out;
+        a.total = r0;
+        launch_qmv(a, nb, st);
+        AttnArgs aa{};
+        aa.q_raw = s.q_raw;
+        aa.k_raw = s.k_raw;
+        aa.v_raw = s.v_raw;
+        aa.idx_raw = s.idx_raw;
+        aa.q_norm = L.at.q_norm;
+        aa.k_norm = L.at.k_norm;
+        aa.q_ready = s.q_ready;
+        for (int b = 0; b < nb; ++b) {
+            aa.kv[b] = kvs[b];
+            aa.pos[b] = rows_pos[b];
+        }
+        aa.part = s.part;
+        aa.out = s.attn_out;
+        aa.nh = D.nh;
+        aa.nkv = D.nkv;
+        aa.hd = D.hd;
+        aa.rot = D.rot;
+        aa.inh = D.inh;
+        aa.ihd = D.ihd;
+        aa.max_chunks = max_chunks;
+        aa.eps = D.eps;
+        aa.theta = D.theta;
+        aa.scale = D.attn_scale;
+        launch_attn(aa, nb, st);
+        launch_qmv_inject(L.at.o, s.attn_out, D.nh * D.hd, hyper, inj, D.hc, raw_out, nb, st);
+    }
+
+    void moe(const LayerDev& L, uint32_t route_slot, const float* x, int nb, float* hyper, const float* inj,
+             float* raw_out) {
+        RouterArgs r{};
+        r.router = L.moe.router;
+        r.shared_gate = L.moe.shared_gate;
+        r.x = x;
+        r.logits = s.router_logits;
+        r.probs = s.router_probs + (uint64_t)route_slot * MAX_NB * D.E;
+        r.sg = s.sg;
+        r.ids = s.route_ids + (uint64_t)route_slot * MAX_NB * D.topk;
+        r.w = s.route_w + (uint64_t)route_slot * MAX_NB * D.topk;
+        r.counter = s.counter;
+        r.E = D.E;
+        r.H = D.H;
+        r.topk = D.topk;
+        r.norm_topk = D.norm_topk;
+        launch_router(r, nb, st);
+        MoeArgs m{};
+        m.X = experts_dev();
+        m.record_layer = L.moe.record_layer;
+        m.sh_gate = L.moe.sh_gate;
+        m.sh_up = L.moe.sh_up;
+        m.sh_down = L.moe.sh_down;
+        m.x = x;
+        m.ids = r.ids;
+        m.w = r.w;
+        m.sg = s.sg;
+        m.act = s.act;
+        m.hyper = hyper;
+        m.inj = inj;
+        m.raw_out = raw_out;
+        m.nb = nb;
+        m.H = D.H;
+        m.I = D.I;
+        m.topk = D.topk;
+        m.hc = D.hc;
+        // algorithmic bytes: each routed row-slot's expert record (gate, up,
+        // down) + the shared expert, the activations in and out
+        uint64_t bytes = (uint64_t)nb * D.topk * 3 * expert_mat_bytes() + 3 * q4_bytes(L.moe.sh_gate) +
+                         (uint64_t)nb * (D.H * 4 + (D.topk + 1) * D.I * 8 + D.H * 8);
+        prof_begin(PROF_MOE);
+        launch_moe(m, st);
+        prof_end(PROF_MOE, bytes);
+    }
+
+    // ---------------------------------------------------------- step
+    void run_rows(int nb, bool snap) {
+        launch_embed(s.tokens, embed, s.hyper, D.H, D.hc, nb, st);
+        KvDev kvs[MAX_NB];
+        uint32_t rows_pos[MAX_NB];
+        for (int b = 0; b < nb; ++b) rows_pos[b] = pos + b;
+        for (uint32_t l = 0; l < c.num_hidden_layers; ++l) {
+            const LayerDev& L = layers[l];
+            hc_read(L.attn_hc, s.hyper, s.inj_a, nb);
+            if (L.linear) {
+                deltanet(L, s.mixed, nb, snap, s.hyper, s.inj_a, nullptr);
+            } else {
+                for (int b = 0; b < nb; ++b) kvs[b] = kv[L.at_idx];
+                attention(L, s.mixed, nb, kvs, rows_pos, s.hyper, s.inj_a, nullptr);
+            }
+            hc_read(L.mlp_hc, s.hyper, s.inj_m, nb);
+            moe(L, l, s.mixed, nb, s.hyper, s.inj_m, nullptr);
+            if (tracing && s.trace)
+                HIPCHK(hipMemcpyAsync(s.trace + (uint64_t)l * MAX_NB * D.hh, s.hyper, (uint64_t)nb * D.hh * 4,
+                                      hipMemcpyDeviceToDevice, st));
+        }
+        hc_read(final_mixer, s.hyper, nullptr, nb);
+        prof_begin(PROF_LM_HEAD);
+        launch_lm_head(lm_head, s.mixed, s.logits, s.pv, s.pi, lm_parts, s.out_tok, nb, st);
+        prof_end(PROF_LM_HEAD, q4_bytes(lm_head) + (uint64_t)nb * (D.H + D.V) * 4);
+    }
+
+    void step_rows(const uint32_t* toks, uint32_t n, bool snap, bool fold, uint32_t* out) {
+        ensure(!fold || has_mtp, "folding the MTP pass needs the MTP head");
+        ensure(n >= 1 && n <= trunk_rows,
+               "rows per step must be 1..=" + std::to_string(trunk_rows) + " (set --drafts to raise it)");
+        ensure(pos + n <= max_t, "context capacity exceeded");
+        ensure(!snap || n - 1 <= (uint32_t)MAX_SNAP, "at most 3 draft rows per verify step");
+        for (uint32_t i = 0; i < n; ++i) ensure(toks[i] < D.V, "token id out of range");
+        folded_valid = false;
+        tokens.resize(pos);
+        tokens.insert(tokens.end(), toks, toks + n);
+        batch_pos = pos;
+        batch_nb = n;
+        batch_snap = snap;
+        HIPCHK(hipMemcpyAsync(s.tokens, toks, n * 4, hipMemcpyHostToDevice, st));
+        run_rows((int)n, snap);
+        if (fold) {
+            // pair row b's residual with the trunk's own prediction for it
+            mtp_pass_trunk((int)n, batch_pos, s.out_tok);
+        }
+        HIPCHK(hipMemcpyAsync(out, s.out_tok, n * 4, hipMemcpyDeviceToHost, st));
+        if (fold) {
+            folded.assign(n, 0);
+            HIPCHK(hipMemcpyAsync(folded.data(), s.mtp_out, n * 4, hipMemcpyDeviceToHost, st));
+        }
+        HIPCHK(hipStreamSynchronize(st));
+        HIPCHK(hipGetLastError());
+        prof_collect();
+        if (fold) {
+            folded_valid = true;
+            last_mtp_rows = n;
+        }
+        logits_fresh = false;
+        mtp_logits_fresh = false;
+    }
+
+    bool logits_fresh = false, mtp_logits_fresh = false;
+
+    void commit(uint32_t n) {
+        ensure(n >= 1 && n <= batch_nb, "commit " + std::to_string(n) + " of " + std::to_string(batch_nb) + " rows");
+        if (n < batch_nb) {
+            ensure(batch_snap, "rollback needs a snapshotting step");
+            uint32_t plane = n - 1;
+            uint64_t sn = (uint64_t)D.nv * D.dv * D.dk, hn = (uint64_t)D.conv_dim * (D.ck - 1);
+            for (size_t i = 0; i < dn_state.size(); ++i) {
+                launch_copy_f32(dn_state[i], dn_snap_state[i] + plane * sn, sn, st);
+                launch_copy_f32(dn_hist[i], dn_snap_hist[i] + plane * hn, hn, st);
+            }
+            HIPCHK(hipStreamSynchronize(st));
+        }
+        pos = batch_pos + n;
+        tokens.resize(pos);
+    }
+
+    // ------------------------------------------------------------ MTP
+    // mtp_forward prelude (cpu.rs:344-369): hyper_g = fc_e(rms_norm_shift(e))
+    // + fc_h(rms_norm_shift(h_g)); then one attention + MoE block with the
+    // MTP layer's own KV, the MTP mixer and the shared LM head.
+    void mtp_rows(int rows, const float* src_hyper, const uint32_t* d_tokens, uint32_t base_pos);
+    void mtp_pass_trunk(int rows, uint32_t base_pos, const uint32_t* d_next);
+    void prefill(const uint32_t* toks, uint32_t n, uint32_t* next, uint32_t* draft);
+    void mtp_draft(const uint32_t* next, uint32_t n, uint32_t chain, uint32_t* drafts, uint32_t* nd);
+};
+
+namespace chk {
+void launch_mtp_prelude(const uint32_t* tokens, const Q4Mat& emb, const uint16_t* enorm, const uint16_t* hnorm,
+                        const float* src_hyper, float* e_n, float* h_n, uint32_t H, uint32_t hc, float eps, int rows,
+                        hipStream_t st);
+void launch_mtp_fold(const float* fe, const float* fh, float* hyper, uint32_t H, uint32_t hc, int rows,
+                     hipStream_t st);
+}  // namespace chk
+
+void ChkEngine::mtp_rows(int rows, const float* src_hyper, const uint32_t* d_tokens, uint32_t base_pos) {
+    // e_n [rows][H] into mtp_fe's input slot (reuse mtp_hn layout: first
+    // rows*H floats hold rms_norm_shift(e), then rows*hc*H the streams)
+    float* en = s.mtp_hn;
+    float* hn = s.mtp_hn + (uint64_t)MAX_NB * D.H;
+    launch_mtp_prelude(d_tokens, embed, mtp_enorm, mtp_hnorm, src_hyper, en, hn, D.H, D.hc, D.eps, rows, st);
+    // fc_e over rows, fc_h over rows * hc stream rows (in batches of 4)
+    SegArgs a{};
+    a.nseg = 1;
+    a.seg[0] = Seg{fc_e, en, s.mtp_fe, D.H, D.H, 0, EPI_RAW};
+    a.total = D.H;
+    launch_qmv(a, rows, st);
+    uint32_t nrows = rows * D.hc;
+    for (uint32_t r0 = 0; r0 < nrows; r0 += MAX_NB) {
+        int nbb = (int)std::min<uint32_t>(MAX_NB, nrows - r0);
+        SegArgs f{};
+        f.nseg = 1;
+        f.seg[0] = Seg{fc_h, hn + (uint64_t)r0 * D.H, s.mtp_fh + (uint64_t)r0 * D.H, D.H, D.H, 0, EPI_RAW};
+        f.total = D.H;
+        launch_qmv(f, nbb, st);
+    }
+    launch_mtp_fold(s.mtp_fe, s.mtp_fh, s.mtp_hyper, D.H, D.hc, rows, st);
+    const LayerDev& L = mtp_layer;
+    KvDev kvs[MAX_NB];
+    uint32_t rows_pos[MAX_NB];
+    for (int b = 0; b < rows; ++b) {
+        kvs[b] = mtp_kv;
+        rows_pos[b] = base_pos + b;
+    }
+    hc_read(L.attn_hc, s.mtp_hyper, s.inj_a, rows);
+    attention(L, s.mixed, rows, kvs, rows_pos, s.mtp_hyper, s.inj_a, nullptr);
+    hc_read(L.mlp_hc, s.mtp_hyper, s.inj_m, rows);
+    moe(L, c.num_hidden_layers, s.mixed, rows, s.mtp_hyper, s.inj_m, nullptr);
+    hc_read(mtp_mixer, s.mtp_hyper, nullptr, rows);
+    launch_lm_head(lm_head, s.mixed, s.mtp_logits, s.pv, s.pi, lm_parts, s.mtp_out, rows, st);
+}
+
+void ChkEngine::mtp_pass_trunk(int rows, uint32_t base_pos, const uint32_t* d_next) {
+    mtp_rows(rows, s.hyper, d_next, base_pos);
+}
+
+// Gpu::mtp_draft (gpu/mtp.rs:11-78)
+void ChkEngine::mtp_draft(const uint32_t* next, uint32_t n, uint32_t chain, uint32_t* drafts, uint32_t* nd) {
+    ensure(has_mtp, "no MTP head");
+    ensure(n >= 1 && n <= batch_nb, "MTP rows must match the committed rows");
+    ensure(mtp_len == batch_pos,
+           "MTP cache out of step: " + std::to_string(mtp_len) + " vs " + std::to_string(batch_pos));
+    std::vector<uint32_t> out;
+    uint32_t c0 = 0;
+    bool first = true;
+    uint32_t token = 0;
+    // the MTP hyper source: the trunk rows (first pass) or the head's own
+    // residual row (chained passes)
+    if (folded_valid) {
+        // the folded pass already ran over the trunk rows with the trunk's
+        // predictions, which equal `next` for every accepted row
+        folded_valid = false;
+        mtp_len = batch_pos + n;
+        first = false;
+        token = folded[n - 1];
+        if (chain > 0) out.push_back(token);
+        c0 = 1;
+        // the head residual of row n-1 becomes the chain source
+        if (n - 1 != 0)
+            HIPCHK(hipMemcpyAsync(s.mtp_hyper, s.mtp_hyper + (uint64_t)(n - 1) * D.hh, D.hh * 4,
+                                  hipMemcpyDeviceToDevice, st));
+    }
+    for (uint32_t ci = c0; ci < std::max<uint32_t>(chain, 1); ++ci) {
+        uint32_t rows = first ? n : 1;
+        uint32_t base = first ? batch_pos : batch_pos + n - 1 + ci;
+        ensure(base + rows <= max_t, "context capacity exceeded");
+        if (first) {
+            HIPCHK(hipMemcpyAsync(s.tokens, next, n * 4, hipMemcpyHostToDevice, st));
+            mtp_rows((int)rows, s.hyper, s.tokens, base);
+        } else {
+            HIPCHK(hipMemcpyAsync(s.tokens, &token, 4, hipMemcpyHostToDevice, st));
+            // chained: hidden input is the head's own residual row
+            HIPCHK(hipMemcpyAsync(s.mtp_src, s.mtp_hyper, D.hh * 4, hipMemcpyDeviceToDevice, st));
+            mtp_rows(1, s.mtp_src, s.tokens, base);
+        }
+        uint32_t res[MAX_NB];
+        HIPCHK(hipMemcpyAsync(res, s.mtp_out, rows * 4, hipMemcpyDeviceToHost, st));
+        HIPCHK(hipStreamSynchronize(st));
+        uint32_t d = res[rows - 1];
+        if (first) {
+            mtp_len = batch_pos + n;
+            if (rows - 1 != 0)
+                HIPCHK(hipMemcpyAsync(s.mtp_hyper, s.mtp_hyper + (uint64_t)(rows - 1) * D.hh, D.hh * 4,
+                                      hipMemcpyDeviceToDevice, st));
+        }
+        if (ci < chain) out.push_back(d);
+        token = d;
+        first = false;
+        last_mtp_rows = rows;
+    }
+    HIPCHK(hipStreamSynchronize(st));
+    for (size_t i = 0; i < out.size(); ++i) drafts[i] = out[i];
+    *nd = (uint32_t)out.size();
+    mtp_logits_fresh = false;
+}
+
+// Prompt processing through the row path: rows of up to MAX_NB tokens,
+// committed as they go, MTP cache kept in step (gpu/prefill.rs semantics:
+// side effects identical to row stepping, prefill.rs:13-15).
+void ChkEngine::prefill(const uint32_t* toks, uint32_t n, uint32_t* next, uint32_t* draft) {
+    ensure(n >= 1, "empty prefill chunk");
+    ensure(pos + n <= max_t, "context capacity exceeded");
+    uint32_t saved_rows = trunk_rows;
+    trunk_rows = MAX_NB;
+    uint32_t last = 0;
+    try {
+        for (uint32_t i = 0; i < n; i += MAX_NB) {
+            uint32_t m = std::min<uint32_t>(MAX_NB, n - i);
+            uint32_t out[MAX_NB];
+            step_rows(toks + i, m, false, false, out);
+            commit(m);
+            if (has_mtp) {
+                // MTP cache rows for these positions pair each row with the
+                // token after it (the next prompt token, or the prediction)
+                uint32_t nx[MAX_NB];
+                for (uint32_t r = 0; r < m; ++r) nx[r] = (i + r + 1 < n) ? toks[i + r + 1] : out[r];
+                uint32_t d[4], nd = 0;
+                mtp_draft(nx, m, i + m >= n ? 1 : 0, d, &nd);
+                if (i + m >= n) *draft = nd ? d[0] : 0xffffffffu;
+            }
+            last = out[m - 1];
+        }
+    } catch (...) {
+        trunk_rows = saved_rows;
+        throw;
+    }
+    trunk_rows = saved_rows;
+    *next = last;
+    if (!has_mtp) *draft = 0xffffffffu;
+}
+
+// ===================================================================== C ABI
+
+#define CHK_TRY(...)                   \
+    try {                              \
+        __VA_ARGS__;                   \
+        return 0;                      \
+    } catch (const std::exception& e_) { \
+        chk::g_err = e_.what();        \
+        return -1;                     \
+    }
+
+extern "C" {
+
+const char* chk_last_error(void) { return chk::g_err.c_str(); }
+
+int chk_engine_load(const ChkConfig* cfg, const ChkOptions* opt, ChkEngine** out) {
+    *out = nullptr;
+    auto e = std::make_unique<ChkEngine>();
+    CHK_TRY(e->load(cfg, opt); *out = e.release())
+}
+
+void chk_engine_free(ChkEngine* e) { delete e; }
+
+int chk_step_rows(ChkEngine* e, const uint32_t* tokens, uint32_t n, int snap, int fold_mtp, uint32_t* out) {
+    CHK_TRY(e->step_rows(tokens, n, snap != 0, fold_mtp != 0, out))
+}
+
+int chk_step(ChkEngine* e, uint32_t token, uint32_t* out) {
+    CHK_TRY(e->step_rows(&token, 1, false, false, out); e->commit(1))
+}
+
+int chk_commit(ChkEngine* e, uint32_t n) { CHK_TRY(e->commit(n)) }
+
+int chk_reset(ChkEngine* e) { CHK_TRY(e->reset_state(); HIPCHK(hipStreamSynchronize(e->st))) }
+
+int chk_mtp_draft(ChkEngine* e, const uint32_t* next, uint32_t n, uint32_t chain, uint32_t* drafts,
+                  uint32_t* n_drafts) {
+    CHK_TRY(e->mtp_draft(next, n, chain, drafts, n_drafts))
+}
+
+int chk_mtp_chain(ChkEngine* e, uint32_t draft, uint32_t* out) {
+    CHK_TRY({
+        ensure(e->has_mtp, "no MTP head");
+        ensure(e->pos + 1 <= e->max_t, "context capacity exceeded");
+        HIPCHK(hipMemcpyAsync(e->s.tokens, &draft, 4, hipMemcpyHostToDevice, e->st));
+        HIPCHK(hipMemcpyAsync(e->s.mtp_src, e->s.mtp_hyper, e->D.hh * 4, hipMemcpyDeviceToDevice, e->st));
+        e->mtp_rows(1, e->s.mtp_src, e->s.tokens, e->pos);
+        HIPCHK(hipMemcpyAsync(out, e->s.mtp_out, 4, hipMemcpyDeviceToHost, e->st));
+        HIPCHK(hipStreamSynchronize(e->st));
+        e->mtp_logits_fresh = false;
+    })
+}
+
+int chk_prefill_chunk(ChkEngine* e, const uint32_t* tokens, uint32_t n, uint32_t* next, uint32_t* draft) {
+    CHK_TRY(e->prefill(tokens, n, next, draft))
+}
+
+const float* chk_logits_row(ChkEngine* e, uint32_t r) {
+    if (r >= e->batch_nb) {
+        chk::g_err = "logits row out of range";
+        return nullptr;
+    }
+    if (!e->logits_fresh) {
+        if (hipMemcpy(e->host_logits.data(), e->s.logits, (size_t)e->batch_nb * e->D.V * 4, hipMemcpyDeviceToHost) !=
+            hipSuccess) {
+            chk::g_err = "logits copy failed";
+            return nullptr;
+        }
+        e->logits_fresh = true;
+    }
+    return e->host_logits.data() + (size_t)r * e->D.V;
+}
+
+const float* chk_mtp_logits_row(ChkEngine* e, uint32_t r) {
+    if (!e->has_mtp || r >= std::max<uint32_t>(e->last_mtp_rows, 1)) {
+        chk::g_err = "MTP logits row out of range";
+        return nullptr;
+    }
+    if (!e->mtp_logits_fresh) {
+        if (hipMemcpy(e->host_mtp_logits.data(), e->s.mtp_logits, (size_t)e->last_mtp_rows * e->D.V * 4,
+                      hipMemcpyDeviceToHost) != hipSuccess) {
+            chk::g_err = "logits copy failed";
+            return nullptr;
+        }
+        e->mtp_logits_fresh = true;
+    }
+    return e->host_mtp_logits.data() + (size_t)r * e->D.V;
+}
+
+uint32_t chk_pos(const ChkEngine* e) { return e->pos; }
+uint32_t chk_eos_token(const ChkEngine* e) { return e->c.eos_token_id; }
+uint32_t chk_max_t(const ChkEngine* e) { return e->max_t; }
+uint32_t chk_trunk_rows(const ChkEngine* e) { return e->trunk_rows; }
+int chk_has_mtp(const ChkEngine* e) { return e->has_mtp ? 1 : 0; }
+
+int chk_memory_stats(const ChkEngine* e, ChkMemoryStats* m) {
+    uint64_t nrec = (uint64_t)e->record_layers * e->D.E;
+    m->dense = e->dense_bytes;
+    m->experts = nrec * e->rl4.stride;
+    m->experts_low_bit = e->experts_lo ? nrec * e->rllo.stride : 0;
+    m->state = e->state_bytes;
+    m->kv_cache = e->kv_bytes;
+    m->scratch = e->scratch_bytes;
+    m->total = m->dense + m->experts + m->experts_low_bit + m->state + m->kv_cache + m->scratch;
+    return 0;
+}
+
+uint32_t chk_pool_slots(const ChkEngine* e) { return e->record_layers * e->D.E; }
+uint32_t chk_pool_resident(const ChkEngine* e) { return e->record_layers * e->D.E; }
+int chk_pool_is_member(const ChkEngine* e, uint32_t rid) { return rid < e->record_layers * e->D.E ? 1 : 0; }
+uint32_t chk_pool_acquire(ChkEngine* e, const uint32_t* rids, uint32_t n, uint32_t* need) {
+    (void)e; (void)rids; (void)n; (void)need;
+    return 0;  // every record is resident: nothing to read
+}
+uint64_t chk_pool_addr(const ChkEngine* e, uint32_t rid) {
+    if (rid >= e->record_layers * e->D.E) return 0;
+    if (e->o.experts == 4) return (uint64_t)(uintptr_t)e->experts4 + (uint64_t)rid * e->rl4.stride;
+    uint64_t tag = e->o.experts == 3 ? (1ull << 63) : (1ull << 62);
+    return ((uint64_t)(uintptr_t)e->experts_lo + (uint64_t)rid * e->rllo.stride) | tag;
+}
+uint32_t chk_pool_kind(const ChkEngine* e, uint32_t rid) {
+    (void)rid;
+    return e->o.experts == 3 ? 1u : (e->o.experts == 2 ? 2u : 0u);
+}
+uint64_t chk_pool_bytes(const ChkEngine* e) {
+    uint64_t nrec = (uint64_t)e->record_layers * e->D.E;
+    return nrec * e->rl4.stride + (e->experts_lo ? nrec * e->rllo.stride : 0);
+}
+
+int chk_last_routes(const ChkEngine* e, uint32_t layer, uint32_t r, uint32_t* ids, float* weights) {
+    CHK_TRY({
+        ensure(layer < e->record_layers, "layer out of range");
+        ensure(r < MAX_NB, "row out of range");
+        uint64_t off = ((uint64_t)layer * MAX_NB + r) * e->D.topk;
+        HIPCHK(hipMemcpy(ids, e->s.route_ids + off, e->D.topk * 4, hipMemcpyDeviceToHost));
+        if (weights) HIPCHK(hipMemcpy(weights, e->s.route_w + off, e->D.topk * 4, hipMemcpyDeviceToHost));
+    })
+}
+
+// ------------------------------------------------------ kernel-level ABI
+
+int chk_q4_matvec(const void* w, const void* s, const void* b, uint32_t out, uint32_t in, const float* x, float* y,
+                  uint32_t nb, void* stream) {
+    CHK_TRY({
+        ensure(nb >= 1 && nb <= (uint32_t)MAX_NB, "nb must be 1..=4");
+        ensure(in % 64 == 0 && in > 0 && out > 0, "in must be a positive multiple of 64");
+        SegArgs a{};
+        a.nseg = 1;
+        a.seg[0] = Seg{Q4Mat{(const uint32_t*)w, (const uint16_t*)s, (const uint16_t*)b, out, in}, x, y, in, out, 0,
+                       EPI_RAW};
+        a.total = out;
+        hipStream_t st = (hipStream_t)stream;
+        launch_qmv(a, (int)nb, st);
+        HIPCHK(hipStreamSynchronize(st));
+        HIPCHK(hipGetLastError());
+    })
+}
+
+static const LayerDev* layer_dev(ChkEngine* e, uint32_t layer) {
+    if (layer < e->c.num_hidden_layers) return &e->layers[layer];
+    if (layer == e->c.num_hidden_layers && e->has_mtp) return &e->mtp_layer;
+    throw Error("layer out of range");
+}
+
+int chk_moe_block(ChkEngine* e, uint32_t layer, const float* x, uint32_t nb, float* out, uint32_t* top_ids,
+                  float* top_w, float* probs) {
+    CHK_TRY({
+        ensure(nb >= 1 && nb <= (uint32_t)MAX_NB, "nb must be 1..=4");
+        const LayerDev* L = layer_dev(e, layer);
+        e->moe(*L, layer, x, (int)nb, nullptr, nullptr, out);
+        uint64_t off = (uint64_t)layer * MAX_NB;
+        if (top_ids)
+            HIPCHK(hipMemcpyAsync(top_ids, e->s.route_ids + off * e->D.topk, nb * e->D.topk * 4,
+                                  hipMemcpyDeviceToDevice, e->st));
+        if (top_w)
+            HIPCHK(hipMemcpyAsync(top_w, e->s.route_w + off * e->D.topk, nb * e->D.topk * 4, hipMemcpyDeviceToDevice,
+                                  e->st));
+        if (probs)
+            HIPCHK(hipMemcpyAsync(probs, e->s.router_probs + off * e->D.E, nb * e->D.E * 4, hipMemcpyDeviceToDevice,
+                                  e->st));
+        HIPCHK(hipStreamSynchronize(e->st));
+        HIPCHK(hipGetLastError());
+    })
+}
+
+int chk_deltanet_block(ChkEngine* e, uint32_t layer, const float* x, uint32_t nb, int snap, float* out) {
+    CHK_TRY({
+        ensure(nb >= 1 && nb <= (uint32_t)MAX_NB, "nb must be 1..=4");
+        ensure(layer < e->c.num_hidden_layers && e->layers[layer].linear, "not a DeltaNet layer");
+        e->deltanet(e->layers[layer], x, (int)nb, snap != 0, nullptr, nullptr, out);
+        HIPCHK(hipStreamSynchronize(e->st));
+        HIPCHK(hipGetLastError());
+    })
+}
+
+int chk_deltanet_state(ChkEngine* e, uint32_t layer, float* s_host, float* conv_host) {
+    CHK_TRY({
+        ensure(layer < e->c.num_hidden_layers && e->layers[layer].linear, "not a DeltaNet layer");
+        int di = e->layers[layer].dn_idx;
+        const Dims& D = e->D;
+        if (s_host) {
+            std::vector<float> t((size_t)D.nv * D.dv * D.dk);
+            HIPCHK(hipMemcpy(t.data(), e->dn_state[di], t.size() * 4, hipMemcpyDeviceToHost));
+            for (uint32_t h = 0; h < D.nv; ++h)
+                for (uint32_t iv = 0; iv < D.dv; ++iv)
+                    for (uint32_t ik = 0; ik < D.dk; ++ik)
+                        s_host[((size_t)h * D.dk + ik) * D.dv + iv] = t[((size_t)h * D.dv + iv) * D.dk + ik];
+        }
+        if (conv_host)
+            HIPCHK(hipMemcpy(conv_host, e->dn_hist[di], (size_t)D.conv_dim * (D.ck - 1) * 4, hipMemcpyDeviceToHost));
+    })
+}
+
+int chk_deltanet_rollback(ChkEngine* e, uint32_t layer, uint32_t plane) {
+    CHK_TRY({
+        ensure(layer < e->c.num_hidden_layers && e->layers[layer].linear, "not a DeltaNet layer");
+        ensure(plane < (uint32_t)MAX_SNAP, "snapshot plane out of range");
+        int di = e->layers[layer].dn_idx;
+        uint64_t sn = (uint64_t)e->D.nv * e->D.dv * e->D.dk, hn = (uint64_t)e->D.conv_dim * (e->D.ck - 1);
+        launch_copy_f32(e->dn_state[di], e->dn_snap_state[di] + plane * sn, sn, e->st);
+        launch_copy_f32(e->dn_hist[di], e->dn_snap_hist[di] + plane * hn, hn, e->st);
+        HIPCHK(hipStreamSynchronize(e->st));
+    })
+}
+
+int chk_attention_block(ChkEngine* e, uint32_t layer, const float* x, uint32_t nb, uint32_t pos, float* out) {
+    CHK_TRY({
+        ensure(nb >= 1 && nb <= (uint32_t)MAX_NB, "nb must be 1..=4");
+        ensure(layer < e->c.num_hidden_layers && !e->layers[layer].linear, "not an attention layer");
+        ensure(pos + nb <= e->max_t, "context capacity exceeded");
+        const LayerDev& L = e->layers[layer];
+        KvDev kvs[MAX_NB];
+        uint32_t rp[MAX_NB];
+        for (uint32_t b = 0; b < nb; ++b) {
+            kvs[b] = e->kv[L.at_idx];
+            rp[b] = pos + b;
+        }
+        e->attention(L, x, (int)nb, kvs, rp, nullptr, nullptr, out);
+        HIPCHK(hipStreamSynchronize(e->st));
+        HIPCHK(hipGetLastError());
+    })
+}
+
+int chk_kv_fill(ChkEngine* e, uint32_t layer, uint32_t seq, const float* k, const float* v, uint32_t T) {
+    CHK_TRY({
+        ensure(layer < e->c.num_hidden_layers && !e->layers[layer].linear, "not an attention layer");
+        ensure(seq <= 1, "sequence slot must be 0 or 1");
+        ensure(T <= e->max_t, "context capacity exceeded");
+        int ai = e->layers[layer].at_idx;
+        if (seq == 1 && e->kv2.empty())
+            for (size_t i = 0; i < e->kv.size(); ++i) e->kv2.push_back(e->alloc_kv());
+        KvDev kv = seq == 0 ? e->kv[ai] : e->kv2[ai];
+        launch_kv_fill(k, v, kv, e->D.kv_row, T, e->st);
+        HIPCHK(hipStreamSynchronize(e->st));
+        HIPCHK(hipGetLastError());
+    })
+}
+
+int chk_attention_block2(ChkEngine* e, uint32_t layer, const float* x, const uint32_t* pos, float* out) {
+    CHK_TRY({
+        ensure(layer < e->c.num_hidden_layers && !e->layers[layer].linear, "not an attention layer");
+        ensure(!e->kv2.empty(), "second sequence slot not initialised (chk_kv_fill seq 1)");
+        ensure(pos[0] < e->max_t && pos[1] < e->max_t, "context capacity exceeded");
+        const LayerDev& L = e->layers[layer];
+        KvDev kvs[MAX_NB] = {e->kv[L.at_idx], e->kv2[L.at_idx]};
+        uint32_t rp[MAX_NB] = {pos[0], pos[1]};
+        e->attention(L, x, 2, kvs, rp, nullptr, nullptr, out);
+        HIPCHK(hipStreamSynchronize(e->st));
+        HIPCHK(hipGetLastError());
+    })
+}
+
+int chk_hc_read(ChkEngine* e, uint32_t layer, uint32_t which, const float* hyper, uint32_t nb, float* mixed,
+                float* inj) {
+    CHK_TRY({
+        ensure(nb >= 1 && nb <= (uint32_t)MAX_NB, "nb must be 1..=4");
+        const HcDev* w = nullptr;
+        if (which == CHK_HC_FINAL) w = &e->final_mixer;
+        else if (which == CHK_HC_MTP) {
+            ensure(e->has_mtp, "no MTP head");
+            w = &e->mtp_mixer;
+        } else {
+            const LayerDev* L = layer_dev(e, layer);
+            w = which == CHK_HC_ATTN ? &L->attn_hc : &L->mlp_hc;
+        }
+        e->hc_read(*w, hyper, e->s.inj_a, (int)nb);
+        HIPCHK(hipMemcpyAsync(mixed, e->s.mixed, (size_t)nb * e->D.H * 4, hipMemcpyDeviceToDevice, e->st));
+        if (inj && w->has_inject)
+            HIPCHK(hipMemcpyAsync(inj, e->s.inj_a, (size_t)nb * e->D.hc * 4, hipMemcpyDeviceToDevice, e->st));
+        HIPCHK(hipStreamSynchronize(e->st));
+        HIPCHK(hipGetLastError());
+    })
+}
+
+int chk_expert_record(ChkEngine* e, uint32_t layer, uint32_t expert, uint32_t bits, void* host, uint64_t n) {
+    CHK_TRY({
+        ensure(layer < e->record_layers && expert < e->D.E, "record out of range");
+        const uint8_t* base;
+        uint64_t stride;
+        if (bits == 4) {
+            base = e->experts4;
+            stride = e->rl4.stride;
+        } else {
+            ensure(e->experts_lo && bits == e->o.experts, "no low-bit store of that precision");
+            base = e->experts_lo;
+            stride = e->rllo.stride;
+        }
+        ensure(n <= stride, "copy larger than the record stride");
+        HIPCHK(hipMemcpy(host, base + ((uint64_t)layer * e->D.E + expert) * stride, n, hipMemcpyDeviceToHost));
+    })
+}
+
+uint64_t chk_record_stride(const ChkEngine* e, uint32_t bits) {
+    if (bits == 4) return e->rl4.stride;
+    return e->experts_lo && bits == e->o.experts ? e->rllo.stride : 0;
+}
+
+int chk_trace_enable(ChkEngine* e, int on) {
+    CHK_TRY({
+        e->tracing = on != 0;
+        if (e->tracing && !e->s.trace)
+            e->s.trace = e->dalloc<float>((uint64_t)e->c.num_hidden_layers * MAX_NB * e->D.hh);
+    })
+}
+
+int chk_layer_hyper(ChkEngine* e, uint32_t layer, uint32_t r, float* host) {
+    CHK_TRY({
+        ensure(e->s.trace, "tracing is off");
+        ensure(layer < e->c.num_hidden_layers && r < MAX_NB, "out of range");
+        HIPCHK(hipMemcpy(host, e->s.trace + ((uint64_t)layer * MAX_NB + r) * e->D.hh, e->D.hh * 4,
+                         hipMemcpyDeviceToHost));
+    })
+}
+
+int chk_profile_kernel(ChkEngine* e, int kind) {
+    CHK_TRY({
+        ensure(kind >= 0 && kind <= 3, "unknown kernel class");
+        e->prof_collect();
+        e->prof_kind = kind;
+        e->prof_ms = 0.0;
+        e->prof_bytes = 0;
+        e->prof_launches = 0;
+    })
+}
+
+int chk_profile_read(ChkEngine* e, double* ms_total, uint64_t* launches, uint64_t* bytes) {
+    CHK_TRY({
+        e->prof_collect();
+        *ms_total = e->prof_ms;
+        *launches = e->prof_launches;
+        *bytes = e->prof_bytes;
+    })
+}
+
+int chk_time_decode(ChkEngine* e, uint32_t first_token, uint32_t steps, float* ms_per_step, uint32_t* last_token) {
+    CHK_TRY({
+        ensure(e->pos + steps <= e->max_t, "context capacity exceeded");
+        hipEvent_t a, b;
+        HIPCHK(hipEventCreate(&a));
+        HIPCHK(hipEventCreate(&b));
+        uint32_t tok = first_token;
+        HIPCHK(hipEventRecord(a, e->st));
+        for (uint32_t i = 0; i < steps; ++i) {
+            uint32_t out;
+            e->step_rows(&tok, 1, false, false, &out);
+            e->commit(1);
+            tok = out;
+        }
+        HIPCHK(hipEventRecord(b, e->st));
+        HIPCHK(hipEventSynchronize(b));
+        float ms = 0;
+        HIPCHK(hipEventElapsedTime(&ms, a, b));
+        *ms_per_step = steps ? ms / steps : 0.0f;
+        *last_token = tok;
+        hipEventDestroy(a);
+        hipEventDestroy(b);
+    })
+}
+
+}  // extern "C"

@@ -1,0 +1,99 @@
+/* Kernel-level test ABI: the engine's blocks and primitives one at a time,
+ * on device buffers the caller owns.  These have no single counterpart in
+ * the reference's public API; they expose, for parity tests and block
+ * benchmarks, the pieces the reference engine dispatches inside
+ * `Gpu::step_rows` (gpu/decode.rs:13-294):
+ *   chk_q4_matvec         qmv_multi_h / fn_qmv_small_b (quant.rs:49-88 semantics)
+ *   chk_moe_block         router_b + experts_b (gpu/experts.rs:8-187)
+ *   chk_deltanet_block    deltanet_b (gpu/deltanet.rs:8-113)
+ *   chk_attention_block   attention_b (gpu/attention.rs:10-273)
+ *   chk_hc_read           hc_read_b (gpu/hyperconnection.rs:59-152)
+ * Device pointers are plain addresses (e.g. torch's data_ptr()); `stream`
+ * is a hipStream_t (0 = the engine's stream).  Calls are stream-ordered and
+ * synchronous on return.
+ */
+#ifndef CHERENKOV_KERNELS_H
+#define CHERENKOV_KERNELS_H
+
+#include <stdint.h>
+
+#include "cherenkov/engine.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* y[b][r] = sum_g s[r,g] sum_j q x_b + b[r,g] sum_j x_b for b < nb <= 4.
+ * w u32 [out][in/8], s/b bf16 [out][in/64], x f32 [nb][in], y f32 [nb][out]. */
+int chk_q4_matvec(const void* w, const void* s, const void* b, uint32_t out, uint32_t in, const float* x,
+                  float* y, uint32_t nb, void* stream);
+
+/* MoE block of decoder layer `layer` (num_hidden_layers = the MTP layer) on
+ * normalised inputs x [nb][H]: out [nb][H] = routed experts (per the
+ * engine's expert precision) + sigmoid-gated shared expert; top_ids
+ * [nb][k] u32 and top_w [nb][k] f32 receive the routing; probs [nb][E]
+ * (optional) the router softmax. */
+int chk_moe_block(ChkEngine* e, uint32_t layer, const float* x, uint32_t nb, float* out, uint32_t* top_ids,
+                  float* top_w, float* probs);
+
+/* DeltaNet mixer of decoder layer `layer` on x [nb][H] -> out [nb][H],
+ * advancing that layer's recurrent state and conv history (snapshots
+ * after each row but the last when `snap`). */
+int chk_deltanet_block(ChkEngine* e, uint32_t layer, const float* x, uint32_t nb, int snap, float* out);
+
+/* Copy a DeltaNet layer's state [nv][dk][dv] (the reference's CPU order)
+ * and conv history [conv_dim][k-1] to host buffers. */
+int chk_deltanet_state(ChkEngine* e, uint32_t layer, float* s_host, float* conv_host);
+
+/* Restore snapshot plane `plane` of a DeltaNet layer into its live state
+ * (the commit rollback, gpu/state.rs:20-47). */
+int chk_deltanet_rollback(ChkEngine* e, uint32_t layer, uint32_t plane);
+
+/* Attention mixer of decoder layer `layer` on x [nb][H] for the engine's
+ * sequence at positions pos.. (rows see positions <= their own) ->
+ * out [nb][H]; appends K/V (q8) and index keys at those positions. */
+int chk_attention_block(ChkEngine* e, uint32_t layer, const float* x, uint32_t nb, uint32_t pos, float* out);
+
+/* Fill positions [0, T) of attention layer `layer`'s q8 KV cache by
+ * quantising k, v f32 [T][nkv * hd] with the engine's q8 rule.
+ * `seq` selects the engine's sequence (0) or a second sequence slot (1)
+ * used by the batch-2 attention decode below. */
+int chk_kv_fill(ChkEngine* e, uint32_t layer, uint32_t seq, const float* k, const float* v, uint32_t T);
+
+/* Batch-2 attention decode over two independent sequences (two interleaved
+ * requests): row b uses sequence slot b at position pos[b]. */
+int chk_attention_block2(ChkEngine* e, uint32_t layer, const float* x, const uint32_t* pos, float* out);
+
+/* Hyper-connection read `which` (0 attn, 1 mlp, 2 final mixer, 3 MTP
+ * mixer) of layer `layer` on hyper [nb][hc H] -> mixed [nb][H] and the
+ * injection weights inj [nb][hc] (absent for the mixers). */
+int chk_hc_read(ChkEngine* e, uint32_t layer, uint32_t which, const float* hyper, uint32_t nb, float* mixed,
+                float* inj);
+
+/* Copy `n` bytes of the routed-expert store record (layer, expert) in the
+ * Q4 layout (bits = 4) or the engine's low-bit layout (bits = 3 or 2). */
+int chk_expert_record(ChkEngine* e, uint32_t layer, uint32_t expert, uint32_t bits, void* host, uint64_t n);
+uint64_t chk_record_stride(const ChkEngine* e, uint32_t bits);
+
+/* Per-layer trace of the trunk residual: when enabled, each step keeps
+ * hyper after every layer; chk_layer_hyper copies layer l, row r. */
+int chk_trace_enable(ChkEngine* e, int on);
+int chk_layer_hyper(ChkEngine* e, uint32_t layer, uint32_t r, float* host);
+
+/* Live kernel profiler: bracket every launch of one kernel class with HIP
+ * events on the engine's stream (1 = MoE experts gate/up + down,
+ * 2 = DeltaNet input projections, 3 = LM head + argmax; 0 = off) and
+ * accumulate its algorithmic HBM bytes; chk_profile_read returns the
+ * summed event time, launch count and bytes since chk_profile_kernel. */
+int chk_profile_kernel(ChkEngine* e, int kind);
+int chk_profile_read(ChkEngine* e, double* ms_total, uint64_t* launches, uint64_t* bytes);
+
+/* Time the decode step on the engine's stream: runs `steps` step_rows(1)
+ * + commit pairs, returns milliseconds per step (HIP events). */
+int chk_time_decode(ChkEngine* e, uint32_t first_token, uint32_t steps, float* ms_per_step, uint32_t* last_token);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif
