@@ -141,22 +141,22 @@ __global__ void __launch_bounds__(256) k_attn_combine(AttnArgs a) {
     }
 }
 
-__global__ void k_copy_f32(float* __restrict__ dst, const float* __restrict__ src, uint64_t n) {
+__global__ void __launch_bounds__(256) k_copy_f32(float* __restrict__ dst, const float* __restrict__ src, uint64_t n) {
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = src[i];
 }
 
-__global__ void k_zero_f32(float* __restrict__ dst, uint64_t n) {
+__global__ void __launch_bounds__(256) k_zero_f32(float* __restrict__ dst, uint64_t n) {
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = 0.0f;
 }
 
+// Positions come from device memory and the chunk grid covers the whole
+// context capacity (chunks past a row's length exit at once), so the
+// launch is the same every step and can live in a captured graph.
 void launch_attn(const AttnArgs& a, int nb, hipStream_t st) {
     k_attn_prep<<<dim3(a.nh + 2 * a.nkv + 1, nb), a.hd, 0, st>>>(a);
-    uint32_t maxT = 0;
-    for (int b = 0; b < nb; ++b) maxT = std::max(maxT, a.pos[b] + 1);
-    uint32_t nc = (maxT + ATTN_CHUNK - 1) / ATTN_CHUNK;
-    k_attn_part<<<dim3(a.nh, nc, nb), ATTN_CHUNK, 0, st>>>(a);
+    k_attn_part<<<dim3(a.nh, a.max_chunks, nb), ATTN_CHUNK, 0, st>>>(a);
     k_attn_combine<<<dim3(a.nh, nb), 256, 0, st>>>(a);
 }
 

@@ -1,11 +1,17 @@
 // Decode / verify kernels for the qwen4_exp token loop on gfx950 (wave64).
 //
 // One step runs `nb` <= 4 rows (one committed token plus drafts).  Every
-// weight matrix is streamed from HBM once per step for all rows: the row
-// loop sits inside each wave, after the weight load.  Reference semantics:
-// /root/reference/src/qwen4_exp/cpu.rs (forward_token and the blocks it
-// calls); the Metal dispatch plan it replaces: src/qwen4_exp/gpu/decode.rs:
-// 13-294 and kernels/{common,qwen4_exp}/*.metal.
+// weight matrix is streamed from HBM once per step for all rows.  Batch-1
+// decode is a chain of HBM-bound matvecs, so each wave keeps its slice of
+// the input vector in VGPRs and issues the weight loads of R rows before it
+// consumes any of them (R x 16 B in flight per lane), on grids that stride
+// over row blocks instead of spawning a wave per row.
+//
+// Reference semantics: /root/reference/src/qwen4_exp/cpu.rs (forward_token
+// and the blocks it calls); the Metal dispatch plan this replaces:
+// src/qwen4_exp/gpu/decode.rs:13-294 and kernels/{common,qwen4_exp}/*.metal.
+#include <stdexcept>
+
 #include "kernels_internal.h"
 
 namespace chk {
@@ -26,105 +32,228 @@ CHK_DEV void ldx32(const float* p, float* x) {
     }
 }
 
-// Row r of a Q4 matrix dotted with NB input rows; LPR lanes per matrix row,
-// lane `lir` takes 32-input chunks lir, lir + LPR, ...  Returns the full dot
-// in every lane of the row group.
-template <int LPR, int NB>
-CHK_DEV void q4_dot(const Q4Mat& m, uint32_t r, const float* __restrict__ x, uint32_t xs, int lir, float* acc) {
-    const uint32_t nch = m.in >> 5;
-    const uint32_t* wr = m.w + (size_t)r * (m.in >> 3);
-    const uint16_t* sr = m.s + (size_t)r * (m.in >> 6);
-    const uint16_t* br = m.b + (size_t)r * (m.in >> 6);
+// This lane's input chunks (ch = lir + c * LPR, c < CPL) of NB input rows
+// and their sums.  Lanes past the last chunk read chunk nch-1 (a valid
+// address) and zero it, so the loads stay unconditional.
+template <int NB, int CPL>
+struct XFrag {
+    float v[NB][CPL][32];
+    float s[NB][CPL];
+
+    template <int LPR>
+    CHK_DEV void load(const float* __restrict__ x, uint32_t xs, uint32_t nch, int lir) {
 #pragma unroll
-    for (int b = 0; b < NB; ++b) acc[b] = 0.0f;
-    for (uint32_t c = lir; c < nch; c += LPR) {
-        uint4 wq = ldw4(wr + c * 4);
-        float s = bf16f(sr[c >> 1]), bb = bf16f(br[c >> 1]);
+        for (int c = 0; c < CPL; ++c) {
+            const uint32_t ch = lir + c * LPR;
+            const uint32_t cc = ch < nch ? ch : nch - 1;
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            float xv[32];
-            ldx32(x + (size_t)b * xs + c * 32, xv);
-            acc[b] += q4_chunk(wq, xv, s, bb);
+            for (int b = 0; b < NB; ++b) ldx32(x + (size_t)b * xs + cc * 32, v[b][c]);
+            if (ch >= nch)
+#pragma unroll
+                for (int b = 0; b < NB; ++b)
+#pragma unroll
+                    for (int j = 0; j < 32; ++j) v[b][c][j] = 0.0f;
         }
     }
+    CHK_DEV void sums() {
 #pragma unroll
-    for (int b = 0; b < NB; ++b) acc[b] = group_sum<LPR>(acc[b]);
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+                float t = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 32; ++j) t += v[b][c][j];
+                s[b][c] = t;
+            }
+    }
+};
+
+template <int LPR, int CPL, int NB>
+CHK_DEV void load_x(const float* __restrict__ x, uint32_t xs, uint32_t nch, int lir, XFrag<NB, CPL>& xf) {
+    xf.template load<LPR>(x, xs, nch, lir);
+    xf.sums();
 }
 
-// Low-bit (Q3/Q2) 32-code chunk in the lowbit.rs layout; codes reconstruct
-// at the midpoint (2q + 0.5 or 4q + 1.5) of the Q4 range they cover:
-// w = mid * s + b, so the chunk partial is s * (step * sum(q x) + half * sum(x)) + b * sum(x).
-template <int BITS>
-CHK_DEV float lowbit_chunk(const uint8_t* p, const float* x, float s, float b) {
-    float qd = 0.0f, xs = 0.0f;
-    uint32_t w0, w1, lo = 0;
-    if (BITS == 2) {
-        uint2 v = *reinterpret_cast<const uint2*>(p);
-        w0 = v.x; w1 = v.y;
-    } else {
-        const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
-        w0 = q[0]; w1 = q[1]; lo = q[2];
+// R rows of a Q4 matrix as this lane sees them: issue() starts every load
+// (unconditionally, raw bf16 scale/bias kept undecoded so nothing waits),
+// dot() consumes them against the lane's input chunks and reduces over the
+// LPR lanes of a row.  Splitting the two lets callers put independent
+// prologue/epilogue loads between them.
+template <int LPR, int CPL, int R>
+struct Q4Frag {
+    uint4 wq[R][CPL];
+    uint16_t s16[R][CPL], b16[R][CPL];
+    bool ok[CPL];
+
+    CHK_DEV void issue(const Q4Mat& m, const uint32_t (&rows)[R], int lir) {
+        const uint32_t wpr = m.in >> 3, gpr = m.in >> 6, nch = m.in >> 5;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const uint32_t ch = lir + c * LPR;
+            ok[c] = ch < nch;
+            const uint32_t cc = ok[c] ? ch : nch - 1;
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                wq[i][c] = ldw4(m.w + (size_t)rows[i] * wpr + cc * 4);
+                s16[i][c] = m.s[(size_t)rows[i] * gpr + (cc >> 1)];
+                b16[i][c] = m.b[(size_t)rows[i] * gpr + (cc >> 1)];
+            }
+        }
     }
+
+    template <int NB>
+    CHK_DEV void dot(const XFrag<NB, CPL>& xf, float (&acc)[R][NB]) const {
+#pragma unroll
+        for (int i = 0; i < R; ++i)
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                float a = 0.0f;
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) {
+                    const float p = q4_chunk(wq[i][c], xf.v[b][c], xf.s[b][c], bf16f(s16[i][c]), bf16f(b16[i][c]));
+                    a += ok[c] ? p : 0.0f;
+                }
+                acc[i][b] = group_sum<LPR>(a);
+            }
+    }
+};
+
+template <int LPR, int CPL, int R, int NB>
+CHK_DEV void q4_block(const Q4Mat& m, const uint32_t (&rows)[R], const XFrag<NB, CPL>& xr, int lir,
+                      float (&acc)[R][NB]) {
+    Q4Frag<LPR, CPL, R> f;
+    f.issue(m, rows, lir);
+    f.template dot<NB>(xr, acc);
+}
+
+// Low-bit (Q3/Q2) 32-code chunk in the lowbit.rs layout (q2_slots /
+// q3_slots, lowbit.rs:143-184).  Codes reconstruct at the midpoint of the
+// Q4 range they cover, w = mid * s + b with mid = 2q + 0.5 (Q3) or
+// 4q + 1.5 (Q2), so a chunk contributes s * (step * sum(q x) + half * sum(x)) + b * sum(x).
+template <int BITS>
+CHK_DEV float lowbit_chunk(uint32_t w0, uint32_t w1, uint32_t lo, const float* x, float xs, float s, float b) {
+    float qd = 0.0f;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-        uint32_t w = t ? w1 : w0;
+        const uint32_t w = t ? w1 : w0;
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) {
 #pragma unroll
             for (int byte = 0; byte < 4; ++byte) {
                 uint32_t code = (w >> (8 * byte + 2 * pp)) & 3u;
                 if (BITS == 3) code = 2u * code + ((lo >> (8 * byte + 4 * t + pp)) & 1u);
-                int r = pp == 0 ? 2 * byte : pp == 1 ? 2 * byte + 8 : pp == 2 ? 2 * byte + 1 : 2 * byte + 9;
-                float xv = x[16 * t + r];
-                qd += (float)code * xv;
+                const int r = pp == 0 ? 2 * byte : pp == 1 ? 2 * byte + 8 : pp == 2 ? 2 * byte + 1 : 2 * byte + 9;
+                qd += (float)code * x[16 * t + r];
             }
         }
     }
-#pragma unroll
-    for (int j = 0; j < 32; ++j) xs += x[j];
     const float step = BITS == 2 ? 4.0f : 2.0f, half = BITS == 2 ? 1.5f : 0.5f;
     return s * (step * qd + half * xs) + b * xs;
 }
 
-// Expert projection `part` (0 gate, 1 up, 2 down) row r, Q4 or low-bit.
-template <int LPR, int NB, int BITS>
-CHK_DEV void expert_dot(const ExpertsDev& X, const uint8_t* rec, int part, uint32_t out, uint32_t in, uint32_t r,
-                        const float* __restrict__ x, uint32_t xs, int lir, float* acc) {
-    uint64_t woff = part == 0 ? X.gate_w : part == 1 ? X.up_w : X.down_w;
-    uint64_t soff = part == 0 ? X.gate_s : part == 1 ? X.up_s : X.down_s;
-    uint64_t boff = part == 0 ? X.gate_b : part == 1 ? X.up_b : X.down_b;
-    if (BITS == 4) {
-        Q4Mat m{(const uint32_t*)(rec + woff), (const uint16_t*)(rec + soff), (const uint16_t*)(rec + boff), out, in};
-        q4_dot<LPR, NB>(m, r, x, xs, lir, acc);
-        return;
-    }
-    const uint32_t nch = in >> 5, cb = BITS == 2 ? 8 : 12;
-    const uint8_t* wr = rec + woff + (size_t)r * nch * cb;
-    const uint16_t* sr = (const uint16_t*)(rec + soff) + (size_t)r * (in >> 6);
-    const uint16_t* br = (const uint16_t*)(rec + boff) + (size_t)r * (in >> 6);
+// A routed-expert projection inside its record: Q4 view or low-bit pointers.
+struct ExpMat {
+    const uint8_t* w;
+    const uint16_t* s;
+    const uint16_t* b;
+    uint32_t out, in;
+};
+
+CHK_DEV ExpMat expert_mat(const ExpertsDev& X, const uint8_t* rec, int part, uint32_t out, uint32_t in) {
+    const uint64_t woff = part == 0 ? X.gate_w : part == 1 ? X.up_w : X.down_w;
+    const uint64_t soff = part == 0 ? X.gate_s : part == 1 ? X.up_s : X.down_s;
+    const uint64_t boff = part == 0 ? X.gate_b : part == 1 ? X.up_b : X.down_b;
+    return ExpMat{rec + woff, (const uint16_t*)(rec + soff), (const uint16_t*)(rec + boff), out, in};
+}
+
+// R rows of an expert projection (any precision), split like Q4Frag.
+template <int LPR, int CPL, int R, int BITS>
+struct ExpFrag {
+    Q4Frag<LPR, CPL, R> q;
+    uint32_t w0[BITS == 4 ? 1 : R][CPL], w1[BITS == 4 ? 1 : R][CPL], lo[BITS == 4 ? 1 : R][CPL];
+
+    CHK_DEV void issue(const ExpMat& m, const uint32_t (&rows)[R], int lir) {
+        if (BITS == 4) {
+            Q4Mat qm{(const uint32_t*)m.w, m.s, m.b, m.out, m.in};
+            q.issue(qm, rows, lir);
+            return;
+        }
+        const uint32_t nch = m.in >> 5, gpr = m.in >> 6, cb = BITS == 2 ? 8 : 12;
 #pragma unroll
-    for (int b = 0; b < NB; ++b) acc[b] = 0.0f;
-    for (uint32_t c = lir; c < nch; c += LPR) {
-        float s = bf16f(sr[c >> 1]), bb = bf16f(br[c >> 1]);
+        for (int c = 0; c < CPL; ++c) {
+            const uint32_t ch = lir + c * LPR;
+            q.ok[c] = ch < nch;
+            const uint32_t cc = q.ok[c] ? ch : nch - 1;
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            float xv[32];
-            ldx32(x + (size_t)b * xs + c * 32, xv);
-            acc[b] += lowbit_chunk<BITS>(wr + (size_t)c * cb, xv, s, bb);
+            for (int i = 0; i < R; ++i) {
+                const int ii = BITS == 4 ? 0 : i;
+                const uint8_t* p = m.w + ((size_t)rows[i] * nch + cc) * cb;
+                if (BITS == 2) {
+                    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+                    u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+                    w0[ii][c] = v.x; w1[ii][c] = v.y; lo[ii][c] = 0;
+                } else {
+                    const uint32_t* qq = reinterpret_cast<const uint32_t*>(p);
+                    w0[ii][c] = __builtin_nontemporal_load(qq);
+                    w1[ii][c] = __builtin_nontemporal_load(qq + 1);
+                    lo[ii][c] = __builtin_nontemporal_load(qq + 2);
+                }
+                q.s16[i][c] = m.s[(size_t)rows[i] * gpr + (cc >> 1)];
+                q.b16[i][c] = m.b[(size_t)rows[i] * gpr + (cc >> 1)];
+            }
         }
     }
+
+    template <int NB>
+    CHK_DEV void dot(const XFrag<NB, CPL>& xr, float (&acc)[R][NB]) const {
+        if (BITS == 4) {
+            q.template dot<NB>(xr, acc);
+            return;
+        }
 #pragma unroll
-    for (int b = 0; b < NB; ++b) acc[b] = group_sum<LPR>(acc[b]);
+        for (int i = 0; i < R; ++i)
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const int ii = BITS == 4 ? 0 : i;
+                float a = 0.0f;
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) {
+                    const float p = lowbit_chunk<BITS>(w0[ii][c], w1[ii][c], lo[ii][c], xr.v[b][c], xr.s[b][c],
+                                                       bf16f(q.s16[i][c]), bf16f(q.b16[i][c]));
+                    a += q.ok[c] ? p : 0.0f;
+                }
+                acc[i][b] = group_sum<LPR>(a);
+            }
+    }
+};
+
+template <int LPR, int CPL, int R, int NB, int BITS>
+CHK_DEV void exp_block(const ExpMat& m, const uint32_t (&rows)[R], const XFrag<NB, CPL>& xr, int lir,
+                       float (&acc)[R][NB]) {
+    ExpFrag<LPR, CPL, R, BITS> f;
+    f.issue(m, rows, lir);
+    f.template dot<NB>(xr, acc);
 }
+
+CHK_DEV uint32_t wave_id() { return threadIdx.x >> 6; }
+// Task order across the grid: consecutive tasks go to different workgroups
+// (and so CUs) before a workgroup takes a second one.
+CHK_DEV uint32_t global_wave() { return (threadIdx.x >> 6) * gridDim.x + blockIdx.x; }
+CHK_DEV uint32_t total_waves() { return gridDim.x * (blockDim.x >> 6); }
 
 // ------------------------------------------------------------------ embed
 // embed.dequant_row + replicate into hc streams (cpu.rs:399-407).  Uses
 // explicitly rounded mul/add so hyper starts bit-identical to the oracle.
-__global__ void k_embed(const uint32_t* __restrict__ tokens, Q4Mat emb, float* __restrict__ hyper, uint32_t H,
-                        uint32_t hc) {
+__global__ void __launch_bounds__(256) k_embed(const StepIn* __restrict__ in, uint32_t* __restrict__ tok_out,
+                                               uint32_t* __restrict__ rowpos, Q4Mat emb, float* __restrict__ hyper,
+                                               uint32_t H, uint32_t hc) {
     uint32_t b = blockIdx.y, i = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t tok = in->tokens[b];
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        tok_out[b] = tok;
+        rowpos[b] = in->pos + b;
+    }
     if (i >= H) return;
-    uint32_t tok = tokens[b];
     uint32_t word = emb.w[(size_t)tok * (H / 8) + i / 8];
     uint32_t g = i / 64;
     float s = bf16f(emb.s[(size_t)tok * (H / 64) + g]), bb = bf16f(emb.b[(size_t)tok * (H / 64) + g]);
@@ -136,126 +265,168 @@ __global__ void k_embed(const uint32_t* __restrict__ tokens, Q4Mat emb, float* _
 // ---------------------------------------------------------- hc read (down)
 // gated_residual first half (cpu.rs:461-475, 493-500): normed = grouped
 // RMSNorm(hyper) * w, d = silu(down(normed) / hc), inj = 2 sigmoid(inject(normed) / hc).
-// One wave per row of [down; inject]; each wave reads the whole hyper row,
-// so the per-stream RMS is a wave reduction (no extra pass).
-template <int NB>
-__global__ void k_hc_down(HcDev w, const float* __restrict__ hyper, float* __restrict__ d, float* __restrict__ inj,
-                          float* __restrict__ inv_out, uint32_t H, uint32_t hc, float eps) {
-    const int lane = threadIdx.x & 63;
-    const uint32_t row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    const uint32_t nrow = w.down.out + (w.has_inject ? w.inject.out : 0);
-    if (row >= nrow) return;
+// One workgroup per row of [down; inject]; wave g takes hc stream g, so its
+// RMS is a wave reduction, and the per-stream partial dots meet in LDS.
+template <int CPL, int NB>
+__global__ void __launch_bounds__(512) k_hc_down(HcDev w, const float* __restrict__ hyper, float* __restrict__ d,
+                                                 float* __restrict__ inj, float* __restrict__ inv_out, uint32_t H,
+                                                 uint32_t hc, float eps) {
+    __shared__ float red[8][NB];
+    const int lane = threadIdx.x & 63, g = (int)wave_id();
+    const uint32_t row = blockIdx.x;
     const Q4Mat& m = row < w.down.out ? w.down : w.inject;
     const uint32_t r = row < w.down.out ? row : row - w.down.out;
-    const uint32_t hh = H * hc, nch = hh >> 5;
-    float acc[NB][8], ss[NB][8];
+    const uint32_t hh = H * hc, nch = H >> 5;  // chunks per stream
+    const uint32_t* wr = m.w + (size_t)r * (hh >> 3) + (size_t)g * (H >> 3);
+    const uint16_t* sr = m.s + (size_t)r * (hh >> 6) + (size_t)g * (H >> 6);
+    const uint16_t* br = m.b + (size_t)r * (hh >> 6) + (size_t)g * (H >> 6);
+    uint4 wq[CPL];
+    float sc[CPL], bi[CPL];
 #pragma unroll
-    for (int b = 0; b < NB; ++b)
-#pragma unroll
-        for (int g = 0; g < 8; ++g) { acc[b][g] = 0.0f; ss[b][g] = 0.0f; }
-    const uint32_t* wr = m.w + (size_t)r * (hh >> 3);
-    const uint16_t* sr = m.s + (size_t)r * (hh >> 6);
-    const uint16_t* br = m.b + (size_t)r * (hh >> 6);
-    for (uint32_t c = lane; c < nch; c += 64) {
-        uint4 wq = ldw4(wr + c * 4);
-        float s = bf16f(sr[c >> 1]), bb = bf16f(br[c >> 1]);
-        uint32_t g = (c * 32) / H;
-        float nw[32];
-#pragma unroll
-        for (int j = 0; j < 32; ++j) nw[j] = bf16f(w.norm[c * 32 + j]);
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            float xv[32];
-            ldx32(hyper + (size_t)b * hh + c * 32, xv);
-            float sq = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 32; ++j) {
-                sq += xv[j] * xv[j];
-                xv[j] *= nw[j];
-            }
-            float part = q4_chunk(wq, xv, s, bb);
-#pragma unroll
-            for (int gg = 0; gg < 8; ++gg)
-                if (gg == (int)g) { acc[b][gg] += part; ss[b][gg] += sq; }
+    for (int c = 0; c < CPL; ++c) {
+        const uint32_t ch = lane + 64 * c;
+        if (ch < nch) {
+            wq[c] = ldw4(wr + ch * 4);
+            sc[c] = bf16f(sr[ch >> 1]);
+            bi[c] = bf16f(br[ch >> 1]);
+        } else {
+            wq[c] = make_uint4(0, 0, 0, 0);
+            sc[c] = bi[c] = 0.0f;
         }
     }
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-        float tot = 0.0f;
+        float part = 0.0f, sq = 0.0f;
 #pragma unroll
-        for (int g = 0; g < 8; ++g) {
-            if (g < (int)hc) {
-                float s2 = wave_sum(ss[b][g]);
-                float inv = 1.0f / sqrtf(s2 / (float)H + eps);
-                tot += inv * wave_sum(acc[b][g]);
-                if (row == 0 && lane == 0) inv_out[b * hc + g] = inv;
+        for (int c = 0; c < CPL; ++c) {
+            const uint32_t ch = lane + 64 * c;
+            if (ch < nch) {
+                float xv[32];
+                ldx32(hyper + (size_t)b * hh + (size_t)g * H + ch * 32, xv);
+                const uint4* np = reinterpret_cast<const uint4*>(w.norm + (size_t)g * H + ch * 32);
+                float xsum = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint4 nv = np[q];
+                    const uint32_t nn[4] = {nv.x, nv.y, nv.z, nv.w};
+#pragma unroll
+                    for (int h = 0; h < 8; ++h) {
+                        const int j = q * 8 + h;
+                        const float wn = __uint_as_float(h & 1 ? nn[h >> 1] & 0xffff0000u : nn[h >> 1] << 16);
+                        sq += xv[j] * xv[j];
+                        xv[j] *= wn;
+                        xsum += xv[j];
+                    }
+                }
+                part += q4_chunk(wq[c], xv, xsum, sc[c], bi[c]);
             }
         }
+        const float inv = 1.0f / sqrtf(wave_sum(sq) / (float)H + eps);
+        part = wave_sum(part) * inv;
         if (lane == 0) {
-            float v = tot / (float)hc;
-            if (row < w.down.out) d[(size_t)b * w.down.out + r] = siluf_(v);
-            else inj[b * hc + r] = 2.0f * sigmoidf_(v);
+            red[g][b] = part;
+            if (row == 0) inv_out[b * hc + g] = inv;
         }
+    }
+    __syncthreads();
+    if (threadIdx.x < NB) {
+        const int b = threadIdx.x;
+        float tot = 0.0f;
+        for (uint32_t gg = 0; gg < hc; ++gg) tot += red[gg][b];
+        const float v = tot / (float)hc;
+        if (row < w.down.out) d[(size_t)b * w.down.out + r] = siluf_(v);
+        else inj[b * hc + r] = 2.0f * sigmoidf_(v);
     }
 }
 
 // ------------------------------------------------------ hc read (up + mix)
 // mixed[i] = (1/hc) sum_g sigmoid(up(d)[g H + i]) * normed[g H + i]
-// (cpu.rs:477-491).  A wave covers RPW = 64/LPR rows: RPW/hc outputs x hc streams.
-template <int LPR, int NB>
-__global__ void k_hc_up_mix(HcDev w, const float* __restrict__ hyper, const float* __restrict__ inv,
+// (cpu.rs:477-491).  A wave has RPW = 64/LPR row slots; slot k serves
+// stream k % hc of output group k / hc, R outputs per group.
+template <int LPR, int R, int NB>
+__global__ void __launch_bounds__(256) k_hc_up_mix(HcDev w, const float* __restrict__ hyper, const float* __restrict__ inv,
                             const float* __restrict__ d, float* __restrict__ mixed, uint32_t H, uint32_t hc) {
     constexpr int RPW = 64 / LPR;
     __shared__ float red[4][NB][64];
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, lir = lane % LPR, k = lane / LPR;
-    const uint32_t outs_pw = RPW / hc;
-    const uint32_t o0 = (blockIdx.x * (blockDim.x >> 6) + wv) * outs_pw;
-    const uint32_t i = o0 + k / hc, g = k % hc;
-    const bool active = (uint32_t)k < outs_pw * hc && i < H;
-    float acc[NB];
-    if (active) {
-        q4_dot<LPR, NB>(w.up, g * H + i, d, w.down.out, lir, acc);
-    }
-    if (lir == 0) {
+    const int lane = threadIdx.x & 63, wv = (int)wave_id(), lir = lane % LPR, k = lane / LPR;
+    const uint32_t groups = RPW / hc;
+    const uint32_t o0 = global_wave() * groups * R;
+    const uint32_t g = k % hc, og = k / hc;
+    const bool slot_ok = (uint32_t)k < groups * hc;
+    uint32_t rows[R];
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            float v = 0.0f;
-            if (active) {
-                size_t j = (size_t)g * H + i;
-                float normed = hyper[(size_t)b * H * hc + j] * inv[b * hc + g] * bf16f(w.norm[j]);
-                v = sigmoidf_(acc[b]) * normed;
-            }
-            red[wv][b][k] = v;
+    for (int i = 0; i < R; ++i) {
+        uint32_t o = o0 + og * R + i;
+        rows[i] = g * H + (o < H ? o : H - 1);
+    }
+    Q4Frag<LPR, 1, R> f;
+    f.issue(w.up, rows, lir);
+    XFrag<NB, 1> xr;
+    load_x<LPR, 1, NB>(d, w.down.out, w.up.in >> 5, lir, xr);
+    // the row-group leader prefetches normed = hyper * inv * w for its outputs
+    float normed[R][NB];
+    if (lir == 0 && slot_ok) {
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            const uint32_t o = min(o0 + og * R + i, H - 1);
+            const size_t j = (size_t)g * H + o;
+            const float wn = bf16f(w.norm[j]);
+#pragma unroll
+            for (int b = 0; b < NB; ++b) normed[i][b] = hyper[(size_t)b * H * hc + j] * inv[b * hc + g] * wn;
+        }
+    }
+    float acc[R][NB];
+    f.template dot<NB>(xr, acc);
+    if (lir == 0 && slot_ok) {
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            const uint32_t o = o0 + og * R + i;
+#pragma unroll
+            for (int b = 0; b < NB; ++b)
+                red[wv][b][(og * R + i) * hc + g] = o < H ? sigmoidf_(acc[i][b]) * normed[i][b] : 0.0f;
         }
     }
     __syncthreads();
-    if ((uint32_t)lane < outs_pw && o0 + lane < H) {
+    if ((uint32_t)lane < groups * R) {
+        const uint32_t o = o0 + lane;
+        if (o < H)
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            float s = 0.0f;
-            for (uint32_t gg = 0; gg < hc; ++gg) s += red[wv][b][lane * hc + gg];
-            mixed[(size_t)b * H + o0 + lane] = s / (float)hc;
-        }
+            for (int b = 0; b < NB; ++b) {
+                float s = 0.0f;
+                for (uint32_t gg = 0; gg < hc; ++gg) s += red[wv][b][lane * hc + gg];
+                mixed[(size_t)b * H + o] = s / (float)hc;
+            }
     }
 }
 
 // ------------------------------------------------- multi-segment Q4 matvec
-// Several matrices over inputs of one width in one launch (horizontal
-// fusion), one wave per output row, with per-segment epilogues.
-template <int NB>
-__global__ void k_qmv(SegArgs a) {
-    const int lane = threadIdx.x & 63;
-    const uint32_t row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (row >= a.total) return;
-    int si = 0;
+// Several matrices over one input width in one launch (horizontal fusion),
+// R rows per wave per grid-stride step, per-segment epilogues.
+// Per-row epilogue inputs, fetched by lane i for row i while the weights
+// are in flight.
+struct EpiIn {
+    float hist[8];
+    float cw[9];
+    float p0, p1;
+};
+
+CHK_DEV void epi_prefetch(const SegArgs& a, const Seg& sg, uint32_t r, EpiIn& e) {
+    if (sg.epi == EPI_DN_CONV) {
+        const uint32_t km1 = a.ck - 1;
 #pragma unroll
-    for (int k = 1; k < MAX_SEG; ++k)
-        if (k < a.nseg && row >= a.seg[k].row0) si = k;
-    const Seg& sg = a.seg[si];
-    const uint32_t r = row - sg.row0;
-    float acc[NB];
-    q4_dot<64, NB>(sg.m, r, sg.x, sg.xs, lane, acc);
-    if (lane != 0) return;
+        for (uint32_t j = 0; j < 8; ++j)
+            if (j < km1) e.hist[j] = a.hist[(size_t)r * km1 + j];
+#pragma unroll
+        for (uint32_t j = 0; j < 9; ++j)
+            if (j < a.ck) e.cw[j] = bf16f(a.conv_w[(size_t)r * a.ck + j]);
+    } else if (sg.epi == EPI_DN_DECAY) {
+        e.p0 = bf16f(a.a_log[r]);
+        e.p1 = bf16f(a.dt_bias[r]);
+    }
+}
+
+template <int NB>
+CHK_DEV void seg_epilogue(const SegArgs& a, const Seg& sg, uint32_t r, const float (&acc)[NB], EpiIn& e) {
     switch (sg.epi) {
     case EPI_RAW:
 #pragma unroll
@@ -265,33 +436,44 @@ __global__ void k_qmv(SegArgs a) {
         // causal_conv (cpu.rs:1067-1085) for channel r, rows in order;
         // history snapshots after every row but the last (conv_b,
         // deltanet.metal:37-42).
+        // history slots are shifted with compile-time indices (km1 <= 8)
         const uint32_t km1 = a.ck - 1;
-        float hist[8];
-        float* hp = a.hist + (size_t)r * km1;
-        for (uint32_t j = 0; j < km1; ++j) hist[j] = hp[j];
-        const uint16_t* cw = a.conv_w + (size_t)r * a.ck;
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-            float cur = acc[b];
-            float s = bf16f(cw[km1]) * cur;
-            for (uint32_t j = 0; j < km1; ++j) s += bf16f(cw[j]) * hist[j];
-            for (uint32_t j = 0; j + 1 < km1; ++j) hist[j] = hist[j + 1];
-            hist[km1 - 1] = cur;
+            const float cur = acc[b];
+            float wl = 0.0f;
+#pragma unroll
+            for (uint32_t j = 0; j < 9; ++j)
+                if (j == km1) wl = e.cw[j];
+            float s = wl * cur;
+#pragma unroll
+            for (uint32_t j = 0; j < 8; ++j)
+                if (j < km1) s += e.cw[j] * e.hist[j];
+#pragma unroll
+            for (uint32_t j = 0; j < 7; ++j)
+                if (j + 1 < km1) e.hist[j] = e.hist[j + 1];
+#pragma unroll
+            for (uint32_t j = 0; j < 8; ++j)
+                if (j + 1 == km1) e.hist[j] = cur;
             sg.y[(size_t)b * sg.ys + r] = siluf_(s);
             if (a.snap && b + 1 < NB) {
                 float* sp = a.snap_hist + (size_t)b * a.conv_dim * km1 + (size_t)r * km1;
-                for (uint32_t j = 0; j < km1; ++j) sp[j] = hist[j];
+#pragma unroll
+                for (uint32_t j = 0; j < 8; ++j)
+                    if (j < km1) sp[j] = e.hist[j];
             }
         }
-        for (uint32_t j = 0; j < km1; ++j) hp[j] = hist[j];
+#pragma unroll
+        for (uint32_t j = 0; j < 8; ++j)
+            if (j < km1) a.hist[(size_t)r * km1 + j] = e.hist[j];
         break;
     }
     case EPI_DN_DECAY:
         // g = -exp(A_log) * softplus(a + dt_bias), decay = e^g (cpu.rs:775-777)
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-            float g = -expf(bf16f(a.a_log[r])) * softplusf_(acc[b] + bf16f(a.dt_bias[r]));
-            sg.y[(size_t)b * sg.ys + r] = expf(g);
+            const float gg = -expf(e.p0) * softplusf_(acc[b] + e.p1);
+            sg.y[(size_t)b * sg.ys + r] = expf(gg);
         }
         break;
     case EPI_DN_BETA:
@@ -301,39 +483,142 @@ __global__ void k_qmv(SegArgs a) {
     }
 }
 
+template <int CPL, int R, int NB>
+__global__ void __launch_bounds__(256) k_qmv(SegArgs a) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t groups = (a.total + R - 1) / R;
+    for (uint32_t grp = global_wave(); grp < groups; grp += total_waves()) {
+        const uint32_t row0 = grp * R;
+        int si = 0;
+#pragma unroll
+        for (int k = 1; k < MAX_SEG; ++k)
+            if (k < a.nseg && row0 >= a.seg[k].row0) si = k;
+        const Seg& sg = a.seg[si];
+        // segments hold whole blocks of R rows except a lone segment's tail
+        uint32_t rows[R];
+#pragma unroll
+        for (int i = 0; i < R; ++i) rows[i] = min(row0 - sg.row0 + i, sg.m.out - 1);
+        Q4Frag<64, CPL, R> f;
+        f.issue(sg.m, rows, lane);
+        XFrag<NB, CPL> xr;
+        load_x<64, CPL, NB>(sg.x, sg.xs, sg.m.in >> 5, lane, xr);
+        // lane i < R owns row i's epilogue; its inputs load alongside the weights
+        uint32_t my_row = rows[0];
+#pragma unroll
+        for (int i = 1; i < R; ++i)
+            if (lane == i) my_row = rows[i];
+        EpiIn e;
+        if (lane < R) epi_prefetch(a, sg, my_row, e);
+        float acc[R][NB];
+        f.template dot<NB>(xr, acc);
+        float mine[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            mine[b] = acc[0][b];
+#pragma unroll
+            for (int i = 1; i < R; ++i)
+                if (lane == i) mine[b] = acc[i][b];
+        }
+        if (lane < R && row0 - sg.row0 + lane < sg.m.out) seg_epilogue<NB>(a, sg, my_row, mine, e);
+    }
+}
+
 // --------------------------------------------- Q4 matvec + hyper inject
 // out = W x; hyper[b][g H + r] += out * inj[b][g] (inject, cpu.rs:971-979).
-template <int NB>
-__global__ void k_qmv_inject(Q4Mat m, const float* __restrict__ x, uint32_t xs, float* __restrict__ hyper,
-                             const float* __restrict__ inj, uint32_t hc, float* __restrict__ raw_out) {
+// XM_DN_GATED: x is the DeltaNet core output y, gated here as
+// rmsnorm(y_head) * w * sigmoid(z) (cpu.rs:814-826, eps 1e-6), the head's
+// sum of squares coming from the scan's per-block partials.
+template <int CPL, int R, int NB, int XM>
+__global__ void __launch_bounds__(256) k_qmv_inject(InjArgs a) {
     const int lane = threadIdx.x & 63;
-    const uint32_t r = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (r >= m.out) return;
-    float acc[NB];
-    q4_dot<64, NB>(m, r, x, xs, lane, acc);
-    if (lane != 0) return;
-    const uint32_t H = m.out;
+    const Q4Mat& m = a.m;
+    const uint32_t nch = m.in >> 5, H = m.out;
+    const uint32_t groups = m.out / R;
+    // lane (i, g) = (lane / hc, lane % hc) owns hyper[b][g H + row_i]
+    const uint32_t li = lane / a.hc, lg = lane % a.hc;
+    const bool owner = li < (uint32_t)R && a.hyper;
+    bool first = true;
+    XFrag<NB, CPL> xr;
+    for (uint32_t grp = global_wave(); grp < groups; grp += total_waves()) {
+        uint32_t rows[R];
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
-        if (raw_out) raw_out[(size_t)b * H + r] = acc[b];
-        if (hyper)
-            for (uint32_t g = 0; g < hc; ++g) hyper[(size_t)b * H * hc + g * H + r] += acc[b] * inj[b * hc + g];
+        for (int i = 0; i < R; ++i) rows[i] = grp * R + i;
+        Q4Frag<64, CPL, R> f;
+        f.issue(m, rows, lane);
+        float hy[NB], ij[NB];
+        if (owner)
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                hy[b] = a.hyper[(size_t)b * H * a.hc + lg * H + grp * R + li];
+                ij[b] = a.inj[b * a.hc + lg];
+            }
+        if (first) {
+            first = false;
+            xr.template load<64>(a.x, a.xs, nch, lane);
+            if (XM == XM_DN_GATED) {
+                // x holds y * w * sigmoid(z); scale each 32-chunk by its
+                // head's 1/sqrt(mean(y^2) + 1e-6)
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) {
+                    const uint32_t ch = min(lane + 64 * c, nch - 1);
+                    const uint32_t head = ch * 32 / a.dv;
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) {
+                        const float4* sp = reinterpret_cast<const float4*>(a.ssq + ((size_t)b * a.nheads + head) * a.ssq_blocks);
+                        float ss = 0.0f;
+                        for (uint32_t k = 0; k < a.ssq_blocks / 4; ++k) {
+                            const float4 q = sp[k];
+                            ss += (q.x + q.y) + (q.z + q.w);
+                        }
+                        const float inv = 1.0f / sqrtf(ss / (float)a.dv + 1e-6f);
+#pragma unroll
+                        for (int j = 0; j < 32; ++j) xr.v[b][c][j] *= inv;
+                    }
+                }
+            }
+            xr.sums();
+        }
+        float acc[R][NB];
+        f.template dot<NB>(xr, acc);
+        if (a.raw_out && lane < R) {
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                float v = acc[0][b];
+#pragma unroll
+                for (int i = 1; i < R; ++i)
+                    if (lane == i) v = acc[i][b];
+                a.raw_out[(size_t)b * H + rows[0] + lane] = v;
+            }
+        }
+        if (owner) {
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                float v = acc[0][b];
+#pragma unroll
+                for (int i = 1; i < R; ++i)
+                    if (li == (uint32_t)i) v = acc[i][b];
+                a.hyper[(size_t)b * H * a.hc + lg * H + grp * R + li] = hy[b] + v * ij[b];
+            }
+        }
     }
 }
 
 // ------------------------------------------------------- DeltaNet step
-// One workgroup per value head: the head's fp32 state [dv][dk] (transposed
-// relative to cpu.rs, as delta_scan2 keeps it) lives in VGPRs, 4 threads
-// per value lane, 32 key lanes each.  Per row: L2-normalise q, k of the
-// key head, S <- decay S, delta = beta (v - S^T k), S <- S + k delta^T,
-// y = S^T q (cpu.rs:745-812); snapshots after rows < nb-1; then the gated
-// RMSNorm y = rmsnorm(y) * w * sigmoid(z) (cpu.rs:814-826, eps 1e-6).
+// One wave per (value head, 16 value lanes): that slice of the head's fp32
+// state [dv][dk] (transposed relative to cpu.rs, as delta_scan2 keeps it)
+// lives in VGPRs, 4 lanes per value lane, 32 key lanes each.  Per row:
+// L2-normalise the key head's q (times dk^-1/2) and k (eps 1e-6),
+// S <- decay S, delta = beta (v - S^T k), S <- S + k delta^T, y = S^T q
+// (cpu.rs:745-812); snapshots after rows < nb-1.  The gated RMSNorm needs
+// the whole head, so each wave leaves its share of sum(y^2) for the
+// out-projection's prologue.
 template <int NB>
-__global__ void __launch_bounds__(512) k_dn_scan(DnScanArgs a) {
-    constexpr int DK = 128, TPC = 4, KPT = DK / TPC;
-    __shared__ float red[8];
-    const uint32_t hv = blockIdx.x;
-    const int t = threadIdx.x, iv = t / TPC, p = t % TPC;
+__global__ void __launch_bounds__(64) k_dn_scan(DnScanArgs a) {
+    constexpr int DK = 128, TPC = 4, KPT = DK / TPC, COLS = 16;
+    const uint32_t blocks = a.dv / COLS;
+    const uint32_t hv = blockIdx.x / blocks, blk = blockIdx.x % blocks;
+    const int t = threadIdx.x, p = t % TPC;
+    const uint32_t iv = blk * COLS + t / TPC;
     const uint32_t hk = hv / (a.nv / a.nk);
     float S[KPT];
     float* sp = a.state + ((size_t)hv * a.dv + iv) * DK + p * KPT;
@@ -347,15 +632,20 @@ __global__ void __launch_bounds__(512) k_dn_scan(DnScanArgs a) {
         float q[KPT], kk[KPT];
         float sq = 0.0f, sk = 0.0f;
 #pragma unroll
+        for (int j = 0; j < KPT; j += 4) {
+            float4 qv = *reinterpret_cast<const float4*>(row + hk * DK + p * KPT + j);
+            float4 kv = *reinterpret_cast<const float4*>(row + a.qk_dim + hk * DK + p * KPT + j);
+            q[j] = qv.x; q[j + 1] = qv.y; q[j + 2] = qv.z; q[j + 3] = qv.w;
+            kk[j] = kv.x; kk[j + 1] = kv.y; kk[j + 2] = kv.z; kk[j + 3] = kv.w;
+        }
+#pragma unroll
         for (int j = 0; j < KPT; ++j) {
-            q[j] = row[hk * DK + p * KPT + j];
-            kk[j] = row[a.qk_dim + hk * DK + p * KPT + j];
             sq += q[j] * q[j];
             sk += kk[j] * kk[j];
         }
         sq = group_sum<TPC>(sq);
         sk = group_sum<TPC>(sk);
-        float iq = 1.0f / sqrtf(sq + 1e-6f), ik = 1.0f / sqrtf(sk + 1e-6f);
+        const float iq = 1.0f / sqrtf(sq + 1e-6f), ik = 1.0f / sqrtf(sk + 1e-6f);
 #pragma unroll
         for (int j = 0; j < KPT; ++j) {
             q[j] = q[j] * iq * a.qscale;
@@ -381,141 +671,200 @@ __global__ void __launch_bounds__(512) k_dn_scan(DnScanArgs a) {
         if (a.snap && b + 1 < NB) {
             float* pp = a.snap_state + (size_t)b * a.nv * a.dv * DK + ((size_t)hv * a.dv + iv) * DK + p * KPT;
 #pragma unroll
-            for (int k = 0; k < KPT; k += 4) *reinterpret_cast<float4*>(pp + k) = make_float4(S[k], S[k + 1], S[k + 2], S[k + 3]);
+            for (int k = 0; k < KPT; k += 4)
+                *reinterpret_cast<float4*>(pp + k) = make_float4(S[k], S[k + 1], S[k + 2], S[k + 3]);
         }
-        float ss = block_sum(p == 0 ? y * y : 0.0f, red);
-        float inv = 1.0f / sqrtf(ss / (float)a.dv + 1e-6f);
+        // gated RMSNorm numerator: y * w * sigmoid(z); the head's
+        // 1/rms (from the partial sums of y^2) is applied by the consumer
+        const float ss = wave_sum(p == 0 ? y * y : 0.0f);
         if (p == 0) {
-            float z = a.z[(size_t)b * a.nv * a.dv + hv * a.dv + iv];
-            a.y[(size_t)b * a.nv * a.dv + hv * a.dv + iv] = y * inv * bf16f(a.norm[iv]) * sigmoidf_(z);
+            const size_t j = (size_t)b * a.nv * a.dv + hv * a.dv + iv;
+            a.y[j] = y * bf16f(a.norm[iv]) * sigmoidf_(a.z[j]);
         }
+        if (t == 0) a.ssq[((size_t)b * a.nv + hv) * blocks + blk] = ss;
     }
 #pragma unroll
     for (int k = 0; k < KPT; k += 4) *reinterpret_cast<float4*>(sp + k) = make_float4(S[k], S[k + 1], S[k + 2], S[k + 3]);
 }
 
 // ------------------------------------------------------------ router
-// logits = W_r x (bf16 [E][H]) and the shared-expert gate dot (cpu.rs:
-// 506-508, 534-535).  The last workgroup to finish runs softmax and top-k
-// (desc probability, lowest index on ties, renormalised; cpu.rs:508-525).
-template <int NB>
-__global__ void k_router(RouterArgs a) {
+// logits = W_r x (bf16 [E][H]) and the shared-expert gate dot as row E
+// (cpu.rs:506-508, 534-535).  Softmax/top-k happen in the experts
+// kernel's prologue.
+template <int R, int NB>
+__global__ void __launch_bounds__(256) k_router(RouterArgs a) {
     const int lane = threadIdx.x & 63;
-    const uint32_t row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    const uint32_t H = a.H;
-    if (row <= a.E) {
-        const uint16_t* wr = row < a.E ? a.router + (size_t)row * H : a.shared_gate;
-        float acc[NB];
+    const uint32_t H = a.H, nch = H >> 5, rows_total = a.E + 1;
+    const uint32_t groups = (rows_total + R - 1) / R;
+    for (uint32_t grp = global_wave(); grp < groups; grp += total_waves()) {
+        uint4 wq[R][4];
+        const uint32_t ch = lane;
 #pragma unroll
-        for (int b = 0; b < NB; ++b) acc[b] = 0.0f;
-        for (uint32_t c = lane; c < H / 32; c += 64) {
-            const uint4* wp = reinterpret_cast<const uint4*>(wr + c * 32);
-            float wv[32];
+        for (int i = 0; i < R; ++i) {
+            uint32_t row = grp * R + i;
+            if (row > a.E) row = a.E;
+            const uint16_t* wr = row < a.E ? a.router + (size_t)row * H : a.shared_gate;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                uint4 u = wp[k];
-                uint32_t uu[4] = {u.x, u.y, u.z, u.w};
+            for (int k = 0; k < 4; ++k)
+                wq[i][k] = ch < nch ? ldw4(reinterpret_cast<const uint32_t*>(wr + ch * 32) + 4 * k) : make_uint4(0, 0, 0, 0);
+        }
+        XFrag<NB, 1> xr;
+        xr.template load<64>(a.x, H, nch, lane);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    wv[k * 8 + 2 * j] = __uint_as_float(uu[j] << 16);
-                    wv[k * 8 + 2 * j + 1] = __uint_as_float(uu[j] & 0xffff0000u);
-                }
-            }
+        for (int i = 0; i < R; ++i) {
+            const uint32_t row = grp * R + i;
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
-                float xv[32];
-                ldx32(a.x + (size_t)b * H + c * 32, xv);
+                float acc = 0.0f;
 #pragma unroll
-                for (int j = 0; j < 32; ++j) acc[b] += wv[j] * xv[j];
-            }
-        }
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t uu[4] = {wq[i][k].x, wq[i][k].y, wq[i][k].z, wq[i][k].w};
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            float s = wave_sum(acc[b]);
-            if (lane == 0) {
-                if (row < a.E) a.logits[(size_t)b * a.E + row] = s;
-                else a.sg[b] = s;
+                    for (int j = 0; j < 4; ++j) {
+                        acc += __uint_as_float(uu[j] << 16) * xr.v[b][0][k * 8 + 2 * j];
+                        acc += __uint_as_float(uu[j] & 0xffff0000u) * xr.v[b][0][k * 8 + 2 * j + 1];
+                    }
+                }
+                acc = wave_sum(acc);
+                if (lane == 0 && row <= a.E) {
+                    if (row < a.E) a.logits[(size_t)b * a.E + row] = acc;
+                    else a.sg[b] = acc;
+                }
             }
         }
     }
-    // last-block-done: the final workgroup computes the routing
-    __shared__ uint32_t ticket;
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) ticket = atomicAdd(a.counter, 1u);
-    __syncthreads();
-    if (ticket != gridDim.x - 1) return;
-    __threadfence();
-    if (threadIdx.x >= 64) return;
-    if (lane == 0) *a.counter = 0u;
-    topk_wave(a.logits, a.probs, a.E, a.topk, a.norm_topk, a.ids, a.w, NB, lane);
 }
 
 // ----------------------------------------------------- experts: gate/up
+// Prologue: softmax + top-k of the router logits (every workgroup, into
+// LDS; workgroup 0 publishes ids/weights for the down kernel).  Then
 // act[b][slot][i] = silu(gate_i . x_b) * (up_i . x_b) for the top-k routed
 // experts of row b (slots 0..k-1) and the shared expert (slot k) (mlp,
-// cpu.rs:981-992).  One wave per (row, slot, i).
-template <int NB1, int BITS>
-__global__ void k_moe_gate_up(MoeArgs a) {
+// cpu.rs:981-992).  A wave task is (row, slot, R consecutive i): the
+// gate and up rows of all R are loaded together.
+template <int R, int NB1, int BITS>
+__global__ void __launch_bounds__(256) k_moe_gate_up(MoeArgs a) {
+    __shared__ uint32_t s_ids[MAX_NB * 64];
+    __shared__ float s_w[MAX_NB * 64];
+    __shared__ uint32_t s_scr[128];
     const int lane = threadIdx.x & 63;
-    const uint32_t t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    const uint32_t slots = a.topk + 1;
-    if (t >= a.nb * slots * a.I) return;
-    const uint32_t b = t / (slots * a.I), slot = (t / a.I) % slots, i = t % a.I;
-    const float* x = a.x + (size_t)b * a.H;
-    float g, u;
-    if (slot < a.topk) {
-        uint32_t e = min(a.ids[b * a.topk + slot], a.X.experts - 1);
-        const uint8_t* rec = a.X.base + ((size_t)a.record_layer * a.X.experts + e) * a.X.stride;
-        float acc[1];
-        expert_dot<64, 1, BITS>(a.X, rec, 0, a.I, a.H, i, x, 0, lane, acc);
-        g = acc[0];
-        expert_dot<64, 1, BITS>(a.X, rec, 1, a.I, a.H, i, x, 0, lane, acc);
-        u = acc[0];
-    } else {
-        float acc[1];
-        q4_dot<64, 1>(a.sh_gate, i, x, 0, lane, acc);
-        g = acc[0];
-        q4_dot<64, 1>(a.sh_up, i, x, 0, lane, acc);
-        u = acc[0];
+    if (wave_id() == 0) {
+        topk_wave(a.logits, a.probs, a.E, a.topk, a.norm_topk, s_ids, s_w, a.nb, lane, blockIdx.x == 0, s_scr);
+        if (blockIdx.x == 0 && lane == 0)
+            for (uint32_t j = 0; j < a.nb * a.topk; ++j) {
+                a.ids_out[j] = s_ids[j];
+                a.w_out[j] = s_w[j];
+            }
     }
-    if (lane == 0) a.act[((size_t)b * slots + slot) * a.I + i] = siluf_(g) * u;
+    __syncthreads();
+    const uint32_t slots = a.topk + 1, blocks = a.I / R;
+    const uint32_t tasks = a.nb * slots * blocks;
+    for (uint32_t t = global_wave(); t < tasks; t += total_waves()) {
+        const uint32_t b = t / (slots * blocks), slot = (t / blocks) % slots, i0 = (t % blocks) * R;
+        uint32_t rows[R];
+#pragma unroll
+        for (int i = 0; i < R; ++i) rows[i] = i0 + i;
+        float g[R][1], u[R][1];
+        XFrag<1, 1> xr;
+        if (slot < a.topk) {
+            const uint32_t e = min(s_ids[b * a.topk + slot], a.X.experts - 1);
+            const uint8_t* rec = a.X.base + ((size_t)a.record_layer * a.X.experts + e) * a.X.stride;
+            ExpFrag<64, 1, R, BITS> fg, fu;
+            fg.issue(expert_mat(a.X, rec, 0, a.I, a.H), rows, lane);
+            fu.issue(expert_mat(a.X, rec, 1, a.I, a.H), rows, lane);
+            load_x<64, 1, 1>(a.x + (size_t)b * a.H, 0, a.H >> 5, lane, xr);
+            fg.template dot<1>(xr, g);
+            fu.template dot<1>(xr, u);
+        } else {
+            Q4Frag<64, 1, R> fg, fu;
+            fg.issue(a.sh_gate, rows, lane);
+            fu.issue(a.sh_up, rows, lane);
+            load_x<64, 1, 1>(a.x + (size_t)b * a.H, 0, a.H >> 5, lane, xr);
+            fg.template dot<1>(xr, g);
+            fu.template dot<1>(xr, u);
+        }
+        if (lane == 0)
+#pragma unroll
+            for (int i = 0; i < R; ++i) a.act[((size_t)b * slots + slot) * a.I + rows[i]] = siluf_(g[i][0]) * u[i][0];
+    }
 }
 
 // ------------------------------------------------- experts: down + combine
 // out[r] = sum_j w_j down_j(act_j)[r] + sigmoid(shared_gate . x) shared_down(act_k)[r]
-// (cpu.rs:527-540), then hyper[g H + r] += out * inj_g.  One wave per
-// output row; LPR lanes per expert row, 64/LPR experts in flight.
-template <int LPR, int NB1, int BITS>
-__global__ void k_moe_down(MoeArgs a) {
+// (cpu.rs:527-540), then hyper[g H + r] += out * inj_g.  A wave covers R
+// output rows; its 64/LPR lane groups take one expert slot each per pass.
+// Two dependent round trips: the routing (ids, weights), then every pass's
+// weight rows and activations at once.
+template <int LPR, int R, int BITS, int PASSES>
+__global__ void __launch_bounds__(256) k_moe_down(MoeArgs a) {
     constexpr int G = 64 / LPR;
     const int lane = threadIdx.x & 63, grp = lane / LPR, lir = lane % LPR;
-    const uint32_t r = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (r >= a.H) return;
     const uint32_t slots = a.topk + 1;
-    for (uint32_t b = 0; b < a.nb; ++b) {
-        float tot = 0.0f;
-        for (uint32_t slot = grp; slot < slots; slot += G) {
-            const float* act = a.act + ((size_t)b * slots + slot) * a.I;
-            float acc[1], wgt;
-            if (slot < a.topk) {
-                uint32_t e = min(a.ids[b * a.topk + slot], a.X.experts - 1);
-                const uint8_t* rec = a.X.base + ((size_t)a.record_layer * a.X.experts + e) * a.X.stride;
-                expert_dot<LPR, 1, BITS>(a.X, rec, 2, a.H, a.I, r, act, 0, lir, acc);
-                wgt = a.w[b * a.topk + slot];
-            } else {
-                q4_dot<LPR, 1>(a.sh_down, r, act, 0, lir, acc);
-                wgt = sigmoidf_(a.sg[b]);
-            }
-            tot += wgt * acc[0];
-        }
+    const uint32_t groups = a.H / R;
+    for (uint32_t gi = global_wave(); gi < groups; gi += total_waves()) {
+        uint32_t rows[R];
 #pragma unroll
-        for (int m = LPR; m < 64; m <<= 1) tot += __shfl_xor(tot, m, 64);
-        if (lane == 0) {
-            if (a.raw_out) a.raw_out[(size_t)b * a.H + r] = tot;
-            if (a.hyper)
-                for (uint32_t g = 0; g < a.hc; ++g)
-                    a.hyper[(size_t)b * a.H * a.hc + g * a.H + r] += tot * a.inj[b * a.hc + g];
+        for (int i = 0; i < R; ++i) rows[i] = gi * R + i;
+        for (uint32_t b = 0; b < a.nb; ++b) {
+            // routing of row b: lane j < topk holds slot j's id and weight
+            uint32_t my_id = 0;
+            float my_w = 0.0f;
+            if ((uint32_t)lane < a.topk) {
+                my_id = min(a.ids[b * a.topk + lane], a.X.experts - 1);
+                my_w = a.w[b * a.topk + lane];
+            } else if ((uint32_t)lane == a.topk) {
+                my_w = sigmoidf_(a.sg[b]);
+            }
+            // hyper of this wave's rows, for the inject below
+            const uint32_t li = lane / a.hc, lg = lane % a.hc;
+            const bool owner = li < (uint32_t)R && a.hyper;
+            float hy = 0.0f, ij = 0.0f;
+            if (owner) {
+                hy = a.hyper[(size_t)b * a.H * a.hc + lg * a.H + rows[0] + li];
+                ij = a.inj[b * a.hc + lg];
+            }
+            ExpFrag<LPR, 1, R, BITS> f[PASSES];
+            Q4Frag<LPR, 1, R> fs;
+            XFrag<1, 1> xr[PASSES];
+            float wgt[PASSES];
+#pragma unroll
+            for (int pass = 0; pass < PASSES; ++pass) {
+                const uint32_t slot = grp + pass * G;
+                const uint32_t sl = slot < slots ? slot : slots - 1;
+                const uint32_t e = __shfl(my_id, sl < a.topk ? sl : 0, 64);
+                wgt[pass] = __shfl(my_w, sl, 64);
+                if (slot >= slots) wgt[pass] = 0.0f;
+                if (sl < a.topk) {
+                    const uint8_t* rec = a.X.base + ((size_t)a.record_layer * a.X.experts + e) * a.X.stride;
+                    f[pass].issue(expert_mat(a.X, rec, 2, a.H, a.I), rows, lir);
+                } else {
+                    fs.issue(a.sh_down, rows, lir);
+                }
+                load_x<LPR, 1, 1>(a.act + ((size_t)b * slots + sl) * a.I, 0, a.I >> 5, lir, xr[pass]);
+            }
+            float tot[R];
+#pragma unroll
+            for (int i = 0; i < R; ++i) tot[i] = 0.0f;
+#pragma unroll
+            for (int pass = 0; pass < PASSES; ++pass) {
+                const uint32_t slot = grp + pass * G;
+                const uint32_t sl = slot < slots ? slot : slots - 1;
+                float acc[R][1];
+                if (sl < a.topk) f[pass].template dot<1>(xr[pass], acc);
+                else fs.template dot<1>(xr[pass], acc);
+#pragma unroll
+                for (int i = 0; i < R; ++i) tot[i] += wgt[pass] * acc[i][0];
+            }
+            float mine = 0.0f;
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                float v = tot[i];
+#pragma unroll
+                for (int m = LPR; m < 64; m <<= 1) v += __shfl_xor(v, m, 64);
+                if (li == (uint32_t)i) mine = v;
+                if (a.raw_out && lane == i) a.raw_out[(size_t)b * a.H + rows[i]] = v;
+            }
+            if (owner) a.hyper[(size_t)b * a.H * a.hc + lg * a.H + rows[0] + li] = hy + mine * ij;
         }
     }
 }
@@ -523,32 +872,39 @@ __global__ void k_moe_down(MoeArgs a) {
 // ------------------------------------------------------- LM head + argmax
 // logits = W_lm mixed; greedy argmax with the lowest index winning ties
 // (argmax_partial/argmax_final, kernels/common/sampling.metal:10-84).
-template <int NB>
-__global__ void k_lm_head(Q4Mat m, const float* __restrict__ x, float* __restrict__ logits, float* __restrict__ pv,
+template <int R, int NB>
+__global__ void __launch_bounds__(256) k_lm_head(Q4Mat m, const float* __restrict__ x, float* __restrict__ logits, float* __restrict__ pv,
                           uint32_t* __restrict__ pi) {
     __shared__ float sv[NB][4];
     __shared__ uint32_t si[NB][4];
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const uint32_t nw = gridDim.x * (blockDim.x >> 6);
+    const int lane = threadIdx.x & 63, wv = (int)wave_id();
     float bv[NB];
     uint32_t bi[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) { bv[b] = -INFINITY; bi[b] = 0xffffffffu; }
-    for (uint32_t r = blockIdx.x * (blockDim.x >> 6) + wv; r < m.out; r += nw) {
-        float acc[NB];
-        q4_dot<64, NB>(m, r, x, m.in, lane, acc);
+    XFrag<NB, 1> xr;
+    load_x<64, 1, NB>(x, m.in, m.in >> 5, lane, xr);
+    const uint32_t groups = m.out / R;
+    for (uint32_t grp = global_wave(); grp < groups; grp += total_waves()) {
+        uint32_t rows[R];
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            if (lane == 0) logits[(size_t)b * m.out + r] = acc[b];
-            if (acc[b] > bv[b] || (acc[b] == bv[b] && r < bi[b])) { bv[b] = acc[b]; bi[b] = r; }
-        }
+        for (int i = 0; i < R; ++i) rows[i] = grp * R + i;
+        float acc[R][NB];
+        q4_block<64, 1, R, NB>(m, rows, xr, lane, acc);
+#pragma unroll
+        for (int i = 0; i < R; ++i)
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                if (lane == i) logits[(size_t)b * m.out + rows[i]] = acc[i][b];
+                if (acc[i][b] > bv[b] || (acc[i][b] == bv[b] && rows[i] < bi[b])) { bv[b] = acc[i][b]; bi[b] = rows[i]; }
+            }
     }
     if (lane == 0)
 #pragma unroll
         for (int b = 0; b < NB; ++b) { sv[b][wv] = bv[b]; si[b][wv] = bi[b]; }
     __syncthreads();
     if (threadIdx.x < NB) {
-        int b = threadIdx.x;
+        const int b = threadIdx.x;
         float v = sv[b][0];
         uint32_t i = si[b][0];
         for (int k = 1; k < (int)(blockDim.x >> 6); ++k)
@@ -558,7 +914,7 @@ __global__ void k_lm_head(Q4Mat m, const float* __restrict__ x, float* __restric
     }
 }
 
-__global__ void k_argmax_final(const float* __restrict__ pv, const uint32_t* __restrict__ pi, uint32_t n,
+__global__ void __launch_bounds__(256) k_argmax_final(const float* __restrict__ pv, const uint32_t* __restrict__ pi, uint32_t n,
                                uint32_t* __restrict__ out) {
     __shared__ float sv[256];
     __shared__ uint32_t si[256];
@@ -566,8 +922,8 @@ __global__ void k_argmax_final(const float* __restrict__ pv, const uint32_t* __r
     float v = -INFINITY;
     uint32_t i = 0xffffffffu;
     for (uint32_t k = threadIdx.x; k < n; k += blockDim.x) {
-        float x = pv[(size_t)b * n + k];
-        uint32_t xi = pi[(size_t)b * n + k];
+        const float x = pv[(size_t)b * n + k];
+        const uint32_t xi = pi[(size_t)b * n + k];
         if (x > v || (x == v && xi < i)) { v = x; i = xi; }
     }
     sv[threadIdx.x] = v;
@@ -575,8 +931,8 @@ __global__ void k_argmax_final(const float* __restrict__ pv, const uint32_t* __r
     __syncthreads();
     for (uint32_t s = blockDim.x / 2; s > 0; s >>= 1) {
         if (threadIdx.x < s) {
-            float x = sv[threadIdx.x + s];
-            uint32_t xi = si[threadIdx.x + s];
+            const float x = sv[threadIdx.x + s];
+            const uint32_t xi = si[threadIdx.x + s];
             if (x > sv[threadIdx.x] || (x == sv[threadIdx.x] && xi < si[threadIdx.x])) {
                 sv[threadIdx.x] = x;
                 si[threadIdx.x] = xi;
@@ -597,98 +953,161 @@ __global__ void k_argmax_final(const float* __restrict__ pv, const uint32_t* __r
     default: { constexpr int NB = 4; CALL; } break; \
     }
 
-void launch_embed(const uint32_t* tokens, const Q4Mat& emb, float* hyper, uint32_t H, uint32_t hc, int nb,
-                  hipStream_t st) {
+static uint32_t grid_for(uint32_t waves_needed, uint32_t cap = 2048) {
+    uint32_t g = (waves_needed + 3) / 4;
+    return std::max<uint32_t>(1, std::min(g, cap));
+}
+
+void launch_embed(const StepIn* in, uint32_t* tokens, uint32_t* rowpos, const Q4Mat& emb, float* hyper, uint32_t H,
+                  uint32_t hc, int nb, hipStream_t st) {
     dim3 grid((H + 255) / 256, nb);
-    k_embed<<<grid, 256, 0, st>>>(tokens, emb, hyper, H, hc);
+    k_embed<<<grid, 256, 0, st>>>(in, tokens, rowpos, emb, hyper, H, hc);
 }
 
 void launch_hc_down(const HcDev& w, const float* hyper, float* d, float* inj, float* inv, uint32_t H, uint32_t hc,
                     float eps, int nb, hipStream_t st) {
-    uint32_t rows = w.down.out + (w.has_inject ? w.inject.out : 0);
-    CHK_NB_SWITCH(nb, (k_hc_down<NB><<<(rows + 3) / 4, 256, 0, st>>>(w, hyper, d, inj, inv, H, hc, eps)));
+    const uint32_t rows = w.down.out + (w.has_inject ? w.inject.out : 0);
+    const uint32_t cpl = (H / 32 + 63) / 64;
+    if (cpl <= 1) {
+        CHK_NB_SWITCH(nb, (k_hc_down<1, NB><<<rows, 64 * hc, 0, st>>>(w, hyper, d, inj, inv, H, hc, eps)))
+    } else {
+        CHK_NB_SWITCH(nb, (k_hc_down<2, NB><<<rows, 64 * hc, 0, st>>>(w, hyper, d, inj, inv, H, hc, eps)))
+    }
 }
 
 void launch_hc_up_mix(const HcDev& w, const float* hyper, const float* inv, const float* d, float* mixed,
                       uint32_t H, uint32_t hc, int nb, hipStream_t st) {
-    uint32_t nch = w.up.in / 32;
-    int lpr = 1;
+    const uint32_t nch = w.up.in / 32;
+    int lpr = 2;
     while (lpr < (int)nch) lpr <<= 1;
-    if (lpr > 64) lpr = 64;
-    uint32_t outs_pw = (64 / lpr) / hc;
-    uint32_t waves = (H + outs_pw - 1) / outs_pw;
-    uint32_t grid = (waves + 3) / 4;
-#define UPMIX(L) CHK_NB_SWITCH(nb, (k_hc_up_mix<L, NB><<<grid, 256, 0, st>>>(w, hyper, inv, d, mixed, H, hc)))
+    constexpr int R = 2;
+    const uint32_t outs_pw = (64 / lpr) / hc * R;
+    const uint32_t grid = grid_for((H + outs_pw - 1) / outs_pw, 1u << 20);
+#define UPMIX(L) CHK_NB_SWITCH(nb, (k_hc_up_mix<L, R, NB><<<grid, 256, 0, st>>>(w, hyper, inv, d, mixed, H, hc)))
     switch (lpr) {
-    case 1: case 2: UPMIX(2); break;
+    case 2: UPMIX(2); break;
     case 4: UPMIX(4); break;
     case 8: UPMIX(8); break;
-    case 16: UPMIX(16); break;
     default: UPMIX(16); break;
     }
 #undef UPMIX
 }
 
 void launch_qmv(const SegArgs& a, int nb, hipStream_t st) {
-    uint32_t grid = (a.total + 3) / 4;
-    CHK_NB_SWITCH(nb, (k_qmv<NB><<<grid, 256, 0, st>>>(a)));
+    const uint32_t in = a.seg[0].m.in;
+    const uint32_t cpl = (in / 32 + 63) / 64;
+    if (cpl > 4) throw std::runtime_error("matvec input wider than 8192");
+#define QMV(C, R) CHK_NB_SWITCH(nb, (k_qmv<C, R, NB><<<grid_for((a.total + R - 1) / R), 256, 0, st>>>(a)))
+    if (nb <= 2) {
+        if (cpl <= 1) {
+            QMV(1, 4);
+        } else if (cpl == 2) {
+            QMV(2, 4);
+        } else {
+            QMV(4, 2);
+        }
+    } else {
+        if (cpl <= 1) {
+            QMV(1, 2);
+        } else if (cpl == 2) {
+            QMV(2, 2);
+        } else {
+            QMV(4, 1);
+        }
+    }
+#undef QMV
 }
 
-void launch_qmv_inject(const Q4Mat& m, const float* x, uint32_t xs, float* hyper, const float* inj, uint32_t hc,
-                       float* raw_out, int nb, hipStream_t st) {
-    uint32_t grid = (m.out + 3) / 4;
-    CHK_NB_SWITCH(nb, (k_qmv_inject<NB><<<grid, 256, 0, st>>>(m, x, xs, hyper, inj, hc, raw_out)));
+void launch_qmv_inject(const InjArgs& a, int nb, hipStream_t st) {
+    const uint32_t cpl = (a.m.in / 32 + 63) / 64;
+    constexpr int R = 2;
+    const uint32_t grid = grid_for(a.m.out / R);
+#define INJ(C, X) CHK_NB_SWITCH(nb, (k_qmv_inject<C, R, NB, X><<<grid, 256, 0, st>>>(a)))
+    if (a.xmode == XM_DN_GATED) {
+        if (cpl <= 1) {
+            INJ(1, XM_DN_GATED);
+        } else {
+            INJ(2, XM_DN_GATED);
+        }
+    } else {
+        if (cpl <= 1) {
+            INJ(1, XM_PLAIN);
+        } else {
+            INJ(2, XM_PLAIN);
+        }
+    }
+#undef INJ
 }
 
 void launch_dn_scan(const DnScanArgs& a, int nb, hipStream_t st) {
-    CHK_NB_SWITCH(nb, (k_dn_scan<NB><<<a.nv, a.dv * 4, 0, st>>>(a)));
+    CHK_NB_SWITCH(nb, (k_dn_scan<NB><<<a.nv * (a.dv / 16), 64, 0, st>>>(a)));
 }
 
 void launch_router(const RouterArgs& a, int nb, hipStream_t st) {
-    uint32_t grid = (a.E + 1 + 3) / 4;
-    CHK_NB_SWITCH(nb, (k_router<NB><<<grid, 256, 0, st>>>(a)));
+    // one wave per workgroup so the 2 MiB matrix spreads over every CU
+    constexpr int R = 2;
+    const uint32_t grid = (a.E + 1 + R - 1) / R;
+    CHK_NB_SWITCH(nb, (k_router<R, NB><<<grid, 64, 0, st>>>(a)));
 }
 
-void launch_moe(const MoeArgs& a, hipStream_t st) {
-    uint32_t tasks = a.nb * (a.topk + 1) * a.I;
-    uint32_t grid = (tasks + 3) / 4;
-    uint32_t nch = a.I / 32;
-    int lpr = 1;
+void launch_moe_gate_up(const MoeArgs& a, hipStream_t st) {
+    constexpr int RG = 2;
+    if (a.topk >= 64 || a.E > 512) throw std::runtime_error("routing too wide");
+    const uint32_t tasks = a.nb * (a.topk + 1) * (a.I / RG);
+    const uint32_t grid = std::max<uint32_t>(1, std::min<uint32_t>((tasks + 1) / 2, 2048));
+    switch (a.X.bits) {
+    case 3: k_moe_gate_up<RG, 1, 3><<<grid, 256, 0, st>>>(a); break;
+    case 2: k_moe_gate_up<RG, 1, 2><<<grid, 256, 0, st>>>(a); break;
+    default: k_moe_gate_up<RG, 1, 4><<<grid, 256, 0, st>>>(a); break;
+    }
+}
+
+void launch_moe_down(const MoeArgs& a, hipStream_t st) {
+    constexpr int RD = 2;
+    const uint32_t nch = a.I / 32;
+    int lpr = 2;
     while (lpr < (int)nch) lpr <<= 1;
-    if (lpr > 64) lpr = 64;
-    if (lpr < 2) lpr = 2;
-    uint32_t gdown = (a.H + 3) / 4;
-#define DOWN(L, B) k_moe_down<L, 1, B><<<gdown, 256, 0, st>>>(a)
+    if (lpr > 32) throw std::runtime_error("expert width above 1024 is not supported");
+    const uint32_t slots = a.topk + 1, groups_per_wave = 64 / lpr;
+    const uint32_t passes = (slots + groups_per_wave - 1) / groups_per_wave;
+    if (passes > 4) throw std::runtime_error("too many experts per token for the down kernel");
+    if (a.topk >= 64 || a.hc * RD > 64) throw std::runtime_error("routing too wide");
+    const uint32_t gdown = grid_for(a.H / RD, 1024);
+#define DOWN(L, B, P) k_moe_down<L, RD, B, P><<<gdown, 256, 0, st>>>(a)
+#define DOWNP(L, B)                           \
+    switch (passes) {                         \
+    case 1: DOWN(L, B, 1); break;             \
+    case 2: DOWN(L, B, 2); break;             \
+    case 3: DOWN(L, B, 3); break;             \
+    default: DOWN(L, B, 4); break;            \
+    }
 #define DOWNB(B)                              \
     switch (lpr) {                            \
-    case 2: DOWN(2, B); break;                \
-    case 4: DOWN(4, B); break;                \
-    case 8: DOWN(8, B); break;                \
-    case 16: DOWN(16, B); break;              \
-    case 32: DOWN(32, B); break;              \
-    default: DOWN(64, B); break;              \
+    case 2: DOWNP(2, B); break;               \
+    case 4: DOWNP(4, B); break;               \
+    case 8: DOWNP(8, B); break;               \
+    case 16: DOWNP(16, B); break;             \
+    default: DOWNP(32, B); break;             \
     }
     switch (a.X.bits) {
-    case 3:
-        k_moe_gate_up<1, 3><<<grid, 256, 0, st>>>(a);
-        DOWNB(3);
-        break;
-    case 2:
-        k_moe_gate_up<1, 2><<<grid, 256, 0, st>>>(a);
-        DOWNB(2);
-        break;
-    default:
-        k_moe_gate_up<1, 4><<<grid, 256, 0, st>>>(a);
-        DOWNB(4);
-        break;
+    case 3: DOWNB(3); break;
+    case 2: DOWNB(2); break;
+    default: DOWNB(4); break;
     }
 #undef DOWNB
+#undef DOWNP
 #undef DOWN
 }
 
 void launch_lm_head(const Q4Mat& m, const float* x, float* logits, float* pv, uint32_t* pi, uint32_t nparts,
                     uint32_t* out, int nb, hipStream_t st) {
-    CHK_NB_SWITCH(nb, (k_lm_head<NB><<<nparts, 256, 0, st>>>(m, x, logits, pv, pi)));
+    if (nb <= 2) {
+        constexpr int R = 8;
+        CHK_NB_SWITCH(nb, (k_lm_head<R, NB><<<nparts, 256, 0, st>>>(m, x, logits, pv, pi)));
+    } else {
+        constexpr int R = 4;
+        CHK_NB_SWITCH(nb, (k_lm_head<R, NB><<<nparts, 256, 0, st>>>(m, x, logits, pv, pi)));
+    }
     k_argmax_final<<<nb, 256, 0, st>>>(pv, pi, nparts, out);
 }
 

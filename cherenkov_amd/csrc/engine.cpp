@@ -8,9 +8,11 @@
 // computed on the device from the router's ids), no expert streaming.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <memory>
 #include <stdexcept>
 #include <string>
@@ -97,12 +99,17 @@ enum { PROF_NONE = 0, PROF_MOE = 1, PROF_DN_PROJ = 2, PROF_LM_HEAD = 3 };
 struct Scratch {
     uint32_t* tokens;
     float *hyper, *hc_d, *hc_inv, *inj_a, *inj_m, *mixed;
-    float *dn_conv, *dn_z, *dn_decay, *dn_beta, *dn_y;
+    float *dn_conv, *dn_z, *dn_decay, *dn_beta, *dn_y, *dn_ssq;
     float *q_raw, *k_raw, *v_raw, *idx_raw, *q_ready, *attn_out, *part;
     float *router_logits, *router_probs, *sg, *route_w, *act, *mix_out;
     uint32_t *route_ids, *counter;
     float *logits, *pv;
     uint32_t *pi, *out_tok;
+    uint32_t *rowpos, *rowpos_aux;  // device row positions: trunk rows / other callers
+    StepIn* h_in;                   // pinned host, device-mapped
+    StepIn* d_in;
+    uint32_t* h_out;                // pinned host, device-mapped argmax output
+    uint32_t* d_out;
     // MTP
     float *mtp_hyper, *mtp_hn, *mtp_fe, *mtp_fh, *mtp_src, *mtp_logits;
     uint32_t* mtp_out;
@@ -149,6 +156,9 @@ struct ChkEngine {
     std::vector<float> host_logits, host_mtp_logits;
     uint32_t last_mtp_rows = 0;
     bool tracing = false;
+    // captured decode steps, keyed by rows * 2 + snap
+    std::map<int, hipGraphExec_t> graphs;
+    bool use_graphs = true;
     // folded MTP pass results of the last step (one draft per row)
     bool folded_valid = false;
     std::vector<uint32_t> folded;
@@ -195,6 +205,9 @@ struct ChkEngine {
 
     ~ChkEngine() {
         if (st) hipStreamSynchronize(st);
+        for (auto& kv : graphs) hipGraphExecDestroy(kv.second);
+        if (s.h_in) hipHostFree(s.h_in);
+        if (s.h_out) hipHostFree(s.h_out);
         for (void* p : allocs) hipFree(p);
         if (st) hipStreamDestroy(st);
     }
@@ -336,8 +349,8 @@ struct ChkEngine {
                "indexer head dim must be a multiple of 32 up to 256 (gpu/load.rs:29-32)");
         ensure(c.indexer_budget % c.indexer_compress_ratio == 0,
                "indexer budget must be a multiple of the block size (gpu/load.rs:33-36)");
-        ensure(c.num_experts <= 1024 && c.num_experts_per_tok <= 64 && c.num_experts_per_tok <= c.num_experts,
-               "experts per token");
+        ensure(c.num_experts <= 512 && c.num_experts_per_tok <= 64 && c.num_experts_per_tok <= c.num_experts,
+               "at most 512 experts and 64 per token");
         ensure(c.ple_layer == 0, "PLE layers are not supported");
         ensure(c.linear_conv_kernel_dim >= 2 && c.linear_conv_kernel_dim <= 9, "conv kernel 2..=9");
         // QSA selection only matters once complete blocks exceed the budget
@@ -374,6 +387,10 @@ struct ChkEngine {
         D.attn_scale = powf((float)D.hd, -0.5f);
         D.qscale = powf((float)D.dk, -0.5f);
         D.norm_topk = c.norm_topk_prob != 0;
+        // the decode kernels walk row blocks of 4 (R) rows
+        for (uint32_t rows : {D.conv_dim, D.v_dim, D.nv, 2 * D.nh * D.hd, D.kv_row, D.idx_out, D.H, D.V, D.I})
+            ensure(rows % 8 == 0 || (rows % 4 == 0 && rows != D.V), "matrix heights must be multiples of 4 (8 for vocab)");
+        ensure(D.dv % 64 == 0 && D.dv <= 512, "DeltaNet value head dim must be a multiple of 64");
         has_mtp = c.mtp_num_hidden_layers > 0;
         ensure(o.drafts == 0 || has_mtp, "drafts need an MTP head");
         max_t = o.max_t;
@@ -432,6 +449,7 @@ struct ChkEngine {
         s.dn_decay = dalloc<float>(NB * D.nv);
         s.dn_beta = dalloc<float>(NB * D.nv);
         s.dn_y = dalloc<float>(NB * D.v_dim);
+        s.dn_ssq = dalloc<float>((uint64_t)NB * D.nv * (D.dv / 16));
         s.q_raw = dalloc<float>(NB * 2 * D.nh * D.hd);
         s.k_raw = dalloc<float>(NB * D.kv_row);
         s.v_raw = dalloc<float>(NB * D.kv_row);
@@ -453,6 +471,13 @@ struct ChkEngine {
         s.pv = dalloc<float>((uint64_t)NB * lm_parts);
         s.pi = dalloc<uint32_t>((uint64_t)NB * lm_parts);
         s.out_tok = dalloc<uint32_t>(NB);
+        s.rowpos = dalloc<uint32_t>(NB);
+        s.rowpos_aux = dalloc<uint32_t>(NB);
+        HIPCHK(hipHostMalloc((void**)&s.h_in, sizeof(StepIn), hipHostMallocMapped));
+        HIPCHK(hipHostGetDevicePointer((void**)&s.d_in, s.h_in, 0));
+        HIPCHK(hipHostMalloc((void**)&s.h_out, 64, hipHostMallocMapped));
+        HIPCHK(hipHostGetDevicePointer((void**)&s.d_out, s.h_out, 0));
+        memset(s.h_in, 0, sizeof(StepIn));
         s.mtp_hyper = dalloc<float>(NB * D.hh);
         s.mtp_hn = dalloc<float>((uint64_t)NB * (D.H + D.hh));
         s.mtp_src = dalloc<float>((uint64_t)D.hh);
@@ -527,6 +552,7 @@ struct ChkEngine {
         sa.z = s.dn_z;
         sa.norm = L.dn.norm;
         sa.y = s.dn_y;
+        sa.ssq = s.dn_ssq;
         sa.nk = D.nk;
         sa.nv = D.nv;
         sa.dv = D.dv;
@@ -535,10 +561,25 @@ struct ChkEngine {
         sa.qscale = D.qscale;
         sa.snap = snap;
         launch_dn_scan(sa, nb, st);
-        launch_qmv_inject(L.dn.out, s.dn_y, D.v_dim, hyper, inj, D.hc, raw_out, nb, st);
+        InjArgs ia{};
+        ia.m = L.dn.out;
+        ia.x = s.dn_y;
+        ia.xs = D.v_dim;
+        ia.xmode = XM_DN_GATED;
+        ia.z = s.dn_z;
+        ia.norm = L.dn.norm;
+        ia.ssq = s.dn_ssq;
+        ia.dv = D.dv;
+        ia.nheads = D.nv;
+        ia.ssq_blocks = D.dv / 16;
+        ia.hyper = hyper;
+        ia.inj = inj;
+        ia.hc = D.hc;
+        ia.raw_out = raw_out;
+        launch_qmv_inject(ia, nb, st);
     }
 
-    void attention(const LayerDev& L, const float* x, int nb, const KvDev* kvs, const uint32_t* rows_pos,
+    void attention(const LayerDev& L, const float* x, int nb, const KvDev* kvs, const uint32_t* d_rowpos,
                    float* hyper, const float* inj, float* raw_out) {
         SegArgs a{};
         a.nseg = 4;
@@ -561,10 +602,8 @@ struct ChkEngine {
         aa.q_norm = L.at.q_norm;
         aa.k_norm = L.at.k_norm;
         aa.q_ready = s.q_ready;
-        for (int b = 0; b < nb; ++b) {
-            aa.kv[b] = kvs[b];
-            aa.pos[b] = rows_pos[b];
-        }
+        for (int b = 0; b < nb; ++b) aa.kv[b] = kvs[b];
+        aa.pos = d_rowpos;
         aa.part = s.part;
         aa.out = s.attn_out;
         aa.nh = D.nh;
@@ -578,7 +617,16 @@ struct ChkEngine {
         aa.theta = D.theta;
         aa.scale = D.attn_scale;
         launch_attn(aa, nb, st);
-        launch_qmv_inject(L.at.o, s.attn_out, D.nh * D.hd, hyper, inj, D.hc, raw_out, nb, st);
+        InjArgs ia{};
+        ia.m = L.at.o;
+        ia.x = s.attn_out;
+        ia.xs = D.nh * D.hd;
+        ia.xmode = XM_PLAIN;
+        ia.hyper = hyper;
+        ia.inj = inj;
+        ia.hc = D.hc;
+        ia.raw_out = raw_out;
+        launch_qmv_inject(ia, nb, st);
     }
 
     void moe(const LayerDev& L, uint32_t route_slot, const float* x, int nb, float* hyper, const float* inj,
@@ -588,15 +636,9 @@ struct ChkEngine {
         r.shared_gate = L.moe.shared_gate;
         r.x = x;
         r.logits = s.router_logits;
-        r.probs = s.router_probs + (uint64_t)route_slot * MAX_NB * D.E;
         r.sg = s.sg;
-        r.ids = s.route_ids + (uint64_t)route_slot * MAX_NB * D.topk;
-        r.w = s.route_w + (uint64_t)route_slot * MAX_NB * D.topk;
-        r.counter = s.counter;
         r.E = D.E;
         r.H = D.H;
-        r.topk = D.topk;
-        r.norm_topk = D.norm_topk;
         launch_router(r, nb, st);
         MoeArgs m{};
         m.X = experts_dev();
@@ -605,8 +647,14 @@ struct ChkEngine {
         m.sh_up = L.moe.sh_up;
         m.sh_down = L.moe.sh_down;
         m.x = x;
-        m.ids = r.ids;
-        m.w = r.w;
+        m.logits = s.router_logits;
+        m.probs = s.router_probs + (uint64_t)route_slot * MAX_NB * D.E;
+        m.E = D.E;
+        m.norm_topk = D.norm_topk;
+        m.ids_out = s.route_ids + (uint64_t)route_slot * MAX_NB * D.topk;
+        m.w_out = s.route_w + (uint64_t)route_slot * MAX_NB * D.topk;
+        m.ids = m.ids_out;
+        m.w = m.w_out;
         m.sg = s.sg;
         m.act = s.act;
         m.hyper = hyper;
@@ -617,21 +665,21 @@ struct ChkEngine {
         m.I = D.I;
         m.topk = D.topk;
         m.hc = D.hc;
-        // algorithmic bytes: each routed row-slot's expert record (gate, up,
-        // down) + the shared expert, the activations in and out
-        uint64_t bytes = (uint64_t)nb * D.topk * 3 * expert_mat_bytes() + 3 * q4_bytes(L.moe.sh_gate) +
-                         (uint64_t)nb * (D.H * 4 + (D.topk + 1) * D.I * 8 + D.H * 8);
+        // algorithmic bytes of the gate/up kernel: each routed row-slot's
+        // gate and up matrices + the shared expert's, the router logits,
+        // the input rows and the activations written
+        const uint64_t gu_bytes = (uint64_t)nb * D.topk * 2 * expert_mat_bytes() + 2 * q4_bytes(L.moe.sh_gate) +
+                                  (uint64_t)nb * (D.E * 4 + D.H * 4 + (D.topk + 1) * D.I * 4);
         prof_begin(PROF_MOE);
-        launch_moe(m, st);
-        prof_end(PROF_MOE, bytes);
+        launch_moe_gate_up(m, st);
+        prof_end(PROF_MOE, gu_bytes);
+        launch_moe_down(m, st);
     }
 
     // ---------------------------------------------------------- step
     void run_rows(int nb, bool snap) {
-        launch_embed(s.tokens, embed, s.hyper, D.H, D.hc, nb, st);
+        launch_embed(s.d_in, s.tokens, s.rowpos, embed, s.hyper, D.H, D.hc, nb, st);
         KvDev kvs[MAX_NB];
-        uint32_t rows_pos[MAX_NB];
-        for (int b = 0; b < nb; ++b) rows_pos[b] = pos + b;
         for (uint32_t l = 0; l < c.num_hidden_layers; ++l) {
             const LayerDev& L = layers[l];
             hc_read(L.attn_hc, s.hyper, s.inj_a, nb);
@@ -639,7 +687,7 @@ struct ChkEngine {
                 deltanet(L, s.mixed, nb, snap, s.hyper, s.inj_a, nullptr);
             } else {
                 for (int b = 0; b < nb; ++b) kvs[b] = kv[L.at_idx];
-                attention(L, s.mixed, nb, kvs, rows_pos, s.hyper, s.inj_a, nullptr);
+                attention(L, s.mixed, nb, kvs, s.rowpos, s.hyper, s.inj_a, nullptr);
             }
             hc_read(L.mlp_hc, s.hyper, s.inj_m, nb);
             moe(L, l, s.mixed, nb, s.hyper, s.inj_m, nullptr);
@@ -649,7 +697,7 @@ struct ChkEngine {
         }
         hc_read(final_mixer, s.hyper, nullptr, nb);
         prof_begin(PROF_LM_HEAD);
-        launch_lm_head(lm_head, s.mixed, s.logits, s.pv, s.pi, lm_parts, s.out_tok, nb, st);
+        launch_lm_head(lm_head, s.mixed, s.logits, s.pv, s.pi, lm_parts, s.d_out, nb, st);
         prof_end(PROF_LM_HEAD, q4_bytes(lm_head) + (uint64_t)nb * (D.H + D.V) * 4);
     }
 
@@ -666,19 +714,38 @@ struct ChkEngine {
         batch_pos = pos;
         batch_nb = n;
         batch_snap = snap;
-        HIPCHK(hipMemcpyAsync(s.tokens, toks, n * 4, hipMemcpyHostToDevice, st));
-        run_rows((int)n, snap);
+        for (uint32_t i = 0; i < n; ++i) s.h_in->tokens[i] = toks[i];
+        s.h_in->pos = pos;
+        std::atomic_thread_fence(std::memory_order_seq_cst);
+        if (use_graphs && !tracing && prof_kind == PROF_NONE) {
+            const int key = (int)n * 2 + (snap ? 1 : 0);
+            auto it = graphs.find(key);
+            if (it == graphs.end()) {
+                hipGraph_t g;
+                HIPCHK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+                run_rows((int)n, snap);
+                HIPCHK(hipStreamEndCapture(st, &g));
+                hipGraphExec_t ge;
+                HIPCHK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+                HIPCHK(hipGraphDestroy(g));
+                it = graphs.emplace(key, ge).first;
+            }
+            HIPCHK(hipGraphLaunch(it->second, st));
+        } else {
+            run_rows((int)n, snap);
+        }
         if (fold) {
             // pair row b's residual with the trunk's own prediction for it
+            HIPCHK(hipMemcpyAsync(s.out_tok, s.d_out, n * 4, hipMemcpyDeviceToDevice, st));
             mtp_pass_trunk((int)n, batch_pos, s.out_tok);
         }
-        HIPCHK(hipMemcpyAsync(out, s.out_tok, n * 4, hipMemcpyDeviceToHost, st));
         if (fold) {
             folded.assign(n, 0);
             HIPCHK(hipMemcpyAsync(folded.data(), s.mtp_out, n * 4, hipMemcpyDeviceToHost, st));
         }
         HIPCHK(hipStreamSynchronize(st));
         HIPCHK(hipGetLastError());
+        for (uint32_t i = 0; i < n; ++i) out[i] = s.h_out[i];
         prof_collect();
         if (fold) {
             folded_valid = true;
@@ -753,8 +820,9 @@ void ChkEngine::mtp_rows(int rows, const float* src_hyper, const uint32_t* d_tok
         kvs[b] = mtp_kv;
         rows_pos[b] = base_pos + b;
     }
+    HIPCHK(hipMemcpyAsync(s.rowpos_aux, rows_pos, rows * 4, hipMemcpyHostToDevice, st));
     hc_read(L.attn_hc, s.mtp_hyper, s.inj_a, rows);
-    attention(L, s.mixed, rows, kvs, rows_pos, s.mtp_hyper, s.inj_a, nullptr);
+    attention(L, s.mixed, rows, kvs, s.rowpos_aux, s.mtp_hyper, s.inj_a, nullptr);
     hc_read(L.mlp_hc, s.mtp_hyper, s.inj_m, rows);
     moe(L, c.num_hidden_layers, s.mixed, rows, s.mtp_hyper, s.inj_m, nullptr);
     hc_read(mtp_mixer, s.mtp_hyper, nullptr, rows);
@@ -1097,7 +1165,8 @@ int chk_attention_block(ChkEngine* e, uint32_t layer, const float* x, uint32_t n
             kvs[b] = e->kv[L.at_idx];
             rp[b] = pos + b;
         }
-        e->attention(L, x, (int)nb, kvs, rp, nullptr, nullptr, out);
+        HIPCHK(hipMemcpyAsync(e->s.rowpos_aux, rp, nb * 4, hipMemcpyHostToDevice, e->st));
+        e->attention(L, x, (int)nb, kvs, e->s.rowpos_aux, nullptr, nullptr, out);
         HIPCHK(hipStreamSynchronize(e->st));
         HIPCHK(hipGetLastError());
     })
@@ -1126,7 +1195,8 @@ int chk_attention_block2(ChkEngine* e, uint32_t layer, const float* x, const uin
         const LayerDev& L = e->layers[layer];
         KvDev kvs[MAX_NB] = {e->kv[L.at_idx], e->kv2[L.at_idx]};
         uint32_t rp[MAX_NB] = {pos[0], pos[1]};
-        e->attention(L, x, 2, kvs, rp, nullptr, nullptr, out);
+        HIPCHK(hipMemcpyAsync(e->s.rowpos_aux, rp, 2 * 4, hipMemcpyHostToDevice, e->st));
+        e->attention(L, x, 2, kvs, e->s.rowpos_aux, nullptr, nullptr, out);
         HIPCHK(hipStreamSynchronize(e->st));
         HIPCHK(hipGetLastError());
     })

@@ -11,7 +11,7 @@
 
 namespace chk {
 
-__global__ void k_gen_q4(uint32_t* w, uint16_t* s, uint16_t* b, uint64_t nwords, uint64_t ngroups,
+__global__ void __launch_bounds__(256) k_gen_q4(uint32_t* w, uint16_t* s, uint16_t* b, uint64_t nwords, uint64_t ngroups,
                          uint64_t kw, uint64_t ks, uint64_t kb) {
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nwords; i += stride)
@@ -22,7 +22,7 @@ __global__ void k_gen_q4(uint32_t* w, uint16_t* s, uint16_t* b, uint64_t nwords,
     }
 }
 
-__global__ void k_gen_bf16(uint16_t* dst, uint64_t n, uint64_t seed, uint64_t id, uint32_t kind) {
+__global__ void __launch_bounds__(256) k_gen_bf16(uint16_t* dst, uint64_t n, uint64_t seed, uint64_t id, uint32_t kind) {
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
         dst[i] = chk_bf16_elem(seed, id, kind, i);
@@ -39,7 +39,7 @@ struct RecGenArgs {
     uint64_t words[3], groups[3];
 };
 
-__global__ void k_gen_records(RecGenArgs a) {
+__global__ void __launch_bounds__(256) k_gen_records(RecGenArgs a) {
     // blockIdx.y = record within the launch, blockIdx.z = part
     uint32_t rec = blockIdx.y, part = blockIdx.z;
     uint32_t rl = a.layer0 + rec / a.experts, e = rec % a.experts;
@@ -70,7 +70,7 @@ CHK_DEV void slot_of(int c, int& t, int& p, int& byte) {
     else { p = 3; byte = (r - 9) >> 1; }
 }
 
-__global__ void k_repack_lowbit(const uint8_t* __restrict__ src, uint64_t src_stride, uint8_t* __restrict__ dst,
+__global__ void __launch_bounds__(256) k_repack_lowbit(const uint8_t* __restrict__ src, uint64_t src_stride, uint8_t* __restrict__ dst,
                                 uint64_t dst_stride, uint32_t n_records, uint32_t bits, uint64_t mat_codes,
                                 uint64_t src_w0, uint64_t src_w1, uint64_t src_w2, uint64_t dst_mat) {
     uint32_t rec = blockIdx.y, m = blockIdx.z;
@@ -118,7 +118,7 @@ __global__ void k_repack_lowbit(const uint8_t* __restrict__ src, uint64_t src_st
 }
 
 // Scale/bias blocks of a low-bit record are copied verbatim from Q4.
-__global__ void k_copy_scales(const uint8_t* __restrict__ src, uint64_t src_stride, uint8_t* __restrict__ dst,
+__global__ void __launch_bounds__(256) k_copy_scales(const uint8_t* __restrict__ src, uint64_t src_stride, uint8_t* __restrict__ dst,
                               uint64_t dst_stride, uint64_t src_off, uint64_t dst_off, uint64_t bytes) {
     uint32_t rec = blockIdx.y;
     const uint32_t* s = (const uint32_t*)(src + (uint64_t)rec * src_stride + src_off);

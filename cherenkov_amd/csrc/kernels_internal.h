@@ -39,12 +39,31 @@ struct DnScanArgs {
     const float* conv_out;  // [nb][conv_dim] (q | k | v after conv + silu)
     const float* decay;     // [nb][nv]
     const float* beta;      // [nb][nv]
-    const float* z;         // [nb][v_dim]
-    const uint16_t* norm;   // [dv]
-    float* y;               // [nb][v_dim] gated-normed output
+    const float* z;         // [nb][v_dim] output gate input
+    const uint16_t* norm;   // [dv] gated-norm weight
+    float* y;               // [nb][v_dim] y * w * sigmoid(z) (before the 1/rms)
+    float* ssq;             // [nb][nv][dv / 16] partial sums of y^2
     uint32_t nk, nv, dv, qk_dim, conv_dim;
     float qscale;
     int snap;
+};
+
+enum XMode { XM_PLAIN = 0, XM_DN_GATED = 1 };
+
+struct InjArgs {
+    Q4Mat m;
+    const float* x;  // [nb][in]
+    uint32_t xs;
+    int xmode;
+    // XM_DN_GATED: gated RMSNorm of the DeltaNet output per value head
+    const float* z;         // [nb][in] (same stride as x)
+    const uint16_t* norm;   // [dv]
+    const float* ssq;       // [nb][nheads][ssq_blocks]
+    uint32_t dv, nheads, ssq_blocks;
+    float* hyper;  // [nb][hc H] (null: no inject)
+    const float* inj;
+    uint32_t hc;
+    float* raw_out;  // [nb][H] (optional)
 };
 
 struct RouterArgs {
@@ -52,13 +71,8 @@ struct RouterArgs {
     const uint16_t* shared_gate;  // [H]
     const float* x;               // [nb][H]
     float* logits;                // [nb][E]
-    float* probs;                 // [nb][E]
     float* sg;                    // [nb]
-    uint32_t* ids;                // [nb][topk]
-    float* w;                     // [nb][topk]
-    uint32_t* counter;
-    uint32_t E, H, topk;
-    int norm_topk;
+    uint32_t E, H;
 };
 
 struct MoeArgs {
@@ -66,6 +80,14 @@ struct MoeArgs {
     uint32_t record_layer;
     Q4Mat sh_gate, sh_up, sh_down;
     const float* x;        // [nb][H]
+    // routing: the gate/up kernel computes it from the router logits and
+    // publishes ids/w; the down kernel reads them back
+    const float* logits;   // [nb][E]
+    float* probs;          // [nb][E]
+    uint32_t E;
+    int norm_topk;
+    uint32_t* ids_out;     // [nb][topk]
+    float* w_out;          // [nb][topk]
     const uint32_t* ids;   // [nb][topk]
     const float* w;        // [nb][topk]
     const float* sg;       // [nb] shared gate logit
@@ -76,62 +98,105 @@ struct MoeArgs {
     uint32_t nb, H, I, topk, hc;
 };
 
-// Softmax over E logits then top-k by (probability desc, index asc),
-// renormalised (cpu.rs:508-525); one wave, rows b < nb.
+// Wave64 reductions through DPP (quad_perm, row_ror, row_bcast): no LDS
+// round trips.  The result is valid in every lane.
+#define CHK_DPP(v, ctrl, rmask, old) \
+    __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), ctrl, rmask, 0xf, false))
+
+CHK_DEV float wave_max_dpp(float v) {
+    v = fmaxf(v, CHK_DPP(v, 0xb1, 0xf, v));  // quad_perm [1,0,3,2]
+    v = fmaxf(v, CHK_DPP(v, 0x4e, 0xf, v));  // quad_perm [2,3,0,1]
+    v = fmaxf(v, CHK_DPP(v, 0x124, 0xf, v)); // row_ror:4
+    v = fmaxf(v, CHK_DPP(v, 0x128, 0xf, v)); // row_ror:8
+    v = fmaxf(v, CHK_DPP(v, 0x142, 0xa, v)); // row_bcast:15 into rows 1, 3
+    v = fmaxf(v, CHK_DPP(v, 0x143, 0xc, v)); // row_bcast:31 into rows 2, 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+CHK_DEV float wave_sum_dpp(float v) {
+    v += CHK_DPP(v, 0xb1, 0xf, 0.0f);
+    v += CHK_DPP(v, 0x4e, 0xf, 0.0f);
+    v += CHK_DPP(v, 0x124, 0xf, 0.0f);
+    v += CHK_DPP(v, 0x128, 0xf, 0.0f);
+    v += CHK_DPP(v, 0x142, 0xa, 0.0f);
+    v += CHK_DPP(v, 0x143, 0xc, 0.0f);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// "a ranks before b": higher probability, then lower index (cpu.rs:514).
+CHK_DEV void rank_swap(float& va, uint32_t& ia, float& vb, uint32_t& ib) {
+    const bool sw = vb > va || (vb == va && ib < ia);
+    const float tv = sw ? vb : va;
+    const uint32_t ti = sw ? ib : ia;
+    vb = sw ? va : vb;
+    ib = sw ? ia : ib;
+    va = tv;
+    ia = ti;
+}
+
+// Softmax over E <= 512 logits then top-k by (probability desc, index asc),
+// renormalised by the sum of the chosen probabilities taken in rank order
+// (cpu.rs:508-525); one wave, rows b < nb.  Lane l holds experts 8l..8l+7,
+// sorts them with a 19-comparator network, and k rounds of a DPP wave max
+// pop the best head (the lowest lane wins ties, i.e. the lowest index).
+// ids/w may be LDS or global.
 CHK_DEV void topk_wave(const float* logits, float* probs, uint32_t E, uint32_t k, int norm, uint32_t* ids,
-                       float* w, int nb, int lane) {
-    constexpr int MAXE = 16;  // up to 1024 experts per wave
+                       float* w, int nb, int lane, bool write_probs, uint32_t* scratch) {
+    (void)scratch;
+    constexpr int PER = 8;
     for (int b = 0; b < nb; ++b) {
         const float* l = logits + (size_t)b * E;
-        float v[MAXE];
+        float v[PER];
+        uint32_t ix[PER];
         float mx = -INFINITY;
 #pragma unroll
-        for (int j = 0; j < MAXE; ++j) {
-            uint32_t e = lane + 64 * j;
-            v[j] = e < E ? l[e] : -INFINITY;
+        for (int j = 0; j < PER; ++j) {
+            ix[j] = lane * PER + j;
+            v[j] = ix[j] < E ? l[ix[j]] : -INFINITY;
             mx = fmaxf(mx, v[j]);
         }
-        mx = wave_max(mx);
+        mx = wave_max_dpp(mx);
         float sum = 0.0f;
 #pragma unroll
-        for (int j = 0; j < MAXE; ++j) {
-            uint32_t e = lane + 64 * j;
-            v[j] = e < E ? expf(v[j] - mx) : 0.0f;
+        for (int j = 0; j < PER; ++j) {
+            v[j] = ix[j] < E ? expf(v[j] - mx) : 0.0f;
             sum += v[j];
         }
-        sum = wave_sum(sum);
-        float inv = 1.0f / sum;
+        sum = wave_sum_dpp(sum);
+        const float inv = 1.0f / sum;
 #pragma unroll
-        for (int j = 0; j < MAXE; ++j) {
-            uint32_t e = lane + 64 * j;
-            v[j] = e < E ? v[j] * inv : -1.0f;
-            if (e < E) probs[(size_t)b * E + e] = v[j];
+        for (int j = 0; j < PER; ++j) {
+            v[j] = ix[j] < E ? v[j] * inv : -1.0f;
+            if (ix[j] < E && write_probs) probs[(size_t)b * E + ix[j]] = v[j];
         }
-        // ranks are written as found; lane 0 renormalises afterwards
+        // Batcher-style optimal 8-input network (19 comparators)
+#define CS(a, c) rank_swap(v[a], ix[a], v[c], ix[c])
+        CS(0, 2); CS(1, 3); CS(4, 6); CS(5, 7);
+        CS(0, 4); CS(1, 5); CS(2, 6); CS(3, 7);
+        CS(0, 1); CS(2, 3); CS(4, 5); CS(6, 7);
+        CS(2, 4); CS(3, 5);
+        CS(1, 4); CS(3, 6);
+        CS(1, 2); CS(3, 4); CS(5, 6);
+#undef CS
         float topsum = 0.0f;
         for (uint32_t r = 0; r < k; ++r) {
-            float bv = -2.0f;
-            uint32_t bi = 0xffffffffu;
-#pragma unroll
-            for (int j = 0; j < MAXE; ++j) {
-                uint32_t e = lane + 64 * j;
-                if (e < E && (v[j] > bv || (v[j] == bv && e < bi))) { bv = v[j]; bi = e; }
-            }
-#pragma unroll
-            for (int m = 32; m >= 1; m >>= 1) {
-                float ov = __shfl_xor(bv, m, 64);
-                uint32_t oi = __shfl_xor(bi, m, 64);
-                if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-            }
-            if (bi >= E) bi = 0;  // only reachable with NaN logits; keeps ids in range
-            topsum += bv;
+            const float m = wave_max_dpp(v[0]);
+            const uint64_t ball = __ballot(v[0] == m);
+            const int win = (int)__builtin_ctzll(ball);
+            const uint32_t idx = (uint32_t)__builtin_amdgcn_readlane((int)ix[0], win);
             if (lane == 0) {
-                ids[b * k + r] = bi;
-                w[b * k + r] = bv;
+                ids[b * k + r] = idx;
+                w[b * k + r] = m;
             }
+            topsum += m;
+            if (lane == win) {
 #pragma unroll
-            for (int j = 0; j < MAXE; ++j)
-                if (lane + 64 * j == bi) v[j] = -1.0f;
+                for (int j = 0; j + 1 < PER; ++j) {
+                    v[j] = v[j + 1];
+                    ix[j] = ix[j + 1];
+                }
+                v[PER - 1] = -2.0f;
+            }
         }
         if (lane == 0 && norm)
             for (uint32_t r = 0; r < k; ++r) w[b * k + r] = w[b * k + r] / topsum;
@@ -148,25 +213,34 @@ struct AttnArgs {
     const uint16_t* k_norm;
     float* q_ready;        // [nb][nh][hd]
     KvDev kv[MAX_NB];      // cache of each row's sequence
-    uint32_t pos[MAX_NB];  // position of each row (its KV row index)
+    const uint32_t* pos;   // [nb] device: position of each row (its KV row index)
     float* part;           // [nb][nh][max_chunks][hd + 2]
     float* out;            // [nb][nh * hd] gated
     uint32_t nh, nkv, hd, rot, inh, ihd, max_chunks;
     float eps, theta, scale;
 };
 
-void launch_embed(const uint32_t* tokens, const Q4Mat& emb, float* hyper, uint32_t H, uint32_t hc, int nb,
-                  hipStream_t st);
+// Per-step inputs written by the host into pinned, device-mapped memory
+// (read once per step by the first kernel, so a captured graph replays
+// with new tokens and positions).
+struct StepIn {
+    uint32_t tokens[MAX_NB];
+    uint32_t pos;
+    uint32_t pad[3];
+};
+
+void launch_embed(const StepIn* in, uint32_t* tokens, uint32_t* rowpos, const Q4Mat& emb, float* hyper, uint32_t H,
+                  uint32_t hc, int nb, hipStream_t st);
 void launch_hc_down(const HcDev& w, const float* hyper, float* d, float* inj, float* inv, uint32_t H, uint32_t hc,
                     float eps, int nb, hipStream_t st);
 void launch_hc_up_mix(const HcDev& w, const float* hyper, const float* inv, const float* d, float* mixed,
                       uint32_t H, uint32_t hc, int nb, hipStream_t st);
 void launch_qmv(const SegArgs& a, int nb, hipStream_t st);
-void launch_qmv_inject(const Q4Mat& m, const float* x, uint32_t xs, float* hyper, const float* inj, uint32_t hc,
-                       float* raw_out, int nb, hipStream_t st);
+void launch_qmv_inject(const InjArgs& a, int nb, hipStream_t st);
 void launch_dn_scan(const DnScanArgs& a, int nb, hipStream_t st);
 void launch_router(const RouterArgs& a, int nb, hipStream_t st);
-void launch_moe(const MoeArgs& a, hipStream_t st);
+void launch_moe_gate_up(const MoeArgs& a, hipStream_t st);
+void launch_moe_down(const MoeArgs& a, hipStream_t st);
 void launch_lm_head(const Q4Mat& m, const float* x, float* logits, float* pv, uint32_t* pi, uint32_t nparts,
                     uint32_t* out, int nb, hipStream_t st);
 void launch_attn(const AttnArgs& a, int nb, hipStream_t st);

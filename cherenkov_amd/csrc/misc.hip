@@ -38,7 +38,7 @@ __global__ void __launch_bounds__(256) k_mtp_prelude(const uint32_t* __restrict_
     }
 }
 
-__global__ void k_mtp_fold(const float* __restrict__ fe, const float* __restrict__ fh, float* __restrict__ hyper,
+__global__ void __launch_bounds__(256) k_mtp_fold(const float* __restrict__ fe, const float* __restrict__ fh, float* __restrict__ hyper,
                            uint32_t H, uint32_t hc) {
     const uint32_t b = blockIdx.y, i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= H) return;
@@ -47,7 +47,7 @@ __global__ void k_mtp_fold(const float* __restrict__ fe, const float* __restrict
 }
 
 // q8 quantisation of whole cache rows (the kv_append_q8 rule).
-__global__ void k_kv_fill(const float* __restrict__ k, const float* __restrict__ v, KvDev kv, uint64_t n,
+__global__ void __launch_bounds__(256) k_kv_fill(const float* __restrict__ k, const float* __restrict__ v, KvDev kv, uint64_t n,
                           uint32_t kv_row) {
     const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int side = blockIdx.y;

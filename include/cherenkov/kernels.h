@@ -81,7 +81,7 @@ int chk_trace_enable(ChkEngine* e, int on);
 int chk_layer_hyper(ChkEngine* e, uint32_t layer, uint32_t r, float* host);
 
 /* Live kernel profiler: bracket every launch of one kernel class with HIP
- * events on the engine's stream (1 = MoE experts gate/up + down,
+ * events on the engine's stream (1 = MoE experts gate/up,
  * 2 = DeltaNet input projections, 3 = LM head + argmax; 0 = off) and
  * accumulate its algorithmic HBM bytes; chk_profile_read returns the
  * summed event time, launch count and bytes since chk_profile_kernel. */
