@@ -65,61 +65,146 @@ __global__ void __launch_bounds__(256) k_attn_prep(AttnArgs a) {
 
 CHK_DEV float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
 
-// Partials over one chunk of ATTN_CHUNK tokens for (row b, q head h).
+// Partials over one chunk of ATTN_CHUNK tokens for (row b, kv head hk):
+// the G = nh / nkv query heads that share the kv head are served from one
+// read of the chunk's K and V.  Every K and V load of the workgroup is
+// issued before any arithmetic, so the kernel pays one memory latency.
+//
+// Scores: 4 threads per token, each a quarter of the head dims (HD / 4,
+// i.e. HD / 128 q8 blocks of 32).  P.V: lanes own 4 consecutive dims (one
+// u32 of int8 values), NS = 256 / (HD / 4) token slots stride the chunk,
+// and the slots are summed through LDS.
+template <int G, int HD>
 __global__ void __launch_bounds__(256) k_attn_part(AttnArgs a) {
-    __shared__ float red[8];
-    __shared__ float sq[512];
-    __shared__ float sp[ATTN_CHUNK];
-    const uint32_t h = blockIdx.x, c = blockIdx.y, b = blockIdx.z, t = threadIdx.x, hd = a.hd;
+    constexpr int CH = ATTN_CHUNK;          // tokens per chunk (64)
+    constexpr int DPT = HD / 4;             // score dims per thread
+    constexpr int KB = DPT / 32;            // q8 blocks per thread
+    constexpr int QP = HD + 16;             // padded q row (bank spread)
+    constexpr int LPV = HD / 4;             // P.V lanes per token
+    constexpr int NS = 256 / LPV;           // P.V token slots
+    constexpr int TPS = CH / NS;            // tokens per slot
+    static_assert(CH * 4 == 256, "one thread quarter per token");
+    __shared__ __align__(16) float sq[G][QP];
+    __shared__ float sp[G][CH];
+    __shared__ float sml[G][2];
+    __shared__ __align__(16) float so[NS][G][HD];
+    const uint32_t hk = blockIdx.x, c = blockIdx.y, b = blockIdx.z, t = threadIdx.x;
     const uint32_t T = a.pos[b] + 1;  // causal: rows see positions <= their own
-    const uint32_t t0 = c * ATTN_CHUNK;
-    float* part = a.part + (((size_t)b * a.nh + h) * a.max_chunks + c) * (hd + 2);
+    const uint32_t t0 = c * CH;
     if (t0 >= T) return;
     const KvDev& kv = a.kv[b];
-    const uint32_t hk = h / (a.nh / a.nkv), kv_row = a.nkv * hd;
-    for (uint32_t d = t; d < hd; d += blockDim.x) sq[d] = a.q_ready[((size_t)b * a.nh + h) * hd + d];
+    const uint32_t kv_row = a.nkv * HD, n = min((uint32_t)CH, T - t0);
+
+    // ---- issue: K quarter-rows, V u32 lanes, their fp16 scales
+    const uint32_t tk = t >> 2, qq = t & 3;
+    const uint32_t ktok = t0 + min(tk, n - 1);
+    uint4 kw[KB][2];
+    uint16_t ksc[KB];
+#pragma unroll
+    for (int k = 0; k < KB; ++k) {
+        const uint32_t d0 = qq * DPT + k * 32;
+        const uint4* kp = reinterpret_cast<const uint4*>(kv.k + (size_t)ktok * kv_row + hk * HD + d0);
+        kw[k][0] = kp[0];
+        kw[k][1] = kp[1];
+        ksc[k] = kv.ks[(size_t)ktok * (kv_row / 32) + (hk * HD + d0) / 32];
+    }
+    const uint32_t slot = t / LPV, vl = t % LPV;
+    uint32_t vw[TPS];
+    uint16_t vsc[TPS];
+#pragma unroll
+    for (int i = 0; i < TPS; ++i) {
+        const uint32_t vt = t0 + min(slot + (uint32_t)(i * NS), n - 1);
+        vw[i] = *reinterpret_cast<const uint32_t*>(kv.v + (size_t)vt * kv_row + hk * HD + vl * 4);
+        vsc[i] = kv.vs[(size_t)vt * (kv_row / 32) + (hk * HD + vl * 4) / 32];
+    }
+    // q of the G heads into LDS
+    for (uint32_t i = t; i < (uint32_t)(G * HD); i += 256) {
+        const uint32_t g = i / HD, d = i % HD;
+        sq[g][(d / DPT) * (DPT + 4) + d % DPT] = a.q_ready[((size_t)b * a.nh + hk * G + g) * HD + d];
+    }
     __syncthreads();
-    const uint32_t tok = t0 + t;
-    float s = -INFINITY;
-    if (tok < T) {
-        const int8_t* kr = kv.k + (size_t)tok * kv_row + hk * hd;
-        const uint16_t* ks = kv.ks + (size_t)tok * (kv_row / 32) + hk * hd / 32;
-        float acc = 0.0f;
-        for (uint32_t blk = 0; blk < hd / 32; ++blk) {
-            const int4* p = reinterpret_cast<const int4*>(kr + blk * 32);
-            int4 u0 = p[0], u1 = p[1];
-            int w[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
-            float part_acc = 0.0f;
+
+    // ---- scores: s[g][tk] = scale * sum_blocks fp16(ks) * (q . k_int8)
+    float kf[KB][32];
+#pragma unroll
+    for (int k = 0; k < KB; ++k) {
+        const uint32_t w[8] = {kw[k][0].x, kw[k][0].y, kw[k][0].z, kw[k][0].w,
+                               kw[k][1].x, kw[k][1].y, kw[k][1].z, kw[k][1].w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) kf[k][j * 4 + e] = (float)(int8_t)(w[j] >> (8 * e));
+    }
+#pragma unroll 1
+    for (int g = 0; g < G; ++g) {
+        float v = 0.0f;
+#pragma unroll
+        for (int k = 0; k < KB; ++k) {
+            const float4* qp = reinterpret_cast<const float4*>(&sq[g][qq * (DPT + 4) + k * 32]);
+            float acc = 0.0f;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    float kvv = (float)(int8_t)((w[j] >> (8 * k)) & 0xff);
-                    part_acc += sq[blk * 32 + j * 4 + k] * kvv;
-                }
+                const float4 qv = qp[j];
+                acc += qv.x * kf[k][4 * j] + qv.y * kf[k][4 * j + 1] + qv.z * kf[k][4 * j + 2] + qv.w * kf[k][4 * j + 3];
             }
-            acc += part_acc * h2f(ks[blk]);
+            v += acc * h2f(ksc[k]);
         }
-        s = acc * a.scale;
+        v += __shfl_xor(v, 1);
+        v += __shfl_xor(v, 2);
+        if (qq == 0) sp[g][tk] = tk < n ? v * a.scale : -INFINITY;
     }
-    float m = block_max(s, red);
-    float p = tok < T ? expf(s - m) : 0.0f;
-    sp[t] = p;
-    float l = block_sum(p, red);
-    const uint32_t n = min(ATTN_CHUNK, T - t0);
-    for (uint32_t d = t; d < hd; d += blockDim.x) {
-        float o = 0.0f;
-        const uint32_t blkd = (hk * hd + d) / 32;
-        for (uint32_t j = 0; j < n; ++j) {
-            uint32_t tk = t0 + j;
-            float vv = (float)kv.v[(size_t)tk * kv_row + hk * hd + d] * h2f(kv.vs[(size_t)tk * (kv_row / 32) + blkd]);
-            o += sp[j] * vv;
+    __syncthreads();
+
+    // ---- per-head chunk softmax numerators: wave w takes heads w, w + 4, ...
+    const uint32_t wv = t >> 6, lane = t & 63;
+    for (uint32_t g = wv; g < (uint32_t)G; g += 4) {
+        const float s = sp[g][lane];
+        const float m = wave_max(s);
+        const float p = lane < n ? expf(s - m) : 0.0f;
+        sp[g][lane] = p;
+        const float l = wave_sum(p);
+        if (lane == 0) {
+            sml[g][0] = m;
+            sml[g][1] = l;
         }
-        part[2 + d] = o;
     }
-    if (t == 0) {
-        part[0] = m;
-        part[1] = l;
+    __syncthreads();
+
+    // ---- P.V over this slot's tokens
+    float o[G][4];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[g][e] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < TPS; ++i) {
+        const uint32_t j = slot + i * NS;
+        const float ds = h2f(vsc[i]);
+        float vf[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) vf[e] = (float)(int8_t)(vw[i] >> (8 * e)) * ds;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float p = sp[g][j];  // 0 past the chunk's valid tokens
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[g][e] += p * vf[e];
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+        *reinterpret_cast<float4*>(&so[slot][g][vl * 4]) = make_float4(o[g][0], o[g][1], o[g][2], o[g][3]);
+    __syncthreads();
+    for (uint32_t i = t; i < (uint32_t)(G * HD); i += 256) {
+        const uint32_t g = i / HD, d = i % HD;
+        float acc = 0.0f;
+#pragma unroll
+        for (int s2 = 0; s2 < NS; ++s2) acc += so[s2][g][d];
+        float* part = a.part + (((size_t)b * a.nh + hk * G + g) * a.max_chunks + c) * (HD + 2);
+        part[2 + d] = acc;
+        if (d == 0) {
+            part[0] = sml[g][0];
+            part[1] = sml[g][1];
+        }
     }
 }
 
@@ -154,10 +239,34 @@ __global__ void __launch_bounds__(256) k_zero_f32(float* __restrict__ dst, uint6
 // Positions come from device memory and the chunk grid covers the whole
 // context capacity (chunks past a row's length exit at once), so the
 // launch is the same every step and can live in a captured graph.
+bool attn_shape_ok(uint32_t nh, uint32_t nkv, uint32_t hd) {
+    if (nkv == 0 || nh % nkv || (hd != 128 && hd != 256)) return false;
+    const uint32_t g = nh / nkv;
+    return g == 1 || g == 2 || g == 4 || g == 8 || g == 12;
+}
+
+void launch_attn_core(const AttnArgs& a, int nb, hipStream_t st) {
+    const dim3 grid(a.nkv, a.max_chunks, nb);
+#define CHK_ATTN_G(HDV)                                                              \
+    switch (a.nh / a.nkv) {                                                          \
+    case 1: k_attn_part<1, HDV><<<grid, 256, 0, st>>>(a); break;                     \
+    case 2: k_attn_part<2, HDV><<<grid, 256, 0, st>>>(a); break;                     \
+    case 4: k_attn_part<4, HDV><<<grid, 256, 0, st>>>(a); break;                     \
+    case 8: k_attn_part<8, HDV><<<grid, 256, 0, st>>>(a); break;                     \
+    default: k_attn_part<12, HDV><<<grid, 256, 0, st>>>(a); break;                   \
+    }
+    if (a.hd == 128) {
+        CHK_ATTN_G(128)
+    } else {
+        CHK_ATTN_G(256)
+    }
+#undef CHK_ATTN_G
+    k_attn_combine<<<dim3(a.nh, nb), 256, 0, st>>>(a);
+}
+
 void launch_attn(const AttnArgs& a, int nb, hipStream_t st) {
     k_attn_prep<<<dim3(a.nh + 2 * a.nkv + 1, nb), a.hd, 0, st>>>(a);
-    k_attn_part<<<dim3(a.nh, a.max_chunks, nb), ATTN_CHUNK, 0, st>>>(a);
-    k_attn_combine<<<dim3(a.nh, nb), 256, 0, st>>>(a);
+    launch_attn_core(a, nb, st);
 }
 
 void launch_copy_f32(float* dst, const float* src, uint64_t n, hipStream_t st) {

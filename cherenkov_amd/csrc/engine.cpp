@@ -391,6 +391,8 @@ struct ChkEngine {
         for (uint32_t rows : {D.conv_dim, D.v_dim, D.nv, 2 * D.nh * D.hd, D.kv_row, D.idx_out, D.H, D.V, D.I})
             ensure(rows % 8 == 0 || (rows % 4 == 0 && rows != D.V), "matrix heights must be multiples of 4 (8 for vocab)");
         ensure(D.dv % 64 == 0 && D.dv <= 512, "DeltaNet value head dim must be a multiple of 64");
+        ensure(attn_shape_ok(D.nh, D.nkv, D.hd),
+               "attention needs head_dim 128 or 256 and 1, 2, 4, 8 or 12 query heads per kv head");
         has_mtp = c.mtp_num_hidden_layers > 0;
         ensure(o.drafts == 0 || has_mtp, "drafts need an MTP head");
         max_t = o.max_t;
@@ -1083,6 +1085,69 @@ int chk_q4_matvec(const void* w, const void* s, const void* b, uint32_t out, uin
         launch_qmv(a, (int)nb, st);
         HIPCHK(hipStreamSynchronize(st));
         HIPCHK(hipGetLastError());
+    })
+}
+
+int chk_lm_head_argmax(const void* w, const void* s, const void* b, uint32_t out, uint32_t in, const float* x,
+                       uint32_t nb, float* logits, uint32_t* ids, void* stream) {
+    CHK_TRY({
+        ensure(nb >= 1 && nb <= (uint32_t)MAX_NB, "nb must be 1..=4");
+        ensure(in % 64 == 0 && in > 0, "in must be a positive multiple of 64");
+        ensure(out > 0 && out % 8 == 0, "out must be a positive multiple of 8");
+        const uint32_t parts = 1024;
+        hipStream_t st = (hipStream_t)stream;
+        float* pv = nullptr;
+        uint32_t* pi = nullptr;
+        uint32_t* d_ids = nullptr;
+        HIPCHK(hipMalloc(&pv, (size_t)nb * parts * 4));
+        HIPCHK(hipMalloc(&pi, (size_t)nb * parts * 4));
+        HIPCHK(hipMalloc(&d_ids, (size_t)nb * 4));
+        launch_lm_head(Q4Mat{(const uint32_t*)w, (const uint16_t*)s, (const uint16_t*)b, out, in}, x, logits, pv, pi,
+                       parts, d_ids, (int)nb, st);
+        HIPCHK(hipMemcpyAsync(ids, d_ids, (size_t)nb * 4, hipMemcpyDeviceToDevice, st));
+        HIPCHK(hipStreamSynchronize(st));
+        HIPCHK(hipGetLastError());
+        HIPCHK(hipFree(pv));
+        HIPCHK(hipFree(pi));
+        HIPCHK(hipFree(d_ids));
+    })
+}
+
+int chk_attn_decode_q8(const float* q, const void* k, const void* v, const void* ks, const void* vs, uint32_t T,
+                       uint32_t nh, uint32_t nkv, uint32_t hd, float* out, void* stream) {
+    CHK_TRY({
+        ensure(T > 0, "empty context");
+        ensure(attn_shape_ok(nh, nkv, hd), "head_dim 128 or 256, 1, 2, 4, 8 or 12 query heads per kv head");
+        hipStream_t st = (hipStream_t)stream;
+        AttnArgs a{};
+        a.nh = nh;
+        a.nkv = nkv;
+        a.hd = hd;
+        a.max_chunks = (T + ATTN_CHUNK - 1) / ATTN_CHUNK;
+        a.scale = powf((float)hd, -0.5f);
+        a.q_raw = q;
+        a.kv[0] = KvDev{(int8_t*)k, (int8_t*)v, (uint16_t*)ks, (uint16_t*)vs, nullptr};
+        float* q_ready = nullptr;
+        float* part = nullptr;
+        uint32_t* pos = nullptr;
+        HIPCHK(hipMalloc(&q_ready, (size_t)nh * hd * 4));
+        HIPCHK(hipMalloc(&part, (size_t)nh * a.max_chunks * (hd + 2) * 4));
+        HIPCHK(hipMalloc(&pos, 4));
+        const uint32_t last = T - 1;
+        HIPCHK(hipMemcpyAsync(pos, &last, 4, hipMemcpyHostToDevice, st));
+        // the q halves of the per-head [q | gate] rows
+        HIPCHK(hipMemcpy2DAsync(q_ready, (size_t)hd * 4, q, (size_t)2 * hd * 4, (size_t)hd * 4, nh,
+                                hipMemcpyDeviceToDevice, st));
+        a.q_ready = q_ready;
+        a.part = part;
+        a.pos = pos;
+        a.out = out;
+        launch_attn_core(a, 1, st);
+        HIPCHK(hipStreamSynchronize(st));
+        HIPCHK(hipGetLastError());
+        HIPCHK(hipFree(q_ready));
+        HIPCHK(hipFree(part));
+        HIPCHK(hipFree(pos));
     })
 }
 

@@ -244,6 +244,8 @@ void launch_moe_down(const MoeArgs& a, hipStream_t st);
 void launch_lm_head(const Q4Mat& m, const float* x, float* logits, float* pv, uint32_t* pi, uint32_t nparts,
                     uint32_t* out, int nb, hipStream_t st);
 void launch_attn(const AttnArgs& a, int nb, hipStream_t st);
+void launch_attn_core(const AttnArgs& a, int nb, hipStream_t st);
+bool attn_shape_ok(uint32_t nh, uint32_t nkv, uint32_t hd);
 void launch_copy_f32(float* dst, const float* src, uint64_t n, hipStream_t st);
 void launch_kv_fill(const float* k, const float* v, KvDev kv, uint32_t kv_row, uint32_t T, hipStream_t st);
 void launch_zero_f32(float* dst, uint64_t n, hipStream_t st);

@@ -28,6 +28,24 @@ extern "C" {
 int chk_q4_matvec(const void* w, const void* s, const void* b, uint32_t out, uint32_t in, const float* x,
                   float* y, uint32_t nb, void* stream);
 
+/* The decode LM head: logits [nb][out] = W x as chk_q4_matvec, and ids[nb]
+ * (device u32) = the greedy token of each row, lowest index on exact ties,
+ * 0 when every logit is -inf (argmax_partial/argmax_final,
+ * kernels/common/sampling.metal:10-84; head_b, gpu/sampling.rs:10-63).
+ * out must be a multiple of 8. */
+int chk_lm_head_argmax(const void* w, const void* s, const void* b, uint32_t out, uint32_t in, const float* x,
+                       uint32_t nb, float* logits, uint32_t* ids, void* stream);
+
+/* Flash-decode core over a q8 KV cache of T tokens (no projections, norms
+ * or RoPE): q f32 [nh][2 hd] holds each head's [q | gate] (the q_proj row
+ * order, cpu.rs:577-582); k, v int8 [T][nkv hd]; ks, vs fp16 [T][nkv hd/32];
+ * out f32 [nh][hd] = softmax(q.k / sqrt(hd)) . v * sigmoid(gate), each
+ * value dequantised as q8 * fp16 scale (attn_part2_q8 + attn_combine,
+ * kernels/common/attention.metal:138-185,236-310).  hd is 128 or 256 and
+ * nh / nkv one of 1, 2, 4, 8, 12. */
+int chk_attn_decode_q8(const float* q, const void* k, const void* v, const void* ks, const void* vs, uint32_t T,
+                       uint32_t nh, uint32_t nkv, uint32_t hd, float* out, void* stream);
+
 /* MoE block of decoder layer `layer` (num_hidden_layers = the MTP layer) on
  * normalised inputs x [nb][H]: out [nb][H] = routed experts (per the
  * engine's expert precision) + sigmoid-gated shared expert; top_ids

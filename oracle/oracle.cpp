@@ -588,6 +588,51 @@ std::vector<float> mlp(const QL& gate, const QL& up, const QL& down, const float
     return out;
 }
 
+// Routing of moe (src/qwen4_exp/cpu.rs:509-525): sort the softmax
+// probabilities by f32::total_cmp descending with the expert index
+// ascending on ties, keep the first k, renormalise by their sum when
+// norm_topk_prob.
+void route_topk(const float* probs, size_t E, size_t k, bool norm, uint32_t* ids, float* wts) {
+    std::vector<uint32_t> idx(E);
+    for (size_t i = 0; i < E; ++i) idx[i] = (uint32_t)i;
+    std::sort(idx.begin(), idx.end(), [&](uint32_t a, uint32_t b) {
+        int32_t ka = total_key(probs[a]), kb = total_key(probs[b]);
+        if (ka != kb) return ka > kb;
+        return a < b;
+    });
+    float sum = 0.0f;
+    for (size_t i = 0; i < k; ++i) sum += probs[idx[i]];
+    for (size_t i = 0; i < k; ++i) {
+        ids[i] = idx[i];
+        wts[i] = norm ? probs[idx[i]] / sum : probs[idx[i]];
+    }
+}
+
+// One value head of the gated delta rule (src/qwen4_exp/cpu.rs:777-812):
+// S <- decay S; kv = S^T k; delta = beta (v - kv); S <- S + k delta^T;
+// y = S^T q.  S is [dk][dv] (the CPU order); y is accumulated into yh.
+void delta_head_step(float* s, const float* qh, const float* kh, const float* vh, float decay, float beta,
+                     size_t dk, size_t dv, float* yh) {
+    std::vector<float> kv_mem(dv, 0.0f), delta(dv);
+    for (size_t ik = 0; ik < dk; ++ik) {
+        float* row = s + ik * dv;
+        float kw = kh[ik];
+        for (size_t iv = 0; iv < dv; ++iv) {
+            row[iv] *= decay;
+            kv_mem[iv] += row[iv] * kw;
+        }
+    }
+    for (size_t iv = 0; iv < dv; ++iv) delta[iv] = (vh[iv] - kv_mem[iv]) * beta;
+    for (size_t ik = 0; ik < dk; ++ik) {
+        float* row = s + ik * dv;
+        float kw = kh[ik], qw = qh[ik];
+        for (size_t iv = 0; iv < dv; ++iv) {
+            row[iv] += kw * delta[iv];
+            yh[iv] += row[iv] * qw;
+        }
+    }
+}
+
 // moe, src/qwen4_exp/cpu.rs:504-541.  Also reports the routing (top ids in
 // rank order, renormalised weights, full softmax) for the parity tests.
 std::vector<float> moe(OrcModel& m, const MoeW& w, const float* x, uint32_t* top_out, float* w_out,
@@ -597,19 +642,13 @@ std::vector<float> moe(OrcModel& m, const MoeW& w, const float* x, uint32_t* top
     std::vector<float> logits = bf16_matvec(w.router.data(), E, h, x);
     softmax(logits.data(), E);
     if (probs_out) memcpy(probs_out, logits.data(), E * 4);
-    std::vector<uint32_t> idx(E);
-    for (size_t i = 0; i < E; ++i) idx[i] = (uint32_t)i;
-    std::sort(idx.begin(), idx.end(), [&](uint32_t a, uint32_t b) {
-        int32_t ka = total_key(logits[a]), kb = total_key(logits[b]);
-        if (ka != kb) return ka > kb;
-        return a < b;
-    });
-    float sum = 0.0f;
-    for (size_t i = 0; i < k; ++i) sum += logits[idx[i]];
+    std::vector<uint32_t> idx(k);
+    std::vector<float> wts(k);
+    route_topk(logits.data(), E, k, c.norm_topk_prob != 0, idx.data(), wts.data());
     std::vector<float> out(h, 0.0f);
     for (size_t i = 0; i < k; ++i) {
         uint32_t ei = idx[i];
-        float weight = c.norm_topk_prob ? logits[ei] / sum : logits[ei];
+        float weight = wts[i];
         if (top_out) top_out[i] = ei;
         if (w_out) w_out[i] = weight;
         const uint8_t* rec = m.record(w.record_layer, ei);
@@ -679,6 +718,37 @@ std::vector<size_t> select_tokens(const OrcModel& m, const AttnW& w, const float
 // q = rint(v/d) clamped to +-127, fp16 d; kernels/common/attention.metal:
 // 225-233) instead of f32 — the q8-aware restatement the attention parity
 // tests compare against.
+// The attention core of attention (src/qwen4_exp/cpu.rs:587-633): per q
+// head h (kv head h / (nh / nkv)), scores = q.k_t * hd^-1/2 over the
+// selected tokens, softmax, o = sum p v_t, then o *= sigmoid(gate).  qg
+// holds each head's [q | gate] (2 hd values); k, v are [T][nkv hd].
+void attend(const float* qg, const float* kc, const float* vc, const std::vector<size_t>& selected, size_t nh,
+            size_t nkv, size_t hd, float* out) {
+    size_t kv_row = nkv * hd, group = nh / nkv;
+    float scale = powf((float)hd, -0.5f);
+    std::vector<float> scores(selected.size());
+    for (size_t hi = 0; hi < nh; ++hi) {
+        size_t hk = hi / group;
+        const float* q = qg + hi * 2 * hd;
+        for (size_t si = 0; si < selected.size(); ++si) {
+            const float* kt = kc + selected[si] * kv_row + hk * hd;
+            float s = 0.0f;
+            for (size_t d = 0; d < hd; ++d) s += q[d] * kt[d];
+            scores[si] = scale * s;
+        }
+        softmax(scores.data(), scores.size());
+        float* oh = out + hi * hd;
+        for (size_t d = 0; d < hd; ++d) oh[d] = 0.0f;
+        for (size_t si = 0; si < selected.size(); ++si) {
+            const float* vt = vc + selected[si] * kv_row + hk * hd;
+            float p = scores[si];
+            for (size_t d = 0; d < hd; ++d) oh[d] += p * vt[d];
+        }
+        const float* gate = qg + hi * 2 * hd + hd;
+        for (size_t d = 0; d < hd; ++d) oh[d] *= sigmoid(gate[d]);
+    }
+}
+
 std::vector<float> attention(const OrcModel& m, const AttnW& w, const float* x, KvCache& cache, size_t pos,
                              bool kv_q8);
 
@@ -705,34 +775,15 @@ std::vector<float> deltanet(const OrcModel& m, const DeltaW& w, const float* x, 
         l2_norm(keys.data() + hi * dk, dk, 1e-6f);
     }
     size_t group = nv / nk;
-    std::vector<float> y(v_dim, 0.0f), kv_mem(dv), delta(dv);
+    std::vector<float> y(v_dim, 0.0f);
     for (size_t hv = 0; hv < nv; ++hv) {
         size_t hk = hv / group;
-        const float* qh = q.data() + hk * dk;
-        const float* kh = keys.data() + hk * dk;
         float beta = sigmoid(beta_input[hv]);
         float g = -(expf(bf(w.a_log[hv]))) * softplus(decay_input[hv] + bf(w.dt_bias[hv]));
         float decay = expf(g);
-        float* s = st.s.data() + hv * dk * dv;
-        std::fill(kv_mem.begin(), kv_mem.end(), 0.0f);
-        for (size_t ik = 0; ik < dk; ++ik) {
-            float* row = s + ik * dv;
-            float kw = kh[ik];
-            for (size_t iv = 0; iv < dv; ++iv) {
-                row[iv] *= decay;
-                kv_mem[iv] += row[iv] * kw;
-            }
-        }
-        for (size_t iv = 0; iv < dv; ++iv) delta[iv] = (v[hv * dv + iv] - kv_mem[iv]) * beta;
         float* yh = y.data() + hv * dv;
-        for (size_t ik = 0; ik < dk; ++ik) {
-            float* row = s + ik * dv;
-            float kw = kh[ik], qw = qh[ik];
-            for (size_t iv = 0; iv < dv; ++iv) {
-                row[iv] += kw * delta[iv];
-                yh[iv] += row[iv] * qw;
-            }
-        }
+        delta_head_step(st.s.data() + hv * dk * dv, q.data() + hk * dk, keys.data() + hk * dk, v + hv * dv, decay,
+                        beta, dk, dv, yh);
         rms_norm(yh, w.norm.data(), dv, 1e-6f);
         for (size_t iv = 0; iv < dv; ++iv) yh[iv] *= sigmoid(gate_input[hv * dv + iv]);
     }
@@ -821,30 +872,8 @@ std::vector<float> attention(const OrcModel& m, const AttnW& w, const float* x, 
     size_t t_len = cache.len;
     if (t_len != pos + 1) throw std::runtime_error("attention cache out of step");
     std::vector<size_t> selected = select_tokens(m, w, qk.data(), cache, pos);
-    float scale = powf((float)hd, -0.5f);
-    size_t group = nh / nkv;
-    std::vector<float> out(nh * hd, 0.0f), scores(selected.size());
-    for (size_t hi = 0; hi < nh; ++hi) {
-        size_t hk = hi / group;
-        const float* q = qg.data() + hi * 2 * hd;
-        for (size_t si = 0; si < selected.size(); ++si) {
-            size_t ti = selected[si];
-            const float* kt = cache.k.data() + ti * kv_row + hk * hd;
-            float s = 0.0f;
-            for (size_t d = 0; d < hd; ++d) s += q[d] * kt[d];
-            scores[si] = scale * s;
-        }
-        softmax(scores.data(), scores.size());
-        float* oh = out.data() + hi * hd;
-        for (size_t si = 0; si < selected.size(); ++si) {
-            size_t ti = selected[si];
-            const float* vt = cache.v.data() + ti * kv_row + hk * hd;
-            float p = scores[si];
-            for (size_t d = 0; d < hd; ++d) oh[d] += p * vt[d];
-        }
-        const float* gate = qg.data() + hi * 2 * hd + hd;
-        for (size_t d = 0; d < hd; ++d) oh[d] *= sigmoid(gate[d]);
-    }
+    std::vector<float> out(nh * hd, 0.0f);
+    attend(qg.data(), cache.k.data(), cache.v.data(), selected, nh, nkv, hd, out.data());
     std::vector<float> o(w.o.view.out);
     matvec(w.o.view, out.data(), o.data());
     return o;
@@ -1171,6 +1200,19 @@ void orc_rms_norm(float* x, const uint16_t* w, uint32_t n, float eps) { rms_norm
 void orc_l2_norm(float* x, uint32_t n, float eps) { l2_norm(x, n, eps); }
 void orc_rope_partial(float* x, uint32_t pos, uint32_t rot, float theta) { rope_partial(x, pos, rot, theta); }
 float orc_softplus(float v) { return softplus(v); }
+void orc_attend(const float* qg, const float* k, const float* v, uint32_t T, uint32_t nh, uint32_t nkv, uint32_t hd,
+                float* out) {
+    std::vector<size_t> all(T);
+    for (uint32_t t = 0; t < T; ++t) all[t] = t;
+    orc::attend(qg, k, v, all, nh, nkv, hd, out);
+}
+void orc_route_topk(const float* probs, uint32_t E, uint32_t k, int norm, uint32_t* ids, float* wts) {
+    orc::route_topk(probs, E, k, norm != 0, ids, wts);
+}
+void orc_delta_head_step(float* s, const float* q, const float* k, const float* v, float decay, float beta,
+                         uint32_t dk, uint32_t dv, float* y) {
+    orc::delta_head_step(s, q, k, v, decay, beta, dk, dv, y);
+}
 void orc_q8_roundtrip(float* row, uint32_t n) { orc::q8_roundtrip(row, n); }
 uint16_t orc_f32_to_f16(float v) { return orc::f32_to_f16(v); }
 void orc_causal_conv(float* qkv, uint32_t n, const uint16_t* w, float* hist, uint32_t ck) {

@@ -45,6 +45,9 @@ _SIGS = [
     ("orc_l2_norm", None, [P, u32, f32]),
     ("orc_rope_partial", None, [P, u32, u32, f32]),
     ("orc_softplus", f32, [f32]),
+    ("orc_route_topk", None, [P, u32, u32, i32, P, P]),
+    ("orc_attend", None, [P, P, P, u32, u32, u32, u32, P]),
+    ("orc_delta_head_step", None, [P, P, P, P, f32, f32, u32, u32, P]),
     ("orc_q8_roundtrip", None, [P, u32]),
     ("orc_f32_to_f16", C.c_uint16, [f32]),
     ("orc_causal_conv", None, [P, u32, P, P, u32]),
@@ -260,6 +263,40 @@ def rope_partial(x, pos, rot, theta) -> np.ndarray:
 
 def softplus(v: float) -> float:
     return lib().orc_softplus(v)
+
+
+def attend(qg, k, v, nh: int, nkv: int, hd: int) -> np.ndarray:
+    """Attention core over all T cached tokens: qg [nh][2 hd] ([q | gate]
+    per head), k, v [T][nkv hd] -> out [nh][hd]."""
+    qg = np.ascontiguousarray(qg, dtype=np.float32)
+    k = np.ascontiguousarray(k, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    T = k.size // (nkv * hd)
+    out = np.empty(nh * hd, np.float32)
+    lib().orc_attend(_p(qg), _p(k), _p(v), T, nh, nkv, hd, _p(out))
+    return out.reshape(nh, hd)
+
+
+def route_topk(probs, k: int, norm: bool):
+    """Expert ids in rank order and their (renormalised) weights."""
+    p = np.ascontiguousarray(probs, dtype=np.float32)
+    ids = np.empty(k, np.uint32)
+    w = np.empty(k, np.float32)
+    lib().orc_route_topk(_p(p), p.size, k, int(norm), _p(ids), _p(w))
+    return ids, w
+
+
+def delta_head_step(state, q, k, v, decay: float, beta: float):
+    """One gated delta-rule step of one value head: returns (new state
+    [dk][dv], y [dv]); the input state is not modified."""
+    s = np.array(state, dtype=np.float32)
+    dk, dv = s.shape
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    y = np.zeros(dv, np.float32)
+    lib().orc_delta_head_step(_p(s), _p(q), _p(k), _p(v), decay, beta, dk, dv, _p(y))
+    return s, y
 
 
 def q8_roundtrip(x) -> np.ndarray:

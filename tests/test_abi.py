@@ -1,0 +1,49 @@
+"""The drop-in boundary without a GPU: libcherenkov.so loads, exports
+every function include/cherenkov/*.h declares, and the Python mirror's
+ctypes signatures cover exactly those functions.  No compute calls."""
+
+from __future__ import annotations
+
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+from cherenkov_amd import abi
+
+ROOT = Path(__file__).resolve().parent.parent
+DECL = re.compile(r"^[A-Za-z_][\w \*]*?\b(chk_\w+)\s*\(", re.M)
+
+
+def header_functions() -> set[str]:
+    names = set()
+    for h in sorted((ROOT / "include" / "cherenkov").glob("*.h")):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        text = re.sub(r"//[^\n]*", "", text)
+        for m in DECL.finditer(text):
+            if not m.group(0).lstrip().startswith(("static", "CHK_HD", "inline")):
+                names.add(m.group(1))
+    return names
+
+
+def test_headers_declare_the_engine_api():
+    names = header_functions()
+    for n in ("chk_engine_load", "chk_step_rows", "chk_commit", "chk_mtp_draft", "chk_prefill_chunk",
+              "chk_q4_matvec", "chk_moe_block", "chk_decode_step", "chk_last_error"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    if not abi.LIB_PATH.exists():
+        pytest.skip("libcherenkov.so not built (run __graft_entry__.build())")
+    L = C.CDLL(str(abi.LIB_PATH))
+    missing = [n for n in sorted(header_functions()) if not hasattr(L, n)]
+    assert not missing, f"declared but not exported: {missing}"
+
+
+def test_python_signatures_match_headers():
+    declared = header_functions()
+    bound = {n for n, _, _ in abi.SIGNATURES}
+    assert bound <= declared, f"bound but not declared: {sorted(bound - declared)}"
+    assert declared <= bound, f"declared but not bound: {sorted(declared - bound)}"
