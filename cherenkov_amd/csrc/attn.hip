@@ -210,18 +210,38 @@ __global__ void __launch_bounds__(256) k_attn_part(AttnArgs a) {
 
 // LSE merge of the chunk partials and the per-dim sigmoid gate
 // (cpu.rs:629-633: the gate is the second half of each head's q_proj rows).
+// The chunk maxima and weights exp(m_c - M) go through LDS; each thread
+// then owns output dims and sums its partials with 8 chunks' loads in
+// flight.
 __global__ void __launch_bounds__(256) k_attn_combine(AttnArgs a) {
-    const uint32_t h = blockIdx.x, b = blockIdx.y, hd = a.hd;
+    __shared__ float red[8];
+    __shared__ float sw[MAX_ATTN_CHUNKS];
+    const uint32_t h = blockIdx.x, b = blockIdx.y, hd = a.hd, t = threadIdx.x;
     const uint32_t T = a.pos[b] + 1, nc = (T + ATTN_CHUNK - 1) / ATTN_CHUNK;
     const float* part = a.part + ((size_t)b * a.nh + h) * a.max_chunks * (hd + 2);
-    float M = -INFINITY;
-    for (uint32_t c = 0; c < nc; ++c) M = fmaxf(M, part[c * (hd + 2)]);
-    float L = 0.0f;
-    for (uint32_t c = 0; c < nc; ++c) L += part[c * (hd + 2) + 1] * expf(part[c * (hd + 2)] - M);
-    for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x) {
+    float m = -INFINITY;
+    for (uint32_t c = t; c < nc; c += blockDim.x) m = fmaxf(m, part[(size_t)c * (hd + 2)]);
+    const float M = block_max(m, red);
+    float l = 0.0f;
+    for (uint32_t c = t; c < nc; c += blockDim.x) {
+        const float w = expf(part[(size_t)c * (hd + 2)] - M);
+        sw[c] = w;
+        l += part[(size_t)c * (hd + 2) + 1] * w;
+    }
+    const float L = block_sum(l, red);  // its barriers also publish sw
+    for (uint32_t d = t; d < hd; d += blockDim.x) {
+        const float* pd = part + 2 + d;
         float o = 0.0f;
-        for (uint32_t c = 0; c < nc; ++c) o += part[c * (hd + 2) + 2 + d] * expf(part[c * (hd + 2)] - M);
-        float gate = a.q_raw[(size_t)b * a.nh * 2 * hd + h * 2 * hd + hd + d];
+        uint32_t c = 0;
+        for (; c + 8 <= nc; c += 8) {
+            float v[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = pd[(size_t)(c + k) * (hd + 2)];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) o += v[k] * sw[c + k];
+        }
+        for (; c < nc; ++c) o += pd[(size_t)c * (hd + 2)] * sw[c];
+        const float gate = a.q_raw[(size_t)b * a.nh * 2 * hd + h * 2 * hd + hd + d];
         a.out[(size_t)b * a.nh * hd + h * hd + d] = o / L * sigmoidf_(gate);
     }
 }

@@ -736,56 +736,68 @@ __global__ void __launch_bounds__(256) k_router(RouterArgs a) {
 }
 
 // ----------------------------------------------------- experts: gate/up
-// Prologue: softmax + top-k of the router logits (every workgroup, into
-// LDS; workgroup 0 publishes ids/weights for the down kernel).  Then
 // act[b][slot][i] = silu(gate_i . x_b) * (up_i . x_b) for the top-k routed
 // experts of row b (slots 0..k-1) and the shared expert (slot k) (mlp,
-// cpu.rs:981-992).  A wave task is (row, slot, R consecutive i): the
-// gate and up rows of all R are loaded together.
-template <int R, int NB1, int BITS>
+// cpu.rs:981-992).  One task per wave: (row, slot, R consecutive i), the
+// gate and up rows of all R loaded together.  A routed wave ranks its own
+// row's experts (route_row) down to its slot while its x loads are in
+// flight; the wave of slot k-1, i0 = 0 ranks all k and publishes the
+// routing (ids, renormalised weights) for the down kernel.
+template <int R, int BITS>
 __global__ void __launch_bounds__(256) k_moe_gate_up(MoeArgs a) {
-    __shared__ uint32_t s_ids[MAX_NB * 64];
-    __shared__ float s_w[MAX_NB * 64];
-    __shared__ uint32_t s_scr[128];
     const int lane = threadIdx.x & 63;
-    if (wave_id() == 0) {
-        topk_wave(a.logits, a.probs, a.E, a.topk, a.norm_topk, s_ids, s_w, a.nb, lane, blockIdx.x == 0, s_scr);
-        if (blockIdx.x == 0 && lane == 0)
-            for (uint32_t j = 0; j < a.nb * a.topk; ++j) {
-                a.ids_out[j] = s_ids[j];
-                a.w_out[j] = s_w[j];
-            }
-    }
-    __syncthreads();
     const uint32_t slots = a.topk + 1, blocks = a.I / R;
     const uint32_t tasks = a.nb * slots * blocks;
-    for (uint32_t t = global_wave(); t < tasks; t += total_waves()) {
-        const uint32_t b = t / (slots * blocks), slot = (t / blocks) % slots, i0 = (t % blocks) * R;
-        uint32_t rows[R];
+    const uint32_t t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (t >= tasks) return;
+    const uint32_t b = t / (slots * blocks), slot = (t / blocks) % slots, i0 = (t % blocks) * R;
+    uint32_t rows[R];
 #pragma unroll
-        for (int i = 0; i < R; ++i) rows[i] = i0 + i;
-        float g[R][1], u[R][1];
-        XFrag<1, 1> xr;
-        if (slot < a.topk) {
-            const uint32_t e = min(s_ids[b * a.topk + slot], a.X.experts - 1);
-            const uint8_t* rec = a.X.base + ((size_t)a.record_layer * a.X.experts + e) * a.X.stride;
-            ExpFrag<64, 1, R, BITS> fg, fu;
-            fg.issue(expert_mat(a.X, rec, 0, a.I, a.H), rows, lane);
-            fu.issue(expert_mat(a.X, rec, 1, a.I, a.H), rows, lane);
-            load_x<64, 1, 1>(a.x + (size_t)b * a.H, 0, a.H >> 5, lane, xr);
-            fg.template dot<1>(xr, g);
-            fu.template dot<1>(xr, u);
-        } else {
-            Q4Frag<64, 1, R> fg, fu;
-            fg.issue(a.sh_gate, rows, lane);
-            fu.issue(a.sh_up, rows, lane);
-            load_x<64, 1, 1>(a.x + (size_t)b * a.H, 0, a.H >> 5, lane, xr);
-            fg.template dot<1>(xr, g);
-            fu.template dot<1>(xr, u);
+    for (int i = 0; i < R; ++i) rows[i] = i0 + i;
+    XFrag<1, 1> xr;
+    xr.template load<64>(a.x + (size_t)b * a.H, 0, a.H >> 5, lane);
+    float g[R][1], u[R][1];
+    if (slot < a.topk) {
+        const bool publish = slot + 1 == a.topk && i0 == 0;
+        uint32_t my_id;
+        float my_p;
+        route_row(a.logits + (size_t)b * a.E, a.E, publish ? a.topk : slot + 1, lane,
+                  publish && a.probs ? a.probs + (size_t)b * a.E : nullptr, my_id, my_p);
+        const uint32_t e = min((uint32_t)__builtin_amdgcn_readlane((int)my_id, (int)slot), a.X.experts - 1);
+        const uint8_t* rec = a.X.base + ((size_t)a.record_layer * a.X.experts + e) * a.X.stride;
+        ExpFrag<64, 1, R, BITS> fg, fu;
+        fg.issue(expert_mat(a.X, rec, 0, a.I, a.H), rows, lane);
+        fu.issue(expert_mat(a.X, rec, 1, a.I, a.H), rows, lane);
+        if (publish) {
+            // weights renormalised by the chosen probabilities summed in rank order
+            float topsum = 0.0f;
+            for (uint32_t r = 0; r < a.topk; ++r)
+                topsum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_p), (int)r));
+            if ((uint32_t)lane < a.topk) {
+                a.ids_out[b * a.topk + lane] = my_id;
+                a.w_out[b * a.topk + lane] = a.norm_topk ? my_p / topsum : my_p;
+            }
         }
-        if (lane == 0)
+        xr.sums();
+        fg.template dot<1>(xr, g);
+        fu.template dot<1>(xr, u);
+    } else {
+        Q4Frag<64, 1, R> fg, fu;
+        fg.issue(a.sh_gate, rows, lane);
+        fu.issue(a.sh_up, rows, lane);
+        xr.sums();
+        fg.template dot<1>(xr, g);
+        fu.template dot<1>(xr, u);
+    }
+    if (lane < R) {
+        float gv = g[0][0], uv = u[0][0];
 #pragma unroll
-            for (int i = 0; i < R; ++i) a.act[((size_t)b * slots + slot) * a.I + rows[i]] = siluf_(g[i][0]) * u[i][0];
+        for (int i = 1; i < R; ++i)
+            if (lane == i) {
+                gv = g[i][0];
+                uv = u[i][0];
+            }
+        a.act[((size_t)b * slots + slot) * a.I + i0 + lane] = siluf_(gv) * uv;
     }
 }
 
@@ -1051,14 +1063,14 @@ void launch_router(const RouterArgs& a, int nb, hipStream_t st) {
 }
 
 void launch_moe_gate_up(const MoeArgs& a, hipStream_t st) {
-    constexpr int RG = 2;
-    if (a.topk >= 64 || a.E > 512) throw std::runtime_error("routing too wide");
+    constexpr int RG = 4;
+    if (a.topk >= 64 || a.E > 512 || a.E % 8 || a.I % RG) throw std::runtime_error("routing too wide");
     const uint32_t tasks = a.nb * (a.topk + 1) * (a.I / RG);
-    const uint32_t grid = std::max<uint32_t>(1, std::min<uint32_t>((tasks + 1) / 2, 2048));
+    const uint32_t grid = (tasks + 3) / 4;  // one task per wave
     switch (a.X.bits) {
-    case 3: k_moe_gate_up<RG, 1, 3><<<grid, 256, 0, st>>>(a); break;
-    case 2: k_moe_gate_up<RG, 1, 2><<<grid, 256, 0, st>>>(a); break;
-    default: k_moe_gate_up<RG, 1, 4><<<grid, 256, 0, st>>>(a); break;
+    case 3: k_moe_gate_up<RG, 3><<<grid, 256, 0, st>>>(a); break;
+    case 2: k_moe_gate_up<RG, 2><<<grid, 256, 0, st>>>(a); break;
+    default: k_moe_gate_up<RG, 4><<<grid, 256, 0, st>>>(a); break;
     }
 }
 

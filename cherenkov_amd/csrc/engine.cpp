@@ -391,6 +391,8 @@ struct ChkEngine {
         for (uint32_t rows : {D.conv_dim, D.v_dim, D.nv, 2 * D.nh * D.hd, D.kv_row, D.idx_out, D.H, D.V, D.I})
             ensure(rows % 8 == 0 || (rows % 4 == 0 && rows != D.V), "matrix heights must be multiples of 4 (8 for vocab)");
         ensure(D.dv % 64 == 0 && D.dv <= 512, "DeltaNet value head dim must be a multiple of 64");
+        ensure(D.E % 8 == 0 && D.E <= 512 && D.topk < 64, "experts must be a multiple of 8, at most 512, top-k below 64");
+        ensure(D.I % 64 == 0, "expert width must be a multiple of 64");
         ensure(attn_shape_ok(D.nh, D.nkv, D.hd),
                "attention needs head_dim 128 or 256 and 1, 2, 4, 8 or 12 query heads per kv head");
         has_mtp = c.mtp_num_hidden_layers > 0;
@@ -436,6 +438,7 @@ struct ChkEngine {
         }
         if (has_mtp) mtp_kv = alloc_kv();
         max_chunks = (max_t + ATTN_CHUNK - 1) / ATTN_CHUNK;
+        ensure(max_chunks <= (uint32_t)MAX_ATTN_CHUNKS, "context capacity above 262144 tokens");
 
         // scratch
         const uint32_t NB = MAX_NB;
@@ -1116,7 +1119,7 @@ int chk_lm_head_argmax(const void* w, const void* s, const void* b, uint32_t out
 int chk_attn_decode_q8(const float* q, const void* k, const void* v, const void* ks, const void* vs, uint32_t T,
                        uint32_t nh, uint32_t nkv, uint32_t hd, float* out, void* stream) {
     CHK_TRY({
-        ensure(T > 0, "empty context");
+        ensure(T > 0 && T <= (uint32_t)MAX_ATTN_CHUNKS * ATTN_CHUNK, "context must be 1..=262144 tokens");
         ensure(attn_shape_ok(nh, nkv, hd), "head_dim 128 or 256, 1, 2, 4, 8 or 12 query heads per kv head");
         hipStream_t st = (hipStream_t)stream;
         AttnArgs a{};

@@ -17,6 +17,7 @@ namespace chk {
 constexpr int MAX_NB = 4;    // rows per step: one token + up to 3 drafts (gpu.rs:68)
 constexpr int MAX_SNAP = 3;  // rollback planes (gpu.rs:70)
 constexpr int ATTN_CHUNK = 64;  // tokens per attention partial
+constexpr int MAX_ATTN_CHUNKS = 4096;  // context capacity / ATTN_CHUNK (256k tokens)
 
 // Byte layout of one routed-expert record (manifest.rs:21-40 fields).
 struct RecordLayout {

@@ -123,9 +123,16 @@ CHK_DEV float wave_sum_dpp(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
-// "a ranks before b": higher probability, then lower index (cpu.rs:514).
+// Routing of one row by one wave (moe, cpu.rs:508-525): softmax of E <=
+// 512 router logits in f32 (E a multiple of 8), then the order
+// (probability desc, index asc) down to rank need - 1.  Lane l holds
+// experts 8l..8l+7 (two float4 loads), sorts them with a branch-free
+// 19-comparator network, and each round a DPP wave max pops the best
+// head; the lowest lane wins ties, i.e. the lowest index.  On return lane
+// r < need holds rank r's expert id and probability.  probs (optional)
+// receives the softmax.
 CHK_DEV void rank_swap(float& va, uint32_t& ia, float& vb, uint32_t& ib) {
-    const bool sw = vb > va || (vb == va && ib < ia);
+    const bool sw = (vb > va) | ((vb == va) & (ib < ia));
     const float tv = sw ? vb : va;
     const uint32_t ti = sw ? ib : ia;
     vb = sw ? va : vb;
@@ -134,72 +141,63 @@ CHK_DEV void rank_swap(float& va, uint32_t& ia, float& vb, uint32_t& ib) {
     ia = ti;
 }
 
-// Softmax over E <= 512 logits then top-k by (probability desc, index asc),
-// renormalised by the sum of the chosen probabilities taken in rank order
-// (cpu.rs:508-525); one wave, rows b < nb.  Lane l holds experts 8l..8l+7,
-// sorts them with a 19-comparator network, and k rounds of a DPP wave max
-// pop the best head (the lowest lane wins ties, i.e. the lowest index).
-// ids/w may be LDS or global.
-CHK_DEV void topk_wave(const float* logits, float* probs, uint32_t E, uint32_t k, int norm, uint32_t* ids,
-                       float* w, int nb, int lane, bool write_probs, uint32_t* scratch) {
-    (void)scratch;
+CHK_DEV void route_row(const float* __restrict__ l, uint32_t E, uint32_t need, int lane, float* probs,
+                       uint32_t& my_id, float& my_p) {
     constexpr int PER = 8;
-    for (int b = 0; b < nb; ++b) {
-        const float* l = logits + (size_t)b * E;
-        float v[PER];
-        uint32_t ix[PER];
-        float mx = -INFINITY;
+    const uint32_t base = (uint32_t)lane * PER;
+    const bool live = base < E;
+    const float4* lp = reinterpret_cast<const float4*>(l + (live ? base : 0));
+    const float4 l0 = lp[0], l1 = lp[1];
+    float v[PER] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+    uint32_t ix[PER];
+    float mx = -INFINITY;
 #pragma unroll
-        for (int j = 0; j < PER; ++j) {
-            ix[j] = lane * PER + j;
-            v[j] = ix[j] < E ? l[ix[j]] : -INFINITY;
-            mx = fmaxf(mx, v[j]);
-        }
-        mx = wave_max_dpp(mx);
-        float sum = 0.0f;
+    for (int j = 0; j < PER; ++j) {
+        ix[j] = base + j;
+        v[j] = live ? v[j] : -INFINITY;
+        mx = fmaxf(mx, v[j]);
+    }
+    mx = wave_max_dpp(mx);
+    float sum = 0.0f;
 #pragma unroll
-        for (int j = 0; j < PER; ++j) {
-            v[j] = ix[j] < E ? expf(v[j] - mx) : 0.0f;
-            sum += v[j];
-        }
-        sum = wave_sum_dpp(sum);
-        const float inv = 1.0f / sum;
+    for (int j = 0; j < PER; ++j) {
+        v[j] = expf(v[j] - mx);  // 0 for the -inf padding
+        sum += v[j];
+    }
+    const float inv = 1.0f / wave_sum_dpp(sum);
 #pragma unroll
-        for (int j = 0; j < PER; ++j) {
-            v[j] = ix[j] < E ? v[j] * inv : -1.0f;
-            if (ix[j] < E && write_probs) probs[(size_t)b * E + ix[j]] = v[j];
-        }
-        // Batcher-style optimal 8-input network (19 comparators)
+    for (int j = 0; j < PER; ++j) v[j] = live ? v[j] * inv : -1.0f;
+    if (probs && live) {
+        float4* pp = reinterpret_cast<float4*>(probs + base);
+        pp[0] = make_float4(v[0], v[1], v[2], v[3]);
+        pp[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
 #define CS(a, c) rank_swap(v[a], ix[a], v[c], ix[c])
-        CS(0, 2); CS(1, 3); CS(4, 6); CS(5, 7);
-        CS(0, 4); CS(1, 5); CS(2, 6); CS(3, 7);
-        CS(0, 1); CS(2, 3); CS(4, 5); CS(6, 7);
-        CS(2, 4); CS(3, 5);
-        CS(1, 4); CS(3, 6);
-        CS(1, 2); CS(3, 4); CS(5, 6);
+    CS(0, 2); CS(1, 3); CS(4, 6); CS(5, 7);
+    CS(0, 4); CS(1, 5); CS(2, 6); CS(3, 7);
+    CS(0, 1); CS(2, 3); CS(4, 5); CS(6, 7);
+    CS(2, 4); CS(3, 5);
+    CS(1, 4); CS(3, 6);
+    CS(1, 2); CS(3, 4); CS(5, 6);
 #undef CS
-        float topsum = 0.0f;
-        for (uint32_t r = 0; r < k; ++r) {
-            const float m = wave_max_dpp(v[0]);
-            const uint64_t ball = __ballot(v[0] == m);
-            const int win = (int)__builtin_ctzll(ball);
-            const uint32_t idx = (uint32_t)__builtin_amdgcn_readlane((int)ix[0], win);
-            if (lane == 0) {
-                ids[b * k + r] = idx;
-                w[b * k + r] = m;
-            }
-            topsum += m;
-            if (lane == win) {
-#pragma unroll
-                for (int j = 0; j + 1 < PER; ++j) {
-                    v[j] = v[j + 1];
-                    ix[j] = ix[j + 1];
-                }
-                v[PER - 1] = -2.0f;
-            }
+    my_id = 0;
+    my_p = 0.0f;
+    for (uint32_t r = 0; r < need; ++r) {
+        const float m = wave_max_dpp(v[0]);
+        const uint64_t ball = __ballot(v[0] == m);
+        const int win = (int)__builtin_ctzll(ball);
+        const uint32_t idx = (uint32_t)__builtin_amdgcn_readlane((int)ix[0], win);
+        if ((uint32_t)lane == r) {
+            my_id = idx;
+            my_p = m;
         }
-        if (lane == 0 && norm)
-            for (uint32_t r = 0; r < k; ++r) w[b * k + r] = w[b * k + r] / topsum;
+        const bool pop = lane == win;
+#pragma unroll
+        for (int j = 0; j + 1 < PER; ++j) {
+            v[j] = pop ? v[j + 1] : v[j];
+            ix[j] = pop ? ix[j + 1] : ix[j];
+        }
+        v[PER - 1] = pop ? -2.0f : v[PER - 1];
     }
 }
 
