@@ -634,17 +634,8 @@ struct ChkEngine {
         launch_qmv_inject(ia, nb, st);
     }
 
-    void moe(const LayerDev& L, uint32_t route_slot, const float* x, int nb, float* hyper, const float* inj,
-             float* raw_out) {
-        RouterArgs r{};
-        r.router = L.moe.router;
-        r.shared_gate = L.moe.shared_gate;
-        r.x = x;
-        r.logits = s.router_logits;
-        r.sg = s.sg;
-        r.E = D.E;
-        r.H = D.H;
-        launch_router(r, nb, st);
+    MoeArgs moe_args(const LayerDev& L, uint32_t route_slot, const float* x, int nb, float* hyper, const float* inj,
+                     float* raw_out) {
         MoeArgs m{};
         m.X = experts_dev();
         m.record_layer = L.moe.record_layer;
@@ -670,15 +661,81 @@ struct ChkEngine {
         m.I = D.I;
         m.topk = D.topk;
         m.hc = D.hc;
-        // algorithmic bytes of the gate/up kernel: each routed row-slot's
-        // gate and up matrices + the shared expert's, the router logits,
-        // the input rows and the activations written
-        const uint64_t gu_bytes = (uint64_t)nb * D.topk * 2 * expert_mat_bytes() + 2 * q4_bytes(L.moe.sh_gate) +
-                                  (uint64_t)nb * (D.E * 4 + D.H * 4 + (D.topk + 1) * D.I * 4);
+        return m;
+    }
+
+    // algorithmic bytes of the gate/up kernel: each routed row-slot's gate
+    // and up matrices + the shared expert's, the router logits, the input
+    // rows and the activations written
+    uint64_t gate_up_bytes(const LayerDev& L, int nb) const {
+        return (uint64_t)nb * D.topk * 2 * expert_mat_bytes() + 2 * q4_bytes(L.moe.sh_gate) +
+               (uint64_t)nb * (D.E * 4 + D.H * 4 + (D.topk + 1) * D.I * 4);
+    }
+
+    void moe(const LayerDev& L, uint32_t route_slot, const float* x, int nb, float* hyper, const float* inj,
+             float* raw_out) {
+        RouterArgs r{};
+        r.router = L.moe.router;
+        r.shared_gate = L.moe.shared_gate;
+        r.x = x;
+        r.logits = s.router_logits;
+        r.sg = s.sg;
+        r.E = D.E;
+        r.H = D.H;
+        launch_router(r, nb, st);
+        const MoeArgs m = moe_args(L, route_slot, x, nb, hyper, inj, raw_out);
         prof_begin(PROF_MOE);
         launch_moe_gate_up(m, st);
-        prof_end(PROF_MOE, gu_bytes);
+        prof_end(PROF_MOE, gate_up_bytes(L, nb));
         launch_moe_down(m, st);
+    }
+
+    // Time one kernel class alone: a captured graph of `reps` rounds of its
+    // launches over every decoder layer (the arguments the decode step
+    // passes at batch 1, on the current router logits and mixer output),
+    // replayed on the engine stream between two HIP events.  The kernels
+    // only write scratch (activations, routing of the profiled layers, LM
+    // head logits), never the sequence state.
+    double profile_graph(int kind, uint32_t reps, uint64_t& bytes, uint64_t& launches) {
+        ensure(kind == PROF_MOE || kind == PROF_LM_HEAD, "graph timing covers the MoE gate/up and LM head kernels");
+        ensure(reps >= 1 && reps <= 64, "reps must be 1..=64");
+        HIPCHK(hipStreamSynchronize(st));
+        bytes = 0;
+        launches = 0;
+        hipGraph_t g;
+        HIPCHK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+        for (uint32_t r = 0; r < reps; ++r) {
+            if (kind == PROF_MOE) {
+                for (uint32_t l = 0; l < c.num_hidden_layers; ++l) {
+                    const LayerDev& L = layers[l];
+                    launch_moe_gate_up(moe_args(L, l, s.mixed, 1, nullptr, nullptr, nullptr), st);
+                    bytes += gate_up_bytes(L, 1);
+                    ++launches;
+                }
+            } else {
+                launch_lm_head(lm_head, s.mixed, s.logits, s.pv, s.pi, lm_parts, s.d_out, 1, st);
+                bytes += q4_bytes(lm_head) + (uint64_t)(D.H + D.V) * 4;
+                ++launches;
+            }
+        }
+        HIPCHK(hipStreamEndCapture(st, &g));
+        hipGraphExec_t ge;
+        HIPCHK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+        hipEvent_t a, b;
+        HIPCHK(hipEventCreate(&a));
+        HIPCHK(hipEventCreate(&b));
+        HIPCHK(hipGraphLaunch(ge, st));  // warm
+        HIPCHK(hipEventRecord(a, st));
+        HIPCHK(hipGraphLaunch(ge, st));
+        HIPCHK(hipEventRecord(b, st));
+        HIPCHK(hipEventSynchronize(b));
+        float ms = 0.0f;
+        HIPCHK(hipEventElapsedTime(&ms, a, b));
+        HIPCHK(hipEventDestroy(a));
+        HIPCHK(hipEventDestroy(b));
+        HIPCHK(hipGraphExecDestroy(ge));
+        HIPCHK(hipGraphDestroy(g));
+        return ms;
     }
 
     // ---------------------------------------------------------- step
@@ -1341,6 +1398,11 @@ int chk_profile_kernel(ChkEngine* e, int kind) {
         e->prof_bytes = 0;
         e->prof_launches = 0;
     })
+}
+
+int chk_profile_graph(ChkEngine* e, int kind, uint32_t reps, double* ms_total, uint64_t* launches,
+                      uint64_t* bytes) {
+    CHK_TRY({ *ms_total = e->profile_graph(kind, reps, *bytes, *launches); })
 }
 
 int chk_profile_read(ChkEngine* e, double* ms_total, uint64_t* launches, uint64_t* bytes) {

@@ -147,6 +147,13 @@ class Engine:
         check(self.L.chk_profile_read(self._h, C.byref(ms), C.byref(n), C.byref(by)))
         return ms.value, n.value, by.value
 
+    def profile_graph(self, kind: int, reps: int) -> tuple[float, int, int]:
+        """(ms, launches, algorithmic bytes) of a graph of `reps` rounds of
+        one kernel class's per-layer launches (chk_profile_graph)."""
+        ms, n, by = C.c_double(), C.c_uint64(), C.c_uint64()
+        check(self.L.chk_profile_graph(self._h, kind, reps, C.byref(ms), C.byref(n), C.byref(by)))
+        return ms.value, n.value, by.value
+
     def time_decode(self, first_token: int, steps: int) -> tuple[float, int]:
         ms, last = C.c_float(), C.c_uint32()
         check(self.L.chk_time_decode(self._h, first_token, steps, C.byref(ms), C.byref(last)))

@@ -106,6 +106,16 @@ int chk_layer_hyper(ChkEngine* e, uint32_t layer, uint32_t r, float* host);
 int chk_profile_kernel(ChkEngine* e, int kind);
 int chk_profile_read(ChkEngine* e, double* ms_total, uint64_t* launches, uint64_t* bytes);
 
+/* Times one kernel class alone (kind 1: MoE gate/up, 3: LM head): a
+ * captured HIP graph of `reps` rounds of its batch-1 launches over every
+ * decoder layer, with the step's own arguments and current inputs,
+ * replayed once between two HIP events on the engine stream.  Returns the
+ * elapsed time, the launch count and their algorithmic HBM bytes.  Only
+ * scratch buffers are written.  Profiling support, no reference
+ * counterpart. */
+int chk_profile_graph(ChkEngine* e, int kind, uint32_t reps, double* ms_total, uint64_t* launches,
+                      uint64_t* bytes);
+
 /* Time the decode step on the engine's stream: runs `steps` step_rows(1)
  * + commit pairs, returns milliseconds per step (HIP events). */
 int chk_time_decode(ChkEngine* e, uint32_t first_token, uint32_t steps, float* ms_per_step, uint32_t* last_token);
