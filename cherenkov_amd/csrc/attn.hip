@@ -11,13 +11,15 @@
 namespace chk {
 
 // Per head: q RMSNorm + partial RoPE -> q_ready; k RMSNorm + RoPE -> q8 K
-// row; v -> q8 V row; the raw indexer key -> index cache.  One workgroup of
-// hd threads per (row, item): items [0, nh) q heads, [nh, nh + nkv) k heads,
-// [nh + nkv, nh + 2 nkv) v heads, nh + 2 nkv the index key.
+// row; v -> q8 V row; the raw indexer key -> index cache.  One CHK_WG-thread
+// workgroup per (row, item), thread d < hd owning dim d: items [0, nh) q
+// heads, [nh, nh + nkv) k heads, [nh + nkv, nh + 2 nkv) v heads,
+// nh + 2 nkv the index key.
 __global__ void __launch_bounds__(256) k_attn_prep(AttnArgs a) {
     __shared__ float red[8];
     __shared__ float sx[512];
     const uint32_t b = blockIdx.y, item = blockIdx.x, d = threadIdx.x, hd = a.hd;
+    const bool live = d < hd;
     const uint32_t pos = a.pos[b];
     const KvDev& kv = a.kv[b];
     if (item == a.nh + 2 * a.nkv) {
@@ -25,16 +27,20 @@ __global__ void __launch_bounds__(256) k_attn_prep(AttnArgs a) {
         return;
     }
     const bool is_q = item < a.nh, is_k = !is_q && item < a.nh + a.nkv;
-    float x;
-    if (is_q) x = a.q_raw[(size_t)b * a.nh * 2 * hd + item * 2 * hd + d];
-    else if (is_k) x = a.k_raw[(size_t)b * a.nkv * hd + (item - a.nh) * hd + d];
-    else x = a.v_raw[(size_t)b * a.nkv * hd + (item - a.nh - a.nkv) * hd + d];
+    float x = 0.0f;
+    if (live) {
+        if (is_q) x = a.q_raw[(size_t)b * a.nh * 2 * hd + item * 2 * hd + d];
+        else if (is_k) x = a.k_raw[(size_t)b * a.nkv * hd + (item - a.nh) * hd + d];
+        else x = a.v_raw[(size_t)b * a.nkv * hd + (item - a.nh - a.nkv) * hd + d];
+    }
     if (is_q || is_k) {
         // nn::rms_norm (nn.rs:6-15) then rope_partial (cpu.rs:1051-1063)
-        float ss = block_sum(x * x, red);
-        float inv = 1.0f / sqrtf(ss / (float)hd + a.eps);
-        x = x * inv * bf16f(is_q ? a.q_norm[d] : a.k_norm[d]);
-        sx[d] = x;
+        const float ss = block_sum(x * x, red);
+        const float inv = 1.0f / sqrtf(ss / (float)hd + a.eps);
+        if (live) {
+            x = x * inv * bf16f(is_q ? a.q_norm[d] : a.k_norm[d]);
+            sx[d] = x;
+        }
         __syncthreads();
         const uint32_t half = a.rot / 2;
         if (d < a.rot) {
@@ -47,14 +53,15 @@ __global__ void __launch_bounds__(256) k_attn_prep(AttnArgs a) {
         }
     }
     if (is_q) {
-        a.q_ready[((size_t)b * a.nh + item) * hd + d] = x;
+        if (live) a.q_ready[((size_t)b * a.nh + item) * hd + d] = x;
         return;
     }
-    // q8: 32-lane blocks are half-waves
+    // q8: 32-lane blocks are half-waves (dims past hd hold 0 and write nothing)
     float amax = group_max<32>(fabsf(x));
     float dq = amax / 127.0f;
     float qv = dq > 0.0f ? rintf(x / dq) : 0.0f;
     qv = fminf(fmaxf(qv, -127.0f), 127.0f);
+    if (!live) return;
     const uint32_t kvh = is_k ? item - a.nh : item - a.nh - a.nkv;
     const uint32_t kv_row = a.nkv * hd;
     int8_t* plane = is_k ? kv.k : kv.v;
@@ -220,16 +227,16 @@ __global__ void __launch_bounds__(256) k_attn_combine(AttnArgs a) {
     const uint32_t T = a.pos[b] + 1, nc = (T + ATTN_CHUNK - 1) / ATTN_CHUNK;
     const float* part = a.part + ((size_t)b * a.nh + h) * a.max_chunks * (hd + 2);
     float m = -INFINITY;
-    for (uint32_t c = t; c < nc; c += blockDim.x) m = fmaxf(m, part[(size_t)c * (hd + 2)]);
+    for (uint32_t c = t; c < nc; c += CHK_WG) m = fmaxf(m, part[(size_t)c * (hd + 2)]);
     const float M = block_max(m, red);
     float l = 0.0f;
-    for (uint32_t c = t; c < nc; c += blockDim.x) {
+    for (uint32_t c = t; c < nc; c += CHK_WG) {
         const float w = expf(part[(size_t)c * (hd + 2)] - M);
         sw[c] = w;
         l += part[(size_t)c * (hd + 2) + 1] * w;
     }
     const float L = block_sum(l, red);  // its barriers also publish sw
-    for (uint32_t d = t; d < hd; d += blockDim.x) {
+    for (uint32_t d = t; d < hd; d += CHK_WG) {
         const float* pd = part + 2 + d;
         float o = 0.0f;
         uint32_t c = 0;
@@ -247,13 +254,13 @@ __global__ void __launch_bounds__(256) k_attn_combine(AttnArgs a) {
 }
 
 __global__ void __launch_bounds__(256) k_copy_f32(float* __restrict__ dst, const float* __restrict__ src, uint64_t n) {
-    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = src[i];
+    uint64_t stride = (uint64_t)gridDim.x * CHK_WG;
+    for (uint64_t i = (uint64_t)blockIdx.x * CHK_WG + threadIdx.x; i < n; i += stride) dst[i] = src[i];
 }
 
 __global__ void __launch_bounds__(256) k_zero_f32(float* __restrict__ dst, uint64_t n) {
-    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = 0.0f;
+    uint64_t stride = (uint64_t)gridDim.x * CHK_WG;
+    for (uint64_t i = (uint64_t)blockIdx.x * CHK_WG + threadIdx.x; i < n; i += stride) dst[i] = 0.0f;
 }
 
 // Positions come from device memory and the chunk grid covers the whole
@@ -285,7 +292,7 @@ void launch_attn_core(const AttnArgs& a, int nb, hipStream_t st) {
 }
 
 void launch_attn(const AttnArgs& a, int nb, hipStream_t st) {
-    k_attn_prep<<<dim3(a.nh + 2 * a.nkv + 1, nb), a.hd, 0, st>>>(a);
+    k_attn_prep<<<dim3(a.nh + 2 * a.nkv + 1, nb), CHK_WG, 0, st>>>(a);
     launch_attn_core(a, nb, st);
 }
 

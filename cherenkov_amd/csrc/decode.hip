@@ -39,6 +39,7 @@ template <int NB, int CPL>
 struct XFrag {
     float v[NB][CPL][32];
     float s[NB][CPL];
+    h2 hi[NB][CPL][16], lo[NB][CPL][16];  // the fp16 dot's pairs (x_pairs)
 
     template <int LPR>
     CHK_DEV void load(const float* __restrict__ x, uint32_t xs, uint32_t nch, int lir) {
@@ -55,6 +56,7 @@ struct XFrag {
                     for (int j = 0; j < 32; ++j) v[b][c][j] = 0.0f;
         }
     }
+    // chunk sums and fp16 pairs of the (possibly rescaled) loaded inputs
     CHK_DEV void sums() {
 #pragma unroll
         for (int b = 0; b < NB; ++b)
@@ -64,6 +66,7 @@ struct XFrag {
 #pragma unroll
                 for (int j = 0; j < 32; ++j) t += v[b][c][j];
                 s[b][c] = t;
+                x_pairs(v[b][c], hi[b][c], lo[b][c]);
             }
     }
 };
@@ -103,6 +106,7 @@ struct Q4Frag {
 
     template <int NB>
     CHK_DEV void dot(const XFrag<NB, CPL>& xf, float (&acc)[R][NB]) const {
+        const Q4Consts k;
 #pragma unroll
         for (int i = 0; i < R; ++i)
 #pragma unroll
@@ -110,7 +114,8 @@ struct Q4Frag {
                 float a = 0.0f;
 #pragma unroll
                 for (int c = 0; c < CPL; ++c) {
-                    const float p = q4_chunk(wq[i][c], xf.v[b][c], xf.s[b][c], bf16f(s16[i][c]), bf16f(b16[i][c]));
+                    const float p = q4_chunk_h(wq[i][c], xf.hi[b][c], xf.lo[b][c], xf.s[b][c], bf16f(s16[i][c]),
+                                               bf16f(b16[i][c]), k);
                     a += ok[c] ? p : 0.0f;
                 }
                 acc[i][b] = group_sum<LPR>(a);
@@ -235,11 +240,14 @@ CHK_DEV void exp_block(const ExpMat& m, const uint32_t (&rows)[R], const XFrag<N
     f.template dot<NB>(xr, acc);
 }
 
-CHK_DEV uint32_t wave_id() { return threadIdx.x >> 6; }
+// The wave index, marked wave-uniform so that everything derived from it
+// (task ids, segment descriptors) stays in SGPRs and kernel arguments are
+// read with scalar loads.
+CHK_DEV uint32_t wave_id() { return (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 // Task order across the grid: consecutive tasks go to different workgroups
 // (and so CUs) before a workgroup takes a second one.
-CHK_DEV uint32_t global_wave() { return (threadIdx.x >> 6) * gridDim.x + blockIdx.x; }
-CHK_DEV uint32_t total_waves() { return gridDim.x * (blockDim.x >> 6); }
+CHK_DEV uint32_t global_wave() { return wave_id() * gridDim.x + blockIdx.x; }
+CHK_DEV uint32_t total_waves() { return gridDim.x * (CHK_WG >> 6); }
 
 // ------------------------------------------------------------------ embed
 // embed.dequant_row + replicate into hc streams (cpu.rs:399-407).  Uses
@@ -247,7 +255,7 @@ CHK_DEV uint32_t total_waves() { return gridDim.x * (blockDim.x >> 6); }
 __global__ void __launch_bounds__(256) k_embed(const StepIn* __restrict__ in, uint32_t* __restrict__ tok_out,
                                                uint32_t* __restrict__ rowpos, Q4Mat emb, float* __restrict__ hyper,
                                                uint32_t H, uint32_t hc) {
-    uint32_t b = blockIdx.y, i = blockIdx.x * blockDim.x + threadIdx.x;
+    uint32_t b = blockIdx.y, i = blockIdx.x * CHK_WG + threadIdx.x;
     const uint32_t tok = in->tokens[b];
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         tok_out[b] = tok;
@@ -265,77 +273,90 @@ __global__ void __launch_bounds__(256) k_embed(const StepIn* __restrict__ in, ui
 // ---------------------------------------------------------- hc read (down)
 // gated_residual first half (cpu.rs:461-475, 493-500): normed = grouped
 // RMSNorm(hyper) * w, d = silu(down(normed) / hc), inj = 2 sigmoid(inject(normed) / hc).
-// One workgroup per row of [down; inject]; wave g takes hc stream g, so its
-// RMS is a wave reduction, and the per-stream partial dots meet in LDS.
+// A workgroup takes HR consecutive rows of [down; inject]; wave g takes hc
+// stream g, so its RMS is a wave reduction, its normalised inputs are
+// prepared once for all HR rows, and the per-stream partial dots meet in LDS.
+constexpr int HR = 4;
+
 template <int CPL, int NB>
-__global__ void __launch_bounds__(512) k_hc_down(HcDev w, const float* __restrict__ hyper, float* __restrict__ d,
+__global__ void __launch_bounds__(256) k_hc_down(HcDev w, const float* __restrict__ hyper, float* __restrict__ d,
                                                  float* __restrict__ inj, float* __restrict__ inv_out, uint32_t H,
                                                  uint32_t hc, float eps) {
-    __shared__ float red[8][NB];
+    __shared__ float red[4][HR][NB];
     const int lane = threadIdx.x & 63, g = (int)wave_id();
-    const uint32_t row = blockIdx.x;
-    const Q4Mat& m = row < w.down.out ? w.down : w.inject;
-    const uint32_t r = row < w.down.out ? row : row - w.down.out;
+    const uint32_t total = w.down.out + (w.has_inject ? w.inject.out : 0u);
+    const uint32_t r0 = blockIdx.x * HR;
     const uint32_t hh = H * hc, nch = H >> 5;  // chunks per stream
-    const uint32_t* wr = m.w + (size_t)r * (hh >> 3) + (size_t)g * (H >> 3);
-    const uint16_t* sr = m.s + (size_t)r * (hh >> 6) + (size_t)g * (H >> 6);
-    const uint16_t* br = m.b + (size_t)r * (hh >> 6) + (size_t)g * (H >> 6);
-    uint4 wq[CPL];
-    float sc[CPL], bi[CPL];
+    // issue every weight load of the HR rows first
+    uint4 wq[HR][CPL];
+    uint16_t s16[HR][CPL], b16[HR][CPL];
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-        const uint32_t ch = lane + 64 * c;
-        if (ch < nch) {
-            wq[c] = ldw4(wr + ch * 4);
-            sc[c] = bf16f(sr[ch >> 1]);
-            bi[c] = bf16f(br[ch >> 1]);
-        } else {
-            wq[c] = make_uint4(0, 0, 0, 0);
-            sc[c] = bi[c] = 0.0f;
-        }
-    }
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-        float part = 0.0f, sq = 0.0f;
+    for (int i = 0; i < HR; ++i) {
+        const uint32_t row = min(r0 + i, total - 1);
+        const Q4Mat& m = row < w.down.out ? w.down : w.inject;
+        const uint32_t r = row < w.down.out ? row : row - w.down.out;
+        const uint32_t* wr = m.w + (size_t)r * (hh >> 3) + (size_t)g * (H >> 3);
+        const uint16_t* sr = m.s + (size_t)r * (hh >> 6) + (size_t)g * (H >> 6);
+        const uint16_t* br = m.b + (size_t)r * (hh >> 6) + (size_t)g * (H >> 6);
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
-            const uint32_t ch = lane + 64 * c;
-            if (ch < nch) {
-                float xv[32];
-                ldx32(hyper + (size_t)b * hh + (size_t)g * H + ch * 32, xv);
-                const uint4* np = reinterpret_cast<const uint4*>(w.norm + (size_t)g * H + ch * 32);
-                float xsum = 0.0f;
+            const uint32_t ch = min(lane + 64 * c, nch - 1);
+            wq[i][c] = ldw4(wr + ch * 4);
+            s16[i][c] = sr[ch >> 1];
+            b16[i][c] = br[ch >> 1];
+        }
+    }
+    const Q4Consts k;
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const uint4 nv = np[q];
-                    const uint32_t nn[4] = {nv.x, nv.y, nv.z, nv.w};
+    for (int b = 0; b < NB; ++b) {
+        float sq = 0.0f, xs[CPL];
+        h2 hi[CPL][16], lo[CPL][16];
 #pragma unroll
-                    for (int h = 0; h < 8; ++h) {
-                        const int j = q * 8 + h;
-                        const float wn = __uint_as_float(h & 1 ? nn[h >> 1] & 0xffff0000u : nn[h >> 1] << 16);
-                        sq += xv[j] * xv[j];
-                        xv[j] *= wn;
-                        xsum += xv[j];
-                    }
+        for (int c = 0; c < CPL; ++c) {
+            const uint32_t ch = lane + 64 * c, cc = min(ch, nch - 1);
+            float xv[32];
+            ldx32(hyper + (size_t)b * hh + (size_t)g * H + cc * 32, xv);
+            const uint4* np = reinterpret_cast<const uint4*>(w.norm + (size_t)g * H + cc * 32);
+            float t = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint4 nv = np[q];
+                const uint32_t nn[4] = {nv.x, nv.y, nv.z, nv.w};
+#pragma unroll
+                for (int h = 0; h < 8; ++h) {
+                    const int j = q * 8 + h;
+                    const float wn = __uint_as_float(h & 1 ? nn[h >> 1] & 0xffff0000u : nn[h >> 1] << 16);
+                    const float xj = ch < nch ? xv[j] : 0.0f;
+                    sq += xj * xj;
+                    xv[j] = xj * wn;
+                    t += xv[j];
                 }
-                part += q4_chunk(wq[c], xv, xsum, sc[c], bi[c]);
             }
+            xs[c] = t;
+            x_pairs(xv, hi[c], lo[c]);
         }
         const float inv = 1.0f / sqrtf(wave_sum(sq) / (float)H + eps);
-        part = wave_sum(part) * inv;
-        if (lane == 0) {
-            red[g][b] = part;
-            if (row == 0) inv_out[b * hc + g] = inv;
+        if (blockIdx.x == 0 && lane == 0) inv_out[b * hc + g] = inv;
+#pragma unroll
+        for (int i = 0; i < HR; ++i) {
+            float part = 0.0f;
+#pragma unroll
+            for (int c = 0; c < CPL; ++c)
+                part += q4_chunk_h(wq[i][c], hi[c], lo[c], xs[c], bf16f(s16[i][c]), bf16f(b16[i][c]), k);
+            part = wave_sum(part) * inv;
+            if (lane == 0) red[g][i][b] = part;
         }
     }
     __syncthreads();
-    if (threadIdx.x < NB) {
-        const int b = threadIdx.x;
-        float tot = 0.0f;
-        for (uint32_t gg = 0; gg < hc; ++gg) tot += red[gg][b];
-        const float v = tot / (float)hc;
-        if (row < w.down.out) d[(size_t)b * w.down.out + r] = siluf_(v);
-        else inj[b * hc + r] = 2.0f * sigmoidf_(v);
+    if (threadIdx.x < HR * NB) {
+        const uint32_t i = threadIdx.x / NB, b = threadIdx.x % NB, row = r0 + i;
+        if (row < total) {
+            float tot = 0.0f;
+            for (uint32_t gg = 0; gg < hc; ++gg) tot += red[gg][i][b];
+            const float v = tot / (float)hc;
+            if (row < w.down.out) d[(size_t)b * w.down.out + row] = siluf_(v);
+            else inj[b * hc + (row - w.down.out)] = 2.0f * sigmoidf_(v);
+        }
     }
 }
 
@@ -743,41 +764,62 @@ __global__ void __launch_bounds__(256) k_router(RouterArgs a) {
 // row's experts (route_row) down to its slot while its x loads are in
 // flight; the wave of slot k-1, i0 = 0 ranks all k and publishes the
 // routing (ids, renormalised weights) for the down kernel.
+// The routing of row b for the down kernel: ids in rank order and weights
+// renormalised by the chosen probabilities summed in rank order
+// (cpu.rs:516-525); lane r holds rank r (route_row).
+CHK_DEV void publish_routing(const MoeArgs& a, uint32_t b, int lane, uint32_t my_id, float my_p) {
+    float topsum = 0.0f;
+    for (uint32_t r = 0; r < a.topk; ++r) topsum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_p), (int)r));
+    if ((uint32_t)lane < a.topk) {
+        a.ids_out[b * a.topk + lane] = my_id;
+        a.w_out[b * a.topk + lane] = a.norm_topk ? my_p / topsum : my_p;
+    }
+}
+
 template <int R, int BITS>
 __global__ void __launch_bounds__(256) k_moe_gate_up(MoeArgs a) {
     const int lane = threadIdx.x & 63;
     const uint32_t slots = a.topk + 1, blocks = a.I / R;
     const uint32_t tasks = a.nb * slots * blocks;
-    const uint32_t t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const uint32_t t = blockIdx.x * (CHK_WG >> 6) + wave_id();
     if (t >= tasks) return;
     const uint32_t b = t / (slots * blocks), slot = (t / blocks) % slots, i0 = (t % blocks) * R;
     uint32_t rows[R];
 #pragma unroll
     for (int i = 0; i < R; ++i) rows[i] = i0 + i;
+    // x loads first; nothing waits on them until the weights are in flight
     XFrag<1, 1> xr;
     xr.template load<64>(a.x + (size_t)b * a.H, 0, a.H >> 5, lane);
-    float g[R][1], u[R][1];
-    if (slot < a.topk) {
-        const bool publish = slot + 1 == a.topk && i0 == 0;
-        uint32_t my_id;
-        float my_p;
+    const bool routed = slot < a.topk;
+    const bool publish = slot + 1 == a.topk && i0 == 0;
+    uint32_t my_id = 0;
+    float my_p = 0.0f;
+    if (routed)
         route_row(a.logits + (size_t)b * a.E, a.E, publish ? a.topk : slot + 1, lane,
                   publish && a.probs ? a.probs + (size_t)b * a.E : nullptr, my_id, my_p);
-        const uint32_t e = min((uint32_t)__builtin_amdgcn_readlane((int)my_id, (int)slot), a.X.experts - 1);
-        const uint8_t* rec = a.X.base + ((size_t)a.record_layer * a.X.experts + e) * a.X.stride;
+    const uint32_t e = routed ? min((uint32_t)__builtin_amdgcn_readlane((int)my_id, (int)slot), a.X.experts - 1) : 0u;
+    const uint8_t* rec = a.X.base + ((size_t)a.record_layer * a.X.experts + e) * a.X.stride;
+    float g[R][1], u[R][1];
+    if (BITS == 4) {
+        // one straight path for routed and shared rows: only the matrices differ
+        Q4Mat mg = a.sh_gate, mu = a.sh_up;
+        if (routed) {
+            const ExpMat eg = expert_mat(a.X, rec, 0, a.I, a.H), eu = expert_mat(a.X, rec, 1, a.I, a.H);
+            mg = Q4Mat{(const uint32_t*)eg.w, eg.s, eg.b, a.I, a.H};
+            mu = Q4Mat{(const uint32_t*)eu.w, eu.s, eu.b, a.I, a.H};
+        }
+        Q4Frag<64, 1, R> fg, fu;
+        fg.issue(mg, rows, lane);
+        fu.issue(mu, rows, lane);
+        if (publish) publish_routing(a, b, lane, my_id, my_p);
+        xr.sums();
+        fg.template dot<1>(xr, g);
+        fu.template dot<1>(xr, u);
+    } else if (routed) {
         ExpFrag<64, 1, R, BITS> fg, fu;
         fg.issue(expert_mat(a.X, rec, 0, a.I, a.H), rows, lane);
         fu.issue(expert_mat(a.X, rec, 1, a.I, a.H), rows, lane);
-        if (publish) {
-            // weights renormalised by the chosen probabilities summed in rank order
-            float topsum = 0.0f;
-            for (uint32_t r = 0; r < a.topk; ++r)
-                topsum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_p), (int)r));
-            if ((uint32_t)lane < a.topk) {
-                a.ids_out[b * a.topk + lane] = my_id;
-                a.w_out[b * a.topk + lane] = a.norm_topk ? my_p / topsum : my_p;
-            }
-        }
+        if (publish) publish_routing(a, b, lane, my_id, my_p);
         xr.sums();
         fg.template dot<1>(xr, g);
         fu.template dot<1>(xr, u);
@@ -919,7 +961,7 @@ __global__ void __launch_bounds__(256) k_lm_head(Q4Mat m, const float* __restric
         const int b = threadIdx.x;
         float v = sv[b][0];
         uint32_t i = si[b][0];
-        for (int k = 1; k < (int)(blockDim.x >> 6); ++k)
+        for (int k = 1; k < (int)(CHK_WG >> 6); ++k)
             if (sv[b][k] > v || (sv[b][k] == v && si[b][k] < i)) { v = sv[b][k]; i = si[b][k]; }
         pv[(size_t)b * gridDim.x + blockIdx.x] = v;
         pi[(size_t)b * gridDim.x + blockIdx.x] = i;
@@ -933,7 +975,7 @@ __global__ void __launch_bounds__(256) k_argmax_final(const float* __restrict__ 
     const uint32_t b = blockIdx.x;
     float v = -INFINITY;
     uint32_t i = 0xffffffffu;
-    for (uint32_t k = threadIdx.x; k < n; k += blockDim.x) {
+    for (uint32_t k = threadIdx.x; k < n; k += CHK_WG) {
         const float x = pv[(size_t)b * n + k];
         const uint32_t xi = pi[(size_t)b * n + k];
         if (x > v || (x == v && xi < i)) { v = x; i = xi; }
@@ -941,7 +983,7 @@ __global__ void __launch_bounds__(256) k_argmax_final(const float* __restrict__ 
     sv[threadIdx.x] = v;
     si[threadIdx.x] = i;
     __syncthreads();
-    for (uint32_t s = blockDim.x / 2; s > 0; s >>= 1) {
+    for (uint32_t s = CHK_WG / 2; s > 0; s >>= 1) {
         if (threadIdx.x < s) {
             const float x = sv[threadIdx.x + s];
             const uint32_t xi = si[threadIdx.x + s];
@@ -980,10 +1022,12 @@ void launch_hc_down(const HcDev& w, const float* hyper, float* d, float* inj, fl
                     float eps, int nb, hipStream_t st) {
     const uint32_t rows = w.down.out + (w.has_inject ? w.inject.out : 0);
     const uint32_t cpl = (H / 32 + 63) / 64;
+    if (hc > 4 || cpl > 2) throw std::runtime_error("hyper-connection read supports hc <= 4 and hidden <= 4096");
+    const uint32_t grid = (rows + HR - 1) / HR;
     if (cpl <= 1) {
-        CHK_NB_SWITCH(nb, (k_hc_down<1, NB><<<rows, 64 * hc, 0, st>>>(w, hyper, d, inj, inv, H, hc, eps)))
+        CHK_NB_SWITCH(nb, (k_hc_down<1, NB><<<grid, 64 * hc, 0, st>>>(w, hyper, d, inj, inv, H, hc, eps)))
     } else {
-        CHK_NB_SWITCH(nb, (k_hc_down<2, NB><<<rows, 64 * hc, 0, st>>>(w, hyper, d, inj, inv, H, hc, eps)))
+        CHK_NB_SWITCH(nb, (k_hc_down<2, NB><<<grid, 64 * hc, 0, st>>>(w, hyper, d, inj, inv, H, hc, eps)))
     }
 }
 

@@ -123,6 +123,27 @@ CHK_DEV float wave_sum_dpp(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// Wave64 max of ints through DPP (the lanes outside a row mask keep their
+// own value); valid in every lane.
+CHK_DEV int wave_max_i32(int v) {
+    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0xb1, 0xf, 0xf, false));   // quad_perm [1,0,3,2]
+    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x4e, 0xf, 0xf, false));   // quad_perm [2,3,0,1]
+    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x124, 0xf, 0xf, false));  // row_ror:4
+    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x128, 0xf, 0xf, false));  // row_ror:8
+    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x142, 0xa, 0xf, false));  // row_bcast:15 into rows 1, 3
+    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x143, 0xc, 0xf, false));  // row_bcast:31 into rows 2, 3
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
+// take in the lanes of `mask`, keep elsewhere: a single v_cndmask_b32 (as
+// an explicit instruction, so the compiler cannot turn a run of them over
+// neighbouring array slots into index-select chains)
+CHK_DEV uint32_t lane_pick(uint32_t keep, uint32_t take, uint64_t mask) {
+    uint32_t r;
+    asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(keep), "v"(take), "s"(mask));
+    return r;
+}
+
 // Routing of one row by one wave (moe, cpu.rs:508-525): softmax of E <=
 // 512 router logits in f32 (E a multiple of 8), then the order
 // (probability desc, index asc) down to rank need - 1.  Lane l holds
@@ -180,24 +201,31 @@ CHK_DEV void route_row(const float* __restrict__ l, uint32_t E, uint32_t need, i
     CS(1, 4); CS(3, 6);
     CS(1, 2); CS(3, 4); CS(5, 6);
 #undef CS
+    // pops on int keys: probabilities are >= 0, so their bit patterns order
+    // like the floats; the padding (< 0) never wins while real entries remain
+    int key[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) key[j] = __float_as_int(v[j]);
     my_id = 0;
     my_p = 0.0f;
     for (uint32_t r = 0; r < need; ++r) {
-        const float m = wave_max_dpp(v[0]);
-        const uint64_t ball = __ballot(v[0] == m);
+        const int m = wave_max_i32(key[0]);
+        const uint64_t ball = __ballot(key[0] == m);
         const int win = (int)__builtin_ctzll(ball);
         const uint32_t idx = (uint32_t)__builtin_amdgcn_readlane((int)ix[0], win);
         if ((uint32_t)lane == r) {
             my_id = idx;
-            my_p = m;
+            my_p = __int_as_float(m);
         }
-        const bool pop = lane == win;
+        // the winning lane drops its head: one v_cndmask per slot on the
+        // winner's lane mask
+        const uint64_t pm = 1ull << win;
 #pragma unroll
         for (int j = 0; j + 1 < PER; ++j) {
-            v[j] = pop ? v[j + 1] : v[j];
-            ix[j] = pop ? ix[j + 1] : ix[j];
+            key[j] = (int)lane_pick((uint32_t)key[j], (uint32_t)key[j + 1], pm);
+            ix[j] = lane_pick(ix[j], ix[j + 1], pm);
         }
-        v[PER - 1] = pop ? -2.0f : v[PER - 1];
+        key[PER - 1] = (int)lane_pick((uint32_t)key[PER - 1], 0xffffffffu, pm);
     }
 }
 

@@ -16,7 +16,7 @@ __global__ void __launch_bounds__(256) k_mtp_prelude(const uint32_t* __restrict_
     float ss = 0.0f;
     if (item == 0) {
         const uint32_t tok = tokens[b];
-        for (uint32_t i = threadIdx.x; i < H; i += blockDim.x) {
+        for (uint32_t i = threadIdx.x; i < H; i += CHK_WG) {
             uint32_t word = emb.w[(size_t)tok * (H / 8) + i / 8];
             float s = bf16f(emb.s[(size_t)tok * (H / 64) + i / 64]), bb = bf16f(emb.b[(size_t)tok * (H / 64) + i / 64]);
             float e = __fadd_rn(__fmul_rn(s, (float)((word >> (4 * (i % 8))) & 15u)), bb);
@@ -25,22 +25,22 @@ __global__ void __launch_bounds__(256) k_mtp_prelude(const uint32_t* __restrict_
         }
         float tot = block_sum(ss, red);
         float inv = 1.0f / sqrtf(tot / (float)H + eps);
-        for (uint32_t i = threadIdx.x; i < H; i += blockDim.x)
+        for (uint32_t i = threadIdx.x; i < H; i += CHK_WG)
             en[(size_t)b * H + i] = en[(size_t)b * H + i] * inv * (1.0f + bf16f(enorm[i]));
     } else {
         const uint32_t g = item - 1;
         const float* x = src + (size_t)b * H * hc + (size_t)g * H;
-        for (uint32_t i = threadIdx.x; i < H; i += blockDim.x) ss += x[i] * x[i];
+        for (uint32_t i = threadIdx.x; i < H; i += CHK_WG) ss += x[i] * x[i];
         float tot = block_sum(ss, red);
         float inv = 1.0f / sqrtf(tot / (float)H + eps);
         float* o = hn + ((size_t)b * hc + g) * H;
-        for (uint32_t i = threadIdx.x; i < H; i += blockDim.x) o[i] = x[i] * inv * (1.0f + bf16f(hnorm[(size_t)g * H + i]));
+        for (uint32_t i = threadIdx.x; i < H; i += CHK_WG) o[i] = x[i] * inv * (1.0f + bf16f(hnorm[(size_t)g * H + i]));
     }
 }
 
 __global__ void __launch_bounds__(256) k_mtp_fold(const float* __restrict__ fe, const float* __restrict__ fh, float* __restrict__ hyper,
                            uint32_t H, uint32_t hc) {
-    const uint32_t b = blockIdx.y, i = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t b = blockIdx.y, i = blockIdx.x * CHK_WG + threadIdx.x;
     if (i >= H) return;
     for (uint32_t g = 0; g < hc; ++g)
         hyper[(size_t)b * H * hc + g * H + i] = fe[(size_t)b * H + i] + fh[((size_t)b * hc + g) * H + i];
@@ -49,7 +49,7 @@ __global__ void __launch_bounds__(256) k_mtp_fold(const float* __restrict__ fe, 
 // q8 quantisation of whole cache rows (the kv_append_q8 rule).
 __global__ void __launch_bounds__(256) k_kv_fill(const float* __restrict__ k, const float* __restrict__ v, KvDev kv, uint64_t n,
                           uint32_t kv_row) {
-    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t i = (uint64_t)blockIdx.x * CHK_WG + threadIdx.x;
     const int side = blockIdx.y;
     const float x = i < n ? (side == 0 ? k[i] : v[i]) : 0.0f;
     float amax = group_max<32>(fabsf(x));
