@@ -40,6 +40,19 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+def measured_traffic(kind: int):
+    """HBM bytes per launch of the dominant kernel from the committed
+    rocprofv3 FETCH_SIZE/WRITE_SIZE runs (profiles/k_moe_gate_up_traffic.md,
+    copy-calibrated); None when absent or for another kernel."""
+    path = ROOT / "profiles" / "k_moe_gate_up_traffic.md"
+    if kind != 1 or not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":")[1]))
+    return None
+
+
 def cpu_baseline(cfg, tokens: list[int], timeout_s: float = 40.0) -> dict:
     """The oracle (C++ restatement of cpu.rs forward_token, OpenMP over
     output rows) on this host: a first pass over `tokens` materialises the
@@ -80,6 +93,8 @@ def main() -> int:
     ap.add_argument("--experts", type=int, default=4)
     ap.add_argument("--prompt", type=int, default=PROMPT)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run the library's copy kernel over 256 MiB (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(
@@ -91,6 +106,18 @@ def main() -> int:
 
     import numpy as np
     import torch
+
+    if args.copy_calibration:
+        from cherenkov_amd.abi import check, lib
+
+        n = 64 << 20  # 64 Mi floats = 256 MiB read + 256 MiB written per launch
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            check(lib().chk_copy_f32(dst.data_ptr(), src.data_ptr(), n, None))
+        print(json.dumps({"copy_kernel": "k_copy_f32", "bytes_read": 4 * n, "bytes_written": 4 * n, "launches": 3}))
+        return 0
 
     from cherenkov_amd import presets
     from cherenkov_amd.engine import Engine
@@ -169,7 +196,9 @@ def main() -> int:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(prof_kind),
+            "traffic_source": "rocprofv3 FETCH_SIZE + WRITE_SIZE per decode launch, copy-calibrated "
+            "(profiles/k_moe_gate_up_traffic.md)",
             "bytes_per_launch": int(bytes_per_launch),
             "avg_launch_us": round(avg_launch_ms * 1e3, 3),
             "launches": prof_n,

@@ -129,6 +129,7 @@ SIGNATURES = [
     ("chk_layer_hyper", i32, [P, u32, u32, P]),
     ("chk_profile_kernel", i32, [P, i32]),
     ("chk_profile_read", i32, [P, C.POINTER(f64), C.POINTER(u64), C.POINTER(u64)]),
+    ("chk_copy_f32", i32, [P, P, u64, P]),
     ("chk_profile_graph", i32, [P, i32, u32, C.POINTER(C.c_double), C.POINTER(u64), C.POINTER(u64)]),
     ("chk_time_decode", i32, [P, u32, u32, C.POINTER(f32), C.POINTER(u32)]),
     # runner (decode loop)

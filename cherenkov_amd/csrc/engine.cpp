@@ -335,7 +335,7 @@ struct ChkEngine {
         ensure(o.drafts <= 3, "drafts must be 0..=3");
         ensure(o.max_t >= 1, "max_t must be positive");
         ensure(c.full_attention_interval >= 1 && c.num_hidden_layers >= 1, "layer pattern");
-        ensure(c.hc_count >= 2 && c.hc_count <= 8, "hc_count must be 2..=8");
+        ensure(c.hc_count >= 2 && c.hc_count <= 4, "hc_count must be 2..=4 (one hyper-connection stream per wave)");
         ensure(c.hidden_size % 256 == 0, "hidden % 256 == 0 (gpu/load.rs:25-28)");
         ensure(c.hc_lowrank % 32 == 0 && c.hc_lowrank <= 2048, "hc_lowrank must be a multiple of 32");
         ensure(c.moe_intermediate_size % 64 == 0, "expert width must be a multiple of 64 (gpu/load.rs:37-40)");
@@ -1397,6 +1397,15 @@ int chk_profile_kernel(ChkEngine* e, int kind) {
         e->prof_ms = 0.0;
         e->prof_bytes = 0;
         e->prof_launches = 0;
+    })
+}
+
+int chk_copy_f32(float* dst, const float* src, uint64_t n, void* stream) {
+    CHK_TRY({
+        hipStream_t st = (hipStream_t)stream;
+        launch_copy_f32(dst, src, n, st);
+        HIPCHK(hipStreamSynchronize(st));
+        HIPCHK(hipGetLastError());
     })
 }
 

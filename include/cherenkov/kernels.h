@@ -106,6 +106,12 @@ int chk_layer_hyper(ChkEngine* e, uint32_t layer, uint32_t r, float* host);
 int chk_profile_kernel(ChkEngine* e, int kind);
 int chk_profile_read(ChkEngine* e, double* ms_total, uint64_t* launches, uint64_t* bytes);
 
+/* dst[i] = src[i], i < n (f32 device buffers): the library's plain copy
+ * kernel, used to calibrate HBM byte counters (rocprofv3 FETCH_SIZE /
+ * WRITE_SIZE) against a transfer of known size.  Profiling support, no
+ * reference counterpart. */
+int chk_copy_f32(float* dst, const float* src, uint64_t n, void* stream);
+
 /* Times one kernel class alone (kind 1: MoE gate/up, 3: LM head): a
  * captured HIP graph of `reps` rounds of its batch-1 launches over every
  * decoder layer, with the step's own arguments and current inputs,
