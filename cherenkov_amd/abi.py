@@ -113,6 +113,7 @@ SIGNATURES = [
     ("chk_last_routes", i32, [P, u32, u32, C.POINTER(u32), C.POINTER(f32)]),
     # kernels.h
     ("chk_q4_matvec", i32, [P, P, P, u32, u32, P, P, u32, P]),
+    ("chk_q4_gemm", i32, [P, P, P, u32, u32, P, u32, P, P]),
     ("chk_lm_head_argmax", i32, [P, P, P, u32, u32, P, u32, P, P, P]),
     ("chk_attn_decode_q8", i32, [P, P, P, P, P, u32, u32, u32, u32, P, P]),
     ("chk_moe_block", i32, [P, u32, P, u32, P, P, P, P]),

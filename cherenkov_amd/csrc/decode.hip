@@ -240,14 +240,6 @@ CHK_DEV void exp_block(const ExpMat& m, const uint32_t (&rows)[R], const XFrag<N
     f.template dot<NB>(xr, acc);
 }
 
-// The wave index, marked wave-uniform so that everything derived from it
-// (task ids, segment descriptors) stays in SGPRs and kernel arguments are
-// read with scalar loads.
-CHK_DEV uint32_t wave_id() { return (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
-// Task order across the grid: consecutive tasks go to different workgroups
-// (and so CUs) before a workgroup takes a second one.
-CHK_DEV uint32_t global_wave() { return wave_id() * gridDim.x + blockIdx.x; }
-CHK_DEV uint32_t total_waves() { return gridDim.x * (CHK_WG >> 6); }
 
 // ------------------------------------------------------------------ embed
 // embed.dequant_row + replicate into hc streams (cpu.rs:399-407).  Uses

@@ -57,6 +57,15 @@ CHK_DEV float wave_max(float v) { return group_max<64>(v); }
 // of every kernel's first weight load.
 constexpr uint32_t CHK_WG = 256;
 
+// The wave index, marked wave-uniform so that everything derived from it
+// (task ids, segment descriptors) stays in SGPRs and kernel arguments are
+// read with scalar loads.
+CHK_DEV uint32_t wave_id() { return (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+// Task order across the grid: consecutive tasks go to different workgroups
+// (and so CUs) before a workgroup takes a second one.
+CHK_DEV uint32_t global_wave() { return wave_id() * gridDim.x + blockIdx.x; }
+CHK_DEV uint32_t total_waves() { return gridDim.x * (CHK_WG >> 6); }
+
 // Block-wide sum of one value per thread over a CHK_WG-thread workgroup;
 // `red` is LDS of >= CHK_WG / 64 floats.
 CHK_DEV float block_sum(float v, float* red) {

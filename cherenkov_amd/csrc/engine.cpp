@@ -1400,6 +1400,27 @@ int chk_profile_kernel(ChkEngine* e, int kind) {
     })
 }
 
+int chk_q4_gemm(const void* w, const void* s, const void* b, uint32_t out, uint32_t in, const float* x, uint32_t T,
+                float* y, void* stream) {
+    CHK_TRY({
+        ensure(in % 64 == 0 && in > 0 && out > 0 && T > 0, "in must be a positive multiple of 64, out and T positive");
+        hipStream_t st = (hipStream_t)stream;
+        uint4 *hi = nullptr, *lo = nullptr;
+        float* xs = nullptr;
+        HIPCHK(hipMalloc(&hi, (size_t)T * in * 2));
+        HIPCHK(hipMalloc(&lo, (size_t)T * in * 2));
+        HIPCHK(hipMalloc(&xs, (size_t)T * (in / 64) * 4));
+        launch_pf_xprep(x, in, T, in, hi, lo, xs, st);
+        launch_pf_gemm(Q4Mat{(const uint32_t*)w, (const uint16_t*)s, (const uint16_t*)b, out, in}, hi, lo, xs, y, T,
+                       out, false, st);
+        HIPCHK(hipStreamSynchronize(st));
+        HIPCHK(hipGetLastError());
+        HIPCHK(hipFree(hi));
+        HIPCHK(hipFree(lo));
+        HIPCHK(hipFree(xs));
+    })
+}
+
 int chk_copy_f32(float* dst, const float* src, uint64_t n, void* stream) {
     CHK_TRY({
         hipStream_t st = (hipStream_t)stream;

@@ -270,6 +270,10 @@ void launch_moe_down(const MoeArgs& a, hipStream_t st);
 void launch_lm_head(const Q4Mat& m, const float* x, float* logits, float* pv, uint32_t* pi, uint32_t nparts,
                     uint32_t* out, int nb, hipStream_t st);
 void launch_attn(const AttnArgs& a, int nb, hipStream_t st);
+void launch_pf_xprep(const float* x, uint32_t ldx, uint32_t T, uint32_t K, uint4* hi, uint4* lo, float* xs,
+                     hipStream_t st);
+void launch_pf_gemm(const Q4Mat& w, const uint4* xhi, const uint4* xlo, const float* xs, float* y, uint32_t T,
+                    uint32_t ldy, bool accumulate, hipStream_t st);
 void launch_attn_core(const AttnArgs& a, int nb, hipStream_t st);
 bool attn_shape_ok(uint32_t nh, uint32_t nkv, uint32_t hd);
 void launch_copy_f32(float* dst, const float* src, uint64_t n, hipStream_t st);

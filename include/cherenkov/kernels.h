@@ -28,6 +28,13 @@ extern "C" {
 int chk_q4_matvec(const void* w, const void* s, const void* b, uint32_t out, uint32_t in, const float* x,
                   float* y, uint32_t nb, void* stream);
 
+/* The prefill GEMM: y [T][out] = x [T][in] W^T for a Q4 g64 W [out][in]
+ * (the prefill qmm, gpu/prefill/projection.rs:8-108): MFMA on the integer
+ * codes, each group's scale and bias applied to its partial sums in f32,
+ * activations split into two fp16 parts.  in a multiple of 64. */
+int chk_q4_gemm(const void* w, const void* s, const void* b, uint32_t out, uint32_t in, const float* x, uint32_t T,
+                float* y, void* stream);
+
 /* The decode LM head: logits [nb][out] = W x as chk_q4_matvec, and ids[nb]
  * (device u32) = the greedy token of each row, lowest index on exact ties,
  * 0 when every logit is -inf (argmax_partial/argmax_final,
