@@ -6,6 +6,8 @@
 // as fp16, dequantised as q * fp16(d).  The split-T flash-decode shape
 // (partials (m, l, o) per chunk, then an LSE merge with the sigmoid output
 // gate) replaces attn_part2_q8/attn_combine (attention.metal:138-310).
+#include <stdexcept>
+
 #include "kernels_internal.h"
 
 namespace chk {
@@ -21,7 +23,7 @@ __global__ void __launch_bounds__(256) k_attn_prep(AttnArgs a) {
     const uint32_t b = blockIdx.y, item = blockIdx.x, d = threadIdx.x, hd = a.hd;
     const bool live = d < hd;
     const uint32_t pos = a.pos[b];
-    const KvDev& kv = a.kv[b];
+    const KvDev& kv = a.kv[a.one_kv ? 0 : b];
     if (item == a.nh + 2 * a.nkv) {
         if (d < a.ihd) kv.index_k[(size_t)pos * a.ihd + d] = a.idx_raw[(size_t)b * (a.inh + 1) * a.ihd + a.inh * a.ihd + d];
         return;
@@ -99,7 +101,7 @@ __global__ void __launch_bounds__(256) k_attn_part(AttnArgs a) {
     const uint32_t T = a.pos[b] + 1;  // causal: rows see positions <= their own
     const uint32_t t0 = c * CH;
     if (t0 >= T) return;
-    const KvDev& kv = a.kv[b];
+    const KvDev& kv = a.kv[a.one_kv ? 0 : b];
     const uint32_t kv_row = a.nkv * HD, n = min((uint32_t)CH, T - t0);
 
     // ---- issue: K quarter-rows, V u32 lanes, their fp16 scales
@@ -291,8 +293,13 @@ void launch_attn_core(const AttnArgs& a, int nb, hipStream_t st) {
     k_attn_combine<<<dim3(a.nh, nb), 256, 0, st>>>(a);
 }
 
-void launch_attn(const AttnArgs& a, int nb, hipStream_t st) {
+void launch_attn_prep(const AttnArgs& a, int nb, hipStream_t st) {
+    if (nb > MAX_NB && !a.one_kv) throw std::runtime_error("rows beyond the step batch must share one sequence");
     k_attn_prep<<<dim3(a.nh + 2 * a.nkv + 1, nb), CHK_WG, 0, st>>>(a);
+}
+
+void launch_attn(const AttnArgs& a, int nb, hipStream_t st) {
+    launch_attn_prep(a, nb, st);
     launch_attn_core(a, nb, st);
 }
 

@@ -116,6 +116,24 @@ struct Scratch {
     float* trace;  // [L][MAX_NB][hh] when tracing
 };
 
+// Chunk buffers of the GEMM prefill (allocated on its first use), `cap`
+// rows per chunk.  The DeltaNet and attention blocks share one arena.
+struct PfBufs {
+    uint32_t cap = 0;
+    uint32_t *tokens, *pos;
+    float* hyper;
+    uint4 *hi, *lo, *bhi, *bmid, *blo;
+    float* xs;
+    float *inv, *d, *inj_a, *inj_m, *mixed;
+    float *raw, *z, *a, *b, *conv, *decay, *beta, *y;
+    float *q_raw, *k_raw, *v_raw, *idx_raw, *q_ready, *attn_out;
+    float* part;
+    uint64_t part_floats;
+    float *logits, *sg, *wts;
+    uint32_t *ids, *list, *count, *tiles, *ntiles;
+    float *act, *yd;
+};
+
 }  // namespace chk
 
 using namespace chk;
@@ -147,6 +165,7 @@ struct ChkEngine {
     std::vector<KvDev> kv, kv2;
     KvDev mtp_kv{};
     Scratch s{};
+    PfBufs pf{};
     uint32_t max_chunks = 1, lm_parts = 1024;
     // sequence
     uint32_t pos = 0, batch_pos = 0, batch_nb = 0, max_t = 0, trunk_rows = 1;
@@ -842,6 +861,15 @@ struct ChkEngine {
     void mtp_rows(int rows, const float* src_hyper, const uint32_t* d_tokens, uint32_t base_pos);
     void mtp_pass_trunk(int rows, uint32_t base_pos, const uint32_t* d_next);
     void prefill(const uint32_t* toks, uint32_t n, uint32_t* next, uint32_t* draft);
+    void prefill_rows(const uint32_t* toks, uint32_t n, uint32_t* next, uint32_t* draft);
+    // ------------------------------------------------- GEMM prefill
+    bool pf_supported() const;
+    void pf_alloc();
+    void pf_hc_read(const HcDev& w, float* inj, uint32_t T, bool for_moe);
+    void pf_deltanet(const LayerDev& L, uint32_t T);
+    void pf_attention(const LayerDev& L, uint32_t T, uint32_t pos0);
+    void pf_moe(const LayerDev& L, uint32_t T);
+    void prefill_gemm(const uint32_t* toks, uint32_t n, uint32_t* next);
     void mtp_draft(const uint32_t* next, uint32_t n, uint32_t chain, uint32_t* drafts, uint32_t* nd);
 };
 
@@ -955,10 +983,22 @@ void ChkEngine::mtp_draft(const uint32_t* next, uint32_t n, uint32_t chain, uint
     mtp_logits_fresh = false;
 }
 
+// Gpu::prefill_chunk (gpu/prefill.rs:196-464): the GEMM path where this
+// engine implements it (Q4 experts, no MTP head), else the row path.  Both
+// leave the same state behind (prefill.rs:13-15).
+void ChkEngine::prefill(const uint32_t* toks, uint32_t n, uint32_t* next, uint32_t* draft) {
+    if (pf_supported()) {
+        prefill_gemm(toks, n, next);
+        *draft = 0xffffffffu;
+        return;
+    }
+    prefill_rows(toks, n, next, draft);
+}
+
 // Prompt processing through the row path: rows of up to MAX_NB tokens,
 // committed as they go, MTP cache kept in step (gpu/prefill.rs semantics:
 // side effects identical to row stepping, prefill.rs:13-15).
-void ChkEngine::prefill(const uint32_t* toks, uint32_t n, uint32_t* next, uint32_t* draft) {
+void ChkEngine::prefill_rows(const uint32_t* toks, uint32_t n, uint32_t* next, uint32_t* draft) {
     ensure(n >= 1, "empty prefill chunk");
     ensure(pos + n <= max_t, "context capacity exceeded");
     uint32_t saved_rows = trunk_rows;
@@ -988,6 +1028,347 @@ void ChkEngine::prefill(const uint32_t* toks, uint32_t n, uint32_t* next, uint32
     trunk_rows = saved_rows;
     *next = last;
     if (!has_mtp) *draft = 0xffffffffu;
+}
+
+// ------------------------------------------------------- GEMM prefill
+constexpr uint32_t PF_MAX_ROWS = 4096;                  // rows per chunk (gpu/prefill.rs:116)
+constexpr uint64_t PF_PART_BYTES = 256ull << 20;        // attention partials per sub-batch
+
+bool ChkEngine::pf_supported() const {
+    return o.experts == 4 && !has_mtp && D.lowrank % 64 == 0 && D.H % 64 == 0 && D.H <= 4096 && D.hc <= 4 &&
+           (D.dv == 64 || D.dv == 128 || D.dv == 256) && D.I % 64 == 0 && (D.nh * D.hd) % 64 == 0 &&
+           D.v_dim % 64 == 0 && D.E + 1 <= 513;
+}
+
+void ChkEngine::pf_alloc() {
+    if (pf.cap) return;
+    const uint64_t C = std::min<uint32_t>(max_t, PF_MAX_ROWS);
+    const uint64_t slots = D.topk + 1;
+    pf.tokens = dalloc<uint32_t>(C);
+    pf.pos = dalloc<uint32_t>(C);
+    pf.hyper = dalloc<float>(C * D.hh);
+    const uint64_t plane = std::max({C * D.hh, C * D.v_dim, C * D.nh * D.hd, C * slots * D.I, C * D.H});
+    pf.hi = dalloc<uint4>(plane / 8);
+    pf.lo = dalloc<uint4>(plane / 8);
+    pf.xs = dalloc<float>(plane / 64);
+    pf.bhi = dalloc<uint4>(C * D.H / 8);
+    pf.bmid = dalloc<uint4>(C * D.H / 8);
+    pf.blo = dalloc<uint4>(C * D.H / 8);
+    pf.inv = dalloc<float>(C * D.hc);
+    pf.d = dalloc<float>(C * D.lowrank);
+    pf.inj_a = dalloc<float>(C * D.hc);
+    pf.inj_m = dalloc<float>(C * D.hc);
+    pf.mixed = dalloc<float>(C * D.H);
+    // DeltaNet / attention arena
+    const uint64_t dn = C * (2ull * D.conv_dim + 2ull * D.v_dim + 4ull * D.nv);
+    const uint64_t at = C * (2ull * D.nh * D.hd + 2ull * D.kv_row + D.idx_out + 2ull * D.nh * D.hd);
+    float* arena = dalloc<float>(std::max(dn, at));
+    float* q = arena;
+    pf.raw = q; q += C * D.conv_dim;
+    pf.conv = q; q += C * D.conv_dim;
+    pf.z = q; q += C * D.v_dim;
+    pf.y = q; q += C * D.v_dim;
+    pf.a = q; q += C * D.nv;
+    pf.b = q; q += C * D.nv;
+    pf.decay = q; q += C * D.nv;
+    pf.beta = q;
+    q = arena;
+    pf.q_raw = q; q += C * 2 * D.nh * D.hd;
+    pf.k_raw = q; q += C * D.kv_row;
+    pf.v_raw = q; q += C * D.kv_row;
+    pf.idx_raw = q; q += C * D.idx_out;
+    pf.q_ready = q; q += C * D.nh * D.hd;
+    pf.attn_out = q;
+    pf.part_floats = PF_PART_BYTES / 4;
+    pf.part = dalloc<float>(pf.part_floats);
+    pf.logits = dalloc<float>(C * D.E);
+    pf.sg = dalloc<float>(C);
+    pf.wts = dalloc<float>(C * D.topk);
+    pf.ids = dalloc<uint32_t>(C * D.topk);
+    pf.list = dalloc<uint32_t>((D.E + 1) * C);
+    pf.count = dalloc<uint32_t>(D.E + 1);
+    pf.tiles = dalloc<uint32_t>(pf_tile_bound((uint32_t)C, D.topk, D.E));
+    pf.ntiles = dalloc<uint32_t>(1);
+    pf.act = dalloc<float>(C * slots * D.I);
+    pf.yd = dalloc<float>(C * slots * D.H);
+    pf.cap = (uint32_t)C;
+}
+
+// gated_residual read (cpu.rs:461-500) over the chunk's rows: grouped
+// RMSNorm into GEMM operands, [down; inject] GEMM with silu / 2 sigmoid,
+// up GEMM with the sigmoid mix, then the mixed rows as the next operands.
+void ChkEngine::pf_hc_read(const HcDev& w, float* inj, uint32_t T, bool for_moe) {
+    const uint32_t mt = (T + 63) / 64;
+    launch_pf_hc_prep(pf.hyper, w.norm, D.H, D.hc, D.eps, pf.inv, pf.hi, pf.lo, pf.xs, T, st);
+    PfGemmArgs g{};
+    g.seg[0] = PfSeg{w.down, pf.d, D.lowrank, 0, PA_SILU};
+    g.seg[1] = PfSeg{w.inject, inj, D.hc, D.lowrank, PA_2SIG};
+    g.nseg = 2;
+    g.N = D.lowrank + D.hc;
+    g.K = D.hh;
+    g.M = T;
+    g.alpha = 1.0f / (float)D.hc;
+    g.xhi = pf.hi;
+    g.xlo = pf.lo;
+    g.xs = pf.xs;
+    launch_pf_gemm_args(g, PE_STORE, mt, st);
+    launch_pf_xprep(pf.d, D.lowrank, T, D.lowrank, pf.hi, pf.lo, pf.xs, st);
+    PfGemmArgs u{};
+    u.seg[0].m = w.up;
+    u.nseg = 1;
+    u.N = D.hh;
+    u.K = D.lowrank;
+    u.M = T;
+    u.xhi = pf.hi;
+    u.xlo = pf.lo;
+    u.xs = pf.xs;
+    u.hyper = pf.hyper;
+    u.inv = pf.inv;
+    u.norm = w.norm;
+    u.out = pf.mixed;
+    u.H = D.H;
+    u.hc = D.hc;
+    launch_pf_gemm_args(u, PE_HC_UP, mt, st);
+    PfPrepArgs p{};
+    p.x = pf.mixed;
+    p.ldx = D.H;
+    p.T = T;
+    p.K = D.H;
+    p.hi = pf.hi;
+    p.lo = pf.lo;
+    p.xs = pf.xs;
+    if (for_moe) {
+        p.bhi = pf.bhi;
+        p.bmid = pf.bmid;
+        p.blo = pf.blo;
+    }
+    launch_pf_prep(p, st);
+}
+
+// linear_attention (cpu.rs:745-826) over the chunk: the four input
+// projections as one GEMM, conv + norms, the sequential scan, the gated
+// norm into the out-projection's operands, out-projection + inject.
+void ChkEngine::pf_deltanet(const LayerDev& L, uint32_t T) {
+    const uint32_t mt = (T + 63) / 64, di = (uint32_t)L.dn_idx;
+    PfGemmArgs g{};
+    g.seg[0] = PfSeg{L.dn.qkv, pf.raw, D.conv_dim, 0, PA_NONE};
+    g.seg[1] = PfSeg{L.dn.z, pf.z, D.v_dim, D.conv_dim, PA_NONE};
+    g.seg[2] = PfSeg{L.dn.a, pf.a, D.nv, D.conv_dim + D.v_dim, PA_NONE};
+    g.seg[3] = PfSeg{L.dn.b, pf.b, D.nv, D.conv_dim + D.v_dim + D.nv, PA_NONE};
+    g.nseg = 4;
+    g.N = D.conv_dim + D.v_dim + 2 * D.nv;
+    g.K = D.H;
+    g.M = T;
+    g.xhi = pf.hi;
+    g.xlo = pf.lo;
+    g.xs = pf.xs;
+    launch_pf_gemm_args(g, PE_STORE, mt, st);
+    PfDnArgs a{};
+    a.raw = pf.raw;
+    a.ld_raw = D.conv_dim;
+    a.a_raw = pf.a;
+    a.b_raw = pf.b;
+    a.ld_ab = D.nv;
+    a.conv_w = L.dn.conv;
+    a.a_log = L.dn.a_log;
+    a.dt_bias = L.dn.dt_bias;
+    a.hist = dn_hist[di];
+    a.conv = pf.conv;
+    a.decay = pf.decay;
+    a.beta = pf.beta;
+    a.state = dn_state[di];
+    a.y = pf.y;
+    a.T = T;
+    a.conv_dim = D.conv_dim;
+    a.ck = D.ck;
+    a.nk = D.nk;
+    a.nv = D.nv;
+    a.dv = D.dv;
+    a.qk_dim = D.qk_dim;
+    a.v_dim = D.v_dim;
+    a.qscale = D.qscale;
+    launch_pf_dn(a, st);
+    PfPrepArgs p{};
+    p.x = pf.y;
+    p.ldx = D.v_dim;
+    p.T = T;
+    p.K = D.v_dim;
+    p.hi = pf.hi;
+    p.lo = pf.lo;
+    p.xs = pf.xs;
+    p.z = pf.z;
+    p.norm = L.dn.norm;
+    p.dv = D.dv;
+    launch_pf_prep(p, st);
+    PfGemmArgs o2{};
+    o2.seg[0].m = L.dn.out;
+    o2.nseg = 1;
+    o2.N = D.H;
+    o2.K = D.v_dim;
+    o2.M = T;
+    o2.xhi = pf.hi;
+    o2.xlo = pf.lo;
+    o2.xs = pf.xs;
+    o2.hyper = pf.hyper;
+    o2.inj = pf.inj_a;
+    o2.H = D.H;
+    o2.hc = D.hc;
+    launch_pf_gemm_args(o2, PE_INJECT, mt, st);
+}
+
+// attention (cpu.rs:544-641) over the chunk: projections as one GEMM, the
+// per-row prep writing the chunk's q8 K/V and index keys at their
+// positions, causal attention of every row over the cache (sub-batches of
+// rows sized to the partials buffer), o-projection + inject.
+void ChkEngine::pf_attention(const LayerDev& L, uint32_t T, uint32_t pos0) {
+    const uint32_t mt = (T + 63) / 64;
+    PfGemmArgs g{};
+    g.seg[0] = PfSeg{L.at.q, pf.q_raw, 2 * D.nh * D.hd, 0, PA_NONE};
+    g.seg[1] = PfSeg{L.at.k, pf.k_raw, D.kv_row, 2 * D.nh * D.hd, PA_NONE};
+    g.seg[2] = PfSeg{L.at.v, pf.v_raw, D.kv_row, 2 * D.nh * D.hd + D.kv_row, PA_NONE};
+    g.seg[3] = PfSeg{L.at.idx, pf.idx_raw, D.idx_out, 2 * D.nh * D.hd + 2 * D.kv_row, PA_NONE};
+    g.nseg = 4;
+    g.N = 2 * D.nh * D.hd + 2 * D.kv_row + D.idx_out;
+    g.K = D.H;
+    g.M = T;
+    g.xhi = pf.hi;
+    g.xlo = pf.lo;
+    g.xs = pf.xs;
+    launch_pf_gemm_args(g, PE_STORE, mt, st);
+    AttnArgs aa{};
+    aa.q_raw = pf.q_raw;
+    aa.k_raw = pf.k_raw;
+    aa.v_raw = pf.v_raw;
+    aa.idx_raw = pf.idx_raw;
+    aa.q_norm = L.at.q_norm;
+    aa.k_norm = L.at.k_norm;
+    aa.q_ready = pf.q_ready;
+    aa.kv[0] = kv[L.at_idx];
+    aa.one_kv = 1;
+    aa.pos = pf.pos;
+    aa.part = pf.part;
+    aa.out = pf.attn_out;
+    aa.nh = D.nh;
+    aa.nkv = D.nkv;
+    aa.hd = D.hd;
+    aa.rot = D.rot;
+    aa.inh = D.inh;
+    aa.ihd = D.ihd;
+    aa.eps = D.eps;
+    aa.theta = D.theta;
+    aa.scale = D.attn_scale;
+    aa.max_chunks = (pos0 + T - 1) / ATTN_CHUNK + 1;
+    launch_attn_prep(aa, (int)T, st);
+    const uint64_t per_row = (uint64_t)D.nh * aa.max_chunks * (D.hd + 2);
+    const uint32_t rows = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(T, pf.part_floats / per_row));
+    for (uint32_t r0 = 0; r0 < T; r0 += rows) {
+        AttnArgs b = aa;
+        const uint32_t nb = std::min(rows, T - r0);
+        b.q_raw = pf.q_raw + (uint64_t)r0 * 2 * D.nh * D.hd;
+        b.q_ready = pf.q_ready + (uint64_t)r0 * D.nh * D.hd;
+        b.out = pf.attn_out + (uint64_t)r0 * D.nh * D.hd;
+        b.pos = pf.pos + r0;
+        launch_attn_core(b, (int)nb, st);
+    }
+    launch_pf_xprep(pf.attn_out, D.nh * D.hd, T, D.nh * D.hd, pf.hi, pf.lo, pf.xs, st);
+    PfGemmArgs o2{};
+    o2.seg[0].m = L.at.o;
+    o2.nseg = 1;
+    o2.N = D.H;
+    o2.K = D.nh * D.hd;
+    o2.M = T;
+    o2.xhi = pf.hi;
+    o2.xlo = pf.lo;
+    o2.xs = pf.xs;
+    o2.hyper = pf.hyper;
+    o2.inj = pf.inj_a;
+    o2.H = D.H;
+    o2.hc = D.hc;
+    launch_pf_gemm_args(o2, PE_INJECT, mt, st);
+}
+
+// moe (cpu.rs:504-541) over the chunk: router GEMM, per-row top-k, entries
+// grouped by expert, grouped gate/up GEMM (shared expert as the last
+// group), grouped down GEMM per entry, weighted combine + inject.
+void ChkEngine::pf_moe(const LayerDev& L, uint32_t T) {
+    const uint32_t slots = D.topk + 1;
+    launch_pf_router(L.moe.router, L.moe.shared_gate, pf.bhi, pf.bmid, pf.blo, pf.logits, pf.sg, T, D.E, D.H, st);
+    launch_pf_route(pf.logits, T, D.E, D.topk, D.norm_topk, pf.ids, pf.wts, st);
+    // the chunk's last row as this layer's "last routes", as a row step leaves them
+    const uint64_t roff = (uint64_t)L.moe.record_layer * MAX_NB * D.topk;
+    HIPCHK(hipMemcpyAsync(s.route_ids + roff, pf.ids + (uint64_t)(T - 1) * D.topk, D.topk * 4,
+                          hipMemcpyDeviceToDevice, st));
+    HIPCHK(hipMemcpyAsync(s.route_w + roff, pf.wts + (uint64_t)(T - 1) * D.topk, D.topk * 4, hipMemcpyDeviceToDevice,
+                          st));
+    launch_pf_group(pf.ids, T, D.topk, D.E, pf.cap, pf.list, pf.count, pf.tiles, pf.ntiles, st);
+    const uint32_t bound = pf_tile_bound(T, D.topk, D.E);
+    PfGemmArgs gu{};
+    gu.seg[0] = PfSeg{L.moe.sh_gate, pf.act, D.I, 0, PA_NONE};
+    gu.seg[1].m = L.moe.sh_up;
+    gu.nseg = 1;
+    gu.N = D.I;
+    gu.K = D.H;
+    gu.xhi = pf.hi;
+    gu.xlo = pf.lo;
+    gu.xs = pf.xs;
+    gu.list = pf.list;
+    gu.count = pf.count;
+    gu.tiles = pf.tiles;
+    gu.ntiles = pf.ntiles;
+    gu.cap = pf.cap;
+    gu.div = slots;
+    gu.X = experts_dev();
+    gu.record_layer = L.moe.record_layer;
+    launch_pf_gemm_args(gu, PE_SILU_MUL, bound, st);
+    launch_pf_xprep(pf.act, D.I, T * slots, D.I, pf.hi, pf.lo, pf.xs, st);
+    PfGemmArgs dn = gu;
+    dn.seg[0] = PfSeg{L.moe.sh_down, pf.yd, D.H, 0, PA_NONE};
+    dn.seg[1] = PfSeg{};
+    dn.N = D.H;
+    dn.K = D.I;
+    dn.div = 1;
+    launch_pf_gemm_args(dn, PE_STORE, bound, st);
+    launch_pf_moe_combine(pf.yd, pf.wts, pf.sg, pf.inj_m, pf.hyper, T, D.H, D.topk, D.hc, st);
+}
+
+void ChkEngine::prefill_gemm(const uint32_t* toks, uint32_t n, uint32_t* next) {
+    ensure(n >= 1, "empty prefill chunk");
+    ensure(pos + n <= max_t, "context capacity exceeded");
+    for (uint32_t i = 0; i < n; ++i) ensure(toks[i] < D.V, "token id out of range");
+    pf_alloc();
+    folded_valid = false;
+    tokens.resize(pos);
+    for (uint32_t c0 = 0; c0 < n; c0 += pf.cap) {
+        const uint32_t T = std::min(pf.cap, n - c0), pos0 = pos;
+        std::vector<uint32_t> rp(T);
+        for (uint32_t t = 0; t < T; ++t) rp[t] = pos0 + t;
+        HIPCHK(hipMemcpy(pf.tokens, toks + c0, T * 4, hipMemcpyHostToDevice));
+        HIPCHK(hipMemcpy(pf.pos, rp.data(), T * 4, hipMemcpyHostToDevice));
+        launch_pf_embed(pf.tokens, embed, pf.hyper, D.H, D.hc, T, st);
+        for (uint32_t l = 0; l < c.num_hidden_layers; ++l) {
+            const LayerDev& L = layers[l];
+            pf_hc_read(L.attn_hc, pf.inj_a, T, false);
+            if (L.linear) pf_deltanet(L, T);
+            else pf_attention(L, T, pos0);
+            pf_hc_read(L.mlp_hc, pf.inj_m, T, true);
+            pf_moe(L, T);
+        }
+        if (c0 + T >= n) {
+            // final mixer and LM head on the chunk's last row (prefill.rs:308-334)
+            hc_read(final_mixer, pf.hyper + (uint64_t)(T - 1) * D.hh, nullptr, 1);
+            launch_lm_head(lm_head, s.mixed, s.logits, s.pv, s.pi, lm_parts, s.d_out, 1, st);
+        }
+        HIPCHK(hipStreamSynchronize(st));
+        HIPCHK(hipGetLastError());
+        tokens.insert(tokens.end(), toks + c0, toks + c0 + T);
+        pos = pos0 + T;
+    }
+    *next = s.h_out[0];
+    batch_pos = pos - 1;
+    batch_nb = 1;
+    batch_snap = false;
+    logits_fresh = false;
+    mtp_logits_fresh = false;
 }
 
 // ===================================================================== C ABI
@@ -1412,7 +1793,7 @@ int chk_q4_gemm(const void* w, const void* s, const void* b, uint32_t out, uint3
         HIPCHK(hipMalloc(&xs, (size_t)T * (in / 64) * 4));
         launch_pf_xprep(x, in, T, in, hi, lo, xs, st);
         launch_pf_gemm(Q4Mat{(const uint32_t*)w, (const uint16_t*)s, (const uint16_t*)b, out, in}, hi, lo, xs, y, T,
-                       out, false, st);
+                       out, st);
         HIPCHK(hipStreamSynchronize(st));
         HIPCHK(hipGetLastError());
         HIPCHK(hipFree(hi));

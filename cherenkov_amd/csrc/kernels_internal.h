@@ -244,6 +244,82 @@ struct AttnArgs {
     float* out;            // [nb][nh * hd] gated
     uint32_t nh, nkv, hd, rot, inh, ihd, max_chunks;
     float eps, theta, scale;
+    int one_kv;            // every row belongs to kv[0]'s sequence (prefill rows)
+};
+
+// ------------------------------------------------------------- prefill
+enum PfEpi { PE_STORE = 0, PE_INJECT = 1, PE_HC_UP = 2, PE_SILU_MUL = 3 };
+enum PfAct { PA_NONE = 0, PA_SILU = 1, PA_2SIG = 2 };
+
+// Operand preparation of one activation matrix (k_pf_prep).
+struct PfPrepArgs {
+    const float* x;    // [T][ldx]
+    uint32_t ldx, T, K;
+    uint4* hi;         // [T][K/8] fp16, permuted 8-blocks
+    uint4* lo;
+    float* xs;         // [T][K/64]
+    uint4* bhi;        // optional bf16 natural-order planes [T][K/8] (hi + mid + lo)
+    uint4* bmid;
+    uint4* blo;
+    // DeltaNet gated norm (z non-null): x = y, z same stride
+    const float* z;
+    const uint16_t* norm;
+    uint32_t dv;
+};
+
+// One output segment of a concatenated projection: outputs [n0, n0 + m.out).
+struct PfSeg {
+    Q4Mat m;
+    float* y;
+    uint32_t ldy, n0;
+    int act;  // PfAct of alpha * v
+    uint32_t wo, so, bo;  // set by the launcher: element offsets of m from wbase / sbase
+};
+
+struct PfGemmArgs {
+    PfSeg seg[4];      // PE_SILU_MUL: seg[0].m gate, seg[1].m up (shared expert), output seg[0].y
+    uint32_t nseg, N, K, M;
+    float alpha;
+    const uint4* xhi;
+    const uint4* xlo;
+    const float* xs;
+    // grouped rows (list non-null)
+    const uint32_t* list;    // [groups][cap] entries
+    const uint32_t* count;   // [groups]
+    const uint32_t* tiles;   // (group << 16 | 64-row tile)
+    const uint32_t* ntiles;
+    uint32_t cap, div;
+    ExpertsDev X;            // routed-expert records for groups < X.experts
+    uint32_t record_layer;
+    const uint32_t* wbase;   // set by the launcher (dense matrices' common bases)
+    const uint16_t* sbase;
+    // PE_INJECT / PE_HC_UP
+    float* hyper;            // [M][hc H]
+    const float* inj;        // [M][hc]
+    const float* inv;        // [M][hc]
+    const uint16_t* norm;    // [hc H]
+    float* out;              // [M][H]
+    uint32_t H, hc;
+};
+
+// DeltaNet prefill (conv, decay/beta, sequential scan) over T rows.
+struct PfDnArgs {
+    const float* raw;      // [T][ld_raw] qkv projection (pre-conv)
+    uint32_t ld_raw;
+    const float* a_raw;    // [T][ld_ab]
+    const float* b_raw;
+    uint32_t ld_ab;
+    const uint16_t* conv_w;
+    const uint16_t* a_log;
+    const uint16_t* dt_bias;
+    float* hist;           // [conv_dim][ck - 1]
+    float* conv;           // [T][conv_dim] after conv, silu, q/k norms
+    float* decay;          // [T][nv]
+    float* beta;           // [T][nv]
+    float* state;          // [nv][dv][dk]
+    float* y;              // [T][v_dim]
+    uint32_t T, conv_dim, ck, nk, nv, dv, qk_dim, v_dim;
+    float qscale;
 };
 
 // Per-step inputs written by the host into pinned, device-mapped memory
@@ -270,10 +346,27 @@ void launch_moe_down(const MoeArgs& a, hipStream_t st);
 void launch_lm_head(const Q4Mat& m, const float* x, float* logits, float* pv, uint32_t* pi, uint32_t nparts,
                     uint32_t* out, int nb, hipStream_t st);
 void launch_attn(const AttnArgs& a, int nb, hipStream_t st);
+void launch_pf_prep(const PfPrepArgs& a, hipStream_t st);
 void launch_pf_xprep(const float* x, uint32_t ldx, uint32_t T, uint32_t K, uint4* hi, uint4* lo, float* xs,
                      hipStream_t st);
+void launch_pf_hc_prep(const float* hyper, const uint16_t* norm, uint32_t H, uint32_t hc, float eps, float* inv,
+                       uint4* hi, uint4* lo, float* xs, uint32_t T, hipStream_t st);
+void launch_pf_gemm_args(const PfGemmArgs& a, int epi, uint32_t grid_y, hipStream_t st);
 void launch_pf_gemm(const Q4Mat& w, const uint4* xhi, const uint4* xlo, const float* xs, float* y, uint32_t T,
-                    uint32_t ldy, bool accumulate, hipStream_t st);
+                    uint32_t ldy, hipStream_t st);
+void launch_pf_router(const uint16_t* router, const uint16_t* shared_gate, const uint4* bhi, const uint4* bmid,
+                      const uint4* blo, float* logits, float* sg, uint32_t T, uint32_t E, uint32_t H, hipStream_t st);
+void launch_pf_route(const float* logits, uint32_t T, uint32_t E, uint32_t topk, int norm_topk, uint32_t* ids,
+                     float* wts, hipStream_t st);
+void launch_pf_group(const uint32_t* ids, uint32_t T, uint32_t topk, uint32_t E, uint32_t cap, uint32_t* list,
+                     uint32_t* count, uint32_t* tiles, uint32_t* ntiles, hipStream_t st);
+uint32_t pf_tile_bound(uint32_t T, uint32_t topk, uint32_t E);
+void launch_pf_moe_combine(const float* yd, const float* wts, const float* sg, const float* inj, float* hyper,
+                           uint32_t T, uint32_t H, uint32_t topk, uint32_t hc, hipStream_t st);
+void launch_pf_embed(const uint32_t* tokens, const Q4Mat& emb, float* hyper, uint32_t H, uint32_t hc, uint32_t T,
+                     hipStream_t st);
+void launch_pf_dn(const PfDnArgs& a, hipStream_t st);
+void launch_attn_prep(const AttnArgs& a, int nb, hipStream_t st);
 void launch_attn_core(const AttnArgs& a, int nb, hipStream_t st);
 bool attn_shape_ok(uint32_t nh, uint32_t nkv, uint32_t hd);
 void launch_copy_f32(float* dst, const float* src, uint64_t n, hipStream_t st);

@@ -1,11 +1,15 @@
-// Prefill GEMMs on gfx950 MFMA: Y[t][n] = sum_k X[t][k] W[n][k] for an MLX
-// affine Q4 (group 64) weight W [N][K] and activations X [T][K], with the
-// reference's quantisation semantics (quant.rs:13-89: w = s q + b per group)
-// kept exact: the MFMA multiplies the integer codes, and the group's scale
-// and bias are applied to its partial sums in f32,
+// Prefill on gfx950: a chunk of T prompt tokens goes through the decoder
+// one layer at a time, every projection as an MFMA GEMM over all T rows
+// (prefill_chunk / pf_layer, src/qwen4_exp/gpu/prefill.rs:124-464).
+//
+// Q4 GEMMs: Y[t][n] = sum_k X[t][k] W[n][k] for an MLX affine Q4 (group 64)
+// weight W [N][K] and activations X [T][K], with the reference's
+// quantisation semantics (quant.rs:13-89: w = s q + b per group) kept
+// exact: the MFMA multiplies the integer codes, and the group's scale and
+// bias are applied to its partial sums in f32,
 //   Y += s[n][g] * (sum_{k in g} q[n][k] x[t][k]) + b[n][g] * (sum_{k in g} x[t][k]).
 //
-// v_mfma_f32_16x16x32_f16 (A: 16 tokens x 32 k, B: 32 k x 16 outputs, D:
+// v_mfma_f32_16x16x32_f16 (A: 16 rows x 32 k, B: 32 k x 16 outputs, D:
 // 16 x 16 f32).  Lane l of B holds output column l % 16 and the 8 k
 // values (l / 16) * 8 .. + 8, which is exactly one packed weight word.  The
 // word unpacks the way the decode dot does (device.h q4_chunk_h): OR-ing
@@ -17,33 +21,66 @@
 // planes (x = hi + lo, ~22 significant bits); each MFMA pair (hi, lo)
 // multiplies exact small integers by exact fp16 values into f32.
 //
-// Reference counterpart: the prefill qmm GEMMs (gpu/prefill/projection.rs:8-108),
-// which run on half operands.
+// Reference counterparts: the prefill qmm GEMMs (gpu/prefill/projection.rs:8-108,
+// half operands there), the grouped experts (gpu/prefill/experts.rs:29-345),
+// the sequential scan (gpu/prefill/deltanet.rs:7-110).
+#include <algorithm>
+#include <cstdint>
 #include <stdexcept>
+#include <type_traits>
 
 #include "kernels_internal.h"
 
 namespace chk {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef __bf16 b8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+CHK_DEV uint32_t f2bf_rne(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
 
 // ------------------------------------------------------ activation prep
-// X f32 [T][K] (row stride ldx) -> hi, lo fp16 [T][K] in the permuted
-// 8-block order above, and xs f32 [T][K/64] = per-group sums of X.
-// One thread per 8-block.
-__global__ void __launch_bounds__(256) k_pf_xprep(const float* __restrict__ x, uint32_t ldx, uint32_t T, uint32_t K,
-                                                  uint4* __restrict__ hi, uint4* __restrict__ lo,
-                                                  float* __restrict__ xs) {
-    const uint32_t blocks = K >> 3;
+// X f32 [T][K] (row stride ldx) -> hi, lo fp16 [T][K/8] uint4 in the
+// permuted 8-block order above, xs f32 [T][K/64] = per-group sums of X, and
+// optionally bf16 hi/lo planes in natural order (the router's operands).
+// One thread per 8-block.  PP_DN_GATE prepares the DeltaNet output instead:
+// x = y, and each value head is gated as rmsnorm(y_head) * w * sigmoid(z)
+// (cpu.rs:814-826, eps 1e-6) before the split.
+enum PfPrepMode { PP_PLAIN = 0, PP_DN_GATE = 1 };
+
+template <int MODE, int HEAD_LANES>
+__global__ void __launch_bounds__(256) k_pf_prep(PfPrepArgs a) {
+    const uint32_t blocks = a.K >> 3;
     const uint64_t i = (uint64_t)blockIdx.x * CHK_WG + threadIdx.x;
-    const bool live = i < (uint64_t)T * blocks;
+    const bool live = i < (uint64_t)a.T * blocks;
     const uint32_t t = live ? (uint32_t)(i / blocks) : 0, kb = live ? (uint32_t)(i % blocks) : 0;
     float v[8];
-    const float4* p = reinterpret_cast<const float4*>(x + (size_t)t * ldx + kb * 8);
-    const float4 a = p[0], b = p[1];
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-    // this 8-block's sum, then the 64-group sum over 8 neighbouring lanes
+    {
+        const float4* p = reinterpret_cast<const float4*>(a.x + (size_t)t * a.ldx + kb * 8);
+        const float4 u0 = p[0], u1 = p[1];
+        v[0] = u0.x; v[1] = u0.y; v[2] = u0.z; v[3] = u0.w; v[4] = u1.x; v[5] = u1.y; v[6] = u1.z; v[7] = u1.w;
+    }
+    if (!live)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = 0.0f;
+    if (MODE == PP_DN_GATE) {
+        float sq = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sq += v[j] * v[j];
+        sq = group_sum<HEAD_LANES>(sq);
+        const float inv = 1.0f / sqrtf(sq / (float)a.dv + 1e-6f);
+        const float4* zp = reinterpret_cast<const float4*>(a.z + (size_t)t * a.ldx + kb * 8);
+        const float4 z0 = zp[0], z1 = zp[1];
+        const float z[8] = {z0.x, z0.y, z0.z, z0.w, z1.x, z1.y, z1.z, z1.w};
+        const uint32_t d0 = (kb * 8) % a.dv;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = live ? v[j] * bf16f(a.norm[d0 + j]) * sigmoidf_(z[j]) * inv : 0.0f;
+    }
     float s = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
     s += __shfl_xor(s, 1, 64);
     s += __shfl_xor(s, 2, 64);
@@ -57,117 +94,808 @@ __global__ void __launch_bounds__(256) k_pf_xprep(const float* __restrict__ x, u
         h[j] = hj;
         l[j] = (_Float16)(o[j] - (float)hj);
     }
-    hi[i] = __builtin_bit_cast(uint4, h);
-    lo[i] = __builtin_bit_cast(uint4, l);
-    if ((kb & 7) == 0) xs[(size_t)t * (K >> 6) + (kb >> 3)] = s;
+    a.hi[i] = __builtin_bit_cast(uint4, h);
+    a.lo[i] = __builtin_bit_cast(uint4, l);
+    if ((kb & 7) == 0) a.xs[(size_t)t * (a.K >> 6) + (kb >> 3)] = s;
+    if (a.bhi) {
+        // three bf16 terms (x = hi + mid + lo, ~24 significant bits)
+        uint32_t bh[8], bm[8], bl[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            bh[j] = f2bf_rne(v[j]);
+            const float r1 = v[j] - __uint_as_float(bh[j] << 16);
+            bm[j] = f2bf_rne(r1);
+            bl[j] = f2bf_rne(r1 - __uint_as_float(bm[j] << 16));
+        }
+        a.bhi[i] = make_uint4(bh[0] | bh[1] << 16, bh[2] | bh[3] << 16, bh[4] | bh[5] << 16, bh[6] | bh[7] << 16);
+        a.bmid[i] = make_uint4(bm[0] | bm[1] << 16, bm[2] | bm[3] << 16, bm[4] | bm[5] << 16, bm[6] | bm[7] << 16);
+        a.blo[i] = make_uint4(bl[0] | bl[1] << 16, bl[2] | bl[3] << 16, bl[4] | bl[5] << 16, bl[6] | bl[7] << 16);
+    }
+}
+
+// ----------------------------------------------- hyper-connection norm
+// normed[t][g H + k] = hyper[t][g H + k] * inv[t][g] * w[g H + k] with
+// inv = 1/sqrt(mean_k(hyper[t][g H + k]^2) + eps) per stream g (the
+// grouped RMSNorm of gated_residual, cpu.rs:461-475), prepared as GEMM
+// operands over K = hc H.  One workgroup per row; thread tau owns 8-blocks
+// tau and tau + 256 of every stream (H <= 4096).
+__global__ void __launch_bounds__(256) k_pf_hc_prep(const float* __restrict__ hyper, const uint16_t* __restrict__ norm,
+                                                    uint32_t H, uint32_t hc, float eps, float* __restrict__ inv_out,
+                                                    uint4* __restrict__ hi, uint4* __restrict__ lo,
+                                                    float* __restrict__ xs) {
+    __shared__ float red[4];
+    const uint32_t t = blockIdx.x, tau = threadIdx.x, bps = H >> 3, hh = H * hc;
+    const float* row = hyper + (size_t)t * hh;
+    float v[4][2][8];
+    float sq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t kb = tau + 256 * j;
+            const bool ok = (uint32_t)g < hc && kb < bps;
+            const float4* p = reinterpret_cast<const float4*>(row + (size_t)(ok ? g : 0) * H + (ok ? kb : 0) * 8);
+            const float4 u0 = p[0], u1 = p[1];
+            const float w8[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                v[g][j][e] = ok ? w8[e] : 0.0f;
+                sq[g] += v[g][j][e] * v[g][j][e];
+            }
+        }
+    float inv[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        if ((uint32_t)g >= hc) {
+            inv[g] = 0.0f;
+            continue;
+        }
+        inv[g] = 1.0f / sqrtf(block_sum(sq[g], red) / (float)H + eps);
+        if (tau == 0) inv_out[(size_t)t * hc + g] = inv[g];
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t kb = tau + 256 * j;
+            if ((uint32_t)g >= hc || 256 * j >= bps) continue;  // uniform
+            const bool ok = kb < bps;
+            float x[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[e] = ok ? v[g][j][e] * inv[g] * bf16f(norm[(size_t)g * H + min(kb, bps - 1) * 8 + e]) : 0.0f;
+            float s = ((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]));
+            s += __shfl_xor(s, 1, 64);
+            s += __shfl_xor(s, 2, 64);
+            s += __shfl_xor(s, 4, 64);
+            if (!ok) continue;
+            const float o[8] = {x[0], x[4], x[1] * 0.0625f, x[5] * 0.0625f, x[2], x[6], x[3] * 0.0625f, x[7] * 0.0625f};
+            h8 h, l;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const _Float16 he = (_Float16)o[e];
+                h[e] = he;
+                l[e] = (_Float16)(o[e] - (float)he);
+            }
+            const size_t idx = (size_t)t * (hh >> 3) + (size_t)g * bps + kb;
+            hi[idx] = __builtin_bit_cast(uint4, h);
+            lo[idx] = __builtin_bit_cast(uint4, l);
+            if ((kb & 7) == 0) xs[(size_t)t * (hh >> 6) + (size_t)g * (H >> 6) + (kb >> 3)] = s;
+        }
 }
 
 // --------------------------------------------------------------- GEMM
-// A wave computes 64 tokens x 64 outputs (4 x 4 MFMA tiles); a workgroup's
-// four waves cover 64 tokens x 256 outputs.  Grid (ceil(N / 256), ceil(T / 64)).
-// Per 64-wide quant group: the group's partial sums accumulate from zero in
-// acc_g (2 K-steps of 32, hi then lo), then fold into acc with the group's
-// scale and bias.
-struct PfGemmArgs {
-    Q4Mat w;               // [N][K]
-    const uint4* xhi;      // [T][K/8] prepared activations
-    const uint4* xlo;
-    const float* xs;       // [T][K/64]
-    float* y;              // [T][ldy]
-    uint32_t T, ldy;
-    int accumulate;        // y += result instead of y = result
-};
+// Tile: a workgroup of 8 waves covers 64 rows x 256 / NMAT outputs of every
+// matrix; wave w takes rows 32 (w % 2) .. + 32 and outputs 64 (w / 2) /
+// NMAT .. (four 16-wide MFMA tiles per 16 rows in all).  The 64-row A tile
+// of each quant group (hi and lo planes, 16 KiB) is staged through LDS once
+// for the 8 waves, double-buffered with the next group's global loads;
+// every wave streams its own weight words one group ahead.  Per group and
+// 16-row slice the MFMA partial sums start from zero (two K-steps of 32,
+// hi then lo) and fold into the accumulator with the group's scale and
+// bias.
+//
+// Rows: dense (row m of A and Y), or grouped: a tile list names (group,
+// 64-row tile); list[group][m] is an entry e, A row e / div, Y row e.  The
+// routed-expert GEMMs group the (token, slot) entries e = t (k+1) + slot
+// by expert (gate/up read token t, down reads the entry's activation);
+// group == X.experts is the shared expert.
+//
+// Epilogues: PE_STORE (concatenated segments, each with its own output,
+// optional silu / 2 sigmoid of alpha v), PE_INJECT (hyper[t][g H + n] +=
+// v inj[t][g], inject, cpu.rs:971-979), PE_HC_UP (the four 16-wide tiles of
+// a wave are the hc streams of the same 16 outputs: mixed = (1/hc) sum_g
+// sigmoid(v_g) normed_g, cpu.rs:477-491), PE_SILU_MUL (NMAT 2:
+// silu(gate) * up, mlp, cpu.rs:981-992).
+constexpr int PF_WG = 512;  // threads per GEMM workgroup
+constexpr int PF_AROW = 9;  // uint4 per staged A row (8 + 1 pad: bank spread)
 
-__global__ void __launch_bounds__(256) k_pf_gemm(PfGemmArgs a) {
-    const int lane = threadIdx.x & 63, col = lane & 15, kq = lane >> 4;
-    const uint32_t N = a.w.out, K = a.w.in, G = K >> 6, KB = K >> 3;
-    const uint32_t n0 = blockIdx.x * 256 + wave_id() * 64, t0 = blockIdx.y * 64;
-    if (n0 >= N) return;
-    uint32_t nrow[4];
+CHK_DEV h8 pf_unpack(uint32_t w, const Q4Consts& qk) {
+    const uint32_t w8 = w >> 8;
+    const h2 p0 = __builtin_bit_cast(h2, (w & qk.m1) | qk.magic) - qk.off;
+    const h2 p1 = __builtin_bit_cast(h2, (w & qk.m2) | qk.magic) - qk.off;
+    const h2 p2 = __builtin_bit_cast(h2, (w8 & qk.m1) | qk.magic) - qk.off;
+    const h2 p3 = __builtin_bit_cast(h2, (w8 & qk.m2) | qk.magic) - qk.off;
+    return h8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+}
+
+template <int NMAT, int EPI>
+__global__ void __launch_bounds__(PF_WG) k_pf_gemm(PfGemmArgs a) {
+    constexpr int NJ = 4 / NMAT;  // 16-wide output tiles per matrix per wave
+    constexpr int NI = 2;         // 16-row slices per wave
+    __shared__ __align__(16) u32x4 sA[2][2][64 * PF_AROW];
+    __shared__ __align__(16) float sX[2][64];
+    const int tid = threadIdx.x, lane = tid & 63, col = lane & 15, kq = lane >> 4;
+    const uint32_t w = wave_id(), rh = w & 1, wn = w >> 1;
+    uint32_t grp = 0, mt = blockIdx.y;
+    if (a.list) {
+        if (blockIdx.y >= *a.ntiles) return;
+        const uint32_t tv = a.tiles[blockIdx.y];
+        grp = tv >> 16;
+        mt = tv & 0xffffu;
+    }
+    const uint32_t M = a.list ? a.count[grp] : a.M;
+    const uint32_t m0 = mt * 64;
+    if (m0 >= M) return;
+    const uint32_t* list = a.list ? a.list + (size_t)grp * a.cap : nullptr;
+    const uint32_t K = a.K, G = K >> 6, KB = K >> 3;
+
+    // ---- this lane's weight rows: one per (matrix, tile), as 32-bit
+    // element offsets from one workgroup-uniform base per array (the
+    // record of a routed expert, else the lowest segment matrix)
+    uint32_t nout[NJ];  // output index of tile j (PE_HC_UP: the output i)
+    uint32_t wo[NMAT][NJ], so[NMAT][NJ], bo[NMAT][NJ];
+    const bool expert = a.X.base && grp < a.X.experts;
+    const uint8_t* rec = a.X.base + ((size_t)a.record_layer * a.X.experts + grp) * a.X.stride;
+    const uint32_t* wb = expert ? reinterpret_cast<const uint32_t*>(rec) : a.wbase;
+    const uint16_t* sbase = expert ? reinterpret_cast<const uint16_t*>(rec) : a.sbase;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) nrow[j] = min(n0 + j * 16 + col, N - 1);
-    uint32_t trow[4];
+    for (int j = 0; j < NJ; ++j) {
+        uint32_t r;
+        if (EPI == PE_HC_UP) {
+            const uint32_t i = blockIdx.x * 64 + wn * 16 + col;
+            nout[j] = i;
+            r = min((uint32_t)j, a.hc - 1) * a.H + min(i, a.H - 1);
+        } else {
+            const uint32_t n = blockIdx.x * (256 / NMAT) + wn * (64 / NMAT) + j * 16 + col;
+            nout[j] = n;
+            r = min(n, a.N - 1);
+        }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) trow[i] = min(t0 + i * 16 + col, a.T - 1);
+        for (int q = 0; q < NMAT; ++q) {
+            if (expert) {
+                const int part = EPI == PE_SILU_MUL ? q : 2;
+                const uint64_t w0 = part == 0 ? a.X.gate_w : part == 1 ? a.X.up_w : a.X.down_w;
+                const uint64_t s0 = part == 0 ? a.X.gate_s : part == 1 ? a.X.up_s : a.X.down_s;
+                const uint64_t b0 = part == 0 ? a.X.gate_b : part == 1 ? a.X.up_b : a.X.down_b;
+                wo[q][j] = (uint32_t)(w0 / 4) + r * KB;
+                so[q][j] = (uint32_t)(s0 / 2) + r * G;
+                bo[q][j] = (uint32_t)(b0 / 2) + r * G;
+            } else {
+                // concatenated segments along n (PE_STORE), else matrix q
+                uint32_t mw = a.seg[q].wo, ms = a.seg[q].so, mb = a.seg[q].bo, rr = r;
+                if (EPI == PE_STORE) {
+#pragma unroll
+                    for (int sgi = 1; sgi < 4; ++sgi)
+                        if ((uint32_t)sgi < a.nseg && r >= a.seg[sgi].n0) {
+                            mw = a.seg[sgi].wo;
+                            ms = a.seg[sgi].so;
+                            mb = a.seg[sgi].bo;
+                            rr = r - a.seg[sgi].n0;
+                        }
+                }
+                wo[q][j] = mw + rr * KB;
+                so[q][j] = ms + rr * G;
+                bo[q][j] = mb + rr * G;
+            }
+        }
+    }
+
+    // ---- A staging: thread tid loads 8-block tid % 8 of row tid / 8 (hi,
+    // lo) and the group sum of row tid % 64
+    const uint32_t lrow = tid >> 3, lkb = tid & 7;
+    uint32_t arow_ld, arow_xs;
+    {
+        const uint32_t m = min(m0 + lrow, M - 1);
+        arow_ld = list ? list[m] / a.div : m;
+        const uint32_t mx = min(m0 + (tid & 63), M - 1);
+        arow_xs = list ? list[mx] / a.div : mx;
+    }
+    const u32x4* ghi = reinterpret_cast<const u32x4*>(a.xhi) + (size_t)arow_ld * KB + lkb;
+    const u32x4* glo = reinterpret_cast<const u32x4*>(a.xlo) + (size_t)arow_ld * KB + lkb;
+    const float* gxs = a.xs + (size_t)arow_xs * G;
+    // Software pipeline: the next group's A tile pieces and weight words
+    // load while this group computes (register slot = group % 2, a
+    // compile-time constant in the unrolled loop).  Every load is
+    // unconditional (past the last group it re-reads the last one), so the
+    // wait counters the compiler derives stay exact: a step waits only for
+    // the loads it consumes.
+    u32x4 rah[2], ral[2];
+    float rx[2];
+    u32x2 bw[2][NMAT][NJ];       // words 2 kq, 2 kq + 1 of the group: K-steps 0, 1
+    uint16_t bs[2][NMAT][NJ], bb[2][NMAT][NJ];  // bf16 scale, bias
+    auto fetch = [&](int slot, uint32_t g) __attribute__((always_inline)) {
+        rah[slot] = ghi[g * 8];
+        ral[slot] = glo[g * 8];
+        rx[slot] = gxs[g];
+#pragma unroll
+        for (int q = 0; q < NMAT; ++q)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                bw[slot][q][j] = *reinterpret_cast<const u32x2*>(wb + wo[q][j] + g * 8 + kq * 2);
+                bs[slot][q][j] = sbase[so[q][j] + g];
+                bb[slot][q][j] = sbase[bo[q][j] + g];
+            }
+    };
+    auto a_store = [&](int slot, uint32_t buf) __attribute__((always_inline)) {
+        sA[buf][0][lrow * PF_AROW + lkb] = rah[slot];
+        sA[buf][1][lrow * PF_AROW + lkb] = ral[slot];
+        sX[buf][tid & 63] = rx[slot];  // eight identical writes per row: no branch
+    };
+
+    f4 acc[NMAT][NI][NJ];
+#pragma unroll
+    for (int q = 0; q < NMAT; ++q)
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) acc[q][i][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     const Q4Consts qk;
+
+    // one quant group g (LDS buffer and register slot S = g % 2)
+    auto step = [&](auto sc_, uint32_t g) __attribute__((always_inline)) {
+        constexpr int S = decltype(sc_)::value;
+        fetch(S ^ 1, min(g + 1, G - 1));
+        // K-step s of lane quarter kq takes the group's word 2 kq + s (A
+        // staged in the same 8-block order)
+        h8 bq[NMAT][NJ][2];
+#pragma unroll
+        for (int q = 0; q < NMAT; ++q)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                bq[q][j][0] = pf_unpack(bw[S][q][j].x, qk);
+                bq[q][j][1] = pf_unpack(bw[S][q][j].y, qk);
+            }
+        float sc[NMAT][NJ], bi[NMAT][NJ];
+#pragma unroll
+        for (int q = 0; q < NMAT; ++q)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                sc[q][j] = bf16f(bs[S][q][j]);
+                bi[q][j] = bf16f(bb[S][q][j]);
+            }
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const uint32_t row16 = rh * 32 + i * 16;
+            f4 accg[NMAT][NJ];
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                const uint32_t ai = (row16 + col) * PF_AROW + kq * 2 + s;
+                const h8 ah = __builtin_bit_cast(h8, sA[S][0][ai]);
+                const h8 al = __builtin_bit_cast(h8, sA[S][1][ai]);
+#pragma unroll
+                for (int q = 0; q < NMAT; ++q)
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j) {
+                        const f4 c0 = s == 0 ? f4{0.0f, 0.0f, 0.0f, 0.0f} : accg[q][j];
+                        accg[q][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq[q][j][s], c0, 0, 0, 0);
+                        accg[q][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bq[q][j][s], accg[q][j], 0, 0, 0);
+                    }
+            }
+            const float4 xv = *reinterpret_cast<const float4*>(&sX[S][row16 + kq * 4]);
+            const float xr[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+            for (int q = 0; q < NMAT; ++q)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[q][i][j][r] += sc[q][j] * accg[q][j][r] + bi[q][j] * xr[r];
+        }
+        // A of group g + 1 into the other buffer, read by nobody since the
+        // last barrier
+        a_store(S ^ 1, S ^ 1);
+        __syncthreads();
+    };
+
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    fetch(0, 0);
+    a_store(0, 0);
+    __syncthreads();
+    uint32_t g = 0;
+    for (; g + 2 <= G; g += 2) {
+        step(I0{}, g);
+        step(I1{}, g + 1);
+    }
+    if (g < G) step(I0{}, g);
+
+    // ---- epilogue
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t m = m0 + rh * 32 + i * 16 + kq * 4 + r;
+            if (m >= M) continue;
+            const uint32_t yrow = list ? list[m] : m;
+            if (EPI == PE_HC_UP) {
+                const uint32_t o = nout[0];
+                if (o >= a.H) continue;
+                const float* hy = a.hyper + (size_t)m * a.hc * a.H;
+                float sum = 0.0f;
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    if ((uint32_t)j >= a.hc) continue;
+                    const size_t k = (size_t)j * a.H + o;
+                    sum += sigmoidf_(acc[0][i][j][r]) * (hy[k] * a.inv[(size_t)m * a.hc + j] * bf16f(a.norm[k]));
+                }
+                a.out[(size_t)m * a.H + o] = sum / (float)a.hc;
+                continue;
+            }
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                const uint32_t n = nout[j];
+                if (n >= a.N) continue;
+                if (EPI == PE_SILU_MUL) {
+                    a.seg[0].y[(size_t)yrow * a.seg[0].ldy + n] = siluf_(acc[0][i][j][r]) * acc[1][i][j][r];
+                } else if (EPI == PE_INJECT) {
+                    const float v = acc[0][i][j][r];
+                    float* hy = a.hyper + (size_t)m * a.hc * a.H + n;
+                    for (uint32_t g = 0; g < a.hc; ++g) hy[(size_t)g * a.H] += v * a.inj[(size_t)m * a.hc + g];
+                } else {
+                    PfSeg sg = a.seg[0];
+#pragma unroll
+                    for (int sgi = 1; sgi < 4; ++sgi)
+                        if ((uint32_t)sgi < a.nseg && n >= a.seg[sgi].n0) sg = a.seg[sgi];
+                    float v = acc[0][i][j][r];
+                    if (sg.act == PA_SILU) v = siluf_(v * a.alpha);
+                    else if (sg.act == PA_2SIG) v = 2.0f * sigmoidf_(v * a.alpha);
+                    sg.y[(size_t)yrow * sg.ldy + (n - sg.n0)] = v;
+                }
+            }
+        }
+}
+
+// ------------------------------------------------------------- router
+// logits[t][e] = W_r[e] . x_t (bf16 [E][H], f32 sums) and the shared-expert
+// gate logit as output E (moe, cpu.rs:506-508, 534-535), on
+// v_mfma_f32_16x16x32_bf16 with x split into three bf16 terms (natural k
+// order): every product of bf16 values is exact in f32, so the logits keep
+// f32-grade accuracy and the top-k cut sees what an f32 dot would.
+// A wave: 64 rows x 64 outputs; a workgroup: 64 rows x 256.
+__global__ void __launch_bounds__(256) k_pf_router(const uint16_t* __restrict__ router,
+                                                   const uint16_t* __restrict__ shared_gate,
+                                                   const uint4* __restrict__ bhi, const uint4* __restrict__ bmid,
+                                                   const uint4* __restrict__ blo, float* __restrict__ logits,
+                                                   float* __restrict__ sg, uint32_t T, uint32_t E, uint32_t H) {
+    const int lane = threadIdx.x & 63, col = lane & 15, kq = lane >> 4;
+    const uint32_t m0 = blockIdx.y * 64, n0 = blockIdx.x * 256 + wave_id() * 64, KB = H >> 3;
+    const uint4* bp[4];
+    uint32_t nn[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        nn[j] = n0 + j * 16 + col;
+        const uint32_t r = min(nn[j], E);
+        bp[j] = reinterpret_cast<const uint4*>(r < E ? router + (size_t)r * H : shared_gate);
+    }
+    const uint4* ah[4];
+    const uint4* am[4];
+    const uint4* al[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t m = min(m0 + i * 16 + col, T - 1);
+        ah[i] = bhi + (size_t)m * KB;
+        am[i] = bmid + (size_t)m * KB;
+        al[i] = blo + (size_t)m * KB;
+    }
     f4 acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    for (uint32_t g = 0; g < G; ++g) {
-        f4 accg[4][4];
+    for (uint32_t k = 0; k < KB; k += 4) {
+        b8 bq[4];
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            const uint32_t kb = g * 8 + s * 4 + kq;  // this lane's 8-block
-            h8 bq[4];
+        for (int j = 0; j < 4; ++j) bq[j] = __builtin_bit_cast(b8, bp[j][k + kq]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const b8 xh = __builtin_bit_cast(b8, ah[i][k + kq]);
+            const b8 xm = __builtin_bit_cast(b8, am[i][k + kq]);
+            const b8 xl = __builtin_bit_cast(b8, al[i][k + kq]);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const uint32_t w = a.w.w[(size_t)nrow[j] * KB + kb], w8 = w >> 8;
-                const h2 p0 = __builtin_bit_cast(h2, (w & qk.m1) | qk.magic) - qk.off;
-                const h2 p1 = __builtin_bit_cast(h2, (w & qk.m2) | qk.magic) - qk.off;
-                const h2 p2 = __builtin_bit_cast(h2, (w8 & qk.m1) | qk.magic) - qk.off;
-                const h2 p3 = __builtin_bit_cast(h2, (w8 & qk.m2) | qk.magic) - qk.off;
-                bq[j] = h8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, bq[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xm, bq[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, bq[j], acc[i][j], 0, 0, 0);
             }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const h8 ah = __builtin_bit_cast(h8, a.xhi[(size_t)trow[i] * KB + kb]);
-                const h8 al = __builtin_bit_cast(h8, a.xlo[(size_t)trow[i] * KB + kb]);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const f4 c0 = s == 0 ? f4{0.0f, 0.0f, 0.0f, 0.0f} : accg[i][j];
-                    accg[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq[j], c0, 0, 0, 0);
-                    accg[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bq[j], accg[i][j], 0, 0, 0);
-                }
-            }
-        }
-        // fold: D lane (col = output n0 + 16 j + col, rows t0 + 16 i + 4 kq + r)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float sc = bf16f(a.w.s[(size_t)nrow[j] * G + g]), bi = bf16f(a.w.b[(size_t)nrow[j] * G + g]);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const uint32_t t = min(t0 + i * 16 + kq * 4 + r, a.T - 1);
-                    acc[i][j][r] += sc * accg[i][j][r] + bi * a.xs[(size_t)t * G + g];
-                }
         }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t n = n0 + j * 16 + col;
-            if (n >= N) continue;
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t m = m0 + i * 16 + kq * 4 + r;
+            if (m >= T) continue;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t t = t0 + i * 16 + kq * 4 + r;
-                if (t < a.T) {
-                    float* yp = a.y + (size_t)t * a.ldy + n;
-                    *yp = a.accumulate ? *yp + acc[i][j][r] : acc[i][j][r];
-                }
+            for (int j = 0; j < 4; ++j) {
+                if (nn[j] < E) logits[(size_t)m * E + nn[j]] = acc[i][j][r];
+                else if (nn[j] == E) sg[m] = acc[i][j][r];
             }
         }
 }
 
+// ------------------------------------------------------------ routing
+// One wave per token: softmax top-k (route_row) and the renormalised
+// weights in rank order (cpu.rs:508-525).
+__global__ void __launch_bounds__(256) k_pf_route(const float* __restrict__ logits, uint32_t T, uint32_t E,
+                                                  uint32_t topk, int norm_topk, uint32_t* __restrict__ ids,
+                                                  float* __restrict__ wts) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t t = blockIdx.x * (CHK_WG >> 6) + wave_id();
+    if (t >= T) return;
+    uint32_t my_id;
+    float my_p;
+    route_row(logits + (size_t)t * E, E, topk, lane, nullptr, my_id, my_p);
+    float topsum = 0.0f;
+    for (uint32_t r = 0; r < topk; ++r) topsum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_p), (int)r));
+    if ((uint32_t)lane < topk) {
+        ids[(size_t)t * topk + lane] = my_id;
+        wts[(size_t)t * topk + lane] = norm_topk ? my_p / topsum : my_p;
+    }
+}
+
+// Entries grouped by expert (the CSR lists of gpu/prefill/experts.rs:29-137):
+// list[e][0..count[e]) holds the entries t (k+1) + slot routed to e (any
+// order: every GEMM row is independent), list[E] every token's shared
+// slot t (k+1) + k, and tiles[] the (group, 64-row tile) pairs in group
+// order, *ntiles of them.  One workgroup.
+__global__ void __launch_bounds__(256) k_pf_group(const uint32_t* __restrict__ ids, uint32_t T, uint32_t topk,
+                                                  uint32_t E, uint32_t cap, uint32_t* __restrict__ list,
+                                                  uint32_t* __restrict__ count, uint32_t* __restrict__ tiles,
+                                                  uint32_t* __restrict__ ntiles) {
+    __shared__ uint32_t cnt[513];
+    __shared__ uint32_t wsum[4];
+    const uint32_t tau = threadIdx.x, lane = tau & 63, wv = tau >> 6;
+    for (uint32_t e = tau; e <= E; e += CHK_WG) cnt[e] = 0;
+    __syncthreads();
+    const uint32_t slots = topk + 1;
+    for (uint32_t i = tau; i < T * topk; i += CHK_WG) {
+        const uint32_t t = i / topk, r = i % topk;
+        const uint32_t e = min(ids[i], E - 1);
+        const uint32_t p = atomicAdd(&cnt[e], 1u);
+        list[(size_t)e * cap + p] = t * slots + r;
+    }
+    for (uint32_t t = tau; t < T; t += CHK_WG) list[(size_t)E * cap + t] = t * slots + topk;
+    __syncthreads();
+    if (tau == 0) cnt[E] = T;
+    __syncthreads();
+    // tiles per group, 3 groups per thread (E + 1 <= 768), block prefix sum
+    uint32_t nt[3], mine = 0;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const uint32_t e = tau * 3 + k;
+        nt[k] = e <= E ? (cnt[e] + 63) / 64 : 0;
+        mine += nt[k];
+        if (e <= E) count[e] = cnt[e];
+    }
+    uint32_t incl = mine;
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t o = __shfl_up(incl, d, 64);
+        if ((int)lane >= d) incl += o;
+    }
+    if (lane == 63) wsum[wv] = incl;
+    __syncthreads();
+    uint32_t off = incl - mine;
+    for (uint32_t k = 0; k < wv; ++k) off += wsum[k];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const uint32_t e = tau * 3 + k;
+        for (uint32_t q = 0; q < nt[k]; ++q) tiles[off + q] = e << 16 | q;
+        off += nt[k];
+    }
+    if (tau == CHK_WG - 1) *ntiles = off;
+}
+
+// out[t][n] = sum_r w[t][r] yd[t][r][n] + sigmoid(sg[t]) yd[t][k][n]
+// (cpu.rs:527-540), then hyper[t][g H + n] += out inj[t][g].
+__global__ void __launch_bounds__(256) k_pf_moe_combine(const float* __restrict__ yd, const float* __restrict__ wts,
+                                                        const float* __restrict__ sg, const float* __restrict__ inj,
+                                                        float* __restrict__ hyper, uint32_t H, uint32_t topk,
+                                                        uint32_t hc) {
+    const uint32_t t = blockIdx.y, n = blockIdx.x * CHK_WG + threadIdx.x;
+    if (n >= H) return;
+    const uint32_t slots = topk + 1;
+    const float* y = yd + (size_t)t * slots * H + n;
+    float out = 0.0f;
+    for (uint32_t r = 0; r < topk; ++r) out += wts[(size_t)t * topk + r] * y[(size_t)r * H];
+    out += sigmoidf_(sg[t]) * y[(size_t)topk * H];
+    float* hy = hyper + (size_t)t * hc * H + n;
+    for (uint32_t g = 0; g < hc; ++g) hy[(size_t)g * H] += out * inj[(size_t)t * hc + g];
+}
+
+// ------------------------------------------------------------- embed
+// embed.dequant_row replicated into the hc streams (cpu.rs:399-407), with
+// explicitly rounded mul/add as on the decode path.
+__global__ void __launch_bounds__(256) k_pf_embed(const uint32_t* __restrict__ tokens, Q4Mat emb,
+                                                  float* __restrict__ hyper, uint32_t H, uint32_t hc) {
+    const uint32_t t = blockIdx.y, i = blockIdx.x * CHK_WG + threadIdx.x;
+    if (i >= H) return;
+    const uint32_t tok = tokens[t];
+    const uint32_t word = emb.w[(size_t)tok * (H / 8) + i / 8];
+    const uint32_t g = i / 64;
+    const float s = bf16f(emb.s[(size_t)tok * (H / 64) + g]), b = bf16f(emb.b[(size_t)tok * (H / 64) + g]);
+    const float q = (float)((word >> (4 * (i % 8))) & 15u);
+    const float e = __fadd_rn(__fmul_rn(s, q), b);
+    for (uint32_t k = 0; k < hc; ++k) hyper[(size_t)t * hc * H + k * H + i] = e;
+}
+
+// ----------------------------------------------------------- DeltaNet
+// Causal conv over time (cpu.rs:1067-1085) + silu for every channel, then
+// the L2 norms of the q (times dk^-1/2) and k heads (eps 1e-6,
+// cpu.rs:745-760).  One wave per (row, 128-channel head span), lane l
+// owning channels 2l, 2l + 1; the window reaches into the layer's
+// history for the first rows.
+__global__ void __launch_bounds__(256) k_pf_dn_conv(PfDnArgs a) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t t = blockIdx.y, span = blockIdx.x * 4 + wave_id();
+    const uint32_t c0 = span * 128 + lane * 2, km1 = a.ck - 1;
+    if (span * 128 >= a.conv_dim) return;
+    float o[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const uint32_t c = min(c0 + e, a.conv_dim - 1);
+        const uint16_t* cw = a.conv_w + (size_t)c * a.ck;
+        float s = bf16f(cw[km1]) * a.raw[(size_t)t * a.ld_raw + c];
+        for (uint32_t j = 0; j < km1; ++j) {
+            const int tau = (int)t - (int)km1 + (int)j;
+            const float x = tau >= 0 ? a.raw[(size_t)tau * a.ld_raw + c] : a.hist[(size_t)c * km1 + (tau + (int)km1)];
+            s += bf16f(cw[j]) * x;
+        }
+        o[e] = siluf_(s);
+    }
+    if (span < 2 * a.nk) {
+        const float sq = wave_sum(o[0] * o[0] + o[1] * o[1]);
+        const float inv = 1.0f / sqrtf(sq + 1e-6f);
+        o[0] *= inv;
+        o[1] *= inv;
+        if (span < a.nk) {
+            o[0] *= a.qscale;
+            o[1] *= a.qscale;
+        }
+    }
+    if (c0 < a.conv_dim) a.conv[(size_t)t * a.conv_dim + c0] = o[0];
+    if (c0 + 1 < a.conv_dim) a.conv[(size_t)t * a.conv_dim + c0 + 1] = o[1];
+}
+
+// The new conv history (the last ck-1 raw inputs, reaching into the old
+// history when T < ck-1) and the per-row decay / beta of every value head:
+// g = -exp(A_log) softplus(a + dt_bias), decay = e^g, beta = sigmoid(b)
+// (cpu.rs:775-777).  Runs after k_pf_dn_conv, which reads the old history.
+__global__ void __launch_bounds__(256) k_pf_dn_misc(PfDnArgs a) {
+    const uint32_t i = blockIdx.x * CHK_WG + threadIdx.x, km1 = a.ck - 1;
+    if (i < a.conv_dim) {
+        float nh[8];
+#pragma unroll
+        for (uint32_t h = 0; h < 8; ++h) {
+            if (h >= km1) break;
+            const int tau = (int)a.T - (int)km1 + (int)h;
+            nh[h] = tau >= 0 ? a.raw[(size_t)tau * a.ld_raw + i] : a.hist[(size_t)i * km1 + (tau + (int)km1)];
+        }
+#pragma unroll
+        for (uint32_t h = 0; h < 8; ++h) {
+            if (h >= km1) break;
+            a.hist[(size_t)i * km1 + h] = nh[h];
+        }
+        return;
+    }
+    const uint32_t j = i - a.conv_dim;
+    if (j >= a.T * a.nv) return;
+    const uint32_t t = j / a.nv, hv = j % a.nv;
+    const float av = a.a_raw[(size_t)t * a.ld_ab + hv], bv = a.b_raw[(size_t)t * a.ld_ab + hv];
+    const float gg = -expf(bf16f(a.a_log[hv])) * softplusf_(av + bf16f(a.dt_bias[hv]));
+    a.decay[(size_t)t * a.nv + hv] = expf(gg);
+    a.beta[(size_t)t * a.nv + hv] = sigmoidf_(bv);
+}
+
+// The gated delta rule over the chunk's rows in order (cpu.rs:745-812; the
+// reference prefill runs the same sequential recurrence, deltanet.rs:80-95).
+// One wave per (value head, 4 value columns): lane (c, p) holds keys
+// 8p..8p+7 of column c of the head's fp32 state (kept transposed, [dv][dk])
+// in VGPRs.  With S the state before row t, the row needs three 16-lane
+// dot products that do not depend on each other, so they reduce together:
+//   sk = S^T k, sq = S^T q, kq = k . q;
+//   delta = beta (v - decay sk), y = decay sq + delta kq,
+//   S <- decay S + k delta^T.
+// The q, k, v, decay, beta of row t + PF_SCAN_AHEAD load while row t
+// computes.
+constexpr int PF_SCAN_AHEAD = 4;
+
+__global__ void __launch_bounds__(64) k_pf_dn_scan(PfDnArgs a) {
+    constexpr int DK = 128, KPL = 8, D = PF_SCAN_AHEAD;
+    const int lane = threadIdx.x, c = lane >> 4, p = lane & 15;
+    const uint32_t blocks = a.dv / 4;
+    const uint32_t hv = blockIdx.x / blocks, iv = (blockIdx.x % blocks) * 4 + c;
+    const uint32_t hk = hv / (a.nv / a.nk);
+    float S[KPL];
+    float* sp = a.state + ((size_t)hv * a.dv + iv) * DK + p * KPL;
+    {
+        const float4 s0 = *reinterpret_cast<const float4*>(sp), s1 = *reinterpret_cast<const float4*>(sp + 4);
+        S[0] = s0.x; S[1] = s0.y; S[2] = s0.z; S[3] = s0.w; S[4] = s1.x; S[5] = s1.y; S[6] = s1.z; S[7] = s1.w;
+    }
+    const float* qb = a.conv + hk * DK + p * KPL;
+    const float* kb = a.conv + a.qk_dim + hk * DK + p * KPL;
+    const float* vb = a.conv + 2 * a.qk_dim + hv * a.dv + iv;
+    float Q[D][KPL], Kk[D][KPL], V[D], DC[D], BT[D];
+    auto load = [&](int d, uint32_t t) __attribute__((always_inline)) {
+        const uint32_t tt = min(t, a.T - 1);
+        const size_t ro = (size_t)tt * a.conv_dim;
+        const float4 q0 = *reinterpret_cast<const float4*>(qb + ro), q1 = *reinterpret_cast<const float4*>(qb + ro + 4);
+        const float4 k0 = *reinterpret_cast<const float4*>(kb + ro), k1 = *reinterpret_cast<const float4*>(kb + ro + 4);
+        Q[d][0] = q0.x; Q[d][1] = q0.y; Q[d][2] = q0.z; Q[d][3] = q0.w;
+        Q[d][4] = q1.x; Q[d][5] = q1.y; Q[d][6] = q1.z; Q[d][7] = q1.w;
+        Kk[d][0] = k0.x; Kk[d][1] = k0.y; Kk[d][2] = k0.z; Kk[d][3] = k0.w;
+        Kk[d][4] = k1.x; Kk[d][5] = k1.y; Kk[d][6] = k1.z; Kk[d][7] = k1.w;
+        V[d] = vb[ro];
+        DC[d] = a.decay[(size_t)tt * a.nv + hv];
+        BT[d] = a.beta[(size_t)tt * a.nv + hv];
+    };
+#pragma unroll
+    for (int d = 0; d < D; ++d) load(d, d);
+    float* yout = a.y + hv * a.dv + iv;
+    for (uint32_t t0 = 0; t0 < a.T; t0 += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            const uint32_t t = t0 + d;
+            if (t >= a.T) break;
+            float sk = 0.0f, sq = 0.0f, kq = 0.0f;
+#pragma unroll
+            for (int j = 0; j < KPL; ++j) {
+                sk += S[j] * Kk[d][j];
+                sq += S[j] * Q[d][j];
+                kq += Kk[d][j] * Q[d][j];
+            }
+            sk = group_sum<16>(sk);
+            sq = group_sum<16>(sq);
+            kq = group_sum<16>(kq);
+            const float dec = DC[d];
+            const float delta = BT[d] * (V[d] - dec * sk);
+            const float y = dec * sq + delta * kq;
+#pragma unroll
+            for (int j = 0; j < KPL; ++j) S[j] = dec * S[j] + Kk[d][j] * delta;
+            if (p == 0) yout[(size_t)t * a.v_dim] = y;
+            load(d, t + D);
+        }
+    }
+    *reinterpret_cast<float4*>(sp) = make_float4(S[0], S[1], S[2], S[3]);
+    *reinterpret_cast<float4*>(sp + 4) = make_float4(S[4], S[5], S[6], S[7]);
+}
+
 // -------------------------------------------------------------- launchers
+
+void launch_pf_prep(const PfPrepArgs& a, hipStream_t st) {
+    const uint64_t n = (uint64_t)a.T * (a.K >> 3);
+    if (!n) return;
+    if (a.K % 64) throw std::runtime_error("prefill operands need K a multiple of 64");
+    const uint32_t grid = (uint32_t)((n + CHK_WG - 1) / CHK_WG);
+    if (!a.z) {
+        k_pf_prep<PP_PLAIN, 1><<<grid, CHK_WG, 0, st>>>(a);
+        return;
+    }
+    switch (a.dv) {
+    case 64: k_pf_prep<PP_DN_GATE, 8><<<grid, CHK_WG, 0, st>>>(a); break;
+    case 128: k_pf_prep<PP_DN_GATE, 16><<<grid, CHK_WG, 0, st>>>(a); break;
+    case 256: k_pf_prep<PP_DN_GATE, 32><<<grid, CHK_WG, 0, st>>>(a); break;
+    default: throw std::runtime_error("prefill gated norm needs a value head dim of 64, 128 or 256");
+    }
+}
 
 void launch_pf_xprep(const float* x, uint32_t ldx, uint32_t T, uint32_t K, uint4* hi, uint4* lo, float* xs,
                      hipStream_t st) {
-    const uint64_t n = (uint64_t)T * (K >> 3);
-    if (!n) return;
-    k_pf_xprep<<<(uint32_t)((n + CHK_WG - 1) / CHK_WG), CHK_WG, 0, st>>>(x, ldx, T, K, hi, lo, xs);
+    PfPrepArgs a{};
+    a.x = x;
+    a.ldx = ldx;
+    a.T = T;
+    a.K = K;
+    a.hi = hi;
+    a.lo = lo;
+    a.xs = xs;
+    launch_pf_prep(a, st);
+}
+
+void launch_pf_hc_prep(const float* hyper, const uint16_t* norm, uint32_t H, uint32_t hc, float eps, float* inv,
+                       uint4* hi, uint4* lo, float* xs, uint32_t T, hipStream_t st) {
+    if (H > 4096 || hc > 4 || H % 64) throw std::runtime_error("prefill hyper-connection norm needs hidden <= 4096, hc <= 4");
+    if (T) k_pf_hc_prep<<<T, CHK_WG, 0, st>>>(hyper, norm, H, hc, eps, inv, hi, lo, xs);
+}
+
+void launch_pf_gemm_args(const PfGemmArgs& args, int epi, uint32_t grid_y, hipStream_t st) {
+    if (args.K % 64 || !args.K) throw std::runtime_error("prefill GEMM needs K a multiple of 64");
+    if (!grid_y) return;
+    // 32-bit element offsets of the dense matrices from the lowest base
+    PfGemmArgs a = args;
+    const int nm = std::max<int>(a.nseg, epi == PE_SILU_MUL ? 2 : 1);
+    uintptr_t wmin = UINTPTR_MAX, smin = UINTPTR_MAX;
+    for (int q = 0; q < nm; ++q) {
+        wmin = std::min(wmin, (uintptr_t)a.seg[q].m.w);
+        smin = std::min({smin, (uintptr_t)a.seg[q].m.s, (uintptr_t)a.seg[q].m.b});
+    }
+    a.wbase = (const uint32_t*)wmin;
+    a.sbase = (const uint16_t*)smin;
+    for (int q = 0; q < nm; ++q) {
+        const uint64_t w = ((uintptr_t)a.seg[q].m.w - wmin) / 4, s = ((uintptr_t)a.seg[q].m.s - smin) / 2,
+                       b = ((uintptr_t)a.seg[q].m.b - smin) / 2;
+        const uint64_t rows = a.seg[q].m.out;
+        if (w + rows * (a.K / 8) > UINT32_MAX || std::max(s, b) + rows * (a.K / 64) > UINT32_MAX)
+            throw std::runtime_error("prefill GEMM weights span more than 32-bit offsets reach");
+        a.seg[q].wo = (uint32_t)w;
+        a.seg[q].so = (uint32_t)s;
+        a.seg[q].bo = (uint32_t)b;
+    }
+    switch (epi) {
+    case PE_STORE: k_pf_gemm<1, PE_STORE><<<dim3((a.N + 255) / 256, grid_y), PF_WG, 0, st>>>(a); break;
+    case PE_INJECT: k_pf_gemm<1, PE_INJECT><<<dim3((a.N + 255) / 256, grid_y), PF_WG, 0, st>>>(a); break;
+    case PE_HC_UP:
+        if (a.hc > 4) throw std::runtime_error("prefill mix needs hc <= 4");
+        k_pf_gemm<1, PE_HC_UP><<<dim3((a.H + 63) / 64, grid_y), PF_WG, 0, st>>>(a);
+        break;
+    default: k_pf_gemm<2, PE_SILU_MUL><<<dim3((a.N + 127) / 128, grid_y), PF_WG, 0, st>>>(a); break;
+    }
 }
 
 void launch_pf_gemm(const Q4Mat& w, const uint4* xhi, const uint4* xlo, const float* xs, float* y, uint32_t T,
-                    uint32_t ldy, bool accumulate, hipStream_t st) {
-    if (w.in % 64) throw std::runtime_error("prefill GEMM needs K a multiple of 64");
-    if (!T) return;
-    PfGemmArgs a{w, xhi, xlo, xs, y, T, ldy, accumulate ? 1 : 0};
-    dim3 grid((w.out + 255) / 256, (T + 63) / 64);
-    k_pf_gemm<<<grid, CHK_WG, 0, st>>>(a);
+                    uint32_t ldy, hipStream_t st) {
+    PfGemmArgs a{};
+    a.seg[0] = PfSeg{w, y, ldy, 0, PA_NONE};
+    a.nseg = 1;
+    a.N = w.out;
+    a.K = w.in;
+    a.M = T;
+    a.xhi = xhi;
+    a.xlo = xlo;
+    a.xs = xs;
+    launch_pf_gemm_args(a, PE_STORE, (T + 63) / 64, st);
+}
+
+void launch_pf_router(const uint16_t* router, const uint16_t* shared_gate, const uint4* bhi, const uint4* bmid,
+                      const uint4* blo, float* logits, float* sg, uint32_t T, uint32_t E, uint32_t H, hipStream_t st) {
+    if (H % 32) throw std::runtime_error("router width must be a multiple of 32");
+    if (T)
+        k_pf_router<<<dim3((E + 1 + 255) / 256, (T + 63) / 64), CHK_WG, 0, st>>>(router, shared_gate, bhi, bmid, blo,
+                                                                                 logits, sg, T, E, H);
+}
+
+void launch_pf_route(const float* logits, uint32_t T, uint32_t E, uint32_t topk, int norm_topk, uint32_t* ids,
+                     float* wts, hipStream_t st) {
+    if (T) k_pf_route<<<(T + 3) / 4, CHK_WG, 0, st>>>(logits, T, E, topk, norm_topk, ids, wts);
+}
+
+void launch_pf_group(const uint32_t* ids, uint32_t T, uint32_t topk, uint32_t E, uint32_t cap, uint32_t* list,
+                     uint32_t* count, uint32_t* tiles, uint32_t* ntiles, hipStream_t st) {
+    if (E + 1 > 513) throw std::runtime_error("prefill grouping supports at most 512 experts");
+    k_pf_group<<<1, CHK_WG, 0, st>>>(ids, T, topk, E, cap, list, count, tiles, ntiles);
+}
+
+uint32_t pf_tile_bound(uint32_t T, uint32_t topk, uint32_t E) {
+    return (T * topk + 63) / 64 + E + (T + 63) / 64 + 1;
+}
+
+void launch_pf_moe_combine(const float* yd, const float* wts, const float* sg, const float* inj, float* hyper,
+                           uint32_t T, uint32_t H, uint32_t topk, uint32_t hc, hipStream_t st) {
+    if (T) k_pf_moe_combine<<<dim3((H + 255) / 256, T), CHK_WG, 0, st>>>(yd, wts, sg, inj, hyper, H, topk, hc);
+}
+
+void launch_pf_embed(const uint32_t* tokens, const Q4Mat& emb, float* hyper, uint32_t H, uint32_t hc, uint32_t T,
+                     hipStream_t st) {
+    if (T) k_pf_embed<<<dim3((H + 255) / 256, T), CHK_WG, 0, st>>>(tokens, emb, hyper, H, hc);
+}
+
+void launch_pf_dn(const PfDnArgs& a, hipStream_t st) {
+    if (!a.T) return;
+    if (a.ck < 2 || a.ck > 9) throw std::runtime_error("conv kernel 2..=9");
+    if (a.dv % 4) throw std::runtime_error("value head dim must be a multiple of 4");
+    const uint32_t spans = (a.conv_dim + 127) / 128;
+    k_pf_dn_conv<<<dim3((spans + 3) / 4, a.T), CHK_WG, 0, st>>>(a);
+    const uint32_t n = a.conv_dim + a.T * a.nv;
+    k_pf_dn_misc<<<(n + CHK_WG - 1) / CHK_WG, CHK_WG, 0, st>>>(a);
+    k_pf_dn_scan<<<a.nv * (a.dv / 4), 64, 0, st>>>(a);
 }
 
 }  // namespace chk
