@@ -218,12 +218,18 @@ CHK_DEV h8 pf_unpack(uint32_t w, const Q4Consts& qk) {
     return h8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
 }
 
-template <int NMAT, int EPI>
+// SBL: the scales and biases of the workgroup's 256 weight rows are staged
+// through LDS in blocks of 8 groups (one 16-byte load per thread per block,
+// interleaved into (scale | bias << 16) words), instead of two 2-byte loads
+// per lane, tile and group; it needs G % 8 == 0 and 16-byte aligned rows.
+template <int NMAT, int EPI, bool SBL>
 __global__ void __launch_bounds__(PF_WG) k_pf_gemm(PfGemmArgs a) {
     constexpr int NJ = 4 / NMAT;  // 16-wide output tiles per matrix per wave
     constexpr int NI = 2;         // 16-row slices per wave
+    constexpr int SBR = 9;        // words per staged scale row (8 groups + pad)
     __shared__ __align__(16) u32x4 sA[2][2][64 * PF_AROW];
     __shared__ __align__(16) float sX[2][64];
+    __shared__ uint32_t sSB[SBL ? 2 : 1][SBL ? 256 * SBR : 1];
     const int tid = threadIdx.x, lane = tid & 63, col = lane & 15, kq = lane >> 4;
     const uint32_t w = wave_id(), rh = w & 1, wn = w >> 1;
     uint32_t grp = 0, mt = blockIdx.y;
@@ -239,55 +245,68 @@ __global__ void __launch_bounds__(PF_WG) k_pf_gemm(PfGemmArgs a) {
     const uint32_t* list = a.list ? a.list + (size_t)grp * a.cap : nullptr;
     const uint32_t K = a.K, G = K >> 6, KB = K >> 3;
 
-    // ---- this lane's weight rows: one per (matrix, tile), as 32-bit
-    // element offsets from one workgroup-uniform base per array (the
-    // record of a routed expert, else the lowest segment matrix)
-    uint32_t nout[NJ];  // output index of tile j (PE_HC_UP: the output i)
-    uint32_t wo[NMAT][NJ], so[NMAT][NJ], bo[NMAT][NJ];
+    // ---- weight rows as 32-bit element offsets from one workgroup-uniform
+    // base per array (the record of a routed expert, else the lowest
+    // segment matrix).  Local row lr = ((wn NMAT + q) NJ + j) 16 + col of the
+    // workgroup's 256 is matrix q, tile j of wave column wn.
     const bool expert = a.X.base && grp < a.X.experts;
     const uint8_t* rec = a.X.base + ((size_t)a.record_layer * a.X.experts + grp) * a.X.stride;
     const uint32_t* wb = expert ? reinterpret_cast<const uint32_t*>(rec) : a.wbase;
     const uint16_t* sbase = expert ? reinterpret_cast<const uint16_t*>(rec) : a.sbase;
+    auto out_of = [&](uint32_t wn_, int j, uint32_t col_) __attribute__((always_inline)) -> uint32_t {
+        return EPI == PE_HC_UP ? blockIdx.x * 64 + wn_ * 16 + col_
+                               : blockIdx.x * (256 / NMAT) + wn_ * (64 / NMAT) + j * 16 + col_;
+    };
+    auto row_of = [&](uint32_t wn_, int j, uint32_t col_) __attribute__((always_inline)) -> uint32_t {
+        const uint32_t o = out_of(wn_, j, col_);
+        return EPI == PE_HC_UP ? min((uint32_t)j, a.hc - 1) * a.H + min(o, a.H - 1) : min(o, a.N - 1);
+    };
+    // offsets (words, scales, biases) of row r of matrix q
+    auto offs = [&](int q, uint32_t r, uint32_t& ow, uint32_t& os, uint32_t& ob) __attribute__((always_inline)) {
+        if (expert) {
+            const int part = EPI == PE_SILU_MUL ? q : 2;
+            const uint64_t w0 = part == 0 ? a.X.gate_w : part == 1 ? a.X.up_w : a.X.down_w;
+            const uint64_t s0 = part == 0 ? a.X.gate_s : part == 1 ? a.X.up_s : a.X.down_s;
+            const uint64_t b0 = part == 0 ? a.X.gate_b : part == 1 ? a.X.up_b : a.X.down_b;
+            ow = (uint32_t)(w0 / 4) + r * KB;
+            os = (uint32_t)(s0 / 2) + r * G;
+            ob = (uint32_t)(b0 / 2) + r * G;
+            return;
+        }
+        // concatenated segments along n (PE_STORE), else matrix q
+        uint32_t mw = a.seg[q].wo, ms = a.seg[q].so, mb = a.seg[q].bo, rr = r;
+        if (EPI == PE_STORE) {
+#pragma unroll
+            for (int sgi = 1; sgi < 4; ++sgi)
+                if ((uint32_t)sgi < a.nseg && r >= a.seg[sgi].n0) {
+                    mw = a.seg[sgi].wo;
+                    ms = a.seg[sgi].so;
+                    mb = a.seg[sgi].bo;
+                    rr = r - a.seg[sgi].n0;
+                }
+        }
+        ow = mw + rr * KB;
+        os = ms + rr * G;
+        ob = mb + rr * G;
+    };
+    uint32_t nout[NJ];  // output index of tile j (PE_HC_UP: the output i)
+    uint32_t wo[NMAT][NJ], so[NMAT][NJ], bo[NMAT][NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-        uint32_t r;
-        if (EPI == PE_HC_UP) {
-            const uint32_t i = blockIdx.x * 64 + wn * 16 + col;
-            nout[j] = i;
-            r = min((uint32_t)j, a.hc - 1) * a.H + min(i, a.H - 1);
-        } else {
-            const uint32_t n = blockIdx.x * (256 / NMAT) + wn * (64 / NMAT) + j * 16 + col;
-            nout[j] = n;
-            r = min(n, a.N - 1);
-        }
+        nout[j] = out_of(wn, j, col);
+        const uint32_t r = row_of(wn, j, col);
 #pragma unroll
-        for (int q = 0; q < NMAT; ++q) {
-            if (expert) {
-                const int part = EPI == PE_SILU_MUL ? q : 2;
-                const uint64_t w0 = part == 0 ? a.X.gate_w : part == 1 ? a.X.up_w : a.X.down_w;
-                const uint64_t s0 = part == 0 ? a.X.gate_s : part == 1 ? a.X.up_s : a.X.down_s;
-                const uint64_t b0 = part == 0 ? a.X.gate_b : part == 1 ? a.X.up_b : a.X.down_b;
-                wo[q][j] = (uint32_t)(w0 / 4) + r * KB;
-                so[q][j] = (uint32_t)(s0 / 2) + r * G;
-                bo[q][j] = (uint32_t)(b0 / 2) + r * G;
-            } else {
-                // concatenated segments along n (PE_STORE), else matrix q
-                uint32_t mw = a.seg[q].wo, ms = a.seg[q].so, mb = a.seg[q].bo, rr = r;
-                if (EPI == PE_STORE) {
-#pragma unroll
-                    for (int sgi = 1; sgi < 4; ++sgi)
-                        if ((uint32_t)sgi < a.nseg && r >= a.seg[sgi].n0) {
-                            mw = a.seg[sgi].wo;
-                            ms = a.seg[sgi].so;
-                            mb = a.seg[sgi].bo;
-                            rr = r - a.seg[sgi].n0;
-                        }
-                }
-                wo[q][j] = mw + rr * KB;
-                so[q][j] = ms + rr * G;
-                bo[q][j] = mb + rr * G;
-            }
-        }
+        for (int q = 0; q < NMAT; ++q) offs(q, r, wo[q][j], so[q][j], bo[q][j]);
+    }
+    // scale loader (SBL): thread tid loads the scales (even tid) or biases
+    // (odd tid) of local row tid / 2
+    uint32_t sb_off = 0;
+    if (SBL) {
+        const uint32_t lr = tid >> 1, wn_ = lr >> 6, rem = lr & 63;
+        const int q = (int)(rem / (NJ * 16)), j = (int)((rem >> 4) % NJ);
+        uint32_t ow, os, ob;
+        offs(q, row_of(wn_, j, lr & 15), ow, os, ob);
+        sb_off = (tid & 1) ? ob : os;
     }
 
     // ---- A staging: thread tid loads 8-block tid % 8 of row tid / 8 (hi,
@@ -311,8 +330,10 @@ __global__ void __launch_bounds__(PF_WG) k_pf_gemm(PfGemmArgs a) {
     // the loads it consumes.
     u32x4 rah[2], ral[2];
     float rx[2];
-    u32x2 bw[2][NMAT][NJ];       // words 2 kq, 2 kq + 1 of the group: K-steps 0, 1
-    uint16_t bs[2][NMAT][NJ], bb[2][NMAT][NJ];  // bf16 scale, bias
+    u32x2 bw[2][NMAT][NJ];                         // words 2 kq, 2 kq + 1: K-steps 0, 1
+    uint16_t bs[2][SBL ? 1 : NMAT][SBL ? 1 : NJ];  // per-lane scale, bias (not SBL)
+    uint16_t bb[2][SBL ? 1 : NMAT][SBL ? 1 : NJ];
+    u32x4 sreg;                                    // SBL: the next block's 8 scales or biases
     auto fetch = [&](int slot, uint32_t g) __attribute__((always_inline)) {
         rah[slot] = ghi[g * 8];
         ral[slot] = glo[g * 8];
@@ -322,14 +343,35 @@ __global__ void __launch_bounds__(PF_WG) k_pf_gemm(PfGemmArgs a) {
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
                 bw[slot][q][j] = *reinterpret_cast<const u32x2*>(wb + wo[q][j] + g * 8 + kq * 2);
-                bs[slot][q][j] = sbase[so[q][j] + g];
-                bb[slot][q][j] = sbase[bo[q][j] + g];
+                if (!SBL) {
+                    bs[slot][SBL ? 0 : q][SBL ? 0 : j] = sbase[so[q][j] + g];
+                    bb[slot][SBL ? 0 : q][SBL ? 0 : j] = sbase[bo[q][j] + g];
+                }
             }
     };
     auto a_store = [&](int slot, uint32_t buf) __attribute__((always_inline)) {
         sA[buf][0][lrow * PF_AROW + lkb] = rah[slot];
         sA[buf][1][lrow * PF_AROW + lkb] = ral[slot];
         sX[buf][tid & 63] = rx[slot];  // eight identical writes per row: no branch
+    };
+    auto sb_fetch = [&](uint32_t g0) __attribute__((always_inline)) {
+        sreg = *reinterpret_cast<const u32x4*>(sbase + sb_off + g0);
+    };
+    // (scale, bias) pairs of groups 0-3 (even tid) or 4-7 (odd tid) of the
+    // block, swapped across the thread pair
+    auto sb_store = [&](uint32_t buf) __attribute__((always_inline)) {
+        const bool odd = tid & 1;
+        const uint32_t x0 = __shfl_xor(odd ? sreg.x : sreg.z, 1, 64);
+        const uint32_t x1 = __shfl_xor(odd ? sreg.y : sreg.w, 1, 64);
+        // even: own scales s0..s7 (x, y hold s0-3), partner biases b0-3 (x0, x1)
+        // odd: own biases b0..b7 (z, w hold b4-7), partner scales s4-7 (x0, x1)
+        const uint32_t sl0 = odd ? x0 : sreg.x, sl1 = odd ? x1 : sreg.y;
+        const uint32_t bl0 = odd ? sreg.z : x0, bl1 = odd ? sreg.w : x1;
+        uint32_t* d = &sSB[buf][(tid >> 1) * SBR + (odd ? 4 : 0)];
+        d[0] = (sl0 & 0xffffu) | (bl0 << 16);
+        d[1] = (sl0 >> 16) | (bl0 & 0xffff0000u);
+        d[2] = (sl1 & 0xffffu) | (bl1 << 16);
+        d[3] = (sl1 >> 16) | (bl1 & 0xffff0000u);
     };
 
     f4 acc[NMAT][NI][NJ];
@@ -341,10 +383,12 @@ __global__ void __launch_bounds__(PF_WG) k_pf_gemm(PfGemmArgs a) {
             for (int j = 0; j < NJ; ++j) acc[q][i][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     const Q4Consts qk;
 
-    // one quant group g (LDS buffer and register slot S = g % 2)
+    // one quant group g; S = g % 8 under SBL (g % 2 otherwise): register slot
+    // S % 2 and LDS buffer g % 2
     auto step = [&](auto sc_, uint32_t g) __attribute__((always_inline)) {
-        constexpr int S = decltype(sc_)::value;
-        fetch(S ^ 1, min(g + 1, G - 1));
+        constexpr int S = decltype(sc_)::value, P = S & 1;
+        fetch(P ^ 1, min(g + 1, G - 1));
+        if (SBL && S == 0) sb_fetch(min(g + 8, G - 8));
         // K-step s of lane quarter kq takes the group's word 2 kq + s (A
         // staged in the same 8-block order)
         h8 bq[NMAT][NJ][2];
@@ -352,16 +396,22 @@ __global__ void __launch_bounds__(PF_WG) k_pf_gemm(PfGemmArgs a) {
         for (int q = 0; q < NMAT; ++q)
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
-                bq[q][j][0] = pf_unpack(bw[S][q][j].x, qk);
-                bq[q][j][1] = pf_unpack(bw[S][q][j].y, qk);
+                bq[q][j][0] = pf_unpack(bw[P][q][j].x, qk);
+                bq[q][j][1] = pf_unpack(bw[P][q][j].y, qk);
             }
         float sc[NMAT][NJ], bi[NMAT][NJ];
 #pragma unroll
         for (int q = 0; q < NMAT; ++q)
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
-                sc[q][j] = bf16f(bs[S][q][j]);
-                bi[q][j] = bf16f(bb[S][q][j]);
+                if (SBL) {
+                    const uint32_t v = sSB[(g >> 3) & 1][(((wn * NMAT + q) * NJ + j) * 16 + col) * SBR + S];
+                    sc[q][j] = __uint_as_float(v << 16);
+                    bi[q][j] = __uint_as_float(v & 0xffff0000u);
+                } else {
+                    sc[q][j] = bf16f(bs[P][SBL ? 0 : q][SBL ? 0 : j]);
+                    bi[q][j] = bf16f(bb[P][SBL ? 0 : q][SBL ? 0 : j]);
+                }
             }
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
@@ -370,8 +420,8 @@ __global__ void __launch_bounds__(PF_WG) k_pf_gemm(PfGemmArgs a) {
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
                 const uint32_t ai = (row16 + col) * PF_AROW + kq * 2 + s;
-                const h8 ah = __builtin_bit_cast(h8, sA[S][0][ai]);
-                const h8 al = __builtin_bit_cast(h8, sA[S][1][ai]);
+                const h8 ah = __builtin_bit_cast(h8, sA[P][0][ai]);
+                const h8 al = __builtin_bit_cast(h8, sA[P][1][ai]);
 #pragma unroll
                 for (int q = 0; q < NMAT; ++q)
 #pragma unroll
@@ -381,7 +431,7 @@ __global__ void __launch_bounds__(PF_WG) k_pf_gemm(PfGemmArgs a) {
                         accg[q][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bq[q][j][s], accg[q][j], 0, 0, 0);
                     }
             }
-            const float4 xv = *reinterpret_cast<const float4*>(&sX[S][row16 + kq * 4]);
+            const float4 xv = *reinterpret_cast<const float4*>(&sX[P][row16 + kq * 4]);
             const float xr[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
             for (int q = 0; q < NMAT; ++q)
@@ -390,23 +440,41 @@ __global__ void __launch_bounds__(PF_WG) k_pf_gemm(PfGemmArgs a) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) acc[q][i][j][r] += sc[q][j] * accg[q][j][r] + bi[q][j] * xr[r];
         }
-        // A of group g + 1 into the other buffer, read by nobody since the
-        // last barrier
-        a_store(S ^ 1, S ^ 1);
+        // A of group g + 1 into the other buffer (read by nobody since the
+        // last barrier); the next scale block at the end of a block
+        a_store(P ^ 1, P ^ 1);
+        if (SBL && S == 7) sb_store(((g >> 3) + 1) & 1);
         __syncthreads();
     };
 
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
     fetch(0, 0);
+    if (SBL) {
+        sb_fetch(0);
+        sb_store(0);
+    }
     a_store(0, 0);
     __syncthreads();
-    uint32_t g = 0;
-    for (; g + 2 <= G; g += 2) {
-        step(I0{}, g);
-        step(I1{}, g + 1);
+    if (SBL) {
+        for (uint32_t g = 0; g < G; g += 8) {
+            step(I0{}, g);
+            step(I1{}, g + 1);
+            step(std::integral_constant<int, 2>{}, g + 2);
+            step(std::integral_constant<int, 3>{}, g + 3);
+            step(std::integral_constant<int, 4>{}, g + 4);
+            step(std::integral_constant<int, 5>{}, g + 5);
+            step(std::integral_constant<int, 6>{}, g + 6);
+            step(std::integral_constant<int, 7>{}, g + 7);
+        }
+    } else {
+        uint32_t g = 0;
+        for (; g + 2 <= G; g += 2) {
+            step(I0{}, g);
+            step(I1{}, g + 1);
+        }
+        if (g < G) step(I0{}, g);
     }
-    if (g < G) step(I0{}, g);
 
     // ---- epilogue
 #pragma unroll
@@ -829,15 +897,26 @@ void launch_pf_gemm_args(const PfGemmArgs& args, int epi, uint32_t grid_y, hipSt
         a.seg[q].so = (uint32_t)s;
         a.seg[q].bo = (uint32_t)b;
     }
+    // staged scales need whole blocks of 8 groups on 16-byte aligned rows
+    bool sbl = (a.K / 64) % 8 == 0 && smin % 16 == 0;
+    for (int q = 0; q < nm; ++q) sbl = sbl && a.seg[q].so % 8 == 0 && a.seg[q].bo % 8 == 0;
+    if (a.X.base)
+        sbl = sbl && (uintptr_t)a.X.base % 16 == 0 && a.X.stride % 16 == 0 && a.X.gate_s % 16 == 0 &&
+              a.X.gate_b % 16 == 0 && a.X.up_s % 16 == 0 && a.X.up_b % 16 == 0 && a.X.down_s % 16 == 0 &&
+              a.X.down_b % 16 == 0;
+    if (epi == PE_HC_UP && a.hc > 4) throw std::runtime_error("prefill mix needs hc <= 4");
+#define PF_GEMM(NM, E, GX)                                                             \
+    do {                                                                               \
+        if (sbl) k_pf_gemm<NM, E, true><<<dim3(GX, grid_y), PF_WG, 0, st>>>(a);       \
+        else k_pf_gemm<NM, E, false><<<dim3(GX, grid_y), PF_WG, 0, st>>>(a);          \
+    } while (0)
     switch (epi) {
-    case PE_STORE: k_pf_gemm<1, PE_STORE><<<dim3((a.N + 255) / 256, grid_y), PF_WG, 0, st>>>(a); break;
-    case PE_INJECT: k_pf_gemm<1, PE_INJECT><<<dim3((a.N + 255) / 256, grid_y), PF_WG, 0, st>>>(a); break;
-    case PE_HC_UP:
-        if (a.hc > 4) throw std::runtime_error("prefill mix needs hc <= 4");
-        k_pf_gemm<1, PE_HC_UP><<<dim3((a.H + 63) / 64, grid_y), PF_WG, 0, st>>>(a);
-        break;
-    default: k_pf_gemm<2, PE_SILU_MUL><<<dim3((a.N + 127) / 128, grid_y), PF_WG, 0, st>>>(a); break;
+    case PE_STORE: PF_GEMM(1, PE_STORE, (a.N + 255) / 256); break;
+    case PE_INJECT: PF_GEMM(1, PE_INJECT, (a.N + 255) / 256); break;
+    case PE_HC_UP: PF_GEMM(1, PE_HC_UP, (a.H + 63) / 64); break;
+    default: PF_GEMM(2, PE_SILU_MUL, (a.N + 127) / 128); break;
     }
+#undef PF_GEMM
 }
 
 void launch_pf_gemm(const Q4Mat& w, const uint4* xhi, const uint4* xlo, const float* xs, float* y, uint32_t T,
