@@ -124,7 +124,7 @@ struct PfBufs {
     float* hyper;
     uint4 *hi, *lo, *bhi, *bmid, *blo;
     float* xs;
-    float *inv, *d, *inj_a, *inj_m, *mixed;
+    float *inv, *d, *inj_a, *inj_m, *mixed, *hc_part;
     float *raw, *z, *a, *b, *conv, *decay, *beta, *y;
     float *q_raw, *k_raw, *v_raw, *idx_raw, *q_ready, *attn_out;
     float* part;
@@ -1056,6 +1056,7 @@ void ChkEngine::pf_alloc() {
     pf.blo = dalloc<uint4>(C * D.H / 8);
     pf.inv = dalloc<float>(C * D.hc);
     pf.d = dalloc<float>(C * D.lowrank);
+    pf.hc_part = dalloc<float>(C * D.hc * (D.lowrank + D.hc));
     pf.inj_a = dalloc<float>(C * D.hc);
     pf.inj_m = dalloc<float>(C * D.hc);
     pf.mixed = dalloc<float>(C * D.H);
@@ -1100,18 +1101,23 @@ void ChkEngine::pf_alloc() {
 void ChkEngine::pf_hc_read(const HcDev& w, float* inj, uint32_t T, bool for_moe) {
     const uint32_t mt = (T + 63) / 64;
     launch_pf_hc_prep(pf.hyper, w.norm, D.H, D.hc, D.eps, pf.inv, pf.hi, pf.lo, pf.xs, T, st);
+    // [down; inject] is narrow (lowrank + hc outputs) over a long K = hc H:
+    // split K by stream, partials summed in stream order by the finisher
+    const uint32_t N = D.lowrank + D.hc;
     PfGemmArgs g{};
-    g.seg[0] = PfSeg{w.down, pf.d, D.lowrank, 0, PA_SILU};
-    g.seg[1] = PfSeg{w.inject, inj, D.hc, D.lowrank, PA_2SIG};
+    g.seg[0] = PfSeg{w.down, pf.hc_part, N, 0, PA_NONE};
+    g.seg[1] = PfSeg{w.inject, pf.hc_part + D.lowrank, N, D.lowrank, PA_NONE};
     g.nseg = 2;
-    g.N = D.lowrank + D.hc;
+    g.N = N;
     g.K = D.hh;
     g.M = T;
-    g.alpha = 1.0f / (float)D.hc;
+    g.ksplit = D.hc;
+    g.zstride = (uint64_t)T * N;
     g.xhi = pf.hi;
     g.xlo = pf.lo;
     g.xs = pf.xs;
     launch_pf_gemm_args(g, PE_STORE, mt, st);
+    launch_pf_hc_down_finish(pf.hc_part, D.hc, T, D.lowrank, D.hc, 1.0f / (float)D.hc, pf.d, inj, st);
     launch_pf_xprep(pf.d, D.lowrank, T, D.lowrank, pf.hi, pf.lo, pf.xs, st);
     PfGemmArgs u{};
     u.seg[0].m = w.up;

@@ -280,6 +280,8 @@ struct PfGemmArgs {
     PfSeg seg[4];      // PE_SILU_MUL: seg[0].m gate, seg[1].m up (shared expert), output seg[0].y
     uint32_t nseg, N, K, M;
     float alpha;
+    uint32_t ksplit;         // K chunks (grid z); PE_STORE then writes chunk z at y + z zstride
+    uint64_t zstride;
     const uint4* xhi;
     const uint4* xlo;
     const float* xs;
@@ -354,6 +356,8 @@ void launch_pf_hc_prep(const float* hyper, const uint16_t* norm, uint32_t H, uin
 void launch_pf_gemm_args(const PfGemmArgs& a, int epi, uint32_t grid_y, hipStream_t st);
 void launch_pf_gemm(const Q4Mat& w, const uint4* xhi, const uint4* xlo, const float* xs, float* y, uint32_t T,
                     uint32_t ldy, hipStream_t st);
+void launch_pf_hc_down_finish(const float* part, uint32_t nsplit, uint32_t T, uint32_t lowrank, uint32_t hc,
+                              float alpha, float* d, float* inj, hipStream_t st);
 void launch_pf_router(const uint16_t* router, const uint16_t* shared_gate, const uint4* bhi, const uint4* bmid,
                       const uint4* blo, float* logits, float* sg, uint32_t T, uint32_t E, uint32_t H, hipStream_t st);
 void launch_pf_route(const float* logits, uint32_t T, uint32_t E, uint32_t topk, int norm_topk, uint32_t* ids,

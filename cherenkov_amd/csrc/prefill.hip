@@ -244,6 +244,8 @@ __global__ void __launch_bounds__(PF_WG) k_pf_gemm(PfGemmArgs a) {
     if (m0 >= M) return;
     const uint32_t* list = a.list ? a.list + (size_t)grp * a.cap : nullptr;
     const uint32_t K = a.K, G = K >> 6, KB = K >> 3;
+    // split K: this workgroup's groups [gb, ge)
+    const uint32_t gc = G / gridDim.z, gb = blockIdx.z * gc, ge = gb + gc;
 
     // ---- weight rows as 32-bit element offsets from one workgroup-uniform
     // base per array (the record of a routed expert, else the lowest
@@ -387,8 +389,8 @@ __global__ void __launch_bounds__(PF_WG) k_pf_gemm(PfGemmArgs a) {
     // S % 2 and LDS buffer g % 2
     auto step = [&](auto sc_, uint32_t g) __attribute__((always_inline)) {
         constexpr int S = decltype(sc_)::value, P = S & 1;
-        fetch(P ^ 1, min(g + 1, G - 1));
-        if (SBL && S == 0) sb_fetch(min(g + 8, G - 8));
+        fetch(P ^ 1, min(g + 1, ge - 1));
+        if (SBL && S == 0) sb_fetch(min(g + 8, ge - 8));
         // K-step s of lane quarter kq takes the group's word 2 kq + s (A
         // staged in the same 8-block order)
         h8 bq[NMAT][NJ][2];
@@ -405,7 +407,7 @@ __global__ void __launch_bounds__(PF_WG) k_pf_gemm(PfGemmArgs a) {
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
                 if (SBL) {
-                    const uint32_t v = sSB[(g >> 3) & 1][(((wn * NMAT + q) * NJ + j) * 16 + col) * SBR + S];
+                    const uint32_t v = sSB[((g - gb) >> 3) & 1][(((wn * NMAT + q) * NJ + j) * 16 + col) * SBR + S];
                     sc[q][j] = __uint_as_float(v << 16);
                     bi[q][j] = __uint_as_float(v & 0xffff0000u);
                 } else {
@@ -443,21 +445,21 @@ __global__ void __launch_bounds__(PF_WG) k_pf_gemm(PfGemmArgs a) {
         // A of group g + 1 into the other buffer (read by nobody since the
         // last barrier); the next scale block at the end of a block
         a_store(P ^ 1, P ^ 1);
-        if (SBL && S == 7) sb_store(((g >> 3) + 1) & 1);
+        if (SBL && S == 7) sb_store((((g - gb) >> 3) + 1) & 1);
         __syncthreads();
     };
 
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
-    fetch(0, 0);
+    fetch(0, gb);
     if (SBL) {
-        sb_fetch(0);
+        sb_fetch(gb);
         sb_store(0);
     }
     a_store(0, 0);
     __syncthreads();
     if (SBL) {
-        for (uint32_t g = 0; g < G; g += 8) {
+        for (uint32_t g = gb; g < ge; g += 8) {
             step(I0{}, g);
             step(I1{}, g + 1);
             step(std::integral_constant<int, 2>{}, g + 2);
@@ -468,12 +470,12 @@ __global__ void __launch_bounds__(PF_WG) k_pf_gemm(PfGemmArgs a) {
             step(std::integral_constant<int, 7>{}, g + 7);
         }
     } else {
-        uint32_t g = 0;
-        for (; g + 2 <= G; g += 2) {
+        uint32_t g = gb;
+        for (; g + 2 <= ge; g += 2) {
             step(I0{}, g);
             step(I1{}, g + 1);
         }
-        if (g < G) step(I0{}, g);
+        if (g < ge) step(I0{}, g);
     }
 
     // ---- epilogue
@@ -516,10 +518,28 @@ __global__ void __launch_bounds__(PF_WG) k_pf_gemm(PfGemmArgs a) {
                     float v = acc[0][i][j][r];
                     if (sg.act == PA_SILU) v = siluf_(v * a.alpha);
                     else if (sg.act == PA_2SIG) v = 2.0f * sigmoidf_(v * a.alpha);
-                    sg.y[(size_t)yrow * sg.ldy + (n - sg.n0)] = v;
+                    sg.y[(size_t)blockIdx.z * a.zstride + (size_t)yrow * sg.ldy + (n - sg.n0)] = v;
                 }
             }
         }
+}
+
+// Split-K hyper-connection read: the [down; inject] partials of the hc
+// stream chunks summed in stream order, then d = silu(v / hc) and inj =
+// 2 sigmoid(v / hc) (cpu.rs:493-500).
+__global__ void __launch_bounds__(256) k_pf_hc_down_finish(const float* __restrict__ part, uint32_t nsplit,
+                                                           uint64_t zstride, uint32_t T, uint32_t lowrank,
+                                                           uint32_t hc, float alpha, float* __restrict__ d,
+                                                           float* __restrict__ inj) {
+    const uint32_t N = lowrank + hc;
+    const uint64_t i = (uint64_t)blockIdx.x * CHK_WG + threadIdx.x;
+    if (i >= (uint64_t)T * N) return;
+    const uint32_t t = (uint32_t)(i / N), n = (uint32_t)(i % N);
+    float v = 0.0f;
+    for (uint32_t z = 0; z < nsplit; ++z) v += part[z * zstride + i];
+    v *= alpha;
+    if (n < lowrank) d[(size_t)t * lowrank + n] = siluf_(v);
+    else inj[(size_t)t * hc + (n - lowrank)] = 2.0f * sigmoidf_(v);
 }
 
 // ------------------------------------------------------------- router
@@ -897,8 +917,11 @@ void launch_pf_gemm_args(const PfGemmArgs& args, int epi, uint32_t grid_y, hipSt
         a.seg[q].so = (uint32_t)s;
         a.seg[q].bo = (uint32_t)b;
     }
+    const uint32_t ksplit = std::max<uint32_t>(1, a.ksplit);
+    if ((a.K / 64) % ksplit || (ksplit > 1 && epi != PE_STORE))
+        throw std::runtime_error("split K needs whole groups per chunk and a plain store");
     // staged scales need whole blocks of 8 groups on 16-byte aligned rows
-    bool sbl = (a.K / 64) % 8 == 0 && smin % 16 == 0;
+    bool sbl = (a.K / 64 / ksplit) % 8 == 0 && smin % 16 == 0;
     for (int q = 0; q < nm; ++q) sbl = sbl && a.seg[q].so % 8 == 0 && a.seg[q].bo % 8 == 0;
     if (a.X.base)
         sbl = sbl && (uintptr_t)a.X.base % 16 == 0 && a.X.stride % 16 == 0 && a.X.gate_s % 16 == 0 &&
@@ -907,8 +930,8 @@ void launch_pf_gemm_args(const PfGemmArgs& args, int epi, uint32_t grid_y, hipSt
     if (epi == PE_HC_UP && a.hc > 4) throw std::runtime_error("prefill mix needs hc <= 4");
 #define PF_GEMM(NM, E, GX)                                                             \
     do {                                                                               \
-        if (sbl) k_pf_gemm<NM, E, true><<<dim3(GX, grid_y), PF_WG, 0, st>>>(a);       \
-        else k_pf_gemm<NM, E, false><<<dim3(GX, grid_y), PF_WG, 0, st>>>(a);          \
+        if (sbl) k_pf_gemm<NM, E, true><<<dim3(GX, grid_y, ksplit), PF_WG, 0, st>>>(a); \
+        else k_pf_gemm<NM, E, false><<<dim3(GX, grid_y, ksplit), PF_WG, 0, st>>>(a);    \
     } while (0)
     switch (epi) {
     case PE_STORE: PF_GEMM(1, PE_STORE, (a.N + 255) / 256); break;
@@ -931,6 +954,12 @@ void launch_pf_gemm(const Q4Mat& w, const uint4* xhi, const uint4* xlo, const fl
     a.xlo = xlo;
     a.xs = xs;
     launch_pf_gemm_args(a, PE_STORE, (T + 63) / 64, st);
+}
+
+void launch_pf_hc_down_finish(const float* part, uint32_t nsplit, uint32_t T, uint32_t lowrank, uint32_t hc,
+                              float alpha, float* d, float* inj, hipStream_t st) {
+    const uint64_t n = (uint64_t)T * (lowrank + hc);
+    if (n) k_pf_hc_down_finish<<<(uint32_t)((n + CHK_WG - 1) / CHK_WG), CHK_WG, 0, st>>>(part, nsplit, n, T, lowrank, hc, alpha, d, inj);
 }
 
 void launch_pf_router(const uint16_t* router, const uint16_t* shared_gate, const uint4* bhi, const uint4* bmid,

@@ -131,12 +131,41 @@ def test_gemm_prefill_matches_oracle(have_gpu):
         assert nxt == int(np.argmax(ref))
 
 
+def test_gemm_prefill_full_width(have_gpu):
+    """Config 5 widths (hidden 2048, 512 experts top-10, 16/32 DeltaNet
+    heads, 16q/2kv x 256 attention, vocab 151936) on 4 layers, where f32
+    rounding stays small end to end: a 200-token GEMM prefill within 1e-3 of
+    the row path (logits, DeltaNet state and history), then 4 greedy tokens."""
+    cfg = presets.qwen3next_80b_shape(layers=4, mtp=0)
+    rng = np.random.default_rng(78)
+    prompt = rng.integers(0, cfg.vocab_size, size=200).tolist()
+    a = Engine(cfg, experts=4, drafts=0, max_t=256)
+    b = Engine(cfg, experts=4, drafts=0, max_t=256)
+    try:
+        nxt_a, _ = a.prefill_chunk(prompt)
+        la = a.logits_row(0)
+        nxt_b, lb = row_prefill(b, prompt)
+        assert_close(la, lb, "full-width prefill logits", abs_frac=1e-3, min_cos=0.99999)
+        if argmax_margin(lb) > 1e-3:
+            assert nxt_a == nxt_b
+        for layer in range(3):
+            sa, ca = dn_state(a, cfg, layer)
+            sb, cb = dn_state(b, cfg, layer)
+            assert_close(sa, sb, f"layer {layer} state", abs_frac=1e-3, min_cos=0.99999)
+            assert_close(ca, cb, f"layer {layer} conv history", abs_frac=1e-3, min_cos=0.99999)
+        greedy_pair(a, b, nxt_b, 4, "full width")
+    finally:
+        a.close()
+        b.close()
+
+
 def test_gemm_prefill_full_shape(have_gpu):
-    """Config 5 shape (48 layers, 512 experts top-10, vocab 151936) against
-    the row path.  The random-init 48-layer stack amplifies f32 rounding
-    with depth (a 1e-6 difference at layer 0 reaches ~1e-3 by layer 46 after
-    one token), and over long prompts a deep layer's top-10 cut meets a
-    near-tie somewhere, so end-to-end logits are compared on a short prompt;
+    """Config 5 shape (48 layers) against the row path.  The random-init
+    48-layer stack amplifies f32 rounding with depth (a 1e-6 difference at
+    layer 0 reaches ~1e-3 by layer 46 after one token, ~1e-2 after a few
+    more), and over long prompts a deep layer's top-10 cut meets a near-tie
+    somewhere, so end-to-end logits are compared at the end of a short
+    prompt (the per-layer kernels are pinned at 4 layers above);
     the long prompt is checked where the bar applies directly: the early
     DeltaNet layers' state and conv history after 256 rows of the sequential
     scan, and the last row's expert choice in the early layers."""
@@ -152,7 +181,6 @@ def test_gemm_prefill_full_shape(have_gpu):
         assert_close(la, lb, "full-shape 8-token prefill logits")
         if argmax_margin(lb) > 1e-3:
             assert nxt_a == nxt_b
-        greedy_pair(a, b, nxt_b, 2, "full shape", abs_frac=2e-2, min_cos=0.999)
         a.reset()
         b.reset()
         prompt = rng.integers(0, cfg.vocab_size, size=256).tolist()
