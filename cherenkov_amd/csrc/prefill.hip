@@ -184,15 +184,15 @@ __global__ void __launch_bounds__(256) k_pf_hc_prep(const float* __restrict__ hy
 }
 
 // --------------------------------------------------------------- GEMM
-// Tile: a workgroup of 8 waves covers 64 rows x 256 / NMAT outputs of every
-// matrix; wave w takes rows 32 (w % 2) .. + 32 and outputs 64 (w / 2) /
-// NMAT .. (four 16-wide MFMA tiles per 16 rows in all).  The 64-row A tile
-// of each quant group (hi and lo planes, 16 KiB) is staged through LDS once
-// for the 8 waves, double-buffered with the next group's global loads;
-// every wave streams its own weight words one group ahead.  Per group and
-// 16-row slice the MFMA partial sums start from zero (two K-steps of 32,
-// hi then lo) and fold into the accumulator with the group's scale and
-// bias.
+// Tile: a workgroup of 4 waves covers 64 rows x 256 / NMAT outputs of every
+// matrix; wave w takes all 64 rows and outputs 64 w / NMAT .. (four 16-wide
+// MFMA tiles per 16 rows in all), so every unpacked weight word feeds 4 x 2
+// MFMAs.  The 64-row A tile of each quant group (hi and lo planes, 16 KiB)
+// is staged through LDS once for the 4 waves, double-buffered with the
+// next group's global loads; every wave streams its own weight words one
+// group ahead.  Per group and 16-row slice the MFMA partial sums start from
+// zero (two K-steps of 32, hi then lo) and fold into the accumulator with
+// the group's scale.  Two workgroups share a CU.
 //
 // Rows: dense (row m of A and Y), or grouped: a tile list names (group,
 // 64-row tile); list[group][m] is an entry e, A row e / div, Y row e.  The
@@ -206,7 +206,7 @@ __global__ void __launch_bounds__(256) k_pf_hc_prep(const float* __restrict__ hy
 // a wave are the hc streams of the same 16 outputs: mixed = (1/hc) sum_g
 // sigmoid(v_g) normed_g, cpu.rs:477-491), PE_SILU_MUL (NMAT 2:
 // silu(gate) * up, mlp, cpu.rs:981-992).
-constexpr int PF_WG = 512;  // threads per GEMM workgroup
+constexpr int PF_WG = 256;  // threads per GEMM workgroup
 constexpr int PF_AROW = 9;  // uint4 per staged A row (8 + 1 pad: bank spread)
 
 CHK_DEV h8 pf_unpack(uint32_t w, const Q4Consts& qk) {
@@ -219,19 +219,24 @@ CHK_DEV h8 pf_unpack(uint32_t w, const Q4Consts& qk) {
 }
 
 // SBL: the scales and biases of the workgroup's 256 weight rows are staged
-// through LDS in blocks of 8 groups (one 16-byte load per thread per block,
-// interleaved into (scale | bias << 16) words), instead of two 2-byte loads
-// per lane, tile and group; it needs G % 8 == 0 and 16-byte aligned rows.
+// through LDS in blocks of 8 groups (thread t loads row t's 8 scales and 8
+// biases with two 16-byte loads per block and interleaves them into
+// (scale | bias << 16) words); the main loop then folds only s * partial,
+// and the bias term sum_g b[n][g] xs[m][g] runs after it as its own small
+// MFMA contraction over the groups (bf16, with xs split into three bf16
+// terms so every product is exact).  Needs G % 8 == 0 and 16-byte aligned
+// rows; otherwise each lane loads its scale and bias per group and folds
+// both in the loop.
 template <int NMAT, int EPI, bool SBL>
-__global__ void __launch_bounds__(PF_WG) k_pf_gemm(PfGemmArgs a) {
+__global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
     constexpr int NJ = 4 / NMAT;  // 16-wide output tiles per matrix per wave
-    constexpr int NI = 2;         // 16-row slices per wave
+    constexpr int NI = 4;         // 16-row slices per wave
     constexpr int SBR = 9;        // words per staged scale row (8 groups + pad)
     __shared__ __align__(16) u32x4 sA[2][2][64 * PF_AROW];
     __shared__ __align__(16) float sX[2][64];
     __shared__ uint32_t sSB[SBL ? 2 : 1][SBL ? 256 * SBR : 1];
     const int tid = threadIdx.x, lane = tid & 63, col = lane & 15, kq = lane >> 4;
-    const uint32_t w = wave_id(), rh = w & 1, wn = w >> 1;
+    const uint32_t wn = wave_id();
     uint32_t grp = 0, mt = blockIdx.y;
     if (a.list) {
         if (blockIdx.y >= *a.ntiles) return;
@@ -249,8 +254,8 @@ __global__ void __launch_bounds__(PF_WG) k_pf_gemm(PfGemmArgs a) {
 
     // ---- weight rows as 32-bit element offsets from one workgroup-uniform
     // base per array (the record of a routed expert, else the lowest
-    // segment matrix).  Local row lr = ((wn NMAT + q) NJ + j) 16 + col of the
-    // workgroup's 256 is matrix q, tile j of wave column wn.
+    // segment matrix).  Local row lr = ((w NMAT + q) NJ + j) 16 + col of the
+    // workgroup's 256 is matrix q, tile j of wave w.
     const bool expert = a.X.base && grp < a.X.experts;
     const uint8_t* rec = a.X.base + ((size_t)a.record_layer * a.X.experts + grp) * a.X.stride;
     const uint32_t* wb = expert ? reinterpret_cast<const uint32_t*>(rec) : a.wbase;
@@ -300,20 +305,18 @@ __global__ void __launch_bounds__(PF_WG) k_pf_gemm(PfGemmArgs a) {
 #pragma unroll
         for (int q = 0; q < NMAT; ++q) offs(q, r, wo[q][j], so[q][j], bo[q][j]);
     }
-    // scale loader (SBL): thread tid loads the scales (even tid) or biases
-    // (odd tid) of local row tid / 2
-    uint32_t sb_off = 0;
+    // scale loader (SBL): thread tid stages local row tid
+    uint32_t ld_so = 0, ld_bo = 0;
     if (SBL) {
-        const uint32_t lr = tid >> 1, wn_ = lr >> 6, rem = lr & 63;
+        const uint32_t wn_ = (uint32_t)tid >> 6, rem = (uint32_t)tid & 63;
         const int q = (int)(rem / (NJ * 16)), j = (int)((rem >> 4) % NJ);
-        uint32_t ow, os, ob;
-        offs(q, row_of(wn_, j, lr & 15), ow, os, ob);
-        sb_off = (tid & 1) ? ob : os;
+        uint32_t ow;
+        offs(q, row_of(wn_, j, rem & 15), ow, ld_so, ld_bo);
     }
 
-    // ---- A staging: thread tid loads 8-block tid % 8 of row tid / 8 (hi,
-    // lo) and the group sum of row tid % 64
-    const uint32_t lrow = tid >> 3, lkb = tid & 7;
+    // ---- A staging: thread tid loads 8-blocks 2 (tid % 4) + {0, 1} of row
+    // tid / 4 (hi, lo planes) and the group sum of row tid % 64
+    const uint32_t lrow = tid >> 2, lkb = (tid & 3) * 2;
     uint32_t arow_ld, arow_xs;
     {
         const uint32_t m = min(m0 + lrow, M - 1);
@@ -330,15 +333,17 @@ __global__ void __launch_bounds__(PF_WG) k_pf_gemm(PfGemmArgs a) {
     // unconditional (past the last group it re-reads the last one), so the
     // wait counters the compiler derives stay exact: a step waits only for
     // the loads it consumes.
-    u32x4 rah[2], ral[2];
+    u32x4 rah0[2], rah1[2], ral0[2], ral1[2];
     float rx[2];
     u32x2 bw[2][NMAT][NJ];                         // words 2 kq, 2 kq + 1: K-steps 0, 1
     uint16_t bs[2][SBL ? 1 : NMAT][SBL ? 1 : NJ];  // per-lane scale, bias (not SBL)
     uint16_t bb[2][SBL ? 1 : NMAT][SBL ? 1 : NJ];
-    u32x4 sreg;                                    // SBL: the next block's 8 scales or biases
+    u32x4 sreg_s, sreg_b;                          // SBL: the next block's 8 scales, 8 biases
     auto fetch = [&](int slot, uint32_t g) __attribute__((always_inline)) {
-        rah[slot] = ghi[g * 8];
-        ral[slot] = glo[g * 8];
+        rah0[slot] = ghi[g * 8];
+        rah1[slot] = ghi[g * 8 + 1];
+        ral0[slot] = glo[g * 8];
+        ral1[slot] = glo[g * 8 + 1];
         rx[slot] = gxs[g];
 #pragma unroll
         for (int q = 0; q < NMAT; ++q)
@@ -352,28 +357,25 @@ __global__ void __launch_bounds__(PF_WG) k_pf_gemm(PfGemmArgs a) {
             }
     };
     auto a_store = [&](int slot, uint32_t buf) __attribute__((always_inline)) {
-        sA[buf][0][lrow * PF_AROW + lkb] = rah[slot];
-        sA[buf][1][lrow * PF_AROW + lkb] = ral[slot];
-        sX[buf][tid & 63] = rx[slot];  // eight identical writes per row: no branch
+        sA[buf][0][lrow * PF_AROW + lkb] = rah0[slot];
+        sA[buf][0][lrow * PF_AROW + lkb + 1] = rah1[slot];
+        sA[buf][1][lrow * PF_AROW + lkb] = ral0[slot];
+        sA[buf][1][lrow * PF_AROW + lkb + 1] = ral1[slot];
+        sX[buf][tid & 63] = rx[slot];  // four identical writes per row: no branch
     };
     auto sb_fetch = [&](uint32_t g0) __attribute__((always_inline)) {
-        sreg = *reinterpret_cast<const u32x4*>(sbase + sb_off + g0);
+        sreg_s = *reinterpret_cast<const u32x4*>(sbase + ld_so + g0);
+        sreg_b = *reinterpret_cast<const u32x4*>(sbase + ld_bo + g0);
     };
-    // (scale, bias) pairs of groups 0-3 (even tid) or 4-7 (odd tid) of the
-    // block, swapped across the thread pair
     auto sb_store = [&](uint32_t buf) __attribute__((always_inline)) {
-        const bool odd = tid & 1;
-        const uint32_t x0 = __shfl_xor(odd ? sreg.x : sreg.z, 1, 64);
-        const uint32_t x1 = __shfl_xor(odd ? sreg.y : sreg.w, 1, 64);
-        // even: own scales s0..s7 (x, y hold s0-3), partner biases b0-3 (x0, x1)
-        // odd: own biases b0..b7 (z, w hold b4-7), partner scales s4-7 (x0, x1)
-        const uint32_t sl0 = odd ? x0 : sreg.x, sl1 = odd ? x1 : sreg.y;
-        const uint32_t bl0 = odd ? sreg.z : x0, bl1 = odd ? sreg.w : x1;
-        uint32_t* d = &sSB[buf][(tid >> 1) * SBR + (odd ? 4 : 0)];
-        d[0] = (sl0 & 0xffffu) | (bl0 << 16);
-        d[1] = (sl0 >> 16) | (bl0 & 0xffff0000u);
-        d[2] = (sl1 & 0xffffu) | (bl1 << 16);
-        d[3] = (sl1 >> 16) | (bl1 & 0xffff0000u);
+        uint32_t* d = &sSB[buf][tid * SBR];
+        const uint32_t sv[4] = {sreg_s.x, sreg_s.y, sreg_s.z, sreg_s.w};
+        const uint32_t bv[4] = {sreg_b.x, sreg_b.y, sreg_b.z, sreg_b.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            d[2 * e] = (sv[e] & 0xffffu) | (bv[e] << 16);
+            d[2 * e + 1] = (sv[e] >> 16) | (bv[e] & 0xffff0000u);
+        }
     };
 
     f4 acc[NMAT][NI][NJ];
@@ -409,7 +411,7 @@ __global__ void __launch_bounds__(PF_WG) k_pf_gemm(PfGemmArgs a) {
                 if (SBL) {
                     const uint32_t v = sSB[((g - gb) >> 3) & 1][(((wn * NMAT + q) * NJ + j) * 16 + col) * SBR + S];
                     sc[q][j] = __uint_as_float(v << 16);
-                    bi[q][j] = __uint_as_float(v & 0xffff0000u);
+                    bi[q][j] = 0.0f;
                 } else {
                     sc[q][j] = bf16f(bs[P][SBL ? 0 : q][SBL ? 0 : j]);
                     bi[q][j] = bf16f(bb[P][SBL ? 0 : q][SBL ? 0 : j]);
@@ -417,11 +419,10 @@ __global__ void __launch_bounds__(PF_WG) k_pf_gemm(PfGemmArgs a) {
             }
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
-            const uint32_t row16 = rh * 32 + i * 16;
             f4 accg[NMAT][NJ];
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
-                const uint32_t ai = (row16 + col) * PF_AROW + kq * 2 + s;
+                const uint32_t ai = (i * 16 + col) * PF_AROW + kq * 2 + s;
                 const h8 ah = __builtin_bit_cast(h8, sA[P][0][ai]);
                 const h8 al = __builtin_bit_cast(h8, sA[P][1][ai]);
 #pragma unroll
@@ -433,14 +434,26 @@ __global__ void __launch_bounds__(PF_WG) k_pf_gemm(PfGemmArgs a) {
                         accg[q][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bq[q][j][s], accg[q][j], 0, 0, 0);
                     }
             }
-            const float4 xv = *reinterpret_cast<const float4*>(&sX[P][row16 + kq * 4]);
-            const float xr[4] = {xv.x, xv.y, xv.z, xv.w};
+            if (SBL) {
 #pragma unroll
-            for (int q = 0; q < NMAT; ++q)
+                for (int q = 0; q < NMAT; ++q)
 #pragma unroll
-                for (int j = 0; j < NJ; ++j)
+                    for (int j = 0; j < NJ; ++j)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[q][i][j][r] += sc[q][j] * accg[q][j][r] + bi[q][j] * xr[r];
+                        for (int r = 0; r < 4; ++r) acc[q][i][j][r] = fmaf(sc[q][j], accg[q][j][r], acc[q][i][j][r]);
+            } else {
+                const float4 xv = *reinterpret_cast<const float4*>(&sX[P][i * 16 + kq * 4]);
+                const float xr[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+                for (int q = 0; q < NMAT; ++q)
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            acc[q][i][j][r] = fmaf(sc[q][j], accg[q][j][r], acc[q][i][j][r]);
+                            acc[q][i][j][r] = fmaf(bi[q][j], xr[r], acc[q][i][j][r]);
+                        }
+            }
         }
         // A of group g + 1 into the other buffer (read by nobody since the
         // last barrier); the next scale block at the end of a block
@@ -469,6 +482,59 @@ __global__ void __launch_bounds__(PF_WG) k_pf_gemm(PfGemmArgs a) {
             step(std::integral_constant<int, 6>{}, g + 6);
             step(std::integral_constant<int, 7>{}, g + 7);
         }
+        // bias term: acc[m][n] += sum_{g in [gb, ge)} b[n][g] xs[m][g], 32
+        // groups per bf16 MFMA K-step; lane (col, kq) takes groups
+        // k0 + 8 kq .. + 8 (whole 8-blocks: zero past ge)
+        const uint16_t zero16 = 0;
+        (void)zero16;
+        for (uint32_t k0 = gb; k0 < ge; k0 += 32) {
+            const uint32_t kg = k0 + 8 * kq;
+            const bool live = kg < ge;
+            const uint32_t kc = live ? kg : gb;
+            b8 bbv[NMAT][NJ];
+#pragma unroll
+            for (int q = 0; q < NMAT; ++q)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    const u32x4 v = *reinterpret_cast<const u32x4*>(sbase + bo[q][j] + kc);
+                    bbv[q][j] = __builtin_bit_cast(b8, live ? v : u32x4{0u, 0u, 0u, 0u});
+                }
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const uint32_t m = min(m0 + i * 16 + col, M - 1);
+                const uint32_t ar = list ? list[m] / a.div : m;
+                const float4* xp = reinterpret_cast<const float4*>(a.xs + (size_t)ar * G + kc);
+                const float4 x0 = xp[0], x1 = xp[1];
+                const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                uint32_t hw[4], mw[4], lw[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    uint32_t h2_[2], m2_[2], l2_[2];
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const float xx = live ? xv[2 * e + u] : 0.0f;
+                        h2_[u] = f2bf_rne(xx);
+                        const float r1 = xx - __uint_as_float(h2_[u] << 16);
+                        m2_[u] = f2bf_rne(r1);
+                        l2_[u] = f2bf_rne(r1 - __uint_as_float(m2_[u] << 16));
+                    }
+                    hw[e] = h2_[0] | h2_[1] << 16;
+                    mw[e] = m2_[0] | m2_[1] << 16;
+                    lw[e] = l2_[0] | l2_[1] << 16;
+                }
+                const b8 xh = __builtin_bit_cast(b8, u32x4{hw[0], hw[1], hw[2], hw[3]});
+                const b8 xm = __builtin_bit_cast(b8, u32x4{mw[0], mw[1], mw[2], mw[3]});
+                const b8 xl = __builtin_bit_cast(b8, u32x4{lw[0], lw[1], lw[2], lw[3]});
+#pragma unroll
+                for (int q = 0; q < NMAT; ++q)
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j) {
+                        acc[q][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, bbv[q][j], acc[q][i][j], 0, 0, 0);
+                        acc[q][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xm, bbv[q][j], acc[q][i][j], 0, 0, 0);
+                        acc[q][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, bbv[q][j], acc[q][i][j], 0, 0, 0);
+                    }
+            }
+        }
     } else {
         uint32_t g = gb;
         for (; g + 2 <= ge; g += 2) {
@@ -483,7 +549,7 @@ __global__ void __launch_bounds__(PF_WG) k_pf_gemm(PfGemmArgs a) {
     for (int i = 0; i < NI; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const uint32_t m = m0 + rh * 32 + i * 16 + kq * 4 + r;
+            const uint32_t m = m0 + i * 16 + kq * 4 + r;
             if (m >= M) continue;
             const uint32_t yrow = list ? list[m] : m;
             if (EPI == PE_HC_UP) {
