@@ -77,6 +77,28 @@ CHK_DEV void load_x(const float* __restrict__ x, uint32_t xs, uint32_t nch, int 
     xf.sums();
 }
 
+// This lane's input chunks (ch = lir + c * LPR) of NB rows in nibble-plane
+// form, read from the workgroup's LDS image (xq_prep: [row][nch] chunks).
+// Lanes past the last chunk read chunk nch-1; the weight side masks them.
+template <int NB, int CPL>
+struct XqFrag {
+    XqChunk c[NB][CPL];
+
+    template <int LPR>
+    CHK_DEV void read(const XqChunk* lds, uint32_t nch, int lir) {
+#pragma unroll
+        for (int k = 0; k < CPL; ++k) {
+            const uint32_t ch = lir + k * LPR;
+            const uint32_t cc = ch < nch ? ch : nch - 1;
+#pragma unroll
+            for (int b = 0; b < NB; ++b) c[b][k] = lds[b * nch + cc];
+        }
+    }
+};
+
+// Dynamic LDS of the matvec kernels: the nibble-plane image of their inputs.
+extern __shared__ XqChunk xq_lds[];
+
 // R rows of a Q4 matrix as this lane sees them: issue() starts every load
 // (unconditionally, raw bf16 scale/bias kept undecoded so nothing waits),
 // dot() consumes them against the lane's input chunks and reduces over the
@@ -104,9 +126,9 @@ struct Q4Frag {
         }
     }
 
+    // against inputs in nibble planes (the u4 dot8 form, device.h)
     template <int NB>
-    CHK_DEV void dot(const XFrag<NB, CPL>& xf, float (&acc)[R][NB]) const {
-        const Q4Consts k;
+    CHK_DEV void dot(const XqFrag<NB, CPL>& xf, float (&acc)[R][NB]) const {
 #pragma unroll
         for (int i = 0; i < R; ++i)
 #pragma unroll
@@ -114,8 +136,7 @@ struct Q4Frag {
                 float a = 0.0f;
 #pragma unroll
                 for (int c = 0; c < CPL; ++c) {
-                    const float p = q4_chunk_h(wq[i][c], xf.hi[b][c], xf.lo[b][c], xf.s[b][c], bf16f(s16[i][c]),
-                                               bf16f(b16[i][c]), k);
+                    const float p = q4_dot8(wq[i][c], xf.c[b][c], bf16f(s16[i][c]), bf16f(b16[i][c]));
                     a += ok[c] ? p : 0.0f;
                 }
                 acc[i][b] = group_sum<LPR>(a);
@@ -124,7 +145,7 @@ struct Q4Frag {
 };
 
 template <int LPR, int CPL, int R, int NB>
-CHK_DEV void q4_block(const Q4Mat& m, const uint32_t (&rows)[R], const XFrag<NB, CPL>& xr, int lir,
+CHK_DEV void q4_block(const Q4Mat& m, const uint32_t (&rows)[R], const XqFrag<NB, CPL>& xr, int lir,
                       float (&acc)[R][NB]) {
     Q4Frag<LPR, CPL, R> f;
     f.issue(m, rows, lir);
@@ -209,12 +230,17 @@ struct ExpFrag {
         }
     }
 
+    // Q4 records: inputs in nibble planes
+    template <int NB>
+    CHK_DEV void dot(const XqFrag<NB, CPL>& xr, float (&acc)[R][NB]) const {
+        static_assert(BITS == 4, "low-bit records take f32 inputs");
+        q.template dot<NB>(xr, acc);
+    }
+
+    // Q3/Q2 records: f32 inputs
     template <int NB>
     CHK_DEV void dot(const XFrag<NB, CPL>& xr, float (&acc)[R][NB]) const {
-        if (BITS == 4) {
-            q.template dot<NB>(xr, acc);
-            return;
-        }
+        static_assert(BITS != 4, "Q4 records take nibble-plane inputs");
 #pragma unroll
         for (int i = 0; i < R; ++i)
 #pragma unroll
@@ -232,13 +258,6 @@ struct ExpFrag {
     }
 };
 
-template <int LPR, int CPL, int R, int NB, int BITS>
-CHK_DEV void exp_block(const ExpMat& m, const uint32_t (&rows)[R], const XFrag<NB, CPL>& xr, int lir,
-                       float (&acc)[R][NB]) {
-    ExpFrag<LPR, CPL, R, BITS> f;
-    f.issue(m, rows, lir);
-    f.template dot<NB>(xr, acc);
-}
 
 
 // ------------------------------------------------------------------ embed
@@ -374,8 +393,6 @@ __global__ void __launch_bounds__(256) k_hc_up_mix(HcDev w, const float* __restr
     }
     Q4Frag<LPR, 1, R> f;
     f.issue(w.up, rows, lir);
-    XFrag<NB, 1> xr;
-    load_x<LPR, 1, NB>(d, w.down.out, w.up.in >> 5, lir, xr);
     // the row-group leader prefetches normed = hyper * inv * w for its outputs
     float normed[R][NB];
     if (lir == 0 && slot_ok) {
@@ -388,6 +405,9 @@ __global__ void __launch_bounds__(256) k_hc_up_mix(HcDev w, const float* __restr
             for (int b = 0; b < NB; ++b) normed[i][b] = hyper[(size_t)b * H * hc + j] * inv[b * hc + g] * wn;
         }
     }
+    xq_prep(d, w.down.out, w.up.in, NB, xq_lds, XqIdentity{});
+    XqFrag<NB, 1> xr;
+    xr.template read<LPR>(xq_lds, w.up.in >> 5, lir);
     float acc[R][NB];
     f.template dot<NB>(xr, acc);
     if (lir == 0 && slot_ok) {
@@ -500,8 +520,14 @@ template <int CPL, int R, int NB>
 __global__ void __launch_bounds__(256) k_qmv(SegArgs a) {
     const int lane = threadIdx.x & 63;
     const uint32_t groups = (a.total + R - 1) / R;
-    for (uint32_t grp = global_wave(); grp < groups; grp += total_waves()) {
-        const uint32_t row0 = grp * R;
+    const uint32_t nch = a.seg[0].m.in >> 5;  // every segment shares x (launch_qmv checks)
+    XqFrag<NB, CPL> xr;
+    // The first pass issues its weight and epilogue loads before the
+    // workgroup quantises x; waves without a group still join that prep.
+    for (uint32_t grp = global_wave(), pass = 0;; grp += total_waves(), ++pass) {
+        const bool live = grp < groups;
+        if (!live && pass > 0) break;
+        const uint32_t row0 = (live ? grp : 0) * R;
         int si = 0;
 #pragma unroll
         for (int k = 1; k < MAX_SEG; ++k)
@@ -512,16 +538,19 @@ __global__ void __launch_bounds__(256) k_qmv(SegArgs a) {
 #pragma unroll
         for (int i = 0; i < R; ++i) rows[i] = min(row0 - sg.row0 + i, sg.m.out - 1);
         Q4Frag<64, CPL, R> f;
-        f.issue(sg.m, rows, lane);
-        XFrag<NB, CPL> xr;
-        load_x<64, CPL, NB>(sg.x, sg.xs, sg.m.in >> 5, lane, xr);
+        if (live) f.issue(sg.m, rows, lane);
         // lane i < R owns row i's epilogue; its inputs load alongside the weights
         uint32_t my_row = rows[0];
 #pragma unroll
         for (int i = 1; i < R; ++i)
             if (lane == i) my_row = rows[i];
         EpiIn e;
-        if (lane < R) epi_prefetch(a, sg, my_row, e);
+        if (live && lane < R) epi_prefetch(a, sg, my_row, e);
+        if (pass == 0) {
+            xq_prep(a.seg[0].x, a.seg[0].xs, a.seg[0].m.in, NB, xq_lds, XqIdentity{});
+            xr.template read<64>(xq_lds, nch, lane);
+        }
+        if (!live) break;
         float acc[R][NB];
         f.template dot<NB>(xr, acc);
         float mine[NB];
@@ -541,6 +570,25 @@ __global__ void __launch_bounds__(256) k_qmv(SegArgs a) {
 // XM_DN_GATED: x is the DeltaNet core output y, gated here as
 // rmsnorm(y_head) * w * sigmoid(z) (cpu.rs:814-826, eps 1e-6), the head's
 // sum of squares coming from the scan's per-block partials.
+// XM_DN_GATED input transform: scale 8 inputs by their value head's
+// 1/sqrt(mean(y^2) + 1e-6), the head's sum of squares summed from the
+// scan's per-block partials.
+struct DnGateScale {
+    const InjArgs* a;
+    CHK_DEV void operator()(uint32_t b, uint32_t e, float (&v)[8]) const {
+        const uint32_t head = e / a->dv;
+        const float4* sp = reinterpret_cast<const float4*>(a->ssq + ((size_t)b * a->nheads + head) * a->ssq_blocks);
+        float ss = 0.0f;
+        for (uint32_t k = 0; k < a->ssq_blocks / 4; ++k) {
+            const float4 q = sp[k];
+            ss += (q.x + q.y) + (q.z + q.w);
+        }
+        const float inv = 1.0f / sqrtf(ss / (float)a->dv + 1e-6f);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] *= inv;
+    }
+};
+
 template <int CPL, int R, int NB, int XM>
 __global__ void __launch_bounds__(256) k_qmv_inject(InjArgs a) {
     const int lane = threadIdx.x & 63;
@@ -550,47 +598,29 @@ __global__ void __launch_bounds__(256) k_qmv_inject(InjArgs a) {
     // lane (i, g) = (lane / hc, lane % hc) owns hyper[b][g H + row_i]
     const uint32_t li = lane / a.hc, lg = lane % a.hc;
     const bool owner = li < (uint32_t)R && a.hyper;
-    bool first = true;
-    XFrag<NB, CPL> xr;
-    for (uint32_t grp = global_wave(); grp < groups; grp += total_waves()) {
+    XqFrag<NB, CPL> xr;
+    for (uint32_t grp = global_wave(), pass = 0;; grp += total_waves(), ++pass) {
+        const bool live = grp < groups;
+        if (!live && pass > 0) break;
+        const uint32_t g0 = live ? grp : 0;
         uint32_t rows[R];
 #pragma unroll
-        for (int i = 0; i < R; ++i) rows[i] = grp * R + i;
+        for (int i = 0; i < R; ++i) rows[i] = g0 * R + i;
         Q4Frag<64, CPL, R> f;
-        f.issue(m, rows, lane);
+        if (live) f.issue(m, rows, lane);
         float hy[NB], ij[NB];
-        if (owner)
+        if (live && owner)
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
-                hy[b] = a.hyper[(size_t)b * H * a.hc + lg * H + grp * R + li];
+                hy[b] = a.hyper[(size_t)b * H * a.hc + lg * H + g0 * R + li];
                 ij[b] = a.inj[b * a.hc + lg];
             }
-        if (first) {
-            first = false;
-            xr.template load<64>(a.x, a.xs, nch, lane);
-            if (XM == XM_DN_GATED) {
-                // x holds y * w * sigmoid(z); scale each 32-chunk by its
-                // head's 1/sqrt(mean(y^2) + 1e-6)
-#pragma unroll
-                for (int c = 0; c < CPL; ++c) {
-                    const uint32_t ch = min(lane + 64 * c, nch - 1);
-                    const uint32_t head = ch * 32 / a.dv;
-#pragma unroll
-                    for (int b = 0; b < NB; ++b) {
-                        const float4* sp = reinterpret_cast<const float4*>(a.ssq + ((size_t)b * a.nheads + head) * a.ssq_blocks);
-                        float ss = 0.0f;
-                        for (uint32_t k = 0; k < a.ssq_blocks / 4; ++k) {
-                            const float4 q = sp[k];
-                            ss += (q.x + q.y) + (q.z + q.w);
-                        }
-                        const float inv = 1.0f / sqrtf(ss / (float)a.dv + 1e-6f);
-#pragma unroll
-                        for (int j = 0; j < 32; ++j) xr.v[b][c][j] *= inv;
-                    }
-                }
-            }
-            xr.sums();
+        if (pass == 0) {
+            if (XM == XM_DN_GATED) xq_prep(a.x, a.xs, m.in, NB, xq_lds, DnGateScale{&a});
+            else xq_prep(a.x, a.xs, m.in, NB, xq_lds, XqIdentity{});
+            xr.template read<64>(xq_lds, nch, lane);
         }
+        if (!live) break;
         float acc[R][NB];
         f.template dot<NB>(xr, acc);
         if (a.raw_out && lane < R) {
@@ -773,17 +803,20 @@ __global__ void __launch_bounds__(256) k_moe_gate_up(MoeArgs a) {
     const int lane = threadIdx.x & 63;
     const uint32_t slots = a.topk + 1, blocks = a.I / R;
     const uint32_t tasks = a.nb * slots * blocks;
-    const uint32_t t = blockIdx.x * (CHK_WG >> 6) + wave_id();
-    if (t >= tasks) return;
+    const uint32_t t0 = blockIdx.x * (CHK_WG >> 6) + wave_id();
+    // waves past the last task still join the workgroup's input prep
+    const bool live = t0 < tasks;
+    const uint32_t t = live ? t0 : tasks - 1;
     const uint32_t b = t / (slots * blocks), slot = (t / blocks) % slots, i0 = (t % blocks) * R;
     uint32_t rows[R];
 #pragma unroll
     for (int i = 0; i < R; ++i) rows[i] = i0 + i;
-    // x loads first; nothing waits on them until the weights are in flight
-    XFrag<1, 1> xr;
-    xr.template load<64>(a.x + (size_t)b * a.H, 0, a.H >> 5, lane);
+    const uint32_t nch = a.H >> 5;
     const bool routed = slot < a.topk;
-    const bool publish = slot + 1 == a.topk && i0 == 0;
+    const bool publish = live && slot + 1 == a.topk && i0 == 0;
+    // f32 inputs only for low-bit records (their dot is not the dot8 form)
+    XFrag<1, 1> xr;
+    if (BITS != 4 && routed) xr.template load<64>(a.x + (size_t)b * a.H, 0, nch, lane);
     uint32_t my_id = 0;
     float my_p = 0.0f;
     if (routed)
@@ -792,38 +825,38 @@ __global__ void __launch_bounds__(256) k_moe_gate_up(MoeArgs a) {
     const uint32_t e = routed ? min((uint32_t)__builtin_amdgcn_readlane((int)my_id, (int)slot), a.X.experts - 1) : 0u;
     const uint8_t* rec = a.X.base + ((size_t)a.record_layer * a.X.experts + e) * a.X.stride;
     float g[R][1], u[R][1];
-    if (BITS == 4) {
-        // one straight path for routed and shared rows: only the matrices differ
+    // Q4 routed and shared rows share one straight path (only the matrices
+    // differ); low-bit routed rows take their own fragments.  The prep sits
+    // outside both so every wave reaches its barrier at the same point.
+    const bool q4path = BITS == 4 || !routed;
+    Q4Frag<64, 1, R> fg, fu;
+    ExpFrag<64, 1, R, BITS> lg, lu;
+    if (q4path) {
         Q4Mat mg = a.sh_gate, mu = a.sh_up;
-        if (routed) {
+        if (BITS == 4 && routed) {
             const ExpMat eg = expert_mat(a.X, rec, 0, a.I, a.H), eu = expert_mat(a.X, rec, 1, a.I, a.H);
             mg = Q4Mat{(const uint32_t*)eg.w, eg.s, eg.b, a.I, a.H};
             mu = Q4Mat{(const uint32_t*)eu.w, eu.s, eu.b, a.I, a.H};
         }
-        Q4Frag<64, 1, R> fg, fu;
         fg.issue(mg, rows, lane);
         fu.issue(mu, rows, lane);
-        if (publish) publish_routing(a, b, lane, my_id, my_p);
-        xr.sums();
-        fg.template dot<1>(xr, g);
-        fu.template dot<1>(xr, u);
-    } else if (routed) {
-        ExpFrag<64, 1, R, BITS> fg, fu;
-        fg.issue(expert_mat(a.X, rec, 0, a.I, a.H), rows, lane);
-        fu.issue(expert_mat(a.X, rec, 1, a.I, a.H), rows, lane);
-        if (publish) publish_routing(a, b, lane, my_id, my_p);
-        xr.sums();
-        fg.template dot<1>(xr, g);
-        fu.template dot<1>(xr, u);
-    } else {
-        Q4Frag<64, 1, R> fg, fu;
-        fg.issue(a.sh_gate, rows, lane);
-        fu.issue(a.sh_up, rows, lane);
-        xr.sums();
-        fg.template dot<1>(xr, g);
-        fu.template dot<1>(xr, u);
+    } else if (BITS != 4) {
+        lg.issue(expert_mat(a.X, rec, 0, a.I, a.H), rows, lane);
+        lu.issue(expert_mat(a.X, rec, 1, a.I, a.H), rows, lane);
     }
-    if (lane < R) {
+    if (publish) publish_routing(a, b, lane, my_id, my_p);
+    xq_prep(a.x, a.H, a.H, a.nb, xq_lds, XqIdentity{});
+    if (q4path) {
+        XqFrag<1, 1> xq;
+        xq.template read<64>(xq_lds + b * nch, nch, lane);
+        fg.template dot<1>(xq, g);
+        fu.template dot<1>(xq, u);
+    } else if constexpr (BITS != 4) {
+        xr.sums();
+        lg.template dot<1>(xr, g);
+        lu.template dot<1>(xr, u);
+    }
+    if (live && lane < R) {
         float gv = g[0][0], uv = u[0][0];
 #pragma unroll
         for (int i = 1; i < R; ++i)
@@ -846,21 +879,39 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a) {
     constexpr int G = 64 / LPR;
     const int lane = threadIdx.x & 63, grp = lane / LPR, lir = lane % LPR;
     const uint32_t slots = a.topk + 1;
-    const uint32_t groups = a.H / R;
+    const uint32_t groups = a.H / R, nch = a.I >> 5;
+    // routing of every row first (lane j < topk: slot j's id and weight;
+    // lane topk: the shared expert's gate), then the workgroup quantises
+    // all act rows [nb][slots][I] while those loads are in flight
+    uint32_t rid[4];
+    float rw[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        rid[b] = 0;
+        rw[b] = 0.0f;
+        if ((uint32_t)b < a.nb) {
+            if ((uint32_t)lane < a.topk) {
+                rid[b] = min(a.ids[b * a.topk + lane], a.X.experts - 1);
+                rw[b] = a.w[b * a.topk + lane];
+            } else if ((uint32_t)lane == a.topk) {
+                rw[b] = sigmoidf_(a.sg[b]);
+            }
+        }
+    }
+    xq_prep(a.act, a.I, a.I, a.nb * slots, xq_lds, XqIdentity{});
     for (uint32_t gi = global_wave(); gi < groups; gi += total_waves()) {
         uint32_t rows[R];
 #pragma unroll
         for (int i = 0; i < R; ++i) rows[i] = gi * R + i;
         for (uint32_t b = 0; b < a.nb; ++b) {
-            // routing of row b: lane j < topk holds slot j's id and weight
-            uint32_t my_id = 0;
-            float my_w = 0.0f;
-            if ((uint32_t)lane < a.topk) {
-                my_id = min(a.ids[b * a.topk + lane], a.X.experts - 1);
-                my_w = a.w[b * a.topk + lane];
-            } else if ((uint32_t)lane == a.topk) {
-                my_w = sigmoidf_(a.sg[b]);
-            }
+            uint32_t my_id = rid[0];
+            float my_w = rw[0];
+#pragma unroll
+            for (int k = 1; k < 4; ++k)
+                if (b == (uint32_t)k) {
+                    my_id = rid[k];
+                    my_w = rw[k];
+                }
             // hyper of this wave's rows, for the inject below
             const uint32_t li = lane / a.hc, lg = lane % a.hc;
             const bool owner = li < (uint32_t)R && a.hyper;
@@ -869,9 +920,12 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a) {
                 hy = a.hyper[(size_t)b * a.H * a.hc + lg * a.H + rows[0] + li];
                 ij = a.inj[b * a.hc + lg];
             }
-            ExpFrag<LPR, 1, R, BITS> f[PASSES];
-            Q4Frag<LPR, 1, R> fs;
+            // Q4: routed and shared slots share one path (per-lane matrices);
+            // low-bit routed slots take their own fragments and f32 inputs
+            Q4Frag<LPR, 1, R> fq[PASSES];
+            ExpFrag<LPR, 1, R, BITS> fl[PASSES];
             XFrag<1, 1> xr[PASSES];
+            XqFrag<1, 1> xq[PASSES];
             float wgt[PASSES];
 #pragma unroll
             for (int pass = 0; pass < PASSES; ++pass) {
@@ -880,13 +934,21 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a) {
                 const uint32_t e = __shfl(my_id, sl < a.topk ? sl : 0, 64);
                 wgt[pass] = __shfl(my_w, sl, 64);
                 if (slot >= slots) wgt[pass] = 0.0f;
-                if (sl < a.topk) {
-                    const uint8_t* rec = a.X.base + ((size_t)a.record_layer * a.X.experts + e) * a.X.stride;
-                    f[pass].issue(expert_mat(a.X, rec, 2, a.H, a.I), rows, lir);
+                const uint8_t* rec = a.X.base + ((size_t)a.record_layer * a.X.experts + e) * a.X.stride;
+                if (BITS == 4) {
+                    Q4Mat mm = a.sh_down;
+                    if (sl < a.topk) {
+                        const ExpMat em = expert_mat(a.X, rec, 2, a.H, a.I);
+                        mm = Q4Mat{(const uint32_t*)em.w, em.s, em.b, a.H, a.I};
+                    }
+                    fq[pass].issue(mm, rows, lir);
+                } else if (sl < a.topk) {
+                    fl[pass].issue(expert_mat(a.X, rec, 2, a.H, a.I), rows, lir);
+                    load_x<LPR, 1, 1>(a.act + ((size_t)b * slots + sl) * a.I, 0, nch, lir, xr[pass]);
                 } else {
-                    fs.issue(a.sh_down, rows, lir);
+                    fq[pass].issue(a.sh_down, rows, lir);
                 }
-                load_x<LPR, 1, 1>(a.act + ((size_t)b * slots + sl) * a.I, 0, a.I >> 5, lir, xr[pass]);
+                xq[pass].template read<LPR>(xq_lds + ((size_t)b * slots + sl) * nch, nch, lir);
             }
             float tot[R];
 #pragma unroll
@@ -896,8 +958,12 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a) {
                 const uint32_t slot = grp + pass * G;
                 const uint32_t sl = slot < slots ? slot : slots - 1;
                 float acc[R][1];
-                if (sl < a.topk) f[pass].template dot<1>(xr[pass], acc);
-                else fs.template dot<1>(xr[pass], acc);
+                if constexpr (BITS != 4) {
+                    if (sl < a.topk) fl[pass].template dot<1>(xr[pass], acc);
+                    else fq[pass].template dot<1>(xq[pass], acc);
+                } else {
+                    fq[pass].template dot<1>(xq[pass], acc);
+                }
 #pragma unroll
                 for (int i = 0; i < R; ++i) tot[i] += wgt[pass] * acc[i][0];
             }
@@ -928,15 +994,27 @@ __global__ void __launch_bounds__(256) k_lm_head(Q4Mat m, const float* __restric
     uint32_t bi[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) { bv[b] = -INFINITY; bi[b] = 0xffffffffu; }
-    XFrag<NB, 1> xr;
-    load_x<64, 1, NB>(x, m.in, m.in >> 5, lane, xr);
-    const uint32_t groups = m.out / R;
-    for (uint32_t grp = global_wave(); grp < groups; grp += total_waves()) {
-        uint32_t rows[R];
+    const uint32_t groups = m.out / R, nch = m.in >> 5;
+    // each wave's next row group is in flight while it reduces the current
+    // one; the first is issued before the workgroup quantises x
+    uint32_t grp = global_wave();
+    uint32_t rows[R];
 #pragma unroll
-        for (int i = 0; i < R; ++i) rows[i] = grp * R + i;
+    for (int i = 0; i < R; ++i) rows[i] = grp * R + i;
+    Q4Frag<64, 1, R> f;
+    if (grp < groups) f.issue(m, rows, lane);
+    xq_prep(x, m.in, m.in, NB, xq_lds, XqIdentity{});
+    XqFrag<NB, 1> xr;
+    xr.template read<64>(xq_lds, nch, lane);
+    while (grp < groups) {
+        const uint32_t nxt = grp + total_waves();
+        uint32_t nrows[R];
+#pragma unroll
+        for (int i = 0; i < R; ++i) nrows[i] = nxt * R + i;
+        Q4Frag<64, 1, R> fn;
+        if (nxt < groups) fn.issue(m, nrows, lane);
         float acc[R][NB];
-        q4_block<64, 1, R, NB>(m, rows, xr, lane, acc);
+        f.template dot<NB>(xr, acc);
 #pragma unroll
         for (int i = 0; i < R; ++i)
 #pragma unroll
@@ -944,6 +1022,10 @@ __global__ void __launch_bounds__(256) k_lm_head(Q4Mat m, const float* __restric
                 if (lane == i) logits[(size_t)b * m.out + rows[i]] = acc[i][b];
                 if (acc[i][b] > bv[b] || (acc[i][b] == bv[b] && rows[i] < bi[b])) { bv[b] = acc[i][b]; bi[b] = rows[i]; }
             }
+        f = fn;
+        grp = nxt;
+#pragma unroll
+        for (int i = 0; i < R; ++i) rows[i] = nrows[i];
     }
     if (lane == 0)
 #pragma unroll
@@ -1004,6 +1086,19 @@ static uint32_t grid_for(uint32_t waves_needed, uint32_t cap = 2048) {
     return std::max<uint32_t>(1, std::min(g, cap));
 }
 
+// Dynamic LDS of a kernel that stages nrows input rows of K floats as
+// nibble planes (xq_prep), checked against gfx950's per-workgroup limit;
+// plain matvecs split their rows above XQ_LDS_SPLIT to keep occupancy.
+constexpr size_t XQ_LDS_MAX = 160 * 1024;
+constexpr size_t XQ_LDS_SPLIT = 64 * 1024;
+
+static size_t xq_bytes(uint32_t nrows, uint32_t K) {
+    if (K % 32) throw std::runtime_error("matvec input width must be a multiple of 32");
+    const size_t b = (size_t)nrows * (K / 32) * sizeof(XqChunk);
+    if (b > XQ_LDS_MAX) throw std::runtime_error("matvec inputs exceed the workgroup's LDS budget");
+    return b;
+}
+
 void launch_embed(const StepIn* in, uint32_t* tokens, uint32_t* rowpos, const Q4Mat& emb, float* hyper, uint32_t H,
                   uint32_t hc, int nb, hipStream_t st) {
     dim3 grid((H + 255) / 256, nb);
@@ -1031,7 +1126,8 @@ void launch_hc_up_mix(const HcDev& w, const float* hyper, const float* inv, cons
     constexpr int R = 2;
     const uint32_t outs_pw = (64 / lpr) / hc * R;
     const uint32_t grid = grid_for((H + outs_pw - 1) / outs_pw, 1u << 20);
-#define UPMIX(L) CHK_NB_SWITCH(nb, (k_hc_up_mix<L, R, NB><<<grid, 256, 0, st>>>(w, hyper, inv, d, mixed, H, hc)))
+    const size_t lds = xq_bytes(nb, w.up.in);
+#define UPMIX(L) CHK_NB_SWITCH(nb, (k_hc_up_mix<L, R, NB><<<grid, 256, lds, st>>>(w, hyper, inv, d, mixed, H, hc)))
     switch (lpr) {
     case 2: UPMIX(2); break;
     case 4: UPMIX(4); break;
@@ -1045,7 +1141,27 @@ void launch_qmv(const SegArgs& a, int nb, hipStream_t st) {
     const uint32_t in = a.seg[0].m.in;
     const uint32_t cpl = (in / 32 + 63) / 64;
     if (cpl > 4) throw std::runtime_error("matvec input wider than 8192");
-#define QMV(C, R) CHK_NB_SWITCH(nb, (k_qmv<C, R, NB><<<grid_for((a.total + R - 1) / R), 256, 0, st>>>(a)))
+    bool raw = true;
+    for (int k = 0; k < a.nseg; ++k) {
+        if (a.seg[k].x != a.seg[0].x || a.seg[k].xs != a.seg[0].xs || a.seg[k].m.in != in)
+            throw std::runtime_error("segments of one matvec launch must share their input");
+        raw = raw && a.seg[k].epi == EPI_RAW;
+    }
+    // rows of plain segments are independent: split a launch whose staged
+    // inputs exceed the LDS budget (only wide test shapes reach this)
+    if (nb > 1 && raw && (size_t)nb * (in / 32) * sizeof(XqChunk) > XQ_LDS_SPLIT) {
+        const int h = nb / 2;
+        SegArgs lo = a, hi = a;
+        for (int k = 0; k < a.nseg; ++k) {
+            hi.seg[k].x += (size_t)h * a.seg[k].xs;
+            hi.seg[k].y += (size_t)h * a.seg[k].ys;
+        }
+        launch_qmv(lo, h, st);
+        launch_qmv(hi, nb - h, st);
+        return;
+    }
+    const size_t lds = xq_bytes(nb, in);
+#define QMV(C, R) CHK_NB_SWITCH(nb, (k_qmv<C, R, NB><<<grid_for((a.total + R - 1) / R), 256, lds, st>>>(a)))
     if (nb <= 2) {
         if (cpl <= 1) {
             QMV(1, 4);
@@ -1070,7 +1186,8 @@ void launch_qmv_inject(const InjArgs& a, int nb, hipStream_t st) {
     const uint32_t cpl = (a.m.in / 32 + 63) / 64;
     constexpr int R = 2;
     const uint32_t grid = grid_for(a.m.out / R);
-#define INJ(C, X) CHK_NB_SWITCH(nb, (k_qmv_inject<C, R, NB, X><<<grid, 256, 0, st>>>(a)))
+    const size_t lds = xq_bytes(nb, a.m.in);
+#define INJ(C, X) CHK_NB_SWITCH(nb, (k_qmv_inject<C, R, NB, X><<<grid, 256, lds, st>>>(a)))
     if (a.xmode == XM_DN_GATED) {
         if (cpl <= 1) {
             INJ(1, XM_DN_GATED);
@@ -1103,10 +1220,11 @@ void launch_moe_gate_up(const MoeArgs& a, hipStream_t st) {
     if (a.topk >= 64 || a.E > 512 || a.E % 8 || a.I % RG) throw std::runtime_error("routing too wide");
     const uint32_t tasks = a.nb * (a.topk + 1) * (a.I / RG);
     const uint32_t grid = (tasks + 3) / 4;  // one task per wave
+    const size_t lds = xq_bytes(a.nb, a.H);
     switch (a.X.bits) {
-    case 3: k_moe_gate_up<RG, 3><<<grid, 256, 0, st>>>(a); break;
-    case 2: k_moe_gate_up<RG, 2><<<grid, 256, 0, st>>>(a); break;
-    default: k_moe_gate_up<RG, 4><<<grid, 256, 0, st>>>(a); break;
+    case 3: k_moe_gate_up<RG, 3><<<grid, 256, lds, st>>>(a); break;
+    case 2: k_moe_gate_up<RG, 2><<<grid, 256, lds, st>>>(a); break;
+    default: k_moe_gate_up<RG, 4><<<grid, 256, lds, st>>>(a); break;
     }
 }
 
@@ -1121,7 +1239,9 @@ void launch_moe_down(const MoeArgs& a, hipStream_t st) {
     if (passes > 4) throw std::runtime_error("too many experts per token for the down kernel");
     if (a.topk >= 64 || a.hc * RD > 64) throw std::runtime_error("routing too wide");
     const uint32_t gdown = grid_for(a.H / RD, 1024);
-#define DOWN(L, B, P) k_moe_down<L, RD, B, P><<<gdown, 256, 0, st>>>(a)
+    if (a.nb > 4) throw std::runtime_error("the down kernel takes at most 4 rows");
+    const size_t lds = xq_bytes(a.nb * slots, a.I);
+#define DOWN(L, B, P) k_moe_down<L, RD, B, P><<<gdown, 256, lds, st>>>(a)
 #define DOWNP(L, B)                           \
     switch (passes) {                         \
     case 1: DOWN(L, B, 1); break;             \
@@ -1149,13 +1269,10 @@ void launch_moe_down(const MoeArgs& a, hipStream_t st) {
 
 void launch_lm_head(const Q4Mat& m, const float* x, float* logits, float* pv, uint32_t* pi, uint32_t nparts,
                     uint32_t* out, int nb, hipStream_t st) {
-    if (nb <= 2) {
-        constexpr int R = 8;
-        CHK_NB_SWITCH(nb, (k_lm_head<R, NB><<<nparts, 256, 0, st>>>(m, x, logits, pv, pi)));
-    } else {
-        constexpr int R = 4;
-        CHK_NB_SWITCH(nb, (k_lm_head<R, NB><<<nparts, 256, 0, st>>>(m, x, logits, pv, pi)));
-    }
+    if (m.out % 4) throw std::runtime_error("LM head rows must be a multiple of 4");
+    const size_t lds = xq_bytes(nb, m.in);
+    constexpr int R = 4;
+    CHK_NB_SWITCH(nb, (k_lm_head<R, NB><<<nparts, 256, lds, st>>>(m, x, logits, pv, pi)));
     k_argmax_final<<<nb, 256, 0, st>>>(pv, pi, nparts, out);
 }
 

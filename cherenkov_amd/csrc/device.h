@@ -178,4 +178,125 @@ CHK_DEV float q4_chunk_h(uint4 wq, const h2 (&hi)[16], const h2 (&lo)[16], float
     return s * d + b * xsum;
 }
 
+// ---- inputs as fixed-point nibble planes (the u4 dot8 product)
+//
+// A 32-input chunk x_0..x_31 is held as u_j = rint((x_j - m) / d) in
+// [0, 2^(4 XQ_PLANES) - 1] with m = min_j x_j and d = (max - min) / (2^(4 XQ_PLANES) - 1),
+// split into XQ_PLANES planes of nibbles: plane p, word k holds bits
+// 4p..4p+3 of u_{8k+j} in nibble j.  A packed Q4 weight word holds q_{8k+j}
+// in nibble j, so v_dot8_u32_u4(word, plane p) = sum_j q_j nibble_p(u_j)
+// exactly, and
+//   sum_j q_j x_j ~= m Q + d sum_p 16^p dot8(w, plane_p),   Q = dot8(w, 0x11111111).
+// The plane sums are combined in two exact integer halves (planes 0-2 and
+// 3-5, each < 15 * 4095 * 32 < 2^21) before the f32 scale.  The one
+// approximation is the input's quantisation, |x - (m + d u)| <= d / 2: with
+// six planes, 2^-25 of the chunk's range, on a par with the f32 inputs'
+// own rounding.  The bias term uses the exact f32 chunk sum.  Per weight
+// word: 7 v_dot8 instead of the 16 VALU ops of the fp16 pair form above,
+// which is what keeps batch-1 matvecs HBM-bound.
+constexpr int XQ_PLANES = 6;
+constexpr float XQ_LEVELS = (float)((1u << (4 * XQ_PLANES)) - 1u);
+
+struct XqChunk {
+    uint4 p[XQ_PLANES];  // planes, words k = 0..3
+    float4 prm;          // (m, d, sum of the chunk's x, 0)
+};
+
+// Product of one Q4 weight chunk (4 words = 32 weights of one row) with an
+// input chunk, scaled: s * sum(q x) + b * sum(x) (quant.rs:70-85 per half group).
+CHK_DEV float q4_dot8(const uint4& w, const XqChunk& xc, float s, float b) {
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    uint32_t a[XQ_PLANES], q = 0u;
+#pragma unroll
+    for (int p = 0; p < XQ_PLANES; ++p) a[p] = 0u;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+#pragma unroll
+        for (int p = 0; p < XQ_PLANES; ++p) {
+            const uint4 P = xc.p[p];
+            const uint32_t pk = k == 0 ? P.x : k == 1 ? P.y : k == 2 ? P.z : P.w;
+            a[p] = __builtin_amdgcn_udot8(ws[k], pk, a[p], false);
+        }
+        q = __builtin_amdgcn_udot8(ws[k], 0x11111111u, q, false);
+    }
+    uint32_t lo = 0u, hi = 0u;
+#pragma unroll
+    for (int p = 0; p < XQ_PLANES; ++p) {
+        if (p < 3) lo += a[p] << (4 * p);
+        else hi += a[p] << (4 * (p - 3));
+    }
+    const float U = XQ_PLANES > 3 ? fmaf((float)hi, 4096.0f, (float)lo) : (float)lo;
+    return s * fmaf(xc.prm.x, (float)q, xc.prm.y * U) + b * xc.prm.z;
+}
+
+// Quantise one thread's 8 consecutive inputs (a quarter chunk; the four
+// quarters of a chunk sit in one lane quad) into its plane words.  Every
+// lane of the wave must call it (DPP quad reductions).  Returns the plane
+// words; the quad's lane 0 also gets the chunk's (m, d, sum).
+CHK_DEV void xq_quarter(const float (&v)[8], uint32_t (&P)[XQ_PLANES], float4& prm) {
+    float mn = v[0], mx = v[0], sm = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        mn = fminf(mn, v[j]);
+        mx = fmaxf(mx, v[j]);
+        sm += v[j];
+    }
+    mn = fminf(mn, CHK_DPPF(mn, 0xb1, 0xf, mn));
+    mn = fminf(mn, CHK_DPPF(mn, 0x4e, 0xf, mn));
+    mx = fmaxf(mx, CHK_DPPF(mx, 0xb1, 0xf, mx));
+    mx = fmaxf(mx, CHK_DPPF(mx, 0x4e, 0xf, mx));
+    sm += CHK_DPPF(sm, 0xb1, 0xf, 0.0f);
+    sm += CHK_DPPF(sm, 0x4e, 0xf, 0.0f);
+    const float range = mx - mn;
+    const float inv = range > 0.0f ? XQ_LEVELS / range : 0.0f;
+    constexpr uint32_t top = (1u << (4 * XQ_PLANES)) - 1u;
+    uint32_t u[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) u[j] = min(__float2uint_rn((v[j] - mn) * inv), top);
+#pragma unroll
+    for (int p = 0; p < XQ_PLANES; ++p) {
+        uint32_t w = 0u;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) w |= ((u[j] >> (4 * p)) & 15u) << (4 * j);
+        P[p] = w;
+    }
+    prm = make_float4(mn, range / XQ_LEVELS, sm, 0.0f);
+}
+
+// Workgroup-cooperative quantisation of nrows input rows of K floats (row
+// stride xs) into LDS chunks out[b * K/32 + c].  `xform(b, e, v)` may
+// rescale the 8 inputs starting at element e of row b before quantisation
+// (identity for plain inputs).  Every thread of the CHK_WG-thread workgroup
+// must call it with the same arguments; it ends with a barrier.  K must be
+// a multiple of 32.
+template <class F>
+CHK_DEV void xq_prep(const float* __restrict__ x, uint32_t xs, uint32_t K, uint32_t nrows, XqChunk* out, F&& xform) {
+    const uint32_t nblk = K >> 3, total = nrows * nblk;
+    for (uint32_t base = 0; base < total; base += CHK_WG) {
+        const uint32_t i = base + threadIdx.x;
+        const bool live = i < total;
+        const uint32_t ii = live ? i : total - 1;
+        const uint32_t b = ii / nblk, e = (ii % nblk) * 8;
+        const float4* p4 = reinterpret_cast<const float4*>(x + (size_t)b * xs + e);
+        const float4 v0 = p4[0], v1 = p4[1];
+        float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        xform(b, e, v);
+        uint32_t P[XQ_PLANES];
+        float4 prm;
+        xq_quarter(v, P, prm);
+        if (live) {
+            const uint32_t c = ii >> 2, k = ii & 3;
+            uint32_t* dst = reinterpret_cast<uint32_t*>(out + c);
+#pragma unroll
+            for (int p = 0; p < XQ_PLANES; ++p) dst[4 * p + k] = P[p];
+            if (k == 0) out[c].prm = prm;
+        }
+    }
+    __syncthreads();
+}
+
+struct XqIdentity {
+    CHK_DEV void operator()(uint32_t, uint32_t, float (&)[8]) const {}
+};
+
 }  // namespace chk
