@@ -111,6 +111,7 @@ SIGNATURES = [
     ("chk_pool_kind", u32, [P, u32]),
     ("chk_pool_bytes", u64, [P]),
     ("chk_last_routes", i32, [P, u32, u32, C.POINTER(u32), C.POINTER(f32)]),
+    ("chk_last_probs", i32, [P, u32, u32, P]),
     # kernels.h
     ("chk_q4_matvec", i32, [P, P, P, u32, u32, P, P, u32, P]),
     ("chk_q4_gemm", i32, [P, P, P, u32, u32, P, u32, P, P]),

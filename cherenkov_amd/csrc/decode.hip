@@ -287,7 +287,7 @@ __global__ void __launch_bounds__(256) k_embed(const StepIn* __restrict__ in, ui
 // A workgroup takes HR consecutive rows of [down; inject]; wave g takes hc
 // stream g, so its RMS is a wave reduction, its normalised inputs are
 // prepared once for all HR rows, and the per-stream partial dots meet in LDS.
-constexpr int HR = 4;
+constexpr int HR = 2;
 
 template <int CPL, int NB>
 __global__ void __launch_bounds__(256) k_hc_down(HcDev w, const float* __restrict__ hyper, float* __restrict__ d,
@@ -616,9 +616,35 @@ __global__ void __launch_bounds__(256) k_qmv_inject(InjArgs a) {
                 ij[b] = a.inj[b * a.hc + lg];
             }
         if (pass == 0) {
-            if (XM == XM_DN_GATED) xq_prep(a.x, a.xs, m.in, NB, xq_lds, DnGateScale{&a});
-            else xq_prep(a.x, a.xs, m.in, NB, xq_lds, XqIdentity{});
-            xr.template read<64>(xq_lds, nch, lane);
+            if (XM == XM_DN_GATED && a.x_xq) {
+                // the scan's chunks of y w sigmoid(z), scaled by their head's
+                // 1/rms: a common factor of m, d and the chunk sum
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) {
+                    const uint32_t cc = min(lane + 64u * c, nch - 1);
+                    const uint32_t head = cc * 32 / a.dv;
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) {
+                        XqChunk q = a.x_xq[(size_t)b * nch + cc];
+                        const float4* sp =
+                            reinterpret_cast<const float4*>(a.ssq + ((size_t)b * a.nheads + head) * a.ssq_blocks);
+                        float ss = 0.0f;
+                        for (uint32_t k = 0; k < a.ssq_blocks / 4; ++k) {
+                            const float4 v = sp[k];
+                            ss += (v.x + v.y) + (v.z + v.w);
+                        }
+                        const float inv = 1.0f / sqrtf(ss / (float)a.dv + 1e-6f);
+                        q.prm.x *= inv;
+                        q.prm.y *= inv;
+                        q.prm.z *= inv;
+                        xr.c[b][c] = q;
+                    }
+                }
+            } else {
+                if (XM == XM_DN_GATED) xq_prep(a.x, a.xs, m.in, NB, xq_lds, DnGateScale{&a});
+                else xq_prep(a.x, a.xs, m.in, NB, xq_lds, XqIdentity{});
+                xr.template read<64>(xq_lds, nch, lane);
+            }
         }
         if (!live) break;
         float acc[R][NB];
@@ -655,9 +681,12 @@ __global__ void __launch_bounds__(256) k_qmv_inject(InjArgs a) {
 // (cpu.rs:745-812); snapshots after rows < nb-1.  The gated RMSNorm needs
 // the whole head, so each wave leaves its share of sum(y^2) for the
 // out-projection's prologue.
+// A workgroup (two waves) takes 32 value lanes of one head, so each row's
+// gated outputs form one 32-value chunk that leaves in nibble planes too.
 template <int NB>
-__global__ void __launch_bounds__(64) k_dn_scan(DnScanArgs a) {
-    constexpr int DK = 128, TPC = 4, KPT = DK / TPC, COLS = 16;
+__global__ void __launch_bounds__(DN_SCAN_COLS * 4) k_dn_scan(DnScanArgs a) {
+    constexpr int DK = 128, TPC = 4, KPT = DK / TPC, COLS = DN_SCAN_COLS;
+    __shared__ float ys[COLS];
     const uint32_t blocks = a.dv / COLS;
     const uint32_t hv = blockIdx.x / blocks, blk = blockIdx.x % blocks;
     const int t = threadIdx.x, p = t % TPC;
@@ -718,13 +747,21 @@ __global__ void __launch_bounds__(64) k_dn_scan(DnScanArgs a) {
                 *reinterpret_cast<float4*>(pp + k) = make_float4(S[k], S[k + 1], S[k + 2], S[k + 3]);
         }
         // gated RMSNorm numerator: y * w * sigmoid(z); the head's
-        // 1/rms (from the partial sums of y^2) is applied by the consumer
+        // 1/rms (from the partial sums of y^2, one per 16 value lanes) is
+        // applied by the consumer
         const float ss = wave_sum(p == 0 ? y * y : 0.0f);
         if (p == 0) {
             const size_t j = (size_t)b * a.nv * a.dv + hv * a.dv + iv;
-            a.y[j] = y * bf16f(a.norm[iv]) * sigmoidf_(a.z[j]);
+            const float yv = y * bf16f(a.norm[iv]) * sigmoidf_(a.z[j]);
+            a.y[j] = yv;
+            ys[t / TPC] = yv;
         }
-        if (t == 0) a.ssq[((size_t)b * a.nv + hv) * blocks + blk] = ss;
+        if ((t & 63) == 0) a.ssq[((size_t)b * a.nv + hv) * (a.dv / 16) + blk * (COLS / 16) + (t >> 6)] = ss;
+        if (COLS == 32 && a.y_xq) {
+            __syncthreads();
+            if (t < 64) xq_chunk_store(ys, a.y_xq + (size_t)b * (a.nv * a.dv / COLS) + hv * blocks + blk, t);
+            __syncthreads();
+        }
     }
 #pragma unroll
     for (int k = 0; k < KPT; k += 4) *reinterpret_cast<float4*>(sp + k) = make_float4(S[k], S[k + 1], S[k + 2], S[k + 3]);
@@ -798,22 +835,32 @@ CHK_DEV void publish_routing(const MoeArgs& a, uint32_t b, int lane, uint32_t my
     }
 }
 
+// A workgroup of GU_WAVES waves covers one 32-row chunk of one (row, slot),
+// R = 32 / GU_WAVES rows per wave, so the chunk's act values meet in LDS
+// and leave quantised (act_xq, the down kernel's input form) as well as
+// in f32.
+#ifndef CHK_GU_WAVES
+#define CHK_GU_WAVES 8
+#endif
+constexpr uint32_t GU_WAVES = CHK_GU_WAVES;
+constexpr uint32_t GU_WG = 64 * GU_WAVES;
+
 template <int R, int BITS>
-__global__ void __launch_bounds__(256) k_moe_gate_up(MoeArgs a) {
+__global__ void __launch_bounds__(GU_WG) k_moe_gate_up(MoeArgs a) {
+    static_assert(R * GU_WAVES == 32, "a workgroup covers one 32-row chunk");
+    __shared__ float act_s[32];
     const int lane = threadIdx.x & 63;
-    const uint32_t slots = a.topk + 1, blocks = a.I / R;
-    const uint32_t tasks = a.nb * slots * blocks;
-    const uint32_t t0 = blockIdx.x * (CHK_WG >> 6) + wave_id();
-    // waves past the last task still join the workgroup's input prep
-    const bool live = t0 < tasks;
-    const uint32_t t = live ? t0 : tasks - 1;
-    const uint32_t b = t / (slots * blocks), slot = (t / blocks) % slots, i0 = (t % blocks) * R;
+    const uint32_t w = wave_id();
+    const uint32_t slots = a.topk + 1, cpr = a.I / 32;
+    const uint32_t task = blockIdx.x;
+    const uint32_t b = task / (slots * cpr), slot = (task / cpr) % slots, c = task % cpr;
+    const uint32_t i0 = c * 32 + w * R;
     uint32_t rows[R];
 #pragma unroll
     for (int i = 0; i < R; ++i) rows[i] = i0 + i;
     const uint32_t nch = a.H >> 5;
     const bool routed = slot < a.topk;
-    const bool publish = live && slot + 1 == a.topk && i0 == 0;
+    const bool publish = slot + 1 == a.topk && c == 0 && w == 0;
     // f32 inputs only for low-bit records (their dot is not the dot8 form)
     XFrag<1, 1> xr;
     if (BITS != 4 && routed) xr.template load<64>(a.x + (size_t)b * a.H, 0, nch, lane);
@@ -845,7 +892,7 @@ __global__ void __launch_bounds__(256) k_moe_gate_up(MoeArgs a) {
         lu.issue(expert_mat(a.X, rec, 1, a.I, a.H), rows, lane);
     }
     if (publish) publish_routing(a, b, lane, my_id, my_p);
-    xq_prep(a.x, a.H, a.H, a.nb, xq_lds, XqIdentity{});
+    xq_prep<GU_WG>(a.x, a.H, a.H, a.nb, xq_lds, XqIdentity{});
     if (q4path) {
         XqFrag<1, 1> xq;
         xq.template read<64>(xq_lds + b * nch, nch, lane);
@@ -856,7 +903,7 @@ __global__ void __launch_bounds__(256) k_moe_gate_up(MoeArgs a) {
         lg.template dot<1>(xr, g);
         lu.template dot<1>(xr, u);
     }
-    if (live && lane < R) {
+    if (lane < R) {
         float gv = g[0][0], uv = u[0][0];
 #pragma unroll
         for (int i = 1; i < R; ++i)
@@ -864,8 +911,12 @@ __global__ void __launch_bounds__(256) k_moe_gate_up(MoeArgs a) {
                 gv = g[i][0];
                 uv = u[i][0];
             }
-        a.act[((size_t)b * slots + slot) * a.I + i0 + lane] = siluf_(gv) * uv;
+        const float act = siluf_(gv) * uv;
+        a.act[((size_t)b * slots + slot) * a.I + i0 + lane] = act;
+        act_s[w * R + lane] = act;
     }
+    __syncthreads();
+    if (w == 0) xq_chunk_store(act_s, a.act_xq + ((size_t)b * slots + slot) * cpr + c, lane);
 }
 
 // ------------------------------------------------- experts: down + combine
@@ -880,9 +931,8 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a) {
     const int lane = threadIdx.x & 63, grp = lane / LPR, lir = lane % LPR;
     const uint32_t slots = a.topk + 1;
     const uint32_t groups = a.H / R, nch = a.I >> 5;
-    // routing of every row first (lane j < topk: slot j's id and weight;
-    // lane topk: the shared expert's gate), then the workgroup quantises
-    // all act rows [nb][slots][I] while those loads are in flight
+    // routing of every row (lane j < topk: slot j's id and weight; lane
+    // topk: the shared expert's gate); act comes quantised from gate/up
     uint32_t rid[4];
     float rw[4];
 #pragma unroll
@@ -898,7 +948,6 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a) {
             }
         }
     }
-    xq_prep(a.act, a.I, a.I, a.nb * slots, xq_lds, XqIdentity{});
     for (uint32_t gi = global_wave(); gi < groups; gi += total_waves()) {
         uint32_t rows[R];
 #pragma unroll
@@ -948,7 +997,7 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a) {
                 } else {
                     fq[pass].issue(a.sh_down, rows, lir);
                 }
-                xq[pass].template read<LPR>(xq_lds + ((size_t)b * slots + sl) * nch, nch, lir);
+                xq[pass].template read<LPR>(a.act_xq + ((size_t)b * slots + sl) * nch, nch, lir);
             }
             float tot[R];
 #pragma unroll
@@ -1186,7 +1235,8 @@ void launch_qmv_inject(const InjArgs& a, int nb, hipStream_t st) {
     const uint32_t cpl = (a.m.in / 32 + 63) / 64;
     constexpr int R = 2;
     const uint32_t grid = grid_for(a.m.out / R);
-    const size_t lds = xq_bytes(nb, a.m.in);
+    const size_t lds = (a.xmode == XM_DN_GATED && a.x_xq) ? 0 : xq_bytes(nb, a.m.in);
+    if (a.x_xq && a.xs != a.m.in) throw std::runtime_error("chunked inputs must be dense rows");
 #define INJ(C, X) CHK_NB_SWITCH(nb, (k_qmv_inject<C, R, NB, X><<<grid, 256, lds, st>>>(a)))
     if (a.xmode == XM_DN_GATED) {
         if (cpl <= 1) {
@@ -1205,7 +1255,9 @@ void launch_qmv_inject(const InjArgs& a, int nb, hipStream_t st) {
 }
 
 void launch_dn_scan(const DnScanArgs& a, int nb, hipStream_t st) {
-    CHK_NB_SWITCH(nb, (k_dn_scan<NB><<<a.nv * (a.dv / 16), 64, 0, st>>>(a)));
+    if (a.dv % 32) throw std::runtime_error("value head width must be a multiple of 32");
+    if (a.y_xq && DN_SCAN_COLS != 32) throw std::runtime_error("y chunks need 32-lane scan workgroups");
+    CHK_NB_SWITCH(nb, (k_dn_scan<NB><<<a.nv * (a.dv / DN_SCAN_COLS), DN_SCAN_COLS * 4, 0, st>>>(a)));
 }
 
 void launch_router(const RouterArgs& a, int nb, hipStream_t st) {
@@ -1216,15 +1268,18 @@ void launch_router(const RouterArgs& a, int nb, hipStream_t st) {
 }
 
 void launch_moe_gate_up(const MoeArgs& a, hipStream_t st) {
-    constexpr int RG = 4;
+    constexpr int RG = 32 / GU_WAVES;
     if (a.topk >= 64 || a.E > 512 || a.E % 8 || a.I % RG) throw std::runtime_error("routing too wide");
     const uint32_t tasks = a.nb * (a.topk + 1) * (a.I / RG);
-    const uint32_t grid = (tasks + 3) / 4;  // one task per wave
+    (void)tasks;
+    if (a.I % 32) throw std::runtime_error("expert width must be a multiple of 32");
+    if (!a.act_xq) throw std::runtime_error("the gate/up kernel needs the act chunk buffer");
+    const uint32_t grid = a.nb * (a.topk + 1) * (a.I / 32);  // one 32-row chunk per workgroup
     const size_t lds = xq_bytes(a.nb, a.H);
     switch (a.X.bits) {
-    case 3: k_moe_gate_up<RG, 3><<<grid, 256, lds, st>>>(a); break;
-    case 2: k_moe_gate_up<RG, 2><<<grid, 256, lds, st>>>(a); break;
-    default: k_moe_gate_up<RG, 4><<<grid, 256, lds, st>>>(a); break;
+    case 3: k_moe_gate_up<RG, 3><<<grid, GU_WG, lds, st>>>(a); break;
+    case 2: k_moe_gate_up<RG, 2><<<grid, GU_WG, lds, st>>>(a); break;
+    default: k_moe_gate_up<RG, 4><<<grid, GU_WG, lds, st>>>(a); break;
     }
 }
 
@@ -1240,8 +1295,7 @@ void launch_moe_down(const MoeArgs& a, hipStream_t st) {
     if (a.topk >= 64 || a.hc * RD > 64) throw std::runtime_error("routing too wide");
     const uint32_t gdown = grid_for(a.H / RD, 1024);
     if (a.nb > 4) throw std::runtime_error("the down kernel takes at most 4 rows");
-    const size_t lds = xq_bytes(a.nb * slots, a.I);
-#define DOWN(L, B, P) k_moe_down<L, RD, B, P><<<gdown, 256, lds, st>>>(a)
+#define DOWN(L, B, P) k_moe_down<L, RD, B, P><<<gdown, 256, 0, st>>>(a)
 #define DOWNP(L, B)                           \
     switch (passes) {                         \
     case 1: DOWN(L, B, 1); break;             \

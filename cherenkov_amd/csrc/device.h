@@ -248,31 +248,53 @@ CHK_DEV void xq_quarter(const float (&v)[8], uint32_t (&P)[XQ_PLANES], float4& p
     sm += CHK_DPPF(sm, 0xb1, 0xf, 0.0f);
     sm += CHK_DPPF(sm, 0x4e, 0xf, 0.0f);
     const float range = mx - mn;
-    const float inv = range > 0.0f ? XQ_LEVELS / range : 0.0f;
+    // v_rcp (1 ulp) instead of an IEEE divide: u only has to be a rounding
+    // of (x - m) / d to within a level, and d below is range / levels
+    const float inv = range > 0.0f ? XQ_LEVELS * __builtin_amdgcn_rcpf(range) : 0.0f;
     constexpr uint32_t top = (1u << (4 * XQ_PLANES)) - 1u;
+    static_assert(XQ_PLANES == 6, "the byte transpose below is written for six planes");
+    // u = round-half-up((x - m) / d), 24 bits
     uint32_t u[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) u[j] = min(__float2uint_rn((v[j] - mn) * inv), top);
+    for (int j = 0; j < 8; ++j) u[j] = min((uint32_t)fmaf(v[j] - mn, inv, 0.5f), top);
+    // Pair (u_2j, u_2j+1) -> t_j holds byte j of planes 0, 2, 4 in its
+    // bytes 0, 1, 2 (low nibble from u_2j, high nibble from u_2j+1), s_j the
+    // same for planes 1, 3, 5; v_perm_b32 then gathers byte j of the four
+    // pairs into each plane word.
+    uint32_t t[4], sv[4];
 #pragma unroll
-    for (int p = 0; p < XQ_PLANES; ++p) {
-        uint32_t w = 0u;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) w |= ((u[j] >> (4 * p)) & 15u) << (4 * j);
-        P[p] = w;
+    for (int j = 0; j < 4; ++j) {
+        t[j] = (u[2 * j] & 0x0F0F0Fu) | ((u[2 * j + 1] << 4) & 0xF0F0F0u);
+        sv[j] = ((u[2 * j] >> 4) & 0x0F0F0Fu) | (u[2 * j + 1] & 0xF0F0F0u);
     }
-    prm = make_float4(mn, range / XQ_LEVELS, sm, 0.0f);
+    // perm(a, b, sel): result byte i = byte sel_i of {a:b} (b is bytes 0-3)
+    const uint32_t a01 = __builtin_amdgcn_perm(t[1], t[0], 0x05010400u);   // t0.0 t1.0 t0.1 t1.1
+    const uint32_t a23 = __builtin_amdgcn_perm(t[3], t[2], 0x05010400u);
+    const uint32_t b01 = __builtin_amdgcn_perm(t[1], t[0], 0x07030602u);   // t0.2 t1.2 -- --
+    const uint32_t b23 = __builtin_amdgcn_perm(t[3], t[2], 0x07030602u);
+    const uint32_t c01 = __builtin_amdgcn_perm(sv[1], sv[0], 0x05010400u);
+    const uint32_t c23 = __builtin_amdgcn_perm(sv[3], sv[2], 0x05010400u);
+    const uint32_t d01 = __builtin_amdgcn_perm(sv[1], sv[0], 0x07030602u);
+    const uint32_t d23 = __builtin_amdgcn_perm(sv[3], sv[2], 0x07030602u);
+    P[0] = __builtin_amdgcn_perm(a23, a01, 0x05040100u);
+    P[2] = __builtin_amdgcn_perm(a23, a01, 0x07060302u);
+    P[4] = __builtin_amdgcn_perm(b23, b01, 0x05040100u);
+    P[1] = __builtin_amdgcn_perm(c23, c01, 0x05040100u);
+    P[3] = __builtin_amdgcn_perm(c23, c01, 0x07060302u);
+    P[5] = __builtin_amdgcn_perm(d23, d01, 0x05040100u);
+    prm = make_float4(mn, range * (1.0f / XQ_LEVELS), sm, 0.0f);
 }
 
 // Workgroup-cooperative quantisation of nrows input rows of K floats (row
 // stride xs) into LDS chunks out[b * K/32 + c].  `xform(b, e, v)` may
 // rescale the 8 inputs starting at element e of row b before quantisation
-// (identity for plain inputs).  Every thread of the CHK_WG-thread workgroup
+// (identity for plain inputs).  Every thread of the WGS-thread workgroup
 // must call it with the same arguments; it ends with a barrier.  K must be
 // a multiple of 32.
-template <class F>
+template <uint32_t WGS = CHK_WG, class F>
 CHK_DEV void xq_prep(const float* __restrict__ x, uint32_t xs, uint32_t K, uint32_t nrows, XqChunk* out, F&& xform) {
     const uint32_t nblk = K >> 3, total = nrows * nblk;
-    for (uint32_t base = 0; base < total; base += CHK_WG) {
+    for (uint32_t base = 0; base < total; base += WGS) {
         const uint32_t i = base + threadIdx.x;
         const bool live = i < total;
         const uint32_t ii = live ? i : total - 1;
@@ -293,6 +315,26 @@ CHK_DEV void xq_prep(const float* __restrict__ x, uint32_t xs, uint32_t K, uint3
         }
     }
     __syncthreads();
+}
+
+// One wave quantises 32 values (v32, e.g. in LDS) into the chunk *dst in
+// global memory: lanes 0..3 take 8 values each (the other quads repeat them
+// so the quad reductions stay defined), lanes 0..3 store the plane words
+// and lane 0 the chunk parameters.  Every lane of the wave must call it.
+CHK_DEV void xq_chunk_store(const float* v32, XqChunk* dst, int lane) {
+    const int k = lane & 3;
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = v32[8 * k + j];
+    uint32_t P[XQ_PLANES];
+    float4 prm;
+    xq_quarter(v, P, prm);
+    if (lane < 4) {
+        uint32_t* d = reinterpret_cast<uint32_t*>(dst);
+#pragma unroll
+        for (int p = 0; p < XQ_PLANES; ++p) d[4 * p + k] = P[p];
+        if (lane == 0) dst->prm = prm;
+    }
 }
 
 struct XqIdentity {

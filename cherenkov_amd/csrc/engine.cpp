@@ -100,6 +100,7 @@ struct Scratch {
     uint32_t* tokens;
     float *hyper, *hc_d, *hc_inv, *inj_a, *inj_m, *mixed;
     float *dn_conv, *dn_z, *dn_decay, *dn_beta, *dn_y, *dn_ssq;
+    XqChunk *dn_y_xq, *act_xq;
     float *q_raw, *k_raw, *v_raw, *idx_raw, *q_ready, *attn_out, *part;
     float *router_logits, *router_probs, *sg, *route_w, *act, *mix_out;
     uint32_t *route_ids, *counter;
@@ -473,6 +474,7 @@ struct ChkEngine {
         s.dn_decay = dalloc<float>(NB * D.nv);
         s.dn_beta = dalloc<float>(NB * D.nv);
         s.dn_y = dalloc<float>(NB * D.v_dim);
+        s.dn_y_xq = dalloc<XqChunk>(NB * D.v_dim / 32);
         s.dn_ssq = dalloc<float>((uint64_t)NB * D.nv * (D.dv / 16));
         s.q_raw = dalloc<float>(NB * 2 * D.nh * D.hd);
         s.k_raw = dalloc<float>(NB * D.kv_row);
@@ -488,6 +490,7 @@ struct ChkEngine {
         s.route_w = dalloc<float>((uint64_t)LR * NB * D.topk);
         s.sg = dalloc<float>(NB);
         s.act = dalloc<float>((uint64_t)NB * (D.topk + 1) * D.I);
+        s.act_xq = dalloc<XqChunk>((uint64_t)NB * (D.topk + 1) * (D.I / 32));
         s.mix_out = dalloc<float>(NB * D.H);
         s.counter = dalloc<uint32_t>(64);
         HIPCHK(hipMemsetAsync(s.counter, 0, 256, st));
@@ -576,6 +579,7 @@ struct ChkEngine {
         sa.z = s.dn_z;
         sa.norm = L.dn.norm;
         sa.y = s.dn_y;
+        sa.y_xq = DN_SCAN_COLS == 32 ? s.dn_y_xq : nullptr;
         sa.ssq = s.dn_ssq;
         sa.nk = D.nk;
         sa.nv = D.nv;
@@ -593,6 +597,7 @@ struct ChkEngine {
         ia.z = s.dn_z;
         ia.norm = L.dn.norm;
         ia.ssq = s.dn_ssq;
+        ia.x_xq = sa.y_xq;
         ia.dv = D.dv;
         ia.nheads = D.nv;
         ia.ssq_blocks = D.dv / 16;
@@ -672,6 +677,7 @@ struct ChkEngine {
         m.w = m.w_out;
         m.sg = s.sg;
         m.act = s.act;
+        m.act_xq = s.act_xq;
         m.hyper = hyper;
         m.inj = inj;
         m.raw_out = raw_out;
@@ -1513,6 +1519,15 @@ int chk_last_routes(const ChkEngine* e, uint32_t layer, uint32_t r, uint32_t* id
         uint64_t off = ((uint64_t)layer * MAX_NB + r) * e->D.topk;
         HIPCHK(hipMemcpy(ids, e->s.route_ids + off, e->D.topk * 4, hipMemcpyDeviceToHost));
         if (weights) HIPCHK(hipMemcpy(weights, e->s.route_w + off, e->D.topk * 4, hipMemcpyDeviceToHost));
+    })
+}
+
+int chk_last_probs(const ChkEngine* e, uint32_t layer, uint32_t r, float* probs) {
+    CHK_TRY({
+        ensure(layer < e->record_layers, "layer out of range");
+        ensure(r < MAX_NB, "row out of range");
+        const uint64_t off = ((uint64_t)layer * MAX_NB + r) * e->D.E;
+        HIPCHK(hipMemcpy(probs, e->s.router_probs + off, e->D.E * 4, hipMemcpyDeviceToHost));
     })
 }
 

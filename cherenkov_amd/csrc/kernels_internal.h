@@ -7,6 +7,14 @@ namespace chk {
 
 constexpr int MAX_SEG = 5;
 
+// Value lanes per DeltaNet scan workgroup: 32 makes each workgroup's
+// outputs one nibble-plane chunk for the out-projection (16: plain f32 y,
+// quantised by the consumer).
+#ifndef CHK_DN_SCAN_COLS
+#define CHK_DN_SCAN_COLS 32
+#endif
+constexpr int DN_SCAN_COLS = CHK_DN_SCAN_COLS;
+
 enum Epi { EPI_RAW = 0, EPI_DN_CONV = 1, EPI_DN_DECAY = 2, EPI_DN_BETA = 3 };
 
 struct Seg {
@@ -42,6 +50,7 @@ struct DnScanArgs {
     const float* z;         // [nb][v_dim] output gate input
     const uint16_t* norm;   // [dv] gated-norm weight
     float* y;               // [nb][v_dim] y * w * sigmoid(z) (before the 1/rms)
+    XqChunk* y_xq;          // [nb][v_dim / 32] the same in nibble planes (optional)
     float* ssq;             // [nb][nv][dv / 16] partial sums of y^2
     uint32_t nk, nv, dv, qk_dim, conv_dim;
     float qscale;
@@ -59,6 +68,7 @@ struct InjArgs {
     const float* z;         // [nb][in] (same stride as x)
     const uint16_t* norm;   // [dv]
     const float* ssq;       // [nb][nheads][ssq_blocks]
+    const XqChunk* x_xq;    // [nb][in / 32] x in nibble planes before the 1/rms (optional)
     uint32_t dv, nheads, ssq_blocks;
     float* hyper;  // [nb][hc H] (null: no inject)
     const float* inj;
@@ -92,6 +102,7 @@ struct MoeArgs {
     const float* w;        // [nb][topk]
     const float* sg;       // [nb] shared gate logit
     float* act;            // [nb][topk + 1][I]
+    XqChunk* act_xq;       // [nb][topk + 1][I / 32] act in nibble planes
     float* hyper;          // [nb][hc H] (null: no inject)
     const float* inj;      // [nb][hc]
     float* raw_out;        // [nb][H] (optional)

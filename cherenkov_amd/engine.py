@@ -122,6 +122,11 @@ class Engine:
         check(self.L.chk_last_routes(self._h, layer, row, ids, w))
         return list(ids), list(w)
 
+    def last_probs(self, layer: int, row: int) -> np.ndarray:
+        p = np.empty(self.cfg.num_experts, np.float32)
+        check(self.L.chk_last_probs(self._h, layer, row, p.ctypes.data))
+        return p
+
     # ---- tracing / kernel-level helpers ----
     def trace(self, on: bool = True) -> None:
         check(self.L.chk_trace_enable(self._h, int(on)))

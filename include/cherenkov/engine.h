@@ -108,6 +108,11 @@ uint64_t chk_pool_bytes(const ChkEngine* e);
 /* Per-step expert activity (gpu/activity.rs:110): routed ids of row r of
  * the last step for layer l (num_experts_per_tok entries). */
 int chk_last_routes(const ChkEngine* e, uint32_t layer, uint32_t r, uint32_t* ids, float* weights);
+/* Router softmax (num_experts entries) behind those routes, for row r of
+ * the last row-path step at layer l: the margin of the top-k cut is what
+ * the parity bar exempts near-ties on (diagnostic; no reference
+ * counterpart beyond activity.rs, whose per-expert counts come from it). */
+int chk_last_probs(const ChkEngine* e, uint32_t layer, uint32_t r, float* probs);
 
 /* ---- runner: the greedy speculative decode loop ----
  * Decode::new / Decode::step (src/runner/decode.rs:28-171) for the greedy

@@ -14,7 +14,7 @@ from cherenkov_amd import presets
 from cherenkov_amd.abi import check, lib
 from cherenkov_amd.engine import Engine
 from oracle.oracle import OracleModel, q4_matvec
-from tests.gpu_util import argmax_margin, assert_close, empty_dev, to_dev, to_host
+from tests.gpu_util import argmax_margin, assert_close, empty_dev, to_dev, to_host, topk_margin
 from tests.numerics import bf16_bits
 
 pytestmark = pytest.mark.gpu
@@ -178,9 +178,20 @@ def test_gemm_prefill_full_shape(have_gpu):
         nxt_a, _ = a.prefill_chunk(prompt)
         la = a.logits_row(0)
         nxt_b, lb = row_prefill(b, prompt)
-        assert_close(la, lb, "full-shape 8-token prefill logits")
-        if argmax_margin(lb) > 1e-3:
-            assert nxt_a == nxt_b
+        # The north-star bar applied end to end: the last row's logits agree
+        # unless some layer's top-10 cut parts the two paths, and a parting
+        # is allowed only at a near-tie of the reference (row) path, margin
+        # <= 1e-3 (beyond it the stacks run different experts).
+        k = cfg.num_experts_per_tok
+        first = next((l for l in range(cfg.num_hidden_layers)
+                      if sorted(a.last_routes(l, 0)[0]) != sorted(b.last_routes(l, 0)[0])), None)
+        if first is None:
+            assert_close(la, lb, "full-shape 8-token prefill logits")
+            if argmax_margin(lb) > 1e-3:
+                assert nxt_a == nxt_b
+        else:
+            margin = topk_margin(b.last_probs(first, 0), k)
+            assert margin <= 1e-3, f"routes part at layer {first} with top-{k} margin {margin:.2e}"
         a.reset()
         b.reset()
         prompt = rng.integers(0, cfg.vocab_size, size=256).tolist()
