@@ -186,7 +186,7 @@ def main() -> int:
             "expert_bits": args.experts,
             "context_at_mid_decode": ctx_mid,
             "prefill_tok_s": round(args.prompt / prefill_s, 2),
-            "prefill_path": "row path (4 rows per step)",
+            "prefill_path": "MFMA Q4 GEMM chunk (one chunk of up to 4096 rows, layer by layer)",
             "step_launch": "one captured HIP graph per step",
         },
         "roofline": {

@@ -692,9 +692,12 @@ struct ChkEngine {
     // algorithmic bytes of the gate/up kernel: each routed row-slot's gate
     // and up matrices + the shared expert's, the router logits, the input
     // rows and the activations written
+    // (routed and shared gate/up matrices; logits, x and the act rows out,
+    // in f32 and as nibble-plane chunks)
     uint64_t gate_up_bytes(const LayerDev& L, int nb) const {
         return (uint64_t)nb * D.topk * 2 * expert_mat_bytes() + 2 * q4_bytes(L.moe.sh_gate) +
-               (uint64_t)nb * (D.E * 4 + D.H * 4 + (D.topk + 1) * D.I * 4);
+               (uint64_t)nb * (D.E * 4 + D.H * 4 + (D.topk + 1) * D.I * 4 +
+                               (uint64_t)(D.topk + 1) * (D.I / 32) * sizeof(XqChunk));
     }
 
     void moe(const LayerDev& L, uint32_t route_slot, const float* x, int nb, float* hyper, const float* inj,
