@@ -12,11 +12,36 @@
 
 namespace chk {
 
+// rms_norm then rope_partial at position `pos` of one vector held one
+// element per thread (d < n live), as cpu.rs:575-587 and 676-681 apply them
+// to q/k heads and to the indexer's query heads.
+CHK_DEV float norm_rope(float x, bool live, uint32_t d, uint32_t n, const uint16_t* w, float eps, uint32_t rot,
+                        float theta, uint32_t pos, float* red, float* sx) {
+    const float ss = block_sum(live ? x * x : 0.0f, red);
+    const float inv = 1.0f / sqrtf(ss / (float)n + eps);
+    if (live) {
+        x = x * inv * bf16f(w[d]);
+        sx[d] = x;
+    }
+    __syncthreads();
+    const uint32_t half = rot / 2;
+    if (d < rot) {
+        const uint32_t j = d < half ? d : d - half;
+        const float inv_freq = powf(theta, -(2.0f * (float)j) / (float)rot);
+        const float ang = (float)pos * inv_freq;
+        const float sn = sinf(ang), cs = cosf(ang);
+        const float av = sx[j], bv = sx[j + half];
+        x = d < half ? av * cs - bv * sn : bv * cs + av * sn;
+    }
+    return x;
+}
+
 // Per head: q RMSNorm + partial RoPE -> q_ready; k RMSNorm + RoPE -> q8 K
-// row; v -> q8 V row; the raw indexer key -> index cache.  One CHK_WG-thread
+// row; v -> q8 V row; the raw indexer key -> index cache; with QSA the
+// indexer's query heads, normed and roped -> iq_ready.  One CHK_WG-thread
 // workgroup per (row, item), thread d < hd owning dim d: items [0, nh) q
 // heads, [nh, nh + nkv) k heads, [nh + nkv, nh + 2 nkv) v heads,
-// nh + 2 nkv the index key.
+// nh + 2 nkv the index key, then inh index query heads.
 __global__ void __launch_bounds__(256) k_attn_prep(AttnArgs a) {
     __shared__ float red[8];
     __shared__ float sx[512];
@@ -28,6 +53,15 @@ __global__ void __launch_bounds__(256) k_attn_prep(AttnArgs a) {
         if (d < a.ihd) kv.index_k[(size_t)pos * a.ihd + d] = a.idx_raw[(size_t)b * (a.inh + 1) * a.ihd + a.inh * a.ihd + d];
         return;
     }
+    if (item > a.nh + 2 * a.nkv) {
+        // select_tokens' query heads (cpu.rs:676-681): index_q_norm, rope at pos
+        const uint32_t h = item - (a.nh + 2 * a.nkv + 1);
+        const bool il = d < a.ihd;
+        const float x0 = il ? a.idx_raw[(size_t)b * (a.inh + 1) * a.ihd + h * a.ihd + d] : 0.0f;
+        const float x = norm_rope(x0, il, d, a.ihd, a.iq_norm, a.eps, a.rot, a.theta, pos, red, sx);
+        if (il) a.iq_ready[((size_t)b * a.inh + h) * a.ihd + d] = x;
+        return;
+    }
     const bool is_q = item < a.nh, is_k = !is_q && item < a.nh + a.nkv;
     float x = 0.0f;
     if (live) {
@@ -35,25 +69,9 @@ __global__ void __launch_bounds__(256) k_attn_prep(AttnArgs a) {
         else if (is_k) x = a.k_raw[(size_t)b * a.nkv * hd + (item - a.nh) * hd + d];
         else x = a.v_raw[(size_t)b * a.nkv * hd + (item - a.nh - a.nkv) * hd + d];
     }
-    if (is_q || is_k) {
+    if (is_q || is_k)
         // nn::rms_norm (nn.rs:6-15) then rope_partial (cpu.rs:1051-1063)
-        const float ss = block_sum(x * x, red);
-        const float inv = 1.0f / sqrtf(ss / (float)hd + a.eps);
-        if (live) {
-            x = x * inv * bf16f(is_q ? a.q_norm[d] : a.k_norm[d]);
-            sx[d] = x;
-        }
-        __syncthreads();
-        const uint32_t half = a.rot / 2;
-        if (d < a.rot) {
-            uint32_t j = d < half ? d : d - half;
-            float inv_freq = powf(a.theta, -(2.0f * (float)j) / (float)a.rot);
-            float ang = (float)pos * inv_freq;
-            float sn = sinf(ang), cs = cosf(ang);
-            float av = sx[j], bv = sx[j + half];
-            x = d < half ? av * cs - bv * sn : bv * cs + av * sn;
-        }
-    }
+        x = norm_rope(x, live, d, hd, is_q ? a.q_norm : a.k_norm, a.eps, a.rot, a.theta, pos, red, sx);
     if (is_q) {
         if (live) a.q_ready[((size_t)b * a.nh + item) * hd + d] = x;
         return;
@@ -70,6 +88,184 @@ __global__ void __launch_bounds__(256) k_attn_prep(AttnArgs a) {
     uint16_t* sc = is_k ? kv.ks : kv.vs;
     plane[(size_t)pos * kv_row + kvh * hd + d] = (int8_t)qv;
     if ((d & 31) == 0) sc[(size_t)pos * (kv_row / 32) + (kvh * hd + d) / 32] = __half_as_ushort(__float2half_rn(dq));
+}
+
+
+// ---------------------------------------------------------------- QSA
+// select_tokens (cpu.rs:643-719) for rows whose complete blocks exceed the
+// budget: blocks of `ratio` tokens, scored by sum_h relu(q_h . key_b) /
+// sqrt(ihd) against the block's pooled key (mean of its index keys,
+// index_k_norm, rope at the block's first position); the top kblk blocks
+// (ties: lowest block) plus the incomplete tail stay visible.
+//
+// Row b's sequence started this batch at position pos0: rows of one
+// sequence are consecutive positions (decode verify rows, prefill rows).
+CHK_DEV uint32_t qsa_pos0(const AttnArgs& a, uint32_t b) {
+    return (a.one_kv || a.kv[b].index_k == a.kv[0].index_k) ? a.pos[0] : a.pos[b];
+}
+
+// Is row b past the budget (selective), and how many complete blocks has it?
+CHK_DEV bool qsa_selective(const AttnArgs& a, uint32_t b, uint32_t& nblk) {
+    nblk = (a.pos[b] + 1) / a.ratio;
+    return a.qsa && nblk > a.kblk;
+}
+
+// Block keys and block scores.  A wave takes QSA_BPW blocks of one row;
+// lane l holds dims l + 64 i.  A block whose last token arrived in this
+// batch gets its key computed here (from the index keys k_attn_prep just
+// appended) and cached in block_k; older blocks read the cache.  Rows that
+// are still dense only complete keys.
+constexpr uint32_t QSA_BPW = 8;
+constexpr uint32_t QSA_BPG = QSA_BPW * (CHK_WG / 64);
+
+template <int DPL>
+__global__ void __launch_bounds__(256) k_qsa_score(AttnArgs a) {
+    __shared__ float sq[8 * 256];
+    const uint32_t b = blockIdx.y, t = threadIdx.x, lane = t & 63, w = wave_id();
+    const KvDev& kv = a.kv[a.one_kv ? 0 : b];
+    uint32_t nblk;
+    const bool sel = qsa_selective(a, b, nblk);
+    const uint32_t pos0 = qsa_pos0(a, b);
+    if (sel)
+        for (uint32_t i = t; i < a.inh * a.ihd; i += CHK_WG) sq[i] = a.iq_ready[(size_t)b * a.inh * a.ihd + i];
+    __syncthreads();
+    const uint32_t half = a.rot / 2;
+    for (uint32_t j = 0; j < QSA_BPW; ++j) {
+        const uint32_t blk = blockIdx.x * QSA_BPG + w * QSA_BPW + j;
+        if (blk >= nblk) break;
+        const bool fresh = (blk + 1) * a.ratio - 1 >= pos0;
+        if (!fresh && !sel) continue;
+        float x[DPL];
+        if (fresh) {
+            // pooled mean, rms_norm(index_k_norm), rope at blk * ratio (cpu.rs:687-697)
+            float ss = 0.0f;
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) {
+                const uint32_t d = lane + 64 * i;
+                float p = 0.0f;
+                for (uint32_t tk = blk * a.ratio; tk < (blk + 1) * a.ratio; ++tk) p += kv.index_k[(size_t)tk * a.ihd + d];
+                x[i] = p / (float)a.ratio;
+                ss += x[i] * x[i];
+            }
+            const float inv = 1.0f / sqrtf(wave_sum(ss) / (float)a.ihd + a.eps);
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) x[i] = x[i] * inv * bf16f(a.ik_norm[lane + 64 * i]);
+            // rot <= 64: pair (j, j + half) sits in lanes (l, l ^ half) of slot 0
+            const float other = __shfl_xor(x[0], (int)half, 64);
+            if (lane < a.rot) {
+                const uint32_t jj = lane < half ? lane : lane - half;
+                const float inv_freq = powf(a.theta, -(2.0f * (float)jj) / (float)a.rot);
+                const float ang = (float)(blk * a.ratio) * inv_freq;
+                const float sn = sinf(ang), cs = cosf(ang);
+                x[0] = lane < half ? x[0] * cs - other * sn : x[0] * cs + other * sn;
+            }
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) kv.block_k[(size_t)blk * a.ihd + lane + 64 * i] = x[i];
+        } else {
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) x[i] = kv.block_k[(size_t)blk * a.ihd + lane + 64 * i];
+        }
+        if (!sel) continue;
+        float s = 0.0f;
+        for (uint32_t h = 0; h < a.inh; ++h) {
+            float dot = 0.0f;
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) dot += sq[h * a.ihd + lane + 64 * i] * x[i];
+            s += fmaxf(wave_sum(dot), 0.0f);
+        }
+        if (lane == 0) a.bscore[(size_t)b * a.max_blocks + blk] = s / sqrtf((float)a.ihd);
+    }
+}
+
+// The top kblk of a row's nblk block scores by (score desc, block asc):
+// scores are >= 0, so their bit patterns order like the floats.  A radix
+// select over four 8-bit digits finds the kblk-th largest key K and how
+// many blocks equal to K to keep; an ordered count over the blocks then
+// keeps the lowest-indexed of those.  One 1024-thread workgroup per row;
+// vmask gets one bit per selected complete block.
+constexpr uint32_t QSA_SEL_WG = 1024;
+constexpr uint32_t QSA_MAX_WORDS = 2048;  // 65536 blocks
+
+__global__ void __launch_bounds__(1024) k_qsa_select(AttnArgs a) {
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t s_key, s_need;
+    __shared__ uint32_t wsum[QSA_SEL_WG / 64];
+    __shared__ uint32_t mask[QSA_MAX_WORDS];
+    const uint32_t b = blockIdx.x, t = threadIdx.x, lane = t & 63, w = t >> 6;
+    uint32_t nblk;
+    if (!qsa_selective(a, b, nblk)) return;
+    const uint32_t* key = reinterpret_cast<const uint32_t*>(a.bscore + (size_t)b * a.max_blocks);
+    uint32_t prefix = 0, pmask = 0, need = a.kblk;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        if (t < 256) hist[t] = 0;
+        __syncthreads();
+        for (uint32_t i = t; i < nblk; i += QSA_SEL_WG) {
+            const uint32_t k = key[i];
+            if ((k & pmask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (w == 0) {
+            // lane l owns digits 255 - 4l .. 252 - 4l; find the digit where
+            // the count from the top reaches `need`
+            uint32_t c[4], tot = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                c[i] = hist[255 - 4 * lane - i];
+                tot += c[i];
+            }
+            uint32_t incl = tot;  // inclusive prefix over lanes 0..l (from the top digit down)
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t v = __shfl_up(incl, o, 64);
+                if (lane >= (uint32_t)o) incl += v;
+            }
+            const uint32_t above = incl - tot;
+            if (above < need && need <= incl) {
+                uint32_t cum = above;
+                int i = 0;
+                for (; i < 3; ++i) {
+                    if (cum + c[i] >= need) break;
+                    cum += c[i];
+                }
+                s_key = prefix | ((255u - 4u * lane - (uint32_t)i) << shift);
+                s_need = need - cum;
+            }
+        }
+        __syncthreads();
+        prefix = s_key;
+        need = s_need;
+        pmask |= 255u << shift;
+        __syncthreads();
+    }
+    // keep key > K, and the first `need` blocks (by index) with key == K
+    const uint32_t words = (nblk + 31) / 32;
+    for (uint32_t i = t; i < words; i += QSA_SEL_WG) mask[i] = 0u;
+    const uint32_t seg = (nblk + QSA_SEL_WG - 1) / QSA_SEL_WG;
+    const uint32_t lo = min(t * seg, nblk), hi = min(lo + seg, nblk);
+    uint32_t eq = 0;
+    for (uint32_t i = lo; i < hi; ++i) eq += key[i] == prefix;
+    // exclusive count of equal keys before this thread's segment
+    uint32_t incl = eq;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t v = __shfl_up(incl, o, 64);
+        if (lane >= (uint32_t)o) incl += v;
+    }
+    if (lane == 63) wsum[w] = incl;
+    __syncthreads();
+    uint32_t before = incl - eq;
+    for (uint32_t k = 0; k < w; ++k) before += wsum[k];
+    for (uint32_t i = lo; i < hi; ++i) {
+        const uint32_t k = key[i];
+        bool keep = k > prefix;
+        if (k == prefix) {
+            keep = before < need;
+            ++before;
+        }
+        if (keep) atomicOr(&mask[i >> 5], 1u << (i & 31));
+    }
+    __syncthreads();
+    for (uint32_t i = t; i < words; i += QSA_SEL_WG) a.vmask[(size_t)b * a.mask_words + i] = mask[i];
 }
 
 CHK_DEV float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
@@ -101,6 +297,9 @@ __global__ void __launch_bounds__(256) k_attn_part(AttnArgs a) {
     const uint32_t T = a.pos[b] + 1;  // causal: rows see positions <= their own
     const uint32_t t0 = c * CH;
     if (t0 >= T) return;
+    // QSA: past the budget only the selected complete blocks and the tail
+    uint32_t nblk;
+    const bool sel = qsa_selective(a, b, nblk);
     const KvDev& kv = a.kv[a.one_kv ? 0 : b];
     const uint32_t kv_row = a.nkv * HD, n = min((uint32_t)CH, T - t0);
 
@@ -144,6 +343,11 @@ __global__ void __launch_bounds__(256) k_attn_part(AttnArgs a) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) kf[k][j * 4 + e] = (float)(int8_t)(w[j] >> (8 * e));
     }
+    bool vis = true;
+    if (sel) {
+        const uint32_t tok = t0 + tk, blk = tok / a.ratio;
+        vis = blk >= nblk || ((a.vmask[(size_t)b * a.mask_words + (blk >> 5)] >> (blk & 31)) & 1u);
+    }
 #pragma unroll 1
     for (int g = 0; g < G; ++g) {
         float v = 0.0f;
@@ -160,7 +364,7 @@ __global__ void __launch_bounds__(256) k_attn_part(AttnArgs a) {
         }
         v += __shfl_xor(v, 1);
         v += __shfl_xor(v, 2);
-        if (qq == 0) sp[g][tk] = tk < n ? v * a.scale : -INFINITY;
+        if (qq == 0) sp[g][tk] = tk < n && vis ? v * a.scale : -INFINITY;
     }
     __syncthreads();
 
@@ -169,7 +373,8 @@ __global__ void __launch_bounds__(256) k_attn_part(AttnArgs a) {
     for (uint32_t g = wv; g < (uint32_t)G; g += 4) {
         const float s = sp[g][lane];
         const float m = wave_max(s);
-        const float p = lane < n ? expf(s - m) : 0.0f;
+        // a chunk may hold no visible token (QSA): then m = -inf and p = 0
+        const float p = lane < n && s != -INFINITY ? expf(s - m) : 0.0f;
         sp[g][lane] = p;
         const float l = wave_sum(p);
         if (lane == 0) {
@@ -295,11 +500,34 @@ void launch_attn_core(const AttnArgs& a, int nb, hipStream_t st) {
 
 void launch_attn_prep(const AttnArgs& a, int nb, hipStream_t st) {
     if (nb > MAX_NB && !a.one_kv) throw std::runtime_error("rows beyond the step batch must share one sequence");
-    k_attn_prep<<<dim3(a.nh + 2 * a.nkv + 1, nb), CHK_WG, 0, st>>>(a);
+    k_attn_prep<<<dim3(a.nh + 2 * a.nkv + 1 + (a.qsa ? a.inh : 0), nb), CHK_WG, 0, st>>>(a);
+}
+
+// Block keys, scores and selection; a no-op for rows still within the budget
+// (their block keys are still cached as blocks complete).
+void launch_qsa(const AttnArgs& a, int nb, hipStream_t st) {
+    if (!a.qsa) return;
+    if (a.ihd % 64 || a.ihd > 256 || a.rot > 64 || a.rot > a.ihd || (a.rot & (a.rot - 1)) || a.rot < 2 ||
+        a.inh * a.ihd > 8 * 256 ||
+        a.mask_words > QSA_MAX_WORDS || !a.iq_ready || !a.bscore || !a.vmask || !a.kv[0].block_k)
+        throw std::runtime_error("QSA indexer shape not supported");
+    const dim3 grid((a.max_blocks + QSA_BPG - 1) / QSA_BPG, nb);
+    switch (a.ihd / 64) {
+    case 1: k_qsa_score<1><<<grid, CHK_WG, 0, st>>>(a); break;
+    case 2: k_qsa_score<2><<<grid, CHK_WG, 0, st>>>(a); break;
+    default: k_qsa_score<4><<<grid, CHK_WG, 0, st>>>(a); break;
+    }
+    k_qsa_select<<<nb, QSA_SEL_WG, 0, st>>>(a);
+}
+
+void launch_qsa_select(const AttnArgs& a, int nb, hipStream_t st) {
+    if (a.mask_words > QSA_MAX_WORDS) throw std::runtime_error("more QSA blocks than one selection workgroup holds");
+    k_qsa_select<<<nb, QSA_SEL_WG, 0, st>>>(a);
 }
 
 void launch_attn(const AttnArgs& a, int nb, hipStream_t st) {
     launch_attn_prep(a, nb, st);
+    launch_qsa(a, nb, st);
     launch_attn_core(a, nb, st);
 }
 

@@ -102,6 +102,8 @@ struct Scratch {
     float *dn_conv, *dn_z, *dn_decay, *dn_beta, *dn_y, *dn_ssq;
     XqChunk *dn_y_xq, *act_xq;
     float *q_raw, *k_raw, *v_raw, *idx_raw, *q_ready, *attn_out, *part;
+    float *iq_ready, *bscore;  // QSA (allocated when some context can pass the budget)
+    uint32_t* vmask;
     float *router_logits, *router_probs, *sg, *route_w, *act, *mix_out;
     uint32_t *route_ids, *counter;
     float *logits, *pv;
@@ -345,6 +347,10 @@ struct ChkEngine {
         k.vs = dalloc<uint16_t>((uint64_t)max_t * D.kv_row / 32);
         k.index_k = dalloc<float>((uint64_t)max_t * D.ihd);
         kv_bytes += (uint64_t)max_t * (2 * D.kv_row + D.kv_row / 8 + 4 * D.ihd);
+        if (D.qsa) {
+            k.block_k = dalloc<float>((uint64_t)D.max_blocks * D.ihd);
+            kv_bytes += (uint64_t)D.max_blocks * D.ihd * 4;
+        }
         return k;
     }
 
@@ -373,10 +379,8 @@ struct ChkEngine {
                "at most 512 experts and 64 per token");
         ensure(c.ple_layer == 0, "PLE layers are not supported");
         ensure(c.linear_conv_kernel_dim >= 2 && c.linear_conv_kernel_dim <= 9, "conv kernel 2..=9");
-        // QSA selection only matters once complete blocks exceed the budget
-        // (cpu.rs:651-662); this engine runs the dense case.
-        ensure(o.max_t / c.indexer_compress_ratio <= c.indexer_budget / c.indexer_compress_ratio,
-               "contexts beyond indexer_budget need QSA selective attention, which this engine does not implement");
+        ensure(c.indexer_compress_ratio >= 1 && c.indexer_budget >= c.indexer_compress_ratio,
+               "indexer budget must hold at least one block");
         D.H = c.hidden_size;
         D.hc = c.hc_count;
         D.hh = D.H * D.hc;
@@ -397,6 +401,11 @@ struct ChkEngine {
         D.inh = c.indexer_n_heads;
         D.ihd = c.indexer_head_dim;
         D.idx_out = (D.inh + 1) * D.ihd;
+        D.ratio = c.indexer_compress_ratio;
+        D.kblk = c.indexer_budget / D.ratio;
+        D.max_blocks = o.max_t / D.ratio + 1;
+        D.mask_words = (D.max_blocks + 31) / 32;
+        D.qsa = o.max_t / D.ratio > D.kblk;
         D.E = c.num_experts;
         D.topk = c.num_experts_per_tok;
         D.I = c.moe_intermediate_size;
@@ -483,6 +492,11 @@ struct ChkEngine {
         s.q_ready = dalloc<float>(NB * D.nh * D.hd);
         s.attn_out = dalloc<float>(NB * D.nh * D.hd);
         s.part = dalloc<float>((uint64_t)NB * D.nh * max_chunks * (D.hd + 2));
+        if (D.qsa) {
+            s.iq_ready = dalloc<float>(NB * D.inh * D.ihd);
+            s.bscore = dalloc<float>((uint64_t)NB * D.max_blocks);
+            s.vmask = dalloc<uint32_t>((uint64_t)NB * D.mask_words);
+        }
         s.router_logits = dalloc<float>(NB * D.E);
         uint32_t LR = record_layers;
         s.router_probs = dalloc<float>((uint64_t)LR * NB * D.E);
@@ -645,6 +659,7 @@ struct ChkEngine {
         aa.eps = D.eps;
         aa.theta = D.theta;
         aa.scale = D.attn_scale;
+        set_qsa(aa, L);
         launch_attn(aa, nb, st);
         InjArgs ia{};
         ia.m = L.at.o;
@@ -656,6 +671,20 @@ struct ChkEngine {
         ia.hc = D.hc;
         ia.raw_out = raw_out;
         launch_qmv_inject(ia, nb, st);
+    }
+
+    // the QSA indexer's fields of an attention launch (dense: qsa = 0)
+    void set_qsa(AttnArgs& aa, const LayerDev& L) const {
+        aa.qsa = D.qsa;
+        aa.iq_norm = L.at.idx_q_norm;
+        aa.ik_norm = L.at.idx_k_norm;
+        aa.iq_ready = s.iq_ready;
+        aa.bscore = s.bscore;
+        aa.vmask = s.vmask;
+        aa.ratio = D.ratio;
+        aa.kblk = D.kblk;
+        aa.max_blocks = D.max_blocks;
+        aa.mask_words = D.mask_words;
     }
 
     MoeArgs moe_args(const LayerDev& L, uint32_t route_slot, const float* x, int nb, float* hyper, const float* inj,
@@ -1044,7 +1073,7 @@ constexpr uint32_t PF_MAX_ROWS = 4096;                  // rows per chunk (gpu/p
 constexpr uint64_t PF_PART_BYTES = 256ull << 20;        // attention partials per sub-batch
 
 bool ChkEngine::pf_supported() const {
-    return o.experts == 4 && !has_mtp && D.lowrank % 64 == 0 && D.H % 64 == 0 && D.H <= 4096 && D.hc <= 4 &&
+    return o.experts == 4 && !has_mtp && !D.qsa && D.lowrank % 64 == 0 && D.H % 64 == 0 && D.H <= 4096 && D.hc <= 4 &&
            (D.dv == 64 || D.dv == 128 || D.dv == 256) && D.I % 64 == 0 && (D.nh * D.hd) % 64 == 0 &&
            D.v_dim % 64 == 0 && D.E + 1 <= 513;
 }
@@ -1612,6 +1641,32 @@ int chk_attn_decode_q8(const float* q, const void* k, const void* v, const void*
         HIPCHK(hipGetLastError());
         HIPCHK(hipFree(q_ready));
         HIPCHK(hipFree(part));
+        HIPCHK(hipFree(pos));
+    })
+}
+
+int chk_qsa_select(const float* scores, uint32_t t_len, uint32_t kblk, uint32_t ratio, uint32_t* vmask, void* stream) {
+    CHK_TRY({
+        ensure(ratio >= 1 && kblk >= 1, "ratio and kblk must be positive");
+        ensure(t_len / ratio <= 65536, "at most 65536 blocks");
+        hipStream_t st = (hipStream_t)stream;
+        AttnArgs a{};
+        a.qsa = 1;
+        a.one_kv = 1;
+        a.ratio = ratio;
+        a.kblk = kblk;
+        a.max_blocks = t_len / ratio + 1;
+        a.mask_words = (a.max_blocks + 31) / 32;
+        a.bscore = const_cast<float*>(scores);
+        a.vmask = vmask;
+        uint32_t* pos = nullptr;
+        HIPCHK(hipMalloc(&pos, 4));
+        const uint32_t last = t_len - 1;
+        HIPCHK(hipMemcpyAsync(pos, &last, 4, hipMemcpyHostToDevice, st));
+        a.pos = pos;
+        launch_qsa_select(a, 1, st);
+        HIPCHK(hipStreamSynchronize(st));
+        HIPCHK(hipGetLastError());
         HIPCHK(hipFree(pos));
     })
 }

@@ -67,6 +67,8 @@ struct Dims {
     uint32_t nk, nv, dk, dv, qk_dim, v_dim, conv_dim, ck;
     uint32_t nh, nkv, hd, rot, kv_row;
     uint32_t inh, ihd, idx_out;
+    uint32_t ratio, kblk, max_blocks, mask_words;  // QSA blocks (cpu.rs:650-653)
+    int qsa;                                       // some context can pass the budget
     uint32_t E, topk, I, SI;
     uint32_t V;
     float eps, theta, attn_scale, qscale;
@@ -81,6 +83,7 @@ struct KvDev {
     uint16_t* ks;
     uint16_t* vs;
     float* index_k;  // [max_t][ihd]
+    float* block_k;  // [max_t / ratio][ihd] QSA block keys: pooled, normed, roped (null while dense)
 };
 
 // ----------------------------------------------------------- launchers

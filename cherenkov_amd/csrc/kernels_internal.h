@@ -256,6 +256,14 @@ struct AttnArgs {
     uint32_t nh, nkv, hd, rot, inh, ihd, max_chunks;
     float eps, theta, scale;
     int one_kv;            // every row belongs to kv[0]'s sequence (prefill rows)
+    // QSA indexer (cpu.rs:643-719); qsa = 0 keeps every row dense
+    int qsa;
+    const uint16_t* iq_norm;  // [ihd]
+    const uint16_t* ik_norm;  // [ihd]
+    float* iq_ready;          // [nb][inh][ihd] normed, roped index queries
+    float* bscore;            // [nb][max_blocks] block scores
+    uint32_t* vmask;          // [nb][mask_words] selected complete blocks
+    uint32_t ratio, kblk, max_blocks, mask_words;
 };
 
 // ------------------------------------------------------------- prefill
@@ -382,6 +390,7 @@ void launch_pf_embed(const uint32_t* tokens, const Q4Mat& emb, float* hyper, uin
                      hipStream_t st);
 void launch_pf_dn(const PfDnArgs& a, hipStream_t st);
 void launch_attn_prep(const AttnArgs& a, int nb, hipStream_t st);
+void launch_qsa_select(const AttnArgs& a, int nb, hipStream_t st);
 void launch_attn_core(const AttnArgs& a, int nb, hipStream_t st);
 bool attn_shape_ok(uint32_t nh, uint32_t nkv, uint32_t hd);
 void launch_copy_f32(float* dst, const float* src, uint64_t n, hipStream_t st);

@@ -58,7 +58,7 @@ def qwen3next_80b_shape(seed: int = 20261201, layers: int = 48, mtp: int = 1) ->
     )
 
 
-def tiny(seed: int = 1234, layers: int = 4, mtp: int = 1) -> ChkConfig:
+def tiny(seed: int = 1234, layers: int = 4, mtp: int = 1, indexer_budget: int = QSA_DENSE_BUDGET) -> ChkConfig:
     return make_config(
         hidden_size=512,
         num_hidden_layers=layers,
@@ -81,7 +81,7 @@ def tiny(seed: int = 1234, layers: int = 4, mtp: int = 1) -> ChkConfig:
         norm_topk_prob=1,
         indexer_n_heads=2,
         indexer_head_dim=128,
-        indexer_budget=QSA_DENSE_BUDGET,
+        indexer_budget=indexer_budget,
         indexer_compress_ratio=4,
         mtp_num_hidden_layers=mtp,
         eos_token_id=4095,

@@ -53,6 +53,14 @@ int chk_lm_head_argmax(const void* w, const void* s, const void* b, uint32_t out
 int chk_attn_decode_q8(const float* q, const void* k, const void* v, const void* ks, const void* vs, uint32_t T,
                        uint32_t nh, uint32_t nkv, uint32_t hd, float* out, void* stream);
 
+/* QSA block selection (select_tokens' sparse branch, cpu.rs:701-716; the
+ * Metal index_select kernel of kernels/qwen4_exp/qsa.metal): of the
+ * t_len / ratio complete blocks' scores (device f32, >= 0), keep the kblk
+ * largest, ties to the lowest block; vmask (device u32, one bit per block,
+ * ceil((t_len / ratio + 1) / 32) words) receives the selection.  Writes
+ * nothing while t_len / ratio <= kblk (the dense case). */
+int chk_qsa_select(const float* scores, uint32_t t_len, uint32_t kblk, uint32_t ratio, uint32_t* vmask, void* stream);
+
 /* MoE block of decoder layer `layer` (num_hidden_layers = the MTP layer) on
  * normalised inputs x [nb][H]: out [nb][H] = routed experts (per the
  * engine's expert precision) + sigmoid-gated shared expert; top_ids

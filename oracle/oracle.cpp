@@ -662,10 +662,32 @@ std::vector<float> moe(OrcModel& m, const MoeW& w, const float* x, uint32_t* top
     return out;
 }
 
-// select_tokens, src/qwen4_exp/cpu.rs:643-719.  Only the dense branch
-// (blocks <= budget / ratio) is reachable in the configurations this
-// library runs; the sparse branch is restated for completeness but its
-// parity is unpinned.
+// The selection tail of select_tokens (cpu.rs:701-716): blocks sorted by
+// (score desc, block asc), the first topk kept as token runs, the
+// incomplete tail appended, tokens ascending.  Pinned by the reference's
+// tie test (tests/unit/qwen4_exp/gpu/qsa.rs:300-372) restated in
+// tests/test_oracle.py.
+std::vector<size_t> qsa_pick(std::vector<std::pair<float, size_t>> bs, size_t topk, size_t ratio, size_t t_len) {
+    const size_t blocks = t_len / ratio;
+    std::sort(bs.begin(), bs.end(), [](const std::pair<float, size_t>& a, const std::pair<float, size_t>& b) {
+        int32_t ka = total_key(a.first), kb = total_key(b.first);
+        if (ka != kb) return ka > kb;
+        return a.second < b.second;
+    });
+    std::vector<size_t> sel;
+    for (size_t i = 0; i < topk; ++i)
+        for (size_t t = bs[i].second * ratio; t < (bs[i].second + 1) * ratio; ++t) sel.push_back(t);
+    for (size_t t = blocks * ratio; t < t_len; ++t) sel.push_back(t);
+    std::sort(sel.begin(), sel.end());
+    return sel;
+}
+
+// select_tokens, src/qwen4_exp/cpu.rs:643-719: dense while the complete
+// blocks fit the budget, else block scores (pooled index keys,
+// index_k_norm, rope at the block start, relu dots with the normed and
+// roped index queries) and qsa_pick.  Scoring is pinned by its parts'
+// closed forms (rms_norm, rope_partial) and, end to end, only against the
+// GPU's independent implementation (tests/test_gpu_qsa.py).
 std::vector<size_t> select_tokens(const OrcModel& m, const AttnW& w, const float* iq, const KvCache& cache,
                                   size_t pos) {
     const ChkConfig& c = m.c;
@@ -701,16 +723,7 @@ std::vector<size_t> select_tokens(const OrcModel& m, const AttnW& w, const float
         }
         bs.push_back({s / sqrtf((float)ihd), b});
     }
-    std::sort(bs.begin(), bs.end(), [](const std::pair<float, size_t>& a, const std::pair<float, size_t>& b) {
-        int32_t ka = total_key(a.first), kb = total_key(b.first);
-        if (ka != kb) return ka > kb;
-        return a.second < b.second;
-    });
-    for (size_t i = 0; i < topk; ++i)
-        for (size_t t = bs[i].second * ratio; t < (bs[i].second + 1) * ratio; ++t) sel.push_back(t);
-    for (size_t t = blocks * ratio; t < t_len; ++t) sel.push_back(t);
-    std::sort(sel.begin(), sel.end());
-    return sel;
+    return qsa_pick(std::move(bs), topk, ratio, t_len);
 }
 
 // attention, src/qwen4_exp/cpu.rs:544-641.  With `kv_q8`, cached K/V rows
@@ -926,6 +939,17 @@ struct OrcModel* make_model(const ChkConfig* cfg, uint32_t bits) {
 extern "C" {
 
 const char* orc_last_error(void) { return g_err.c_str(); }
+
+// qsa_pick over given block scores: vis receives the visible tokens
+// (capacity topk * ratio + ratio), *nvis their count.
+void orc_qsa_pick(const float* scores, uint32_t t_len, uint32_t topk, uint32_t ratio, uint32_t* vis, uint32_t* nvis) {
+    const size_t blocks = t_len / ratio;
+    std::vector<std::pair<float, size_t>> bs;
+    for (size_t b = 0; b < blocks; ++b) bs.push_back({scores[b], b});
+    const std::vector<size_t> sel = orc::qsa_pick(std::move(bs), topk, ratio, t_len);
+    for (size_t i = 0; i < sel.size(); ++i) vis[i] = (uint32_t)sel[i];
+    *nvis = (uint32_t)sel.size();
+}
 
 void* orc_model_new(const ChkConfig* cfg, uint32_t expert_bits) {
     if (!validate(*cfg) || (expert_bits != 2 && expert_bits != 3 && expert_bits != 4)) {

@@ -53,6 +53,7 @@ _SIGS = [
     ("orc_causal_conv", None, [P, u32, P, P, u32]),
     ("orc_expert_record", i32, [P, u32, u32, P, u64]),
     ("orc_record_stride", u64, [P]),
+    ("orc_qsa_pick", None, [P, u32, u32, u32, P, P]),
 ]
 
 _lib = None
@@ -193,6 +194,16 @@ class OracleState:
 
 
 # ---- primitives ----
+
+def qsa_pick(scores, t_len: int, topk: int, ratio: int) -> np.ndarray:
+    """Visible tokens of select_tokens' sparse branch for given block
+    scores (cpu.rs:701-716)."""
+    scores = np.ascontiguousarray(scores, dtype=np.float32)
+    vis = np.empty(topk * ratio + ratio, np.uint32)
+    n = C.c_uint32(0)
+    lib().orc_qsa_pick(_p(scores), t_len, topk, ratio, _p(vis), C.byref(n))
+    return vis[: n.value].copy()
+
 
 def q4_matvec(w, s, b, out_dim, in_dim, x) -> np.ndarray:
     y = np.empty(out_dim, np.float32)

@@ -364,3 +364,41 @@ def test_attention_core_reference_case():
     q, _, _, _, _, kd, vd, want = reference_attention_case(300)
     got = O.attend(q, kd.astype(np.float32), vd.astype(np.float32), 24, 2, 256)
     assert np.max(np.abs(got - want)) < 1e-5 * max(1.0, np.max(np.abs(want)))
+
+
+# ------------------------------------------------------------ QSA selection
+
+def _qsa_expect(scores, t_len, k, ratio):
+    """The reference test's construction (tests/unit/qwen4_exp/gpu/qsa.rs:
+    318-330): blocks ordered by (score desc, block asc), the first k as token
+    runs, the incomplete tail appended, ascending."""
+    n = t_len // ratio
+    order = sorted(range(n), key=lambda b: (-float(scores[b]), b))
+    vis = [t for b in order[:k] for t in range(b * ratio, (b + 1) * ratio)]
+    vis += list(range(n * ratio, t_len))
+    return sorted(vis)
+
+
+def test_qsa_pick_reference_ties():
+    """index_select_handles_ties (tests/unit/qwen4_exp/gpu/qsa.rs:300-372):
+    600 complete blocks + 2 tail tokens, five distinct values and many
+    zeros; ties go to the lowest block."""
+    ratio, k, base_pos = 4, 512, 2401
+    t_len = base_pos + 1
+    n = t_len // ratio
+    scores = np.array([0.0 if i % 3 == 0 else ((i * 7) % 5) * 0.5 for i in range(n + 8)], np.float32)
+    got = O.qsa_pick(scores[:n], t_len, k, ratio)
+    assert got.tolist() == _qsa_expect(scores, t_len, k, ratio)
+    assert got.size == k * ratio + 2
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_qsa_pick_random_with_duplicates(seed):
+    rng = np.random.default_rng(seed)
+    ratio = int(rng.choice([2, 4, 8]))
+    t_len = int(rng.integers(40, 3000))
+    n = t_len // ratio
+    k = int(rng.integers(1, n))
+    scores = rng.choice(np.float32([0.0, 0.25, 0.5, 1.5, 2.0]), size=n) + (rng.random(n) < 0.3) * rng.random(n).astype(np.float32)
+    got = O.qsa_pick(scores.astype(np.float32), t_len, k, ratio)
+    assert got.tolist() == _qsa_expect(scores.astype(np.float32), t_len, k, ratio)
