@@ -620,16 +620,14 @@ __global__ void __launch_bounds__(256) k_pf_router(const uint16_t* __restrict__ 
                                                    const uint4* __restrict__ bhi, const uint4* __restrict__ bmid,
                                                    const uint4* __restrict__ blo, float* __restrict__ logits,
                                                    float* __restrict__ sg, uint32_t T, uint32_t E, uint32_t H) {
+    // a workgroup covers 64 rows x 64 outputs, each wave one 16-output
+    // column tile over the 64 rows (4 accumulators), so the grid spreads
+    // the [T x (E + 1)] output over every CU
     const int lane = threadIdx.x & 63, col = lane & 15, kq = lane >> 4;
-    const uint32_t m0 = blockIdx.y * 64, n0 = blockIdx.x * 256 + wave_id() * 64, KB = H >> 3;
-    const uint4* bp[4];
-    uint32_t nn[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        nn[j] = n0 + j * 16 + col;
-        const uint32_t r = min(nn[j], E);
-        bp[j] = reinterpret_cast<const uint4*>(r < E ? router + (size_t)r * H : shared_gate);
-    }
+    const uint32_t m0 = blockIdx.y * 64, KB = H >> 3;
+    const uint32_t nn = blockIdx.x * 64 + wave_id() * 16 + col;
+    const uint32_t r = min(nn, E);
+    const uint4* bp = reinterpret_cast<const uint4*>(r < E ? router + (size_t)r * H : shared_gate);
     const uint4* ah[4];
     const uint4* am[4];
     const uint4* al[4];
@@ -640,39 +638,29 @@ __global__ void __launch_bounds__(256) k_pf_router(const uint16_t* __restrict__ 
         am[i] = bmid + (size_t)m * KB;
         al[i] = blo + (size_t)m * KB;
     }
-    f4 acc[4][4];
+    f4 acc[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < 4; ++i) acc[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     for (uint32_t k = 0; k < KB; k += 4) {
-        b8 bq[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) bq[j] = __builtin_bit_cast(b8, bp[j][k + kq]);
+        const b8 bq = __builtin_bit_cast(b8, bp[k + kq]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const b8 xh = __builtin_bit_cast(b8, ah[i][k + kq]);
             const b8 xm = __builtin_bit_cast(b8, am[i][k + kq]);
             const b8 xl = __builtin_bit_cast(b8, al[i][k + kq]);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, bq[j], acc[i][j], 0, 0, 0);
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xm, bq[j], acc[i][j], 0, 0, 0);
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, bq[j], acc[i][j], 0, 0, 0);
-            }
+            acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, bq, acc[i], 0, 0, 0);
+            acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xm, bq, acc[i], 0, 0, 0);
+            acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, bq, acc[i], 0, 0, 0);
         }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint32_t m = m0 + i * 16 + kq * 4 + r;
+        for (int rr = 0; rr < 4; ++rr) {
+            const uint32_t m = m0 + i * 16 + kq * 4 + rr;
             if (m >= T) continue;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                if (nn[j] < E) logits[(size_t)m * E + nn[j]] = acc[i][j][r];
-                else if (nn[j] == E) sg[m] = acc[i][j][r];
-            }
+            if (nn < E) logits[(size_t)m * E + nn] = acc[i][rr];
+            else if (nn == E) sg[m] = acc[i][rr];
         }
 }
 
@@ -860,7 +848,7 @@ __global__ void __launch_bounds__(256) k_pf_dn_misc(PfDnArgs a) {
 //   S <- decay S + k delta^T.
 // The q, k, v, decay, beta of row t + PF_SCAN_AHEAD load while row t
 // computes.
-constexpr int PF_SCAN_AHEAD = 4;
+constexpr int PF_SCAN_AHEAD = 16;
 
 __global__ void __launch_bounds__(64) k_pf_dn_scan(PfDnArgs a) {
     constexpr int DK = 128, KPL = 8, D = PF_SCAN_AHEAD;
@@ -1032,8 +1020,8 @@ void launch_pf_router(const uint16_t* router, const uint16_t* shared_gate, const
                       const uint4* blo, float* logits, float* sg, uint32_t T, uint32_t E, uint32_t H, hipStream_t st) {
     if (H % 32) throw std::runtime_error("router width must be a multiple of 32");
     if (T)
-        k_pf_router<<<dim3((E + 1 + 255) / 256, (T + 63) / 64), CHK_WG, 0, st>>>(router, shared_gate, bhi, bmid, blo,
-                                                                                 logits, sg, T, E, H);
+        k_pf_router<<<dim3((E + 1 + 63) / 64, (T + 63) / 64), CHK_WG, 0, st>>>(router, shared_gate, bhi, bmid, blo,
+                                                                               logits, sg, T, E, H);
 }
 
 void launch_pf_route(const float* logits, uint32_t T, uint32_t E, uint32_t topk, int norm_topk, uint32_t* ids,
