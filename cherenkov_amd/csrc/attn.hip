@@ -293,7 +293,11 @@ __global__ void __launch_bounds__(256) k_attn_part(AttnArgs a) {
     __shared__ float sp[G][CH];
     __shared__ float sml[G][2];
     __shared__ __align__(16) float so[NS][G][HD];
-    const uint32_t hk = blockIdx.x, c = blockIdx.y, b = blockIdx.z, t = threadIdx.x;
+    // blockIdx.x = (kv head, slice of G of its query heads): a kv head's
+    // query heads may be split over several workgroups for parallelism
+    const uint32_t split = (a.nh / a.nkv) / G;
+    const uint32_t hk = blockIdx.x / split, h0 = hk * (a.nh / a.nkv) + (blockIdx.x % split) * G;
+    const uint32_t c = blockIdx.y, b = blockIdx.z, t = threadIdx.x;
     const uint32_t T = a.pos[b] + 1;  // causal: rows see positions <= their own
     const uint32_t t0 = c * CH;
     if (t0 >= T) return;
@@ -328,7 +332,7 @@ __global__ void __launch_bounds__(256) k_attn_part(AttnArgs a) {
     // q of the G heads into LDS
     for (uint32_t i = t; i < (uint32_t)(G * HD); i += 256) {
         const uint32_t g = i / HD, d = i % HD;
-        sq[g][(d / DPT) * (DPT + 4) + d % DPT] = a.q_ready[((size_t)b * a.nh + hk * G + g) * HD + d];
+        sq[g][(d / DPT) * (DPT + 4) + d % DPT] = a.q_ready[((size_t)b * a.nh + h0 + g) * HD + d];
     }
     __syncthreads();
 
@@ -413,7 +417,7 @@ __global__ void __launch_bounds__(256) k_attn_part(AttnArgs a) {
         float acc = 0.0f;
 #pragma unroll
         for (int s2 = 0; s2 < NS; ++s2) acc += so[s2][g][d];
-        float* part = a.part + (((size_t)b * a.nh + hk * G + g) * a.max_chunks + c) * (HD + 2);
+        float* part = a.part + (((size_t)b * a.nh + h0 + g) * a.max_chunks + c) * (HD + 2);
         part[2 + d] = acc;
         if (d == 0) {
             part[0] = sml[g][0];
@@ -424,13 +428,17 @@ __global__ void __launch_bounds__(256) k_attn_part(AttnArgs a) {
 
 // LSE merge of the chunk partials and the per-dim sigmoid gate
 // (cpu.rs:629-633: the gate is the second half of each head's q_proj rows).
-// The chunk maxima and weights exp(m_c - M) go through LDS; each thread
-// then owns output dims and sums its partials with 8 chunks' loads in
-// flight.
+// COMBINE_SPLIT workgroups per head each own hd / COMBINE_SPLIT dims; every
+// one forms the chunk weights exp(m_c - M) in LDS, then its waves sum
+// interleaved chunks for its dims (8 loads in flight) and meet in LDS.
+constexpr uint32_t COMBINE_SPLIT = 4;
+
 __global__ void __launch_bounds__(256) k_attn_combine(AttnArgs a) {
     __shared__ float red[8];
     __shared__ float sw[MAX_ATTN_CHUNKS];
-    const uint32_t h = blockIdx.x, b = blockIdx.y, hd = a.hd, t = threadIdx.x;
+    __shared__ float acc_s[4][64];
+    const uint32_t h = blockIdx.x / COMBINE_SPLIT, ds = blockIdx.x % COMBINE_SPLIT, b = blockIdx.y, hd = a.hd,
+                   t = threadIdx.x;
     const uint32_t T = a.pos[b] + 1, nc = (T + ATTN_CHUNK - 1) / ATTN_CHUNK;
     const float* part = a.part + ((size_t)b * a.nh + h) * a.max_chunks * (hd + 2);
     float m = -INFINITY;
@@ -443,20 +451,28 @@ __global__ void __launch_bounds__(256) k_attn_combine(AttnArgs a) {
         l += part[(size_t)c * (hd + 2) + 1] * w;
     }
     const float L = block_sum(l, red);  // its barriers also publish sw
-    for (uint32_t d = t; d < hd; d += CHK_WG) {
+    const uint32_t per = hd / COMBINE_SPLIT;  // dims of this workgroup (<= 64)
+    const uint32_t dl = t & 63, cg = t >> 6;
+    const uint32_t d = ds * per + dl;
+    float o = 0.0f;
+    if (dl < per) {
         const float* pd = part + 2 + d;
-        float o = 0.0f;
-        uint32_t c = 0;
-        for (; c + 8 <= nc; c += 8) {
+        uint32_t c = cg;
+        for (; c + 28 < nc; c += 32) {
             float v[8];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) v[k] = pd[(size_t)(c + k) * (hd + 2)];
+            for (int k = 0; k < 8; ++k) v[k] = pd[(size_t)(c + 4 * k) * (hd + 2)];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) o += v[k] * sw[c + k];
+            for (int k = 0; k < 8; ++k) o += v[k] * sw[c + 4 * k];
         }
-        for (; c < nc; ++c) o += pd[(size_t)c * (hd + 2)] * sw[c];
+        for (; c < nc; c += 4) o += pd[(size_t)c * (hd + 2)] * sw[c];
+    }
+    acc_s[cg][dl] = o;
+    __syncthreads();
+    if (cg == 0 && dl < per) {
+        const float ot = (acc_s[0][dl] + acc_s[1][dl]) + (acc_s[2][dl] + acc_s[3][dl]);
         const float gate = a.q_raw[(size_t)b * a.nh * 2 * hd + h * 2 * hd + hd + d];
-        a.out[(size_t)b * a.nh * hd + h * hd + d] = o / L * sigmoidf_(gate);
+        a.out[(size_t)b * a.nh * hd + h * hd + d] = ot / L * sigmoidf_(gate);
     }
 }
 
@@ -480,14 +496,17 @@ bool attn_shape_ok(uint32_t nh, uint32_t nkv, uint32_t hd) {
 }
 
 void launch_attn_core(const AttnArgs& a, int nb, hipStream_t st) {
-    const dim3 grid(a.nkv, a.max_chunks, nb);
+    const uint32_t g = a.nh / a.nkv, gw = g < 4 ? g : 4;
+    if (g % gw) throw std::runtime_error("query heads per kv head must be 1, 2, 4, 8 or 12");
+    if (a.hd % COMBINE_SPLIT || a.hd / COMBINE_SPLIT > 64) throw std::runtime_error("head_dim 128 or 256");
+    const dim3 grid(a.nkv * (g / gw), a.max_chunks, nb);
+// query heads per partial workgroup: at most 4 (a kv head with 8 or 12
+// query heads is split over 2 or 3 workgroups that read the same chunk)
 #define CHK_ATTN_G(HDV)                                                              \
-    switch (a.nh / a.nkv) {                                                          \
+    switch (gw) {                                                                    \
     case 1: k_attn_part<1, HDV><<<grid, 256, 0, st>>>(a); break;                     \
     case 2: k_attn_part<2, HDV><<<grid, 256, 0, st>>>(a); break;                     \
-    case 4: k_attn_part<4, HDV><<<grid, 256, 0, st>>>(a); break;                     \
-    case 8: k_attn_part<8, HDV><<<grid, 256, 0, st>>>(a); break;                     \
-    default: k_attn_part<12, HDV><<<grid, 256, 0, st>>>(a); break;                   \
+    default: k_attn_part<4, HDV><<<grid, 256, 0, st>>>(a); break;                    \
     }
     if (a.hd == 128) {
         CHK_ATTN_G(128)
@@ -495,7 +514,7 @@ void launch_attn_core(const AttnArgs& a, int nb, hipStream_t st) {
         CHK_ATTN_G(256)
     }
 #undef CHK_ATTN_G
-    k_attn_combine<<<dim3(a.nh, nb), 256, 0, st>>>(a);
+    k_attn_combine<<<dim3(a.nh * COMBINE_SPLIT, nb), 256, 0, st>>>(a);
 }
 
 void launch_attn_prep(const AttnArgs& a, int nb, hipStream_t st) {
