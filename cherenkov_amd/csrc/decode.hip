@@ -320,7 +320,7 @@ __global__ void __launch_bounds__(256) k_hc_down(HcDev w, const float* __restric
     const Q4Consts k;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-        float sq = 0.0f, xs[CPL];
+        float sq4[4] = {0.0f, 0.0f, 0.0f, 0.0f}, xs[CPL];
         h2 hi[CPL][16], lo[CPL][16];
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
@@ -328,7 +328,8 @@ __global__ void __launch_bounds__(256) k_hc_down(HcDev w, const float* __restric
             float xv[32];
             ldx32(hyper + (size_t)b * hh + (size_t)g * H + cc * 32, xv);
             const uint4* np = reinterpret_cast<const uint4*>(w.norm + (size_t)g * H + cc * 32);
-            float t = 0.0f;
+            // four independent partial sums per reduction (short chains)
+            float t4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const uint4 nv = np[q];
@@ -338,14 +339,15 @@ __global__ void __launch_bounds__(256) k_hc_down(HcDev w, const float* __restric
                     const int j = q * 8 + h;
                     const float wn = __uint_as_float(h & 1 ? nn[h >> 1] & 0xffff0000u : nn[h >> 1] << 16);
                     const float xj = ch < nch ? xv[j] : 0.0f;
-                    sq += xj * xj;
+                    sq4[h & 3] += xj * xj;
                     xv[j] = xj * wn;
-                    t += xv[j];
+                    t4[h & 3] += xv[j];
                 }
             }
-            xs[c] = t;
+            xs[c] = (t4[0] + t4[1]) + (t4[2] + t4[3]);
             x_pairs(xv, hi[c], lo[c]);
         }
+        const float sq = (sq4[0] + sq4[1]) + (sq4[2] + sq4[3]);
         const float inv = 1.0f / sqrtf(wave_sum(sq) / (float)H + eps);
         if (blockIdx.x == 0 && lane == 0) inv_out[b * hc + g] = inv;
 #pragma unroll

@@ -161,7 +161,8 @@ CHK_DEV void x_pairs(const float (&v)[32], h2 (&hi)[16], h2 (&lo)[16]) {
 CHK_DEV float q4_chunk_h(uint4 wq, const h2 (&hi)[16], const h2 (&lo)[16], float xsum, float s, float b,
                          const Q4Consts& k) {
     const uint32_t ws[4] = {wq.x, wq.y, wq.z, wq.w};
-    float d = 0.0f;
+    // hi and lo products in two independent chains (half the dependent depth)
+    float dh = 0.0f, dl = 0.0f;
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
         const uint32_t w = ws[m], w8 = w >> 8;
@@ -171,11 +172,11 @@ CHK_DEV float q4_chunk_h(uint4 wq, const h2 (&hi)[16], const h2 (&lo)[16], float
                          __builtin_bit_cast(h2, (w8 & k.m2) | k.magic) - k.off};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            d = __builtin_amdgcn_fdot2(q[j], hi[4 * m + j], d, false);
-            d = __builtin_amdgcn_fdot2(q[j], lo[4 * m + j], d, false);
+            dh = __builtin_amdgcn_fdot2(q[j], hi[4 * m + j], dh, false);
+            dl = __builtin_amdgcn_fdot2(q[j], lo[4 * m + j], dl, false);
         }
     }
-    return s * d + b * xsum;
+    return s * (dh + dl) + b * xsum;
 }
 
 // ---- inputs as fixed-point nibble planes (the u4 dot8 product)

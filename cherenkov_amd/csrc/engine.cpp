@@ -130,8 +130,6 @@ struct PfBufs {
     float *inv, *d, *inj_a, *inj_m, *mixed, *hc_part;
     float *raw, *z, *a, *b, *conv, *decay, *beta, *y;
     float *q_raw, *k_raw, *v_raw, *idx_raw, *q_ready, *attn_out;
-    float* part;
-    uint64_t part_floats;
     float *logits, *sg, *wts;
     uint32_t *ids, *list, *count, *tiles, *ntiles;
     float *act, *yd;
@@ -1070,12 +1068,13 @@ void ChkEngine::prefill_rows(const uint32_t* toks, uint32_t n, uint32_t* next, u
 
 // ------------------------------------------------------- GEMM prefill
 constexpr uint32_t PF_MAX_ROWS = 4096;                  // rows per chunk (gpu/prefill.rs:116)
-constexpr uint64_t PF_PART_BYTES = 256ull << 20;        // attention partials per sub-batch
 
 bool ChkEngine::pf_supported() const {
     return o.experts == 4 && !has_mtp && !D.qsa && D.lowrank % 64 == 0 && D.H % 64 == 0 && D.H <= 4096 && D.hc <= 4 &&
            (D.dv == 64 || D.dv == 128 || D.dv == 256) && D.I % 64 == 0 && (D.nh * D.hd) % 64 == 0 &&
-           D.v_dim % 64 == 0 && D.E + 1 <= 513;
+           D.v_dim % 64 == 0 && D.E + 1 <= 513 && D.nh % D.nkv == 0 &&
+           (D.nh / D.nkv == 1 || D.nh / D.nkv == 2 || D.nh / D.nkv == 4 || D.nh / D.nkv == 8) &&
+           (D.hd == 128 || D.hd == 256);
 }
 
 void ChkEngine::pf_alloc() {
@@ -1118,8 +1117,6 @@ void ChkEngine::pf_alloc() {
     pf.idx_raw = q; q += C * D.idx_out;
     pf.q_ready = q; q += C * D.nh * D.hd;
     pf.attn_out = q;
-    pf.part_floats = PF_PART_BYTES / 4;
-    pf.part = dalloc<float>(pf.part_floats);
     pf.logits = dalloc<float>(C * D.E);
     pf.sg = dalloc<float>(C);
     pf.wts = dalloc<float>(C * D.topk);
@@ -1290,7 +1287,6 @@ void ChkEngine::pf_attention(const LayerDev& L, uint32_t T, uint32_t pos0) {
     aa.kv[0] = kv[L.at_idx];
     aa.one_kv = 1;
     aa.pos = pf.pos;
-    aa.part = pf.part;
     aa.out = pf.attn_out;
     aa.nh = D.nh;
     aa.nkv = D.nkv;
@@ -1303,17 +1299,7 @@ void ChkEngine::pf_attention(const LayerDev& L, uint32_t T, uint32_t pos0) {
     aa.scale = D.attn_scale;
     aa.max_chunks = (pos0 + T - 1) / ATTN_CHUNK + 1;
     launch_attn_prep(aa, (int)T, st);
-    const uint64_t per_row = (uint64_t)D.nh * aa.max_chunks * (D.hd + 2);
-    const uint32_t rows = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(T, pf.part_floats / per_row));
-    for (uint32_t r0 = 0; r0 < T; r0 += rows) {
-        AttnArgs b = aa;
-        const uint32_t nb = std::min(rows, T - r0);
-        b.q_raw = pf.q_raw + (uint64_t)r0 * 2 * D.nh * D.hd;
-        b.q_ready = pf.q_ready + (uint64_t)r0 * D.nh * D.hd;
-        b.out = pf.attn_out + (uint64_t)r0 * D.nh * D.hd;
-        b.pos = pf.pos + r0;
-        launch_attn_core(b, (int)nb, st);
-    }
+    launch_pf_flash(pf.q_ready, pf.q_raw, kv[L.at_idx], pf.attn_out, T, pos0, D.nh, D.nkv, D.hd, D.attn_scale, st);
     launch_pf_xprep(pf.attn_out, D.nh * D.hd, T, D.nh * D.hd, pf.hi, pf.lo, pf.xs, st);
     PfGemmArgs o2{};
     o2.seg[0].m = L.at.o;

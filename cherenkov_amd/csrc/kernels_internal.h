@@ -373,6 +373,8 @@ void launch_pf_xprep(const float* x, uint32_t ldx, uint32_t T, uint32_t K, uint4
 void launch_pf_hc_prep(const float* hyper, const uint16_t* norm, uint32_t H, uint32_t hc, float eps, float* inv,
                        uint4* hi, uint4* lo, float* xs, uint32_t T, hipStream_t st);
 void launch_pf_gemm_args(const PfGemmArgs& a, int epi, uint32_t grid_y, hipStream_t st);
+void launch_pf_flash(const float* q_ready, const float* q_raw, const KvDev& kv, float* out, uint32_t T, uint32_t pos0,
+                     uint32_t nh, uint32_t nkv, uint32_t hd, float scale, hipStream_t st);
 void launch_pf_gemm(const Q4Mat& w, const uint4* xhi, const uint4* xlo, const float* xs, float* y, uint32_t T,
                     uint32_t ldy, hipStream_t st);
 void launch_pf_hc_down_finish(const float* part, uint32_t nsplit, uint32_t T, uint32_t lowrank, uint32_t hc,

@@ -1061,3 +1061,268 @@ void launch_pf_dn(const PfDnArgs& a, hipStream_t st) {
 }
 
 }  // namespace chk
+
+namespace chk {
+
+// ------------------------------------------------- causal flash attention
+// Prefill attention (the reference's GEMM attention, gpu/prefill/attention.rs,
+// with the decode semantics of cpu.rs:589-634 over the engine's q8 KV rule):
+// for every prompt row r at position pos0 + r and query head h,
+//   o = softmax_t(scale q . k_t) . v_t over t <= pos0 + r, times sigmoid(gate).
+//
+// A workgroup takes 16 rows and one kv head; wave w serves that kv head's
+// query head w (GQA: the group's waves share every staged K/V tile).  Per
+// 32-token tile the workgroup dequantises K and V (int8 x fp16 scale,
+// exact in f32) into LDS as fp16 hi + lo planes (V transposed), then each
+// wave runs S = Q K^T and O += P V on v_mfma_f32_16x16x32_f16 with three
+// passes (hi.hi + hi.lo + lo.hi, ~22-bit operands) and an online softmax in
+// f32.  Layouts (16x16x32): A lane l = row l%16, k (l/16)*8..+8; B lane l =
+// column l%16, k (l/16)*8..+8; D lane l = column l%16, rows 4(l/16)..+4.
+constexpr int FA_TOK = 32;    // tokens per staged tile
+constexpr int FA_ROWS = 16;   // query rows per workgroup
+
+struct PfFlashArgs {
+    const float* q_ready;  // [T][nh][hd] normed, roped queries
+    const float* q_raw;    // [T][nh][2 hd] (the gate is each head's second half)
+    KvDev kv;
+    float* out;            // [T][nh * hd]
+    uint32_t T, pos0, nh, nkv;
+    float scale;
+};
+
+CHK_DEV h8 split_hi(const float (&v)[8], h8& lo) {
+    h8 hi;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        hi[j] = (_Float16)v[j];
+        lo[j] = (_Float16)(v[j] - (float)hi[j]);
+    }
+    return hi;
+}
+
+template <int HD, int G>
+__global__ void __launch_bounds__(64 * G) k_pf_flash(PfFlashArgs a) {
+    constexpr int KS = HD / 32;          // dim steps of 32
+    constexpr int DT = HD / 16;          // 16-dim output tiles
+    constexpr int KP = HD + 8;           // padded K row (halves)
+    constexpr int VP = FA_TOK + 8;       // padded V^T row (halves)
+    constexpr int PP = FA_TOK + 8;       // padded P row (halves)
+    __shared__ __align__(16) _Float16 kh[FA_TOK][KP], kl[FA_TOK][KP];
+    __shared__ __align__(16) _Float16 vh[HD][VP], vl[HD][VP];
+    __shared__ __align__(16) _Float16 ph[G][FA_ROWS][PP], pl[G][FA_ROWS][PP];
+    constexpr uint32_t nthr = 64 * G;
+    constexpr int IPT = (FA_TOK * HD / 16 + nthr - 1) / nthr;  // staging items per thread
+    const uint32_t tid = threadIdx.x, lane = tid & 63, w = wave_id();
+    const uint32_t col = lane & 15, kq = lane >> 4;
+    // heavy (late) row blocks first
+    const uint32_t rb = gridDim.x - 1 - blockIdx.x, hk = blockIdx.y, h = hk * G + w;
+    const uint32_t r0 = rb * FA_ROWS, rlast = min(r0 + FA_ROWS, a.T) - 1;
+    const uint32_t kv_row = a.nkv * HD, last_tok = a.pos0 + a.T - 1;
+    // this wave's queries as A operands
+    h8 qh[KS], ql[KS];
+    {
+        const uint32_t r = min(r0 + col, a.T - 1);
+        const float* qp = a.q_ready + ((size_t)r * a.nh + h) * HD;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            const float4 v0 = *reinterpret_cast<const float4*>(qp + s * 32 + kq * 8);
+            const float4 v1 = *reinterpret_cast<const float4*>(qp + s * 32 + kq * 8 + 4);
+            const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            qh[s] = split_hi(v, ql[s]);
+        }
+    }
+    // positions of the 4 rows this lane holds in D layout (rows past T
+    // repeat the last row; they are never written)
+    uint32_t qpos[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qpos[i] = a.pos0 + min(r0 + kq * 4 + i, a.T - 1);
+    f4 o[DT];
+#pragma unroll
+    for (int d = 0; d < DT; ++d) o[d] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        m[i] = -INFINITY;
+        l[i] = 0.0f;
+    }
+    const uint32_t ntile = (a.pos0 + rlast) / FA_TOK + 1;
+    // Staging: K as (token tid % 32, 16 dims), V as (token pair tid % 16,
+    // 8 dims) so that the transposed V writes are whole dwords in
+    // consecutive banks; a tile's raw bytes are loaded one tile ahead.
+    uint4 kraw[IPT];
+    uint2 vraw[IPT][2];
+    uint16_t ksc[IPT], vsc[IPT][2];
+    auto load_raw = [&](uint32_t t0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int r = 0; r < IPT; ++r) {
+            const uint32_t i = tid + r * nthr;
+            kraw[r] = make_uint4(0, 0, 0, 0);
+            vraw[r][0] = vraw[r][1] = make_uint2(0, 0);
+            ksc[r] = vsc[r][0] = vsc[r][1] = 0;
+            if (i >= (uint32_t)(FA_TOK * HD / 16)) continue;
+            const uint32_t kt = t0 + i % FA_TOK, kd = (i / FA_TOK) * 16;
+            if (kt <= last_tok) {
+                kraw[r] = *reinterpret_cast<const uint4*>(a.kv.k + (size_t)kt * kv_row + hk * HD + kd);
+                ksc[r] = a.kv.ks[(size_t)kt * (kv_row / 32) + (hk * HD + kd) / 32];
+            }
+            const uint32_t vt = t0 + 2 * (i % (FA_TOK / 2)), vd = (i / (FA_TOK / 2)) * 8;
+#pragma unroll
+            for (int e = 0; e < 2; ++e)
+                if (vt + e <= last_tok) {
+                    vraw[r][e] = *reinterpret_cast<const uint2*>(a.kv.v + (size_t)(vt + e) * kv_row + hk * HD + vd);
+                    vsc[r][e] = a.kv.vs[(size_t)(vt + e) * (kv_row / 32) + (hk * HD + vd) / 32];
+                }
+        }
+    };
+    auto store_tile = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int r = 0; r < IPT; ++r) {
+            const uint32_t i = tid + r * nthr;
+            if (i >= (uint32_t)(FA_TOK * HD / 16)) continue;
+            const uint32_t kt = i % FA_TOK, kd = (i / FA_TOK) * 16;
+            const float kscale = __half2float(__ushort_as_half(ksc[r]));
+            const uint32_t kwv[4] = {kraw[r].x, kraw[r].y, kraw[r].z, kraw[r].w};
+#pragma unroll
+            for (int hlf = 0; hlf < 2; ++hlf) {
+                float kv8[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    kv8[j] = (float)(int8_t)(kwv[hlf * 2 + j / 4] >> (8 * (j % 4))) * kscale;
+                h8 lo8;
+                const h8 hi8 = split_hi(kv8, lo8);
+                *reinterpret_cast<h8*>(&kh[kt][kd + hlf * 8]) = hi8;
+                *reinterpret_cast<h8*>(&kl[kt][kd + hlf * 8]) = lo8;
+            }
+            const uint32_t vt = 2 * (i % (FA_TOK / 2)), vd = (i / (FA_TOK / 2)) * 8;
+            const float vs0 = __half2float(__ushort_as_half(vsc[r][0])), vs1 = __half2float(__ushort_as_half(vsc[r][1]));
+            const uint32_t v0[2] = {vraw[r][0].x, vraw[r][0].y}, v1[2] = {vraw[r][1].x, vraw[r][1].y};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float x0 = (float)(int8_t)(v0[j / 4] >> (8 * (j % 4))) * vs0;
+                const float x1 = (float)(int8_t)(v1[j / 4] >> (8 * (j % 4))) * vs1;
+                const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
+                typedef _Float16 hh2 __attribute__((ext_vector_type(2)));
+                *reinterpret_cast<hh2*>(&vh[vd + j][vt]) = hh2{h0, h1};
+                *reinterpret_cast<hh2*>(&vl[vd + j][vt]) = hh2{(_Float16)(x0 - (float)h0), (_Float16)(x1 - (float)h1)};
+            }
+        }
+    };
+    load_raw(0);
+    store_tile();
+    __syncthreads();
+    for (uint32_t tile = 0; tile < ntile; ++tile) {
+        const uint32_t t0 = tile * FA_TOK;
+        if (tile + 1 < ntile) load_raw(t0 + FA_TOK);
+        // ---- S = Q K^T for 2 token tiles
+        f4 s[2];
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            s[tt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const h8 bh = *reinterpret_cast<const h8*>(&kh[tt * 16 + col][ks * 32 + kq * 8]);
+                const h8 bl = *reinterpret_cast<const h8*>(&kl[tt * 16 + col][ks * 32 + kq * 8]);
+                s[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[ks], bh, s[tt], 0, 0, 0);
+                s[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[ks], bl, s[tt], 0, 0, 0);
+                s[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[ks], bh, s[tt], 0, 0, 0);
+            }
+        }
+        // ---- online softmax over the tile (rows kq*4 + i, tokens col, 16 + col)
+        float p[2][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                const uint32_t t = t0 + tt * 16 + col;
+                const float v = t <= qpos[i] ? s[tt][i] * a.scale : -INFINITY;
+                p[tt][i] = v;
+                mx = fmaxf(mx, v);
+            }
+            mx = group_max<16>(mx);
+            const float mn = fmaxf(m[i], mx);
+            const float corr = m[i] == -INFINITY ? 0.0f : expf(m[i] - mn);
+            float rs = 0.0f;
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                const float e = p[tt][i] == -INFINITY ? 0.0f : expf(p[tt][i] - mn);
+                p[tt][i] = e;
+                rs += e;
+            }
+            rs = group_sum<16>(rs);
+            l[i] = l[i] * corr + rs;
+            m[i] = mn;
+#pragma unroll
+            for (int d = 0; d < DT; ++d) o[d][i] *= corr;
+        }
+        // ---- P to this wave's LDS rows (hi, lo), read back as A operands:
+        // LDS instructions of one wave complete in order, so only the
+        // compiler has to be kept from reordering them
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const _Float16 hi = (_Float16)p[tt][i];
+                ph[w][kq * 4 + i][tt * 16 + col] = hi;
+                pl[w][kq * 4 + i][tt * 16 + col] = (_Float16)(p[tt][i] - (float)hi);
+            }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const h8 pah = *reinterpret_cast<const h8*>(&ph[w][col][kq * 8]);
+        const h8 pal = *reinterpret_cast<const h8*>(&pl[w][col][kq * 8]);
+#pragma unroll
+        for (int d = 0; d < DT; ++d) {
+            const h8 bh = *reinterpret_cast<const h8*>(&vh[d * 16 + col][kq * 8]);
+            const h8 bl = *reinterpret_cast<const h8*>(&vl[d * 16 + col][kq * 8]);
+            o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pal, bh, o[d], 0, 0, 0);
+            o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pah, bl, o[d], 0, 0, 0);
+            o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pah, bh, o[d], 0, 0, 0);
+        }
+        if (tile + 1 < ntile) {
+            __syncthreads();  // every wave is done with this tile's K and V
+            store_tile();
+            __syncthreads();
+        }
+    }
+    // ---- o / l times the per-dim sigmoid gate (cpu.rs:629-633)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t r = r0 + kq * 4 + i;
+        if (r >= a.T) continue;
+        const float inv = 1.0f / l[i];
+        const float* gp = a.q_raw + ((size_t)r * a.nh + h) * 2 * HD + HD;
+        float* op = a.out + (size_t)r * a.nh * HD + (size_t)h * HD;
+#pragma unroll
+        for (int d = 0; d < DT; ++d) {
+            const uint32_t dd = d * 16 + col;
+            op[dd] = o[d][i] * inv * sigmoidf_(gp[dd]);
+        }
+    }
+}
+
+void launch_pf_flash(const float* q_ready, const float* q_raw, const KvDev& kv, float* out, uint32_t T, uint32_t pos0,
+                     uint32_t nh, uint32_t nkv, uint32_t hd, float scale, hipStream_t st) {
+    if (nkv == 0 || nh % nkv || nh / nkv > 8 || (hd != 128 && hd != 256))
+        throw std::runtime_error("flash prefill takes head_dim 128 or 256 and up to 8 query heads per kv head");
+    if (!T) return;
+    PfFlashArgs a{q_ready, q_raw, kv, out, T, pos0, nh, nkv, scale};
+    const dim3 grid((T + FA_ROWS - 1) / FA_ROWS, nkv);
+#define CHK_FA(HDV)                                                           \
+    switch (nh / nkv) {                                                       \
+    case 1: k_pf_flash<HDV, 1><<<grid, 64, 0, st>>>(a); break;                \
+    case 2: k_pf_flash<HDV, 2><<<grid, 128, 0, st>>>(a); break;               \
+    case 3: case 4: k_pf_flash<HDV, 4><<<grid, 256, 0, st>>>(a); break;       \
+    default: k_pf_flash<HDV, 8><<<grid, 512, 0, st>>>(a); break;              \
+    }
+    if (nh / nkv != 1 && nh / nkv != 2 && nh / nkv != 4 && nh / nkv != 8)
+        throw std::runtime_error("flash prefill takes 1, 2, 4 or 8 query heads per kv head");
+    if (hd == 256) {
+        CHK_FA(256)
+    } else {
+        CHK_FA(128)
+    }
+#undef CHK_FA
+}
+
+}  // namespace chk
