@@ -129,6 +129,7 @@ struct PfBufs {
     float* xs;
     float *inv, *d, *inj_a, *inj_m, *mixed, *hc_part;
     float *raw, *z, *a, *b, *conv, *decay, *beta, *y;
+    float* dcw;  // chunked-scan workspace (null: sequential scan)
     float *q_raw, *k_raw, *v_raw, *idx_raw, *q_ready, *attn_out;
     float *logits, *sg, *wts;
     uint32_t *ids, *list, *count, *tiles, *ntiles;
@@ -1127,6 +1128,7 @@ void ChkEngine::pf_alloc() {
     pf.ntiles = dalloc<uint32_t>(1);
     pf.act = dalloc<float>(C * slots * D.I);
     pf.yd = dalloc<float>(C * slots * D.H);
+    pf.dcw = dc_supported(D.nk, D.nv, D.dk, D.dv) ? dalloc<float>(dc_work_floats((uint32_t)C, D.nv, D.dv)) : nullptr;
     pf.cap = (uint32_t)C;
 }
 
@@ -1187,8 +1189,9 @@ void ChkEngine::pf_hc_read(const HcDev& w, float* inj, uint32_t T, bool for_moe)
 }
 
 // linear_attention (cpu.rs:745-826) over the chunk: the four input
-// projections as one GEMM, conv + norms, the sequential scan, the gated
-// norm into the out-projection's operands, out-projection + inject.
+// projections as one GEMM, conv + norms, the scan (chunked, 64 rows per
+// chunk, for head dims of 128; else sequential), the gated norm into the
+// out-projection's operands, out-projection + inject.
 void ChkEngine::pf_deltanet(const LayerDev& L, uint32_t T) {
     const uint32_t mt = (T + 63) / 64, di = (uint32_t)L.dn_idx;
     PfGemmArgs g{};
@@ -1228,7 +1231,7 @@ void ChkEngine::pf_deltanet(const LayerDev& L, uint32_t T) {
     a.qk_dim = D.qk_dim;
     a.v_dim = D.v_dim;
     a.qscale = D.qscale;
-    launch_pf_dn(a, st);
+    launch_pf_dn(a, pf.dcw, st);
     PfPrepArgs p{};
     p.x = pf.y;
     p.ldx = D.v_dim;
@@ -1631,6 +1634,35 @@ int chk_attn_decode_q8(const float* q, const void* k, const void* v, const void*
     })
 }
 
+int chk_dn_scan(const float* conv, const float* decay, const float* beta, float* state, float* y, uint32_t T,
+                uint32_t nk, uint32_t nv, uint32_t dk, uint32_t dv, int chunked, void* stream) {
+    CHK_TRY({
+        ensure(T > 0 && T <= 65536, "1..=65536 rows");
+        ensure(nk > 0 && nv % nk == 0 && dk == 128 && dv % 4 == 0 && dv > 0, "key head dim 128, nv a multiple of nk");
+        ensure(!chunked || dc_supported(nk, nv, dk, dv), "the chunked scan needs key and value head dims of 128");
+        hipStream_t st = (hipStream_t)stream;
+        PfDnArgs a{};
+        a.conv = const_cast<float*>(conv);
+        a.decay = const_cast<float*>(decay);
+        a.beta = const_cast<float*>(beta);
+        a.state = state;
+        a.y = y;
+        a.T = T;
+        a.nk = nk;
+        a.nv = nv;
+        a.dv = dv;
+        a.qk_dim = nk * dk;
+        a.v_dim = nv * dv;
+        a.conv_dim = 2 * a.qk_dim + a.v_dim;
+        float* work = nullptr;
+        if (chunked) HIPCHK(hipMalloc(&work, dc_work_floats(T, nv, dv) * 4));
+        launch_pf_dn_scan(a, work, st);
+        HIPCHK(hipStreamSynchronize(st));
+        HIPCHK(hipGetLastError());
+        if (work) HIPCHK(hipFree(work));
+    })
+}
+
 int chk_qsa_select(const float* scores, uint32_t t_len, uint32_t kblk, uint32_t ratio, uint32_t* vmask, void* stream) {
     CHK_TRY({
         ensure(ratio >= 1 && kblk >= 1, "ratio and kblk must be positive");
@@ -1856,14 +1888,25 @@ int chk_q4_gemm(const void* w, const void* s, const void* b, uint32_t out, uint3
         HIPCHK(hipMalloc(&hi, (size_t)T * in * 2));
         HIPCHK(hipMalloc(&lo, (size_t)T * in * 2));
         HIPCHK(hipMalloc(&xs, (size_t)T * (in / 64) * 4));
+        // the GEMM addresses a matrix's codes, scales and biases by 32-bit
+        // offsets from one base (the engine keeps them in one arena), so the
+        // caller's three buffers are packed together first
+        const size_t wb = (size_t)out * in / 2, sb = (size_t)out * (in / 64) * 2;
+        const size_t so = (wb + 255) & ~(size_t)255, bo = so + ((sb + 255) & ~(size_t)255);
+        uint8_t* pack = nullptr;
+        HIPCHK(hipMalloc(&pack, bo + sb));
+        HIPCHK(hipMemcpyAsync(pack, w, wb, hipMemcpyDeviceToDevice, st));
+        HIPCHK(hipMemcpyAsync(pack + so, s, sb, hipMemcpyDeviceToDevice, st));
+        HIPCHK(hipMemcpyAsync(pack + bo, b, sb, hipMemcpyDeviceToDevice, st));
         launch_pf_xprep(x, in, T, in, hi, lo, xs, st);
-        launch_pf_gemm(Q4Mat{(const uint32_t*)w, (const uint16_t*)s, (const uint16_t*)b, out, in}, hi, lo, xs, y, T,
-                       out, st);
+        launch_pf_gemm(Q4Mat{(const uint32_t*)pack, (const uint16_t*)(pack + so), (const uint16_t*)(pack + bo), out, in},
+                       hi, lo, xs, y, T, out, st);
         HIPCHK(hipStreamSynchronize(st));
         HIPCHK(hipGetLastError());
         HIPCHK(hipFree(hi));
         HIPCHK(hipFree(lo));
         HIPCHK(hipFree(xs));
+        HIPCHK(hipFree(pack));
     })
 }
 

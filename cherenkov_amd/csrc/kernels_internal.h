@@ -390,7 +390,13 @@ void launch_pf_moe_combine(const float* yd, const float* wts, const float* sg, c
                            uint32_t T, uint32_t H, uint32_t topk, uint32_t hc, hipStream_t st);
 void launch_pf_embed(const uint32_t* tokens, const Q4Mat& emb, float* hyper, uint32_t H, uint32_t hc, uint32_t T,
                      hipStream_t st);
-void launch_pf_dn(const PfDnArgs& a, hipStream_t st);
+// conv + norms, decay / beta, then the scan: chunked (dnscan.hip) when
+// `work` is given and the head dims allow it, else the sequential kernel.
+void launch_pf_dn(const PfDnArgs& a, float* work, hipStream_t st);
+void launch_pf_dn_scan(const PfDnArgs& a, float* work, hipStream_t st);
+bool dc_supported(uint32_t nk, uint32_t nv, uint32_t dk, uint32_t dv);
+uint64_t dc_work_floats(uint32_t T, uint32_t nv, uint32_t dv);
+void launch_dc_scan(const PfDnArgs& a, float* work, hipStream_t st);
 void launch_attn_prep(const AttnArgs& a, int nb, hipStream_t st);
 void launch_qsa_select(const AttnArgs& a, int nb, hipStream_t st);
 void launch_attn_core(const AttnArgs& a, int nb, hipStream_t st);

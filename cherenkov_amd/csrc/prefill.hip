@@ -1049,7 +1049,14 @@ void launch_pf_embed(const uint32_t* tokens, const Q4Mat& emb, float* hyper, uin
     if (T) k_pf_embed<<<dim3((H + 255) / 256, T), CHK_WG, 0, st>>>(tokens, emb, hyper, H, hc);
 }
 
-void launch_pf_dn(const PfDnArgs& a, hipStream_t st) {
+void launch_pf_dn_scan(const PfDnArgs& a, float* work, hipStream_t st) {
+    if (!a.T) return;
+    if (a.dv % 4 || a.qk_dim != a.nk * 128) throw std::runtime_error("scan needs key head dim 128, value head dim a multiple of 4");
+    if (work && dc_supported(a.nk, a.nv, a.qk_dim / a.nk, a.dv)) launch_dc_scan(a, work, st);
+    else k_pf_dn_scan<<<a.nv * (a.dv / 4), 64, 0, st>>>(a);
+}
+
+void launch_pf_dn(const PfDnArgs& a, float* work, hipStream_t st) {
     if (!a.T) return;
     if (a.ck < 2 || a.ck > 9) throw std::runtime_error("conv kernel 2..=9");
     if (a.dv % 4) throw std::runtime_error("value head dim must be a multiple of 4");
@@ -1057,7 +1064,7 @@ void launch_pf_dn(const PfDnArgs& a, hipStream_t st) {
     k_pf_dn_conv<<<dim3((spans + 3) / 4, a.T), CHK_WG, 0, st>>>(a);
     const uint32_t n = a.conv_dim + a.T * a.nv;
     k_pf_dn_misc<<<(n + CHK_WG - 1) / CHK_WG, CHK_WG, 0, st>>>(a);
-    k_pf_dn_scan<<<a.nv * (a.dv / 4), 64, 0, st>>>(a);
+    launch_pf_dn_scan(a, work, st);
 }
 
 }  // namespace chk

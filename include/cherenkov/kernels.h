@@ -61,6 +61,16 @@ int chk_attn_decode_q8(const float* q, const void* k, const void* v, const void*
  * nothing while t_len / ratio <= kblk (the dense case). */
 int chk_qsa_select(const float* scores, uint32_t t_len, uint32_t kblk, uint32_t ratio, uint32_t* vmask, void* stream);
 
+/* The prefill's gated delta rule over T rows (linear_attention's recurrence,
+ * cpu.rs:745-812; the reference prefill scan, gpu/prefill/deltanet.rs:80-95):
+ * conv f32 [T][2 nk dk + nv dv] holds each row's q (normed, scaled), k
+ * (normed) and v as the conv stage leaves them; decay, beta f32 [T][nv];
+ * state f32 [nv][dv][dk] is read and left updated; y f32 [T][nv dv].
+ * chunked = 0 runs the recurrence row by row, 1 the chunked form (64 rows
+ * per chunk, MFMA products; key and value head dims 128).  dk is 128. */
+int chk_dn_scan(const float* conv, const float* decay, const float* beta, float* state, float* y, uint32_t T,
+                uint32_t nk, uint32_t nv, uint32_t dk, uint32_t dv, int chunked, void* stream);
+
 /* MoE block of decoder layer `layer` (num_hidden_layers = the MTP layer) on
  * normalised inputs x [nb][H]: out [nb][H] = routed experts (per the
  * engine's expert precision) + sigmoid-gated shared expert; top_ids
