@@ -94,6 +94,24 @@ __global__ void __launch_bounds__(256) k_dc_prep(PfDnArgs a, float* __restrict__
     float* const QGw = Uw + DC_C * a.dv + DC_OFF_QG;
     float* const KFw = Uw + DC_C * a.dv + DC_OFF_KF;
     float* const Ew = Uw + DC_C * a.dv + DC_OFF_E;
+    // waves 0-1 fetch their V right-hand sides (D layout: rows
+    // 16 bi + 4 kq + r of column tile ct) now, so the loads land while the
+    // factors below are built; padding rows repeat the last row (their
+    // beta is 0)
+    const bool vcol = w < 2;
+    float vr[4][4][4];
+    if (vcol) {
+#pragma unroll
+        for (int bi = 0; bi < 4; ++bi)
+#pragma unroll
+            for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t t = min((uint32_t)(16 * bi + 4 * kq + r), n - 1);
+                    vr[bi][ct][r] = a.conv[(size_t)(t0 + t) * a.conv_dim + 2 * (size_t)a.qk_dim + (size_t)hv * a.dv +
+                                           64 * (w & 1) + 16 * ct + i16];
+                }
+    }
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
         const int idx = tid + 256 * m, r = idx >> 5, f = idx & 31;
@@ -217,7 +235,6 @@ __global__ void __launch_bounds__(256) k_dc_prep(PfDnArgs a, float* __restrict__
     __syncthreads();
     // right-hand sides (D layout: rows 16 bi + 4 kq + r of column tile ct):
     // waves 0-1 b V (value columns), waves 2-3 b gamma K
-    const bool vcol = w < 2;
     f4v X[4][4];
 #pragma unroll
     for (int bi = 0; bi < 4; ++bi) {
@@ -228,14 +245,7 @@ __global__ void __launch_bounds__(256) k_dc_prep(PfDnArgs a, float* __restrict__
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int t = 16 * bi + 4 * kq + r;
-                float bv;
-                if (vcol)
-                    bv = (uint32_t)t < n ? Bs[t] * a.conv[(size_t)(t0 + t) * a.conv_dim + 2 * (size_t)a.qk_dim +
-                                                          (size_t)hv * a.dv + col]
-                                         : 0.0f;
-                else
-                    bv = Bs[t] * Es[t] * Ks[t][col];
-                acc[ct][r] = bv;
+                acc[ct][r] = vcol ? Bs[t] * vr[bi][ct][r] : Bs[t] * Es[t] * Ks[t][col];
             }
         }
         // B_i - sum_{j < i} A_ij X_j

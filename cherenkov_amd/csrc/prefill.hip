@@ -772,39 +772,65 @@ __global__ void __launch_bounds__(256) k_pf_embed(const uint32_t* __restrict__ t
 // ----------------------------------------------------------- DeltaNet
 // Causal conv over time (cpu.rs:1067-1085) + silu for every channel, then
 // the L2 norms of the q (times dk^-1/2) and k heads (eps 1e-6,
-// cpu.rs:745-760).  One wave per (row, 128-channel head span), lane l
-// owning channels 2l, 2l + 1; the window reaches into the layer's
+// cpu.rs:745-760).  Lane l of a workgroup owns four adjacent channels of
+// one row (float4 loads of the row and of the rows before it), so a
+// 128-channel head is a half wave; the window reaches into the layer's
 // history for the first rows.
+template <int CK>
 __global__ void __launch_bounds__(256) k_pf_dn_conv(PfDnArgs a) {
-    const int lane = threadIdx.x & 63;
-    const uint32_t t = blockIdx.y, span = blockIdx.x * 4 + wave_id();
-    const uint32_t c0 = span * 128 + lane * 2, km1 = a.ck - 1;
-    if (span * 128 >= a.conv_dim) return;
-    float o[2];
+    // CK > 0: the kernel width at compile time (its taps load as whole
+    // words), else a.ck
+    const uint32_t ck = CK > 0 ? (uint32_t)CK : a.ck, km1 = ck - 1;
+    const uint32_t t = blockIdx.y, c0 = (blockIdx.x * CHK_WG + threadIdx.x) * 4;
+    const bool live = c0 < a.conv_dim;
+    const uint32_t cc = live ? c0 : 0;
+    // taps of the four channels: w[e][j] = conv_w[(cc + e) ck + j]
+    float w[4][CK > 0 ? CK : 9];
+    if constexpr (CK == 4) {
+        const uint4* wp = reinterpret_cast<const uint4*>(a.conv_w + (size_t)cc * 4);
+        const uint4 w0 = wp[0], w1 = wp[1];
+        const uint32_t ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-        const uint32_t c = min(c0 + e, a.conv_dim - 1);
-        const uint16_t* cw = a.conv_w + (size_t)c * a.ck;
-        float s = bf16f(cw[km1]) * a.raw[(size_t)t * a.ld_raw + c];
-        for (uint32_t j = 0; j < km1; ++j) {
-            const int tau = (int)t - (int)km1 + (int)j;
-            const float x = tau >= 0 ? a.raw[(size_t)tau * a.ld_raw + c] : a.hist[(size_t)c * km1 + (tau + (int)km1)];
-            s += bf16f(cw[j]) * x;
-        }
-        o[e] = siluf_(s);
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t word = ww[(e * 4 + j) >> 1];
+                w[e][j] = __uint_as_float((j & 1) ? word & 0xffff0000u : word << 16);
+            }
+    } else {
+        for (int e = 0; e < 4; ++e)
+            for (uint32_t j = 0; j < ck; ++j) w[e][j] = bf16f(a.conv_w[(size_t)(cc + e) * ck + j]);
     }
-    if (span < 2 * a.nk) {
-        const float sq = wave_sum(o[0] * o[0] + o[1] * o[1]);
-        const float inv = 1.0f / sqrtf(sq + 1e-6f);
-        o[0] *= inv;
-        o[1] *= inv;
-        if (span < a.nk) {
-            o[0] *= a.qscale;
-            o[1] *= a.qscale;
+    const float4 cur = *reinterpret_cast<const float4*>(a.raw + (size_t)t * a.ld_raw + cc);
+    float o[4] = {w[0][km1] * cur.x, w[1][km1] * cur.y, w[2][km1] * cur.z, w[3][km1] * cur.w};
+#pragma unroll
+    for (uint32_t j = 0; j < km1; ++j) {
+        const int tau = (int)t - (int)km1 + (int)j;
+        float x[4];
+        if (tau >= 0) {
+            const float4 v = *reinterpret_cast<const float4*>(a.raw + (size_t)tau * a.ld_raw + cc);
+            x[0] = v.x;
+            x[1] = v.y;
+            x[2] = v.z;
+            x[3] = v.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[e] = a.hist[(size_t)(cc + e) * km1 + (tau + (int)km1)];
         }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] += w[e][j] * x[e];
     }
-    if (c0 < a.conv_dim) a.conv[(size_t)t * a.conv_dim + c0] = o[0];
-    if (c0 + 1 < a.conv_dim) a.conv[(size_t)t * a.conv_dim + c0 + 1] = o[1];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = siluf_(o[e]);
+    // q and k heads: 128 channels = the 32 lanes of a half wave
+    const float sq = group_sum<32>((o[0] * o[0] + o[1] * o[1]) + (o[2] * o[2] + o[3] * o[3]));
+    if (c0 < 2 * a.qk_dim) {
+        float inv = 1.0f / sqrtf(sq + 1e-6f);
+        if (c0 < a.qk_dim) inv *= a.qscale;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] *= inv;
+    }
+    if (live) *reinterpret_cast<float4*>(a.conv + (size_t)t * a.conv_dim + c0) = make_float4(o[0], o[1], o[2], o[3]);
 }
 
 // The new conv history (the last ck-1 raw inputs, reaching into the old
@@ -1060,8 +1086,11 @@ void launch_pf_dn(const PfDnArgs& a, float* work, hipStream_t st) {
     if (!a.T) return;
     if (a.ck < 2 || a.ck > 9) throw std::runtime_error("conv kernel 2..=9");
     if (a.dv % 4) throw std::runtime_error("value head dim must be a multiple of 4");
-    const uint32_t spans = (a.conv_dim + 127) / 128;
-    k_pf_dn_conv<<<dim3((spans + 3) / 4, a.T), CHK_WG, 0, st>>>(a);
+    if (a.conv_dim % 128 || a.qk_dim % 128 || a.ld_raw % 4)
+        throw std::runtime_error("prefill conv needs whole 128-channel heads");
+    const dim3 grid((a.conv_dim + 4 * CHK_WG - 1) / (4 * CHK_WG), a.T);
+    if (a.ck == 4 && (uintptr_t)a.conv_w % 16 == 0) k_pf_dn_conv<4><<<grid, CHK_WG, 0, st>>>(a);
+    else k_pf_dn_conv<0><<<grid, CHK_WG, 0, st>>>(a);
     const uint32_t n = a.conv_dim + a.T * a.nv;
     k_pf_dn_misc<<<(n + CHK_WG - 1) / CHK_WG, CHK_WG, 0, st>>>(a);
     launch_pf_dn_scan(a, work, st);
