@@ -614,45 +614,76 @@ __global__ void __launch_bounds__(256) k_pf_hc_down_finish(const float* __restri
 // v_mfma_f32_16x16x32_bf16 with x split into three bf16 terms (natural k
 // order): every product of bf16 values is exact in f32, so the logits keep
 // f32-grade accuracy and the top-k cut sees what an f32 dot would.
-// A wave: 64 rows x 64 outputs; a workgroup: 64 rows x 256.
+// A workgroup covers 64 rows x 64 outputs, each wave one 16-output column
+// tile over the 64 rows.  Per 64-wide k block the three x planes of the 64
+// rows are staged through LDS once for the four waves (double-buffered;
+// the next block's pieces and weight words load while this one computes).
+constexpr int RT_AROW = 9;  // uint4 per staged row (8 + 1 pad)
+
 __global__ void __launch_bounds__(256) k_pf_router(const uint16_t* __restrict__ router,
                                                    const uint16_t* __restrict__ shared_gate,
                                                    const uint4* __restrict__ bhi, const uint4* __restrict__ bmid,
                                                    const uint4* __restrict__ blo, float* __restrict__ logits,
                                                    float* __restrict__ sg, uint32_t T, uint32_t E, uint32_t H) {
-    // a workgroup covers 64 rows x 64 outputs, each wave one 16-output
-    // column tile over the 64 rows (4 accumulators), so the grid spreads
-    // the [T x (E + 1)] output over every CU
-    const int lane = threadIdx.x & 63, col = lane & 15, kq = lane >> 4;
-    const uint32_t m0 = blockIdx.y * 64, KB = H >> 3;
+    __shared__ __align__(16) u32x4 sA[2][3][64 * RT_AROW];
+    const int tid = threadIdx.x, lane = tid & 63, col = lane & 15, kq = lane >> 4;
+    const uint32_t m0 = blockIdx.y * 64, KB = H >> 3, NB = H >> 6;
     const uint32_t nn = blockIdx.x * 64 + wave_id() * 16 + col;
     const uint32_t r = min(nn, E);
-    const uint4* bp = reinterpret_cast<const uint4*>(r < E ? router + (size_t)r * H : shared_gate);
-    const uint4* ah[4];
-    const uint4* am[4];
-    const uint4* al[4];
+    const u32x4* bp = reinterpret_cast<const u32x4*>(r < E ? router + (size_t)r * H : shared_gate);
+    // staging: piece u of thread tid is plane u / 2, row (tid + 256 (u % 2)) / 8, 8-block tid % 8
+    const uint32_t srow = (uint32_t)tid >> 3, skb = (uint32_t)tid & 7;
+    size_t soff[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t m = min(m0 + i * 16 + col, T - 1);
-        ah[i] = bhi + (size_t)m * KB;
-        am[i] = bmid + (size_t)m * KB;
-        al[i] = blo + (size_t)m * KB;
-    }
+    for (int h = 0; h < 2; ++h) soff[h] = (size_t)min(m0 + srow + 32 * h, T - 1) * KB + skb;
+    u32x4 ra[2][6], rb[2][2];
+    auto fetch = [&](int slot, uint32_t blk) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < 6; ++u) {
+            const u32x4* pl = reinterpret_cast<const u32x4*>(u < 2 ? bhi : u < 4 ? bmid : blo);
+            ra[slot][u] = pl[soff[u & 1] + blk * 8];
+        }
+        rb[slot][0] = bp[blk * 8 + kq];
+        rb[slot][1] = bp[blk * 8 + 4 + kq];
+    };
+    auto store = [&](int slot, int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < 6; ++u) sA[buf][u >> 1][(srow + 32 * (u & 1)) * RT_AROW + skb] = ra[slot][u];
+    };
     f4 acc[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    for (uint32_t k = 0; k < KB; k += 4) {
-        const b8 bq = __builtin_bit_cast(b8, bp[k + kq]);
+    auto step = [&](auto sc_, uint32_t blk) __attribute__((always_inline)) {
+        constexpr int P = decltype(sc_)::value;
+        fetch(P ^ 1, min(blk + 1, NB - 1));
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const b8 xh = __builtin_bit_cast(b8, ah[i][k + kq]);
-            const b8 xm = __builtin_bit_cast(b8, am[i][k + kq]);
-            const b8 xl = __builtin_bit_cast(b8, al[i][k + kq]);
-            acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, bq, acc[i], 0, 0, 0);
-            acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xm, bq, acc[i], 0, 0, 0);
-            acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, bq, acc[i], 0, 0, 0);
+        for (int s = 0; s < 2; ++s) {
+            const b8 bq = __builtin_bit_cast(b8, rb[P][s]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t ai = (16 * i + col) * RT_AROW + 4 * s + kq;
+                const b8 xh = __builtin_bit_cast(b8, sA[P][0][ai]);
+                const b8 xm = __builtin_bit_cast(b8, sA[P][1][ai]);
+                const b8 xl = __builtin_bit_cast(b8, sA[P][2][ai]);
+                acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, bq, acc[i], 0, 0, 0);
+                acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xm, bq, acc[i], 0, 0, 0);
+                acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, bq, acc[i], 0, 0, 0);
+            }
         }
+        store(P ^ 1, P ^ 1);
+        __syncthreads();
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    fetch(0, 0);
+    store(0, 0);
+    __syncthreads();
+    uint32_t blk = 0;
+    for (; blk + 1 < NB; blk += 2) {
+        step(I0{}, blk);
+        step(I1{}, blk + 1);
     }
+    if (blk < NB) step(I0{}, blk);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -1044,7 +1075,7 @@ void launch_pf_hc_down_finish(const float* part, uint32_t nsplit, uint32_t T, ui
 
 void launch_pf_router(const uint16_t* router, const uint16_t* shared_gate, const uint4* bhi, const uint4* bmid,
                       const uint4* blo, float* logits, float* sg, uint32_t T, uint32_t E, uint32_t H, hipStream_t st) {
-    if (H % 32) throw std::runtime_error("router width must be a multiple of 32");
+    if (H % 64) throw std::runtime_error("router width must be a multiple of 64");
     if (T)
         k_pf_router<<<dim3((E + 1 + 63) / 64, (T + 63) / 64), CHK_WG, 0, st>>>(router, shared_gate, bhi, bmid, blo,
                                                                                logits, sg, T, E, H);
