@@ -123,7 +123,7 @@ __global__ void __launch_bounds__(256) k_pf_hc_prep(const float* __restrict__ hy
                                                     uint32_t H, uint32_t hc, float eps, float* __restrict__ inv_out,
                                                     uint4* __restrict__ hi, uint4* __restrict__ lo,
                                                     float* __restrict__ xs) {
-    __shared__ float red[4];
+    __shared__ float red[4][4];
     const uint32_t t = blockIdx.x, tau = threadIdx.x, bps = H >> 3, hh = H * hc;
     const float* row = hyper + (size_t)t * hh;
     float v[4][2][8];
@@ -143,6 +143,13 @@ __global__ void __launch_bounds__(256) k_pf_hc_prep(const float* __restrict__ hy
                 sq[g] += v[g][j][e] * v[g][j][e];
             }
         }
+    // the four streams' sums of squares in one pass (one barrier)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) sq[g] = wave_sum(sq[g]);
+    if ((tau & 63) == 0)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) red[tau >> 6][g] = sq[g];
+    __syncthreads();
     float inv[4];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
@@ -150,7 +157,7 @@ __global__ void __launch_bounds__(256) k_pf_hc_prep(const float* __restrict__ hy
             inv[g] = 0.0f;
             continue;
         }
-        inv[g] = 1.0f / sqrtf(block_sum(sq[g], red) / (float)H + eps);
+        inv[g] = 1.0f / sqrtf(((red[0][g] + red[1][g]) + (red[2][g] + red[3][g])) / (float)H + eps);
         if (tau == 0) inv_out[(size_t)t * hc + g] = inv[g];
     }
 #pragma unroll
@@ -161,8 +168,13 @@ __global__ void __launch_bounds__(256) k_pf_hc_prep(const float* __restrict__ hy
             if ((uint32_t)g >= hc || 256 * j >= bps) continue;  // uniform
             const bool ok = kb < bps;
             float x[8];
+            const uint4 nw = *reinterpret_cast<const uint4*>(norm + (size_t)g * H + min(kb, bps - 1) * 8);
+            const uint32_t nn[4] = {nw.x, nw.y, nw.z, nw.w};
 #pragma unroll
-            for (int e = 0; e < 8; ++e) x[e] = ok ? v[g][j][e] * inv[g] * bf16f(norm[(size_t)g * H + min(kb, bps - 1) * 8 + e]) : 0.0f;
+            for (int e = 0; e < 8; ++e) {
+                const float wn = __uint_as_float(e & 1 ? nn[e >> 1] & 0xffff0000u : nn[e >> 1] << 16);
+                x[e] = ok ? v[g][j][e] * inv[g] * wn : 0.0f;
+            }
             float s = ((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]));
             s += __shfl_xor(s, 1, 64);
             s += __shfl_xor(s, 2, 64);
@@ -720,51 +732,43 @@ __global__ void __launch_bounds__(256) k_pf_route(const float* __restrict__ logi
 // order: every GEMM row is independent), list[E] every token's shared
 // slot t (k+1) + k, and tiles[] the (group, 64-row tile) pairs in group
 // order, *ntiles of them.  One workgroup.
-__global__ void __launch_bounds__(256) k_pf_group(const uint32_t* __restrict__ ids, uint32_t T, uint32_t topk,
-                                                  uint32_t E, uint32_t cap, uint32_t* __restrict__ list,
-                                                  uint32_t* __restrict__ count, uint32_t* __restrict__ tiles,
-                                                  uint32_t* __restrict__ ntiles) {
-    __shared__ uint32_t cnt[513];
-    __shared__ uint32_t wsum[4];
+constexpr uint32_t PG_WG = 1024;  // threads of the grouping workgroup (one group each)
+
+__global__ void __launch_bounds__(PG_WG) k_pf_group(const uint32_t* __restrict__ ids, uint32_t T, uint32_t topk,
+                                                    uint32_t E, uint32_t cap, uint32_t* __restrict__ list,
+                                                    uint32_t* __restrict__ count, uint32_t* __restrict__ tiles,
+                                                    uint32_t* __restrict__ ntiles) {
+    __shared__ uint32_t cnt[PG_WG];
+    __shared__ uint32_t wsum[PG_WG / 64];
     const uint32_t tau = threadIdx.x, lane = tau & 63, wv = tau >> 6;
-    for (uint32_t e = tau; e <= E; e += CHK_WG) cnt[e] = 0;
+    cnt[tau] = 0;
     __syncthreads();
     const uint32_t slots = topk + 1;
-    for (uint32_t i = tau; i < T * topk; i += CHK_WG) {
+    for (uint32_t i = tau; i < T * topk; i += PG_WG) {
         const uint32_t t = i / topk, r = i % topk;
         const uint32_t e = min(ids[i], E - 1);
         const uint32_t p = atomicAdd(&cnt[e], 1u);
         list[(size_t)e * cap + p] = t * slots + r;
     }
-    for (uint32_t t = tau; t < T; t += CHK_WG) list[(size_t)E * cap + t] = t * slots + topk;
+    for (uint32_t t = tau; t < T; t += PG_WG) list[(size_t)E * cap + t] = t * slots + topk;
     __syncthreads();
     if (tau == 0) cnt[E] = T;
     __syncthreads();
-    // tiles per group, 3 groups per thread (E + 1 <= 768), block prefix sum
-    uint32_t nt[3], mine = 0;
-#pragma unroll
-    for (int k = 0; k < 3; ++k) {
-        const uint32_t e = tau * 3 + k;
-        nt[k] = e <= E ? (cnt[e] + 63) / 64 : 0;
-        mine += nt[k];
-        if (e <= E) count[e] = cnt[e];
-    }
-    uint32_t incl = mine;
+    // tiles per group (thread e takes group e), workgroup prefix sum
+    const uint32_t e = tau;
+    const uint32_t nt = e <= E ? (cnt[e] + 63) / 64 : 0;
+    if (e <= E) count[e] = cnt[e];
+    uint32_t incl = nt;
     for (int d = 1; d < 64; d <<= 1) {
         const uint32_t o = __shfl_up(incl, d, 64);
         if ((int)lane >= d) incl += o;
     }
     if (lane == 63) wsum[wv] = incl;
     __syncthreads();
-    uint32_t off = incl - mine;
+    uint32_t off = incl - nt;
     for (uint32_t k = 0; k < wv; ++k) off += wsum[k];
-#pragma unroll
-    for (int k = 0; k < 3; ++k) {
-        const uint32_t e = tau * 3 + k;
-        for (uint32_t q = 0; q < nt[k]; ++q) tiles[off + q] = e << 16 | q;
-        off += nt[k];
-    }
-    if (tau == CHK_WG - 1) *ntiles = off;
+    for (uint32_t q = 0; q < nt; ++q) tiles[off + q] = e << 16 | q;
+    if (tau == PG_WG - 1) *ntiles = off + nt;
 }
 
 // out[t][n] = sum_r w[t][r] yd[t][r][n] + sigmoid(sg[t]) yd[t][k][n]
@@ -1088,8 +1092,8 @@ void launch_pf_route(const float* logits, uint32_t T, uint32_t E, uint32_t topk,
 
 void launch_pf_group(const uint32_t* ids, uint32_t T, uint32_t topk, uint32_t E, uint32_t cap, uint32_t* list,
                      uint32_t* count, uint32_t* tiles, uint32_t* ntiles, hipStream_t st) {
-    if (E + 1 > 513) throw std::runtime_error("prefill grouping supports at most 512 experts");
-    k_pf_group<<<1, CHK_WG, 0, st>>>(ids, T, topk, E, cap, list, count, tiles, ntiles);
+    if (E + 1 > PG_WG) throw std::runtime_error("prefill grouping supports at most 1023 experts");
+    k_pf_group<<<1, PG_WG, 0, st>>>(ids, T, topk, E, cap, list, count, tiles, ntiles);
 }
 
 uint32_t pf_tile_bound(uint32_t T, uint32_t topk, uint32_t E) {
