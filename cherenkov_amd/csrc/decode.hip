@@ -177,6 +177,22 @@ CHK_DEV float lowbit_chunk(uint32_t w0, uint32_t w1, uint32_t lo, const float* x
     return s * (step * qd + half * xs) + b * xs;
 }
 
+// The same chunk's codes as Q4-order nibble words (word k holds inputs
+// 8k .. 8k + 7, lowest nibble first), for the dot8 form.  Byte b of word t
+// holds, at 2-bit positions pp = 0, 2, the codes of inputs 16 t + 2b and
+// 16 t + 2b + 1 (nibbles 2b, 2b + 1 of word 2t: mask 0x33 keeps exactly
+// them) and at pp = 1, 3 those of inputs 16 t + 2b + 8, + 9 (word 2t + 1).
+// Q3 codes are 2 code + lo bit (8 byte + 4 t + pp).
+template <int BITS>
+CHK_DEV uint4 lowbit_nibbles(uint32_t w0, uint32_t w1, uint32_t lo) {
+    constexpr uint32_t M = 0x33333333u;
+    if (BITS == 2) return make_uint4(w0 & M, (w0 >> 2) & M, w1 & M, (w1 >> 2) & M);
+    // lo bits sh and sh + 2 of every byte -> bits 0 and 4 of that byte
+    auto lob = [&](int sh) { return ((lo >> sh) & 0x01010101u) | (((lo >> (sh + 2)) & 0x01010101u) << 4); };
+    return make_uint4(((w0 & M) << 1) | lob(0), (((w0 >> 2) & M) << 1) | lob(1), ((w1 & M) << 1) | lob(4),
+                      (((w1 >> 2) & M) << 1) | lob(5));
+}
+
 // A routed-expert projection inside its record: Q4 view or low-bit pointers.
 struct ExpMat {
     const uint8_t* w;
@@ -230,11 +246,38 @@ struct ExpFrag {
         }
     }
 
-    // Q4 records: inputs in nibble planes
+    // inputs in nibble planes: Q4 words as they are, Q3/Q2 codes expanded
+    // to nibbles, the midpoint rule folded into the scale and bias
+    // (step s, half s + b)
     template <int NB>
     CHK_DEV void dot(const XqFrag<NB, CPL>& xr, float (&acc)[R][NB]) const {
-        static_assert(BITS == 4, "low-bit records take f32 inputs");
-        q.template dot<NB>(xr, acc);
+        if constexpr (BITS == 4) {
+            q.template dot<NB>(xr, acc);
+        } else {
+            constexpr float step = BITS == 2 ? 4.0f : 2.0f, half = BITS == 2 ? 1.5f : 0.5f;
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                uint4 wn[CPL];
+                float s2[CPL], b2[CPL];
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) {
+                    wn[c] = lowbit_nibbles<BITS>(w0[i][c], w1[i][c], lo[i][c]);
+                    const float sc = bf16f(q.s16[i][c]);
+                    s2[c] = step * sc;
+                    b2[c] = fmaf(half, sc, bf16f(q.b16[i][c]));
+                }
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+                    float a = 0.0f;
+#pragma unroll
+                    for (int c = 0; c < CPL; ++c) {
+                        const float p = q4_dot8(wn[c], xr.c[b][c], s2[c], b2[c]);
+                        a += q.ok[c] ? p : 0.0f;
+                    }
+                    acc[i][b] = group_sum<LPR>(a);
+                }
+            }
+        }
     }
 
     // Q3/Q2 records: f32 inputs
@@ -863,9 +906,6 @@ __global__ void __launch_bounds__(GU_WG) k_moe_gate_up(MoeArgs a) {
     const uint32_t nch = a.H >> 5;
     const bool routed = slot < a.topk;
     const bool publish = slot + 1 == a.topk && c == 0 && w == 0;
-    // f32 inputs only for low-bit records (their dot is not the dot8 form)
-    XFrag<1, 1> xr;
-    if (BITS != 4 && routed) xr.template load<64>(a.x + (size_t)b * a.H, 0, nch, lane);
     uint32_t my_id = 0;
     float my_p = 0.0f;
     if (routed)
@@ -895,15 +935,14 @@ __global__ void __launch_bounds__(GU_WG) k_moe_gate_up(MoeArgs a) {
     }
     if (publish) publish_routing(a, b, lane, my_id, my_p);
     xq_prep<GU_WG>(a.x, a.H, a.H, a.nb, xq_lds, XqIdentity{});
+    XqFrag<1, 1> xq;
+    xq.template read<64>(xq_lds + b * nch, nch, lane);
     if (q4path) {
-        XqFrag<1, 1> xq;
-        xq.template read<64>(xq_lds + b * nch, nch, lane);
         fg.template dot<1>(xq, g);
         fu.template dot<1>(xq, u);
     } else if constexpr (BITS != 4) {
-        xr.sums();
-        lg.template dot<1>(xr, g);
-        lu.template dot<1>(xr, u);
+        lg.template dot<1>(xq, g);
+        lu.template dot<1>(xq, u);
     }
     if (lane < R) {
         float gv = g[0][0], uv = u[0][0];
@@ -975,7 +1014,6 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a) {
             // low-bit routed slots take their own fragments and f32 inputs
             Q4Frag<LPR, 1, R> fq[PASSES];
             ExpFrag<LPR, 1, R, BITS> fl[PASSES];
-            XFrag<1, 1> xr[PASSES];
             XqFrag<1, 1> xq[PASSES];
             float wgt[PASSES];
 #pragma unroll
@@ -995,7 +1033,6 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a) {
                     fq[pass].issue(mm, rows, lir);
                 } else if (sl < a.topk) {
                     fl[pass].issue(expert_mat(a.X, rec, 2, a.H, a.I), rows, lir);
-                    load_x<LPR, 1, 1>(a.act + ((size_t)b * slots + sl) * a.I, 0, nch, lir, xr[pass]);
                 } else {
                     fq[pass].issue(a.sh_down, rows, lir);
                 }
@@ -1010,7 +1047,7 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a) {
                 const uint32_t sl = slot < slots ? slot : slots - 1;
                 float acc[R][1];
                 if constexpr (BITS != 4) {
-                    if (sl < a.topk) fl[pass].template dot<1>(xr[pass], acc);
+                    if (sl < a.topk) fl[pass].template dot<1>(xq[pass], acc);
                     else fq[pass].template dot<1>(xq[pass], acc);
                 } else {
                     fq[pass].template dot<1>(xq[pass], acc);
