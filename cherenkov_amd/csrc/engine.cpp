@@ -1071,7 +1071,7 @@ void ChkEngine::prefill_rows(const uint32_t* toks, uint32_t n, uint32_t* next, u
 constexpr uint32_t PF_MAX_ROWS = 4096;                  // rows per chunk (gpu/prefill.rs:116)
 
 bool ChkEngine::pf_supported() const {
-    return o.experts == 4 && !has_mtp && !D.qsa && D.lowrank % 64 == 0 && D.H % 64 == 0 && D.H <= 4096 && D.hc <= 4 &&
+    return (o.experts == 4 || o.experts == 3 || o.experts == 2) && !has_mtp && !D.qsa && D.lowrank % 64 == 0 && D.H % 64 == 0 && D.H <= 4096 && D.hc <= 4 &&
            (D.dv == 64 || D.dv == 128 || D.dv == 256) && D.I % 64 == 0 && (D.nh * D.hd) % 64 == 0 &&
            D.v_dim % 64 == 0 && D.E + 1 <= 513 && D.nh % D.nkv == 0 &&
            (D.nh / D.nkv == 1 || D.nh / D.nkv == 2 || D.nh / D.nkv == 4 || D.nh / D.nkv == 8) &&

@@ -239,8 +239,15 @@ CHK_DEV h8 pf_unpack(uint32_t w, const Q4Consts& qk) {
 // terms so every product is exact).  Needs G % 8 == 0 and 16-byte aligned
 // rows; otherwise each lane loads its scale and bias per group and folds
 // both in the loop.
-template <int NMAT, int EPI, bool SBL>
+// BITS: the routed-expert records' precision.  Q3 / Q2 rows (lowbit.rs
+// chunks of 32 codes in 3 / 2 words) load, per group and lane, the word of
+// the lane's 16 inputs (and Q3's low-bit word) and expand it to the two
+// Q4-order nibble words the unpack expects; their scale and bias carry the
+// midpoint rule (step s, half s + b), folded per lane in f32, so such
+// launches run without staged scales.
+template <int NMAT, int EPI, bool SBL, int BITS = 4>
 __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
+    static_assert(BITS == 4 || !SBL, "low-bit records fold their scales per lane");
     constexpr int NJ = 4 / NMAT;  // 16-wide output tiles per matrix per wave
     constexpr int NI = 4;         // 16-row slices per wave
     constexpr int SBR = 9;        // words per staged scale row (8 groups + pad)
@@ -269,6 +276,8 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
     // segment matrix).  Local row lr = ((w NMAT + q) NJ + j) 16 + col of the
     // workgroup's 256 is matrix q, tile j of wave w.
     const bool expert = a.X.base && grp < a.X.experts;
+    const bool lowbit = BITS != 4 && expert;
+    constexpr uint32_t CW = BITS == 2 ? 2 : 3;  // words per 32-code low-bit chunk
     const uint8_t* rec = a.X.base + ((size_t)a.record_layer * a.X.experts + grp) * a.X.stride;
     const uint32_t* wb = expert ? reinterpret_cast<const uint32_t*>(rec) : a.wbase;
     const uint16_t* sbase = expert ? reinterpret_cast<const uint16_t*>(rec) : a.sbase;
@@ -287,7 +296,7 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
             const uint64_t w0 = part == 0 ? a.X.gate_w : part == 1 ? a.X.up_w : a.X.down_w;
             const uint64_t s0 = part == 0 ? a.X.gate_s : part == 1 ? a.X.up_s : a.X.down_s;
             const uint64_t b0 = part == 0 ? a.X.gate_b : part == 1 ? a.X.up_b : a.X.down_b;
-            ow = (uint32_t)(w0 / 4) + r * KB;
+            ow = (uint32_t)(w0 / 4) + r * (BITS == 4 ? KB : (K >> 5) * CW);
             os = (uint32_t)(s0 / 2) + r * G;
             ob = (uint32_t)(b0 / 2) + r * G;
             return;
@@ -361,7 +370,17 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
         for (int q = 0; q < NMAT; ++q)
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
-                bw[slot][q][j] = *reinterpret_cast<const u32x2*>(wb + wo[q][j] + g * 8 + kq * 2);
+                if (BITS == 4) {
+                    bw[slot][q][j] = *reinterpret_cast<const u32x2*>(wb + wo[q][j] + g * 8 + kq * 2);
+                } else {
+                    // two word loads either way: a Q4 row's words 2 kq, + 1, or a
+                    // low-bit row's word for inputs 16 (kq % 2) .. of chunk
+                    // 2 g + kq / 2 and (Q3) that chunk's low-bit word
+                    const uint32_t cb = wo[q][j] + (2 * g + (kq >> 1)) * CW;
+                    const uint32_t i0 = lowbit ? cb + (kq & 1) : wo[q][j] + g * 8 + kq * 2;
+                    const uint32_t i1 = lowbit ? (BITS == 3 ? cb + 2 : i0) : i0 + 1;
+                    bw[slot][q][j] = u32x2{wb[i0], wb[i1]};
+                }
                 if (!SBL) {
                     bs[slot][SBL ? 0 : q][SBL ? 0 : j] = sbase[so[q][j] + g];
                     bb[slot][SBL ? 0 : q][SBL ? 0 : j] = sbase[bo[q][j] + g];
@@ -412,8 +431,23 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
         for (int q = 0; q < NMAT; ++q)
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
-                bq[q][j][0] = pf_unpack(bw[P][q][j].x, qk);
-                bq[q][j][1] = pf_unpack(bw[P][q][j].y, qk);
+                uint32_t w0 = bw[P][q][j].x, w1 = bw[P][q][j].y;
+                if (BITS != 4 && lowbit) {
+                    // the code word's 2-bit fields pp = 0, 2 of each byte are the
+                    // nibbles of the lane's first Q4 word (mask 0x33), pp = 1, 3
+                    // those of its second; Q3 codes take the low bit from the
+                    // lo word (bit 8 byte + 4 (kq % 2) + pp) as 2 code + bit
+                    constexpr uint32_t M = 0x33333333u;
+                    const uint32_t c = bw[P][q][j].x, lo = bw[P][q][j].y, sh = 4 * (kq & 1);
+                    w0 = c & M;
+                    w1 = (c >> 2) & M;
+                    if (BITS == 3) {
+                        w0 = (w0 << 1) | ((lo >> sh) & 0x01010101u) | (((lo >> (sh + 2)) & 0x01010101u) << 4);
+                        w1 = (w1 << 1) | ((lo >> (sh + 1)) & 0x01010101u) | (((lo >> (sh + 3)) & 0x01010101u) << 4);
+                    }
+                }
+                bq[q][j][0] = pf_unpack(w0, qk);
+                bq[q][j][1] = pf_unpack(w1, qk);
             }
         float sc[NMAT][NJ], bi[NMAT][NJ];
 #pragma unroll
@@ -427,6 +461,11 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
                 } else {
                     sc[q][j] = bf16f(bs[P][SBL ? 0 : q][SBL ? 0 : j]);
                     bi[q][j] = bf16f(bb[P][SBL ? 0 : q][SBL ? 0 : j]);
+                    if (BITS != 4 && lowbit) {
+                        // midpoint rule: w = (step q + half) s + b
+                        bi[q][j] = fmaf(BITS == 2 ? 1.5f : 0.5f, sc[q][j], bi[q][j]);
+                        sc[q][j] *= BITS == 2 ? 4.0f : 2.0f;
+                    }
                 }
             }
 #pragma unroll
@@ -1048,6 +1087,19 @@ void launch_pf_gemm_args(const PfGemmArgs& args, int epi, uint32_t grid_y, hipSt
         if (sbl) k_pf_gemm<NM, E, true><<<dim3(GX, grid_y, ksplit), PF_WG, 0, st>>>(a); \
         else k_pf_gemm<NM, E, false><<<dim3(GX, grid_y, ksplit), PF_WG, 0, st>>>(a);    \
     } while (0)
+    const uint32_t xbits = a.X.base ? a.X.bits : 4;
+    if (xbits != 4) {
+        // grouped expert GEMMs over Q3 / Q2 records (scales folded per lane)
+        if (epi != PE_STORE && epi != PE_SILU_MUL) throw std::runtime_error("low-bit records: gate/up and down only");
+        const uint32_t gx = epi == PE_STORE ? (a.N + 255) / 256 : (a.N + 127) / 128;
+        const dim3 grid(gx, grid_y, ksplit);
+        if (xbits == 3 && epi == PE_STORE) k_pf_gemm<1, PE_STORE, false, 3><<<grid, PF_WG, 0, st>>>(a);
+        else if (xbits == 3) k_pf_gemm<2, PE_SILU_MUL, false, 3><<<grid, PF_WG, 0, st>>>(a);
+        else if (xbits == 2 && epi == PE_STORE) k_pf_gemm<1, PE_STORE, false, 2><<<grid, PF_WG, 0, st>>>(a);
+        else if (xbits == 2) k_pf_gemm<2, PE_SILU_MUL, false, 2><<<grid, PF_WG, 0, st>>>(a);
+        else throw std::runtime_error("expert records of 4, 3 or 2 bits");
+        return;
+    }
     switch (epi) {
     case PE_STORE: PF_GEMM(1, PE_STORE, (a.N + 255) / 256); break;
     case PE_INJECT: PF_GEMM(1, PE_INJECT, (a.N + 255) / 256); break;

@@ -109,6 +109,37 @@ def test_gemm_prefill_matches_row_path(have_gpu, splits):
         b.close()
 
 
+@pytest.mark.parametrize("bits,splits", [(3, [100]), (3, [70, 45]), (2, [100]), (2, [5])])
+def test_gemm_prefill_lowbit_experts_matches_row_path(have_gpu, bits, splits):
+    """Q3/Q2 expert records (dense weights stay Q4): the grouped expert
+    GEMM expands the codes in registers and folds the midpoint rule into
+    scale and bias; logits, DeltaNet state and greedy tokens match the row
+    path over the same prompt."""
+    cfg = presets.tiny(mtp=0)
+    rng = np.random.default_rng(100 * bits + sum(splits))
+    prompt = rng.integers(0, cfg.vocab_size, size=sum(splits)).tolist()
+    a = Engine(cfg, experts=bits, drafts=0, max_t=256)
+    b = Engine(cfg, experts=bits, drafts=0, max_t=256)
+    try:
+        i = 0
+        for n in splits:
+            a.prefill_chunk(prompt[i:i + n])
+            i += n
+        la = a.logits_row(0)
+        nxt_b, lb = row_prefill(b, prompt)
+        assert_close(la, lb, f"Q{bits} prefill last-row logits", abs_frac=1e-3, min_cos=0.99999)
+        for layer in range(cfg.num_hidden_layers):
+            if (layer + 1) % cfg.full_attention_interval == 0:
+                continue
+            sa, _ = dn_state(a, cfg, layer)
+            sb, _ = dn_state(b, cfg, layer)
+            assert_close(sa, sb, f"Q{bits} layer {layer} state", abs_frac=1e-3, min_cos=0.99999)
+        greedy_pair(a, b, nxt_b, 4, f"Q{bits}")
+    finally:
+        a.close()
+        b.close()
+
+
 def test_gemm_prefill_matches_oracle(have_gpu):
     """The GEMM prefill's last-row logits against the oracle run token by
     token over the same prompt (forward_token, cpu.rs, with the q8 KV rule),
@@ -131,16 +162,18 @@ def test_gemm_prefill_matches_oracle(have_gpu):
         assert nxt == int(np.argmax(ref))
 
 
-def test_gemm_prefill_full_width(have_gpu):
+@pytest.mark.parametrize("bits", [4, 3, 2])
+def test_gemm_prefill_full_width(have_gpu, bits):
     """Config 5 widths (hidden 2048, 512 experts top-10, 16/32 DeltaNet
     heads, 16q/2kv x 256 attention, vocab 151936) on 4 layers, where f32
     rounding stays small end to end: a 200-token GEMM prefill within 1e-3 of
-    the row path (logits, DeltaNet state and history), then 4 greedy tokens."""
+    the row path (logits, DeltaNet state and history), then 4 greedy tokens,
+    with Q4, Q3 and Q2 expert records."""
     cfg = presets.qwen3next_80b_shape(layers=4, mtp=0)
-    rng = np.random.default_rng(78)
+    rng = np.random.default_rng(82 - bits)
     prompt = rng.integers(0, cfg.vocab_size, size=200).tolist()
-    a = Engine(cfg, experts=4, drafts=0, max_t=256)
-    b = Engine(cfg, experts=4, drafts=0, max_t=256)
+    a = Engine(cfg, experts=bits, drafts=0, max_t=256)
+    b = Engine(cfg, experts=bits, drafts=0, max_t=256)
     try:
         nxt_a, _ = a.prefill_chunk(prompt)
         la = a.logits_row(0)
