@@ -11,6 +11,7 @@
 // and the blocks it calls); the Metal dispatch plan this replaces:
 // src/qwen4_exp/gpu/decode.rs:13-294 and kernels/{common,qwen4_exp}/*.metal.
 #include <stdexcept>
+#include <type_traits>
 
 #include "kernels_internal.h"
 
@@ -107,7 +108,10 @@ extern __shared__ XqChunk xq_lds[];
 template <int LPR, int CPL, int R>
 struct Q4Frag {
     uint4 wq[R][CPL];
-    uint16_t s16[R][CPL], b16[R][CPL];
+    // raw bf16 scale and bias, one per 32-bit register: packing two into
+    // one register (or converting them where they load) would make the
+    // wave wait for them, and for every load issued before, right there
+    uint32_t s16[R][CPL], b16[R][CPL];
     bool ok[CPL];
 
     CHK_DEV void issue(const Q4Mat& m, const uint32_t (&rows)[R], int lir) {
@@ -136,7 +140,8 @@ struct Q4Frag {
                 float a = 0.0f;
 #pragma unroll
                 for (int c = 0; c < CPL; ++c) {
-                    const float p = q4_dot8(wq[i][c], xf.c[b][c], bf16f(s16[i][c]), bf16f(b16[i][c]));
+                    const float p = q4_dot8(wq[i][c], xf.c[b][c], __uint_as_float(s16[i][c] << 16),
+                                            __uint_as_float(b16[i][c] << 16));
                     a += ok[c] ? p : 0.0f;
                 }
                 acc[i][b] = group_sum<LPR>(a);
@@ -341,9 +346,22 @@ __global__ void __launch_bounds__(256) k_hc_down(HcDev w, const float* __restric
     const uint32_t total = w.down.out + (w.has_inject ? w.inject.out : 0u);
     const uint32_t r0 = blockIdx.x * HR;
     const uint32_t hh = H * hc, nch = H >> 5;  // chunks per stream
-    // issue every weight load of the HR rows first
+    // this stream's inputs first, then every weight load of the HR rows:
+    // the RMS and the normalised pairs are formed while the weights fly
+    float xin[NB][CPL][32];
+    uint4 nrm[CPL][4];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        const uint32_t cc = min(lane + 64u * c, nch - 1);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) ldx32(hyper + (size_t)b * hh + (size_t)g * H + cc * 32, xin[b][c]);
+        const uint4* np = reinterpret_cast<const uint4*>(w.norm + (size_t)g * H + cc * 32);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) nrm[c][q] = np[q];
+    }
+    asm volatile("" ::: "memory");  // compiler-only: weight loads stay behind these
     uint4 wq[HR][CPL];
-    uint16_t s16[HR][CPL], b16[HR][CPL];
+    uint32_t s16[HR][CPL], b16[HR][CPL];  // raw bf16, one per register
 #pragma unroll
     for (int i = 0; i < HR; ++i) {
         const uint32_t row = min(r0 + i, total - 1);
@@ -360,6 +378,19 @@ __global__ void __launch_bounds__(256) k_hc_down(HcDev w, const float* __restric
             b16[i][c] = br[ch >> 1];
         }
     }
+    // compiler-only: the input work below may not be hoisted above the
+    // weight loads
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int j = 0; j < 32; ++j) asm volatile("" : "+v"(xin[b][c][j])::"memory");
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            asm volatile("" : "+v"(nrm[c][q].x), "+v"(nrm[c][q].y), "+v"(nrm[c][q].z), "+v"(nrm[c][q].w)::"memory");
+    }
     const Q4Consts k;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
@@ -368,14 +399,12 @@ __global__ void __launch_bounds__(256) k_hc_down(HcDev w, const float* __restric
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
             const uint32_t ch = lane + 64 * c, cc = min(ch, nch - 1);
-            float xv[32];
-            ldx32(hyper + (size_t)b * hh + (size_t)g * H + cc * 32, xv);
-            const uint4* np = reinterpret_cast<const uint4*>(w.norm + (size_t)g * H + cc * 32);
+            float (&xv)[32] = xin[b][c];
             // four independent partial sums per reduction (short chains)
             float t4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const uint4 nv = np[q];
+                const uint4 nv = nrm[c][q];
                 const uint32_t nn[4] = {nv.x, nv.y, nv.z, nv.w};
 #pragma unroll
                 for (int h = 0; h < 8; ++h) {
@@ -436,21 +465,32 @@ __global__ void __launch_bounds__(256) k_hc_up_mix(HcDev w, const float* __restr
         uint32_t o = o0 + og * R + i;
         rows[i] = g * H + (o < H ? o : H - 1);
     }
+    // d first: its quantisation then overlaps the up rows' flight
+    XqStaged<1, 256> xs;
+    const bool staged = xs.fits(w.up.in, NB);
+    if (staged) xs.load(d, w.down.out, w.up.in, NB);
     Q4Frag<LPR, 1, R> f;
     f.issue(w.up, rows, lir);
-    // the row-group leader prefetches normed = hyper * inv * w for its outputs
-    float normed[R][NB];
+    // the row-group leader prefetches hyper, inv and w for its outputs'
+    // normed = hyper * inv * w, formed only at the end (using them here
+    // would wait for every weight load issued above)
+    float hyv[R][NB], invv[NB];
+    uint32_t wnr[R];  // raw bf16, one per register (packing would wait)
     if (lir == 0 && slot_ok) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) invv[b] = inv[b * hc + g];
 #pragma unroll
         for (int i = 0; i < R; ++i) {
             const uint32_t o = min(o0 + og * R + i, H - 1);
             const size_t j = (size_t)g * H + o;
-            const float wn = bf16f(w.norm[j]);
+            wnr[i] = w.norm[j];
 #pragma unroll
-            for (int b = 0; b < NB; ++b) normed[i][b] = hyper[(size_t)b * H * hc + j] * inv[b * hc + g] * wn;
+            for (int b = 0; b < NB; ++b) hyv[i][b] = hyper[(size_t)b * H * hc + j];
         }
     }
-    xq_prep(d, w.down.out, w.up.in, NB, xq_lds, XqIdentity{});
+    __builtin_amdgcn_sched_barrier(0);
+    if (staged) xs.store(w.up.in, NB, xq_lds, XqIdentity{});
+    else xq_prep(d, w.down.out, w.up.in, NB, xq_lds, XqIdentity{});
     XqFrag<NB, 1> xr;
     xr.template read<LPR>(xq_lds, w.up.in >> 5, lir);
     float acc[R][NB];
@@ -461,7 +501,8 @@ __global__ void __launch_bounds__(256) k_hc_up_mix(HcDev w, const float* __restr
             const uint32_t o = o0 + og * R + i;
 #pragma unroll
             for (int b = 0; b < NB; ++b)
-                red[wv][b][(og * R + i) * hc + g] = o < H ? sigmoidf_(acc[i][b]) * normed[i][b] : 0.0f;
+                red[wv][b][(og * R + i) * hc + g] =
+                    o < H ? sigmoidf_(acc[i][b]) * (hyv[i][b] * invv[b] * __uint_as_float(wnr[i] << 16)) : 0.0f;
         }
     }
     __syncthreads();
@@ -482,10 +523,13 @@ __global__ void __launch_bounds__(256) k_hc_up_mix(HcDev w, const float* __restr
 // R rows per wave per grid-stride step, per-segment epilogues.
 // Per-row epilogue inputs, fetched by lane i for row i while the weights
 // are in flight.
+// The bf16 parameters stay raw, one per 32-bit register, until the
+// epilogue: converting (or packing) them at the load would make the wave
+// wait for each one, and for every weight load issued before it, there.
 struct EpiIn {
     float hist[8];
-    float cw[9];
-    float p0, p1;
+    uint32_t cw[9];
+    uint32_t p0, p1;
 };
 
 CHK_DEV void epi_prefetch(const SegArgs& a, const Seg& sg, uint32_t r, EpiIn& e) {
@@ -496,15 +540,25 @@ CHK_DEV void epi_prefetch(const SegArgs& a, const Seg& sg, uint32_t r, EpiIn& e)
             if (j < km1) e.hist[j] = a.hist[(size_t)r * km1 + j];
 #pragma unroll
         for (uint32_t j = 0; j < 9; ++j)
-            if (j < a.ck) e.cw[j] = bf16f(a.conv_w[(size_t)r * a.ck + j]);
+            if (j < a.ck) e.cw[j] = a.conv_w[(size_t)r * a.ck + j];
     } else if (sg.epi == EPI_DN_DECAY) {
-        e.p0 = bf16f(a.a_log[r]);
-        e.p1 = bf16f(a.dt_bias[r]);
+        e.p0 = a.a_log[r];
+        e.p1 = a.dt_bias[r];
     }
+    asm volatile("" ::: "memory");  // compiler-only: later loads stay behind these
+    __builtin_amdgcn_sched_barrier(0);
 }
 
 template <int NB>
 CHK_DEV void seg_epilogue(const SegArgs& a, const Seg& sg, uint32_t r, const float (&acc)[NB], EpiIn& e) {
+    // compiler-only: the prefetched values are redefined here, so no work
+    // on them (exp(A_log), the history products) is hoisted to the
+    // prefetch, where it would wait for the whole weight stream
+#pragma unroll
+    for (int j = 0; j < 8; ++j) asm volatile("" : "+v"(e.hist[j]));
+#pragma unroll
+    for (int j = 0; j < 9; ++j) asm volatile("" : "+v"(e.cw[j]));
+    asm volatile("" : "+v"(e.p0), "+v"(e.p1));
     switch (sg.epi) {
     case EPI_RAW:
 #pragma unroll
@@ -522,11 +576,11 @@ CHK_DEV void seg_epilogue(const SegArgs& a, const Seg& sg, uint32_t r, const flo
             float wl = 0.0f;
 #pragma unroll
             for (uint32_t j = 0; j < 9; ++j)
-                if (j == km1) wl = e.cw[j];
+                if (j == km1) wl = __uint_as_float(e.cw[j] << 16);
             float s = wl * cur;
 #pragma unroll
             for (uint32_t j = 0; j < 8; ++j)
-                if (j < km1) s += e.cw[j] * e.hist[j];
+                if (j < km1) s += __uint_as_float(e.cw[j] << 16) * e.hist[j];
 #pragma unroll
             for (uint32_t j = 0; j < 7; ++j)
                 if (j + 1 < km1) e.hist[j] = e.hist[j + 1];
@@ -550,7 +604,7 @@ CHK_DEV void seg_epilogue(const SegArgs& a, const Seg& sg, uint32_t r, const flo
         // g = -exp(A_log) * softplus(a + dt_bias), decay = e^g (cpu.rs:775-777)
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-            const float gg = -expf(e.p0) * softplusf_(acc[b] + e.p1);
+            const float gg = -expf(__uint_as_float(e.p0 << 16)) * softplusf_(acc[b] + __uint_as_float(e.p1 << 16));
             sg.y[(size_t)b * sg.ys + r] = expf(gg);
         }
         break;
@@ -567,11 +621,17 @@ __global__ void __launch_bounds__(256) k_qmv(SegArgs a) {
     const uint32_t groups = (a.total + R - 1) / R;
     const uint32_t nch = a.seg[0].m.in >> 5;  // every segment shares x (launch_qmv checks)
     XqFrag<NB, CPL> xr;
-    // The first pass issues its weight and epilogue loads before the
-    // workgroup quantises x; waves without a group still join that prep.
-    for (uint32_t grp = global_wave(), pass = 0;; grp += total_waves(), ++pass) {
+    // First pass: the epilogue inputs, then x, then the weights go out, and
+    // the workgroup quantises x while the weights fly (waves without a
+    // group still join that prep).  The epilogue loads come first because
+    // their count differs between segments: behind x they would make the
+    // compiler's wait for x cover the weights.  The pass is peeled: a loop
+    // around it would make the compiler wait at the loop head for x too.
+    XqStaged<NB, 256> xs;
+    const bool staged = xs.fits(a.seg[0].m.in, NB);
+    auto pass_body = [&](uint32_t grp, auto first) {
+        constexpr bool FIRST = decltype(first)::value;
         const bool live = grp < groups;
-        if (!live && pass > 0) break;
         const uint32_t row0 = (live ? grp : 0) * R;
         int si = 0;
 #pragma unroll
@@ -582,20 +642,24 @@ __global__ void __launch_bounds__(256) k_qmv(SegArgs a) {
         uint32_t rows[R];
 #pragma unroll
         for (int i = 0; i < R; ++i) rows[i] = min(row0 - sg.row0 + i, sg.m.out - 1);
-        Q4Frag<64, CPL, R> f;
-        if (live) f.issue(sg.m, rows, lane);
-        // lane i < R owns row i's epilogue; its inputs load alongside the weights
+        // lane i < R owns row i's epilogue; its inputs load ahead of the weights
         uint32_t my_row = rows[0];
 #pragma unroll
         for (int i = 1; i < R; ++i)
             if (lane == i) my_row = rows[i];
         EpiIn e;
         if (live && lane < R) epi_prefetch(a, sg, my_row, e);
-        if (pass == 0) {
-            xq_prep(a.seg[0].x, a.seg[0].xs, a.seg[0].m.in, NB, xq_lds, XqIdentity{});
+        if constexpr (FIRST) {
+            if (staged) xs.load(a.seg[0].x, a.seg[0].xs, a.seg[0].m.in, NB);
+        }
+        Q4Frag<64, CPL, R> f;
+        f.issue(sg.m, rows, lane);  // dead waves load clamped rows, unused
+        if constexpr (FIRST) {
+            if (staged) xs.store(a.seg[0].m.in, NB, xq_lds, XqIdentity{});
+            else xq_prep(a.seg[0].x, a.seg[0].xs, a.seg[0].m.in, NB, xq_lds, XqIdentity{});
             xr.template read<64>(xq_lds, nch, lane);
         }
-        if (!live) break;
+        if (!live) return;
         float acc[R][NB];
         f.template dot<NB>(xr, acc);
         float mine[NB];
@@ -607,7 +671,10 @@ __global__ void __launch_bounds__(256) k_qmv(SegArgs a) {
                 if (lane == i) mine[b] = acc[i][b];
         }
         if (lane < R && row0 - sg.row0 + lane < sg.m.out) seg_epilogue<NB>(a, sg, my_row, mine, e);
-    }
+    };
+    pass_body(global_wave(), std::true_type{});
+    for (uint32_t grp = global_wave() + total_waves(); grp < groups; grp += total_waves())
+        pass_body(grp, std::false_type{});
 }
 
 // --------------------------------------------- Q4 matvec + hyper inject
@@ -644,15 +711,17 @@ __global__ void __launch_bounds__(256) k_qmv_inject(InjArgs a) {
     const uint32_t li = lane / a.hc, lg = lane % a.hc;
     const bool owner = li < (uint32_t)R && a.hyper;
     XqFrag<NB, CPL> xr;
-    for (uint32_t grp = global_wave(), pass = 0;; grp += total_waves(), ++pass) {
+    // plain inputs load ahead of the weights (see XqStaged)
+    // (first pass peeled, and the hyper loads ahead of x, as in k_qmv)
+    XqStaged<(NB < 2 ? 2 : NB), 256> xs;
+    const bool staged = XM != XM_DN_GATED && xs.fits(m.in, NB);
+    auto pass_body = [&](uint32_t grp, auto first) {
+        constexpr bool FIRST = decltype(first)::value;
         const bool live = grp < groups;
-        if (!live && pass > 0) break;
         const uint32_t g0 = live ? grp : 0;
         uint32_t rows[R];
 #pragma unroll
         for (int i = 0; i < R; ++i) rows[i] = g0 * R + i;
-        Q4Frag<64, CPL, R> f;
-        if (live) f.issue(m, rows, lane);
         float hy[NB], ij[NB];
         if (live && owner)
 #pragma unroll
@@ -660,7 +729,13 @@ __global__ void __launch_bounds__(256) k_qmv_inject(InjArgs a) {
                 hy[b] = a.hyper[(size_t)b * H * a.hc + lg * H + g0 * R + li];
                 ij[b] = a.inj[b * a.hc + lg];
             }
-        if (pass == 0) {
+        asm volatile("" ::: "memory");  // compiler-only: x and the weights stay behind
+        if constexpr (FIRST) {
+            if (staged) xs.load(a.x, a.xs, m.in, NB);
+        }
+        Q4Frag<64, CPL, R> f;
+        f.issue(m, rows, lane);  // dead waves load clamped rows, unused
+        if constexpr (FIRST) {
             if (XM == XM_DN_GATED && a.x_xq) {
                 // the scan's chunks of y w sigmoid(z), scaled by their head's
                 // 1/rms: a common factor of m, d and the chunk sum
@@ -687,11 +762,12 @@ __global__ void __launch_bounds__(256) k_qmv_inject(InjArgs a) {
                 }
             } else {
                 if (XM == XM_DN_GATED) xq_prep(a.x, a.xs, m.in, NB, xq_lds, DnGateScale{&a});
+                else if (staged) xs.store(m.in, NB, xq_lds, XqIdentity{});
                 else xq_prep(a.x, a.xs, m.in, NB, xq_lds, XqIdentity{});
                 xr.template read<64>(xq_lds, nch, lane);
             }
         }
-        if (!live) break;
+        if (!live) return;
         float acc[R][NB];
         f.template dot<NB>(xr, acc);
         if (a.raw_out && lane < R) {
@@ -714,7 +790,10 @@ __global__ void __launch_bounds__(256) k_qmv_inject(InjArgs a) {
                 a.hyper[(size_t)b * H * a.hc + lg * H + grp * R + li] = hy[b] + v * ij[b];
             }
         }
-    }
+    };
+    pass_body(global_wave(), std::true_type{});
+    for (uint32_t grp = global_wave() + total_waves(); grp < groups; grp += total_waves())
+        pass_body(grp, std::false_type{});
 }
 
 // ------------------------------------------------------- DeltaNet step
@@ -906,6 +985,11 @@ __global__ void __launch_bounds__(GU_WG) k_moe_gate_up(MoeArgs a) {
     const uint32_t nch = a.H >> 5;
     const bool routed = slot < a.topk;
     const bool publish = slot + 1 == a.topk && c == 0 && w == 0;
+    // x (independent of the routing) first, so its quantisation overlaps
+    // the expert weights' flight
+    XqStaged<2, GU_WG> xs;
+    const bool staged = xs.fits(a.H, a.nb);
+    if (staged) xs.load(a.x, a.H, a.H, a.nb);
     uint32_t my_id = 0;
     float my_p = 0.0f;
     if (routed)
@@ -934,7 +1018,8 @@ __global__ void __launch_bounds__(GU_WG) k_moe_gate_up(MoeArgs a) {
         lu.issue(expert_mat(a.X, rec, 1, a.I, a.H), rows, lane);
     }
     if (publish) publish_routing(a, b, lane, my_id, my_p);
-    xq_prep<GU_WG>(a.x, a.H, a.H, a.nb, xq_lds, XqIdentity{});
+    if (staged) xs.store(a.H, a.nb, xq_lds, XqIdentity{});
+    else xq_prep<GU_WG>(a.x, a.H, a.H, a.nb, xq_lds, XqIdentity{});
     XqFrag<1, 1> xq;
     xq.template read<64>(xq_lds + b * nch, nch, lane);
     if (q4path) {
@@ -1084,14 +1169,19 @@ __global__ void __launch_bounds__(256) k_lm_head(Q4Mat m, const float* __restric
     for (int b = 0; b < NB; ++b) { bv[b] = -INFINITY; bi[b] = 0xffffffffu; }
     const uint32_t groups = m.out / R, nch = m.in >> 5;
     // each wave's next row group is in flight while it reduces the current
-    // one; the first is issued before the workgroup quantises x
+    // one; x loads first, then the first group's, then the workgroup
+    // quantises x
+    XqStaged<NB, 256> xs;
+    const bool staged = xs.fits(m.in, NB);
+    if (staged) xs.load(x, m.in, m.in, NB);
     uint32_t grp = global_wave();
     uint32_t rows[R];
 #pragma unroll
     for (int i = 0; i < R; ++i) rows[i] = grp * R + i;
     Q4Frag<64, 1, R> f;
     if (grp < groups) f.issue(m, rows, lane);
-    xq_prep(x, m.in, m.in, NB, xq_lds, XqIdentity{});
+    if (staged) xs.store(m.in, NB, xq_lds, XqIdentity{});
+    else xq_prep(x, m.in, m.in, NB, xq_lds, XqIdentity{});
     XqFrag<NB, 1> xr;
     xr.template read<64>(xq_lds, nch, lane);
     while (grp < groups) {

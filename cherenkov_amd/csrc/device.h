@@ -342,4 +342,77 @@ struct XqIdentity {
     CHK_DEV void operator()(uint32_t, uint32_t, float (&)[8]) const {}
 };
 
+// xq_prep in two steps, for a workgroup that issues its input loads ahead
+// of its weight loads.  Vector loads return in issue order, so inputs
+// issued first can be quantised while the weights are still in flight;
+// issued after them, the quantisation waits for every weight as well.
+// load() reads up to IT * WGS blocks of 8 inputs into registers (fits()
+// says whether the shape is covered; otherwise use xq_prep), store()
+// quantises them into LDS exactly as xq_prep does and ends with a barrier.
+template <int IT, uint32_t WGS>
+struct XqStaged {
+    float v[IT][8];
+
+    CHK_DEV static bool fits(uint32_t K, uint32_t nrows) { return nrows * (K >> 3) <= IT * WGS; }
+
+    // Compiler-only ordering (no instruction is emitted): load() ends with
+    // a memory clobber so the caller's weight loads stay behind the input
+    // loads, and store() starts by redefining the inputs under another, so
+    // the quantisation is not hoisted above those weight loads (which
+    // would make the wave wait for its inputs before issuing them).
+    CHK_DEV void load(const float* __restrict__ x, uint32_t xs, uint32_t K, uint32_t nrows) {
+        const uint32_t nblk = K >> 3, total = nrows * nblk;
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+            if (it * WGS >= total) break;
+            const uint32_t i = it * WGS + threadIdx.x, ii = i < total ? i : total - 1;
+            const uint32_t b = ii / nblk, e = (ii % nblk) * 8;
+            const float4* p4 = reinterpret_cast<const float4*>(x + (size_t)b * xs + e);
+            const float4 v0 = p4[0], v1 = p4[1];
+            v[it][0] = v0.x;
+            v[it][1] = v0.y;
+            v[it][2] = v0.z;
+            v[it][3] = v0.w;
+            v[it][4] = v1.x;
+            v[it][5] = v1.y;
+            v[it][6] = v1.z;
+            v[it][7] = v1.w;
+        }
+        asm volatile("" ::: "memory");
+    }
+
+    template <class F>
+    CHK_DEV void store(uint32_t K, uint32_t nrows, XqChunk* out, F&& xform) {
+        const uint32_t nblk = K >> 3, total = nrows * nblk;
+#pragma unroll
+        for (int it = 0; it < IT; ++it)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) asm volatile("" : "+v"(v[it][j])::"memory");
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+            if (it * WGS >= total) break;
+            const uint32_t i = it * WGS + threadIdx.x;
+            const bool live = i < total;
+            const uint32_t ii = live ? i : total - 1;
+            const uint32_t b = ii / nblk, e = (ii % nblk) * 8;
+            float w[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) w[j] = v[it][j];
+            xform(b, e, w);
+            uint32_t P[XQ_PLANES];
+            float4 prm;
+            xq_quarter(w, P, prm);
+            if (live) {
+                const uint32_t c = ii >> 2, k = ii & 3;
+                uint32_t* dst = reinterpret_cast<uint32_t*>(out + c);
+#pragma unroll
+                for (int p = 0; p < XQ_PLANES; ++p) dst[4 * p + k] = P[p];
+                if (k == 0) out[c].prm = prm;
+            }
+        }
+        __syncthreads();
+    }
+};
+
 }  // namespace chk
