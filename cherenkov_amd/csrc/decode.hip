@@ -834,6 +834,15 @@ __global__ void __launch_bounds__(DN_SCAN_COLS * 4) k_dn_scan(DnScanArgs a) {
             q[j] = qv.x; q[j + 1] = qv.y; q[j + 2] = qv.z; q[j + 3] = qv.w;
             kk[j] = kv.x; kk[j + 1] = kv.y; kk[j + 2] = kv.z; kk[j + 3] = kv.w;
         }
+        // every other input of the row too (the state above for the first):
+        // one round trip, not one per use
+        const float decay = a.decay[b * a.nv + hv], beta = a.beta[b * a.nv + hv];
+        const float v = row[2 * a.qk_dim + hv * a.dv + iv];
+        const size_t jy = (size_t)b * a.nv * a.dv + hv * a.dv + iv;
+        const float zr = a.z[jy];
+        const uint32_t nr = a.norm[iv];
+        asm volatile("" ::: "memory");  // compiler-only: no load sinks below this
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < KPT; ++j) {
             sq += q[j] * q[j];
@@ -847,8 +856,6 @@ __global__ void __launch_bounds__(DN_SCAN_COLS * 4) k_dn_scan(DnScanArgs a) {
             q[j] = q[j] * iq * a.qscale;
             kk[j] *= ik;
         }
-        const float decay = a.decay[b * a.nv + hv], beta = a.beta[b * a.nv + hv];
-        const float v = row[2 * a.qk_dim + hv * a.dv + iv];
         float kvm = 0.0f;
 #pragma unroll
         for (int j = 0; j < KPT; ++j) {
@@ -875,9 +882,8 @@ __global__ void __launch_bounds__(DN_SCAN_COLS * 4) k_dn_scan(DnScanArgs a) {
         // applied by the consumer
         const float ss = wave_sum(p == 0 ? y * y : 0.0f);
         if (p == 0) {
-            const size_t j = (size_t)b * a.nv * a.dv + hv * a.dv + iv;
-            const float yv = y * bf16f(a.norm[iv]) * sigmoidf_(a.z[j]);
-            a.y[j] = yv;
+            const float yv = y * __uint_as_float(nr << 16) * sigmoidf_(zr);
+            a.y[jy] = yv;
             ys[t / TPC] = yv;
         }
         if ((t & 63) == 0) a.ssq[((size_t)b * a.nv + hv) * (a.dv / 16) + blk * (COLS / 16) + (t >> 6)] = ss;
@@ -1057,24 +1063,39 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a) {
     const int lane = threadIdx.x & 63, grp = lane / LPR, lir = lane % LPR;
     const uint32_t slots = a.topk + 1;
     const uint32_t groups = a.H / R, nch = a.I >> 5;
+    const uint32_t li = lane / a.hc, lg = lane % a.hc;
+    const bool owner = li < (uint32_t)R && a.hyper;
     // routing of every row (lane j < topk: slot j's id and weight; lane
-    // topk: the shared expert's gate); act comes quantised from gate/up
+    // topk: the shared expert's gate), loaded raw together with the first
+    // (group, row)'s hyper inputs so that one round trip precedes the
+    // weights; act comes quantised from gate/up
+    // (branch-free clamped loads: a loaded value merged with a default at
+    // a branch join is copied there, which waits for the load)
     uint32_t rid[4];
-    float rw[4];
+    float rw[4], sgv[4];
+    const uint32_t rl = min((uint32_t)lane, a.topk - 1);
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-        rid[b] = 0;
-        rw[b] = 0.0f;
-        if ((uint32_t)b < a.nb) {
-            if ((uint32_t)lane < a.topk) {
-                rid[b] = min(a.ids[b * a.topk + lane], a.X.experts - 1);
-                rw[b] = a.w[b * a.topk + lane];
-            } else if ((uint32_t)lane == a.topk) {
-                rw[b] = sigmoidf_(a.sg[b]);
-            }
-        }
+        const uint32_t bb = min((uint32_t)b, a.nb - 1);
+        rid[b] = a.ids[bb * a.topk + rl];
+        rw[b] = a.w[bb * a.topk + rl];
+        sgv[b] = a.sg[bb];
     }
-    for (uint32_t gi = global_wave(); gi < groups; gi += total_waves()) {
+    const uint32_t gi0 = global_wave();
+    float hy0 = 0.0f, ij0 = 0.0f;
+    if (a.hyper) {
+        hy0 = a.hyper[lg * a.H + min(gi0 * R + min(li, (uint32_t)R - 1), a.H - 1)];
+        ij0 = a.inj[lg];
+    }
+    asm volatile("" ::: "memory");  // compiler-only: the weight loads stay behind these
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        const bool live = (uint32_t)b < a.nb;
+        rid[b] = live && (uint32_t)lane < a.topk ? min(rid[b], a.X.experts - 1) : 0u;
+        rw[b] = !live ? 0.0f : (uint32_t)lane < a.topk ? rw[b] : (uint32_t)lane == a.topk ? sigmoidf_(sgv[b]) : 0.0f;
+    }
+    for (uint32_t gi = gi0; gi < groups; gi += total_waves()) {
         uint32_t rows[R];
 #pragma unroll
         for (int i = 0; i < R; ++i) rows[i] = gi * R + i;
@@ -1088,10 +1109,8 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a) {
                     my_w = rw[k];
                 }
             // hyper of this wave's rows, for the inject below
-            const uint32_t li = lane / a.hc, lg = lane % a.hc;
-            const bool owner = li < (uint32_t)R && a.hyper;
-            float hy = 0.0f, ij = 0.0f;
-            if (owner) {
+            float hy = hy0, ij = ij0;
+            if (owner && (gi != gi0 || b != 0)) {
                 hy = a.hyper[(size_t)b * a.H * a.hc + lg * a.H + rows[0] + li];
                 ij = a.inj[b * a.hc + lg];
             }
@@ -1149,6 +1168,7 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a) {
                 if (li == (uint32_t)i) mine = v;
                 if (a.raw_out && lane == i) a.raw_out[(size_t)b * a.H + rows[i]] = v;
             }
+            asm volatile("" : "+v"(hy), "+v"(ij));  // compiler-only: not consumed earlier
             if (owner) a.hyper[(size_t)b * a.H * a.hc + lg * a.H + rows[0] + li] = hy + mine * ij;
         }
     }
