@@ -307,11 +307,22 @@ __global__ void __launch_bounds__(256) k_attn_part(AttnArgs a) {
     const KvDev& kv = a.kv[a.one_kv ? 0 : b];
     const uint32_t kv_row = a.nkv * HD, n = min((uint32_t)CH, T - t0);
 
-    // ---- issue: K quarter-rows, V u32 lanes, their fp16 scales
+    // ---- issue: q of the G heads first (written by the previous kernel;
+    // loads return in issue order, so behind the cache rows its LDS
+    // staging would wait for all of them), then K quarter-rows, V u32
+    // lanes and their fp16 scales (raw, one per 32-bit register)
+    constexpr uint32_t QI = (G * HD + 255) / 256;
+    float qreg[QI];
+#pragma unroll
+    for (uint32_t j = 0; j < QI; ++j) {
+        const uint32_t i = min(t + 256 * j, (uint32_t)(G * HD) - 1);
+        qreg[j] = a.q_ready[((size_t)b * a.nh + h0 + i / HD) * HD + i % HD];
+    }
+    asm volatile("" ::: "memory");  // compiler-only: the cache loads stay behind q
     const uint32_t tk = t >> 2, qq = t & 3;
     const uint32_t ktok = t0 + min(tk, n - 1);
     uint4 kw[KB][2];
-    uint16_t ksc[KB];
+    uint32_t ksc[KB];
 #pragma unroll
     for (int k = 0; k < KB; ++k) {
         const uint32_t d0 = qq * DPT + k * 32;
@@ -322,7 +333,7 @@ __global__ void __launch_bounds__(256) k_attn_part(AttnArgs a) {
     }
     const uint32_t slot = t / LPV, vl = t % LPV;
     uint32_t vw[TPS];
-    uint16_t vsc[TPS];
+    uint32_t vsc[TPS];
 #pragma unroll
     for (int i = 0; i < TPS; ++i) {
         const uint32_t vt = t0 + min(slot + (uint32_t)(i * NS), n - 1);
@@ -330,9 +341,16 @@ __global__ void __launch_bounds__(256) k_attn_part(AttnArgs a) {
         vsc[i] = kv.vs[(size_t)vt * (kv_row / 32) + (hk * HD + vl * 4) / 32];
     }
     // q of the G heads into LDS
-    for (uint32_t i = t; i < (uint32_t)(G * HD); i += 256) {
-        const uint32_t g = i / HD, d = i % HD;
-        sq[g][(d / DPT) * (DPT + 4) + d % DPT] = a.q_ready[((size_t)b * a.nh + h0 + g) * HD + d];
+#pragma unroll
+    for (uint32_t j = 0; j < QI; ++j) asm volatile("" : "+v"(qreg[j])::"memory");
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (uint32_t j = 0; j < QI; ++j) {
+        const uint32_t i = t + 256 * j;
+        if (i < (uint32_t)(G * HD)) {
+            const uint32_t g = i / HD, d = i % HD;
+            sq[g][(d / DPT) * (DPT + 4) + d % DPT] = qreg[j];
+        }
     }
     __syncthreads();
 
