@@ -17,19 +17,25 @@ namespace chk {
 // to q/k heads and to the indexer's query heads.
 CHK_DEV float norm_rope(float x, bool live, uint32_t d, uint32_t n, const uint16_t* w, float eps, uint32_t rot,
                         float theta, uint32_t pos, float* red, float* sx) {
+    // the norm weight (raw bf16 in a 32-bit register) and the rotation
+    // are fetched and computed ahead of the reduction, not after it
+    const uint32_t wv = w[min(d, n - 1)];
+    const uint32_t half = rot / 2, j = d < half ? d : d - half;
+    float sn = 0.0f, cs = 1.0f;
+    if (d < rot) {
+        const float inv_freq = powf(theta, -(2.0f * (float)j) / (float)rot);
+        const float ang = (float)pos * inv_freq;
+        sn = sinf(ang);
+        cs = cosf(ang);
+    }
     const float ss = block_sum(live ? x * x : 0.0f, red);
     const float inv = 1.0f / sqrtf(ss / (float)n + eps);
     if (live) {
-        x = x * inv * bf16f(w[d]);
+        x = x * inv * __uint_as_float(wv << 16);
         sx[d] = x;
     }
     __syncthreads();
-    const uint32_t half = rot / 2;
     if (d < rot) {
-        const uint32_t j = d < half ? d : d - half;
-        const float inv_freq = powf(theta, -(2.0f * (float)j) / (float)rot);
-        const float ang = (float)pos * inv_freq;
-        const float sn = sinf(ang), cs = cosf(ang);
         const float av = sx[j], bv = sx[j + half];
         x = d < half ? av * cs - bv * sn : bv * cs + av * sn;
     }
@@ -459,23 +465,44 @@ __global__ void __launch_bounds__(256) k_attn_combine(AttnArgs a) {
                    t = threadIdx.x;
     const uint32_t T = a.pos[b] + 1, nc = (T + ATTN_CHUNK - 1) / ATTN_CHUNK;
     const float* part = a.part + ((size_t)b * a.nh + h) * a.max_chunks * (hd + 2);
-    float m = -INFINITY;
-    for (uint32_t c = t; c < nc; c += CHK_WG) m = fmaxf(m, part[(size_t)c * (hd + 2)]);
+    const uint32_t per = hd / COMBINE_SPLIT;  // dims of this workgroup (<= 64)
+    const uint32_t dl = t & 63, cg = t >> 6;
+    const uint32_t d = ds * per + dl;
+    const float* pd = part + 2 + d;
+    // The first chunk's (max, sum) of this thread, the first 32 chunks'
+    // partial outputs of its dimension and the gate load together, ahead
+    // of any use (branch-free, clamped): one round trip instead of one
+    // per pass.  Longer contexts continue in the loops below.
+    const uint32_t tc = min(t, nc - 1), dc = min(d, hd - 1);
+    const float m0 = part[(size_t)tc * (hd + 2)], l0 = part[(size_t)tc * (hd + 2) + 1];
+    float v0[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v0[k] = part[2 + dc + (size_t)min(cg + 4 * k, nc - 1) * (hd + 2)];
+    const float gate = a.q_raw[(size_t)b * a.nh * 2 * hd + h * 2 * hd + hd + dc];
+    asm volatile("" ::: "memory");  // compiler-only: later loads stay behind these
+    float m = t < nc ? m0 : -INFINITY;
+    for (uint32_t c = t + CHK_WG; c < nc; c += CHK_WG) m = fmaxf(m, part[(size_t)c * (hd + 2)]);
     const float M = block_max(m, red);
     float l = 0.0f;
-    for (uint32_t c = t; c < nc; c += CHK_WG) {
+    if (t < nc) {
+        const float w = expf(m0 - M);
+        sw[t] = w;
+        l += l0 * w;
+    }
+    for (uint32_t c = t + CHK_WG; c < nc; c += CHK_WG) {
         const float w = expf(part[(size_t)c * (hd + 2)] - M);
         sw[c] = w;
         l += part[(size_t)c * (hd + 2) + 1] * w;
     }
     const float L = block_sum(l, red);  // its barriers also publish sw
-    const uint32_t per = hd / COMBINE_SPLIT;  // dims of this workgroup (<= 64)
-    const uint32_t dl = t & 63, cg = t >> 6;
-    const uint32_t d = ds * per + dl;
     float o = 0.0f;
     if (dl < per) {
-        const float* pd = part + 2 + d;
         uint32_t c = cg;
+        if (c + 28 < nc) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) o += v0[k] * sw[c + 4 * k];
+            c += 32;
+        }
         for (; c + 28 < nc; c += 32) {
             float v[8];
 #pragma unroll
@@ -489,7 +516,6 @@ __global__ void __launch_bounds__(256) k_attn_combine(AttnArgs a) {
     __syncthreads();
     if (cg == 0 && dl < per) {
         const float ot = (acc_s[0][dl] + acc_s[1][dl]) + (acc_s[2][dl] + acc_s[3][dl]);
-        const float gate = a.q_raw[(size_t)b * a.nh * 2 * hd + h * 2 * hd + hd + d];
         a.out[(size_t)b * a.nh * hd + h * hd + d] = ot / L * sigmoidf_(gate);
     }
 }
