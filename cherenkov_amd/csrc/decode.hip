@@ -730,26 +730,54 @@ __global__ void __launch_bounds__(256) k_qmv_inject(InjArgs a) {
                 ij[b] = a.inj[b * a.hc + lg];
             }
         asm volatile("" ::: "memory");  // compiler-only: x and the weights stay behind
+        // the scan's chunks and the first SQ float4 of their heads' sums of
+        // squares load ahead of the weights too (branch-free), so neither
+        // waits behind them
+        constexpr uint32_t SQ = 2;
+        XqChunk q0[NB][CPL];
+        float4 sq0[NB][CPL][SQ];
+        const bool chunks = XM == XM_DN_GATED && a.x_xq;
         if constexpr (FIRST) {
             if (staged) xs.load(a.x, a.xs, m.in, NB);
-        }
-        Q4Frag<64, CPL, R> f;
-        f.issue(m, rows, lane);  // dead waves load clamped rows, unused
-        if constexpr (FIRST) {
-            if (XM == XM_DN_GATED && a.x_xq) {
-                // the scan's chunks of y w sigmoid(z), scaled by their head's
-                // 1/rms: a common factor of m, d and the chunk sum
+            if (chunks) {
+                const uint32_t nq = a.ssq_blocks / 4;
 #pragma unroll
                 for (int c = 0; c < CPL; ++c) {
                     const uint32_t cc = min(lane + 64u * c, nch - 1);
                     const uint32_t head = cc * 32 / a.dv;
 #pragma unroll
                     for (int b = 0; b < NB; ++b) {
-                        XqChunk q = a.x_xq[(size_t)b * nch + cc];
+                        q0[b][c] = a.x_xq[(size_t)b * nch + cc];
+                        const float4* sp =
+                            reinterpret_cast<const float4*>(a.ssq + ((size_t)b * a.nheads + head) * a.ssq_blocks);
+#pragma unroll
+                        for (uint32_t k = 0; k < SQ; ++k) sq0[b][c][k] = sp[min(k, nq - 1)];
+                    }
+                }
+            }
+            asm volatile("" ::: "memory");  // compiler-only: the weights stay behind these
+        }
+        Q4Frag<64, CPL, R> f;
+        f.issue(m, rows, lane);  // dead waves load clamped rows, unused
+        if constexpr (FIRST) {
+            if (chunks) {
+                // the scan's chunks of y w sigmoid(z), scaled by their head's
+                // 1/rms: a common factor of m, d and the chunk sum
+                const uint32_t nq = a.ssq_blocks / 4;
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) {
+                    const uint32_t cc = min(lane + 64u * c, nch - 1);
+                    const uint32_t head = cc * 32 / a.dv;
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) {
+                        XqChunk q = q0[b][c];
                         const float4* sp =
                             reinterpret_cast<const float4*>(a.ssq + ((size_t)b * a.nheads + head) * a.ssq_blocks);
                         float ss = 0.0f;
-                        for (uint32_t k = 0; k < a.ssq_blocks / 4; ++k) {
+#pragma unroll
+                        for (uint32_t k = 0; k < SQ; ++k)
+                            if (k < nq) ss += (sq0[b][c][k].x + sq0[b][c][k].y) + (sq0[b][c][k].z + sq0[b][c][k].w);
+                        for (uint32_t k = SQ; k < nq; ++k) {
                             const float4 v = sp[k];
                             ss += (v.x + v.y) + (v.z + v.w);
                         }
