@@ -120,7 +120,7 @@ def spec_decode(prompt: list[int], tokens: int, drafts: int = 2) -> dict:
         "verify_steps": steps,
         "accepted_drafts": acc,
         "acceptance": round(acc / max(steps * drafts, 1), 4),
-        "prefill_path": "4-row steps (the GEMM prefill does not cover the MTP head)",
+        "prefill_path": "MFMA Q4 GEMM chunk with the MTP head over every prompt row",
         "prefill_s": round(pf_s, 3),
     }
 

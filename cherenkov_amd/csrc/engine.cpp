@@ -134,6 +134,10 @@ struct PfBufs {
     float *logits, *sg, *wts;
     uint32_t *ids, *list, *count, *tiles, *ntiles;
     float *act, *yd;
+    // MTP head over a chunk: the tokens after each row, rms_norm_shift(e),
+    // the normed trunk streams, fc_e / fc_h outputs and the head's residual
+    uint32_t* mtp_tok;
+    float *mtp_en, *mtp_hn, *mtp_fe, *mtp_fh, *mtp_hyper;
 };
 
 }  // namespace chk
@@ -904,7 +908,8 @@ struct ChkEngine {
     void pf_alloc();
     void pf_hc_read(const HcDev& w, float* inj, uint32_t T, bool for_moe);
     void pf_deltanet(const LayerDev& L, uint32_t T);
-    void pf_attention(const LayerDev& L, uint32_t T, uint32_t pos0);
+    void pf_attention(const LayerDev& L, uint32_t T, uint32_t pos0, const KvDev* kvo = nullptr);
+    void pf_mtp(const uint32_t* toks, uint32_t n, uint32_t c0, uint32_t T, uint32_t pos0, bool last);
     void pf_moe(const LayerDev& L, uint32_t T);
     void prefill_gemm(const uint32_t* toks, uint32_t n, uint32_t* next);
     void mtp_draft(const uint32_t* next, uint32_t n, uint32_t chain, uint32_t* drafts, uint32_t* nd);
@@ -1027,6 +1032,7 @@ void ChkEngine::prefill(const uint32_t* toks, uint32_t n, uint32_t* next, uint32
     if (pf_supported()) {
         prefill_gemm(toks, n, next);
         *draft = 0xffffffffu;
+        if (has_mtp) HIPCHK(hipMemcpy(draft, s.mtp_out, 4, hipMemcpyDeviceToHost));
         return;
     }
     prefill_rows(toks, n, next, draft);
@@ -1071,7 +1077,7 @@ void ChkEngine::prefill_rows(const uint32_t* toks, uint32_t n, uint32_t* next, u
 constexpr uint32_t PF_MAX_ROWS = 4096;                  // rows per chunk (gpu/prefill.rs:116)
 
 bool ChkEngine::pf_supported() const {
-    return (o.experts == 4 || o.experts == 3 || o.experts == 2) && !has_mtp && !D.qsa && D.lowrank % 64 == 0 && D.H % 64 == 0 && D.H <= 4096 && D.hc <= 4 &&
+    return (o.experts == 4 || o.experts == 3 || o.experts == 2) && !D.qsa && D.lowrank % 64 == 0 && D.H % 64 == 0 && D.H <= 4096 && D.hc <= 4 &&
            (D.dv == 64 || D.dv == 128 || D.dv == 256) && D.I % 64 == 0 && (D.nh * D.hd) % 64 == 0 &&
            D.v_dim % 64 == 0 && D.E + 1 <= 513 && D.nh % D.nkv == 0 &&
            (D.nh / D.nkv == 1 || D.nh / D.nkv == 2 || D.nh / D.nkv == 4 || D.nh / D.nkv == 8) &&
@@ -1085,6 +1091,14 @@ void ChkEngine::pf_alloc() {
     pf.tokens = dalloc<uint32_t>(C);
     pf.pos = dalloc<uint32_t>(C);
     pf.hyper = dalloc<float>(C * D.hh);
+    if (has_mtp) {
+        pf.mtp_tok = dalloc<uint32_t>(C);
+        pf.mtp_en = dalloc<float>(C * D.H);
+        pf.mtp_hn = dalloc<float>(C * D.hh);
+        pf.mtp_fe = dalloc<float>(C * D.H);
+        pf.mtp_fh = dalloc<float>(C * D.hh);
+        pf.mtp_hyper = dalloc<float>(C * D.hh);
+    }
     const uint64_t plane = std::max({C * D.hh, C * D.v_dim, C * D.nh * D.hd, C * slots * D.I, C * D.H});
     pf.hi = dalloc<uint4>(plane / 8);
     pf.lo = dalloc<uint4>(plane / 8);
@@ -1264,7 +1278,8 @@ void ChkEngine::pf_deltanet(const LayerDev& L, uint32_t T) {
 // per-row prep writing the chunk's q8 K/V and index keys at their
 // positions, causal attention of every row over the cache (sub-batches of
 // rows sized to the partials buffer), o-projection + inject.
-void ChkEngine::pf_attention(const LayerDev& L, uint32_t T, uint32_t pos0) {
+void ChkEngine::pf_attention(const LayerDev& L, uint32_t T, uint32_t pos0, const KvDev* kvo) {
+    const KvDev& kvl = kvo ? *kvo : kv[L.at_idx];
     const uint32_t mt = (T + 63) / 64;
     PfGemmArgs g{};
     g.seg[0] = PfSeg{L.at.q, pf.q_raw, 2 * D.nh * D.hd, 0, PA_NONE};
@@ -1287,7 +1302,7 @@ void ChkEngine::pf_attention(const LayerDev& L, uint32_t T, uint32_t pos0) {
     aa.q_norm = L.at.q_norm;
     aa.k_norm = L.at.k_norm;
     aa.q_ready = pf.q_ready;
-    aa.kv[0] = kv[L.at_idx];
+    aa.kv[0] = kvl;
     aa.one_kv = 1;
     aa.pos = pf.pos;
     aa.out = pf.attn_out;
@@ -1302,7 +1317,7 @@ void ChkEngine::pf_attention(const LayerDev& L, uint32_t T, uint32_t pos0) {
     aa.scale = D.attn_scale;
     aa.max_chunks = (pos0 + T - 1) / ATTN_CHUNK + 1;
     launch_attn_prep(aa, (int)T, st);
-    launch_pf_flash(pf.q_ready, pf.q_raw, kv[L.at_idx], pf.attn_out, T, pos0, D.nh, D.nkv, D.hd, D.attn_scale, st);
+    launch_pf_flash(pf.q_ready, pf.q_raw, kvl, pf.attn_out, T, pos0, D.nh, D.nkv, D.hd, D.attn_scale, st);
     launch_pf_xprep(pf.attn_out, D.nh * D.hd, T, D.nh * D.hd, pf.hi, pf.lo, pf.xs, st);
     PfGemmArgs o2{};
     o2.seg[0].m = L.at.o;
@@ -1386,11 +1401,13 @@ void ChkEngine::prefill_gemm(const uint32_t* toks, uint32_t n, uint32_t* next) {
             pf_hc_read(L.mlp_hc, pf.inj_m, T, true);
             pf_moe(L, T);
         }
-        if (c0 + T >= n) {
+        const bool last = c0 + T >= n;
+        if (last) {
             // final mixer and LM head on the chunk's last row (prefill.rs:308-334)
             hc_read(final_mixer, pf.hyper + (uint64_t)(T - 1) * D.hh, nullptr, 1);
             launch_lm_head(lm_head, s.mixed, s.logits, s.pv, s.pi, lm_parts, s.d_out, 1, st);
         }
+        if (has_mtp) pf_mtp(toks, n, c0, T, pos0, last);
         HIPCHK(hipStreamSynchronize(st));
         HIPCHK(hipGetLastError());
         tokens.insert(tokens.end(), toks + c0, toks + c0 + T);
@@ -1402,6 +1419,50 @@ void ChkEngine::prefill_gemm(const uint32_t* toks, uint32_t n, uint32_t* next) {
     batch_snap = false;
     logits_fresh = false;
     mtp_logits_fresh = false;
+    if (has_mtp) {
+        mtp_len = pos;
+        last_mtp_rows = 1;
+    }
+}
+
+// The MTP head over a prefill chunk (gpu/prefill.rs:335-446): row r pairs
+// the trunk residual at pos0 + r with the token after it (the next prompt
+// token; on the last row of the final chunk the trunk's greedy token),
+// fc_e / fc_h as GEMMs over the chunk, the MTP layer through the prefill
+// layer path on its own residual and KV cache, the last row's residual
+// kept where chained drafts re-enter, and on the final chunk the MTP mixer
+// and LM head on that row (the draft).
+void ChkEngine::pf_mtp(const uint32_t* toks, uint32_t n, uint32_t c0, uint32_t T, uint32_t pos0, bool last) {
+    if (T > 1) HIPCHK(hipMemcpyAsync(pf.mtp_tok, toks + c0 + 1, (T - 1) * 4, hipMemcpyHostToDevice, st));
+    if (last) HIPCHK(hipMemcpyAsync(pf.mtp_tok + T - 1, s.d_out, 4, hipMemcpyDeviceToDevice, st));
+    else HIPCHK(hipMemcpyAsync(pf.mtp_tok + T - 1, toks + c0 + T, 4, hipMemcpyHostToDevice, st));
+    (void)n;
+    launch_mtp_prelude(pf.mtp_tok, embed, mtp_enorm, mtp_hnorm, pf.hyper, pf.mtp_en, pf.mtp_hn, D.H, D.hc, D.eps,
+                       (int)T, st);
+    launch_pf_xprep(pf.mtp_en, D.H, T, D.H, pf.hi, pf.lo, pf.xs, st);
+    launch_pf_gemm(fc_e, pf.hi, pf.lo, pf.xs, pf.mtp_fe, T, D.H, st);
+    launch_pf_xprep(pf.mtp_hn, D.H, T * D.hc, D.H, pf.hi, pf.lo, pf.xs, st);
+    launch_pf_gemm(fc_h, pf.hi, pf.lo, pf.xs, pf.mtp_fh, T * D.hc, D.H, st);
+    launch_mtp_fold(pf.mtp_fe, pf.mtp_fh, pf.mtp_hyper, D.H, D.hc, (int)T, st);
+    float* trunk = pf.hyper;
+    pf.hyper = pf.mtp_hyper;
+    try {
+        const LayerDev& L = mtp_layer;
+        pf_hc_read(L.attn_hc, pf.inj_a, T, false);
+        pf_attention(L, T, pos0, &mtp_kv);
+        pf_hc_read(L.mlp_hc, pf.inj_m, T, true);
+        pf_moe(L, T);
+    } catch (...) {
+        pf.hyper = trunk;
+        throw;
+    }
+    pf.hyper = trunk;
+    const float* tail = pf.mtp_hyper + (uint64_t)(T - 1) * D.hh;
+    HIPCHK(hipMemcpyAsync(s.mtp_hyper, tail, D.hh * 4, hipMemcpyDeviceToDevice, st));
+    if (last) {
+        hc_read(mtp_mixer, tail, nullptr, 1);
+        launch_lm_head(lm_head, s.mixed, s.mtp_logits, s.pv, s.pi, lm_parts, s.mtp_out, 1, st);
+    }
 }
 
 // ===================================================================== C ABI

@@ -162,6 +162,46 @@ def test_gemm_prefill_matches_oracle(have_gpu):
         assert nxt == int(np.argmax(ref))
 
 
+@pytest.mark.parametrize("splits", [[40], [25, 15]])
+def test_gemm_prefill_mtp_head_matches_oracle(have_gpu, splits):
+    """MTP engines take the GEMM prefill too (gpu/prefill.rs:335-446): each
+    prompt row's MTP pass pairs the trunk residual with the token after it
+    (across chunk boundaries, and the trunk's greedy token after the last
+    row).  The last row's MTP logits and the draft match the oracle run
+    token by token (forward_token, then mtp_forward over the same pairs),
+    and the trunk's last-row logits as well."""
+    cfg = presets.tiny(mtp=1)
+    rng = np.random.default_rng(500 + len(splits))
+    prompt = rng.integers(0, cfg.vocab_size, size=sum(splits)).tolist()
+    eng = Engine(cfg, experts=4, drafts=2, max_t=128)
+    try:
+        i = 0
+        for k in splits:
+            nxt, dr = eng.prefill_chunk(prompt[i:i + k])
+            i += k
+        got_trunk = eng.logits_row(0)
+        got_mtp = eng.mtp_logits_row(0)
+    finally:
+        eng.close()
+    st = OracleModel(cfg).new_state()
+    ref = None
+    for t in prompt:
+        ref = st.forward_token(t, True)
+    assert_close(got_trunk, ref, "prefill trunk vs oracle")
+    if argmax_margin(ref) > 1e-3:
+        assert nxt == int(np.argmax(ref))
+    st2 = OracleModel(cfg).new_state()
+    mref = None
+    for p, t in enumerate(prompt):
+        st2.forward_token(t, True)
+        after = prompt[p + 1] if p + 1 < len(prompt) else nxt
+        mref, _ = st2.mtp_forward(after, st2.last_hyper(), p)
+    assert_close(got_mtp, mref, "prefill MTP head vs oracle")
+    assert dr is not None
+    if argmax_margin(mref) > 1e-3:
+        assert dr == int(np.argmax(mref))
+
+
 @pytest.mark.parametrize("bits", [4, 3, 2])
 def test_gemm_prefill_full_width(have_gpu, bits):
     """Config 5 widths (hidden 2048, 512 experts top-10, 16/32 DeltaNet
