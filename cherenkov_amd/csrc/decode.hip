@@ -1110,6 +1110,13 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a) {
         sgv[b] = a.sg[bb];
     }
     const uint32_t gi0 = global_wave();
+    // the first row's activation chunks do not depend on the routing either
+    XqFrag<1, 1> xq0[PASSES];
+#pragma unroll
+    for (int pass = 0; pass < PASSES; ++pass) {
+        const uint32_t slot = grp + pass * G, sl = slot < slots ? slot : slots - 1;
+        xq0[pass].template read<LPR>(a.act_xq + (size_t)sl * nch, nch, lir);
+    }
     float hy0 = 0.0f, ij0 = 0.0f;
     if (a.hyper) {
         hy0 = a.hyper[lg * a.H + min(gi0 * R + min(li, (uint32_t)R - 1), a.H - 1)];
@@ -1168,7 +1175,8 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a) {
                 } else {
                     fq[pass].issue(a.sh_down, rows, lir);
                 }
-                xq[pass].template read<LPR>(a.act_xq + ((size_t)b * slots + sl) * nch, nch, lir);
+                if (gi == gi0 && b == 0) xq[pass] = xq0[pass];
+                else xq[pass].template read<LPR>(a.act_xq + ((size_t)b * slots + sl) * nch, nch, lir);
             }
             float tot[R];
 #pragma unroll
