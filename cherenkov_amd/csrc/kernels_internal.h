@@ -137,12 +137,16 @@ CHK_DEV float wave_sum_dpp(float v) {
 // Wave64 max of ints through DPP (the lanes outside a row mask keep their
 // own value); valid in every lane.
 CHK_DEV int wave_max_i32(int v) {
-    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0xb1, 0xf, 0xf, false));   // quad_perm [1,0,3,2]
-    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x4e, 0xf, 0xf, false));   // quad_perm [2,3,0,1]
-    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x124, 0xf, 0xf, false));  // row_ror:4
-    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x128, 0xf, 0xf, false));  // row_ror:8
-    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x142, 0xa, 0xf, false));  // row_bcast:15 into rows 1, 3
-    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x143, 0xc, 0xf, false));  // row_bcast:31 into rows 2, 3
+    // the moved value defaults to INT_MIN (max's identity) where a row mask
+    // excludes a lane, so the compiler can fold each move into its v_max
+    // as a DPP operand (one instruction per step instead of two)
+    constexpr int LO = -2147483647 - 1;
+    v = max(v, __builtin_amdgcn_update_dpp(LO, v, 0xb1, 0xf, 0xf, false));   // quad_perm [1,0,3,2]
+    v = max(v, __builtin_amdgcn_update_dpp(LO, v, 0x4e, 0xf, 0xf, false));   // quad_perm [2,3,0,1]
+    v = max(v, __builtin_amdgcn_update_dpp(LO, v, 0x124, 0xf, 0xf, false));  // row_ror:4
+    v = max(v, __builtin_amdgcn_update_dpp(LO, v, 0x128, 0xf, 0xf, false));  // row_ror:8
+    v = max(v, __builtin_amdgcn_update_dpp(LO, v, 0x142, 0xa, 0xf, false));  // row_bcast:15 into rows 1, 3
+    v = max(v, __builtin_amdgcn_update_dpp(LO, v, 0x143, 0xc, 0xf, false));  // row_bcast:31 into rows 2, 3
     return __builtin_amdgcn_readlane(v, 63);
 }
 
