@@ -14,6 +14,7 @@ from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
 LIB_PATH = PKG / "libcherenkov.so"
+NO_TOKEN = 0xFFFFFFFF  # CHK_NO_TOKEN: an absent optional token
 
 u32, u64, f32, f64, i32 = C.c_uint32, C.c_uint64, C.c_float, C.c_double, C.c_int
 P = C.c_void_p
@@ -94,8 +95,13 @@ SIGNATURES = [
     ("chk_reset", i32, [P]),
     ("chk_mtp_draft", i32, [P, C.POINTER(u32), u32, u32, C.POINTER(u32), C.POINTER(u32)]),
     ("chk_mtp_chain", i32, [P, u32, C.POINTER(u32)]),
-    ("chk_prefill_chunk", i32, [P, C.POINTER(u32), u32, C.POINTER(u32), C.POINTER(u32)]),
+    ("chk_prefill_chunk", i32, [P, C.POINTER(u32), u32, u32, i32, C.POINTER(u32), C.POINTER(u32)]),
+    ("chk_prefill_release", None, [P]),
+    ("chk_prefill_rows_fit", i32, [P, i32, C.POINTER(u32)]),
+    ("chk_pf_logits_row", C.POINTER(f32), [P, u32]),
     ("chk_logits_row", C.POINTER(f32), [P, u32]),
+    ("chk_logits", C.POINTER(f32), [P]),
+    ("chk_last_logits_row", u32, [P]),
     ("chk_mtp_logits_row", C.POINTER(f32), [P, u32]),
     ("chk_pos", u32, [P]),
     ("chk_eos_token", u32, [P]),
@@ -103,12 +109,34 @@ SIGNATURES = [
     ("chk_trunk_rows", u32, [P]),
     ("chk_has_mtp", i32, [P]),
     ("chk_memory_stats", i32, [P, C.POINTER(ChkMemoryStats)]),
+    ("chk_allocated_gb", f64, [P]),
+    ("chk_kv_cache_bytes", u64, [P]),
+    ("chk_kv_cache_capacity", u64, [P]),
+    ("chk_kv_cache_fullness", f64, [P]),
+    ("chk_context_fullness", f64, [P]),
+    ("chk_reset_request", i32, [P]),
+    ("chk_clear_profile", i32, [P]),
+    ("chk_prefix_state_bytes", u64, [P]),
+    ("chk_state_bytes_at", u64, [P, u32, u32]),
+    ("chk_save_prefix", i32, [P, C.POINTER(P)]),
+    ("chk_save_into", i32, [P, C.POINTER(P)]),
+    ("chk_restore_prefix", i32, [P, P]),
+    ("chk_prefix_free", None, [P]),
+    ("chk_prefix_pos", u32, [P]),
+    ("chk_prefix_mtp_len", u32, [P]),
+    ("chk_prefix_tokens", u32, [P, C.POINTER(u32), u32]),
     ("chk_pool_slots", u32, [P]),
+    ("chk_pool_budget", u32, [P]),
     ("chk_pool_resident", u32, [P]),
     ("chk_pool_is_member", i32, [P, u32]),
-    ("chk_pool_acquire", u32, [P, C.POINTER(u32), u32, C.POINTER(u32)]),
+    ("chk_pool_acquire", i32, [P, C.POINTER(u32), u32, u64, C.POINTER(u32), C.POINTER(u32)]),
+    ("chk_pool_plan_reads", i32, [P, C.POINTER(u32), u32, C.POINTER(u32), C.POINTER(u32)]),
+    ("chk_pool_finish", i32, [P, C.POINTER(u32), u32]),
     ("chk_pool_addr", u64, [P, u32]),
+    ("chk_pool_buf", i32, [P, u32, C.POINTER(P), C.POINTER(u64)]),
     ("chk_pool_kind", u32, [P, u32]),
+    ("chk_pool_set_kind", i32, [P, u32, u32]),
+    ("chk_pool_store", i32, [P, u32, C.POINTER(P), C.POINTER(u64)]),
     ("chk_pool_bytes", u64, [P]),
     ("chk_last_routes", i32, [P, u32, u32, C.POINTER(u32), C.POINTER(f32)]),
     ("chk_last_probs", i32, [P, u32, u32, P]),
@@ -133,6 +161,9 @@ SIGNATURES = [
     ("chk_layer_hyper", i32, [P, u32, u32, P]),
     ("chk_profile_kernel", i32, [P, i32]),
     ("chk_profile_read", i32, [P, C.POINTER(f64), C.POINTER(u64), C.POINTER(u64)]),
+    ("chk_prefix_regions", i32, [P, u32, u32, C.POINTER(u64), C.POINTER(u64), u32, C.POINTER(u32)]),
+    ("chk_prefix_read", i32, [P, u32, P, u64]),
+    ("chk_fill_u8", i32, [P, u32, u64, P]),
     ("chk_copy_f32", i32, [P, P, u64, P]),
     ("chk_profile_graph", i32, [P, i32, u32, C.POINTER(C.c_double), C.POINTER(u64), C.POINTER(u64)]),
     ("chk_time_decode", i32, [P, u32, u32, C.POINTER(f32), C.POINTER(u32)]),

@@ -530,6 +530,11 @@ __global__ void __launch_bounds__(256) k_zero_f32(float* __restrict__ dst, uint6
     for (uint64_t i = (uint64_t)blockIdx.x * CHK_WG + threadIdx.x; i < n; i += stride) dst[i] = 0.0f;
 }
 
+__global__ void __launch_bounds__(256) k_fill_u8(uint8_t* __restrict__ dst, uint8_t v, uint64_t n) {
+    uint64_t stride = (uint64_t)gridDim.x * CHK_WG;
+    for (uint64_t i = (uint64_t)blockIdx.x * CHK_WG + threadIdx.x; i < n; i += stride) dst[i] = v;
+}
+
 // Positions come from device memory and the chunk grid covers the whole
 // context capacity (chunks past a row's length exit at once), so the
 // launch is the same every step and can live in a captured graph.
@@ -602,6 +607,11 @@ void launch_copy_f32(float* dst, const float* src, uint64_t n, hipStream_t st) {
 void launch_zero_f32(float* dst, uint64_t n, hipStream_t st) {
     uint32_t grid = (uint32_t)std::min<uint64_t>((n + 255) / 256, 2048);
     if (n) k_zero_f32<<<grid, 256, 0, st>>>(dst, n);
+}
+
+void launch_fill_u8(uint8_t* dst, uint8_t v, uint64_t n, hipStream_t st) {
+    uint32_t grid = (uint32_t)std::min<uint64_t>((n + 255) / 256, 2048);
+    if (n) k_fill_u8<<<grid, 256, 0, st>>>(dst, v, n);
 }
 
 }  // namespace chk

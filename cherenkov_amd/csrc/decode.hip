@@ -935,38 +935,53 @@ __global__ void __launch_bounds__(256) k_router(RouterArgs a) {
     const uint32_t H = a.H, nch = H >> 5, rows_total = a.E + 1;
     const uint32_t groups = (rows_total + R - 1) / R;
     for (uint32_t grp = global_wave(); grp < groups; grp += total_waves()) {
-        uint4 wq[R][4];
-        const uint32_t ch = lane;
+        float acc[R][NB];
 #pragma unroll
-        for (int i = 0; i < R; ++i) {
-            uint32_t row = grp * R + i;
-            if (row > a.E) row = a.E;
-            const uint16_t* wr = row < a.E ? a.router + (size_t)row * H : a.shared_gate;
+        for (int i = 0; i < R; ++i)
 #pragma unroll
-            for (int k = 0; k < 4; ++k)
-                wq[i][k] = ch < nch ? ldw4(reinterpret_cast<const uint32_t*>(wr + ch * 32) + 4 * k) : make_uint4(0, 0, 0, 0);
+            for (int b = 0; b < NB; ++b) acc[i][b] = 0.0f;
+        // lane l takes input chunk c0 + l (32 inputs) of each pass; one pass
+        // covers 2048 inputs
+        for (uint32_t c0 = 0; c0 < nch; c0 += 64) {
+            uint4 wq[R][4];
+            const uint32_t ch = c0 + lane;
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                uint32_t row = grp * R + i;
+                if (row > a.E) row = a.E;
+                const uint16_t* wr = row < a.E ? a.router + (size_t)row * H : a.shared_gate;
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    wq[i][k] = ch < nch ? ldw4(reinterpret_cast<const uint32_t*>(wr + ch * 32) + 4 * k)
+                                        : make_uint4(0, 0, 0, 0);
+            }
+            XFrag<NB, 1> xr;
+            xr.template load<64>(a.x + (size_t)c0 * 32, H, nch - c0, lane);
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const uint32_t uu[4] = {wq[i][k].x, wq[i][k].y, wq[i][k].z, wq[i][k].w};
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            acc[i][b] += __uint_as_float(uu[j] << 16) * xr.v[b][0][k * 8 + 2 * j];
+                            acc[i][b] += __uint_as_float(uu[j] & 0xffff0000u) * xr.v[b][0][k * 8 + 2 * j + 1];
+                        }
+                    }
+                }
+            }
         }
-        XFrag<NB, 1> xr;
-        xr.template load<64>(a.x, H, nch, lane);
 #pragma unroll
         for (int i = 0; i < R; ++i) {
             const uint32_t row = grp * R + i;
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
-                float acc = 0.0f;
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const uint32_t uu[4] = {wq[i][k].x, wq[i][k].y, wq[i][k].z, wq[i][k].w};
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        acc += __uint_as_float(uu[j] << 16) * xr.v[b][0][k * 8 + 2 * j];
-                        acc += __uint_as_float(uu[j] & 0xffff0000u) * xr.v[b][0][k * 8 + 2 * j + 1];
-                    }
-                }
-                acc = wave_sum(acc);
+                const float t = wave_sum(acc[i][b]);
                 if (lane == 0 && row <= a.E) {
-                    if (row < a.E) a.logits[(size_t)b * a.E + row] = acc;
-                    else a.sg[b] = acc;
+                    if (row < a.E) a.logits[(size_t)b * a.E + row] = t;
+                    else a.sg[b] = t;
                 }
             }
         }
@@ -1446,6 +1461,7 @@ void launch_dn_scan(const DnScanArgs& a, int nb, hipStream_t st) {
 }
 
 void launch_router(const RouterArgs& a, int nb, hipStream_t st) {
+    if (a.H % 32) throw std::runtime_error("router input width must be a multiple of 32");
     // one wave per workgroup so the 2 MiB matrix spreads over every CU
     constexpr int R = 2;
     const uint32_t grid = (a.E + 1 + R - 1) / R;

@@ -172,6 +172,14 @@ struct ChkEngine {
     KvDev mtp_kv{};
     Scratch s{};
     PfBufs pf{};
+    // all-logits mode of prefill_chunk: every row's logits of the last call
+    float* pf_all = nullptr;
+    uint64_t pf_all_cap = 0;  // rows the buffer holds
+    uint32_t pf_all_rows = 0; // rows of the last call kept (0: not kept)
+    std::vector<float> host_pf_row;
+    // rows of s.logits valid for logits_row (the last step's rows; 1 after
+    // a prefill, which writes its final row only)
+    uint32_t logit_rows = 0;
     uint32_t max_chunks = 1, lm_parts = 1024;
     // sequence
     uint32_t pos = 0, batch_pos = 0, batch_nb = 0, max_t = 0, trunk_rows = 1;
@@ -234,15 +242,36 @@ struct ChkEngine {
         if (s.h_in) hipHostFree(s.h_in);
         if (s.h_out) hipHostFree(s.h_out);
         for (void* p : allocs) hipFree(p);
+        for (void* p : pf_allocs) hipFree(p);
         if (st) hipStreamDestroy(st);
     }
 
+    // Device allocations: engine lifetime (`allocs`) or prefill scratch
+    // (`pf_allocs`, dropped by prefill_release); `alloc_bytes` counts both.
+    std::vector<void*> pf_allocs;
+    uint64_t alloc_bytes = 0, pf_alloc_bytes = 0;
     template <class T>
-    T* dalloc(uint64_t n) {
+    T* dalloc(uint64_t n, bool prefill_scratch = false) {
         void* p = nullptr;
-        HIPCHK(hipMalloc(&p, std::max<uint64_t>(n * sizeof(T), 256)));
-        allocs.push_back(p);
+        const uint64_t bytes = std::max<uint64_t>(n * sizeof(T), 256);
+        HIPCHK(hipMalloc(&p, bytes));
+        (prefill_scratch ? pf_allocs : allocs).push_back(p);
+        alloc_bytes += bytes;
+        if (prefill_scratch) pf_alloc_bytes += bytes;
         return reinterpret_cast<T*>(p);
+    }
+    template <class T>
+    T* pfalloc(uint64_t n) { return dalloc<T>(n, true); }
+    void prefill_release() {
+        if (st) hipStreamSynchronize(st);
+        for (void* p : pf_allocs) hipFree(p);
+        pf_allocs.clear();
+        alloc_bytes -= pf_alloc_bytes;
+        pf_alloc_bytes = 0;
+        pf = PfBufs{};
+        pf_all = nullptr;
+        pf_all_rows = 0;
+        pf_all_cap = 0;
     }
 
     bool is_linear(uint32_t l) const { return (l + 1) % c.full_attention_interval != 0; }
@@ -366,6 +395,9 @@ struct ChkEngine {
         ensure(c.full_attention_interval >= 1 && c.num_hidden_layers >= 1, "layer pattern");
         ensure(c.hc_count >= 2 && c.hc_count <= 4, "hc_count must be 2..=4 (one hyper-connection stream per wave)");
         ensure(c.hidden_size % 256 == 0, "hidden % 256 == 0 (gpu/load.rs:25-28)");
+        // the batch-1 expert kernels hold one 32-input chunk per lane of a
+        // wave (64 chunks)
+        ensure(c.hidden_size <= 2048, "hidden size must be at most 2048 (one 32-input chunk per lane)");
         ensure(c.hc_lowrank % 32 == 0 && c.hc_lowrank <= 2048, "hc_lowrank must be a multiple of 32");
         ensure(c.moe_intermediate_size % 64 == 0, "expert width must be a multiple of 64 (gpu/load.rs:37-40)");
         ensure(c.shared_expert_intermediate_size == c.moe_intermediate_size,
@@ -550,6 +582,7 @@ struct ChkEngine {
         mtp_len = 0;
         tokens.clear();
         folded_valid = false;
+        logit_rows = 0;
     }
 
     // ----------------------------------------------------------- blocks
@@ -836,6 +869,7 @@ struct ChkEngine {
         batch_pos = pos;
         batch_nb = n;
         batch_snap = snap;
+        logit_rows = n;
         for (uint32_t i = 0; i < n; ++i) s.h_in->tokens[i] = toks[i];
         s.h_in->pos = pos;
         std::atomic_thread_fence(std::memory_order_seq_cst);
@@ -895,23 +929,72 @@ struct ChkEngine {
         tokens.resize(pos);
     }
 
+    // ------------------------------------------------ prefix checkpoints
+    // Gpu::prefix_regions (gpu/state.rs:85-124): the device ranges that hold
+    // a sequence's state at trunk length `n` and MTP length `mtp_n`: every
+    // DeltaNet layer's recurrent state and conv history (whole), every
+    // attention layer's q8 K and V rows and their fp16 scale rows, its
+    // index keys and (past the QSA budget) its pooled block keys up to the
+    // length, then the MTP layer's at its own length.
+    struct Region {
+        void* ptr;
+        uint64_t bytes;
+    };
+    std::vector<Region> prefix_regions(uint32_t n, uint32_t mtp_n) const {
+        std::vector<Region> r;
+        const uint64_t sn = (uint64_t)D.nv * D.dv * D.dk * 4, hn = (uint64_t)D.conv_dim * (D.ck - 1) * 4;
+        auto attn = [&](const KvDev& k, uint32_t len) {
+            r.push_back({k.k, (uint64_t)len * D.kv_row});
+            r.push_back({k.ks, (uint64_t)len * (D.kv_row / 32) * 2});
+            r.push_back({k.v, (uint64_t)len * D.kv_row});
+            r.push_back({k.vs, (uint64_t)len * (D.kv_row / 32) * 2});
+            r.push_back({k.index_k, (uint64_t)len * D.ihd * 4});
+            if (k.block_k) r.push_back({k.block_k, (uint64_t)((len + D.ratio - 1) / D.ratio) * D.ihd * 4});
+        };
+        for (uint32_t l = 0; l < c.num_hidden_layers; ++l) {
+            if (layers[l].linear) {
+                r.push_back({dn_state[layers[l].dn_idx], sn});
+                r.push_back({dn_hist[layers[l].dn_idx], hn});
+            } else {
+                attn(kv[layers[l].at_idx], n);
+            }
+        }
+        if (has_mtp) attn(mtp_kv, mtp_n);
+        return r;
+    }
+    uint64_t state_bytes_at(uint32_t n, uint32_t mtp_n) const;
+    void save_into(ChkPrefixState*& cp);
+    void restore_prefix(const ChkPrefixState& cp);
+    void clear_profile() {
+        prof_collect();
+        prof_kind = PROF_NONE;
+        prof_ms = 0.0;
+        prof_bytes = 0;
+        prof_launches = 0;
+    }
+
     // ------------------------------------------------------------ MTP
     // mtp_forward prelude (cpu.rs:344-369): hyper_g = fc_e(rms_norm_shift(e))
     // + fc_h(rms_norm_shift(h_g)); then one attention + MoE block with the
     // MTP layer's own KV, the MTP mixer and the shared LM head.
     void mtp_rows(int rows, const float* src_hyper, const uint32_t* d_tokens, uint32_t base_pos);
     void mtp_pass_trunk(int rows, uint32_t base_pos, const uint32_t* d_next);
-    void prefill(const uint32_t* toks, uint32_t n, uint32_t* next, uint32_t* draft);
-    void prefill_rows(const uint32_t* toks, uint32_t n, uint32_t* next, uint32_t* draft);
+    void prefill(const uint32_t* toks, uint32_t n, uint32_t next_after, bool all_logits, uint32_t* next,
+                 uint32_t* draft);
+    void prefill_rows(const uint32_t* toks, uint32_t n, uint32_t next_after, bool all_logits, uint32_t* next,
+                      uint32_t* draft);
+    void pf_keep_logits(uint32_t rows);
+    uint64_t prefill_scratch_bytes(uint64_t rows, bool all_logits) const;
+    uint32_t prefill_rows_fit(bool all_logits) const;
     // ------------------------------------------------- GEMM prefill
     bool pf_supported() const;
     void pf_alloc();
     void pf_hc_read(const HcDev& w, float* inj, uint32_t T, bool for_moe);
     void pf_deltanet(const LayerDev& L, uint32_t T);
     void pf_attention(const LayerDev& L, uint32_t T, uint32_t pos0, const KvDev* kvo = nullptr);
-    void pf_mtp(const uint32_t* toks, uint32_t n, uint32_t c0, uint32_t T, uint32_t pos0, bool last);
+    void pf_mtp(const uint32_t* toks, uint32_t c0, uint32_t T, uint32_t pos0, bool last, uint32_t next_after);
     void pf_moe(const LayerDev& L, uint32_t T);
-    void prefill_gemm(const uint32_t* toks, uint32_t n, uint32_t* next);
+    void prefill_gemm(const uint32_t* toks, uint32_t n, uint32_t next_after, bool all_logits, uint32_t* next);
     void mtp_draft(const uint32_t* next, uint32_t n, uint32_t chain, uint32_t* drafts, uint32_t* nd);
 };
 
@@ -1025,25 +1108,51 @@ void ChkEngine::mtp_draft(const uint32_t* next, uint32_t n, uint32_t chain, uint
     mtp_logits_fresh = false;
 }
 
-// Gpu::prefill_chunk (gpu/prefill.rs:196-464): the GEMM path where this
-// engine implements it (Q4 experts, no MTP head), else the row path.  Both
-// leave the same state behind (prefill.rs:13-15).
-void ChkEngine::prefill(const uint32_t* toks, uint32_t n, uint32_t* next, uint32_t* draft) {
+// Gpu::prefill_chunk (gpu/prefill.rs:196-464): the GEMM path wherever this
+// engine implements it (every expert precision and the MTP head; not past
+// the QSA budget), else the row path.  Both leave the same state behind
+// (prefill.rs:13-15).  `next_after` (CHK_NO_TOKEN: none) is the token that
+// follows the chunk, paired with its last row by the MTP head; without it
+// the trunk's greedy token is (prefill.rs:354-355).  With `all_logits`
+// every row's logits are kept for pf_logits_row.
+void ChkEngine::prefill(const uint32_t* toks, uint32_t n, uint32_t next_after, bool all_logits, uint32_t* next,
+                        uint32_t* draft) {
+    ensure(n >= 1, "empty chunk");
+    ensure(pos + n <= max_t, "context capacity exceeded");
+    for (uint32_t i = 0; i < n; ++i) ensure(toks[i] < D.V, "token id out of range");
+    ensure(next_after == CHK_NO_TOKEN || next_after < D.V, "token id out of range");
+    pf_all_rows = 0;
+    if (all_logits) pf_keep_logits(n);
     if (pf_supported()) {
-        prefill_gemm(toks, n, next);
+        prefill_gemm(toks, n, next_after, all_logits, next);
         *draft = 0xffffffffu;
         if (has_mtp) HIPCHK(hipMemcpy(draft, s.mtp_out, 4, hipMemcpyDeviceToHost));
-        return;
+    } else {
+        prefill_rows(toks, n, next_after, all_logits, next, draft);
     }
-    prefill_rows(toks, n, next, draft);
+    if (all_logits) pf_all_rows = n;
+    // like the reference, the chunk leaves no step in flight: its final
+    // row's logits are logits_row(0)
+    batch_pos = pos;
+    batch_nb = 0;
+    batch_snap = false;
+    logit_rows = 1;
+    logits_fresh = false;
+    mtp_logits_fresh = false;
+}
+
+// The all-logits buffer: rows x vocab f32, grown to the largest chunk seen.
+void ChkEngine::pf_keep_logits(uint32_t rows) {
+    if (pf_all_cap >= rows) return;
+    pf_all = pfalloc<float>((uint64_t)rows * D.V);
+    pf_all_cap = rows;
 }
 
 // Prompt processing through the row path: rows of up to MAX_NB tokens,
 // committed as they go, MTP cache kept in step (gpu/prefill.rs semantics:
 // side effects identical to row stepping, prefill.rs:13-15).
-void ChkEngine::prefill_rows(const uint32_t* toks, uint32_t n, uint32_t* next, uint32_t* draft) {
-    ensure(n >= 1, "empty prefill chunk");
-    ensure(pos + n <= max_t, "context capacity exceeded");
+void ChkEngine::prefill_rows(const uint32_t* toks, uint32_t n, uint32_t next_after, bool all_logits, uint32_t* next,
+                             uint32_t* draft) {
     uint32_t saved_rows = trunk_rows;
     trunk_rows = MAX_NB;
     uint32_t last = 0;
@@ -1052,12 +1161,19 @@ void ChkEngine::prefill_rows(const uint32_t* toks, uint32_t n, uint32_t* next, u
             uint32_t m = std::min<uint32_t>(MAX_NB, n - i);
             uint32_t out[MAX_NB];
             step_rows(toks + i, m, false, false, out);
+            if (all_logits)
+                HIPCHK(hipMemcpyAsync(pf_all + (uint64_t)i * D.V, s.logits, (uint64_t)m * D.V * 4,
+                                      hipMemcpyDeviceToDevice, st));
             commit(m);
             if (has_mtp) {
                 // MTP cache rows for these positions pair each row with the
-                // token after it (the next prompt token, or the prediction)
+                // token after it: the next prompt token, `next_after` after
+                // the chunk's last row, else the trunk's prediction
                 uint32_t nx[MAX_NB];
-                for (uint32_t r = 0; r < m; ++r) nx[r] = (i + r + 1 < n) ? toks[i + r + 1] : out[r];
+                for (uint32_t r = 0; r < m; ++r) {
+                    const uint32_t p = i + r + 1;
+                    nx[r] = p < n ? toks[p] : (next_after != CHK_NO_TOKEN ? next_after : out[r]);
+                }
                 uint32_t d[4], nd = 0;
                 mtp_draft(nx, m, i + m >= n ? 1 : 0, d, &nd);
                 if (i + m >= n) *draft = nd ? d[0] : 0xffffffffu;
@@ -1069,8 +1185,50 @@ void ChkEngine::prefill_rows(const uint32_t* toks, uint32_t n, uint32_t* next, u
         throw;
     }
     trunk_rows = saved_rows;
+    // the final row's logits as logits_row(0)
+    if (batch_nb > 1)
+        HIPCHK(hipMemcpyAsync(s.logits, s.logits + (uint64_t)(batch_nb - 1) * D.V, (uint64_t)D.V * 4,
+                              hipMemcpyDeviceToDevice, st));
+    HIPCHK(hipStreamSynchronize(st));
     *next = last;
     if (!has_mtp) *draft = 0xffffffffu;
+}
+
+// Scratch a prefill of `rows` rows per GEMM chunk allocates (pf_alloc's
+// buffers, plus the all-logits rows).
+uint64_t ChkEngine::prefill_scratch_bytes(uint64_t C, bool all_logits) const {
+    const uint64_t slots = D.topk + 1, f = 4;
+    uint64_t b = C * 8 + C * D.hh * f;
+    if (has_mtp) b += C * 4 + C * (2ull * D.H + 3ull * D.hh) * f;
+    const uint64_t plane = std::max({C * D.hh, C * D.v_dim, C * D.nh * D.hd, C * slots * D.I, C * D.H});
+    b += plane * 2 * 2 + plane / 64 * f + 3 * C * D.H * 2;
+    b += C * (3ull * D.hc + D.lowrank + D.H + (uint64_t)D.hc * (D.lowrank + D.hc)) * f;
+    const uint64_t dn = C * (2ull * D.conv_dim + 2ull * D.v_dim + 4ull * D.nv);
+    const uint64_t at = C * (2ull * D.nh * D.hd + 2ull * D.kv_row + D.idx_out + 2ull * D.nh * D.hd);
+    b += std::max(dn, at) * f;
+    b += C * (D.E + 1 + 2ull * D.topk) * f + (D.E + 1ull) * C * 4 + (D.E + 1) * 4;
+    b += (uint64_t)pf_tile_bound((uint32_t)C, D.topk, D.E) * 4 + C * slots * (D.I + D.H) * f;
+    if (dc_supported(D.nk, D.nv, D.dk, D.dv)) b += dc_work_floats((uint32_t)C, D.nv, D.dv) * f;
+    if (all_logits) b += C * D.V * f;
+    return b;
+}
+
+// Gpu::prefill_rows_fit (prefill/allocation.rs:150-169): the largest chunk
+// (at most the context and 4096 rows, prefill.rs:116) whose scratch fits
+// the device memory that is free now (this engine's own prefill scratch
+// counts as free: it is reused or released before a replacement).
+uint32_t ChkEngine::prefill_rows_fit(bool all_logits) const {
+    size_t free_b = 0, total_b = 0;
+    HIPCHK(hipMemGetInfo(&free_b, &total_b));
+    const uint64_t avail = (uint64_t)free_b + pf_alloc_bytes;
+    uint32_t lo = 0, hi = std::min<uint32_t>(max_t, 4096);
+    while (lo < hi) {
+        const uint32_t mid = lo + (hi - lo + 1) / 2;
+        if (prefill_scratch_bytes(mid, all_logits) <= avail) lo = mid;
+        else hi = mid - 1;
+    }
+    ensure(lo > 0, "insufficient memory for prefill scratch; reduce expert pool or context capacity");
+    return lo;
 }
 
 // ------------------------------------------------------- GEMM prefill
@@ -1088,34 +1246,34 @@ void ChkEngine::pf_alloc() {
     if (pf.cap) return;
     const uint64_t C = std::min<uint32_t>(max_t, PF_MAX_ROWS);
     const uint64_t slots = D.topk + 1;
-    pf.tokens = dalloc<uint32_t>(C);
-    pf.pos = dalloc<uint32_t>(C);
-    pf.hyper = dalloc<float>(C * D.hh);
+    pf.tokens = pfalloc<uint32_t>(C);
+    pf.pos = pfalloc<uint32_t>(C);
+    pf.hyper = pfalloc<float>(C * D.hh);
     if (has_mtp) {
-        pf.mtp_tok = dalloc<uint32_t>(C);
-        pf.mtp_en = dalloc<float>(C * D.H);
-        pf.mtp_hn = dalloc<float>(C * D.hh);
-        pf.mtp_fe = dalloc<float>(C * D.H);
-        pf.mtp_fh = dalloc<float>(C * D.hh);
-        pf.mtp_hyper = dalloc<float>(C * D.hh);
+        pf.mtp_tok = pfalloc<uint32_t>(C);
+        pf.mtp_en = pfalloc<float>(C * D.H);
+        pf.mtp_hn = pfalloc<float>(C * D.hh);
+        pf.mtp_fe = pfalloc<float>(C * D.H);
+        pf.mtp_fh = pfalloc<float>(C * D.hh);
+        pf.mtp_hyper = pfalloc<float>(C * D.hh);
     }
     const uint64_t plane = std::max({C * D.hh, C * D.v_dim, C * D.nh * D.hd, C * slots * D.I, C * D.H});
-    pf.hi = dalloc<uint4>(plane / 8);
-    pf.lo = dalloc<uint4>(plane / 8);
-    pf.xs = dalloc<float>(plane / 64);
-    pf.bhi = dalloc<uint4>(C * D.H / 8);
-    pf.bmid = dalloc<uint4>(C * D.H / 8);
-    pf.blo = dalloc<uint4>(C * D.H / 8);
-    pf.inv = dalloc<float>(C * D.hc);
-    pf.d = dalloc<float>(C * D.lowrank);
-    pf.hc_part = dalloc<float>(C * D.hc * (D.lowrank + D.hc));
-    pf.inj_a = dalloc<float>(C * D.hc);
-    pf.inj_m = dalloc<float>(C * D.hc);
-    pf.mixed = dalloc<float>(C * D.H);
+    pf.hi = pfalloc<uint4>(plane / 8);
+    pf.lo = pfalloc<uint4>(plane / 8);
+    pf.xs = pfalloc<float>(plane / 64);
+    pf.bhi = pfalloc<uint4>(C * D.H / 8);
+    pf.bmid = pfalloc<uint4>(C * D.H / 8);
+    pf.blo = pfalloc<uint4>(C * D.H / 8);
+    pf.inv = pfalloc<float>(C * D.hc);
+    pf.d = pfalloc<float>(C * D.lowrank);
+    pf.hc_part = pfalloc<float>(C * D.hc * (D.lowrank + D.hc));
+    pf.inj_a = pfalloc<float>(C * D.hc);
+    pf.inj_m = pfalloc<float>(C * D.hc);
+    pf.mixed = pfalloc<float>(C * D.H);
     // DeltaNet / attention arena
     const uint64_t dn = C * (2ull * D.conv_dim + 2ull * D.v_dim + 4ull * D.nv);
     const uint64_t at = C * (2ull * D.nh * D.hd + 2ull * D.kv_row + D.idx_out + 2ull * D.nh * D.hd);
-    float* arena = dalloc<float>(std::max(dn, at));
+    float* arena = pfalloc<float>(std::max(dn, at));
     float* q = arena;
     pf.raw = q; q += C * D.conv_dim;
     pf.conv = q; q += C * D.conv_dim;
@@ -1132,17 +1290,17 @@ void ChkEngine::pf_alloc() {
     pf.idx_raw = q; q += C * D.idx_out;
     pf.q_ready = q; q += C * D.nh * D.hd;
     pf.attn_out = q;
-    pf.logits = dalloc<float>(C * D.E);
-    pf.sg = dalloc<float>(C);
-    pf.wts = dalloc<float>(C * D.topk);
-    pf.ids = dalloc<uint32_t>(C * D.topk);
-    pf.list = dalloc<uint32_t>((D.E + 1) * C);
-    pf.count = dalloc<uint32_t>(D.E + 1);
-    pf.tiles = dalloc<uint32_t>(pf_tile_bound((uint32_t)C, D.topk, D.E));
-    pf.ntiles = dalloc<uint32_t>(1);
-    pf.act = dalloc<float>(C * slots * D.I);
-    pf.yd = dalloc<float>(C * slots * D.H);
-    pf.dcw = dc_supported(D.nk, D.nv, D.dk, D.dv) ? dalloc<float>(dc_work_floats((uint32_t)C, D.nv, D.dv)) : nullptr;
+    pf.logits = pfalloc<float>(C * D.E);
+    pf.sg = pfalloc<float>(C);
+    pf.wts = pfalloc<float>(C * D.topk);
+    pf.ids = pfalloc<uint32_t>(C * D.topk);
+    pf.list = pfalloc<uint32_t>((D.E + 1) * C);
+    pf.count = pfalloc<uint32_t>(D.E + 1);
+    pf.tiles = pfalloc<uint32_t>(pf_tile_bound((uint32_t)C, D.topk, D.E));
+    pf.ntiles = pfalloc<uint32_t>(1);
+    pf.act = pfalloc<float>(C * slots * D.I);
+    pf.yd = pfalloc<float>(C * slots * D.H);
+    pf.dcw = dc_supported(D.nk, D.nv, D.dk, D.dv) ? pfalloc<float>(dc_work_floats((uint32_t)C, D.nv, D.dv)) : nullptr;
     pf.cap = (uint32_t)C;
 }
 
@@ -1379,10 +1537,8 @@ void ChkEngine::pf_moe(const LayerDev& L, uint32_t T) {
     launch_pf_moe_combine(pf.yd, pf.wts, pf.sg, pf.inj_m, pf.hyper, T, D.H, D.topk, D.hc, st);
 }
 
-void ChkEngine::prefill_gemm(const uint32_t* toks, uint32_t n, uint32_t* next) {
-    ensure(n >= 1, "empty prefill chunk");
-    ensure(pos + n <= max_t, "context capacity exceeded");
-    for (uint32_t i = 0; i < n; ++i) ensure(toks[i] < D.V, "token id out of range");
+void ChkEngine::prefill_gemm(const uint32_t* toks, uint32_t n, uint32_t next_after, bool all_logits,
+                             uint32_t* next) {
     pf_alloc();
     folded_valid = false;
     tokens.resize(pos);
@@ -1401,24 +1557,29 @@ void ChkEngine::prefill_gemm(const uint32_t* toks, uint32_t n, uint32_t* next) {
             pf_hc_read(L.mlp_hc, pf.inj_m, T, true);
             pf_moe(L, T);
         }
+        if (all_logits) {
+            // every row through the final mixer and the LM head, four rows
+            // per launch pair (the decode kernels; a checking mode)
+            for (uint32_t r0 = 0; r0 < T; r0 += MAX_NB) {
+                const int nb = (int)std::min<uint32_t>(MAX_NB, T - r0);
+                hc_read(final_mixer, pf.hyper + (uint64_t)r0 * D.hh, nullptr, nb);
+                launch_lm_head(lm_head, s.mixed, pf_all + (uint64_t)(c0 + r0) * D.V, s.pv, s.pi, lm_parts, s.out_tok,
+                               nb, st);
+            }
+        }
         const bool last = c0 + T >= n;
         if (last) {
             // final mixer and LM head on the chunk's last row (prefill.rs:308-334)
             hc_read(final_mixer, pf.hyper + (uint64_t)(T - 1) * D.hh, nullptr, 1);
             launch_lm_head(lm_head, s.mixed, s.logits, s.pv, s.pi, lm_parts, s.d_out, 1, st);
         }
-        if (has_mtp) pf_mtp(toks, n, c0, T, pos0, last);
+        if (has_mtp) pf_mtp(toks, c0, T, pos0, last, next_after);
         HIPCHK(hipStreamSynchronize(st));
         HIPCHK(hipGetLastError());
         tokens.insert(tokens.end(), toks + c0, toks + c0 + T);
         pos = pos0 + T;
     }
     *next = s.h_out[0];
-    batch_pos = pos - 1;
-    batch_nb = 1;
-    batch_snap = false;
-    logits_fresh = false;
-    mtp_logits_fresh = false;
     if (has_mtp) {
         mtp_len = pos;
         last_mtp_rows = 1;
@@ -1427,16 +1588,19 @@ void ChkEngine::prefill_gemm(const uint32_t* toks, uint32_t n, uint32_t* next) {
 
 // The MTP head over a prefill chunk (gpu/prefill.rs:335-446): row r pairs
 // the trunk residual at pos0 + r with the token after it (the next prompt
-// token; on the last row of the final chunk the trunk's greedy token),
+// token; after the call's last row `next_after` when the caller knows it,
+// else the trunk's greedy token),
 // fc_e / fc_h as GEMMs over the chunk, the MTP layer through the prefill
 // layer path on its own residual and KV cache, the last row's residual
 // kept where chained drafts re-enter, and on the final chunk the MTP mixer
 // and LM head on that row (the draft).
-void ChkEngine::pf_mtp(const uint32_t* toks, uint32_t n, uint32_t c0, uint32_t T, uint32_t pos0, bool last) {
+void ChkEngine::pf_mtp(const uint32_t* toks, uint32_t c0, uint32_t T, uint32_t pos0, bool last,
+                       uint32_t next_after) {
     if (T > 1) HIPCHK(hipMemcpyAsync(pf.mtp_tok, toks + c0 + 1, (T - 1) * 4, hipMemcpyHostToDevice, st));
-    if (last) HIPCHK(hipMemcpyAsync(pf.mtp_tok + T - 1, s.d_out, 4, hipMemcpyDeviceToDevice, st));
-    else HIPCHK(hipMemcpyAsync(pf.mtp_tok + T - 1, toks + c0 + T, 4, hipMemcpyHostToDevice, st));
-    (void)n;
+    if (!last) HIPCHK(hipMemcpyAsync(pf.mtp_tok + T - 1, toks + c0 + T, 4, hipMemcpyHostToDevice, st));
+    else if (next_after != CHK_NO_TOKEN)
+        HIPCHK(hipMemcpyAsync(pf.mtp_tok + T - 1, &next_after, 4, hipMemcpyHostToDevice, st));
+    else HIPCHK(hipMemcpyAsync(pf.mtp_tok + T - 1, s.d_out, 4, hipMemcpyDeviceToDevice, st));
     launch_mtp_prelude(pf.mtp_tok, embed, mtp_enorm, mtp_hnorm, pf.hyper, pf.mtp_en, pf.mtp_hn, D.H, D.hc, D.eps,
                        (int)T, st);
     launch_pf_xprep(pf.mtp_en, D.H, T, D.H, pf.hi, pf.lo, pf.xs, st);
@@ -1463,6 +1627,86 @@ void ChkEngine::pf_mtp(const uint32_t* toks, uint32_t n, uint32_t c0, uint32_t T
         hc_read(mtp_mixer, tail, nullptr, 1);
         launch_lm_head(lm_head, s.mixed, s.mtp_logits, s.pv, s.pi, lm_parts, s.mtp_out, 1, st);
     }
+}
+
+// A sequence checkpoint (Gpu's PrefixState, gpu.rs:560-566): position, MTP
+// length, the token history and a copy of every prefix region.  The copies
+// stay in HBM (one device buffer per region, grown and reused by
+// save_into), so a save or restore is a device-to-device copy.
+struct ChkPrefixState {
+    uint32_t pos = 0, mtp_len = 0;
+    std::vector<uint32_t> tokens;
+    struct Buf {
+        void* ptr = nullptr;
+        uint64_t bytes = 0, cap = 0;
+    };
+    std::vector<Buf> data;
+    ~ChkPrefixState() {
+        for (auto& b : data)
+            if (b.ptr) hipFree(b.ptr);
+    }
+};
+
+// Gpu::state_bytes_at (gpu/state.rs:130-137): the bytes a checkpoint at
+// these lengths holds (regions, token history and the record itself).
+uint64_t ChkEngine::state_bytes_at(uint32_t n, uint32_t mtp_n) const {
+    uint64_t b = sizeof(ChkPrefixState) + (uint64_t)n * 4;
+    for (const Region& r : prefix_regions(n, mtp_n)) b += r.bytes + sizeof(ChkPrefixState::Buf);
+    return b;
+}
+
+// Gpu::save_prefix / save_into (gpu/state.rs:139-193): copy the regions at
+// the current lengths, reusing the checkpoint's buffers where they are large
+// enough (only initialised prefixes are copied).
+void ChkEngine::save_into(ChkPrefixState*& cp) {
+    std::unique_ptr<ChkPrefixState> fresh;
+    if (!cp) {
+        fresh.reset(new ChkPrefixState());
+        cp = fresh.get();
+    }
+    try {
+        const std::vector<Region> regs = prefix_regions(pos, mtp_len);
+        cp->data.resize(regs.size());
+        for (size_t i = 0; i < regs.size(); ++i) {
+            ChkPrefixState::Buf& b = cp->data[i];
+            if (b.cap < regs[i].bytes) {
+                if (b.ptr) HIPCHK(hipFree(b.ptr));
+                b.ptr = nullptr;
+                b.cap = 0;
+                HIPCHK(hipMalloc(&b.ptr, std::max<uint64_t>(regs[i].bytes, 256)));
+                b.cap = std::max<uint64_t>(regs[i].bytes, 256);
+            }
+            b.bytes = regs[i].bytes;
+            if (b.bytes) HIPCHK(hipMemcpyAsync(b.ptr, regs[i].ptr, b.bytes, hipMemcpyDeviceToDevice, st));
+        }
+        HIPCHK(hipStreamSynchronize(st));
+    } catch (...) {
+        if (fresh) cp = nullptr;
+        throw;
+    }
+    cp->pos = pos;
+    cp->mtp_len = mtp_len;
+    cp->tokens.assign(tokens.begin(), tokens.begin() + std::min<size_t>(pos, tokens.size()));
+    fresh.release();
+}
+
+// Gpu::restore_prefix (gpu/state.rs:195-230).
+void ChkEngine::restore_prefix(const ChkPrefixState& cp) {
+    ensure(cp.pos <= max_t && cp.mtp_len <= max_t, "prefix exceeds context");
+    const std::vector<Region> regs = prefix_regions(cp.pos, cp.mtp_len);
+    ensure(regs.size() == cp.data.size(), "prefix state layout mismatch");
+    for (size_t i = 0; i < regs.size(); ++i) ensure(regs[i].bytes == cp.data[i].bytes, "prefix region mismatch");
+    for (size_t i = 0; i < regs.size(); ++i)
+        if (regs[i].bytes)
+            HIPCHK(hipMemcpyAsync(regs[i].ptr, cp.data[i].ptr, regs[i].bytes, hipMemcpyDeviceToDevice, st));
+    HIPCHK(hipStreamSynchronize(st));
+    pos = cp.pos;
+    mtp_len = cp.mtp_len;
+    tokens = cp.tokens;
+    batch_pos = pos;
+    batch_nb = 0;
+    folded_valid = false;
+    logit_rows = 0;
 }
 
 // ===================================================================== C ABI
@@ -1518,17 +1762,42 @@ int chk_mtp_chain(ChkEngine* e, uint32_t draft, uint32_t* out) {
     })
 }
 
-int chk_prefill_chunk(ChkEngine* e, const uint32_t* tokens, uint32_t n, uint32_t* next, uint32_t* draft) {
-    CHK_TRY(e->prefill(tokens, n, next, draft))
+int chk_prefill_chunk(ChkEngine* e, const uint32_t* tokens, uint32_t n, uint32_t next_after, int all_logits,
+                      uint32_t* next, uint32_t* draft) {
+    CHK_TRY(e->prefill(tokens, n, next_after, all_logits != 0, next, draft))
+}
+
+void chk_prefill_release(ChkEngine* e) { e->prefill_release(); }
+
+int chk_prefill_rows_fit(const ChkEngine* e, int all_logits, uint32_t* rows) {
+    CHK_TRY(*rows = e->prefill_rows_fit(all_logits != 0))
+}
+
+const float* chk_pf_logits_row(ChkEngine* e, uint32_t r) {
+    if (!e->pf_all_rows) {
+        chk::g_err = "prefill logits not kept";
+        return nullptr;
+    }
+    if (r >= e->pf_all_rows) {
+        chk::g_err = "prefill logits row out of range";
+        return nullptr;
+    }
+    e->host_pf_row.resize(e->D.V);
+    if (hipMemcpy(e->host_pf_row.data(), e->pf_all + (size_t)r * e->D.V, (size_t)e->D.V * 4, hipMemcpyDeviceToHost) !=
+        hipSuccess) {
+        chk::g_err = "logits copy failed";
+        return nullptr;
+    }
+    return e->host_pf_row.data();
 }
 
 const float* chk_logits_row(ChkEngine* e, uint32_t r) {
-    if (r >= e->batch_nb) {
+    if (r >= e->logit_rows) {
         chk::g_err = "logits row out of range";
         return nullptr;
     }
     if (!e->logits_fresh) {
-        if (hipMemcpy(e->host_logits.data(), e->s.logits, (size_t)e->batch_nb * e->D.V * 4, hipMemcpyDeviceToHost) !=
+        if (hipMemcpy(e->host_logits.data(), e->s.logits, (size_t)e->logit_rows * e->D.V * 4, hipMemcpyDeviceToHost) !=
             hipSuccess) {
             chk::g_err = "logits copy failed";
             return nullptr;
@@ -1560,6 +1829,74 @@ uint32_t chk_max_t(const ChkEngine* e) { return e->max_t; }
 uint32_t chk_trunk_rows(const ChkEngine* e) { return e->trunk_rows; }
 int chk_has_mtp(const ChkEngine* e) { return e->has_mtp ? 1 : 0; }
 
+const float* chk_logits(ChkEngine* e) { return chk_logits_row(e, 0); }
+
+uint32_t chk_last_logits_row(const ChkEngine* e) { return e->batch_nb ? e->batch_nb - 1 : 0; }
+
+double chk_allocated_gb(const ChkEngine* e) { return (double)e->alloc_bytes / 1e9; }
+
+// kv_layer_bytes (gpu.rs:631-642) at n positions, for this engine's layout:
+// q8 K and V with fp16 scales per 32 values, f32 index keys, and the pooled
+// block keys when the context can pass the QSA budget
+static uint64_t kv_layer_bytes(const ChkEngine* e, uint64_t n) {
+    const Dims& D = e->D;
+    uint64_t b = 2 * (n * D.kv_row + n * (D.kv_row / 32) * 2) + n * D.ihd * 4;
+    if (D.qsa) b += (n + D.ratio - 1) / D.ratio * D.ihd * 4;
+    return b;
+}
+
+uint64_t chk_kv_cache_bytes(const ChkEngine* e) {
+    return e->kv.size() * kv_layer_bytes(e, e->pos) + (e->has_mtp ? kv_layer_bytes(e, e->mtp_len) : 0);
+}
+
+uint64_t chk_kv_cache_capacity(const ChkEngine* e) {
+    return (e->kv.size() + (e->has_mtp ? 1 : 0)) * kv_layer_bytes(e, e->max_t);
+}
+
+double chk_kv_cache_fullness(const ChkEngine* e) {
+    return (double)chk_kv_cache_bytes(e) / (double)std::max<uint64_t>(chk_kv_cache_capacity(e), 1);
+}
+
+double chk_context_fullness(const ChkEngine* e) { return (double)e->pos / (double)std::max<uint32_t>(e->max_t, 1); }
+
+int chk_reset_request(ChkEngine* e) {
+    CHK_TRY(e->reset_state(); e->clear_profile(); HIPCHK(hipStreamSynchronize(e->st)))
+}
+
+int chk_clear_profile(ChkEngine* e) { CHK_TRY(e->clear_profile()) }
+
+uint64_t chk_prefix_state_bytes(const ChkEngine* e) { return e->state_bytes_at(e->pos, e->mtp_len); }
+
+uint64_t chk_state_bytes_at(const ChkEngine* e, uint32_t pos, uint32_t mtp_len) {
+    return e->state_bytes_at(pos, mtp_len);
+}
+
+int chk_save_prefix(ChkEngine* e, ChkPrefixState** out) {
+    *out = nullptr;
+    CHK_TRY(e->save_into(*out))
+}
+
+int chk_save_into(ChkEngine* e, ChkPrefixState** checkpoint) { CHK_TRY(e->save_into(*checkpoint)) }
+
+int chk_restore_prefix(ChkEngine* e, const ChkPrefixState* state) {
+    CHK_TRY({
+        ensure(state != nullptr, "no checkpoint");
+        e->restore_prefix(*state);
+    })
+}
+
+void chk_prefix_free(ChkPrefixState* state) { delete state; }
+
+uint32_t chk_prefix_pos(const ChkPrefixState* state) { return state->pos; }
+
+uint32_t chk_prefix_mtp_len(const ChkPrefixState* state) { return state->mtp_len; }
+
+uint32_t chk_prefix_tokens(const ChkPrefixState* state, uint32_t* out, uint32_t cap) {
+    const uint32_t n = (uint32_t)state->tokens.size();
+    for (uint32_t i = 0; i < std::min(n, cap); ++i) out[i] = state->tokens[i];
+    return n;
+}
+
 int chk_memory_stats(const ChkEngine* e, ChkMemoryStats* m) {
     uint64_t nrec = (uint64_t)e->record_layers * e->D.E;
     m->dense = e->dense_bytes;
@@ -1572,26 +1909,88 @@ int chk_memory_stats(const ChkEngine* e, ChkMemoryStats* m) {
     return 0;
 }
 
-uint32_t chk_pool_slots(const ChkEngine* e) { return e->record_layers * e->D.E; }
-uint32_t chk_pool_resident(const ChkEngine* e) { return e->record_layers * e->D.E; }
-int chk_pool_is_member(const ChkEngine* e, uint32_t rid) { return rid < e->record_layers * e->D.E ? 1 : 0; }
-uint32_t chk_pool_acquire(ChkEngine* e, const uint32_t* rids, uint32_t n, uint32_t* need) {
-    (void)e; (void)rids; (void)n; (void)need;
-    return 0;  // every record is resident: nothing to read
+// ---- expert-cache interface (residency::Pool, gpu/residency.rs:255-460)
+// over the all-resident HBM store: every record of the store is a member
+// from load on, so acquire never needs a read, plan_reads plans none and
+// finish has nothing to wait for.
+
+static uint32_t pool_records(const ChkEngine* e) { return e->record_layers * e->D.E; }
+static uint32_t pool_store_kind(const ChkEngine* e) { return e->o.experts == 3 ? 1u : (e->o.experts == 2 ? 2u : 0u); }
+
+uint32_t chk_pool_slots(const ChkEngine* e) { return pool_records(e); }
+uint32_t chk_pool_budget(const ChkEngine* e) { return pool_records(e); }
+uint32_t chk_pool_resident(const ChkEngine* e) { return pool_records(e); }
+int chk_pool_is_member(const ChkEngine* e, uint32_t rid) { return rid < pool_records(e) ? 1 : 0; }
+
+int chk_pool_acquire(ChkEngine* e, const uint32_t* rids, uint32_t n, uint64_t step, uint32_t* need,
+                     uint32_t* n_need) {
+    CHK_TRY({
+        (void)step;
+        (void)need;
+        for (uint32_t i = 0; i < n; ++i) ensure(rids[i] < pool_records(e), "record id out of range");
+        *n_need = 0;  // every record is resident: nothing to read
+    })
 }
+
+int chk_pool_plan_reads(const ChkEngine* e, const uint32_t* need, uint32_t n, uint32_t* n_reads, uint32_t* warm) {
+    CHK_TRY({
+        for (uint32_t i = 0; i < n; ++i) ensure(need[i] < pool_records(e), "record id out of range");
+        *n_reads = 0;
+        *warm = n;
+    })
+}
+
+int chk_pool_finish(ChkEngine* e, const uint32_t* rids, uint32_t n) {
+    CHK_TRY({
+        for (uint32_t i = 0; i < n; ++i) ensure(rids[i] < pool_records(e), "record id out of range");
+    })
+}
+
 uint64_t chk_pool_addr(const ChkEngine* e, uint32_t rid) {
-    if (rid >= e->record_layers * e->D.E) return 0;
+    if (rid >= pool_records(e)) return 0;
     if (e->o.experts == 4) return (uint64_t)(uintptr_t)e->experts4 + (uint64_t)rid * e->rl4.stride;
     uint64_t tag = e->o.experts == 3 ? (1ull << 63) : (1ull << 62);
     return ((uint64_t)(uintptr_t)e->experts_lo + (uint64_t)rid * e->rllo.stride) | tag;
 }
-uint32_t chk_pool_kind(const ChkEngine* e, uint32_t rid) {
-    (void)rid;
-    return e->o.experts == 3 ? 1u : (e->o.experts == 2 ? 2u : 0u);
+
+int chk_pool_buf(const ChkEngine* e, uint32_t rid, void** base, uint64_t* offset) {
+    CHK_TRY({
+        ensure(rid < pool_records(e), "record id out of range");
+        const bool q4 = e->o.experts == 4;
+        *base = q4 ? (void*)e->experts4 : (void*)e->experts_lo;
+        *offset = (uint64_t)rid * (q4 ? e->rl4.stride : e->rllo.stride);
+    })
 }
+
+uint32_t chk_pool_kind(const ChkEngine* e, uint32_t rid) {
+    return rid < pool_records(e) ? pool_store_kind(e) : 0u;
+}
+
+int chk_pool_set_kind(ChkEngine* e, uint32_t rid, uint32_t kind) {
+    CHK_TRY({
+        ensure(rid < pool_records(e), "record id out of range");
+        ensure(kind <= 2, "kind must be 0 (4-bit), 1 (3-bit) or 2 (2-bit)");
+        ensure(kind == pool_store_kind(e),
+               "every record of this store has the store's precision (per-record precision is not supported)");
+    })
+}
+
+int chk_pool_store(const ChkEngine* e, uint32_t kind, void** base, uint64_t* stride) {
+    CHK_TRY({
+        if (kind == 0) {
+            *base = e->experts4;
+            *stride = e->rl4.stride;
+        } else {
+            ensure(e->experts_lo && kind == pool_store_kind(e), "low-bit store of that kind not attached");
+            *base = e->experts_lo;
+            *stride = e->rllo.stride;
+        }
+    })
+}
+
 uint64_t chk_pool_bytes(const ChkEngine* e) {
-    uint64_t nrec = (uint64_t)e->record_layers * e->D.E;
-    return nrec * e->rl4.stride + (e->experts_lo ? nrec * e->rllo.stride : 0);
+    uint64_t nrec = pool_records(e);
+    return nrec * (e->o.experts == 4 ? e->rl4.stride : e->rllo.stride);
 }
 
 int chk_last_routes(const ChkEngine* e, uint32_t layer, uint32_t r, uint32_t* ids, float* weights) {
@@ -1968,6 +2367,36 @@ int chk_q4_gemm(const void* w, const void* s, const void* b, uint32_t out, uint3
         HIPCHK(hipFree(lo));
         HIPCHK(hipFree(xs));
         HIPCHK(hipFree(pack));
+    })
+}
+
+int chk_prefix_regions(const ChkEngine* e, uint32_t pos, uint32_t mtp_len, uint64_t* ptrs, uint64_t* bytes,
+                       uint32_t cap, uint32_t* count) {
+    CHK_TRY({
+        ensure(pos <= e->max_t && mtp_len <= e->max_t, "prefix exceeds context");
+        const auto regs = e->prefix_regions(pos, mtp_len);
+        *count = (uint32_t)regs.size();
+        for (uint32_t i = 0; i < std::min<uint32_t>(cap, (uint32_t)regs.size()); ++i) {
+            ptrs[i] = (uint64_t)(uintptr_t)regs[i].ptr;
+            bytes[i] = regs[i].bytes;
+        }
+    })
+}
+
+int chk_prefix_read(const ChkPrefixState* state, uint32_t i, void* host, uint64_t n) {
+    CHK_TRY({
+        ensure(i < state->data.size(), "region out of range");
+        ensure(n <= state->data[i].bytes, "read past the region");
+        if (n) HIPCHK(hipMemcpy(host, state->data[i].ptr, n, hipMemcpyDeviceToHost));
+    })
+}
+
+int chk_fill_u8(void* dst, uint32_t value, uint64_t n, void* stream) {
+    CHK_TRY({
+        hipStream_t st = (hipStream_t)stream;
+        launch_fill_u8((uint8_t*)dst, (uint8_t)value, n, st);
+        HIPCHK(hipStreamSynchronize(st));
+        HIPCHK(hipGetLastError());
     })
 }
 

@@ -14,6 +14,9 @@
 
 namespace chk {
 
+// last error message of the calling thread (chk_last_error)
+extern thread_local std::string g_err;
+
 constexpr int MAX_NB = 4;    // rows per step: one token + up to 3 drafts (gpu.rs:68)
 constexpr int MAX_SNAP = 3;  // rollback planes (gpu.rs:70)
 constexpr int ATTN_CHUNK = 64;  // tokens per attention partial

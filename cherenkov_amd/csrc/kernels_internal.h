@@ -408,5 +408,6 @@ bool attn_shape_ok(uint32_t nh, uint32_t nkv, uint32_t hd);
 void launch_copy_f32(float* dst, const float* src, uint64_t n, hipStream_t st);
 void launch_kv_fill(const float* k, const float* v, KvDev kv, uint32_t kv_row, uint32_t T, hipStream_t st);
 void launch_zero_f32(float* dst, uint64_t n, hipStream_t st);
+void launch_fill_u8(uint8_t* dst, uint8_t v, uint64_t n, hipStream_t st);
 
 }  // namespace chk

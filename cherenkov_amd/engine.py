@@ -14,7 +14,7 @@ from typing import Iterable, Sequence
 
 import numpy as np
 
-from .abi import ChkConfig, ChkMemoryStats, ChkOptions, EngineError, check, lib
+from .abi import NO_TOKEN, ChkConfig, ChkMemoryStats, ChkOptions, EngineError, check, lib
 
 U32P = C.POINTER(C.c_uint32)
 
@@ -77,16 +77,39 @@ class Engine:
         check(self.L.chk_mtp_chain(self._h, draft, C.byref(out)))
         return out.value
 
-    def prefill_chunk(self, tokens: Sequence[int]) -> tuple[int, int | None]:
+    def prefill_chunk(self, tokens: Sequence[int], next_after: int | None = None,
+                      all_logits: bool = False) -> tuple[int, int | None]:
+        """Gpu::prefill_chunk(tokens, next_after, all_logits) -> (next, draft)."""
         nxt, dr = C.c_uint32(), C.c_uint32()
-        check(self.L.chk_prefill_chunk(self._h, _u32(tokens), len(tokens), C.byref(nxt), C.byref(dr)))
-        return nxt.value, (None if dr.value == 0xFFFFFFFF else dr.value)
+        na = NO_TOKEN if next_after is None else int(next_after)
+        check(self.L.chk_prefill_chunk(self._h, _u32(tokens), len(tokens), na, int(all_logits), C.byref(nxt),
+                                       C.byref(dr)))
+        return nxt.value, (None if dr.value == NO_TOKEN else dr.value)
 
-    def logits_row(self, r: int) -> np.ndarray:
-        p = self.L.chk_logits_row(self._h, r)
+    def prefill_release(self) -> None:
+        self.L.chk_prefill_release(self._h)
+
+    def prefill_rows_fit(self, all_logits: bool = False) -> int:
+        r = C.c_uint32()
+        check(self.L.chk_prefill_rows_fit(self._h, int(all_logits), C.byref(r)))
+        return r.value
+
+    def pf_logits_row(self, r: int) -> np.ndarray:
+        return self._vocab_row(self.L.chk_pf_logits_row(self._h, r))
+
+    def _vocab_row(self, p) -> np.ndarray:
         if not p:
             raise EngineError(self.L.chk_last_error().decode())
         return np.ctypeslib.as_array(p, shape=(self.cfg.vocab_size,)).copy()
+
+    def logits_row(self, r: int) -> np.ndarray:
+        return self._vocab_row(self.L.chk_logits_row(self._h, r))
+
+    def logits(self) -> np.ndarray:
+        return self._vocab_row(self.L.chk_logits(self._h))
+
+    def last_logits_row(self) -> int:
+        return self.L.chk_last_logits_row(self._h)
 
     def mtp_logits_row(self, r: int) -> np.ndarray:
         p = self.L.chk_mtp_logits_row(self._h, r)
@@ -109,6 +132,90 @@ class Engine:
     @property
     def has_mtp(self) -> bool:
         return bool(self.L.chk_has_mtp(self._h))
+
+    def allocated_gb(self) -> float:
+        return self.L.chk_allocated_gb(self._h)
+
+    def kv_cache_bytes(self) -> int:
+        return self.L.chk_kv_cache_bytes(self._h)
+
+    def kv_cache_capacity(self) -> int:
+        return self.L.chk_kv_cache_capacity(self._h)
+
+    def kv_cache_fullness(self) -> float:
+        return self.L.chk_kv_cache_fullness(self._h)
+
+    def context_fullness(self) -> float:
+        return self.L.chk_context_fullness(self._h)
+
+    def reset_request(self) -> None:
+        check(self.L.chk_reset_request(self._h))
+
+    def clear_profile(self) -> None:
+        check(self.L.chk_clear_profile(self._h))
+
+    # ---- sequence checkpoints (gpu/state.rs:85-230) ----
+    def prefix_state_bytes(self) -> int:
+        return self.L.chk_prefix_state_bytes(self._h)
+
+    def state_bytes_at(self, pos: int, mtp_len: int) -> int:
+        return self.L.chk_state_bytes_at(self._h, pos, mtp_len)
+
+    def save_prefix(self) -> "PrefixState":
+        h = C.c_void_p()
+        check(self.L.chk_save_prefix(self._h, C.byref(h)))
+        return PrefixState(self, h)
+
+    def save_into(self, checkpoint: "PrefixState | None") -> "PrefixState":
+        if checkpoint is None:
+            return self.save_prefix()
+        check(self.L.chk_save_into(self._h, C.byref(checkpoint._h)))
+        return checkpoint
+
+    def restore_prefix(self, state: "PrefixState") -> None:
+        check(self.L.chk_restore_prefix(self._h, state._h))
+
+    def prefix_regions(self, pos: int, mtp_len: int) -> list[tuple[int, int]]:
+        n = C.c_uint32()
+        check(self.L.chk_prefix_regions(self._h, pos, mtp_len, None, None, 0, C.byref(n)))
+        ptrs = (C.c_uint64 * max(n.value, 1))()
+        lens = (C.c_uint64 * max(n.value, 1))()
+        check(self.L.chk_prefix_regions(self._h, pos, mtp_len, ptrs, lens, n.value, C.byref(n)))
+        return [(ptrs[i], lens[i]) for i in range(n.value)]
+
+    # ---- expert-cache interface (residency::Pool) ----
+    def pool_acquire(self, rids: Sequence[int], step: int) -> list[int]:
+        need = (C.c_uint32 * max(len(rids), 1))()
+        nn = C.c_uint32()
+        check(self.L.chk_pool_acquire(self._h, _u32(rids), len(rids), step, need, C.byref(nn)))
+        return list(need[: nn.value])
+
+    def pool_plan_reads(self, need: Sequence[int]) -> tuple[int, int]:
+        nr, warm = C.c_uint32(), C.c_uint32()
+        check(self.L.chk_pool_plan_reads(self._h, _u32(need), len(need), C.byref(nr), C.byref(warm)))
+        return nr.value, warm.value
+
+    def pool_finish(self, rids: Sequence[int]) -> None:
+        check(self.L.chk_pool_finish(self._h, _u32(rids), len(rids)))
+
+    def pool_addr(self, rid: int) -> int:
+        return self.L.chk_pool_addr(self._h, rid)
+
+    def pool_buf(self, rid: int) -> tuple[int, int]:
+        base, off = C.c_void_p(), C.c_uint64()
+        check(self.L.chk_pool_buf(self._h, rid, C.byref(base), C.byref(off)))
+        return base.value or 0, off.value
+
+    def pool_kind(self, rid: int) -> int:
+        return self.L.chk_pool_kind(self._h, rid)
+
+    def pool_set_kind(self, rid: int, kind: int) -> None:
+        check(self.L.chk_pool_set_kind(self._h, rid, kind))
+
+    def pool_store(self, kind: int) -> tuple[int, int]:
+        base, stride = C.c_void_p(), C.c_uint64()
+        check(self.L.chk_pool_store(self._h, kind, C.byref(base), C.byref(stride)))
+        return base.value or 0, stride.value
 
     def memory_stats(self) -> dict:
         m = ChkMemoryStats()
@@ -163,6 +270,45 @@ class Engine:
         ms, last = C.c_float(), C.c_uint32()
         check(self.L.chk_time_decode(self._h, first_token, steps, C.byref(ms), C.byref(last)))
         return ms.value, last.value
+
+
+class PrefixState:
+    """A sequence checkpoint (Gpu's PrefixState) held by the engine library."""
+
+    def __init__(self, eng: Engine, h: C.c_void_p):
+        self.eng = eng
+        self._h = h
+
+    @property
+    def pos(self) -> int:
+        return self.eng.L.chk_prefix_pos(self._h)
+
+    @property
+    def mtp_len(self) -> int:
+        return self.eng.L.chk_prefix_mtp_len(self._h)
+
+    @property
+    def tokens(self) -> list[int]:
+        n = self.eng.L.chk_prefix_tokens(self._h, None, 0)
+        out = (C.c_uint32 * max(n, 1))()
+        self.eng.L.chk_prefix_tokens(self._h, out, n)
+        return list(out[:n])
+
+    def region(self, i: int, n: int) -> np.ndarray:
+        out = np.empty(n, np.uint8)
+        check(self.eng.L.chk_prefix_read(self._h, i, out.ctypes.data, n))
+        return out
+
+    def free(self) -> None:
+        if self._h:
+            self.eng.L.chk_prefix_free(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
 
 
 class Decode:

@@ -27,6 +27,10 @@ extern "C" {
 #endif
 
 typedef struct ChkEngine ChkEngine;
+typedef struct ChkPrefixState ChkPrefixState;
+
+/* "no token" for optional token arguments (Option<u32>::None). */
+#define CHK_NO_TOKEN 0xffffffffu
 
 /* Last error message of this thread ("" if none). */
 const char* chk_last_error(void);
@@ -65,14 +69,37 @@ int chk_mtp_draft(ChkEngine* e, const uint32_t* next, uint32_t n, uint32_t chain
  * residual left by the last draft pass. */
 int chk_mtp_chain(ChkEngine* e, uint32_t draft, uint32_t* out);
 
-/* Gpu::prefill_chunk (gpu/prefill.rs:196-464): process tokens[0..n) as
+/* Gpu::prefill_chunk (gpu/prefill.rs:190-464): process tokens[0..n) as
  * prompt rows, commit them, and write the greedy next token (and, with an
- * MTP head, its first draft, else UINT32_MAX). */
-int chk_prefill_chunk(ChkEngine* e, const uint32_t* tokens, uint32_t n, uint32_t* next, uint32_t* draft);
+ * MTP head, its first draft, else CHK_NO_TOKEN).  `next_after` is the token
+ * that follows the chunk when the caller knows it (the next chunk's first
+ * token, runner.rs:124): the MTP head pairs it with the chunk's last row,
+ * else the trunk's greedy token (CHK_NO_TOKEN).  With all_logits every
+ * row's logits are kept for chk_pf_logits_row.  Afterwards no step is in
+ * flight (commit has nothing to keep) and logits_row(0) is the last row's. */
+int chk_prefill_chunk(ChkEngine* e, const uint32_t* tokens, uint32_t n, uint32_t next_after, int all_logits,
+                      uint32_t* next, uint32_t* draft);
 
-/* Gpu::logits_row / last_logits_row / mtp_logits_row (gpu.rs:601-624):
- * host copy of the logits of row r of the last step (vocab_size floats). */
+/* Gpu::prefill_release (gpu/prefill.rs:467-469): free the prefill scratch
+ * (reallocated by the next chunk). */
+void chk_prefill_release(ChkEngine* e);
+
+/* Gpu::prefill_rows_fit (prefill/allocation.rs:150-169): the largest chunk,
+ * at most min(max_t, 4096) rows, whose prefill scratch fits the device
+ * memory free now (errors when not even one row fits). */
+int chk_prefill_rows_fit(const ChkEngine* e, int all_logits, uint32_t* rows);
+
+/* Gpu::pf_logits_row (gpu/prefill.rs:496-507): row r of the last prefill
+ * chunk's logits (all-logits mode only; NULL + error otherwise). */
+const float* chk_pf_logits_row(ChkEngine* e, uint32_t r);
+
+/* Gpu::logits_row / logits / last_logits_row / mtp_logits_row
+ * (gpu.rs:601-624): host copy of the logits of row r of the last step
+ * (vocab_size floats); chk_logits is row 0; chk_last_logits_row is the row
+ * that holds the latest token's logits (rows - 1; 0 after a prefill). */
 const float* chk_logits_row(ChkEngine* e, uint32_t r);
+const float* chk_logits(ChkEngine* e);
+uint32_t chk_last_logits_row(const ChkEngine* e);
 const float* chk_mtp_logits_row(ChkEngine* e, uint32_t r);
 
 uint32_t chk_pos(const ChkEngine* e);
@@ -93,16 +120,67 @@ typedef struct ChkMemoryStats {
 } ChkMemoryStats;
 int chk_memory_stats(const ChkEngine* e, ChkMemoryStats* out);
 
+/* Gpu::allocated_gb (gpu.rs:626-628): device memory this engine holds, in
+ * decimal GB (units.rs:7). */
+double chk_allocated_gb(const ChkEngine* e);
+
+/* KV-cache occupancy (gpu.rs:630-690): bytes of the positional caches in
+ * use (trunk attention layers at pos, the MTP layer at its own length),
+ * their capacity at max_t, the ratio, and pos / max_t. */
+uint64_t chk_kv_cache_bytes(const ChkEngine* e);
+uint64_t chk_kv_cache_capacity(const ChkEngine* e);
+double chk_kv_cache_fullness(const ChkEngine* e);
+double chk_context_fullness(const ChkEngine* e);
+
+/* Gpu::reset_request / clear_profile (gpu/state.rs:232-263): reset the
+ * sequence and drop the profiling counters; the weights stay loaded. */
+int chk_reset_request(ChkEngine* e);
+int chk_clear_profile(ChkEngine* e);
+
+/* Sequence checkpoints (gpu/state.rs:85-230).  A checkpoint holds the
+ * position, the MTP cache length, the token history and a copy of every
+ * prefix region (DeltaNet state and conv history, q8 K/V rows and scales,
+ * index and block keys up to the length; the MTP layer's at its own
+ * length).  Copies stay in device memory.
+ *   chk_prefix_state_bytes  prefix_state_bytes (bytes a checkpoint now takes)
+ *   chk_state_bytes_at      state_bytes_at(pos, mtp_len)
+ *   chk_save_prefix         save_prefix: a new checkpoint (free it with chk_prefix_free)
+ *   chk_save_into           save_into: reuse *checkpoint's buffers (created when NULL)
+ *   chk_restore_prefix      restore_prefix: errors "prefix exceeds context" /
+ *                           "prefix state layout mismatch" / "prefix region mismatch" */
+uint64_t chk_prefix_state_bytes(const ChkEngine* e);
+uint64_t chk_state_bytes_at(const ChkEngine* e, uint32_t pos, uint32_t mtp_len);
+int chk_save_prefix(ChkEngine* e, ChkPrefixState** out);
+int chk_save_into(ChkEngine* e, ChkPrefixState** checkpoint);
+int chk_restore_prefix(ChkEngine* e, const ChkPrefixState* state);
+void chk_prefix_free(ChkPrefixState* state);
+uint32_t chk_prefix_pos(const ChkPrefixState* state);
+uint32_t chk_prefix_mtp_len(const ChkPrefixState* state);
+/* Copies min(cap, length) token ids; returns the history's length. */
+uint32_t chk_prefix_tokens(const ChkPrefixState* state, uint32_t* out, uint32_t cap);
+
 /* Expert-cache interface (residency::Pool, gpu/residency.rs:255-460) over
- * the all-resident HBM store: every record is a member, acquire never
- * needs a read, addr(rid) = base + rid * stride with the kind tag in bits
- * 62-63 (1 = Q3, 2 = Q2; residency.rs:437-451). */
+ * the all-resident HBM store: every record is a member from load on, so
+ * acquire(rids, step) never needs a read (n_need = 0), plan_reads plans no
+ * read (warm = n) and finish waits for nothing; addr(rid) = base + rid *
+ * stride with the kind tag in bits 62-63 (1 = Q3, 2 = Q2;
+ * residency.rs:437-451); buf(rid) = (store base, byte offset); every record
+ * has the store's kind (set_kind accepts only that kind); chk_pool_store
+ * gives the device store behind a kind (store_file, residency.rs:300-311;
+ * the low-bit store is attached at load time by ChkOptions.experts). */
 uint32_t chk_pool_slots(const ChkEngine* e);
+uint32_t chk_pool_budget(const ChkEngine* e);
 uint32_t chk_pool_resident(const ChkEngine* e);
 int chk_pool_is_member(const ChkEngine* e, uint32_t rid);
-uint32_t chk_pool_acquire(ChkEngine* e, const uint32_t* rids, uint32_t n, uint32_t* need);
+int chk_pool_acquire(ChkEngine* e, const uint32_t* rids, uint32_t n, uint64_t step, uint32_t* need,
+                     uint32_t* n_need);
+int chk_pool_plan_reads(const ChkEngine* e, const uint32_t* need, uint32_t n, uint32_t* n_reads, uint32_t* warm);
+int chk_pool_finish(ChkEngine* e, const uint32_t* rids, uint32_t n);
 uint64_t chk_pool_addr(const ChkEngine* e, uint32_t rid);
+int chk_pool_buf(const ChkEngine* e, uint32_t rid, void** base, uint64_t* offset);
 uint32_t chk_pool_kind(const ChkEngine* e, uint32_t rid);
+int chk_pool_set_kind(ChkEngine* e, uint32_t rid, uint32_t kind);
+int chk_pool_store(const ChkEngine* e, uint32_t kind, void** base, uint64_t* stride);
 uint64_t chk_pool_bytes(const ChkEngine* e);
 
 /* Per-step expert activity (gpu/activity.rs:110): routed ids of row r of

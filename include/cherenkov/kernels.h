@@ -131,6 +131,17 @@ int chk_layer_hyper(ChkEngine* e, uint32_t layer, uint32_t r, float* host);
 int chk_profile_kernel(ChkEngine* e, int kind);
 int chk_profile_read(ChkEngine* e, double* ms_total, uint64_t* launches, uint64_t* bytes);
 
+/* The device ranges of the prefix regions at (pos, mtp_len), in the order
+ * a checkpoint stores them: count receives their number, ptrs/bytes the
+ * first `cap`.  Test support for the checkpoint round trip (the reference
+ * test writes the regions directly, tests/unit/qwen4_exp/gpu/state.rs). */
+int chk_prefix_regions(const ChkEngine* e, uint32_t pos, uint32_t mtp_len, uint64_t* ptrs, uint64_t* bytes,
+                       uint32_t cap, uint32_t* count);
+/* Copy the first n bytes of a checkpoint's region i to host memory. */
+int chk_prefix_read(const ChkPrefixState* state, uint32_t i, void* host, uint64_t n);
+/* dst[i] = value for i < n bytes of device memory. */
+int chk_fill_u8(void* dst, uint32_t value, uint64_t n, void* stream);
+
 /* dst[i] = src[i], i < n (f32 device buffers): the library's plain copy
  * kernel, used to calibrate HBM byte counters (rocprofv3 FETCH_SIZE /
  * WRITE_SIZE) against a transfer of known size.  Profiling support, no

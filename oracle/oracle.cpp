@@ -1255,4 +1255,129 @@ int orc_expert_record(void* mp, uint32_t record_layer, uint32_t e, uint8_t* dst,
 
 uint64_t orc_record_stride(void* mp) { return ((OrcModel*)mp)->rec_stride; }
 
+// ---- weight overrides (the closed-form pins of tests/test_oracle.py) ----
+// Replace one tensor of the synthetic model with caller-given values of
+// the same shape, so a composed function can be run on special weights
+// whose result has a closed form.  `layer` selects the decoder layer
+// (num_hidden_layers: the MTP layer); model-level tensors ignore it.
+static HcW* hc_of(OrcModel* m, uint32_t layer, const std::string& grp) {
+    if (grp == "final") return &m->final_mixer;
+    if (grp == "mtp_mixer") return &m->mtp_mixer;
+    LayerW* L = layer_of(m, layer);
+    if (!L) return nullptr;
+    if (grp == "attn_hc") return &L->attn_hc;
+    if (grp == "mlp_hc") return &L->mlp_hc;
+    return nullptr;
+}
+
+static QStore* q4_of(OrcModel* m, uint32_t layer, const std::string& name) {
+    if (name == "embed") return &m->embed;
+    if (name == "lm_head") return &m->lm_head;
+    if (name == "mtp.fc_e") return &m->mtp_fc_e;
+    if (name == "mtp.fc_h") return &m->mtp_fc_h;
+    const size_t dot = name.find('.');
+    if (dot == std::string::npos) return nullptr;
+    const std::string grp = name.substr(0, dot), t = name.substr(dot + 1);
+    if (HcW* h = hc_of(m, layer, grp)) {
+        if (t == "down") return &h->down;
+        if (t == "up") return &h->up;
+        if (t == "inject") return h->has_inject ? &h->inject : nullptr;
+        return nullptr;
+    }
+    LayerW* L = layer_of(m, layer);
+    if (!L) return nullptr;
+    if (grp == "dn" && L->linear) {
+        if (t == "qkv") return &L->dn.qkv;
+        if (t == "z") return &L->dn.z;
+        if (t == "a") return &L->dn.a;
+        if (t == "b") return &L->dn.b;
+        if (t == "out") return &L->dn.out;
+    }
+    if (grp == "at" && !L->linear) {
+        if (t == "q") return &L->at.q;
+        if (t == "k") return &L->at.k;
+        if (t == "v") return &L->at.v;
+        if (t == "o") return &L->at.o;
+        if (t == "idx") return &L->at.idx;
+    }
+    if (grp == "moe") {
+        if (t == "sh_gate") return &L->moe.sh_gate;
+        if (t == "sh_up") return &L->moe.sh_up;
+        if (t == "sh_down") return &L->moe.sh_down;
+    }
+    return nullptr;
+}
+
+static std::vector<uint16_t>* bf16_of(OrcModel* m, uint32_t layer, const std::string& name) {
+    if (name == "mtp.enorm") return &m->mtp_enorm;
+    if (name == "mtp.hnorm") return &m->mtp_hnorm;
+    const size_t dot = name.find('.');
+    if (dot == std::string::npos) return nullptr;
+    const std::string grp = name.substr(0, dot), t = name.substr(dot + 1);
+    if (HcW* h = hc_of(m, layer, grp)) return t == "norm" ? &h->norm : nullptr;
+    LayerW* L = layer_of(m, layer);
+    if (!L) return nullptr;
+    if (grp == "dn" && L->linear) {
+        if (t == "conv") return &L->dn.conv;
+        if (t == "a_log") return &L->dn.a_log;
+        if (t == "dt_bias") return &L->dn.dt_bias;
+        if (t == "norm") return &L->dn.norm;
+    }
+    if (grp == "at" && !L->linear) {
+        if (t == "q_norm") return &L->at.q_norm;
+        if (t == "k_norm") return &L->at.k_norm;
+        if (t == "idx_q_norm") return &L->at.idx_q_norm;
+        if (t == "idx_k_norm") return &L->at.idx_k_norm;
+    }
+    if (grp == "moe") {
+        if (t == "router") return &L->moe.router;
+        if (t == "shared_gate") return &L->moe.shared_gate;
+    }
+    return nullptr;
+}
+
+int orc_set_q4(void* mp, uint32_t layer, const char* name, const uint32_t* w, const uint16_t* s, const uint16_t* b,
+               uint64_t n_words) {
+    OrcModel* m = (OrcModel*)mp;
+    QStore* q = q4_of(m, layer, name);
+    if (!q) {
+        g_err = std::string("no Q4 tensor ") + name;
+        return -1;
+    }
+    if (n_words != q->w.size()) {
+        g_err = std::string("shape mismatch for ") + name;
+        return -1;
+    }
+    std::copy(w, w + q->w.size(), q->w.begin());
+    std::copy(s, s + q->s.size(), q->s.begin());
+    std::copy(b, b + q->b.size(), q->b.begin());
+    return 0;
+}
+
+int orc_set_bf16(void* mp, uint32_t layer, const char* name, const uint16_t* v, uint64_t n) {
+    OrcModel* m = (OrcModel*)mp;
+    std::vector<uint16_t>* t = bf16_of(m, layer, name);
+    if (!t) {
+        g_err = std::string("no bf16 tensor ") + name;
+        return -1;
+    }
+    if (n != t->size()) {
+        g_err = std::string("shape mismatch for ") + name;
+        return -1;
+    }
+    std::copy(v, v + n, t->begin());
+    return 0;
+}
+
+int orc_set_record(void* mp, uint32_t record_layer, uint32_t e, const uint8_t* src, uint64_t n) {
+    OrcModel* m = (OrcModel*)mp;
+    if (n > m->rec_stride) {
+        g_err = "record larger than the stride";
+        return -1;
+    }
+    uint8_t* dst = const_cast<uint8_t*>(m->record(record_layer, e));
+    std::copy(src, src + n, dst);
+    return 0;
+}
+
 }  // extern "C"

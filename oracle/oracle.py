@@ -54,6 +54,9 @@ _SIGS = [
     ("orc_expert_record", i32, [P, u32, u32, P, u64]),
     ("orc_record_stride", u64, [P]),
     ("orc_qsa_pick", None, [P, u32, u32, u32, P, P]),
+    ("orc_set_q4", i32, [P, u32, C.c_char_p, P, P, P, u64]),
+    ("orc_set_bf16", i32, [P, u32, C.c_char_p, P, u64]),
+    ("orc_set_record", i32, [P, u32, u32, P, u64]),
 ]
 
 _lib = None
@@ -136,6 +139,22 @@ class OracleModel:
         out = np.empty(n, np.uint8)
         _check(self.L.orc_expert_record(self.h, layer, e, _p(out), n))
         return out
+
+    # ---- weight overrides: special weights for closed-form checks ----
+    def set_q4(self, layer: int, name: str, w: np.ndarray, s: np.ndarray, b: np.ndarray) -> None:
+        w = np.ascontiguousarray(w, dtype=np.uint32)
+        s = np.ascontiguousarray(s, dtype=np.uint16)
+        b = np.ascontiguousarray(b, dtype=np.uint16)
+        assert s.size == b.size == w.size // 8
+        _check(self.L.orc_set_q4(self.h, layer, name.encode(), _p(w), _p(s), _p(b), w.size))
+
+    def set_bf16(self, layer: int, name: str, v: np.ndarray) -> None:
+        v = np.ascontiguousarray(v, dtype=np.uint16)
+        _check(self.L.orc_set_bf16(self.h, layer, name.encode(), _p(v), v.size))
+
+    def set_record(self, record_layer: int, e: int, rec: np.ndarray) -> None:
+        rec = np.ascontiguousarray(rec, dtype=np.uint8)
+        _check(self.L.orc_set_record(self.h, record_layer, e, _p(rec), rec.size))
 
 
 class OracleState:

@@ -47,3 +47,28 @@ def test_python_signatures_match_headers():
     bound = {n for n, _, _ in abi.SIGNATURES}
     assert bound <= declared, f"bound but not declared: {sorted(bound - declared)}"
     assert declared <= bound, f"declared but not bound: {sorted(declared - bound)}"
+
+
+def test_load_validates_before_touching_the_device():
+    """Configs the kernels cannot run are refused by chk_engine_load before
+    any device call (so this runs without a GPU): hidden sizes above 2048
+    (one 32-input chunk per lane in the batch-1 expert kernels), PLE layers,
+    more than 3 drafts."""
+    if not abi.LIB_PATH.exists():
+        pytest.skip("libcherenkov.so not built (run __graft_entry__.build())")
+    from cherenkov_amd import presets
+
+    L = abi.lib()
+    cases = []
+    c = presets.tiny()
+    c.hidden_size = 2304
+    cases.append((c, abi.ChkOptions(4, 0, 64, 0), "hidden size must be at most 2048"))
+    c = presets.tiny()
+    cases.append((c, abi.ChkOptions(4, 4, 64, 0), "drafts must be 0..=3"))
+    c = presets.tiny()
+    cases.append((c, abi.ChkOptions(5, 0, 64, 0), "expert precision"))
+    for cfg, opt, msg in cases:
+        h = C.c_void_p()
+        rc = L.chk_engine_load(C.byref(cfg), C.byref(opt), C.byref(h))
+        assert rc != 0 and not h.value
+        assert msg in L.chk_last_error().decode()

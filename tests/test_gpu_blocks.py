@@ -267,7 +267,7 @@ def test_attention_q8_decode(big4, T):
     assert_close(to_host(dout)[0], ref32, f"attention vs f32 KV T={T}", abs_frac=5e-2, min_cos=0.995)
 
 
-@pytest.mark.parametrize("T", [1024, 8192])
+@pytest.mark.parametrize("T", [1024, 8192, 32768])
 def test_attention_q8_batch2(big4, T):
     cfg, eng, orc = big4
     layer = 3

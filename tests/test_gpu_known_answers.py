@@ -43,13 +43,13 @@ def test_lm_head_argmax_ties_partial_blocks(have_gpu, nb):
     in_dim = 2048  # every lane holds a chunk: -inf biases never meet a zero x sum
     x = np.ones((nb, in_dim), np.float32)
     x[1:] *= 2.0
-    lo, hi = bf16_bits(np.float32(-10.0 / in_dim))[()], bf16_bits(np.float32(3.5 / in_dim))[()]
+    lo, hi = int(bf16_bits(np.float32(-10.0 / in_dim))[0]), int(bf16_bits(np.float32(3.5 / in_dim))[0])
     cases = []
     bias = np.full(n, lo, np.uint16)
     bias[[5, 36, 4097, stride + 5]] = hi
     cases.append((bias, 5))
     bias = np.full(n, NEG_INF_BF16, np.uint16)
-    bias[n - 1] = bf16_bits(np.float32(-1.0 / in_dim))[()]
+    bias[n - 1] = int(bf16_bits(np.float32(-1.0 / in_dim))[0])
     cases.append((bias, n - 1))
     cases.append((np.full(n, NEG_INF_BF16, np.uint16), 0))
     for bias, want in cases:
