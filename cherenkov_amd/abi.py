@@ -144,6 +144,7 @@ SIGNATURES = [
     ("chk_q4_matvec", i32, [P, P, P, u32, u32, P, P, u32, P]),
     ("chk_q4_gemm", i32, [P, P, P, u32, u32, P, u32, P, P]),
     ("chk_lm_head_argmax", i32, [P, P, P, u32, u32, P, u32, P, P, P]),
+    ("chk_lm_head_argmax_noalloc", i32, [P, P, P, u32, u32, P, u32, P, P, P]),
     ("chk_attn_decode_q8", i32, [P, P, P, P, P, u32, u32, u32, u32, P, P]),
     ("chk_qsa_select", i32, [P, u32, u32, u32, P, P]),
     ("chk_dn_scan", i32, [P, P, P, P, P, u32, u32, u32, u32, u32, i32, P]),

@@ -43,6 +43,16 @@ int chk_q4_gemm(const void* w, const void* s, const void* b, uint32_t out, uint3
 int chk_lm_head_argmax(const void* w, const void* s, const void* b, uint32_t out, uint32_t in, const float* x,
                        uint32_t nb, float* logits, uint32_t* ids, void* stream);
 
+/* chk_lm_head_argmax without any allocation: no counterpart in the
+ * reference; for callers that cannot allocate device memory (code under
+ * graph capture, serving loops that forbid hipMalloc).  Same arguments and
+ * results; the argmax partials live in a 32 KiB file-scope device array of
+ * the library (nb <= 4 rows of 1024 workgroup partials), one per device,
+ * shared by every call on that device: calls that overlap on one device
+ * race. */
+int chk_lm_head_argmax_noalloc(const void* w, const void* s, const void* b, uint32_t out, uint32_t in,
+                               const float* x, uint32_t nb, float* logits, uint32_t* ids, void* stream);
+
 /* Flash-decode core over a q8 KV cache of T tokens (no projections, norms
  * or RoPE): q f32 [nh][2 hd] holds each head's [q | gate] (the q_proj row
  * order, cpu.rs:577-582); k, v int8 [T][nkv hd]; ks, vs fp16 [T][nkv hd/32];
