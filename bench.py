@@ -10,11 +10,14 @@ seeded random prompt: there is no checkpoint or dataset.
 
 Extra fields:
   roofline      — the dominant kernel's achieved algorithmic HBM bandwidth,
-                  timed live with HIP events on the engine's stream around a
-                  captured graph of its per-layer launches (the step's own
-                  arguments and inputs);
+                  timed live with HIP event pairs around each of its
+                  launches inside whole decode steps (the kernel as it runs
+                  in the step); the same kernel alone in a graph of its
+                  launches is reported beside it;
   cpu_baseline  — the C++ restatement of the reference's CPU forward
-                  (oracle/), token at a time, on a bounded sample;
+                  (oracle/), token at a time, decoding at the bench's
+                  context on a bounded sample, with the host's CPU model,
+                  NUMA placement and OMP_NUM_THREADS;
   decode_roofline — the whole step: tok/s x algorithmic bytes/token vs 8 TB/s.
 """
 
@@ -33,6 +36,7 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBPS = 8000.0
 PROMPT = 2048
 PROF_REPS = 4
+PROF_STEPS = 32
 PROF_KINDS = {1: "k_moe_gate_up (routed + shared experts gate/up)", 2: "k_qmv (DeltaNet in-projections)", 3: "k_lm_head (LM head + argmax partials)"}
 
 
@@ -53,16 +57,49 @@ def measured_traffic(kind: int):
     return None
 
 
-def cpu_baseline(cfg, tokens: list[int], timeout_s: float = 40.0) -> dict:
+def host_cpu() -> dict:
+    """The host the CPU baseline ran on: CPU model, logical CPUs, the CPUs
+    and NUMA memory nodes this process may use, and OMP_NUM_THREADS as set."""
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    allowed, mems = None, None
+    try:
+        for line in Path("/proc/self/status").read_text().splitlines():
+            if line.startswith("Cpus_allowed_list:"):
+                allowed = line.split(":", 1)[1].strip()
+            elif line.startswith("Mems_allowed_list:"):
+                mems = line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return {
+        "cpu_model": model,
+        "logical_cpus": os.cpu_count(),
+        "cpus_allowed": allowed,
+        "numa_mems_allowed": mems,
+        "numa_binding": "none (inherited affinity)",
+        "OMP_NUM_THREADS": os.environ.get("OMP_NUM_THREADS", "unset"),
+    }
+
+
+def cpu_baseline(cfg, tokens: list[int], context: int, timeout_s: float = 40.0) -> dict:
     """The oracle (C++ restatement of cpu.rs forward_token, OpenMP over
-    output rows) on this host: a first pass over `tokens` materialises the
-    routed-expert records they touch (the reference reads them from its
-    mmapped store), a second identical pass is timed."""
+    output rows) on this host, decoding at the bench's context: the state
+    jumps to `context` positions of seeded synthetic KV and DeltaNet state
+    (no compute), a first pass over `tokens` materialises the routed-expert
+    records they touch (the reference reads them from its mmapped store),
+    and a second identical pass from the same context is timed."""
     from oracle.oracle import OracleModel
 
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     orc = OracleModel(cfg)
     st = orc.new_state()
+    st.fill_prefix(context)
     t0 = time.time()
     n_warm = 0
     for t in tokens:
@@ -71,6 +108,7 @@ def cpu_baseline(cfg, tokens: list[int], timeout_s: float = 40.0) -> dict:
         if time.time() - t0 > timeout_s / 2:
             break
     st = orc.new_state()
+    st.fill_prefix(context)
     t1 = time.time()
     for t in tokens[:n_warm]:
         st.forward_token(t, True)
@@ -80,8 +118,10 @@ def cpu_baseline(cfg, tokens: list[int], timeout_s: float = 40.0) -> dict:
         "unit": "tok/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"full 48-layer model, forward_token over the first {n_warm} prompt tokens from position 0 "
-        f"(expert records pre-materialised by an untimed identical pass, bounded to ~{timeout_s / 2:.0f} s), {dt:.1f} s",
+        "sample": f"full 48-layer model, forward_token of {n_warm} tokens at positions {context}..{context + n_warm - 1} "
+        f"(the bench's decode context; the caches before it are seeded synthetic values), expert records "
+        f"pre-materialised by an untimed identical pass (bounded to ~{timeout_s / 2:.0f} s), {dt:.1f} s timed",
+        "host": host_cpu(),
     }
 
 
@@ -165,7 +205,7 @@ def main() -> int:
 
     assert torch.cuda.is_available(), "no GPU"
     cfg = presets.qwen3next_80b_shape(mtp=0)
-    ctx_cap = args.prompt + args.warmup + args.steps + 8
+    ctx_cap = args.prompt + args.warmup + args.steps + PROF_STEPS + 8
     t0 = time.time()
     eng = Engine(cfg, experts=args.experts, drafts=0, max_t=ctx_cap, no_eos=True)
     log(f"load {time.time() - t0:.1f}s mem {eng.memory_stats()['total'] / 1e9:.1f} GB")
@@ -194,18 +234,32 @@ def main() -> int:
     ms_step = dt * 1e3 / args.steps
     log(f"decode {args.steps} tokens in {dt:.3f}s ({tok_s:.1f} tok/s), {ms_step:.3f} ms/step")
 
-    # dominant kernel: HIP events on the engine stream around a captured
-    # graph of PROF_REPS rounds of its 48 per-layer launches (graph replay
-    # has the step's back-to-back launch spacing; events inside the step's
-    # own graph are not available)
+    # dominant kernel, in the step: PROF_STEPS more committed tokens after
+    # the timed region, each step's kernels launched in the same sequence
+    # (not from the graph: HIP event records are not timed inside captured
+    # graphs) with a HIP event pair around each launch of the kernel on the
+    # engine stream
     prof_kind = int(os.environ.get("CHK_BENCH_PROF", "1"))
-    prof_ms, prof_n, prof_bytes = eng.profile_graph(prof_kind, PROF_REPS)
+    eng.profile_kernel(prof_kind)
+    t0 = time.perf_counter()
+    for _ in range(PROF_STEPS):
+        tok = eng.step(tok)
+    torch.cuda.synchronize()
+    prof_step_ms = (time.perf_counter() - t0) * 1e3 / PROF_STEPS
+    prof_ms, prof_n, prof_bytes = eng.profile_read()
+    eng.profile_kernel(0)
+    # and alone: a graph of PROF_REPS rounds of its 48 per-layer launches
+    iso_ms, iso_n, iso_bytes = eng.profile_graph(prof_kind, PROF_REPS)
     ctx_mid = args.prompt + args.warmup + args.steps // 2
     bpt = presets.decode_bytes_per_token(cfg, ctx_mid, args.experts)
     step_gbps = tok_s * bpt / 1e9
     avg_launch_ms = prof_ms / max(prof_n, 1)
     bytes_per_launch = prof_bytes / max(prof_n, 1)
     achieved = bytes_per_launch / (avg_launch_ms * 1e-3) / 1e9 if prof_n else 0.0
+    iso_launch_ms = iso_ms / max(iso_n, 1)
+    iso_achieved = (iso_bytes / max(iso_n, 1)) / (iso_launch_ms * 1e-3) / 1e9 if iso_n else 0.0
+    log(f"{PROF_KINDS.get(prof_kind)}: in-step {avg_launch_ms * 1e3:.3f} us/launch ({achieved:.0f} GB/s, "
+        f"{prof_n} launches, profiled step {prof_step_ms:.3f} ms); alone {iso_launch_ms * 1e3:.3f} us")
 
     result = {
         "metric": "batch-1 decode tok/s, 80B-A3B-shape 4-bit qwen4_exp (48 layers, HBM-resident experts)",
@@ -243,7 +297,16 @@ def main() -> int:
             "bytes_per_launch": int(bytes_per_launch),
             "avg_launch_us": round(avg_launch_ms * 1e3, 3),
             "launches": prof_n,
-            "measured": f"HIP events around a captured graph of {PROF_REPS} x 48 per-layer launches after the timed region",
+            "measured": f"HIP event pairs on the engine stream around each of its launches inside {PROF_STEPS} "
+            f"committed decode steps after the timed region (the step's kernel sequence launched directly, "
+            f"{prof_step_ms:.3f} ms per profiled step)",
+            "isolated_graph": {
+                "avg_launch_us": round(iso_launch_ms * 1e3, 3),
+                "achieved": round(iso_achieved, 1),
+                "frac": round(iso_achieved / HBM_PEAK_GBPS, 4),
+                "launches": iso_n,
+                "measured": f"HIP events around a captured graph of {PROF_REPS} x 48 of its per-layer launches alone",
+            },
         },
         "decode_roofline": {
             "bytes_per_token": bpt,
@@ -259,7 +322,7 @@ def main() -> int:
         result["spec_decode"] = spec_decode(prompt, args.steps)
         log(f"spec decode (2 MTP drafts): {result['spec_decode']}")
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(cfg, prompt[:256])
+        result["cpu_baseline"] = cpu_baseline(cfg, prompt[:256], ctx_mid)
     print(json.dumps(result), flush=True)
     return 0
 

@@ -89,6 +89,8 @@ SIGNATURES = [
     ("chk_last_error", C.c_char_p, []),
     ("chk_engine_load", i32, [C.POINTER(ChkConfig), C.POINTER(ChkOptions), C.POINTER(P)]),
     ("chk_engine_free", None, [P]),
+    ("chk_engine_load_store", i32, [C.c_char_p, C.POINTER(ChkOptions), C.POINTER(P)]),
+    ("chk_store_config", i32, [C.c_char_p, C.POINTER(ChkConfig)]),
     ("chk_step_rows", i32, [P, C.POINTER(u32), u32, i32, i32, C.POINTER(u32)]),
     ("chk_step", i32, [P, u32, C.POINTER(u32)]),
     ("chk_commit", i32, [P, u32]),
@@ -168,6 +170,7 @@ SIGNATURES = [
     ("chk_copy_f32", i32, [P, P, u64, P]),
     ("chk_profile_graph", i32, [P, i32, u32, C.POINTER(C.c_double), C.POINTER(u64), C.POINTER(u64)]),
     ("chk_time_decode", i32, [P, u32, u32, C.POINTER(f32), C.POINTER(u32)]),
+    ("chk_phase_bench", i32, [i32, u32, u32, u64, C.POINTER(f64), C.POINTER(u32)]),
     # runner (decode loop)
     ("chk_decode_new", i32, [P, u32, C.POINTER(u32), u32, u32, u32, u32, C.POINTER(P)]),
     ("chk_decode_free", None, [P]),

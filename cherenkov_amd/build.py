@@ -32,8 +32,8 @@ FLAGS = [
     f"-I{ROOT / 'include'}",
     f"-I{CSRC}",
 ]
-SOURCES = ["gen.hip", "decode.hip", "attn.hip", "misc.hip", "prefill.hip", "dnscan.hip", "engine.cpp", "runner.cpp",
-           "noalloc.hip"]
+SOURCES = ["gen.hip", "decode.hip", "attn.hip", "misc.hip", "prefill.hip", "dnscan.hip", "engine.cpp", "runner.cpp", "store.cpp",
+           "noalloc.hip", "phasebench.hip"]
 
 
 def _compile(src: Path) -> Path:

@@ -1468,7 +1468,7 @@ void launch_router(const RouterArgs& a, int nb, hipStream_t st) {
     CHK_NB_SWITCH(nb, (k_router<R, NB><<<grid, 64, 0, st>>>(a)));
 }
 
-void launch_moe_gate_up(const MoeArgs& a, hipStream_t st) {
+void launch_moe_gate_up(const MoeArgs& a, hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop) {
     constexpr int RG = 32 / GU_WAVES;
     if (a.topk >= 64 || a.E > 512 || a.E % 8 || a.I % RG) throw std::runtime_error("routing too wide");
     const uint32_t tasks = a.nb * (a.topk + 1) * (a.I / RG);
@@ -1477,6 +1477,17 @@ void launch_moe_gate_up(const MoeArgs& a, hipStream_t st) {
     if (!a.act_xq) throw std::runtime_error("the gate/up kernel needs the act chunk buffer");
     const uint32_t grid = a.nb * (a.topk + 1) * (a.I / 32);  // one 32-row chunk per workgroup
     const size_t lds = xq_bytes(a.nb, a.H);
+    if (ev_start) {
+        // events recorded by the dispatch itself: the kernel's own start and end
+        const void* fn = a.X.bits == 3   ? (const void*)k_moe_gate_up<RG, 3>
+                         : a.X.bits == 2 ? (const void*)k_moe_gate_up<RG, 2>
+                                         : (const void*)k_moe_gate_up<RG, 4>;
+        MoeArgs arg = a;
+        void* args[] = {&arg};
+        const hipError_t e = hipExtLaunchKernel(fn, dim3(grid), dim3(GU_WG), args, lds, st, ev_start, ev_stop, 0);
+        if (e != hipSuccess) throw std::runtime_error(std::string("gate/up launch: ") + hipGetErrorString(e));
+        return;
+    }
     switch (a.X.bits) {
     case 3: k_moe_gate_up<RG, 3><<<grid, GU_WG, lds, st>>>(a); break;
     case 2: k_moe_gate_up<RG, 2><<<grid, GU_WG, lds, st>>>(a); break;

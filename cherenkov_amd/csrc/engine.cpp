@@ -18,9 +18,13 @@
 #include <string>
 #include <vector>
 
+#include <fcntl.h>
+#include <unistd.h>
+
 #include "cherenkov/engine.h"
 #include "cherenkov/kernels.h"
 #include "kernels_internal.h"
+#include "store.h"
 
 namespace chk {
 
@@ -189,9 +193,21 @@ struct ChkEngine {
     std::vector<float> host_logits, host_mtp_logits;
     uint32_t last_mtp_rows = 0;
     bool tracing = false;
-    // captured decode steps, keyed by rows * 2 + snap
-    std::map<int, hipGraphExec_t> graphs;
+    // captured decode steps, keyed by (rows * 2 + snap) * 4 + profiled
+    // kernel class; a profiled graph holds HIP event pairs around each
+    // launch of that class (graph-owned events [ev0, ev1) of graph_events)
+    struct StepGraph {
+        hipGraphExec_t exec;
+        size_t ev0, ev1;
+    };
+    std::map<int, StepGraph> graphs;
     bool use_graphs = true;
+    bool capturing = false;
+    struct EvPair {
+        hipEvent_t a, b;
+        uint64_t bytes;
+    };
+    std::vector<EvPair> graph_events;
     // folded MTP pass results of the last step (one draft per row)
     bool folded_valid = false;
     std::vector<uint32_t> folded;
@@ -202,8 +218,26 @@ struct ChkEngine {
     uint64_t prof_bytes = 0, prof_launches = 0;
     double prof_ms = 0.0;
 
+    // the next unused eager event pair (created on first use)
+    std::pair<hipEvent_t, hipEvent_t> prof_pair() {
+        if (prof_used == prof_events.size()) {
+            hipEvent_t a, b;
+            HIPCHK(hipEventCreate(&a));
+            HIPCHK(hipEventCreate(&b));
+            prof_events.push_back({a, b});
+        }
+        return prof_events[prof_used];
+    }
     void prof_begin(int kind) {
         if (prof_kind != kind) return;
+        if (capturing) {
+            EvPair ev{};
+            HIPCHK(hipEventCreate(&ev.a));
+            HIPCHK(hipEventCreate(&ev.b));
+            graph_events.push_back(ev);
+            HIPCHK(hipEventRecord(ev.a, st));
+            return;
+        }
         if (prof_used == prof_events.size()) {
             hipEvent_t a, b;
             HIPCHK(hipEventCreate(&a));
@@ -214,6 +248,11 @@ struct ChkEngine {
     }
     void prof_end(int kind, uint64_t bytes) {
         if (prof_kind != kind) return;
+        if (capturing) {
+            graph_events.back().bytes = bytes;
+            HIPCHK(hipEventRecord(graph_events.back().b, st));
+            return;
+        }
         HIPCHK(hipEventRecord(prof_events[prof_used].second, st));
         ++prof_used;
         prof_bytes += bytes;
@@ -229,6 +268,16 @@ struct ChkEngine {
         }
         prof_used = 0;
     }
+    // after a replay of a profiled graph has finished: its event pairs
+    void prof_collect_graph(const StepGraph& g) {
+        for (size_t i = g.ev0; i < g.ev1; ++i) {
+            float ms = 0;
+            HIPCHK(hipEventElapsedTime(&ms, graph_events[i].a, graph_events[i].b));
+            prof_ms += ms;
+            prof_bytes += graph_events[i].bytes;
+            ++prof_launches;
+        }
+    }
     uint64_t q4_bytes(const Q4Mat& m) const { return (uint64_t)m.out * m.in / 2 + 4ull * (m.out * (m.in / 64)); }
     uint64_t expert_mat_bytes() const {
         uint64_t codes = (uint64_t)D.I * D.H;
@@ -238,7 +287,14 @@ struct ChkEngine {
 
     ~ChkEngine() {
         if (st) hipStreamSynchronize(st);
-        for (auto& kv : graphs) hipGraphExecDestroy(kv.second);
+        for (auto& kv : graphs) hipGraphExecDestroy(kv.second.exec);
+        for (auto& ev : graph_events) {
+            hipEventDestroy(ev.a);
+            hipEventDestroy(ev.b);
+        }
+        if (staging) hipHostFree(staging);
+        if (dense_fd >= 0) close(dense_fd);
+        if (experts_fd >= 0) close(experts_fd);
         if (s.h_in) hipHostFree(s.h_in);
         if (s.h_out) hipHostFree(s.h_out);
         for (void* p : allocs) hipFree(p);
@@ -277,6 +333,39 @@ struct ChkEngine {
     bool is_linear(uint32_t l) const { return (l + 1) % c.full_attention_interval != 0; }
 
     // ------------------------------------------------------ store build
+    // Weights come from the seeded generator (synth.h), or, for an engine
+    // loaded from a packed store, from its dense.bin / experts.bin.
+    const Store* src = nullptr;
+    int dense_fd = -1, experts_fd = -1;
+    uint8_t* staging = nullptr;  // pinned host buffer for store uploads
+    static constexpr uint64_t STAGING = 64ull << 20;
+
+    // copy `n` bytes at `off` of an open store file to device memory
+    void upload(int fd, uint64_t off, uint64_t n, void* dst) {
+        uint8_t* d = static_cast<uint8_t*>(dst);
+        for (uint64_t done = 0; done < n;) {
+            const uint64_t m = std::min<uint64_t>(STAGING, n - done);
+            HIPCHK(hipStreamSynchronize(st));  // the staging buffer is free again
+            uint64_t got = 0;
+            while (got < m) {
+                const ssize_t r = pread(fd, staging + got, m - got, (off_t)(off + done + got));
+                ensure(r > 0, "short read of the packed store");
+                got += (uint64_t)r;
+            }
+            HIPCHK(hipMemcpyAsync(d + done, staging, m, hipMemcpyHostToDevice, st));
+            done += m;
+        }
+    }
+    const DenseEntry& store_entry(const std::string& name, const char* dtype, std::vector<uint64_t> shape) {
+        const DenseEntry& e = src->entry(name);
+        ensure(e.dtype == dtype, name + ": expected " + dtype + ", got " + e.dtype);
+        ensure(e.shape == shape, name + ": shape does not match the config");
+        uint64_t n = e.dtype == "U32" ? 4 : 2;
+        for (uint64_t x : shape) n *= x;
+        ensure(e.nbytes == n, name + ": byte count does not match its shape");
+        return e;
+    }
+
     Q4Mat q4(Bump& B, uint32_t kind, uint32_t slot, uint32_t part, uint32_t out, uint32_t in) {
         Q4Mat m{};
         m.out = out;
@@ -285,13 +374,68 @@ struct ChkEngine {
         uint16_t* s = B.take<uint16_t>((uint64_t)out * in / 64);
         uint16_t* b = B.take<uint16_t>((uint64_t)out * in / 64);
         m.w = w; m.s = s; m.b = b;
-        if (B.gen) gen_q4(w, s, b, out, in, c.seed, chk_tensor_id(kind, slot, 0, part), st);
+        if (B.gen && src) {
+            // Packed::qlinear (packed.rs:154-179): {prefix}.weight U32
+            // [out, in/8], .scales / .biases BF16 [out, in/64]
+            const std::string p = tensor_name(c, kind, slot, part);
+            const DenseEntry& ew = store_entry(p + ".weight", "U32", {out, in / 8});
+            const DenseEntry& es = store_entry(p + ".scales", "BF16", {out, in / 64});
+            const DenseEntry& eb = store_entry(p + ".biases", "BF16", {out, in / 64});
+            upload(dense_fd, ew.offset, ew.nbytes, w);
+            upload(dense_fd, es.offset, es.nbytes, s);
+            upload(dense_fd, eb.offset, eb.nbytes, b);
+        } else if (B.gen) {
+            gen_q4(w, s, b, out, in, c.seed, chk_tensor_id(kind, slot, 0, part), st);
+        }
         return m;
     }
     const uint16_t* bf(Bump& B, uint32_t kind, uint32_t slot, uint32_t part, uint64_t n) {
         uint16_t* p = B.take<uint16_t>(n);
-        if (B.gen) gen_bf16(p, n, c.seed, chk_tensor_id(kind, slot, 0, part), kind, st);
+        if (B.gen && src) {
+            const std::string name = tensor_name(c, kind, slot, part);
+            const DenseEntry& e = src->entry(name);
+            ensure(e.dtype == "BF16", name + ": expected BF16, got " + e.dtype);
+            ensure(e.nbytes == n * 2, name + ": element count does not match the config");
+            upload(dense_fd, e.offset, e.nbytes, p);
+        } else if (B.gen) {
+            gen_bf16(p, n, c.seed, chk_tensor_id(kind, slot, 0, part), kind, st);
+        }
         return p;
+    }
+    // experts.bin: record layer rl of this engine is the store's record
+    // layer of the same prefix (main layers in order, then the MTP layer,
+    // pack.rs:351-393); a record's fields move to this engine's layout
+    void upload_records() {
+        const StoreExperts& X = src->experts;
+        const bool same = X.record_stride == rl4.stride && X.gate_w == rl4.gate_w && X.up_w == rl4.up_w &&
+                          X.down_w == rl4.down_w && X.gate_s == rl4.gate_s && X.gate_b == rl4.gate_b &&
+                          X.up_s == rl4.up_s && X.up_b == rl4.up_b && X.down_s == rl4.down_s &&
+                          X.down_b == rl4.down_b;
+        for (uint32_t rl = 0; rl < record_layers; ++rl) {
+            const std::string want = rl < c.num_hidden_layers
+                                         ? "language_model.model.layers." + std::to_string(rl) + ".mlp.switch_mlp"
+                                         : std::string("mtp.layers.0.mlp.switch_mlp");
+            uint64_t idx = X.layers;
+            for (uint64_t i = 0; i < X.layers; ++i)
+                if (X.layer_prefixes[i] == want) idx = i;
+            ensure(idx < X.layers, "no expert records for " + want);
+            uint8_t* dst = experts4 + (uint64_t)rl * D.E * rl4.stride;
+            if (same) {
+                upload(experts_fd, idx * X.experts * X.record_stride, (uint64_t)D.E * rl4.stride, dst);
+                continue;
+            }
+            const uint64_t codes = (uint64_t)D.I * D.H / 2;
+            const uint64_t src_off[9] = {X.gate_w, X.up_w, X.down_w, X.gate_s, X.gate_b, X.up_s, X.up_b, X.down_s, X.down_b};
+            const uint64_t dst_off[9] = {rl4.gate_w, rl4.up_w, rl4.down_w, rl4.gate_s, rl4.gate_b,
+                                         rl4.up_s, rl4.up_b, rl4.down_s, rl4.down_b};
+            const uint64_t len[9] = {codes, codes, codes, rl4.scale_up, rl4.scale_up, rl4.scale_up, rl4.scale_up,
+                                     rl4.scale_down, rl4.scale_down};
+            for (uint32_t e = 0; e < D.E; ++e) {
+                const uint64_t rec = (idx * X.experts + e) * X.record_stride;
+                for (int k = 0; k < 9; ++k) upload(experts_fd, rec + src_off[k], len[k], dst + e * rl4.stride + dst_off[k]);
+            }
+        }
+        HIPCHK(hipStreamSynchronize(st));
     }
     HcDev hc(Bump& B, uint32_t slot, uint32_t part, bool inject) {
         HcDev w{};
@@ -470,6 +614,7 @@ struct ChkEngine {
         build_dense(dry);
         dense_bytes = dry.off;
         dense = dalloc<uint8_t>(dense_bytes);
+        if (src) HIPCHK(hipHostMalloc((void**)&staging, STAGING, hipHostMallocDefault));
         Bump B;
         B.base = dense;
         B.gen = true;
@@ -480,7 +625,8 @@ struct ChkEngine {
         rl4 = record_layout(4, D.H, D.I);
         uint64_t n_rec = (uint64_t)record_layers * D.E;
         experts4 = dalloc<uint8_t>(n_rec * rl4.stride);
-        gen_records(experts4, rl4, c.seed, D.E, 0, record_layers, D.H, D.I, st);
+        if (src) upload_records();
+        else gen_records(experts4, rl4, c.seed, D.E, 0, record_layers, D.H, D.I, st);
         if (o.experts != 4) {
             rllo = record_layout(o.experts, D.H, D.I);
             experts_lo = dalloc<uint8_t>(n_rec * rllo.stride);
@@ -569,6 +715,31 @@ struct ChkEngine {
         reset_state();
         HIPCHK(hipStreamSynchronize(st));
         HIPCHK(hipGetLastError());
+    }
+
+    // Gpu::load over a packed store (gpu/load.rs:8-19 with Packed::open):
+    // the config comes from the store's config.json, every weight from its
+    // dense.bin and experts.bin
+    void load_store(const std::string& dir, const ChkOptions* opt) {
+        std::unique_ptr<Store> S = open_store(dir);
+        dense_fd = open((S->dir + "/dense.bin").c_str(), O_RDONLY);
+        ensure(dense_fd >= 0, "opening " + S->dir + "/dense.bin");
+        experts_fd = open((S->dir + "/experts.bin").c_str(), O_RDONLY);
+        ensure(experts_fd >= 0, "opening " + S->dir + "/experts.bin");
+        src = S.get();
+        const ChkConfig cfg = S->cfg;
+        try {
+            load(&cfg, opt);
+        } catch (...) {
+            src = nullptr;
+            throw;
+        }
+        src = nullptr;
+        hipHostFree(staging);
+        staging = nullptr;
+        close(dense_fd);
+        close(experts_fd);
+        dense_fd = experts_fd = -1;
     }
 
     void reset_state() {
@@ -777,9 +948,16 @@ struct ChkEngine {
         r.H = D.H;
         launch_router(r, nb, st);
         const MoeArgs m = moe_args(L, route_slot, x, nb, hyper, inj, raw_out);
-        prof_begin(PROF_MOE);
-        launch_moe_gate_up(m, st);
-        prof_end(PROF_MOE, gate_up_bytes(L, nb));
+        if (prof_kind == PROF_MOE && !capturing) {
+            // timed by events its own dispatch records (start and end of the kernel)
+            std::pair<hipEvent_t, hipEvent_t> ev = prof_pair();
+            launch_moe_gate_up(m, st, ev.first, ev.second);
+            ++prof_used;
+            prof_bytes += gate_up_bytes(L, nb);
+            ++prof_launches;
+        } else {
+            launch_moe_gate_up(m, st);
+        }
         launch_moe_down(m, st);
     }
 
@@ -873,20 +1051,33 @@ struct ChkEngine {
         for (uint32_t i = 0; i < n; ++i) s.h_in->tokens[i] = toks[i];
         s.h_in->pos = pos;
         std::atomic_thread_fence(std::memory_order_seq_cst);
+        const StepGraph* replayed = nullptr;
         if (use_graphs && !tracing && prof_kind == PROF_NONE) {
-            const int key = (int)n * 2 + (snap ? 1 : 0);
+            const int key = ((int)n * 2 + (snap ? 1 : 0)) * 4 + prof_kind;
             auto it = graphs.find(key);
             if (it == graphs.end()) {
                 hipGraph_t g;
+                StepGraph sg{};
+                sg.ev0 = graph_events.size();
                 HIPCHK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-                run_rows((int)n, snap);
+                capturing = true;
+                try {
+                    run_rows((int)n, snap);
+                } catch (...) {
+                    capturing = false;
+                    hipGraph_t dead;
+                    (void)hipStreamEndCapture(st, &dead);
+                    throw;
+                }
+                capturing = false;
                 HIPCHK(hipStreamEndCapture(st, &g));
-                hipGraphExec_t ge;
-                HIPCHK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+                sg.ev1 = graph_events.size();
+                HIPCHK(hipGraphInstantiate(&sg.exec, g, nullptr, nullptr, 0));
                 HIPCHK(hipGraphDestroy(g));
-                it = graphs.emplace(key, ge).first;
+                it = graphs.emplace(key, sg).first;
             }
-            HIPCHK(hipGraphLaunch(it->second, st));
+            HIPCHK(hipGraphLaunch(it->second.exec, st));
+            replayed = &it->second;
         } else {
             run_rows((int)n, snap);
         }
@@ -903,6 +1094,7 @@ struct ChkEngine {
         HIPCHK(hipGetLastError());
         for (uint32_t i = 0; i < n; ++i) out[i] = s.h_out[i];
         prof_collect();
+        if (replayed && replayed->ev1 > replayed->ev0) prof_collect_graph(*replayed);
         if (fold) {
             folded_valid = true;
             last_mtp_rows = n;
@@ -1731,6 +1923,14 @@ int chk_engine_load(const ChkConfig* cfg, const ChkOptions* opt, ChkEngine** out
 }
 
 void chk_engine_free(ChkEngine* e) { delete e; }
+
+int chk_engine_load_store(const char* dir, const ChkOptions* opt, ChkEngine** out) {
+    *out = nullptr;
+    auto e = std::make_unique<ChkEngine>();
+    CHK_TRY(e->load_store(dir, opt); *out = e.release())
+}
+
+int chk_store_config(const char* dir, ChkConfig* out) { CHK_TRY(*out = chk::open_store(dir)->cfg) }
 
 int chk_step_rows(ChkEngine* e, const uint32_t* tokens, uint32_t n, int snap, int fold_mtp, uint32_t* out) {
     CHK_TRY(e->step_rows(tokens, n, snap != 0, fold_mtp != 0, out))

@@ -366,7 +366,10 @@ void launch_qmv(const SegArgs& a, int nb, hipStream_t st);
 void launch_qmv_inject(const InjArgs& a, int nb, hipStream_t st);
 void launch_dn_scan(const DnScanArgs& a, int nb, hipStream_t st);
 void launch_router(const RouterArgs& a, int nb, hipStream_t st);
-void launch_moe_gate_up(const MoeArgs& a, hipStream_t st);
+// ev_start / ev_stop (optional): HIP events the dispatch itself records at
+// the kernel's start and end (hipExtLaunchKernelGGL)
+void launch_moe_gate_up(const MoeArgs& a, hipStream_t st, hipEvent_t ev_start = nullptr,
+                        hipEvent_t ev_stop = nullptr);
 void launch_moe_down(const MoeArgs& a, hipStream_t st);
 void launch_lm_head(const Q4Mat& m, const float* x, float* logits, float* pv, uint32_t* pi, uint32_t nparts,
                     uint32_t* out, int nb, hipStream_t st);

@@ -33,6 +33,19 @@ class Engine:
         check(L.chk_engine_load(C.byref(cfg), C.byref(self.opt), C.byref(self._h)))
         self.L = L
 
+    @classmethod
+    def load_store(cls, path, experts: int = 4, drafts: int = 0, max_t: int = 2048,
+                   no_eos: bool = False) -> "Engine":
+        """Gpu::load over a packed store directory (chk_engine_load_store)."""
+        self = cls.__new__(cls)
+        self.opt = ChkOptions(experts, drafts, max_t, 1 if no_eos else 0)
+        self._h = C.c_void_p()
+        L = lib()
+        check(L.chk_engine_load_store(str(path).encode(), C.byref(self.opt), C.byref(self._h)))
+        self.cfg = store_config(path)
+        self.L = L
+        return self
+
     def close(self) -> None:
         if self._h:
             self.L.chk_engine_free(self._h)
@@ -270,6 +283,13 @@ class Engine:
         ms, last = C.c_float(), C.c_uint32()
         check(self.L.chk_time_decode(self._h, first_token, steps, C.byref(ms), C.byref(last)))
         return ms.value, last.value
+
+
+def store_config(path) -> ChkConfig:
+    """The ChkConfig of a packed store (chk_store_config: file reads only)."""
+    cfg = ChkConfig()
+    check(lib().chk_store_config(str(path).encode(), C.byref(cfg)))
+    return cfg
 
 
 class PrefixState:

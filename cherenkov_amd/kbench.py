@@ -9,6 +9,12 @@ synthetic inputs (conv rows ~ N(0, 0.05^2), decays U(0.3, 1), betas
 U(0, 1), zero state): the chunked form `--reps` times, then the sequential
 kernel twice.  Prints one line per pass with its wall time.
 
+phases: the cost of one dependent phase (chk_phase_bench): graph launch
+cadence, streaming launches, a persistent kernel's grid barrier with its
+weights streamed after or issued before it, and float-atomic throughput.
+
+    python3 -m cherenkov_amd.kbench phases --wgs 128 256 512 --mbytes 1.5 14
+
 attn: the q8 flash-decode core (chk_attn_decode_q8: partials + combine, no
 projections) at the 80B shape (16 query / 2 kv heads of 256) over a cache
 of each given length: int8 K/V uniform in [-127, 127], fp16 scales
@@ -66,17 +72,58 @@ def attn(ctxs, reps: int) -> None:
             print(f"attn ctx={T} wall_ms={1e3 * (time.perf_counter() - t0):.3f}", flush=True)
 
 
+PHASE_MODES = {
+    0: "graph of empty dependent launches",
+    1: "graph of dependent launches streaming weights",
+    2: "persistent kernel, grid barrier only",
+    3: "persistent kernel, barrier then weights",
+    4: "persistent kernel, next weights issued before the barrier",
+}
+
+
+def phases(wgs_list, mbytes_list, n: int) -> None:
+    """What one dependent phase costs (chk_phase_bench): launch cadence in a
+    graph, streaming launches, and a persistent kernel's grid barrier with
+    its weights streamed after it or issued before it; then float-atomic
+    throughput with and without contention."""
+    import ctypes as C
+
+    from .abi import check, lib
+
+    us, err = C.c_double(), C.c_uint32()
+    for wgs in wgs_list:
+        for mode in (0, 2):
+            check(lib().chk_phase_bench(mode, wgs, n, 0, C.byref(us), C.byref(err)))
+            print(f"phase mode={mode} wgs={wgs} mbytes=0 us_per_phase={us.value:.3f} errors={err.value}  # {PHASE_MODES[mode]}",
+                  flush=True)
+        for mb in mbytes_list:
+            for mode in (1, 3, 4):
+                check(lib().chk_phase_bench(mode, wgs, min(n, 400), int(mb * 1e6), C.byref(us), C.byref(err)))
+                print(f"phase mode={mode} wgs={wgs} mbytes={mb} us_per_phase={us.value:.3f} errors={err.value}  "
+                      f"# {PHASE_MODES[mode]}", flush=True)
+    for wgs, window, per_wg in ((256, 1 << 22, 1300), (256, 1300, 1300), (64, 1300, 1300), (256, 2048, 2048)):
+        check(lib().chk_phase_bench(5, wgs, window, per_wg * 4, C.byref(us), C.byref(err)))
+        n_at = wgs * per_wg
+        print(f"atomics wgs={wgs} adds_per_wg={per_wg} window={window} us={us.value:.3f} "
+              f"adds_per_us={n_at / us.value:.0f}", flush=True)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
-    ap.add_argument("case", choices=["dn_scan", "attn"])
+    ap.add_argument("case", choices=["dn_scan", "attn", "phases"])
+    ap.add_argument("--wgs", type=int, nargs="+", default=[256])
+    ap.add_argument("--mbytes", type=float, nargs="+", default=[1.5, 14.0])
+    ap.add_argument("--phases", type=int, default=2000)
     ap.add_argument("--rows", type=int, default=4096)
     ap.add_argument("--ctx", type=int, nargs="+", default=[1024, 8192, 32768])
     ap.add_argument("--reps", type=int, default=4)
     args = ap.parse_args()
     if args.case == "dn_scan":
         dn_scan(args.rows, args.reps)
-    else:
+    elif args.case == "attn":
         attn(args.ctx, args.reps)
+    else:
+        phases(args.wgs, args.mbytes, args.phases)
 
 
 if __name__ == "__main__":

@@ -1,0 +1,94 @@
+"""Summaries of rocprofv3 traces of bench.py (the tables under profiles/).
+
+    python3 -m cherenkov_amd.rocprof_summary steps <kernel_trace.csv> [first last]
+    python3 -m cherenkov_amd.rocprof_summary pmc <counter_collection.csv> <kernel-name-prefix>
+
+steps: splits the trace into decode steps (each from a `k_embed` to the
+following `k_argmax_final`) and prints kernels per step, kernel busy time
+per step and a per-kernel table (launches per step, average / minimum
+duration, time per step, share); `first last` restricts it to decode steps
+first..last (1-based, inclusive; negative counts from the end).
+
+pmc: the average of each counter over the dispatches of one kernel (e.g.
+FETCH_SIZE and WRITE_SIZE in KiB per dispatch).
+"""
+
+from __future__ import annotations
+
+import collections
+import csv
+import statistics
+import sys
+
+
+def _name(r: dict) -> str:
+    return r["Kernel_Name"].split("(")[0].replace("void ", "").replace("chk::", "")
+
+
+def steps(path: str, first: int | None = None, last: int | None = None) -> None:
+    rows = list(csv.DictReader(open(path)))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    found, cur = [], None
+    for r in rows:
+        n = _name(r)
+        if n == "k_embed":
+            cur = [r]
+        elif cur is not None:
+            cur.append(r)
+            if n == "k_argmax_final":
+                found.append(cur)
+                cur = None
+    if not found:
+        print("no decode steps in the trace")
+        return
+    total = len(found)
+    if first is not None:
+        lo = first - 1 if first > 0 else total + first
+        hi = last if last > 0 else total + last + 1
+        found = found[lo:hi]
+        print(f"decode steps {lo + 1}..{lo + len(found)} of {total}")
+    dur = lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+    per = collections.defaultdict(list)
+    busy, wall = [], []
+    for s in found:
+        b = 0.0
+        for r in s:
+            per[_name(r)].append(dur(r))
+            b += dur(r)
+        busy.append(b)
+        wall.append((int(s[-1]["End_Timestamp"]) - int(s[0]["Start_Timestamp"])) / 1e3)
+    ns = len(found)
+    tot = statistics.mean(busy)
+    print(f"decode steps: {ns}; kernels per step: {statistics.median(len(s) for s in found):.0f}; "
+          f"kernel busy per step {tot:.1f} us; median step wall {statistics.median(wall):.1f} us")
+    print()
+    print("| kernel | launches/step | avg us | min us | us/step | share |")
+    print("|---|---:|---:|---:|---:|---:|")
+    for k, v in sorted(per.items(), key=lambda kv: -sum(kv[1])):
+        print(f"| `{k}` | {len(v) / ns:.0f} | {statistics.mean(v):.2f} | {min(v):.2f} | {sum(v) / ns:.1f} | "
+              f"{100 * sum(v) / ns / tot:.1f}% |")
+
+
+def pmc(path: str, prefix: str) -> None:
+    vals = collections.defaultdict(list)
+    for r in csv.DictReader(open(path)):
+        if _name(r).startswith(prefix):
+            vals[r["Counter_Name"]].append(float(r["Counter_Value"]))
+    for k, v in sorted(vals.items()):
+        print(f"{prefix} {k}: dispatches {len(v)}, mean {statistics.mean(v):.1f}")
+
+
+def main() -> None:
+    if len(sys.argv) >= 5 and sys.argv[1] == "steps":
+        steps(sys.argv[2], int(sys.argv[3]), int(sys.argv[4]))
+    elif len(sys.argv) >= 3 and sys.argv[1] == "steps":
+        steps(sys.argv[2])
+    elif len(sys.argv) >= 4 and sys.argv[1] == "pmc":
+        pmc(sys.argv[2], sys.argv[3])
+    else:
+        print(__doc__)
+        sys.exit(2)
+
+
+if __name__ == "__main__":
+    main()

@@ -11,8 +11,7 @@
  *     the next mutating call on the same handle (gpu.rs:601-607);
  *   - tokens are u32 ids, rows are at most chk_trunk_rows() per step.
  * The weights are the seeded synthetic weights of synth.h, generated in HBM
- * at load time (the reference mmaps a packed checkpoint instead; see
- * INTEGRATION.md for how a packed-store loader plugs in).
+ * at load time (chk_engine_load), or a packed store's (chk_engine_load_store).
  */
 #ifndef CHERENKOV_ENGINE_H
 #define CHERENKOV_ENGINE_H
@@ -41,6 +40,20 @@ const char* chk_last_error(void);
  * and scratch for contexts of opt->max_t tokens and 1 + opt->drafts rows. */
 int chk_engine_load(const ChkConfig* cfg, const ChkOptions* opt, ChkEngine** out);
 void chk_engine_free(ChkEngine* e);
+
+/* Gpu::load over a packed store (gpu/load.rs:8-19 with Packed::open,
+ * packed.rs:66-100): `dir` holds manifest.json, dense.bin and experts.bin
+ * (or a packed/ subdirectory does) and config.json (beside them or in
+ * `dir`), in the reference's formats (manifest.rs:7-110, config.rs:93-122,
+ * pack.rs:351-393).  Every weight is read from the store into the same HBM
+ * layout chk_engine_load generates; a low-bit expert store (opt->experts 3
+ * or 2) is repacked on the device from the Q4 records.  Errors name the
+ * missing or mismatched tensor. */
+int chk_engine_load_store(const char* dir, const ChkOptions* opt, ChkEngine** out);
+
+/* The ChkConfig of a packed store's config.json after the manifest checks
+ * of chk_engine_load_store (file reads only, no device work). */
+int chk_store_config(const char* dir, ChkConfig* out);
 
 /* Gpu::step_rows (gpu/decode.rs:13-58): run tokens[0..n) at positions
  * pos.. as one batch, write the greedy argmax after each row to out[0..n).

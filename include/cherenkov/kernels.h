@@ -168,6 +168,28 @@ int chk_copy_f32(float* dst, const float* src, uint64_t n, void* stream);
 int chk_profile_graph(ChkEngine* e, int kind, uint32_t reps, double* ms_total, uint64_t* launches,
                       uint64_t* bytes);
 
+/* Phase-cost microbenchmarks (profiling support, no reference
+ * counterpart; csrc/phasebench.hip).  One dependent phase of `wgs`
+ * workgroups of 256 threads, `phases` times:
+ *   mode 0  captured graph of empty dependent launches;
+ *   mode 1  graph of launches that each read the previous one's output and
+ *           stream bytes_per_phase of weights;
+ *   mode 2  one cooperative kernel, a grid barrier per phase (per-workgroup
+ *           flags, relaxed system-scope atomics) and data exchanged at
+ *           system scope;
+ *   mode 3  mode 2 + each phase streams its weights after the barrier;
+ *   mode 4  mode 2 + the next phase's weights issued before the wait;
+ *           (modes 3-4 hold at most 16 uint4 = 256 B per thread per phase)
+ *   mode 5  float atomicAdd without return: wgs workgroups x
+ *           bytes_per_phase / 4 adds over a window of `phases` addresses;
+ *           us_per_phase = microseconds per launch.
+ * us_per_phase receives the time per phase (modes 2-4: the slope between
+ * a quarter-length and a full-length run); errors counts values read back
+ * wrong across workgroups (+1e6 if a barrier gave up: every spin is
+ * bounded). */
+int chk_phase_bench(int mode, uint32_t wgs, uint32_t phases, uint64_t bytes_per_phase, double* us_per_phase,
+                    uint32_t* errors);
+
 /* Time the decode step on the engine's stream: runs `steps` step_rows(1)
  * + commit pairs, returns milliseconds per step (HIP events). */
 int chk_time_decode(ChkEngine* e, uint32_t first_token, uint32_t steps, float* ms_per_step, uint32_t* last_token);

@@ -989,6 +989,40 @@ void* orc_state_new(void* mp) {
 
 void orc_state_free(void* s) { delete (OrcState*)s; }
 
+// A synthetic sequence of n positions for timing decode at a long context
+// (the CPU baseline of bench.py): every attention cache gets n rows of
+// seeded N(0, 1) keys, values and index keys, the DeltaNet states small
+// seeded values; no tokens are run.  Not a parity path.
+int orc_state_fill_prefix(void* mp, void* sp, uint32_t n, uint64_t seed) {
+    OrcModel* m = (OrcModel*)mp;
+    OrcState* st = (OrcState*)sp;
+    const ChkConfig& c = m->c;
+    const size_t kv_row = (size_t)c.num_key_value_heads * c.head_dim;
+    uint64_t key = chk_key(seed, 0x5eed, CHK_STREAM_S);
+    uint64_t i = 0;
+    auto next = [&](float sigma) { return chk_bf16_to_f32(chk_normal_bf16(key, i++, sigma)); };
+    for (auto& kv : st->kv) {
+        kv.k.resize(n * kv_row);
+        kv.v.resize(n * kv_row);
+        kv.index_k.resize((size_t)n * c.indexer_head_dim);
+        for (auto& x : kv.k) x = next(1.0f);
+        for (auto& x : kv.v) x = next(1.0f);
+        for (auto& x : kv.index_k) x = next(1.0f);
+        kv.len = n;
+    }
+    if (m->has_mtp) {
+        st->mtp_kv.k.assign(n * kv_row, 0.0f);
+        st->mtp_kv.v.assign(n * kv_row, 0.0f);
+        st->mtp_kv.index_k.assign((size_t)n * c.indexer_head_dim, 0.0f);
+        st->mtp_kv.len = n;
+    }
+    for (auto& d : st->delta)
+        for (auto& x : d.s) x = next(0.01f);
+    st->pos = n;
+    st->tokens.assign(n, 0);
+    return 0;
+}
+
 uint32_t orc_state_pos(void* s) { return (uint32_t)((OrcState*)s)->pos; }
 
 // CpuModel::forward_token, src/qwen4_exp/cpu.rs:392-456.  `kv_q8` selects
@@ -1366,6 +1400,31 @@ int orc_set_bf16(void* mp, uint32_t layer, const char* name, const uint16_t* v, 
         return -1;
     }
     std::copy(v, v + n, t->begin());
+    return 0;
+}
+
+// Read one tensor back (the packed-store writer of the tests).
+int orc_get_q4(void* mp, uint32_t layer, const char* name, uint32_t* w, uint16_t* s, uint16_t* b, uint64_t n_words) {
+    OrcModel* m = (OrcModel*)mp;
+    QStore* q = q4_of(m, layer, name);
+    if (!q || n_words != q->w.size()) {
+        g_err = std::string("no Q4 tensor of that shape: ") + name;
+        return -1;
+    }
+    std::copy(q->w.begin(), q->w.end(), w);
+    std::copy(q->s.begin(), q->s.end(), s);
+    std::copy(q->b.begin(), q->b.end(), b);
+    return 0;
+}
+
+int orc_get_bf16(void* mp, uint32_t layer, const char* name, uint16_t* v, uint64_t n) {
+    OrcModel* m = (OrcModel*)mp;
+    std::vector<uint16_t>* t = bf16_of(m, layer, name);
+    if (!t || n != t->size()) {
+        g_err = std::string("no bf16 tensor of that size: ") + name;
+        return -1;
+    }
+    std::copy(t->begin(), t->end(), v);
     return 0;
 }
 

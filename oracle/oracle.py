@@ -54,9 +54,12 @@ _SIGS = [
     ("orc_expert_record", i32, [P, u32, u32, P, u64]),
     ("orc_record_stride", u64, [P]),
     ("orc_qsa_pick", None, [P, u32, u32, u32, P, P]),
+    ("orc_state_fill_prefix", i32, [P, P, u32, u64]),
     ("orc_set_q4", i32, [P, u32, C.c_char_p, P, P, P, u64]),
     ("orc_set_bf16", i32, [P, u32, C.c_char_p, P, u64]),
     ("orc_set_record", i32, [P, u32, u32, P, u64]),
+    ("orc_get_q4", i32, [P, u32, C.c_char_p, P, P, P, u64]),
+    ("orc_get_bf16", i32, [P, u32, C.c_char_p, P, u64]),
 ]
 
 _lib = None
@@ -152,6 +155,18 @@ class OracleModel:
         v = np.ascontiguousarray(v, dtype=np.uint16)
         _check(self.L.orc_set_bf16(self.h, layer, name.encode(), _p(v), v.size))
 
+    def get_q4(self, layer: int, name: str, out_dim: int, in_dim: int):
+        w = np.empty((out_dim, in_dim // 8), np.uint32)
+        s = np.empty((out_dim, in_dim // 64), np.uint16)
+        b = np.empty((out_dim, in_dim // 64), np.uint16)
+        _check(self.L.orc_get_q4(self.h, layer, name.encode(), _p(w), _p(s), _p(b), w.size))
+        return w, s, b
+
+    def get_bf16(self, layer: int, name: str, n: int) -> np.ndarray:
+        v = np.empty(n, np.uint16)
+        _check(self.L.orc_get_bf16(self.h, layer, name.encode(), _p(v), n))
+        return v
+
     def set_record(self, record_layer: int, e: int, rec: np.ndarray) -> None:
         rec = np.ascontiguousarray(rec, dtype=np.uint8)
         _check(self.L.orc_set_record(self.h, record_layer, e, _p(rec), rec.size))
@@ -176,6 +191,10 @@ class OracleState:
         out = np.empty(self.m.cfg.vocab_size, np.float32)
         _check(self.m.L.orc_forward_token(self.m.h, self.h, token, int(kv_q8), _p(out)))
         return out
+
+    def fill_prefix(self, n: int, seed: int = 1) -> None:
+        """Jump to position n with seeded synthetic caches (timing only)."""
+        _check(self.m.L.orc_state_fill_prefix(self.m.h, self.h, n, seed))
 
     def last_hyper(self) -> np.ndarray:
         c = self.m.cfg

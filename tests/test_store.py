@@ -1,0 +1,78 @@
+"""The packed-store reader without a GPU: a store written in the
+reference's format (tests/store_writer.py: config.json, manifest.json,
+dense.bin, experts.bin) yields the model's ChkConfig through
+chk_store_config, and malformed stores are refused with the reference's
+messages (manifest.rs:67-110, config.rs:93-122, packed.rs:75-90)."""
+
+from __future__ import annotations
+
+import ctypes as C
+import json
+
+import pytest
+
+from cherenkov_amd import abi, presets
+from tests.store_writer import write_store
+
+
+def store_config(path):
+    cfg = abi.ChkConfig()
+    rc = abi.lib().chk_store_config(str(path).encode(), C.byref(cfg))
+    return rc, cfg, abi.lib().chk_last_error().decode()
+
+
+@pytest.fixture(scope="module")
+def tiny_store(tmp_path_factory):
+    if not abi.LIB_PATH.exists():
+        pytest.skip("libcherenkov.so not built")
+    cfg = presets.tiny(mtp=1)
+    return cfg, write_store(cfg, tmp_path_factory.mktemp("store") / "packed")
+
+
+def test_store_config_matches_the_model(tiny_store):
+    cfg, path = tiny_store
+    rc, got, err = store_config(path)
+    assert rc == 0, err
+    for k, _ in cfg._fields_:
+        if k != "seed":
+            assert getattr(got, k) == getattr(cfg, k), k
+    # a model directory whose packed files sit in packed/ works the same
+    rc, got2, err = store_config(path.parent)
+    assert rc == 0, err
+    assert got2.hidden_size == cfg.hidden_size
+
+
+def _edit(path, fname, fn):
+    p = path / fname
+    d = json.loads(p.read_text())
+    fn(d)
+    p.write_text(json.dumps(d))
+
+
+@pytest.mark.parametrize("case,msg", [
+    ("version", "unsupported packed layout version 2"),
+    ("group", "expert group size must be 64"),
+    ("prefixes", "expert layer count does not match layer prefixes"),
+    ("mtp_records", "no expert records for mtp.layers.0.mlp.switch_mlp"),
+    ("model_type", "unsupported model_type llama"),
+    ("layer_types", "layer_types length mismatch"),
+    ("gate", "output_gate_type must be sigmoid"),
+])
+def test_malformed_stores_are_refused(tmp_path, case, msg):
+    if not abi.LIB_PATH.exists():
+        pytest.skip("libcherenkov.so not built")
+    cfg = presets.tiny(mtp=1, layers=4)
+    path = write_store(cfg, tmp_path / "s")
+    edits = {
+        "version": ("manifest.json", lambda d: d.update(version=2)),
+        "group": ("manifest.json", lambda d: d["experts"].update(group=32)),
+        "prefixes": ("manifest.json", lambda d: d["experts"]["layer_prefixes"].pop()),
+        "mtp_records": ("manifest.json", lambda d: (d["experts"]["layer_prefixes"].__setitem__(-1, "mtp.layers.1.x"))),
+        "model_type": ("config.json", lambda d: d.update(model_type="llama")),
+        "layer_types": ("config.json", lambda d: d["text_config"]["layer_types"].pop()),
+        "gate": ("config.json", lambda d: d["text_config"].update(output_gate_type="silu")),
+    }
+    fname, fn = edits[case]
+    _edit(path, fname, fn)
+    rc, _, err = store_config(path)
+    assert rc != 0 and msg in err, err
