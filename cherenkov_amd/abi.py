@@ -74,6 +74,18 @@ class ChkMemoryStats(C.Structure):
     ]
 
 
+class ChkSampling(C.Structure):
+    _fields_ = [
+        ("temperature", f64),
+        ("top_p", f64),
+        ("top_k", u32),
+        ("has_seed", u32),
+        ("seed", u64),
+        ("presence_penalty", f64),
+        ("frequency_penalty", f64),
+    ]
+
+
 def make_config(**kw) -> ChkConfig:
     c = ChkConfig()
     for k, v in kw.items():
@@ -107,6 +119,7 @@ SIGNATURES = [
     ("chk_mtp_logits_row", C.POINTER(f32), [P, u32]),
     ("chk_pos", u32, [P]),
     ("chk_eos_token", u32, [P]),
+    ("chk_vocab_size", u32, [P]),
     ("chk_max_t", u32, [P]),
     ("chk_trunk_rows", u32, [P]),
     ("chk_has_mtp", i32, [P]),
@@ -171,8 +184,20 @@ SIGNATURES = [
     ("chk_profile_graph", i32, [P, i32, u32, C.POINTER(C.c_double), C.POINTER(u64), C.POINTER(u64)]),
     ("chk_time_decode", i32, [P, u32, u32, C.POINTER(f32), C.POINTER(u32)]),
     ("chk_phase_bench", i32, [i32, u32, u32, u64, C.POINTER(f64), C.POINTER(u32)]),
+    # sampling
+    ("chk_sampling_validate", i32, [C.POINTER(ChkSampling)]),
+    ("chk_sampling_greedy", i32, [C.POINTER(ChkSampling)]),
+    ("chk_sampler_new", i32, [C.POINTER(ChkSampling), C.POINTER(u32), u32, u32, C.POINTER(P)]),
+    ("chk_sampler_free", None, [P]),
+    ("chk_sampler_accept", i32, [P, u32]),
+    ("chk_sampler_sample", i32, [P, C.POINTER(f32), u32, C.POINTER(u32)]),
+    ("chk_rng_u64", i32, [C.c_char_p, u64, C.POINTER(u64), u32]),
+    ("chk_pcg32", None, [u64, u64, C.POINTER(u32), u32]),
+    ("chk_chacha_block", None, [C.POINTER(u32), i32, C.POINTER(u32)]),
     # runner (decode loop)
     ("chk_decode_new", i32, [P, u32, C.POINTER(u32), u32, u32, u32, u32, C.POINTER(P)]),
+    ("chk_decode_new_sampling", i32, [P, C.POINTER(ChkSampling), C.POINTER(u32), u32, C.POINTER(f32), u32,
+                                      C.POINTER(u32), u32, u32, u32, u32, C.POINTER(P)]),
     ("chk_decode_free", None, [P]),
     ("chk_decode_step", i32, [P, C.POINTER(u32), C.POINTER(u32)]),
     ("chk_decode_finished", i32, [P]),

@@ -2025,6 +2025,7 @@ const float* chk_mtp_logits_row(ChkEngine* e, uint32_t r) {
 
 uint32_t chk_pos(const ChkEngine* e) { return e->pos; }
 uint32_t chk_eos_token(const ChkEngine* e) { return e->c.eos_token_id; }
+uint32_t chk_vocab_size(const ChkEngine* e) { return e->c.vocab_size; }
 uint32_t chk_max_t(const ChkEngine* e) { return e->max_t; }
 uint32_t chk_trunk_rows(const ChkEngine* e) { return e->trunk_rows; }
 int chk_has_mtp(const ChkEngine* e) { return e->has_mtp ? 1 : 0; }

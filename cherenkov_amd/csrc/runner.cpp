@@ -1,12 +1,16 @@
-// Greedy decode loop: the reference runner's `Decode` (/root/reference/
+// Decode loop: the reference runner's `Decode` (/root/reference/
 // src/runner/decode.rs:6-171) over the engine ABI.  Rows are the current
 // token plus the MTP drafts; the longest prefix of drafts that matches the
 // trunk's own greedy predictions is accepted, the step is committed to
 // that length (rolling the recurrent state back), and new drafts are
-// chained from the MTP head (one after a rejection, else n_draft).
+// chained from the MTP head (one after a rejection, else n_draft).  With
+// non-greedy sampling options there are no drafts: each step runs the
+// current token alone and the request's sampler draws the next one from
+// that row's logits.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <memory>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -28,6 +32,9 @@ struct ChkDecode {
     std::vector<uint32_t> tokens;
     int finish = 0;  // 0 running, 1 stop, 2 length
     uint32_t steps = 0, accepted = 0;
+    ChkSampler* sampler = nullptr;  // owned; null when greedy
+
+    ~ChkDecode() { chk_sampler_free(sampler); }
 
     bool is_eos(uint32_t t) const { return use_eos && t == eos; }
 
@@ -35,7 +42,14 @@ struct ChkDecode {
         if (rc != 0) throw std::runtime_error(chk_last_error());
     }
 
-    // Decode::step (decode.rs:88-171), greedy sampler only.
+    // Decode::emit (decode.rs:76-84)
+    void emit(uint32_t t, std::vector<uint32_t>& emitted) {
+        tokens.push_back(t);
+        if (sampler) check(chk_sampler_accept(sampler, t));
+        emitted.push_back(t);
+    }
+
+    // Decode::step (decode.rs:88-171)
     void step(std::vector<uint32_t>& emitted) {
         emitted.clear();
         if (finish) return;
@@ -51,8 +65,7 @@ struct ChkDecode {
         uint32_t remaining = limit - (uint32_t)tokens.size() - 1;
         for (uint32_t i = 0; i < std::min<uint32_t>(n_draft, remaining) && i < drafts.size(); ++i)
             rows.push_back(drafts[i]);
-        tokens.push_back(cur);
-        emitted.push_back(cur);
+        emit(cur, emitted);
         std::vector<uint32_t> result(rows.size());
         check(chk_step_rows(e, rows.data(), (uint32_t)rows.size(), rows.size() > 1, n_draft > 0, result.data()));
         uint32_t n = 1;
@@ -69,15 +82,18 @@ struct ChkDecode {
             check(chk_mtp_draft(e, next.data(), (uint32_t)next.size(), chain, d.data(), &nd));
             drafts.assign(d.begin(), d.begin() + nd);
         }
-        for (uint32_t i = 1; i < n; ++i) {
-            tokens.push_back(rows[i]);
-            emitted.push_back(rows[i]);
-        }
+        for (uint32_t i = 1; i < n; ++i) emit(rows[i], emitted);
         if (tokens.size() == limit) {
             finish = 2;
             return;
         }
-        cur = result[n - 1];
+        if (sampler) {
+            const float* l = chk_logits_row(e, n - 1);
+            if (!l) throw std::runtime_error(chk_last_error());
+            check(chk_sampler_sample(sampler, l, chk_vocab_size(e), &cur));
+        } else {
+            cur = result[n - 1];
+        }
     }
 };
 
@@ -89,16 +105,39 @@ extern "C" {
 // generation unless no_eos.
 int chk_decode_new(ChkEngine* e, uint32_t next, const uint32_t* drafts, uint32_t n_drafts, uint32_t n_draft,
                    uint32_t limit, uint32_t no_eos, ChkDecode** out) {
+    ChkSampling greedy{};
+    greedy.top_p = 1.0;
+    return chk_decode_new_sampling(e, &greedy, nullptr, 0, nullptr, next, drafts, n_drafts, n_draft, limit, no_eos,
+                                   out);
+}
+
+// Decode::new with the request's sampling options: greedy options keep the
+// prefill's token and drafts; otherwise the sampler (counts from the
+// prompt) draws the first token from the prompt's final logits and the
+// effective draft count is 0 (options.rs:165-171).
+int chk_decode_new_sampling(ChkEngine* e, const ChkSampling* sampling, const uint32_t* prompt, uint32_t n_prompt,
+                            const float* final_logits, uint32_t next, const uint32_t* drafts, uint32_t n_drafts,
+                            uint32_t n_draft, uint32_t limit, uint32_t no_eos, ChkDecode** out) {
+    *out = nullptr;
     try {
-        auto d = new ChkDecode();
+        std::unique_ptr<ChkDecode> d(new ChkDecode());
         d->e = e;
-        d->cur = next;
-        d->drafts.assign(drafts, drafts + n_drafts);
-        d->n_draft = n_draft;
         d->limit = limit;
         d->use_eos = no_eos == 0;
         d->eos = chk_eos_token(e);
-        *out = d;
+        if (chk_sampling_greedy(sampling)) {
+            ChkDecode::check(chk_sampling_validate(sampling));
+            d->cur = next;
+            d->drafts.assign(drafts, drafts + n_drafts);
+            d->n_draft = n_draft;
+        } else {
+            const uint32_t vocab = final_logits ? chk_vocab_size(e) : 0;
+            ChkDecode::check(chk_sampler_new(sampling, prompt, n_prompt, vocab, &d->sampler));
+            if (!final_logits) throw std::runtime_error("sampling needs final prompt logits");
+            ChkDecode::check(chk_sampler_sample(d->sampler, final_logits, vocab, &d->cur));
+            d->n_draft = 0;
+        }
+        *out = d.release();
         return 0;
     } catch (const std::exception& ex) {
         g_runner_err = ex.what();

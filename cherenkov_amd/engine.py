@@ -332,13 +332,31 @@ class PrefixState:
 
 
 class Decode:
-    """The runner's greedy speculative decode loop (native, runner.cpp)."""
+    """The runner's decode loop (native, runner.cpp; decode.rs:6-171).
 
-    def __init__(self, eng: Engine, nxt: int, drafts: Iterable[int], n_draft: int, limit: int, no_eos: bool = True):
+    Greedy options (the default) verify MTP drafts against the trunk's
+    argmax.  Other sampling options draw each token from the request's
+    sampler: the first from `final_logits` (the prompt's last-row logits),
+    the sampler's counts starting from `prompt`, and no drafts."""
+
+    def __init__(self, eng: Engine, nxt: int, drafts: Iterable[int], n_draft: int, limit: int, no_eos: bool = True,
+                 sampling=None, prompt: Sequence[int] = (), final_logits=None):
         self.eng = eng
         dl = list(drafts)
         self._h = C.c_void_p()
-        check(eng.L.chk_decode_new(eng.handle, nxt, _u32(dl), len(dl), n_draft, limit, int(no_eos), C.byref(self._h)))
+        if sampling is None:
+            rc = eng.L.chk_decode_new(eng.handle, nxt, _u32(dl), len(dl), n_draft, limit, int(no_eos),
+                                      C.byref(self._h))
+        else:
+            self._opts = sampling.native()
+            fl = None
+            if final_logits is not None:
+                self._fl = np.ascontiguousarray(final_logits, dtype=np.float32)
+                fl = self._fl.ctypes.data_as(C.POINTER(C.c_float))
+            rc = eng.L.chk_decode_new_sampling(eng.handle, C.byref(self._opts), _u32(list(prompt)), len(prompt), fl,
+                                               nxt, _u32(dl), len(dl), n_draft, limit, int(no_eos), C.byref(self._h))
+        if rc != 0:
+            raise EngineError(eng.L.chk_decode_error().decode())
 
     def step(self) -> list[int]:
         em = (C.c_uint32 * 4)()

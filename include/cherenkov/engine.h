@@ -117,6 +117,7 @@ const float* chk_mtp_logits_row(ChkEngine* e, uint32_t r);
 
 uint32_t chk_pos(const ChkEngine* e);
 uint32_t chk_eos_token(const ChkEngine* e);
+uint32_t chk_vocab_size(const ChkEngine* e);
 uint32_t chk_max_t(const ChkEngine* e);
 uint32_t chk_trunk_rows(const ChkEngine* e);
 int chk_has_mtp(const ChkEngine* e);
@@ -205,6 +206,46 @@ int chk_last_routes(const ChkEngine* e, uint32_t layer, uint32_t r, uint32_t* id
  * counterpart beyond activity.rs, whose per-expert counts come from it). */
 int chk_last_probs(const ChkEngine* e, uint32_t layer, uint32_t r, float* probs);
 
+/* ---- request sampling ----
+ * Sampling / Sampler (src/sampling.rs:8-226): the request's options and
+ * its host sampler over one row of logits (f64 penalties, temperature,
+ * top-k, nucleus, then a draw from the seeded stream).  The stream is
+ * rand 0.9's StdRng (ChaCha12, seed_from_u64); has_seed = 0 seeds from
+ * the OS.  Errors carry the reference's messages (chk_last_error). */
+typedef struct ChkSampling {
+    double temperature;       /* 0..2; 0 = greedy (argmax) */
+    double top_p;             /* (0, 1] */
+    uint32_t top_k;           /* 0 = whole vocabulary, else <= 1000000 */
+    uint32_t has_seed;
+    uint64_t seed;
+    double presence_penalty;  /* -2..2 */
+    double frequency_penalty; /* -2..2 */
+} ChkSampling;
+/* Sampling::validate (sampling.rs:46-68). */
+int chk_sampling_validate(const ChkSampling* s);
+/* Sampling::greedy (sampling.rs:71-73): 1 when argmax MTP verification
+ * applies (temperature and both penalties zero). */
+int chk_sampling_greedy(const ChkSampling* s);
+typedef struct ChkSampler ChkSampler;
+/* Sampler::new (sampling.rs:114-134): counts start from the prompt. */
+int chk_sampler_new(const ChkSampling* s, const uint32_t* prompt, uint32_t n, uint32_t vocab, ChkSampler** out);
+void chk_sampler_free(ChkSampler* s);
+/* Sampler::accept (sampling.rs:136-144). */
+int chk_sampler_accept(ChkSampler* s, uint32_t token);
+/* Sampler::sample (sampling.rs:146-209) over logits[0..n), n = vocab. */
+int chk_sampler_sample(ChkSampler* s, const float* logits, uint32_t n, uint32_t* token);
+/* The sampler's stream alone: n next_u64 draws of StdRng::from_seed(seed32)
+ * or, with seed32 NULL, of seed_from_u64(seed) (no reference counterpart;
+ * pins the ChaCha12 restatement in tests). */
+int chk_rng_u64(const uint8_t* seed32, uint64_t seed, uint64_t* out, uint32_t n);
+/* PCG32 as its reference generator seeds and runs it (pcg32_srandom_r /
+ * pcg32_random_r) on the step and output the seeding uses (no reference
+ * counterpart; pins seed_from_u64's generator in tests). */
+void chk_pcg32(uint64_t init_state, uint64_t init_seq, uint32_t* out, uint32_t n);
+/* The ChaCha block function, `rounds` rounds over a 16-word input state
+ * (no reference counterpart; RFC 8439 vectors pin it in tests). */
+void chk_chacha_block(const uint32_t* in, int rounds, uint32_t* out);
+
 /* ---- runner: the greedy speculative decode loop ----
  * Decode::new / Decode::step (src/runner/decode.rs:28-171) for the greedy
  * sampler.  `next` and drafts[0..n_drafts) come from the prompt's prefill;
@@ -213,6 +254,15 @@ int chk_last_probs(const ChkEngine* e, uint32_t layer, uint32_t r, float* probs)
 typedef struct ChkDecode ChkDecode;
 int chk_decode_new(ChkEngine* e, uint32_t next, const uint32_t* drafts, uint32_t n_drafts, uint32_t n_draft,
                    uint32_t limit, uint32_t no_eos, ChkDecode** out);
+/* Decode::new (decode.rs:28-71) with the request's sampling options.
+ * Greedy options behave as chk_decode_new.  Otherwise the sampler starts
+ * from prompt[0..n_prompt), the first token is sampled from
+ * final_logits (the prompt's last-row logits, vocab_size floats), and no
+ * drafts are used (Options::effective_drafts, options.rs:165-171): each
+ * step runs one row and samples from its logits. */
+int chk_decode_new_sampling(ChkEngine* e, const ChkSampling* sampling, const uint32_t* prompt, uint32_t n_prompt,
+                            const float* final_logits, uint32_t next, const uint32_t* drafts, uint32_t n_drafts,
+                            uint32_t n_draft, uint32_t limit, uint32_t no_eos, ChkDecode** out);
 void chk_decode_free(ChkDecode* d);
 /* One step: the tokens it emits (1 + accepted drafts, <= 4) go to emitted. */
 int chk_decode_step(ChkDecode* d, uint32_t* emitted, uint32_t* n_emitted);
