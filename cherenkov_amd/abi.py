@@ -52,6 +52,12 @@ class ChkConfig(C.Structure):
         ("partial_rotary_factor", f64),
         ("rope_theta", f64),
         ("seed", u64),
+        ("ple_conv_kernel_size", u32),
+        ("ple_embed_dim", u32),
+        ("ngram_size", u32),
+        ("heads_per_ngram", u32),
+        ("ngram_group", u32),
+        ("ngram_head_rows", u32),
     ]
 
     def as_dict(self) -> dict:

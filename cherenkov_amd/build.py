@@ -33,7 +33,7 @@ FLAGS = [
     f"-I{CSRC}",
 ]
 SOURCES = ["gen.hip", "decode.hip", "attn.hip", "misc.hip", "prefill.hip", "dnscan.hip", "engine.cpp", "runner.cpp", "sampler.cpp", "store.cpp",
-           "noalloc.hip", "phasebench.hip"]
+           "noalloc.hip", "phasebench.hip", "ple.hip"]
 
 
 def _compile(src: Path) -> Path:

@@ -89,6 +89,14 @@ struct Bump {
     }
 };
 
+// The PLE block's weights (PleWeights, cpu.rs:62-75): key / value
+// projections of the n-gram embedding, three grouped-norm weights and the
+// depthwise conv [hc * H][kernel].
+struct PleDev {
+    Q4Mat key{}, value{};
+    const uint16_t *norm_key = nullptr, *norm_query = nullptr, *norm_conv = nullptr, *conv = nullptr;
+};
+
 struct LayerDev {
     bool linear = false;
     int dn_idx = -1, at_idx = -1;
@@ -96,6 +104,8 @@ struct LayerDev {
     DnDev dn{};
     AtDev at{};
     MoeDev moe{};
+    bool has_ple = false;
+    PleDev ple{};
 };
 
 enum { PROF_NONE = 0, PROF_MOE = 1, PROF_DN_PROJ = 2, PROF_LM_HEAD = 3 };
@@ -121,6 +131,8 @@ struct Scratch {
     float *mtp_hyper, *mtp_hn, *mtp_fe, *mtp_fh, *mtp_src, *mtp_logits;
     uint32_t* mtp_out;
     float* trace;  // [L][MAX_NB][hh] when tracing
+    // PLE: n-gram embedding, key, value, gated value and its norm per row
+    float *ple_e, *ple_key, *ple_value, *ple_gated, *ple_gvn;
 };
 
 // Chunk buffers of the GEMM prefill (allocated on its first use), `cap`
@@ -142,6 +154,9 @@ struct PfBufs {
     // the normed trunk streams, fc_e / fc_h outputs and the head's residual
     uint32_t* mtp_tok;
     float *mtp_en, *mtp_hn, *mtp_fe, *mtp_fh, *mtp_hyper;
+    // PLE over a chunk: table rows of each row's token, then as Scratch
+    uint32_t* ple_ids;
+    float *ple_e, *ple_key, *ple_value, *ple_gated, *ple_gvn;
 };
 
 }  // namespace chk
@@ -170,6 +185,18 @@ struct ChkEngine {
     const uint16_t* mtp_enorm = nullptr;
     const uint16_t* mtp_hnorm = nullptr;
     Q4Mat fc_e{}, fc_h{};
+    // PLE n-gram block: its decoder layer (-1: none), the n-gram table
+    // (ngram.bin rows in HBM), the hash metadata the host computes row ids
+    // with, the gvn ring [span][hh] and the ring rows a verify step may
+    // roll back [MAX_NB][hh]
+    int ple_l = -1;
+    uint8_t* ngram = nullptr;
+    uint64_t ngram_rows = 0, ngram_row_bytes = 0;
+    uint32_t ngram_dim = 0, ngram_group = 0, ngram_heads = 0, ple_span = 0;
+    std::vector<int64_t> ngram_mult;
+    std::vector<uint64_t> ngram_offs, ngram_sizes;
+    float* ple_ring = nullptr;
+    float* ple_backup = nullptr;
     // state
     std::vector<float*> dn_state, dn_hist, dn_snap_state, dn_snap_hist;
     std::vector<KvDev> kv, kv2;
@@ -295,6 +322,7 @@ struct ChkEngine {
         if (staging) hipHostFree(staging);
         if (dense_fd >= 0) close(dense_fd);
         if (experts_fd >= 0) close(experts_fd);
+        if (ngram_fd >= 0) close(ngram_fd);
         if (s.h_in) hipHostFree(s.h_in);
         if (s.h_out) hipHostFree(s.h_out);
         for (void* p : allocs) hipFree(p);
@@ -336,7 +364,7 @@ struct ChkEngine {
     // Weights come from the seeded generator (synth.h), or, for an engine
     // loaded from a packed store, from its dense.bin / experts.bin.
     const Store* src = nullptr;
-    int dense_fd = -1, experts_fd = -1;
+    int dense_fd = -1, experts_fd = -1, ngram_fd = -1;
     uint8_t* staging = nullptr;  // pinned host buffer for store uploads
     static constexpr uint64_t STAGING = 64ull << 20;
 
@@ -360,12 +388,23 @@ struct ChkEngine {
         const DenseEntry& e = src->entry(name);
         ensure(e.dtype == dtype, name + ": expected " + dtype + ", got " + e.dtype);
         ensure(e.shape == shape, name + ": shape does not match the config");
-        uint64_t n = e.dtype == "U32" ? 4 : 2;
+        uint64_t n = e.dtype == "U32" ? 4 : e.dtype == "I64" ? 8 : 2;
         for (uint64_t x : shape) n *= x;
         ensure(e.nbytes == n, name + ": byte count does not match its shape");
         return e;
     }
 
+    std::vector<int64_t> store_i64(const std::string& name, uint64_t n) {
+        const DenseEntry& e = store_entry(name, "I64", {n});
+        std::vector<int64_t> v(n);
+        for (uint64_t done = 0; done < e.nbytes;) {
+            const ssize_t r = pread(dense_fd, reinterpret_cast<uint8_t*>(v.data()) + done, e.nbytes - done,
+                                    (off_t)(e.offset + done));
+            ensure(r > 0, "short read of the packed store");
+            done += (uint64_t)r;
+        }
+        return v;
+    }
     Q4Mat q4(Bump& B, uint32_t kind, uint32_t slot, uint32_t part, uint32_t out, uint32_t in) {
         Q4Mat m{};
         m.out = out;
@@ -479,6 +518,54 @@ struct ChkEngine {
         L.moe.sh_up = q4(B, CHK_T_MOE_SH_UP, slot, 0, D.SI, H);
         L.moe.sh_down = q4(B, CHK_T_MOE_SH_DOWN, slot, 0, H, D.SI);
         L.moe.record_layer = record_layer;
+        if ((int)slot == ple_l) {
+            const uint32_t E = c.ple_embed_dim;
+            L.has_ple = true;
+            L.ple.key = q4(B, CHK_T_PLE_KEY, slot, 0, D.hh, E);
+            L.ple.value = q4(B, CHK_T_PLE_VALUE, slot, 0, H, E);
+            L.ple.norm_key = bf(B, CHK_T_PLE_NORM_KEY, slot, 0, D.hh);
+            L.ple.norm_query = bf(B, CHK_T_PLE_NORM_QUERY, slot, 0, D.hh);
+            L.ple.norm_conv = bf(B, CHK_T_PLE_NORM_CONV, slot, 0, D.hh);
+            L.ple.conv = bf(B, CHK_T_PLE_CONV, slot, 0, (uint64_t)D.hh * c.ple_conv_kernel_size);
+        }
+    }
+    // The n-gram table and its hash metadata: a store's ngram.bin and
+    // {layer}.ple.ple_embedding.* tensors (packed.rs:134-148), else the
+    // synthetic table of synth.h.
+    void build_ngram() {
+        const uint32_t heads = ngram_heads;
+        if (src) {
+            const StoreNgram& N = src->ngram;
+            const std::string pre = tensor_name(c, CHK_T_NGRAM_MULT, (uint32_t)ple_l, 0);
+            ngram_mult = store_i64(pre + ".layer_multipliers", c.ngram_size);
+            const std::vector<int64_t> offs = store_i64(pre + ".ngram_heads_offsets", heads);
+            const std::vector<int64_t> sizes = store_i64(pre + ".ngram_heads_vocab_sizes", heads);
+            ngram_offs.assign(offs.begin(), offs.end());
+            ngram_sizes.assign(sizes.begin(), sizes.end());
+            ensure(N.dim * heads == c.ple_embed_dim, "n-gram head layout mismatch");
+            ngram_rows = N.rows;
+            ngram_row_bytes = N.row_bytes;
+        } else {
+            ngram_mult.resize(c.ngram_size);
+            for (uint32_t k = 0; k < c.ngram_size; ++k) ngram_mult[k] = chk_ngram_multiplier(c.seed, k);
+            ngram_offs.resize(heads);
+            ngram_sizes.resize(heads);
+            uint64_t off = 0;
+            for (uint32_t h = 0; h < heads; ++h) {
+                ngram_sizes[h] = chk_ngram_head_size(c.ngram_head_rows, h);
+                ngram_offs[h] = off;
+                off += ngram_sizes[h];
+            }
+            ngram_rows = off;
+            ngram_row_bytes = chk_ngram_row_bytes(ngram_dim, ngram_group);
+        }
+        for (uint32_t h = 0; h < heads; ++h)
+            ensure(ngram_sizes[h] >= 1 && ngram_sizes[h] < (1ull << 62) && ngram_offs[h] + ngram_sizes[h] <= ngram_rows,
+                   "n-gram heads exceed the table");
+        ensure(ngram_rows < (1ull << 32), "n-gram table above 2^32 rows");
+        ngram = dalloc<uint8_t>(ngram_rows * ngram_row_bytes);
+        if (src) upload(ngram_fd, 0, ngram_rows * ngram_row_bytes, ngram);
+        else gen_ngram_table(ngram, ngram_rows, ngram_dim, ngram_group, c.seed, st);
     }
     void build_dense(Bump& B) {
         uint32_t H = D.H, L = c.num_hidden_layers;
@@ -556,7 +643,24 @@ struct ChkEngine {
                "indexer budget must be a multiple of the block size (gpu/load.rs:33-36)");
         ensure(c.num_experts <= 512 && c.num_experts_per_tok <= 64 && c.num_experts_per_tok <= c.num_experts,
                "at most 512 experts and 64 per token");
-        ensure(c.ple_layer == 0, "PLE layers are not supported");
+        ensure(c.ple_layer <= c.num_hidden_layers, "ple_layer_ids beyond the decoder layers");
+        if (c.ple_layer) {
+            ple_l = (int)c.ple_layer - 1;
+            ensure(c.ngram_size >= 2 && c.ngram_size <= 16 && c.heads_per_ngram >= 1,
+                   "n-gram orders 2..=ngram_size (at most 16) need heads");
+            ngram_heads = (c.ngram_size - 1) * c.heads_per_ngram;
+            ensure(ngram_heads <= MAX_NGRAM_IDS, "at most 32 n-gram heads");
+            ensure(c.ple_embed_dim % 64 == 0 && c.ple_embed_dim % ngram_heads == 0,
+                   "ple_embed_dim must be a multiple of 64 and of the n-gram heads");
+            ngram_dim = c.ple_embed_dim / ngram_heads;
+            ngram_group = src ? (uint32_t)src->ngram.group : c.ngram_group;
+            ensure(ngram_group >= 1 && ngram_dim % 8 == 0 && ngram_dim % ngram_group == 0,
+                   "n-gram rows must be whole words and groups");
+            ensure(c.ple_conv_kernel_size >= 2 && c.ple_conv_kernel_size <= 16, "PLE conv kernel 2..=16");
+            ple_span = (c.ple_conv_kernel_size - 1) * c.ngram_size;
+            ensure(ple_span >= MAX_NB, "PLE ring shorter than a verify step");
+            ensure(src || c.ngram_head_rows > ngram_heads, "synthetic n-gram heads need rows");
+        }
         ensure(c.linear_conv_kernel_dim >= 2 && c.linear_conv_kernel_dim <= 9, "conv kernel 2..=9");
         ensure(c.indexer_compress_ratio >= 1 && c.indexer_budget >= c.indexer_compress_ratio,
                "indexer budget must hold at least one block");
@@ -619,6 +723,7 @@ struct ChkEngine {
         B.base = dense;
         B.gen = true;
         build_dense(B);
+        if (ple_l >= 0) build_ngram();
 
         // routed-expert store: all records resident, main layers then MTP
         record_layers = c.num_hidden_layers + (has_mtp ? 1 : 0);
@@ -647,6 +752,11 @@ struct ChkEngine {
             }
         }
         if (has_mtp) mtp_kv = alloc_kv();
+        if (ple_l >= 0) {
+            ple_ring = dalloc<float>((uint64_t)ple_span * D.hh);
+            ple_backup = dalloc<float>((uint64_t)MAX_NB * D.hh);
+            state_bytes += (uint64_t)(ple_span + MAX_NB) * D.hh * 4;
+        }
         max_chunks = (max_t + ATTN_CHUNK - 1) / ATTN_CHUNK;
         ensure(max_chunks <= (uint32_t)MAX_ATTN_CHUNKS, "context capacity above 262144 tokens");
 
@@ -708,6 +818,13 @@ struct ChkEngine {
         s.mtp_logits = dalloc<float>((uint64_t)NB * D.V);
         s.mtp_out = dalloc<uint32_t>(NB);
         s.trace = nullptr;
+        if (ple_l >= 0) {
+            s.ple_e = dalloc<float>((uint64_t)NB * c.ple_embed_dim);
+            s.ple_key = dalloc<float>((uint64_t)NB * D.hh);
+            s.ple_value = dalloc<float>((uint64_t)NB * D.H);
+            s.ple_gated = dalloc<float>((uint64_t)NB * D.hh);
+            s.ple_gvn = dalloc<float>((uint64_t)NB * D.hh);
+        }
         scratch_bytes = 4ull * (NB * (3 * D.hh + 4 * D.H + D.conv_dim + 3 * D.v_dim + 4 * D.nh * D.hd) +
                                  (uint64_t)NB * D.nh * max_chunks * (D.hd + 2) + 2ull * NB * D.V);
         host_logits.resize((size_t)NB * D.V);
@@ -726,6 +843,10 @@ struct ChkEngine {
         ensure(dense_fd >= 0, "opening " + S->dir + "/dense.bin");
         experts_fd = open((S->dir + "/experts.bin").c_str(), O_RDONLY);
         ensure(experts_fd >= 0, "opening " + S->dir + "/experts.bin");
+        if (S->cfg.ple_layer) {
+            ngram_fd = open((S->dir + "/ngram.bin").c_str(), O_RDONLY);
+            ensure(ngram_fd >= 0, "opening " + S->dir + "/ngram.bin");
+        }
         src = S.get();
         const ChkConfig cfg = S->cfg;
         try {
@@ -739,7 +860,8 @@ struct ChkEngine {
         staging = nullptr;
         close(dense_fd);
         close(experts_fd);
-        dense_fd = experts_fd = -1;
+        if (ngram_fd >= 0) close(ngram_fd);
+        dense_fd = experts_fd = ngram_fd = -1;
     }
 
     void reset_state() {
@@ -747,6 +869,7 @@ struct ChkEngine {
             launch_zero_f32(dn_state[i], (uint64_t)D.nv * D.dv * D.dk, st);
             launch_zero_f32(dn_hist[i], (uint64_t)D.conv_dim * (D.ck - 1), st);
         }
+        if (ple_ring) launch_zero_f32(ple_ring, (uint64_t)ple_span * D.hh, st);
         pos = 0;
         batch_pos = 0;
         batch_nb = 0;
@@ -1009,12 +1132,79 @@ struct ChkEngine {
         return ms;
     }
 
+    // ------------------------------------------------------------ PLE
+    // the table rows of tokens[t0 .. t0 + n) into out[i * stride ..]
+    void ple_ids(size_t t0, uint32_t n, uint32_t* out, uint32_t stride) const {
+        for (uint32_t i = 0; i < n; ++i) ngram_rows_at(t0 + i, out + (size_t)i * stride);
+    }
+    // CpuModel::ngram_ids_from (cpu.rs:848-887) for the token at index t of
+    // `tokens`: bigram heads, then trigram heads, each hashing the token
+    // and the ones before it (EOS when the window [t - k, t) holds an EOS
+    // or reaches before the start) with wrapping i64 products, XOR, and the
+    // Euclidean remainder by the head's size; the host computes these for
+    // the gather kernel, as the reference's GPU path does (gpu/ple.rs:7-15).
+    void ngram_rows_at(size_t t, uint32_t* out) const {
+        const uint32_t eos = c.eos_token_id;
+        int64_t shifted[16];
+        for (uint32_t k = 0; k < c.ngram_size; ++k) {
+            if (k == 0) {
+                shifted[0] = (int64_t)tokens[t];
+                continue;
+            }
+            bool before = t < k;
+            for (size_t j = before ? t : t - k; j < t && !before; ++j) before = tokens[j] == eos;
+            shifted[k] = before ? (int64_t)eos : (int64_t)tokens[t - k];
+        }
+        uint32_t n = 0;
+        for (uint32_t ng = 2; ng <= c.ngram_size; ++ng) {
+            uint64_t mixed = (uint64_t)shifted[0] * (uint64_t)ngram_mult[0];
+            for (uint32_t p = 1; p < ng; ++p) mixed ^= (uint64_t)shifted[p] * (uint64_t)ngram_mult[p];
+            const int64_t mx = (int64_t)mixed;
+            for (uint32_t h = (ng - 2) * c.heads_per_ngram; h < (ng - 1) * c.heads_per_ngram; ++h) {
+                const int64_t size = (int64_t)ngram_sizes[h];
+                int64_t r = mx % size;
+                if (r < 0) r += size;
+                out[n++] = (uint32_t)((uint64_t)r + ngram_offs[h]);
+            }
+        }
+    }
+
+    // The PLE block over `rows` rows whose n-gram table rows are `ids`
+    // ([rows][heads], device-visible), hyper rows `hyper` at positions
+    // `rowpos`; `backup`: where the ring rows go that a rollback restores.
+    void ple_rows(const PleDev& P, const uint32_t* ids, uint32_t ids_stride, float* hyper, const uint32_t* rowpos,
+                  uint32_t rows, float* e, float* key, float* value, float* gated, float* gvn, float* backup,
+                  bool gemm) {
+        const uint32_t E = c.ple_embed_dim;
+        launch_ple_gather(ids, ids_stride, ngram_heads, ngram, ngram_row_bytes, ngram_dim, ngram_group, e, rows, st);
+        if (gemm) {
+            launch_pf_xprep(e, E, rows, E, pf.hi, pf.lo, pf.xs, st);
+            launch_pf_gemm(P.key, pf.hi, pf.lo, pf.xs, key, rows, D.hh, st);
+            launch_pf_gemm(P.value, pf.hi, pf.lo, pf.xs, value, rows, D.H, st);
+        } else {
+            SegArgs a{};
+            a.nseg = 2;
+            a.seg[0] = Seg{P.key, e, key, E, D.hh, 0, EPI_RAW};
+            a.seg[1] = Seg{P.value, e, value, E, D.H, D.hh, EPI_RAW};
+            a.total = D.hh + D.H;
+            launch_qmv(a, (int)rows, st);
+        }
+        launch_ple_gate(key, hyper, D.hh, value, P.norm_key, P.norm_query, P.norm_conv, gated, gvn, D.H, D.hc, D.eps,
+                        rows, st);
+        launch_ple_conv(gated, gvn, P.conv, ple_ring, hyper, D.hh, rowpos, D.hh, c.ple_conv_kernel_size,
+                        c.ngram_size, ple_span, rows, st);
+        launch_ple_ring(gvn, ple_ring, backup, rowpos, D.hh, ple_span, rows, st);
+    }
+
     // ---------------------------------------------------------- step
     void run_rows(int nb, bool snap) {
         launch_embed(s.d_in, s.tokens, s.rowpos, embed, s.hyper, D.H, D.hc, nb, st);
         KvDev kvs[MAX_NB];
         for (uint32_t l = 0; l < c.num_hidden_layers; ++l) {
             const LayerDev& L = layers[l];
+            if (L.has_ple)
+                ple_rows(L.ple, &s.d_in->ngram[0][0], MAX_NGRAM_IDS, s.hyper, s.rowpos, (uint32_t)nb, s.ple_e, s.ple_key,
+                         s.ple_value, s.ple_gated, s.ple_gvn, snap ? ple_backup : nullptr, false);
             hc_read(L.attn_hc, s.hyper, s.inj_a, nb);
             if (L.linear) {
                 deltanet(L, s.mixed, nb, snap, s.hyper, s.inj_a, nullptr);
@@ -1050,6 +1240,7 @@ struct ChkEngine {
         logit_rows = n;
         for (uint32_t i = 0; i < n; ++i) s.h_in->tokens[i] = toks[i];
         s.h_in->pos = pos;
+        if (ple_l >= 0) ple_ids(pos, n, &s.h_in->ngram[0][0], MAX_NGRAM_IDS);
         std::atomic_thread_fence(std::memory_order_seq_cst);
         const StepGraph* replayed = nullptr;
         if (use_graphs && !tracing && prof_kind == PROF_NONE) {
@@ -1115,6 +1306,13 @@ struct ChkEngine {
                 launch_copy_f32(dn_state[i], dn_snap_state[i] + plane * sn, sn, st);
                 launch_copy_f32(dn_hist[i], dn_snap_hist[i] + plane * hn, hn, st);
             }
+            // the ring slots the rejected rows overwrote get their old rows
+            // back: the oldest tap (back = span) of a later position reads
+            // exactly the slot its own row writes, so positional overwrite
+            // alone would leave a rejected row's gvn there
+            for (uint32_t j = n; ple_ring && j < batch_nb; ++j)
+                launch_copy_f32(ple_ring + (uint64_t)((batch_pos + j) % ple_span) * D.hh,
+                                ple_backup + (uint64_t)j * D.hh, D.hh, st);
             HIPCHK(hipStreamSynchronize(st));
         }
         pos = batch_pos + n;
@@ -1152,6 +1350,7 @@ struct ChkEngine {
             }
         }
         if (has_mtp) attn(mtp_kv, mtp_n);
+        if (ple_ring) r.push_back({ple_ring, (uint64_t)ple_span * D.hh * 4});
         return r;
     }
     uint64_t state_bytes_at(uint32_t n, uint32_t mtp_n) const;
@@ -1402,6 +1601,7 @@ uint64_t ChkEngine::prefill_scratch_bytes(uint64_t C, bool all_logits) const {
     b += (uint64_t)pf_tile_bound((uint32_t)C, D.topk, D.E) * 4 + C * slots * (D.I + D.H) * f;
     if (dc_supported(D.nk, D.nv, D.dk, D.dv)) b += dc_work_floats((uint32_t)C, D.nv, D.dv) * f;
     if (all_logits) b += C * D.V * f;
+    if (ple_l >= 0) b += C * (ngram_heads + c.ple_embed_dim + 3ull * D.hh + D.H) * 4;
     return b;
 }
 
@@ -1493,6 +1693,14 @@ void ChkEngine::pf_alloc() {
     pf.act = pfalloc<float>(C * slots * D.I);
     pf.yd = pfalloc<float>(C * slots * D.H);
     pf.dcw = dc_supported(D.nk, D.nv, D.dk, D.dv) ? pfalloc<float>(dc_work_floats((uint32_t)C, D.nv, D.dv)) : nullptr;
+    if (ple_l >= 0) {
+        pf.ple_ids = pfalloc<uint32_t>(C * ngram_heads);
+        pf.ple_e = pfalloc<float>(C * c.ple_embed_dim);
+        pf.ple_key = pfalloc<float>(C * D.hh);
+        pf.ple_value = pfalloc<float>(C * D.H);
+        pf.ple_gated = pfalloc<float>(C * D.hh);
+        pf.ple_gvn = pfalloc<float>(C * D.hh);
+    }
     pf.cap = (uint32_t)C;
 }
 
@@ -1740,9 +1948,20 @@ void ChkEngine::prefill_gemm(const uint32_t* toks, uint32_t n, uint32_t next_aft
         for (uint32_t t = 0; t < T; ++t) rp[t] = pos0 + t;
         HIPCHK(hipMemcpy(pf.tokens, toks + c0, T * 4, hipMemcpyHostToDevice));
         HIPCHK(hipMemcpy(pf.pos, rp.data(), T * 4, hipMemcpyHostToDevice));
+        if (ple_l >= 0) {
+            // the chunk's n-gram rows need the history through each row
+            tokens.insert(tokens.end(), toks + c0, toks + c0 + T);
+            std::vector<uint32_t> ids((size_t)T * ngram_heads);
+            ple_ids(pos0, T, ids.data(), ngram_heads);
+            tokens.resize(pos0);
+            HIPCHK(hipMemcpy(pf.ple_ids, ids.data(), ids.size() * 4, hipMemcpyHostToDevice));
+        }
         launch_pf_embed(pf.tokens, embed, pf.hyper, D.H, D.hc, T, st);
         for (uint32_t l = 0; l < c.num_hidden_layers; ++l) {
             const LayerDev& L = layers[l];
+            if (L.has_ple)
+                ple_rows(L.ple, pf.ple_ids, ngram_heads, pf.hyper, pf.pos, T, pf.ple_e, pf.ple_key, pf.ple_value, pf.ple_gated,
+                         pf.ple_gvn, nullptr, true);
             pf_hc_read(L.attn_hc, pf.inj_a, T, false);
             if (L.linear) pf_deltanet(L, T);
             else pf_attention(L, T, pos0);

@@ -350,10 +350,12 @@ struct PfDnArgs {
 // Per-step inputs written by the host into pinned, device-mapped memory
 // (read once per step by the first kernel, so a captured graph replays
 // with new tokens and positions).
+constexpr uint32_t MAX_NGRAM_IDS = 32;  // n-gram heads of a PLE block
 struct StepIn {
     uint32_t tokens[MAX_NB];
     uint32_t pos;
     uint32_t pad[3];
+    uint32_t ngram[MAX_NB][MAX_NGRAM_IDS];  // PLE table rows of each row's token
 };
 
 void launch_embed(const StepIn* in, uint32_t* tokens, uint32_t* rowpos, const Q4Mat& emb, float* hyper, uint32_t H,
@@ -411,6 +413,19 @@ bool attn_shape_ok(uint32_t nh, uint32_t nkv, uint32_t hd);
 void launch_copy_f32(float* dst, const float* src, uint64_t n, hipStream_t st);
 void launch_kv_fill(const float* k, const float* v, KvDev kv, uint32_t kv_row, uint32_t T, hipStream_t st);
 void launch_zero_f32(float* dst, uint64_t n, hipStream_t st);
+// PLE n-gram block (ple.hip)
+void gen_ngram_table(uint8_t* table, uint64_t rows, uint32_t dim, uint32_t group, uint64_t seed, hipStream_t st);
+// ids: row r's table rows at ids[r * ids_stride ..]
+void launch_ple_gather(const uint32_t* ids, uint32_t ids_stride, uint32_t nids, const uint8_t* table,
+                       uint64_t row_bytes, uint32_t dim, uint32_t group, float* e, uint32_t rows, hipStream_t st);
+void launch_ple_gate(const float* key, const float* hyper, uint64_t hyper_stride, const float* value,
+                     const uint16_t* wk, const uint16_t* wq, const uint16_t* wc, float* gated, float* gvn, uint32_t H,
+                     uint32_t hc, float eps, uint32_t rows, hipStream_t st);
+void launch_ple_conv(const float* gated, const float* gvn, const uint16_t* conv, const float* ring, float* hyper,
+                     uint64_t hyper_stride, const uint32_t* pos, uint32_t hh, uint32_t K, uint32_t dil, uint32_t span,
+                     uint32_t rows, hipStream_t st);
+void launch_ple_ring(const float* gvn, float* ring, float* backup, const uint32_t* pos, uint32_t hh, uint32_t span,
+                     uint32_t rows, hipStream_t st);
 void launch_fill_u8(uint8_t* dst, uint8_t v, uint64_t n, hipStream_t st);
 
 }  // namespace chk

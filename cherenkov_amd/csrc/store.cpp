@@ -284,6 +284,11 @@ static ChkConfig read_config(const std::string& path) {
     if (gate != "sigmoid") fail("output_gate_type must be sigmoid (gpu/load.rs:49-52)");
     if (const Json* ple = t.get("ple_layer_ids"); ple && ple->kind == Json::ARR && !ple->arr.empty())
         c.ple_layer = (uint32_t)ple->arr[0].u64();
+    // config.rs:36-43 (ple_embed_dim has no default there)
+    c.ple_embed_dim = u32f(t, "ple_embed_dim");
+    c.ple_conv_kernel_size = u32d(t, "ple_conv_kernel_size", 4);
+    c.ngram_size = u32d(t, "ngram_size", 3);
+    c.heads_per_ngram = u32d(t, "heads_per_ngram", 8);
     const Json& lt = t.at("layer_types");
     if (lt.kind != Json::ARR || lt.arr.size() != c.num_hidden_layers) fail("layer_types length mismatch");
     uint32_t interval = 0;
@@ -358,6 +363,23 @@ std::unique_ptr<Store> open_store(const std::string& model_dir) {
                                                     {X.down_b, sc_down}};
     for (const auto& f : fields)
         if (f.first + f.second > X.record_bytes) fail("expert record field outside the record");
+    // NgramLayout, read when the config has a PLE layer; the row group
+    // reaches the config (ngram rows are not necessarily groups of 64)
+    if (const Json* n = m.get("ngram"); n && c.ple_layer) {
+        StoreNgram& N = S->ngram;
+        N.rows = n->at("rows").u64();
+        N.row_bytes = n->at("row_bytes").u64();
+        N.dim = n->at("dim").u64();
+        N.group = n->at("group").u64();
+        N.weight_bytes = n->at("weight_bytes").u64();
+        N.scale_bytes = n->at("scale_bytes").u64();
+        if (N.group == 0 || N.dim % 8 || N.dim % N.group || N.weight_bytes != N.dim / 2 ||
+            N.scale_bytes != N.dim / N.group * 2 || N.row_bytes != N.weight_bytes + 2 * N.scale_bytes)
+            fail("n-gram row layout is inconsistent");
+        S->cfg.ngram_group = (uint32_t)N.group;
+    } else if (c.ple_layer) {
+        fail("manifest has no n-gram layout");
+    }
     // the record layers the engine reads: each main layer, then the MTP layer
     for (uint32_t l = 0; l < c.num_hidden_layers; ++l)
         if (l >= X.layers || X.layer_prefixes[l] != "language_model.model.layers." + std::to_string(l) + ".mlp.switch_mlp")
@@ -420,6 +442,13 @@ std::string tensor_name(const ChkConfig& c, uint32_t kind, uint32_t slot, uint32
     case CHK_T_MTP_HNORM: return "mtp.pre_fc_norm_hidden.weight";
     case CHK_T_MTP_FC_E: return "mtp.fc_embedding";
     case CHK_T_MTP_FC_H: return "mtp.fc_hidden";
+    case CHK_T_PLE_KEY: return lp + ".ple.key_proj";
+    case CHK_T_PLE_VALUE: return lp + ".ple.value_proj";
+    case CHK_T_PLE_NORM_KEY: return lp + ".ple.norm_key.weight";
+    case CHK_T_PLE_NORM_QUERY: return lp + ".ple.norm_query.weight";
+    case CHK_T_PLE_NORM_CONV: return lp + ".ple.norm_conv.weight";
+    case CHK_T_PLE_CONV: return lp + ".ple.conv1d.weight";
+    case CHK_T_NGRAM_MULT: return lp + ".ple.ple_embedding";  // prefix of the hash metadata
     default: fail("no store name for tensor kind " + std::to_string(kind));
     }
     return "";

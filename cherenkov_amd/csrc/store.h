@@ -47,11 +47,17 @@ struct StoreExperts {
     uint64_t gate_w = 0, up_w = 0, down_w = 0, gate_s = 0, gate_b = 0, up_s = 0, up_b = 0, down_s = 0, down_b = 0;
 };
 
+// NgramLayout (manifest.rs:42-55): ngram.bin rows of weight | scales | biases
+struct StoreNgram {
+    uint64_t rows = 0, row_bytes = 0, dim = 0, group = 0, weight_bytes = 0, scale_bytes = 0;
+};
+
 struct Store {
     std::string dir;
     ChkConfig cfg{};
     std::map<std::string, DenseEntry> dense;
     StoreExperts experts;
+    StoreNgram ngram;
     const DenseEntry& entry(const std::string& name) const;
 };
 

@@ -93,6 +93,24 @@ def tiny(seed: int = 1234, layers: int = 4, mtp: int = 1, indexer_budget: int = 
     )
 
 
+def with_ple(c: ChkConfig, layer: int = 2, embed_dim: int = 256, ngram_size: int = 3, heads_per_ngram: int = 8,
+             group: int = 16, head_rows: int = 1021, kernel: int = 4) -> ChkConfig:
+    """`c` with a PLE n-gram block before decoder layer `layer` (1-based, as
+    ple_layer_ids writes it).  The defaults are the qwen4_exp fixture's
+    (tests/fixtures/qwen4_exp/config.json: ple_layer_ids [2], embed dim 256,
+    3-grams, 8 heads per order, conv kernel 4; its n-gram rows are groups of
+    16, tests/import.rs:52); the synthetic table has head_rows - h rows in
+    head h."""
+    c.ple_layer = layer
+    c.ple_embed_dim = embed_dim
+    c.ngram_size = ngram_size
+    c.heads_per_ngram = heads_per_ngram
+    c.ngram_group = group
+    c.ngram_head_rows = head_rows
+    c.ple_conv_kernel_size = kernel
+    return c
+
+
 def decode_bytes_per_token(c: ChkConfig, ctx: int, expert_bits: int = 4) -> int:
     """Algorithmic HBM bytes of one batch-1 decode step (drafts = 0):
     every weight the step reads once, DeltaNet state read + write, conv

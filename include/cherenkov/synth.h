@@ -72,7 +72,16 @@ enum ChkTensorKind {
     CHK_T_MTP_ENORM,
     CHK_T_MTP_HNORM,
     CHK_T_MTP_FC_E,
-    CHK_T_MTP_FC_H
+    CHK_T_MTP_FC_H,
+    /* PLE n-gram block (slot: its decoder layer) */
+    CHK_T_PLE_KEY,
+    CHK_T_PLE_VALUE,
+    CHK_T_PLE_NORM_KEY,
+    CHK_T_PLE_NORM_QUERY,
+    CHK_T_PLE_NORM_CONV,
+    CHK_T_PLE_CONV,
+    CHK_T_NGRAM_TABLE, /* rows of (words | scales | biases), ngram.bin layout */
+    CHK_T_NGRAM_MULT   /* per-order hash multipliers */
 };
 
 enum { CHK_HC_ATTN = 0, CHK_HC_MLP = 1, CHK_HC_FINAL = 2, CHK_HC_MTP = 3 };
@@ -173,6 +182,7 @@ static inline CHK_HD ChkDist chk_dist(uint32_t kind) {
     case CHK_T_MTP_HNORM:
         d.a = -0.1f; d.b = 0.1f; break;
     case CHK_T_DN_CONV:
+    case CHK_T_PLE_CONV:
         d.a = -0.5f; d.b = 0.5f; break;
     case CHK_T_DN_ALOG:
         d.a = -2.0f; d.b = 0.5f; break;
@@ -193,5 +203,25 @@ static inline CHK_HD uint16_t chk_bf16_elem(uint64_t seed, uint64_t tensor_id, u
 
 #define CHK_SCALE_SIGMA 0.02f
 #define CHK_BIAS_SIGMA 0.01f
+
+/* Synthetic n-gram table (PLE): head h of the table has
+ * ngram_head_rows - h rows, heads laid out back to back (head_offsets the
+ * running sums); a row holds dim / 8 words of 4-bit codes, then dim / group
+ * bf16 scales, then as many biases (manifest.rs:42-55).  Word j of row r is
+ * element r * dim / 8 + j of the table's word stream; scale / bias g of row
+ * r element r * dim / group + g of its stream.  The hash multipliers are
+ * positive odd 63-bit integers. */
+static inline CHK_HD uint64_t chk_ngram_head_size(uint32_t head_rows, uint32_t h) {
+    return (uint64_t)(head_rows - h);
+}
+
+static inline CHK_HD int64_t chk_ngram_multiplier(uint64_t seed, uint32_t k) {
+    uint64_t key = chk_key(seed, chk_tensor_id(CHK_T_NGRAM_MULT, 0, 0, 0), CHK_STREAM_W);
+    return (int64_t)((chk_draw(key, k) >> 1) | 1u);
+}
+
+static inline CHK_HD uint64_t chk_ngram_row_bytes(uint32_t dim, uint32_t group) {
+    return (uint64_t)dim / 2 + 4ull * (dim / group);
+}
 
 #endif

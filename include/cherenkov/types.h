@@ -10,8 +10,11 @@
  *     (tests/fixtures/qwen4_exp/config.json "full_attention_interval": 4);
  *   - `output_gate_type` must be "sigmoid" (the reference engine refuses any
  *     other, src/qwen4_exp/gpu/load.rs:49-52), so it is not a field.
- * PLE (`ple_layer_ids`) is absent from every configuration this library
- * runs; `ple_layer` must be 0 ("none").
+ * PLE (`ple_layer_ids`, config.rs:36-43): `ple_layer` is the first entry
+ * of ple_layer_ids (1-based, as the config writes it; Qwen4ExpConfig::
+ * ple_layer, config.rs:119-122), 0 for none.  The n-gram table's row group
+ * comes from the store's manifest (manifest.rs:42-55); a synthetic table
+ * has ngram_head_rows - h rows in head h.
  */
 #ifndef CHERENKOV_TYPES_H
 #define CHERENKOV_TYPES_H
@@ -54,12 +57,19 @@ typedef struct ChkConfig {
     /* misc */
     uint32_t mtp_num_hidden_layers;
     uint32_t eos_token_id;
-    uint32_t ple_layer; /* 0 = no PLE block (the only supported value) */
+    uint32_t ple_layer; /* 1-based layer of the PLE block, 0 = none */
     double rms_norm_eps;
     double partial_rotary_factor;
     double rope_theta;
     /* synthetic weights: seed of the counter-hash generator (synth.h) */
     uint64_t seed;
+    /* PLE n-gram block (read when ple_layer != 0) */
+    uint32_t ple_conv_kernel_size; /* dilated depthwise conv taps */
+    uint32_t ple_embed_dim;        /* n-gram embedding width: ids x row dim */
+    uint32_t ngram_size;           /* largest n-gram (3: bigram + trigram heads); the conv dilation */
+    uint32_t heads_per_ngram;
+    uint32_t ngram_group;          /* quantisation group of a table row */
+    uint32_t ngram_head_rows;      /* synthetic table: rows of head 0 */
 } ChkConfig;
 
 /* Expert precision of the routed-expert store (Options::experts,

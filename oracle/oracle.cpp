@@ -24,9 +24,11 @@
 // Parity pins: every function here is checked by tests/test_oracle_*.py
 // against the reference's own known-answer tests (quant.rs, lowbit.rs),
 // against brute force / closed forms (top-k, DeltaNet invariants, attention
-// with one token), or against an independent numpy restatement.  The QSA
-// block selection and PLE are not exercised (dense QSA, no PLE) — see the
-// headers of the functions concerned.
+// with one token), or against an independent numpy restatement; the
+// compositions (gated_residual, moe, deltanet, attention, select_tokens,
+// mtp_forward, forward_token) by closed forms on special weights
+// (tests/test_oracle_compositions.py); PLE (ngram_ids_from, ngram_row, ple)
+// by hand-worked id cases and closed forms (tests/test_oracle_ple.py).
 
 #include <algorithm>
 #include <cmath>
@@ -310,12 +312,28 @@ struct MoeW {
     QStore sh_gate, sh_up, sh_down;
     uint32_t record_layer = 0;
 };
+// PleWeights, src/qwen4_exp/cpu.rs:62-75
+struct PleW {
+    QStore key, value;
+    std::vector<uint16_t> norm_key, norm_query, norm_conv, conv;  // conv [hh][kernel]
+    uint32_t kernel = 0, dilation = 0;
+    std::vector<int64_t> multipliers;
+    std::vector<uint64_t> head_offsets, head_sizes;
+};
+// ngram.bin rows (NgramLayout, src/qwen4_exp/manifest.rs:42-55)
+struct NgramTable {
+    std::vector<uint8_t> bytes;
+    uint64_t rows = 0, row_bytes = 0;
+    uint32_t dim = 0, group = 0;
+};
 struct LayerW {
     HcW attn_hc, mlp_hc;
     bool linear = false;
     AttnW at;
     DeltaW dn;
     MoeW moe;
+    bool has_ple = false;
+    PleW ple;
 };
 
 struct KvCache {
@@ -324,6 +342,11 @@ struct KvCache {
 };
 struct DeltaState {
     std::vector<float> s, conv;
+};
+// PleState, src/qwen4_exp/cpu.rs:302-310: the gvn ring of the dilated conv
+struct PleRing {
+    std::vector<float> hist;  // [span][hh]
+    size_t span = 0, filled = 0;
 };
 
 }  // namespace
@@ -335,6 +358,7 @@ struct OrcState {
     std::vector<DeltaState> delta;
     std::vector<float> last_hyper;
     KvCache mtp_kv;
+    PleRing ple;
 };
 
 struct OrcModel {
@@ -348,6 +372,7 @@ struct OrcModel {
     QStore mtp_fc_e, mtp_fc_h;
     LayerW mtp_layer;
     HcW mtp_mixer;
+    NgramTable ngram;
     // lazily generated Q4 expert records, pack.rs:351-393 layout
     size_t rec_gate_w = 0, rec_up_w = 0, rec_down_w = 0, rec_gate_s = 0, rec_gate_b = 0,
            rec_up_s = 0, rec_up_b = 0, rec_down_s = 0, rec_down_b = 0, rec_bytes = 0, rec_stride = 0;
@@ -411,6 +436,61 @@ void gen_layer(LayerW& L, const ChkConfig& c, uint32_t slot, bool linear, uint32
     gen_qlinear(L.moe.sh_up, sd, chk_tensor_id(CHK_T_MOE_SH_UP, slot, 0, 0), si, h);
     gen_qlinear(L.moe.sh_down, sd, chk_tensor_id(CHK_T_MOE_SH_DOWN, slot, 0, 0), h, si);
     L.moe.record_layer = record_layer;
+}
+
+// The PLE block of decoder layer `slot` (cpu.rs:243-266) and the n-gram
+// table's metadata, from the synthetic generator (synth.h).
+void gen_ple(PleW& P, const ChkConfig& c, uint32_t slot) {
+    const uint64_t sd = c.seed;
+    const uint32_t h = c.hidden_size, hh = h * c.hc_count, E = c.ple_embed_dim;
+    gen_qlinear(P.key, sd, chk_tensor_id(CHK_T_PLE_KEY, slot, 0, 0), hh, E);
+    gen_qlinear(P.value, sd, chk_tensor_id(CHK_T_PLE_VALUE, slot, 0, 0), h, E);
+    P.norm_key = gen_bf16(sd, CHK_T_PLE_NORM_KEY, slot, 0, hh);
+    P.norm_query = gen_bf16(sd, CHK_T_PLE_NORM_QUERY, slot, 0, hh);
+    P.norm_conv = gen_bf16(sd, CHK_T_PLE_NORM_CONV, slot, 0, hh);
+    P.conv = gen_bf16(sd, CHK_T_PLE_CONV, slot, 0, (size_t)hh * c.ple_conv_kernel_size);
+    P.kernel = c.ple_conv_kernel_size;
+    P.dilation = c.ngram_size;
+    const uint32_t heads = (c.ngram_size - 1) * c.heads_per_ngram;
+    P.multipliers.resize(c.ngram_size);
+    for (uint32_t k = 0; k < c.ngram_size; ++k) P.multipliers[k] = chk_ngram_multiplier(sd, k);
+    P.head_offsets.resize(heads);
+    P.head_sizes.resize(heads);
+    uint64_t off = 0;
+    for (uint32_t hd = 0; hd < heads; ++hd) {
+        P.head_sizes[hd] = chk_ngram_head_size(c.ngram_head_rows, hd);
+        P.head_offsets[hd] = off;
+        off += P.head_sizes[hd];
+    }
+}
+
+void gen_ngram(NgramTable& T, const ChkConfig& c, uint64_t rows) {
+    const uint32_t heads = (c.ngram_size - 1) * c.heads_per_ngram;
+    T.dim = c.ple_embed_dim / heads;
+    T.group = c.ngram_group;
+    T.rows = rows;
+    T.row_bytes = chk_ngram_row_bytes(T.dim, T.group);
+    T.bytes.assign(rows * T.row_bytes, 0);
+    const uint64_t id = chk_tensor_id(CHK_T_NGRAM_TABLE, 0, 0, 0);
+    const uint64_t kw = chk_key(c.seed, id, CHK_STREAM_W), ks = chk_key(c.seed, id, CHK_STREAM_S),
+                   kb = chk_key(c.seed, id, CHK_STREAM_B);
+    const uint32_t wpr = T.dim / 8, gpr = T.dim / T.group;
+    uint8_t* base = T.bytes.data();
+    const uint64_t rb = T.row_bytes;
+#pragma omp parallel for schedule(static)
+    for (long r = 0; r < (long)rows; ++r) {
+        uint8_t* rec = base + (uint64_t)r * rb;
+        for (uint32_t j = 0; j < wpr; ++j) {
+            const uint32_t w = chk_q4_word(kw, (uint64_t)r * wpr + j);
+            memcpy(rec + 4 * j, &w, 4);
+        }
+        for (uint32_t g = 0; g < gpr; ++g) {
+            const uint16_t sv = chk_normal_bf16(ks, (uint64_t)r * gpr + g, CHK_SCALE_SIGMA);
+            const uint16_t bv = chk_normal_bf16(kb, (uint64_t)r * gpr + g, CHK_BIAS_SIGMA);
+            memcpy(rec + 4 * wpr + 2 * g, &sv, 2);
+            memcpy(rec + 4 * wpr + 2 * gpr + 2 * g, &bv, 2);
+        }
+    }
 }
 
 }  // namespace
@@ -892,15 +972,133 @@ std::vector<float> attention(const OrcModel& m, const AttnW& w, const float* x, 
     return o;
 }
 
+// CpuModel::ngram_ids_from, src/qwen4_exp/cpu.rs:848-887: the hashed
+// n-gram row ids of the last token of tokens[0..n): bigram heads, then
+// trigram heads.  shifted[k] is the token k back, or EOS when that reaches
+// before the start or the window [t - k, t) holds an EOS; the products wrap
+// like i64 and the head index is the Euclidean remainder.
+std::vector<uint64_t> ngram_ids_from(const ChkConfig& c, const std::vector<int64_t>& mult,
+                                     const std::vector<uint64_t>& offs, const std::vector<uint64_t>& sizes,
+                                     const uint32_t* tokens, size_t n) {
+    const uint32_t eos = c.eos_token_id;
+    const size_t t = n - 1;
+    std::vector<int64_t> shifted(c.ngram_size);
+    for (size_t k = 0; k < c.ngram_size; ++k) {
+        if (k == 0) {
+            shifted[k] = (int64_t)tokens[t];
+            continue;
+        }
+        bool before = t < k;
+        for (size_t j = before ? t : t - k; j < t; ++j) before = before || tokens[j] == eos;
+        shifted[k] = before ? (int64_t)eos : (int64_t)tokens[t - k];
+    }
+    std::vector<uint64_t> ids;
+    for (size_t ng = 2; ng <= c.ngram_size; ++ng) {
+        uint64_t mixed = (uint64_t)shifted[0] * (uint64_t)mult[0];
+        for (size_t p = 1; p < ng; ++p) mixed ^= (uint64_t)shifted[p] * (uint64_t)mult[p];
+        const int64_t mx = (int64_t)mixed;
+        const size_t start = (ng - 2) * c.heads_per_ngram;
+        for (size_t h = start; h < start + c.heads_per_ngram; ++h) {
+            const int64_t size = (int64_t)sizes[h];
+            int64_t r = mx % size;
+            if (r < 0) r += size;
+            ids.push_back((uint64_t)r + offs[h]);
+        }
+    }
+    return ids;
+}
+
+// Packed::ngram_row, src/qwen4_exp/packed.rs:233-256
+void ngram_row(const NgramTable& T, uint64_t id, float* dst) {
+    if (id >= T.rows) throw std::runtime_error("n-gram id beyond the table");
+    const uint8_t* rec = T.bytes.data() + id * T.row_bytes;
+    const size_t wb = T.dim / 2, sb = T.dim / T.group * 2;
+    for (size_t i = 0; i < T.dim; ++i) {
+        const uint32_t word = rd32(rec + i / 8 * 4);
+        const uint32_t q = (word >> (4 * (i % 8))) & 0xF;
+        const size_t gi = i / T.group;
+        const float sc = bf((uint16_t)(rec[wb + 2 * gi] | rec[wb + 2 * gi + 1] << 8));
+        const float bi = bf((uint16_t)(rec[wb + sb + 2 * gi] | rec[wb + sb + 2 * gi + 1] << 8));
+        dst[i] = sc * (float)q + bi;
+    }
+}
+
+// CpuModel::ple, src/qwen4_exp/cpu.rs:889-967: the n-gram embedding of the
+// current (last) token, key / value projections, per-stream gating of the
+// value by sigmoid(sign(dot) sqrt(max(|dot|, 1e-6))) with dot = key_g .
+// query_g / sqrt(h), the gated value's grouped RMSNorm (gvn), and the
+// dilated causal depthwise conv over the gvn ring with SiLU, added to the
+// gated value.  Returns the hc * h addend; `gvn_out` (optional) receives gvn.
+std::vector<float> ple(const OrcModel& m, const PleW& w, const float* hyper, OrcState& st,
+                       std::vector<float>* gvn_out) {
+    const ChkConfig& c = m.c;
+    const size_t h = c.hidden_size, hc = c.hc_count, hh = h * hc;
+    const float eps = (float)c.rms_norm_eps;
+    const size_t dim = m.ngram.dim;
+    const std::vector<uint64_t> ids =
+        ngram_ids_from(c, w.multipliers, w.head_offsets, w.head_sizes, st.tokens.data(), st.tokens.size());
+    if (ids.size() * dim != c.ple_embed_dim) throw std::runtime_error("n-gram head layout mismatch");
+    std::vector<float> e(c.ple_embed_dim, 0.0f);
+    for (size_t hi = 0; hi < ids.size(); ++hi) ngram_row(m.ngram, ids[hi], e.data() + hi * dim);
+    std::vector<float> key(w.key.view.out);
+    matvec(w.key.view, e.data(), key.data());
+    key = grouped_rms_norm(key.data(), w.norm_key.data(), key.size(), h, eps);
+    std::vector<float> value(w.value.view.out);
+    matvec(w.value.view, e.data(), value.data());
+    const std::vector<float> query = grouped_rms_norm(hyper, w.norm_query.data(), hh, h, eps);
+    std::vector<float> gated(hh);
+    for (size_t g = 0; g < hc; ++g) {
+        // Iterator::sum over f32 starts from -0.0 (Rust 1.98, the reference's
+        // toolchain); only an all-(-0.0) sum keeps the sign
+        float dot = -0.0f;
+        for (size_t i = 0; i < h; ++i) dot += key[g * h + i] * query[g * h + i];
+        dot /= sqrtf((float)h);
+        const float gate = sqrtf(fmaxf(fabsf(dot), 1e-6f)) * copysignf(1.0f, dot);
+        const float sg = sigmoid(gate);
+        for (size_t i = 0; i < h; ++i) gated[g * h + i] = sg * value[i];
+    }
+    const std::vector<float> gvn = grouped_rms_norm(gated.data(), w.norm_conv.data(), hh, h, eps);
+    PleRing& ps = st.ple;
+    if (ps.span == 0) throw std::runtime_error("PLE state missing");
+    const size_t span = ps.span, K = w.kernel;
+    std::vector<float> out = gated;
+    for (size_t ch = 0; ch < hh; ++ch) {
+        const uint16_t* wrow = w.conv.data() + ch * K;
+        float acc = bf(wrow[K - 1]) * gvn[ch];
+        for (size_t k = 0; k + 1 < K; ++k) {
+            const size_t back = (size_t)w.dilation * (K - 1 - k);
+            if (back <= ps.filled) {
+                const size_t slot = (ps.filled - back) % span;
+                acc += bf(wrow[k]) * ps.hist[slot * hh + ch];
+            }
+        }
+        out[ch] += silu(acc);
+    }
+    const size_t slot = ps.filled % span;
+    std::copy(gvn.begin(), gvn.end(), ps.hist.begin() + slot * hh);
+    ps.filled += 1;
+    if (gvn_out) *gvn_out = gvn;
+    return out;
+}
+
 }  // namespace orc
 
 // ---------------------------------------------------------------- model
 static bool validate(const ChkConfig& c) {
     if (c.hidden_size == 0 || c.hidden_size % 64 || c.hc_count < 2 || c.hc_lowrank % 64 ||
         c.moe_intermediate_size % 64 || c.shared_expert_intermediate_size % 64 ||
-        c.full_attention_interval == 0 || c.ple_layer != 0) {
+        c.full_attention_interval == 0 || c.ple_layer > c.num_hidden_layers) {
         g_err = "unsupported configuration";
         return false;
+    }
+    if (c.ple_layer) {
+        const uint32_t heads = c.ngram_size >= 2 ? (c.ngram_size - 1) * c.heads_per_ngram : 0;
+        if (heads == 0 || c.ple_embed_dim % 64 || c.ple_embed_dim % heads || c.ple_conv_kernel_size < 2 ||
+            c.ngram_group == 0 || (c.ple_embed_dim / heads) % 8 || (c.ple_embed_dim / heads) % c.ngram_group ||
+            c.ngram_head_rows <= heads) {
+            g_err = "unsupported PLE configuration";
+            return false;
+        }
     }
     return true;
 }
@@ -923,6 +1121,14 @@ struct OrcModel* make_model(const ChkConfig* cfg, uint32_t bits) {
     gen_qlinear(m->lm_head, c.seed, chk_tensor_id(CHK_T_LM_HEAD, 0, 0, 0), c.vocab_size, H);
     m->layers.resize(L);
     for (uint32_t l = 0; l < L; ++l) gen_layer(m->layers[l], c, l, m->is_linear(l), l);
+    if (c.ple_layer) {
+        LayerW& PL = m->layers[c.ple_layer - 1];
+        PL.has_ple = true;
+        gen_ple(PL.ple, c, c.ple_layer - 1);
+        uint64_t rows = 0;
+        for (uint64_t v : PL.ple.head_sizes) rows += v;
+        gen_ngram(m->ngram, c, rows);
+    }
     gen_hc(m->final_mixer, c, 0, CHK_HC_FINAL, false);
     m->has_mtp = c.mtp_num_hidden_layers > 0;
     if (m->has_mtp) {
@@ -984,6 +1190,10 @@ void* orc_state_new(void* mp) {
             st->kv.emplace_back();
         }
     }
+    if (c.ple_layer) {
+        st->ple.span = (size_t)(c.ple_conv_kernel_size - 1) * c.ngram_size;
+        st->ple.hist.assign(st->ple.span * c.hc_count * c.hidden_size, 0.0f);
+    }
     return st;
 }
 
@@ -1034,7 +1244,6 @@ int orc_forward_token(void* mp, void* sp, uint32_t token, int kv_q8, float* logi
     try {
         if (token >= c.vocab_size) throw std::runtime_error("token out of range");
         size_t h = c.hidden_size, hc = c.hc_count, hh = h * hc;
-        float eps = (float)c.rms_norm_eps;
         std::vector<float> e(h);
         dequant_row(m->embed.view, token, e.data());
         std::vector<float> hyper(hh);
@@ -1043,6 +1252,10 @@ int orc_forward_token(void* mp, void* sp, uint32_t token, int kv_q8, float* logi
         size_t kv_idx = 0, delta_idx = 0;
         std::vector<float> mixed, inj;
         for (auto& layer : m->layers) {
+            if (layer.has_ple) {
+                const std::vector<float> add = orc::ple(*m, layer.ple, hyper.data(), *st, nullptr);
+                for (size_t i = 0; i < hh; ++i) hyper[i] += add[i];
+            }
             orc::gated_residual(*m, layer.attn_hc, hyper.data(), mixed, inj);
             std::vector<float> out;
             if (layer.linear) out = orc::deltanet(*m, layer.dn, mixed.data(), st->delta[delta_idx++]);
@@ -1334,6 +1547,10 @@ static QStore* q4_of(OrcModel* m, uint32_t layer, const std::string& name) {
         if (t == "o") return &L->at.o;
         if (t == "idx") return &L->at.idx;
     }
+    if (grp == "ple" && L->has_ple) {
+        if (t == "key") return &L->ple.key;
+        if (t == "value") return &L->ple.value;
+    }
     if (grp == "moe") {
         if (t == "sh_gate") return &L->moe.sh_gate;
         if (t == "sh_up") return &L->moe.sh_up;
@@ -1362,6 +1579,12 @@ static std::vector<uint16_t>* bf16_of(OrcModel* m, uint32_t layer, const std::st
         if (t == "k_norm") return &L->at.k_norm;
         if (t == "idx_q_norm") return &L->at.idx_q_norm;
         if (t == "idx_k_norm") return &L->at.idx_k_norm;
+    }
+    if (grp == "ple" && L->has_ple) {
+        if (t == "norm_key") return &L->ple.norm_key;
+        if (t == "norm_query") return &L->ple.norm_query;
+        if (t == "norm_conv") return &L->ple.norm_conv;
+        if (t == "conv") return &L->ple.conv;
     }
     if (grp == "moe") {
         if (t == "router") return &L->moe.router;
@@ -1425,6 +1648,101 @@ int orc_get_bf16(void* mp, uint32_t layer, const char* name, uint16_t* v, uint64
         return -1;
     }
     std::copy(t->begin(), t->end(), v);
+    return 0;
+}
+
+// ---- PLE ----
+static PleW* ple_of(OrcModel* m) {
+    if (!m->c.ple_layer) {
+        g_err = "the model has no PLE block";
+        return nullptr;
+    }
+    return &m->layers[m->c.ple_layer - 1].ple;
+}
+
+// ngram_ids_from over tokens[0..n) (the ids of its last token); cap >= the
+// number of heads
+int orc_ngram_ids(void* mp, const uint32_t* tokens, uint32_t n, uint64_t* ids, uint32_t cap, uint32_t* n_ids) {
+    OrcModel* m = (OrcModel*)mp;
+    PleW* P = ple_of(m);
+    if (!P) return -1;
+    if (n == 0) {
+        g_err = "no tokens";
+        return -1;
+    }
+    const std::vector<uint64_t> v =
+        orc::ngram_ids_from(m->c, P->multipliers, P->head_offsets, P->head_sizes, tokens, n);
+    if (v.size() > cap) {
+        g_err = "id buffer too small";
+        return -1;
+    }
+    std::copy(v.begin(), v.end(), ids);
+    *n_ids = (uint32_t)v.size();
+    return 0;
+}
+
+// The PLE block alone for the next token: appends `token` to the state's
+// history, runs CpuModel::ple on `hyper` (hc * h), writes the addend and
+// gvn (each hc * h) and advances the ring; the position is untouched.
+int orc_ple(void* mp, void* sp, uint32_t token, const float* hyper, float* add, float* gvn) {
+    OrcModel* m = (OrcModel*)mp;
+    OrcState* st = (OrcState*)sp;
+    PleW* P = ple_of(m);
+    if (!P) return -1;
+    try {
+        st->tokens.push_back(token);
+        std::vector<float> g;
+        const std::vector<float> a = orc::ple(*m, *P, hyper, *st, &g);
+        std::copy(a.begin(), a.end(), add);
+        std::copy(g.begin(), g.end(), gvn);
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return -1;
+    }
+}
+
+// The hash metadata (multipliers [ngram_size], head offsets and sizes
+// [heads]): copied out, or replaced when `set`.
+int orc_ngram_meta(void* mp, int64_t* mult, uint64_t* offs, uint64_t* sizes, int set) {
+    OrcModel* m = (OrcModel*)mp;
+    PleW* P = ple_of(m);
+    if (!P) return -1;
+    if (set) {
+        std::copy(mult, mult + P->multipliers.size(), P->multipliers.begin());
+        std::copy(offs, offs + P->head_offsets.size(), P->head_offsets.begin());
+        std::copy(sizes, sizes + P->head_sizes.size(), P->head_sizes.begin());
+    } else {
+        std::copy(P->multipliers.begin(), P->multipliers.end(), mult);
+        std::copy(P->head_offsets.begin(), P->head_offsets.end(), offs);
+        std::copy(P->head_sizes.begin(), P->head_sizes.end(), sizes);
+    }
+    return 0;
+}
+
+uint64_t orc_ngram_table_bytes(void* mp) { return ((OrcModel*)mp)->ngram.bytes.size(); }
+
+// Packed::ngram_row of table row `id` (dim floats).
+int orc_ngram_row(void* mp, uint64_t id, float* dst) {
+    try {
+        orc::ngram_row(((OrcModel*)mp)->ngram, id, dst);
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return -1;
+    }
+}
+
+// The n-gram table's bytes (ngram.bin layout): copied out, or replaced
+// when `set` (n must be the table's size).
+int orc_ngram_table(void* mp, uint8_t* buf, uint64_t n, int set) {
+    OrcModel* m = (OrcModel*)mp;
+    if (n != m->ngram.bytes.size()) {
+        g_err = "n-gram table size mismatch";
+        return -1;
+    }
+    if (set) std::copy(buf, buf + n, m->ngram.bytes.begin());
+    else std::copy(m->ngram.bytes.begin(), m->ngram.bytes.end(), buf);
     return 0;
 }
 

@@ -60,6 +60,12 @@ _SIGS = [
     ("orc_set_record", i32, [P, u32, u32, P, u64]),
     ("orc_get_q4", i32, [P, u32, C.c_char_p, P, P, P, u64]),
     ("orc_get_bf16", i32, [P, u32, C.c_char_p, P, u64]),
+    ("orc_ngram_ids", i32, [P, P, u32, P, u32, P]),
+    ("orc_ple", i32, [P, P, u32, P, P, P]),
+    ("orc_ngram_meta", i32, [P, P, P, P, i32]),
+    ("orc_ngram_table_bytes", u64, [P]),
+    ("orc_ngram_row", i32, [P, u64, P]),
+    ("orc_ngram_table", i32, [P, P, u64, i32]),
 ]
 
 _lib = None
@@ -171,6 +177,50 @@ class OracleModel:
         rec = np.ascontiguousarray(rec, dtype=np.uint8)
         _check(self.L.orc_set_record(self.h, record_layer, e, _p(rec), rec.size))
 
+    # ---- PLE ----
+    def ngram_heads(self) -> int:
+        c = self.cfg
+        return (c.ngram_size - 1) * c.heads_per_ngram
+
+    def ngram_ids(self, tokens) -> np.ndarray:
+        """ngram_ids_from: the row ids of the last of `tokens`."""
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        out = np.empty(64, np.uint64)
+        n = C.c_uint32()
+        _check(self.L.orc_ngram_ids(self.h, _p(t), t.size, _p(out), out.size, C.byref(n)))
+        return out[: n.value].copy()
+
+    def ngram_meta(self):
+        """(multipliers int64 [ngram_size], head offsets, head sizes uint64 [heads])."""
+        mult = np.empty(self.cfg.ngram_size, np.int64)
+        offs = np.empty(self.ngram_heads(), np.uint64)
+        sizes = np.empty(self.ngram_heads(), np.uint64)
+        _check(self.L.orc_ngram_meta(self.h, _p(mult), _p(offs), _p(sizes), 0))
+        return mult, offs, sizes
+
+    def set_ngram_meta(self, mult, offs, sizes) -> None:
+        mult = np.ascontiguousarray(mult, dtype=np.int64)
+        offs = np.ascontiguousarray(offs, dtype=np.uint64)
+        sizes = np.ascontiguousarray(sizes, dtype=np.uint64)
+        assert mult.size == self.cfg.ngram_size and offs.size == sizes.size == self.ngram_heads()
+        _check(self.L.orc_ngram_meta(self.h, _p(mult), _p(offs), _p(sizes), 1))
+
+    def ngram_table(self) -> np.ndarray:
+        n = self.L.orc_ngram_table_bytes(self.h)
+        out = np.empty(n, np.uint8)
+        _check(self.L.orc_ngram_table(self.h, _p(out), n, 0))
+        return out
+
+    def ngram_row(self, row: int) -> np.ndarray:
+        c = self.cfg
+        out = np.empty(c.ple_embed_dim // self.ngram_heads(), np.float32)
+        _check(self.L.orc_ngram_row(self.h, row, _p(out)))
+        return out
+
+    def set_ngram_table(self, t: np.ndarray) -> None:
+        t = np.ascontiguousarray(t, dtype=np.uint8)
+        _check(self.L.orc_ngram_table(self.h, _p(t), t.size, 1))
+
 
 class OracleState:
     def __init__(self, m: OracleModel):
@@ -229,6 +279,16 @@ class OracleState:
         out = np.empty(self.m.cfg.hidden_size, np.float32)
         _check(self.m.L.orc_attention(self.m.h, self.h, layer, _p(x), pos, int(kv_q8), _p(out)))
         return out
+
+    def ple(self, token: int, hyper: np.ndarray):
+        """The PLE block for the next token (appended to the history) on
+        `hyper`: (addend, gvn), each hc * hidden."""
+        c = self.m.cfg
+        hyper = np.ascontiguousarray(hyper, dtype=np.float32)
+        add = np.empty(c.hidden_size * c.hc_count, np.float32)
+        gvn = np.empty_like(add)
+        _check(self.m.L.orc_ple(self.m.h, self.h, token, _p(hyper), _p(add), _p(gvn)))
+        return add, gvn
 
 
 # ---- primitives ----

@@ -16,7 +16,11 @@ src/qwen4_exp/packed.rs:66-231):
                  record_stride, fields gate_w, up_w, down_w, gate_s,
                  gate_b, up_s, up_b, down_s, down_b (pack.rs:351-393),
                  the stride padded to 16 KiB pages;
-  ngram.bin      empty (no PLE layer).
+  ngram.bin      the n-gram table's rows (weight | scales | biases) of a
+                 PLE layer, else empty; its hash metadata are I64 dense
+                 tensors {layer}.ple.ple_embedding.{layer_multipliers,
+                 ngram_heads_offsets, ngram_heads_vocab_sizes}
+                 (packed.rs:134-148, 233-256; pack.rs:476-592).
 Tensor names follow src/qwen4_exp/cpu.rs:143-272.
 """
 
@@ -91,6 +95,17 @@ def _names(cfg) -> list[tuple[str, str, int, str, tuple]]:
 
     for l in range(L):
         layer(f"{m}.layers.{l}", l, (l + 1) % c.full_attention_interval != 0)
+        if c.ple_layer == l + 1:
+            p = f"{m}.layers.{l}.ple"
+            E, K = c.ple_embed_dim, c.ple_conv_kernel_size
+            out.extend([
+                (f"{p}.key_proj", "q4", l, "ple.key", (hh, E)),
+                (f"{p}.value_proj", "q4", l, "ple.value", (H, E)),
+                (f"{p}.norm_key.weight", "bf16", l, "ple.norm_key", (hh,)),
+                (f"{p}.norm_query.weight", "bf16", l, "ple.norm_query", (hh,)),
+                (f"{p}.norm_conv.weight", "bf16", l, "ple.norm_conv", (hh,)),
+                (f"{p}.conv1d.weight", "bf16", l, "ple.conv", (hh, 1, K)),
+            ])
     hc_block(f"{m}.hyper_connection_mixer", "final", 0, False)
     if c.mtp_num_hidden_layers:
         out.extend([
@@ -120,7 +135,9 @@ def text_config(cfg) -> dict:
         "hc_count": c.hc_count, "hc_lowrank": c.hc_lowrank, "num_experts": c.num_experts,
         "num_experts_per_tok": c.num_experts_per_tok, "moe_intermediate_size": c.moe_intermediate_size,
         "shared_expert_intermediate_size": c.shared_expert_intermediate_size,
-        "norm_topk_prob": bool(c.norm_topk_prob), "ple_layer_ids": [], "ple_embed_dim": 0,
+        "norm_topk_prob": bool(c.norm_topk_prob), "ple_layer_ids": [c.ple_layer] if c.ple_layer else [],
+        "ple_embed_dim": c.ple_embed_dim, "ple_conv_kernel_size": c.ple_conv_kernel_size,
+        "ngram_size": c.ngram_size, "heads_per_ngram": c.heads_per_ngram,
         "indexer_n_heads": c.indexer_n_heads, "indexer_kv_heads": 1, "indexer_head_dim": c.indexer_head_dim,
         "indexer_budget": c.indexer_budget, "indexer_compress_ratio": c.indexer_compress_ratio,
         "output_gate_type": "sigmoid", "eos_token_id": c.eos_token_id,
@@ -160,6 +177,30 @@ def write_store(cfg, path, shuffle_dense: bool = True, field_order: tuple | None
             entries.append({"name": name + suffix, "dtype": dtype, "shape": shp, "offset": off, "nbytes": len(data)})
             chunks.append(data)
             off += len(data)
+    ngram = {"rows": 0, "row_bytes": 0, "dim": 0, "group": 64, "weight_bytes": 0, "scale_bytes": 0,
+             "head_offsets": [], "head_vocab_sizes": [], "layer_multipliers": []}
+    table = b""
+    if c.ple_layer:
+        mult, offs, sz = orc.ngram_meta()
+        pre = f"language_model.model.layers.{c.ple_layer - 1}.ple.ple_embedding"
+        for leaf, arr in (("layer_multipliers", mult), ("ngram_heads_offsets", offs.astype(np.int64)),
+                          ("ngram_heads_vocab_sizes", sz.astype(np.int64))):
+            data = np.ascontiguousarray(arr, dtype="<i8").tobytes()
+            pad = (-off) % 64
+            chunks.append(b"\0" * pad)
+            off += pad
+            entries.append({"name": f"{pre}.{leaf}", "dtype": "I64", "shape": [len(arr)], "offset": off,
+                            "nbytes": len(data)})
+            chunks.append(data)
+            off += len(data)
+        dim = c.ple_embed_dim // orc.ngram_heads()
+        table = orc.ngram_table().tobytes()
+        wb, sb = dim // 2, dim // c.ngram_group * 2
+        # the manifest keeps copies of the metadata; readers use the dense
+        # tensors (packed.rs:134-148), so these copies are deliberately off
+        ngram = {"rows": len(table) // (wb + 2 * sb), "row_bytes": wb + 2 * sb, "dim": dim, "group": c.ngram_group,
+                 "weight_bytes": wb, "scale_bytes": sb, "head_offsets": [0] * len(offs),
+                 "head_vocab_sizes": [1] * len(sz), "layer_multipliers": [0] * len(mult)}
     (path / "dense.bin").write_bytes(b"".join(chunks))
     # experts: main layers then the MTP layer
     I, H = c.moe_intermediate_size, c.hidden_size
@@ -192,15 +233,14 @@ def write_store(cfg, path, shuffle_dense: bool = True, field_order: tuple | None
                 for k in order:
                     out[dst_off[k]:dst_off[k] + sizes[k]] = rec[src_off[k]:src_off[k] + sizes[k]]
                 f.write(out.tobytes())
-    (path / "ngram.bin").write_bytes(b"")
+    (path / "ngram.bin").write_bytes(table)
     manifest = {
         "version": 1,
         "source_dir": "synthetic (seed %d)" % c.seed,
         "dense": entries,
         "experts": {"layers": len(prefixes), "experts": c.num_experts, "inter": I, "hidden": H, "group": 64,
                     "record_bytes": rec_bytes, "record_stride": stride, "layer_prefixes": prefixes, **dst_off},
-        "ngram": {"rows": 0, "row_bytes": 0, "dim": 0, "group": 64, "weight_bytes": 0, "scale_bytes": 0,
-                  "head_offsets": [], "head_vocab_sizes": [], "layer_multipliers": []},
+        "ngram": ngram,
     }
     (path / "manifest.json").write_text(json.dumps(manifest, indent=1))
     (path / "config.json").write_text(json.dumps({"model_type": "qwen4_exp", "text_config": text_config(cfg)},

@@ -52,8 +52,8 @@ def test_python_signatures_match_headers():
 def test_load_validates_before_touching_the_device():
     """Configs the kernels cannot run are refused by chk_engine_load before
     any device call (so this runs without a GPU): hidden sizes above 2048
-    (one 32-input chunk per lane in the batch-1 expert kernels), PLE layers,
-    more than 3 drafts."""
+    (one 32-input chunk per lane in the batch-1 expert kernels), more than
+    3 drafts, PLE blocks the kernels cannot lay out."""
     if not abi.LIB_PATH.exists():
         pytest.skip("libcherenkov.so not built (run __graft_entry__.build())")
     from cherenkov_amd import presets
@@ -67,6 +67,14 @@ def test_load_validates_before_touching_the_device():
     cases.append((c, abi.ChkOptions(4, 4, 64, 0), "drafts must be 0..=3"))
     c = presets.tiny()
     cases.append((c, abi.ChkOptions(5, 0, 64, 0), "expert precision"))
+    c = presets.with_ple(presets.tiny(), layer=5)
+    cases.append((c, abi.ChkOptions(4, 0, 64, 0), "ple_layer_ids beyond the decoder layers"))
+    c = presets.with_ple(presets.tiny(), heads_per_ngram=17)
+    cases.append((c, abi.ChkOptions(4, 0, 64, 0), "at most 32 n-gram heads"))
+    c = presets.with_ple(presets.tiny(), embed_dim=272)
+    cases.append((c, abi.ChkOptions(4, 0, 64, 0), "ple_embed_dim must be a multiple of 64"))
+    c = presets.with_ple(presets.tiny(), kernel=2, ngram_size=1)
+    cases.append((c, abi.ChkOptions(4, 0, 64, 0), "n-gram orders"))
     for cfg, opt, msg in cases:
         h = C.c_void_p()
         rc = L.chk_engine_load(C.byref(cfg), C.byref(opt), C.byref(h))

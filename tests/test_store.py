@@ -42,6 +42,43 @@ def test_store_config_matches_the_model(tiny_store):
     assert got2.hidden_size == cfg.hidden_size
 
 
+def test_store_config_with_a_ple_layer(tmp_path):
+    """ple_layer_ids, the PLE widths and the manifest's n-gram row group
+    reach the config (the synthetic table's head_rows is not a store
+    field)."""
+    if not abi.LIB_PATH.exists():
+        pytest.skip("libcherenkov.so not built")
+    cfg = presets.with_ple(presets.tiny(mtp=0), layer=2, group=8)
+    path = write_store(cfg, tmp_path / "s")
+    rc, got, err = store_config(path)
+    assert rc == 0, err
+    for k, _ in cfg._fields_:
+        if k not in ("seed", "ngram_head_rows"):
+            assert getattr(got, k) == getattr(cfg, k), k
+    assert got.ngram_group == 8
+
+
+@pytest.mark.parametrize("case,msg", [
+    ("row_bytes", "n-gram row layout is inconsistent"),
+    ("no_ngram", "manifest has no n-gram layout"),
+    ("no_embed_dim", "ple_embed_dim"),
+])
+def test_malformed_ple_stores_are_refused(tmp_path, case, msg):
+    if not abi.LIB_PATH.exists():
+        pytest.skip("libcherenkov.so not built")
+    cfg = presets.with_ple(presets.tiny(mtp=0), layer=2)
+    path = write_store(cfg, tmp_path / "s")
+    edits = {
+        "row_bytes": ("manifest.json", lambda d: d["ngram"].update(row_bytes=d["ngram"]["row_bytes"] + 4)),
+        "no_ngram": ("manifest.json", lambda d: d.pop("ngram")),
+        "no_embed_dim": ("config.json", lambda d: d["text_config"].pop("ple_embed_dim")),
+    }
+    fname, fn = edits[case]
+    _edit(path, fname, fn)
+    rc, _, err = store_config(path)
+    assert rc != 0 and msg in err, err
+
+
 def _edit(path, fname, fn):
     p = path / fname
     d = json.loads(p.read_text())
