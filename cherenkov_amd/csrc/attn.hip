@@ -124,6 +124,47 @@ CHK_DEV bool qsa_selective(const AttnArgs& a, uint32_t b, uint32_t& nblk) {
 constexpr uint32_t QSA_BPW = 8;
 constexpr uint32_t QSA_BPG = QSA_BPW * (CHK_WG / 64);
 
+// The pooled key of block blk (cpu.rs:687-697): mean of its `ratio` index
+// keys, rms_norm(index_k_norm), rope at blk * ratio; lane l ends with dims
+// l + 64 i in x[i], and the key is stored in block_k.
+template <int DPL>
+CHK_DEV void qsa_block_key(const AttnArgs& a, const KvDev& kv, uint32_t blk, uint32_t lane, float (&x)[DPL]) {
+    const uint32_t half = a.rot / 2;
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) {
+        const uint32_t d = lane + 64 * i;
+        float p = 0.0f;
+        for (uint32_t tk = blk * a.ratio; tk < (blk + 1) * a.ratio; ++tk) p += kv.index_k[(size_t)tk * a.ihd + d];
+        x[i] = p / (float)a.ratio;
+        ss += x[i] * x[i];
+    }
+    const float inv = 1.0f / sqrtf(wave_sum(ss) / (float)a.ihd + a.eps);
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) x[i] = x[i] * inv * bf16f(a.ik_norm[lane + 64 * i]);
+    // rot <= 64: pair (j, j + half) sits in lanes (l, l ^ half) of slot 0
+    const float other = __shfl_xor(x[0], (int)half, 64);
+    if (lane < a.rot) {
+        const uint32_t jj = lane < half ? lane : lane - half;
+        const float inv_freq = powf(a.theta, -(2.0f * (float)jj) / (float)a.rot);
+        const float ang = (float)(blk * a.ratio) * inv_freq;
+        const float sn = sinf(ang), cs = cosf(ang);
+        x[0] = lane < half ? x[0] * cs - other * sn : x[0] * cs + other * sn;
+    }
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) kv.block_k[(size_t)blk * a.ihd + lane + 64 * i] = x[i];
+}
+
+// Block keys of blocks [blk0, blk1) (their index keys all appended): a
+// prefill chunk's completed blocks, one wave per block.
+template <int DPL>
+__global__ void __launch_bounds__(256) k_qsa_block_keys(AttnArgs a, uint32_t blk0, uint32_t blk1) {
+    const uint32_t blk = blk0 + blockIdx.x * (CHK_WG / 64) + wave_id(), lane = threadIdx.x & 63;
+    if (blk >= blk1) return;
+    float x[DPL];
+    qsa_block_key<DPL>(a, a.kv[0], blk, lane, x);
+}
+
 template <int DPL>
 __global__ void __launch_bounds__(256) k_qsa_score(AttnArgs a) {
     __shared__ float sq[8 * 256];
@@ -135,7 +176,6 @@ __global__ void __launch_bounds__(256) k_qsa_score(AttnArgs a) {
     if (sel)
         for (uint32_t i = t; i < a.inh * a.ihd; i += CHK_WG) sq[i] = a.iq_ready[(size_t)b * a.inh * a.ihd + i];
     __syncthreads();
-    const uint32_t half = a.rot / 2;
     for (uint32_t j = 0; j < QSA_BPW; ++j) {
         const uint32_t blk = blockIdx.x * QSA_BPG + w * QSA_BPW + j;
         if (blk >= nblk) break;
@@ -143,30 +183,7 @@ __global__ void __launch_bounds__(256) k_qsa_score(AttnArgs a) {
         if (!fresh && !sel) continue;
         float x[DPL];
         if (fresh) {
-            // pooled mean, rms_norm(index_k_norm), rope at blk * ratio (cpu.rs:687-697)
-            float ss = 0.0f;
-#pragma unroll
-            for (int i = 0; i < DPL; ++i) {
-                const uint32_t d = lane + 64 * i;
-                float p = 0.0f;
-                for (uint32_t tk = blk * a.ratio; tk < (blk + 1) * a.ratio; ++tk) p += kv.index_k[(size_t)tk * a.ihd + d];
-                x[i] = p / (float)a.ratio;
-                ss += x[i] * x[i];
-            }
-            const float inv = 1.0f / sqrtf(wave_sum(ss) / (float)a.ihd + a.eps);
-#pragma unroll
-            for (int i = 0; i < DPL; ++i) x[i] = x[i] * inv * bf16f(a.ik_norm[lane + 64 * i]);
-            // rot <= 64: pair (j, j + half) sits in lanes (l, l ^ half) of slot 0
-            const float other = __shfl_xor(x[0], (int)half, 64);
-            if (lane < a.rot) {
-                const uint32_t jj = lane < half ? lane : lane - half;
-                const float inv_freq = powf(a.theta, -(2.0f * (float)jj) / (float)a.rot);
-                const float ang = (float)(blk * a.ratio) * inv_freq;
-                const float sn = sinf(ang), cs = cosf(ang);
-                x[0] = lane < half ? x[0] * cs - other * sn : x[0] * cs + other * sn;
-            }
-#pragma unroll
-            for (int i = 0; i < DPL; ++i) kv.block_k[(size_t)blk * a.ihd + lane + 64 * i] = x[i];
+            qsa_block_key<DPL>(a, kv, blk, lane, x);
         } else {
 #pragma unroll
             for (int i = 0; i < DPL; ++i) x[i] = kv.block_k[(size_t)blk * a.ihd + lane + 64 * i];
@@ -575,7 +592,9 @@ void launch_attn_prep(const AttnArgs& a, int nb, hipStream_t st) {
 // (their block keys are still cached as blocks complete).
 void launch_qsa(const AttnArgs& a, int nb, hipStream_t st) {
     if (!a.qsa) return;
-    if (a.ihd % 64 || a.ihd > 256 || a.rot > 64 || a.rot > a.ihd || (a.rot & (a.rot - 1)) || a.rot < 2 ||
+    // DPL = ihd / 64 dims per lane: 1, 2 or 4 (no 3-dim instantiation)
+    if ((a.ihd != 64 && a.ihd != 128 && a.ihd != 256) || a.rot > 64 || a.rot > a.ihd || (a.rot & (a.rot - 1)) ||
+        a.rot < 2 ||
         a.inh * a.ihd > 8 * 256 ||
         a.mask_words > QSA_MAX_WORDS || !a.iq_ready || !a.bscore || !a.vmask || !a.kv[0].block_k)
         throw std::runtime_error("QSA indexer shape not supported");
@@ -586,6 +605,18 @@ void launch_qsa(const AttnArgs& a, int nb, hipStream_t st) {
     default: k_qsa_score<4><<<grid, CHK_WG, 0, st>>>(a); break;
     }
     k_qsa_select<<<nb, QSA_SEL_WG, 0, st>>>(a);
+}
+
+void launch_qsa_block_keys(const AttnArgs& a, uint32_t blk0, uint32_t blk1, hipStream_t st) {
+    if (blk1 <= blk0) return;
+    if ((a.ihd != 64 && a.ihd != 128 && a.ihd != 256) || a.rot > 64 || !a.kv[0].block_k)
+        throw std::runtime_error("QSA indexer shape not supported");
+    const uint32_t grid = (blk1 - blk0 + CHK_WG / 64 - 1) / (CHK_WG / 64);
+    switch (a.ihd / 64) {
+    case 1: k_qsa_block_keys<1><<<grid, CHK_WG, 0, st>>>(a, blk0, blk1); break;
+    case 2: k_qsa_block_keys<2><<<grid, CHK_WG, 0, st>>>(a, blk0, blk1); break;
+    default: k_qsa_block_keys<4><<<grid, CHK_WG, 0, st>>>(a, blk0, blk1); break;
+    }
 }
 
 void launch_qsa_select(const AttnArgs& a, int nb, hipStream_t st) {

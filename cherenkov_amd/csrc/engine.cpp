@@ -154,6 +154,11 @@ struct PfBufs {
     // the normed trunk streams, fc_e / fc_h outputs and the head's residual
     uint32_t* mtp_tok;
     float *mtp_en, *mtp_hn, *mtp_fe, *mtp_fh, *mtp_hyper;
+    // QSA past the budget: every row's index queries; scores, selections
+    // and attention partials of qsa_rows rows at a time
+    float *iq_ready, *qsa_bscore, *qsa_part;
+    uint32_t* qsa_vmask;
+    uint32_t qsa_rows;
     // PLE over a chunk: table rows of each row's token, then as Scratch
     uint32_t* ple_ids;
     float *ple_e, *ple_key, *ple_value, *ple_gated, *ple_gvn;
@@ -1379,6 +1384,7 @@ struct ChkEngine {
     uint32_t prefill_rows_fit(bool all_logits) const;
     // ------------------------------------------------- GEMM prefill
     bool pf_supported() const;
+    uint32_t pf_qsa_rows() const;
     void pf_alloc();
     void pf_hc_read(const HcDev& w, float* inj, uint32_t T, bool for_moe);
     void pf_deltanet(const LayerDev& L, uint32_t T);
@@ -1602,6 +1608,9 @@ uint64_t ChkEngine::prefill_scratch_bytes(uint64_t C, bool all_logits) const {
     if (dc_supported(D.nk, D.nv, D.dk, D.dv)) b += dc_work_floats((uint32_t)C, D.nv, D.dv) * f;
     if (all_logits) b += C * D.V * f;
     if (ple_l >= 0) b += C * (ngram_heads + c.ple_embed_dim + 3ull * D.hh + D.H) * 4;
+    if (D.qsa)
+        b += (C * D.inh * D.ihd + (uint64_t)pf_qsa_rows() * (D.max_blocks + D.mask_words +
+                                                             (uint64_t)D.nh * max_chunks * (D.hd + 2))) * 4;
     return b;
 }
 
@@ -1627,11 +1636,20 @@ uint32_t ChkEngine::prefill_rows_fit(bool all_logits) const {
 constexpr uint32_t PF_MAX_ROWS = 4096;                  // rows per chunk (gpu/prefill.rs:116)
 
 bool ChkEngine::pf_supported() const {
-    return (o.experts == 4 || o.experts == 3 || o.experts == 2) && !D.qsa && D.lowrank % 64 == 0 && D.H % 64 == 0 && D.H <= 4096 && D.hc <= 4 &&
+    return (o.experts == 4 || o.experts == 3 || o.experts == 2) && D.lowrank % 64 == 0 && D.H % 64 == 0 && D.H <= 4096 && D.hc <= 4 &&
            (D.dv == 64 || D.dv == 128 || D.dv == 256) && D.I % 64 == 0 && (D.nh * D.hd) % 64 == 0 &&
            D.v_dim % 64 == 0 && D.E + 1 <= 513 && D.nh % D.nkv == 0 &&
            (D.nh / D.nkv == 1 || D.nh / D.nkv == 2 || D.nh / D.nkv == 4 || D.nh / D.nkv == 8) &&
            (D.hd == 128 || D.hd == 256);
+}
+
+// Rows whose QSA selection and attention partials one prefill launch holds:
+// the partials of a row span every chunk of the context, so the group is
+// sized to about 256 MB of them (4..64 rows, a multiple of 4).
+uint32_t ChkEngine::pf_qsa_rows() const {
+    const uint64_t per_row = ((uint64_t)D.nh * max_chunks * (D.hd + 2) + D.max_blocks + D.mask_words) * 4;
+    const uint64_t fit = (256ull << 20) / std::max<uint64_t>(per_row, 1);
+    return (uint32_t)std::max<uint64_t>(4, std::min<uint64_t>(64, fit) / 4 * 4);
 }
 
 void ChkEngine::pf_alloc() {
@@ -1693,6 +1711,13 @@ void ChkEngine::pf_alloc() {
     pf.act = pfalloc<float>(C * slots * D.I);
     pf.yd = pfalloc<float>(C * slots * D.H);
     pf.dcw = dc_supported(D.nk, D.nv, D.dk, D.dv) ? pfalloc<float>(dc_work_floats((uint32_t)C, D.nv, D.dv)) : nullptr;
+    if (D.qsa) {
+        pf.qsa_rows = pf_qsa_rows();
+        pf.iq_ready = pfalloc<float>(C * D.inh * D.ihd);
+        pf.qsa_bscore = pfalloc<float>((uint64_t)pf.qsa_rows * D.max_blocks);
+        pf.qsa_vmask = pfalloc<uint32_t>((uint64_t)pf.qsa_rows * D.mask_words);
+        pf.qsa_part = pfalloc<float>((uint64_t)pf.qsa_rows * D.nh * max_chunks * (D.hd + 2));
+    }
     if (ple_l >= 0) {
         pf.ple_ids = pfalloc<uint32_t>(C * ngram_heads);
         pf.ple_e = pfalloc<float>(C * c.ple_embed_dim);
@@ -1874,8 +1899,40 @@ void ChkEngine::pf_attention(const LayerDev& L, uint32_t T, uint32_t pos0, const
     aa.theta = D.theta;
     aa.scale = D.attn_scale;
     aa.max_chunks = (pos0 + T - 1) / ATTN_CHUNK + 1;
-    launch_attn_prep(aa, (int)T, st);
-    launch_pf_flash(pf.q_ready, pf.q_raw, kvl, pf.attn_out, T, pos0, D.nh, D.nkv, D.hd, D.attn_scale, st);
+    if (!D.qsa) {
+        launch_attn_prep(aa, (int)T, st);
+        launch_pf_flash(pf.q_ready, pf.q_raw, kvl, pf.attn_out, T, pos0, D.nh, D.nkv, D.hd, D.attn_scale, st);
+    } else {
+        // select_tokens (cpu.rs:643-719) over the chunk: every row's KV,
+        // index key and index queries first, then the pooled keys of the
+        // blocks the chunk completes (later chunks and decode steps read
+        // them from block_k); rows still within the budget attend densely
+        // (the flash kernel), later rows through the decode path's block
+        // scores, top-kblk selection and masked partials, qsa_rows at a time
+        set_qsa(aa, L);
+        aa.iq_ready = pf.iq_ready;
+        launch_attn_prep(aa, (int)T, st);
+        launch_qsa_block_keys(aa, pos0 / D.ratio, (pos0 + T) / D.ratio, st);
+        const uint32_t first_sel = (D.kblk + 1) * D.ratio - 1;  // first position with nblk > kblk
+        const uint32_t td = first_sel <= pos0 ? 0 : std::min(T, first_sel - pos0);
+        if (td)
+            launch_pf_flash(pf.q_ready, pf.q_raw, kvl, pf.attn_out, td, pos0, D.nh, D.nkv, D.hd, D.attn_scale, st);
+        for (uint32_t r0 = td; r0 < T; r0 += pf.qsa_rows) {
+            const uint32_t nr = std::min(pf.qsa_rows, T - r0);
+            AttnArgs ag = aa;
+            ag.q_raw = pf.q_raw + (uint64_t)r0 * 2 * D.nh * D.hd;
+            ag.q_ready = pf.q_ready + (uint64_t)r0 * D.nh * D.hd;
+            ag.iq_ready = pf.iq_ready + (uint64_t)r0 * D.inh * D.ihd;
+            ag.pos = pf.pos + r0;
+            ag.out = pf.attn_out + (uint64_t)r0 * D.nh * D.hd;
+            ag.bscore = pf.qsa_bscore;
+            ag.vmask = pf.qsa_vmask;
+            ag.part = pf.qsa_part;
+            ag.max_chunks = (pos0 + r0 + nr - 1) / ATTN_CHUNK + 1;
+            launch_qsa(ag, (int)nr, st);
+            launch_attn_core(ag, (int)nr, st);
+        }
+    }
     launch_pf_xprep(pf.attn_out, D.nh * D.hd, T, D.nh * D.hd, pf.hi, pf.lo, pf.xs, st);
     PfGemmArgs o2{};
     o2.seg[0].m = L.at.o;

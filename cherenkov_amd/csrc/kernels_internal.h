@@ -408,6 +408,10 @@ uint64_t dc_work_floats(uint32_t T, uint32_t nv, uint32_t dv);
 void launch_dc_scan(const PfDnArgs& a, float* work, hipStream_t st);
 void launch_attn_prep(const AttnArgs& a, int nb, hipStream_t st);
 void launch_qsa_select(const AttnArgs& a, int nb, hipStream_t st);
+// block keys + scores + selection of nb rows (a no-op without QSA)
+void launch_qsa(const AttnArgs& a, int nb, hipStream_t st);
+// pooled keys of blocks [blk0, blk1) of kv[0]'s sequence
+void launch_qsa_block_keys(const AttnArgs& a, uint32_t blk0, uint32_t blk1, hipStream_t st);
 void launch_attn_core(const AttnArgs& a, int nb, hipStream_t st);
 bool attn_shape_ok(uint32_t nh, uint32_t nkv, uint32_t hd);
 void launch_copy_f32(float* dst, const float* src, uint64_t n, hipStream_t st);

@@ -15,8 +15,8 @@ import pytest
 from cherenkov_amd import presets
 from cherenkov_amd.abi import check, lib
 from cherenkov_amd.engine import Decode, Engine
-from oracle.oracle import qsa_pick
-from tests.gpu_util import empty_dev, to_dev, to_host
+from oracle.oracle import OracleModel, qsa_pick
+from tests.gpu_util import argmax_margin, assert_close, empty_dev, to_dev, to_host
 from tests.test_gpu_model import teacher_forced
 from tests.test_oracle import _qsa_expect
 
@@ -121,5 +121,46 @@ def test_tiny_qsa_changes_attention(have_gpu):
             if p >= 24:
                 worst = min(worst, cosine(got, ref))
         assert worst < 0.999, f"selection left every logit row within the dense bar (cos {worst:.6f})"
+    finally:
+        eng.close()
+
+
+@pytest.mark.parametrize("splits", [[60], [37, 23], [10, 50]])
+def test_tiny_qsa_gemm_prefill_matches_oracle(have_gpu, splits):
+    """The GEMM prefill past the budget (16 tokens: rows from position 19 on
+    select their 4 best blocks): rows before the boundary through the flash
+    kernel, later rows through block scores and masked partials, the
+    chunk's block keys cached for the next chunk.  Every row's logits
+    (all-logits mode) against the oracle, the MTP draft against its
+    mtp_forward, then decode steps reading the cached block keys."""
+    cfg = presets.tiny(indexer_budget=16, mtp=1)
+    rng = np.random.default_rng(22 + len(splits))
+    prompt = rng.integers(0, cfg.vocab_size, size=sum(splits)).tolist()
+    eng = Engine(cfg, experts=4, drafts=2, max_t=128)
+    rows = []
+    try:
+        i = 0
+        for k in splits:
+            after = prompt[i + k] if i + k < len(prompt) else None
+            nxt, dr = eng.prefill_chunk(prompt[i:i + k], next_after=after, all_logits=True)
+            rows += [eng.pf_logits_row(r) for r in range(k)]
+            i += k
+        got_mtp = eng.mtp_logits_row(0)
+        st = OracleModel(cfg).new_state()
+        st2 = OracleModel(cfg).new_state()
+        mref = None
+        for p, t in enumerate(prompt):
+            ref = st.forward_token(t, True)
+            assert_close(rows[p], ref, f"prefill row {p}")
+            st2.forward_token(t, True)
+            after = prompt[p + 1] if p + 1 < len(prompt) else nxt
+            mref, _ = st2.mtp_forward(after, st2.last_hyper(), p)
+        if argmax_margin(ref) > 1e-3:
+            assert nxt == int(np.argmax(ref))
+        assert_close(got_mtp, mref, "MTP draft logits", abs_frac=2e-3, min_cos=0.99999)
+        for t in rng.integers(0, cfg.vocab_size, size=6).tolist():
+            eng.step_rows([t])
+            eng.commit(1)
+            assert_close(eng.logits_row(0), st.forward_token(t, True), "decode after prefill")
     finally:
         eng.close()
