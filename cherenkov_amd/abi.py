@@ -200,6 +200,21 @@ SIGNATURES = [
     ("chk_rng_u64", i32, [C.c_char_p, u64, C.POINTER(u64), u32]),
     ("chk_pcg32", None, [u64, u64, C.POINTER(u32), u32]),
     ("chk_chacha_block", None, [C.POINTER(u32), i32, C.POINTER(u32)]),
+    # prefix cache
+    ("chk_prefix_matches", i32, [C.POINTER(u32), u32, i32, u32, i32, C.POINTER(u32), u32]),
+    ("chk_prefill_chunk_len", i32, [u32, u32, u32, C.POINTER(u32)]),
+    ("chk_prefill_pacing_sample", i32, [u32, u32, u32, i32]),
+    ("chk_prefix_cache_new", i32, [u64, u64, u64, C.POINTER(P)]),
+    ("chk_prefix_cache_free", None, [P]),
+    ("chk_prefix_cache_expire", None, [P]),
+    ("chk_prefix_cache_stats", None, [P, C.POINTER(u64), C.POINTER(u64), C.POINTER(u64)]),
+    ("chk_prefix_cache_begin", i32, [P, P, C.POINTER(u32), u32, C.POINTER(u32), u32, u32, C.POINTER(P)]),
+    ("chk_prefill_free", None, [P]),
+    ("chk_prefill_cached", u32, [P]),
+    ("chk_prefill_advance", i32, [P, P, P, C.POINTER(u32), u32, u32, u32, C.POINTER(i32), C.POINTER(u32)]),
+    ("chk_prefill_next", u32, [P]),
+    ("chk_prefill_drafts", u32, [P, C.POINTER(u32), u32]),
+    ("chk_prefill_logits", C.POINTER(f32), [P]),
     # runner (decode loop)
     ("chk_decode_new", i32, [P, u32, C.POINTER(u32), u32, u32, u32, u32, C.POINTER(P)]),
     ("chk_decode_new_sampling", i32, [P, C.POINTER(ChkSampling), C.POINTER(u32), u32, C.POINTER(f32), u32,

@@ -32,7 +32,7 @@ FLAGS = [
     f"-I{ROOT / 'include'}",
     f"-I{CSRC}",
 ]
-SOURCES = ["gen.hip", "decode.hip", "attn.hip", "misc.hip", "prefill.hip", "dnscan.hip", "engine.cpp", "runner.cpp", "sampler.cpp", "store.cpp",
+SOURCES = ["gen.hip", "decode.hip", "attn.hip", "misc.hip", "prefill.hip", "dnscan.hip", "engine.cpp", "runner.cpp", "sampler.cpp", "prefix_cache.cpp", "store.cpp",
            "noalloc.hip", "phasebench.hip", "ple.hip"]
 
 

@@ -246,6 +246,48 @@ void chk_pcg32(uint64_t init_state, uint64_t init_seq, uint32_t* out, uint32_t n
  * (no reference counterpart; RFC 8439 vectors pin it in tests). */
 void chk_chacha_block(const uint32_t* in, int rounds, uint32_t* out);
 
+/* ---- prefix cache: bounded LRU checkpoints of prompt prefixes ----
+ * PrefixCache / Prefill (src/prefix_cache.rs:12-335) over this ABI.
+ *   chk_prefix_matches        matches (prefix_cache.rs:35-45): may an entry of
+ *                             tokens (made while drafting: `following`
+ *                             pinned) serve this request?
+ *   chk_prefill_chunk_len     chunk_len (prefix_cache.rs:256-266)
+ *   chk_prefill_pacing_sample pacing_sample (prefix_cache.rs:251-253)
+ *   chk_prefix_cache_new      PrefixCache::new(capacity bytes, max entries,
+ *                             idle seconds; 0 = never)
+ *   chk_prefix_cache_begin    PrefixCache::begin: restore the longest
+ *                             matching entry into the engine and plan the
+ *                             prompt's boundaries (stable ones kept when
+ *                             the cache can hold entries)
+ *   chk_prefill_advance       Prefill::advance: one chunk toward the next
+ *                             boundary (engine prefill from
+ *                             CHERENKOV_PREFILL_MIN rows, else row steps),
+ *                             storing an entry at boundaries and after
+ *                             engine chunks; *done when the prompt is in
+ *   chk_prefill_next / drafts / logits  the resume point for decode
+ * An entry's bytes are its checkpoint, its tokens, its drafts and logits
+ * and the host record. */
+typedef struct ChkPrefixCache ChkPrefixCache;
+typedef struct ChkPrefill ChkPrefill;
+int chk_prefix_matches(const uint32_t* tokens, uint32_t n_tokens, int has_following, uint32_t following,
+                       int complete, const uint32_t* request, uint32_t n_request);
+int chk_prefill_chunk_len(uint32_t remaining, uint32_t capacity, uint32_t quantum, uint32_t* out);
+int chk_prefill_pacing_sample(uint32_t remaining, uint32_t capacity, uint32_t quantum, int engine);
+int chk_prefix_cache_new(uint64_t capacity, uint64_t max_entries, uint64_t idle_seconds, ChkPrefixCache** out);
+void chk_prefix_cache_free(ChkPrefixCache* c);
+void chk_prefix_cache_expire(ChkPrefixCache* c);
+void chk_prefix_cache_stats(const ChkPrefixCache* c, uint64_t* entries, uint64_t* used, uint64_t* evictions);
+int chk_prefix_cache_begin(ChkPrefixCache* c, ChkEngine* e, const uint32_t* ids, uint32_t n,
+                           const uint32_t* stable_boundaries, uint32_t n_boundaries, uint32_t effective_drafts,
+                           ChkPrefill** out);
+void chk_prefill_free(ChkPrefill* p);
+uint32_t chk_prefill_cached(const ChkPrefill* p);
+int chk_prefill_advance(ChkPrefill* p, ChkPrefixCache* c, ChkEngine* e, const uint32_t* ids, uint32_t n,
+                        uint32_t effective_drafts, uint32_t quantum, int* done, uint32_t* pacing_tokens);
+uint32_t chk_prefill_next(const ChkPrefill* p);
+uint32_t chk_prefill_drafts(const ChkPrefill* p, uint32_t* out, uint32_t cap);
+const float* chk_prefill_logits(const ChkPrefill* p);
+
 /* ---- runner: the greedy speculative decode loop ----
  * Decode::new / Decode::step (src/runner/decode.rs:28-171) for the greedy
  * sampler.  `next` and drafts[0..n_drafts) come from the prompt's prefill;
