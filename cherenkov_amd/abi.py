@@ -80,6 +80,17 @@ class ChkMemoryStats(C.Structure):
     ]
 
 
+class ChkExpertCounters(C.Structure):
+    _fields_ = [
+        ("selected_rows", u64),
+        ("cache_hits", u64),
+        ("cache_misses", u64),
+        ("prefetch_requests", u64),
+        ("read_requests", u64),
+        ("read_bytes_requested", u64),
+    ]
+
+
 class ChkSampling(C.Structure):
     _fields_ = [
         ("temperature", f64),
@@ -159,6 +170,9 @@ SIGNATURES = [
     ("chk_pool_set_kind", i32, [P, u32, u32]),
     ("chk_pool_store", i32, [P, u32, C.POINTER(P), C.POINTER(u64)]),
     ("chk_pool_bytes", u64, [P]),
+    ("chk_throttle_ms", i32, [P, C.POINTER(f64)]),
+    ("chk_working_set_limit_gb", f64, [P]),
+    ("chk_expert_activity", i32, [P, C.POINTER(ChkExpertCounters), u32, C.POINTER(f64)]),
     ("chk_last_routes", i32, [P, u32, u32, C.POINTER(u32), C.POINTER(f32)]),
     ("chk_last_probs", i32, [P, u32, u32, P]),
     # kernels.h

@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 
 #include <atomic>
+#include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -202,6 +203,10 @@ struct ChkEngine {
     std::vector<uint64_t> ngram_offs, ngram_sizes;
     float* ple_ring = nullptr;
     float* ple_backup = nullptr;
+    // cumulative routed-expert activity (activity.rs:11-89): per record
+    // (record layer, expert) the rows that chose it and its lookups
+    uint64_t* act = nullptr;
+    std::chrono::steady_clock::time_point act_started;
     // state
     std::vector<float*> dn_state, dn_hist, dn_snap_state, dn_snap_hist;
     std::vector<KvDev> kv, kv2;
@@ -802,6 +807,9 @@ struct ChkEngine {
         s.act = dalloc<float>((uint64_t)NB * (D.topk + 1) * D.I);
         s.act_xq = dalloc<XqChunk>((uint64_t)NB * (D.topk + 1) * (D.I / 32));
         s.mix_out = dalloc<float>(NB * D.H);
+        act = dalloc<uint64_t>((uint64_t)LR * D.E * 2);
+        HIPCHK(hipMemsetAsync(act, 0, (uint64_t)LR * D.E * 2 * 8, st));
+        act_started = std::chrono::steady_clock::now();
         s.counter = dalloc<uint32_t>(64);
         HIPCHK(hipMemsetAsync(s.counter, 0, 256, st));
         s.logits = dalloc<float>((uint64_t)NB * D.V);
@@ -1223,6 +1231,8 @@ struct ChkEngine {
                 HIPCHK(hipMemcpyAsync(s.trace + (uint64_t)l * MAX_NB * D.hh, s.hyper, (uint64_t)nb * D.hh * 4,
                                       hipMemcpyDeviceToDevice, st));
         }
+        launch_expert_activity(s.route_ids, (uint64_t)MAX_NB * D.topk, c.num_hidden_layers, (uint32_t)nb, D.topk, D.E,
+                               act, 0, st);
         hc_read(final_mixer, s.hyper, nullptr, nb);
         prof_begin(PROF_LM_HEAD);
         launch_lm_head(lm_head, s.mixed, s.logits, s.pv, s.pi, lm_parts, s.d_out, nb, st);
@@ -1437,6 +1447,8 @@ void ChkEngine::mtp_rows(int rows, const float* src_hyper, const uint32_t* d_tok
     attention(L, s.mixed, rows, kvs, s.rowpos_aux, s.mtp_hyper, s.inj_a, nullptr);
     hc_read(L.mlp_hc, s.mtp_hyper, s.inj_m, rows);
     moe(L, c.num_hidden_layers, s.mixed, rows, s.mtp_hyper, s.inj_m, nullptr);
+    launch_expert_activity(s.route_ids + (uint64_t)c.num_hidden_layers * MAX_NB * D.topk, 0, 1, (uint32_t)rows,
+                           D.topk, D.E, act, c.num_hidden_layers, st);
     hc_read(mtp_mixer, s.mtp_hyper, nullptr, rows);
     launch_lm_head(lm_head, s.mixed, s.mtp_logits, s.pv, s.pi, lm_parts, s.mtp_out, rows, st);
 }
@@ -1957,6 +1969,7 @@ void ChkEngine::pf_moe(const LayerDev& L, uint32_t T) {
     const uint32_t slots = D.topk + 1;
     launch_pf_router(L.moe.router, L.moe.shared_gate, pf.bhi, pf.bmid, pf.blo, pf.logits, pf.sg, T, D.E, D.H, st);
     launch_pf_route(pf.logits, T, D.E, D.topk, D.norm_topk, pf.ids, pf.wts, st);
+    launch_expert_activity(pf.ids, 0, 1, T, D.topk, D.E, act, L.moe.record_layer, st);
     // the chunk's last row as this layer's "last routes", as a row step leaves them
     const uint64_t roff = (uint64_t)L.moe.record_layer * MAX_NB * D.topk;
     HIPCHK(hipMemcpyAsync(s.route_ids + roff, pf.ids + (uint64_t)(T - 1) * D.topk, D.topk * 4,
@@ -2468,6 +2481,60 @@ int chk_pool_store(const ChkEngine* e, uint32_t kind, void** base, uint64_t* str
 uint64_t chk_pool_bytes(const ChkEngine* e) {
     uint64_t nrec = pool_records(e);
     return nrec * (e->o.experts == 4 ? e->rl4.stride : e->rllo.stride);
+}
+
+// Gpu::throttle_ms (gpu.rs:596-599): the wall time in ms of the second of
+// two runs of the dependent-FMA probe (60,000 iterations per thread), from
+// submission to completion, as MetalContext::throttle_probe times it.
+int chk_throttle_ms(ChkEngine* e, double* ms) {
+    CHK_TRY({
+        float* out = nullptr;
+        HIPCHK(hipMalloc(&out, 65536 * 4));
+        double last = 0.0;
+        try {
+            for (int r = 0; r < 2; ++r) {
+                HIPCHK(hipStreamSynchronize(e->st));
+                const auto t0 = std::chrono::steady_clock::now();
+                launch_clock_probe(out, 60000, e->st);
+                HIPCHK(hipStreamSynchronize(e->st));
+                last = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+            }
+        } catch (...) {
+            hipFree(out);
+            throw;
+        }
+        HIPCHK(hipFree(out));
+        *ms = last;
+    })
+}
+
+// Gpu::working_set_limit_gb (gpu.rs:690-694): the device memory the engine
+// may work in, in decimal GB (units.rs:7): the device's total memory.
+double chk_working_set_limit_gb(const ChkEngine* e) {
+    (void)e;
+    size_t free_b = 0, total_b = 0;
+    if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) return 0.0;
+    return (double)total_b / 1e9;
+}
+
+// Gpu::expert_activity (activity.rs:11-89, 110): cumulative per-record
+// counters since load, records in record order (main layers, then the MTP
+// layer; E per layer).  Every record is resident: a lookup is a hit, and
+// nothing is prefetched or read.
+int chk_expert_activity(const ChkEngine* e, ChkExpertCounters* records, uint32_t n, double* elapsed_seconds) {
+    CHK_TRY({
+        const uint32_t total = e->record_layers * e->D.E;
+        ensure(n == total, "expert activity holds " + std::to_string(total) + " records");
+        std::vector<uint64_t> h((size_t)total * 2);
+        HIPCHK(hipStreamSynchronize(e->st));
+        HIPCHK(hipMemcpy(h.data(), e->act, h.size() * 8, hipMemcpyDeviceToHost));
+        for (uint32_t r = 0; r < total; ++r) {
+            records[r] = ChkExpertCounters{};
+            records[r].selected_rows = h[2 * r];
+            records[r].cache_hits = h[2 * r + 1];
+        }
+        *elapsed_seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - e->act_started).count();
+    })
 }
 
 int chk_last_routes(const ChkEngine* e, uint32_t layer, uint32_t r, uint32_t* ids, float* weights) {

@@ -417,6 +417,12 @@ bool attn_shape_ok(uint32_t nh, uint32_t nkv, uint32_t hd);
 void launch_copy_f32(float* dst, const float* src, uint64_t n, hipStream_t st);
 void launch_kv_fill(const float* k, const float* v, KvDev kv, uint32_t kv_row, uint32_t T, hipStream_t st);
 void launch_zero_f32(float* dst, uint64_t n, hipStream_t st);
+// per-record selected rows and lookups of `layers` record layers from
+// layer0 on (misc.hip); act [record layers][E][2]
+void launch_expert_activity(const uint32_t* ids, uint64_t layer_stride, uint32_t layers, uint32_t rows,
+                            uint32_t topk, uint32_t E, uint64_t* act, uint32_t layer0, hipStream_t st);
+// dependent-FMA clock probe over 65536 threads (out: 65536 floats)
+void launch_clock_probe(float* out, uint32_t iters, hipStream_t st);
 // PLE n-gram block (ple.hip)
 void gen_ngram_table(uint8_t* table, uint64_t rows, uint32_t dim, uint32_t group, uint64_t seed, hipStream_t st);
 // ids: row r's table rows at ids[r * ids_stride ..]

@@ -130,6 +130,25 @@ class Engine:
             raise EngineError(self.L.chk_last_error().decode())
         return np.ctypeslib.as_array(p, shape=(self.cfg.vocab_size,)).copy()
 
+    def throttle_ms(self) -> float:
+        ms = C.c_double()
+        check(self.L.chk_throttle_ms(self._h, C.byref(ms)))
+        return ms.value
+
+    def working_set_limit_gb(self) -> float:
+        return self.L.chk_working_set_limit_gb(self._h)
+
+    def expert_activity(self) -> tuple[np.ndarray, float]:
+        """Gpu::expert_activity: (counters [record layers][experts][6] as
+        ChkExpertCounters fields, seconds since load)."""
+        from .abi import ChkExpertCounters
+        n = (self.cfg.num_hidden_layers + (1 if self.has_mtp else 0)) * self.cfg.num_experts
+        buf = (ChkExpertCounters * n)()
+        sec = C.c_double()
+        check(self.L.chk_expert_activity(self._h, buf, n, C.byref(sec)))
+        arr = np.frombuffer(buf, dtype=np.uint64).reshape(-1, self.cfg.num_experts, 6).copy()
+        return arr, sec.value
+
     @property
     def pos(self) -> int:
         return self.L.chk_pos(self._h)
@@ -298,6 +317,25 @@ class PrefixState:
     def __init__(self, eng: Engine, h: C.c_void_p):
         self.eng = eng
         self._h = h
+
+    def throttle_ms(self) -> float:
+        ms = C.c_double()
+        check(self.L.chk_throttle_ms(self._h, C.byref(ms)))
+        return ms.value
+
+    def working_set_limit_gb(self) -> float:
+        return self.L.chk_working_set_limit_gb(self._h)
+
+    def expert_activity(self) -> tuple[np.ndarray, float]:
+        """Gpu::expert_activity: (counters [record layers][experts][6] as
+        ChkExpertCounters fields, seconds since load)."""
+        from .abi import ChkExpertCounters
+        n = (self.cfg.num_hidden_layers + (1 if self.has_mtp else 0)) * self.cfg.num_experts
+        buf = (ChkExpertCounters * n)()
+        sec = C.c_double()
+        check(self.L.chk_expert_activity(self._h, buf, n, C.byref(sec)))
+        arr = np.frombuffer(buf, dtype=np.uint64).reshape(-1, self.cfg.num_experts, 6).copy()
+        return arr, sec.value
 
     @property
     def pos(self) -> int:

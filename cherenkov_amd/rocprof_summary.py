@@ -43,6 +43,8 @@ def steps(path: str, first: int | None = None, last: int | None = None) -> None:
         return
     total = len(found)
     if first is not None:
+        if first == 0 or last == 0:
+            raise SystemExit("steps are numbered from 1 (negative: from the end)")
         lo = first - 1 if first > 0 else total + first
         hi = last if last > 0 else total + last + 1
         found = found[lo:hi]

@@ -197,6 +197,27 @@ int chk_pool_set_kind(ChkEngine* e, uint32_t rid, uint32_t kind);
 int chk_pool_store(const ChkEngine* e, uint32_t kind, void** base, uint64_t* stride);
 uint64_t chk_pool_bytes(const ChkEngine* e);
 
+/* Gpu::throttle_ms (gpu.rs:596-599): milliseconds of a fixed dependent-FMA
+ * probe (higher = lower clocks). */
+int chk_throttle_ms(ChkEngine* e, double* ms);
+/* Gpu::working_set_limit_gb (gpu.rs:690-694): device memory, decimal GB. */
+double chk_working_set_limit_gb(const ChkEngine* e);
+
+/* Gpu::expert_activity (gpu/activity.rs:11-89, 110): cumulative counters per
+ * expert record since load (n = record layers x num_experts, main layers
+ * then the MTP layer), fields as ExpertCounters; verification and draft
+ * rows count even when rolled back; every record is resident, so each
+ * lookup is a cache hit and no read is requested. */
+typedef struct ChkExpertCounters {
+    uint64_t selected_rows;
+    uint64_t cache_hits;
+    uint64_t cache_misses;
+    uint64_t prefetch_requests;
+    uint64_t read_requests;
+    uint64_t read_bytes_requested;
+} ChkExpertCounters;
+int chk_expert_activity(const ChkEngine* e, ChkExpertCounters* records, uint32_t n, double* elapsed_seconds);
+
 /* Per-step expert activity (gpu/activity.rs:110): routed ids of row r of
  * the last step for layer l (num_experts_per_tok entries). */
 int chk_last_routes(const ChkEngine* e, uint32_t layer, uint32_t r, uint32_t* ids, float* weights);
