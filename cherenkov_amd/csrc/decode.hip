@@ -915,7 +915,7 @@ __global__ void __launch_bounds__(DN_SCAN_COLS * 4) k_dn_scan(DnScanArgs a) {
             ys[t / TPC] = yv;
         }
         if ((t & 63) == 0) a.ssq[((size_t)b * a.nv + hv) * (a.dv / 16) + blk * (COLS / 16) + (t >> 6)] = ss;
-        if (COLS == 32 && a.y_xq) {
+        {
             __syncthreads();
             if (t < 64) xq_chunk_store(ys, a.y_xq + (size_t)b * (a.nv * a.dv / COLS) + hv * blocks + blk, t);
             __syncthreads();
@@ -1435,6 +1435,8 @@ void launch_qmv_inject(const InjArgs& a, int nb, hipStream_t st) {
     const uint32_t cpl = (a.m.in / 32 + 63) / 64;
     constexpr int R = 2;
     const uint32_t grid = grid_for(a.m.out / R);
+    if (a.xmode == XM_DN_GATED && !a.x_xq)
+        throw std::runtime_error("the gated-norm input comes as the scan's nibble-plane chunks");
     const size_t lds = (a.xmode == XM_DN_GATED && a.x_xq) ? 0 : xq_bytes(nb, a.m.in);
     if (a.x_xq && a.xs != a.m.in) throw std::runtime_error("chunked inputs must be dense rows");
 #define INJ(C, X) CHK_NB_SWITCH(nb, (k_qmv_inject<C, R, NB, X><<<grid, 256, lds, st>>>(a)))
@@ -1456,7 +1458,7 @@ void launch_qmv_inject(const InjArgs& a, int nb, hipStream_t st) {
 
 void launch_dn_scan(const DnScanArgs& a, int nb, hipStream_t st) {
     if (a.dv % 32) throw std::runtime_error("value head width must be a multiple of 32");
-    if (a.y_xq && DN_SCAN_COLS != 32) throw std::runtime_error("y chunks need 32-lane scan workgroups");
+    if (!a.y_xq) throw std::runtime_error("the DeltaNet scan writes its outputs as nibble-plane chunks");
     CHK_NB_SWITCH(nb, (k_dn_scan<NB><<<a.nv * (a.dv / DN_SCAN_COLS), DN_SCAN_COLS * 4, 0, st>>>(a)));
 }
 

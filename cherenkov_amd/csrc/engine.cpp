@@ -740,11 +740,15 @@ struct ChkEngine {
         rl4 = record_layout(4, D.H, D.I);
         uint64_t n_rec = (uint64_t)record_layers * D.E;
         experts4 = dalloc<uint8_t>(n_rec * rl4.stride);
+        // page padding between records stays zero whichever way the
+        // records are filled (generated, uploaded whole, or field by field)
+        HIPCHK(hipMemsetAsync(experts4, 0, n_rec * rl4.stride, st));
         if (src) upload_records();
         else gen_records(experts4, rl4, c.seed, D.E, 0, record_layers, D.H, D.I, st);
         if (o.experts != 4) {
             rllo = record_layout(o.experts, D.H, D.I);
             experts_lo = dalloc<uint8_t>(n_rec * rllo.stride);
+            HIPCHK(hipMemsetAsync(experts_lo, 0, n_rec * rllo.stride, st));
             repack_lowbit(experts4, rl4, experts_lo, rllo, (uint32_t)n_rec, (uint64_t)D.I * D.H, st);
         }
 
@@ -936,7 +940,7 @@ struct ChkEngine {
         sa.z = s.dn_z;
         sa.norm = L.dn.norm;
         sa.y = s.dn_y;
-        sa.y_xq = DN_SCAN_COLS == 32 ? s.dn_y_xq : nullptr;
+        sa.y_xq = s.dn_y_xq;
         sa.ssq = s.dn_ssq;
         sa.nk = D.nk;
         sa.nv = D.nv;

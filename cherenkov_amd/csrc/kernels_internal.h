@@ -7,13 +7,9 @@ namespace chk {
 
 constexpr int MAX_SEG = 5;
 
-// Value lanes per DeltaNet scan workgroup: 32 makes each workgroup's
-// outputs one nibble-plane chunk for the out-projection (16: plain f32 y,
-// quantised by the consumer).
-#ifndef CHK_DN_SCAN_COLS
-#define CHK_DN_SCAN_COLS 32
-#endif
-constexpr int DN_SCAN_COLS = CHK_DN_SCAN_COLS;
+// Value lanes per DeltaNet scan workgroup: 32, so each workgroup's outputs
+// are one nibble-plane chunk for the out-projection.
+constexpr int DN_SCAN_COLS = 32;
 
 enum Epi { EPI_RAW = 0, EPI_DN_CONV = 1, EPI_DN_DECAY = 2, EPI_DN_BETA = 3 };
 
