@@ -29,12 +29,17 @@
 // mtp_forward, forward_token) by closed forms on special weights
 // (tests/test_oracle_compositions.py); PLE (ngram_ids_from, ngram_row, ple)
 // by hand-worked id cases and closed forms (tests/test_oracle_ple.py).
+// The near-tie route hints (follow_route_hint; test-side, no counterpart in
+// the reference) by tests/test_oracle_route_hints.py: an own-set hint is a
+// bit-exact no-op, a boundary swap is taken exactly when the tolerance
+// covers the gap, far or repeated experts are refused.
 
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <iterator>
 #include <map>
 #include <memory>
 #include <mutex>
@@ -351,6 +356,19 @@ struct PleRing {
 
 }  // namespace
 
+// Route hints (test-side, no counterpart in the reference): another
+// implementation's expert choice per MoE layer for the next forward pass,
+// taken only where it departs from this top-k by near-tied experts.
+struct RouteHints {
+    std::vector<uint32_t> ids;  // [layers + 1][k]; layer index == num_hidden_layers is the MTP layer
+    std::vector<uint8_t> set;   // per layer: a hint is present
+    float tol = 0.0f;
+    uint64_t swaps = 0;         // layers whose routing followed a hint, cumulative
+    // the routing each layer took in its latest pass: ids in rank order, softmax
+    std::vector<uint32_t> last_ids;
+    std::vector<float> last_probs;
+};
+
 struct OrcState {
     size_t pos = 0;
     std::vector<uint32_t> tokens;
@@ -359,6 +377,7 @@ struct OrcState {
     std::vector<float> last_hyper;
     KvCache mtp_kv;
     PleRing ple;
+    RouteHints hints;
 };
 
 struct OrcModel {
@@ -713,10 +732,48 @@ void delta_head_step(float* s, const float* qh, const float* kh, const float* vh
     }
 }
 
+// Near-tie routing for the parity tests (no counterpart in the reference).
+// Two f32 implementations of the same forward pass agree to rounding, so
+// where the k-th and (k+1)-th router probabilities lie within rounding of
+// each other they may pick different experts, after which their outputs
+// part by far more than rounding.  `hint` is the other implementation's
+// choice of k experts: when it differs from this top-k (ids, in rank order)
+// only by experts whose probability is within `tol` (relative) of the k-th
+// largest, the hinted set is taken, ranked by this model's probabilities
+// (index ascending on equal keys) and weighted as route_topk weights its
+// set.  Any other difference is a real disagreement and the hint is
+// ignored.  Returns whether the routing changed.
+bool follow_route_hint(const float* probs, size_t E, size_t k, bool norm, const uint32_t* hint, float tol,
+                       uint32_t* ids, float* wts) {
+    const float pk = probs[ids[k - 1]];
+    std::vector<uint32_t> own(ids, ids + k), other(hint, hint + k);
+    std::sort(own.begin(), own.end());
+    std::sort(other.begin(), other.end());
+    if (own == other) return false;
+    if (std::adjacent_find(other.begin(), other.end()) != other.end()) return false;  // duplicate ids
+    std::vector<uint32_t> diff;
+    std::set_symmetric_difference(own.begin(), own.end(), other.begin(), other.end(), std::back_inserter(diff));
+    for (uint32_t e : diff)
+        if (e >= E || std::fabs(probs[e] - pk) > tol * pk) return false;
+    std::sort(other.begin(), other.end(), [&](uint32_t a, uint32_t b) {
+        int32_t ka = total_key(probs[a]), kb = total_key(probs[b]);
+        if (ka != kb) return ka > kb;
+        return a < b;
+    });
+    float sum = 0.0f;
+    for (size_t i = 0; i < k; ++i) sum += probs[other[i]];
+    for (size_t i = 0; i < k; ++i) {
+        ids[i] = other[i];
+        wts[i] = norm ? probs[other[i]] / sum : probs[other[i]];
+    }
+    return true;
+}
+
 // moe, src/qwen4_exp/cpu.rs:504-541.  Also reports the routing (top ids in
 // rank order, renormalised weights, full softmax) for the parity tests.
+// `hints`/`layer`: the near-tie hint of that layer, if one is set.
 std::vector<float> moe(OrcModel& m, const MoeW& w, const float* x, uint32_t* top_out, float* w_out,
-                       float* probs_out) {
+                       float* probs_out, RouteHints* hints = nullptr, size_t layer = 0) {
     const ChkConfig& c = m.c;
     size_t h = c.hidden_size, E = c.num_experts, k = c.num_experts_per_tok;
     std::vector<float> logits = bf16_matvec(w.router.data(), E, h, x);
@@ -725,6 +782,17 @@ std::vector<float> moe(OrcModel& m, const MoeW& w, const float* x, uint32_t* top
     std::vector<uint32_t> idx(k);
     std::vector<float> wts(k);
     route_topk(logits.data(), E, k, c.norm_topk_prob != 0, idx.data(), wts.data());
+    if (hints && layer < hints->set.size() && hints->set[layer] &&
+        follow_route_hint(logits.data(), E, k, c.norm_topk_prob != 0, hints->ids.data() + layer * k, hints->tol,
+                          idx.data(), wts.data()))
+        hints->swaps += 1;
+    if (hints) {
+        const size_t n = c.num_hidden_layers + 1;
+        hints->last_ids.resize(n * k);
+        hints->last_probs.resize(n * E);
+        std::copy(idx.begin(), idx.end(), hints->last_ids.begin() + layer * k);
+        std::copy(logits.begin(), logits.end(), hints->last_probs.begin() + layer * E);
+    }
     std::vector<float> out(h, 0.0f);
     for (size_t i = 0; i < k; ++i) {
         uint32_t ei = idx[i];
@@ -936,7 +1004,6 @@ std::vector<float> attention(const OrcModel& m, const AttnW& w, const float* x, 
     size_t nh = c.num_attention_heads, nkv = c.num_key_value_heads, hd = c.head_dim;
     size_t rot = (size_t)((double)hd * c.partial_rotary_factor);
     float theta = (float)c.rope_theta, eps = (float)c.rms_norm_eps;
-    size_t kv_row = nkv * hd;
     size_t ihd = c.indexer_head_dim, inh = c.indexer_n_heads;
     std::vector<float> qk(w.idx.view.out);
     matvec(w.idx.view, x, qk.data());
@@ -1249,7 +1316,7 @@ int orc_forward_token(void* mp, void* sp, uint32_t token, int kv_q8, float* logi
         std::vector<float> hyper(hh);
         for (size_t g = 0; g < hc; ++g) memcpy(hyper.data() + g * h, e.data(), h * 4);
         st->tokens.push_back(token);
-        size_t kv_idx = 0, delta_idx = 0;
+        size_t kv_idx = 0, delta_idx = 0, li = 0;
         std::vector<float> mixed, inj;
         for (auto& layer : m->layers) {
             if (layer.has_ple) {
@@ -1262,9 +1329,10 @@ int orc_forward_token(void* mp, void* sp, uint32_t token, int kv_q8, float* logi
             else out = orc::attention(*m, layer.at, mixed.data(), st->kv[kv_idx++], st->pos, kv_q8 != 0);
             inject(hyper, out, inj);
             orc::gated_residual(*m, layer.mlp_hc, hyper.data(), mixed, inj);
-            out = orc::moe(*m, layer.moe, mixed.data(), nullptr, nullptr, nullptr);
+            out = orc::moe(*m, layer.moe, mixed.data(), nullptr, nullptr, nullptr, &st->hints, li++);
             inject(hyper, out, inj);
         }
+        if (!st->hints.set.empty()) std::fill(st->hints.set.begin(), st->hints.set.begin() + c.num_hidden_layers, 0);
         st->pos += 1;
         st->last_hyper = hyper;
         orc::gated_residual(*m, m->final_mixer, hyper.data(), mixed, inj);
@@ -1274,6 +1342,37 @@ int orc_forward_token(void* mp, void* sp, uint32_t token, int kv_q8, float* logi
         g_err = ex.what();
         return -1;
     }
+}
+
+// Near-tie route hints for the next forward_token / mtp_forward (see
+// follow_route_hint): ids[layers][k] for `layers` consecutive layers from
+// layer 0 (num_hidden_layers + 1 includes the MTP layer), used once.
+int orc_state_route_hints(void* mp, void* sp, const uint32_t* ids, uint32_t layers, float tol) {
+    OrcModel* m = (OrcModel*)mp;
+    OrcState* st = (OrcState*)sp;
+    const size_t k = m->c.num_experts_per_tok, n = m->c.num_hidden_layers + 1;
+    if (layers > n) { g_err = "more hinted layers than the model has"; return -1; }
+    if (!(tol >= 0.0f)) { g_err = "tolerance must be >= 0"; return -1; }
+    st->hints.ids.assign(n * k, 0);
+    st->hints.set.assign(n, 0);
+    std::copy(ids, ids + (size_t)layers * k, st->hints.ids.begin());
+    std::fill(st->hints.set.begin(), st->hints.set.begin() + layers, 1);
+    st->hints.tol = tol;
+    return 0;
+}
+
+uint64_t orc_state_route_swaps(void* sp) { return ((OrcState*)sp)->hints.swaps; }
+
+// The routing layer `layer` took in the state's latest pass: k ids in rank
+// order and the E softmax probabilities (either output may be null).
+int orc_state_last_routes(void* mp, void* sp, uint32_t layer, uint32_t* ids, float* probs) {
+    OrcModel* m = (OrcModel*)mp;
+    OrcState* st = (OrcState*)sp;
+    const size_t k = m->c.num_experts_per_tok, E = m->c.num_experts;
+    if ((size_t)layer * k >= st->hints.last_ids.size()) { g_err = "no routing recorded for that layer"; return -1; }
+    if (ids) std::copy_n(st->hints.last_ids.begin() + (size_t)layer * k, k, ids);
+    if (probs) std::copy_n(st->hints.last_probs.begin() + (size_t)layer * E, E, probs);
+    return 0;
 }
 
 int orc_state_last_hyper(void* sp, float* out, size_t n) {
@@ -1309,7 +1408,8 @@ int orc_mtp_forward(void* mp, void* sp, uint32_t token, const float* hyper_in, u
         std::vector<float> out = orc::attention(*m, layer.at, mixed.data(), st->mtp_kv, pos, kv_q8 != 0);
         inject(hyper, out, inj);
         orc::gated_residual(*m, layer.mlp_hc, hyper.data(), mixed, inj);
-        out = orc::moe(*m, layer.moe, mixed.data(), nullptr, nullptr, nullptr);
+        out = orc::moe(*m, layer.moe, mixed.data(), nullptr, nullptr, nullptr, &st->hints, c.num_hidden_layers);
+        if (st->hints.set.size() > c.num_hidden_layers) st->hints.set[c.num_hidden_layers] = 0;
         inject(hyper, out, inj);
         orc::gated_residual(*m, m->mtp_mixer, hyper.data(), mixed, inj);
         matvec(m->lm_head.view, mixed.data(), logits);

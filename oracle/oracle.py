@@ -55,6 +55,9 @@ _SIGS = [
     ("orc_record_stride", u64, [P]),
     ("orc_qsa_pick", None, [P, u32, u32, u32, P, P]),
     ("orc_state_fill_prefix", i32, [P, P, u32, u64]),
+    ("orc_state_route_hints", i32, [P, P, P, u32, f32]),
+    ("orc_state_route_swaps", u64, [P]),
+    ("orc_state_last_routes", i32, [P, P, u32, P, P]),
     ("orc_set_q4", i32, [P, u32, C.c_char_p, P, P, P, u64]),
     ("orc_set_bf16", i32, [P, u32, C.c_char_p, P, u64]),
     ("orc_set_record", i32, [P, u32, u32, P, u64]),
@@ -236,6 +239,28 @@ class OracleState:
     @property
     def pos(self) -> int:
         return self.m.L.orc_state_pos(self.h)
+
+    def route_hints(self, ids, tol: float) -> None:
+        """Near-tie route hints for the next forward_token / mtp_forward:
+        ids[layers][k] (row num_hidden_layers is the MTP layer), taken per
+        layer only where they differ from the oracle's own top-k by experts
+        within `tol` (relative) of its k-th probability; used once."""
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        assert ids.ndim == 2 and ids.shape[1] == self.m.cfg.num_experts_per_tok
+        _check(self.m.L.orc_state_route_hints(self.m.h, self.h, _p(ids), ids.shape[0], tol))
+
+    def last_routes(self, layer: int):
+        """(ids in rank order, softmax) of `layer` in the latest pass."""
+        c = self.m.cfg
+        ids = np.empty(c.num_experts_per_tok, np.uint32)
+        probs = np.empty(c.num_experts, np.float32)
+        _check(self.m.L.orc_state_last_routes(self.m.h, self.h, layer, _p(ids), _p(probs)))
+        return ids, probs
+
+    @property
+    def route_swaps(self) -> int:
+        """Layers (cumulative) whose routing followed a hint."""
+        return self.m.L.orc_state_route_swaps(self.h)
 
     def forward_token(self, token: int, kv_q8: bool = True) -> np.ndarray:
         out = np.empty(self.m.cfg.vocab_size, np.float32)

@@ -44,6 +44,17 @@ def to_host(t, dtype=None) -> np.ndarray:
     return a.view(dtype) if dtype is not None else a
 
 
+# Relative band around a layer's k-th router probability inside which the
+# engine and the oracle may pick different experts from f32 rounding alone
+# (the oracle then follows the engine's pick: OracleState.route_hints).
+ROUTE_TIE_TOL = 2e-3
+
+
+def engine_routes(eng, layers: int, row: int = 0) -> np.ndarray:
+    """The engine's expert ids of layers 0..layers-1 in its latest step."""
+    return np.array([eng.last_routes(layer, row)[0] for layer in range(layers)], np.uint32)
+
+
 def cosine(a: np.ndarray, b: np.ndarray) -> float:
     a = a.astype(np.float64).ravel()
     b = b.astype(np.float64).ravel()

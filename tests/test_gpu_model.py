@@ -15,7 +15,7 @@ import pytest
 from cherenkov_amd import presets
 from cherenkov_amd.engine import Decode, Engine
 from oracle.oracle import OracleModel
-from tests.gpu_util import argmax_margin, assert_close
+from tests.gpu_util import ROUTE_TIE_TOL, argmax_margin, assert_close, engine_routes
 
 pytestmark = pytest.mark.gpu
 
@@ -31,16 +31,22 @@ def check_logits(got, ref, label):
 
 def teacher_forced(cfg, eng_tokens, prompt, step_logits, label, kv_q8=True):
     """Run the oracle over prompt + generated tokens, comparing each
-    position's logits with the engine's."""
+    position's logits with the engine's.  Entries are (pos, logits) or
+    (pos, logits, engine routes [layers][k]); with routes the oracle
+    follows the engine through router near-ties (ROUTE_TIE_TOL), at most
+    two layers per position."""
     orc = OracleModel(cfg)
     st = orc.new_state()
     seq = list(prompt) + list(eng_tokens)
     exempt = 0
-    for i, (pos, logits) in enumerate(step_logits):
+    for i, (pos, logits, *routes) in enumerate(step_logits):
         while st.pos < pos:
             st.forward_token(seq[st.pos], kv_q8)
+        if routes:
+            st.route_hints(routes[0], ROUTE_TIE_TOL)
         ref = st.forward_token(seq[pos], kv_q8)
         exempt += check_logits(logits, ref, f"{label} pos {pos}")
+    assert st.route_swaps <= 2 * len(step_logits), f"{label}: {st.route_swaps} near-tie routes followed"
     return exempt
 
 
@@ -162,16 +168,17 @@ def test_full_shape_model_few_tokens(have_gpu):
     try:
         logs = []
         out = None
+        L = cfg.num_hidden_layers
         for p, t in enumerate(prompt):
             out = eng.step_rows([t])
-            logs.append((p, eng.logits_row(0)))
+            logs.append((p, eng.logits_row(0), engine_routes(eng, L)))
             eng.commit(1)
         gen = []
         tok = out[0]
         for i in range(4):
             gen.append(tok)
             out = eng.step_rows([tok])
-            logs.append((len(prompt) + i, eng.logits_row(0)))
+            logs.append((len(prompt) + i, eng.logits_row(0), engine_routes(eng, L)))
             eng.commit(1)
             tok = out[0]
         exempt = teacher_forced(cfg, gen, prompt, logs, "full")

@@ -17,7 +17,7 @@ from cherenkov_amd import presets
 from cherenkov_amd.abi import check, lib
 from cherenkov_amd.engine import Decode, Engine
 from oracle.oracle import OracleModel
-from tests.gpu_util import argmax_margin, assert_close
+from tests.gpu_util import ROUTE_TIE_TOL, argmax_margin, assert_close, engine_routes
 
 pytestmark = pytest.mark.gpu
 
@@ -161,12 +161,15 @@ def test_full_shape_mtp_draft_matches_oracle(have_gpu):
             eng.commit(1)
             d = eng.mtp_draft([toks[p + 1]], 1)
             got = eng.mtp_logits_row(0)
+            # trunk layers then the MTP layer (index num_hidden_layers)
+            st.route_hints(engine_routes(eng, cfg.num_hidden_layers + 1), ROUTE_TIE_TOL)
             ref_t = st.forward_token(toks[p])
             ref, _ = st.mtp_forward(toks[p + 1], st.last_hyper(), p)
             assert_close(got_t, ref_t, f"48-layer trunk pos {p}")
             assert_close(got, ref, f"48-layer MTP pos {p}")
             if argmax_margin(ref) > 1e-3:
                 assert d[0] == int(np.argmax(ref))
+        assert st.route_swaps <= 2 * (len(toks) - 1), f"{st.route_swaps} near-tie routes followed"
     finally:
         eng.close()
 
