@@ -389,7 +389,8 @@ void launch_pf_router(const uint16_t* router, const uint16_t* shared_gate, const
 void launch_pf_route(const float* logits, uint32_t T, uint32_t E, uint32_t topk, int norm_topk, uint32_t* ids,
                      float* wts, hipStream_t st);
 void launch_pf_group(const uint32_t* ids, uint32_t T, uint32_t topk, uint32_t E, uint32_t cap, uint32_t* list,
-                     uint32_t* count, uint32_t* tiles, uint32_t* ntiles, hipStream_t st);
+                     uint32_t* count, uint32_t* tiles, uint32_t* ntiles, uint64_t* act, uint32_t layer,
+                     hipStream_t st);
 uint32_t pf_tile_bound(uint32_t T, uint32_t topk, uint32_t E);
 void launch_pf_moe_combine(const float* yd, const float* wts, const float* sg, const float* inj, float* hyper,
                            uint32_t T, uint32_t H, uint32_t topk, uint32_t hc, hipStream_t st);

@@ -256,10 +256,24 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
     __shared__ uint32_t sSB[SBL ? 2 : 1][SBL ? 256 * SBR : 1];
     const int tid = threadIdx.x, lane = tid & 63, col = lane & 15, kq = lane >> 4;
     const uint32_t wn = wave_id();
-    uint32_t grp = 0, mt = blockIdx.y;
+    uint32_t bx = blockIdx.x, by = blockIdx.y;
     if (a.list) {
-        if (blockIdx.y >= *a.ntiles) return;
-        const uint32_t tv = a.tiles[blockIdx.y];
+        // XCD-aware order: workgroups are dealt to the 8 XCDs round-robin
+        // by linear id, so linear ids L = 8 s + x map to items w = x C + s
+        // % C of chunk s / C (C = 2 gridDim.x items: every column block of
+        // two consecutive tiles).  Each chunk runs on one XCD: its tiles' A
+        // rows come from HBM once for all column blocks, and an expert's
+        // two tiles (the list starts them at even positions) share its
+        // weights through that XCD's L2.  gridDim.y is a multiple of 16.
+        const uint32_t C = 2 * gridDim.x, L = blockIdx.y * gridDim.x + blockIdx.x;
+        const uint32_t sl = L >> 3, w = (sl / C) * 8 * C + (L & 7) * C + sl % C;
+        bx = w % gridDim.x;
+        by = w / gridDim.x;
+    }
+    uint32_t grp = 0, mt = by;
+    if (a.list) {
+        if (by >= *a.ntiles) return;
+        const uint32_t tv = a.tiles[by];
         grp = tv >> 16;
         mt = tv & 0xffffu;
     }
@@ -282,8 +296,7 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
     const uint32_t* wb = expert ? reinterpret_cast<const uint32_t*>(rec) : a.wbase;
     const uint16_t* sbase = expert ? reinterpret_cast<const uint16_t*>(rec) : a.sbase;
     auto out_of = [&](uint32_t wn_, int j, uint32_t col_) __attribute__((always_inline)) -> uint32_t {
-        return EPI == PE_HC_UP ? blockIdx.x * 64 + wn_ * 16 + col_
-                               : blockIdx.x * (256 / NMAT) + wn_ * (64 / NMAT) + j * 16 + col_;
+        return EPI == PE_HC_UP ? bx * 64 + wn_ * 16 + col_ : bx * (256 / NMAT) + wn_ * (64 / NMAT) + j * 16 + col_;
     };
     auto row_of = [&](uint32_t wn_, int j, uint32_t col_) __attribute__((always_inline)) -> uint32_t {
         const uint32_t o = out_of(wn_, j, col_);
@@ -769,14 +782,19 @@ __global__ void __launch_bounds__(256) k_pf_route(const float* __restrict__ logi
 // Entries grouped by expert (the CSR lists of gpu/prefill/experts.rs:29-137):
 // list[e][0..count[e]) holds the entries t (k+1) + slot routed to e (any
 // order: every GEMM row is independent), list[E] every token's shared
-// slot t (k+1) + k, and tiles[] the (group, 64-row tile) pairs in group
-// order, *ntiles of them.  One workgroup.
+// slot t (k+1) + k, and tiles[] the (group, 64-row tile) pairs, *ntiles of
+// them: first every group of two or more tiles, its count rounded up to
+// even (the extra tile has no rows), so each starts at an even position
+// (the GEMMs run tiles 2c and 2c + 1 on one XCD), then the one-tile groups.
+// With `act`, also the expert activity counters of `layer` (selected rows
+// and selections, as k_expert_activity counts them).  One workgroup.
 constexpr uint32_t PG_WG = 1024;  // threads of the grouping workgroup (one group each)
 
 __global__ void __launch_bounds__(PG_WG) k_pf_group(const uint32_t* __restrict__ ids, uint32_t T, uint32_t topk,
                                                     uint32_t E, uint32_t cap, uint32_t* __restrict__ list,
                                                     uint32_t* __restrict__ count, uint32_t* __restrict__ tiles,
-                                                    uint32_t* __restrict__ ntiles) {
+                                                    uint32_t* __restrict__ ntiles,
+                                                    unsigned long long* __restrict__ act, uint32_t layer) {
     __shared__ uint32_t cnt[PG_WG];
     __shared__ uint32_t wsum[PG_WG / 64];
     const uint32_t tau = threadIdx.x, lane = tau & 63, wv = tau >> 6;
@@ -793,21 +811,31 @@ __global__ void __launch_bounds__(PG_WG) k_pf_group(const uint32_t* __restrict__
     __syncthreads();
     if (tau == 0) cnt[E] = T;
     __syncthreads();
-    // tiles per group (thread e takes group e), workgroup prefix sum
+    // tiles per group (thread e takes group e): multi-tile counts in the
+    // high half-word, single tiles in the low one, one workgroup prefix sum
     const uint32_t e = tau;
-    const uint32_t nt = e <= E ? (cnt[e] + 63) / 64 : 0;
+    const uint32_t nt0 = e <= E ? (cnt[e] + 63) / 64 : 0;
+    const uint32_t nt = nt0 > 1 ? (nt0 + 1) & ~1u : nt0;
     if (e <= E) count[e] = cnt[e];
-    uint32_t incl = nt;
+    if (act && e < E && cnt[e]) {
+        unsigned long long* ae = act + ((size_t)layer * E + e) * 2;
+        ae[0] += cnt[e];
+        ae[1] += 1;
+    }
+    const uint32_t packed = nt > 1 ? nt << 16 : nt;
+    uint32_t incl = packed;
     for (int d = 1; d < 64; d <<= 1) {
         const uint32_t o = __shfl_up(incl, d, 64);
         if ((int)lane >= d) incl += o;
     }
     if (lane == 63) wsum[wv] = incl;
     __syncthreads();
-    uint32_t off = incl - nt;
+    uint32_t off = incl - packed, all = 0;
     for (uint32_t k = 0; k < wv; ++k) off += wsum[k];
-    for (uint32_t q = 0; q < nt; ++q) tiles[off + q] = e << 16 | q;
-    if (tau == PG_WG - 1) *ntiles = off + nt;
+    for (uint32_t k = 0; k < PG_WG / 64; ++k) all += wsum[k];
+    const uint32_t start = nt > 1 ? off >> 16 : (all >> 16) + (off & 0xffffu);
+    for (uint32_t q = 0; q < nt; ++q) tiles[start + q] = e << 16 | q;
+    if (tau == PG_WG - 1) *ntiles = (all >> 16) + (all & 0xffffu);
 }
 
 // out[t][n] = sum_r w[t][r] yd[t][r][n] + sigmoid(sg[t]) yd[t][k][n]
@@ -1143,13 +1171,19 @@ void launch_pf_route(const float* logits, uint32_t T, uint32_t E, uint32_t topk,
 }
 
 void launch_pf_group(const uint32_t* ids, uint32_t T, uint32_t topk, uint32_t E, uint32_t cap, uint32_t* list,
-                     uint32_t* count, uint32_t* tiles, uint32_t* ntiles, hipStream_t st) {
+                     uint32_t* count, uint32_t* tiles, uint32_t* ntiles, uint64_t* act, uint32_t layer,
+                     hipStream_t st) {
     if (E + 1 > PG_WG) throw std::runtime_error("prefill grouping supports at most 1023 experts");
-    k_pf_group<<<1, PG_WG, 0, st>>>(ids, T, topk, E, cap, list, count, tiles, ntiles);
+    if (pf_tile_bound(T, topk, E) >= 0x10000u) throw std::runtime_error("prefill grouping: too many tiles");
+    k_pf_group<<<1, PG_WG, 0, st>>>(ids, T, topk, E, cap, list, count, tiles, ntiles,
+                                    reinterpret_cast<unsigned long long*>(act), layer);
 }
 
+// Tiles of a grouped GEMM: every group's rows in 64-row tiles, one more
+// per group for the even rounding, the grid rounded up to 16 tiles.
 uint32_t pf_tile_bound(uint32_t T, uint32_t topk, uint32_t E) {
-    return (T * topk + 63) / 64 + E + (T + 63) / 64 + 1;
+    const uint32_t n = (T * topk + 63) / 64 + E + (T + 63) / 64 + 1 + (E + 1);
+    return (n + 15) & ~15u;
 }
 
 void launch_pf_moe_combine(const float* yd, const float* wts, const float* sg, const float* inj, float* hyper,
