@@ -1972,13 +1972,9 @@ void ChkEngine::pf_attention(const LayerDev& L, uint32_t T, uint32_t pos0, const
 void ChkEngine::pf_moe(const LayerDev& L, uint32_t T) {
     const uint32_t slots = D.topk + 1;
     launch_pf_router(L.moe.router, L.moe.shared_gate, pf.bhi, pf.bmid, pf.blo, pf.logits, pf.sg, T, D.E, D.H, st);
-    launch_pf_route(pf.logits, T, D.E, D.topk, D.norm_topk, pf.ids, pf.wts, st);
-    // the chunk's last row as this layer's "last routes", as a row step leaves them
+    // the chunk's last row also as this layer's "last routes", as a row step leaves them
     const uint64_t roff = (uint64_t)L.moe.record_layer * MAX_NB * D.topk;
-    HIPCHK(hipMemcpyAsync(s.route_ids + roff, pf.ids + (uint64_t)(T - 1) * D.topk, D.topk * 4,
-                          hipMemcpyDeviceToDevice, st));
-    HIPCHK(hipMemcpyAsync(s.route_w + roff, pf.wts + (uint64_t)(T - 1) * D.topk, D.topk * 4, hipMemcpyDeviceToDevice,
-                          st));
+    launch_pf_route(pf.logits, T, D.E, D.topk, D.norm_topk, pf.ids, pf.wts, s.route_ids + roff, s.route_w + roff, st);
     // (also counts the layer's expert activity)
     launch_pf_group(pf.ids, T, D.topk, D.E, pf.cap, pf.list, pf.count, pf.tiles, pf.ntiles, act,
                     L.moe.record_layer, st);

@@ -387,7 +387,7 @@ void launch_pf_hc_down_finish(const float* part, uint32_t nsplit, uint32_t T, ui
 void launch_pf_router(const uint16_t* router, const uint16_t* shared_gate, const uint4* bhi, const uint4* bmid,
                       const uint4* blo, float* logits, float* sg, uint32_t T, uint32_t E, uint32_t H, hipStream_t st);
 void launch_pf_route(const float* logits, uint32_t T, uint32_t E, uint32_t topk, int norm_topk, uint32_t* ids,
-                     float* wts, hipStream_t st);
+                     float* wts, uint32_t* last_ids, float* last_wts, hipStream_t st);
 void launch_pf_group(const uint32_t* ids, uint32_t T, uint32_t topk, uint32_t E, uint32_t cap, uint32_t* list,
                      uint32_t* count, uint32_t* tiles, uint32_t* ntiles, uint64_t* act, uint32_t layer,
                      hipStream_t st);

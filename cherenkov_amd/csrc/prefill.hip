@@ -761,10 +761,12 @@ __global__ void __launch_bounds__(256) k_pf_router(const uint16_t* __restrict__ 
 
 // ------------------------------------------------------------ routing
 // One wave per token: softmax top-k (route_row) and the renormalised
-// weights in rank order (cpu.rs:508-525).
+// weights in rank order (cpu.rs:508-525); the last token's routing also
+// goes to last_ids / last_wts (the layer's "last routes").
 __global__ void __launch_bounds__(256) k_pf_route(const float* __restrict__ logits, uint32_t T, uint32_t E,
                                                   uint32_t topk, int norm_topk, uint32_t* __restrict__ ids,
-                                                  float* __restrict__ wts) {
+                                                  float* __restrict__ wts, uint32_t* __restrict__ last_ids,
+                                                  float* __restrict__ last_wts) {
     const int lane = threadIdx.x & 63;
     const uint32_t t = blockIdx.x * (CHK_WG >> 6) + wave_id();
     if (t >= T) return;
@@ -774,8 +776,13 @@ __global__ void __launch_bounds__(256) k_pf_route(const float* __restrict__ logi
     float topsum = 0.0f;
     for (uint32_t r = 0; r < topk; ++r) topsum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_p), (int)r));
     if ((uint32_t)lane < topk) {
+        const float w = norm_topk ? my_p / topsum : my_p;
         ids[(size_t)t * topk + lane] = my_id;
-        wts[(size_t)t * topk + lane] = norm_topk ? my_p / topsum : my_p;
+        wts[(size_t)t * topk + lane] = w;
+        if (t + 1 == T && last_ids) {
+            last_ids[lane] = my_id;
+            last_wts[lane] = w;
+        }
     }
 }
 
@@ -1166,8 +1173,8 @@ void launch_pf_router(const uint16_t* router, const uint16_t* shared_gate, const
 }
 
 void launch_pf_route(const float* logits, uint32_t T, uint32_t E, uint32_t topk, int norm_topk, uint32_t* ids,
-                     float* wts, hipStream_t st) {
-    if (T) k_pf_route<<<(T + 3) / 4, CHK_WG, 0, st>>>(logits, T, E, topk, norm_topk, ids, wts);
+                     float* wts, uint32_t* last_ids, float* last_wts, hipStream_t st) {
+    if (T) k_pf_route<<<(T + 3) / 4, CHK_WG, 0, st>>>(logits, T, E, topk, norm_topk, ids, wts, last_ids, last_wts);
 }
 
 void launch_pf_group(const uint32_t* ids, uint32_t T, uint32_t topk, uint32_t E, uint32_t cap, uint32_t* list,
