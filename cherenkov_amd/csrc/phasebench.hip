@@ -135,6 +135,64 @@ __global__ void __launch_bounds__(PB_WG) k_pb_persistent(PbArgs a) {
     if (x == 0x9e3779b9u) a.err[1] = x;  // keeps the loads live
 }
 
+// XCD-local barrier: the workgroups of one XCD (dealt round-robin by
+// linear id, so workgroup g runs on XCD g % 8, checked against the
+// hardware's XCC_ID) meet at a counter in that XCD's L2: agent-scope
+// read-modify-writes without the system-coherence bit are performed in the
+// local L2, which every CU of the XCD shares, so neither the counter nor
+// the exchanged values go to memory.  The counter only grows (arrival k of
+// a phase waits for the next multiple of the XCD's workgroup count), so no
+// reset is needed between launches.
+struct PbXArgs {
+    uint32_t* bar;  // [8] counters, 64 B apart
+    uint32_t* abort_flag;
+    uint32_t* err;  // [0] wrong values read, [1] workgroups not on XCD g % 8
+    float* data;    // [8][2][per][64]
+    uint32_t phases;
+};
+
+__global__ void __launch_bounds__(PB_WG) k_pb_xcd(PbXArgs a) {
+    const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const uint32_t xcc = __builtin_amdgcn_s_getreg((3 << 11) | 20);  // hwreg(HW_REG_XCC_ID, 0, 4)
+    const uint32_t per = gridDim.x >> 3, rank = blockIdx.x >> 3, x = blockIdx.x & 7;
+    __shared__ uint32_t s_abort;
+    if (t == 0) {
+        s_abort = 0;
+        if (xcc != x) atomicAdd(a.err + 1, 1u);
+    }
+    __syncthreads();
+    uint32_t bad = 0;
+    uint32_t* bar = a.bar + x * 16;
+    for (uint32_t p = 0; p < a.phases; ++p) {
+        float* buf = a.data + ((size_t)(x * 2 + (p & 1)) * per) * 64;
+        if (wave == 0) buf[rank * 64 + lane] = (float)(p * 7 + rank);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (t == 0) {
+            const uint32_t old = __hip_atomic_fetch_add(bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const uint32_t target = (old / per + 1) * per;
+            uint32_t spins = 0;
+            while ((int32_t)(__hip_atomic_fetch_add(bar, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
+                if (++spins > PB_SPIN_LIMIT || ld_sys(a.abort_flag)) {
+                    st_sys(a.abort_flag, 1);
+                    s_abort = 1;
+                    break;
+                }
+            }
+        }
+        __syncthreads();
+        if (s_abort) break;
+        if (wave == 1) {
+            // other workgroups' values, read at device scope (past this CU's L1)
+            const uint32_t o1 = (rank + 1) % per, o2 = (rank + per / 2) % per;
+            const float v1 = __hip_atomic_load(buf + o1 * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const float v2 = __hip_atomic_load(buf + o2 * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            bad += (v1 != (float)(p * 7 + o1)) + (v2 != (float)(p * 7 + o2));
+        }
+    }
+    if (wave == 1 && bad) atomicAdd(a.err, bad);
+}
+
 // Float atomics without a return value: workgroup g adds 1 to `per_wg`
 // addresses starting at (g * stride) % n_addr.
 __global__ void __launch_bounds__(PB_WG) k_pb_atomics(float* acc, uint32_t n_addr, uint32_t per_wg, uint32_t stride) {
@@ -245,6 +303,35 @@ extern "C" int chk_phase_bench(int mode, uint32_t wgs, uint32_t phases, uint64_t
             }
             // slope between the two timed runs removes the launch's fixed cost
             ms = (t[2] - t[1]) * (float)phases / (float)(ph[2] - ph[1]);
+        } else if (mode == 6) {
+            // XCD-local barrier (wgs a multiple of 8)
+            if (wgs % 8) throw std::runtime_error("the XCD-local barrier takes a multiple of 8 workgroups");
+            PbXArgs a{};
+            a.bar = d.alloc<uint32_t>(8 * 16 * 4);
+            a.abort_flag = d.alloc<uint32_t>(256);
+            a.err = d.alloc<uint32_t>(256);
+            a.data = d.alloc<float>((size_t)2 * wgs * 64 * 4);
+            ck(hipMemsetAsync(a.bar, 0, 8 * 16 * 4, st), "memset");
+            float t[3];
+            const uint32_t ph[3] = {phases / 4, phases / 4, phases};
+            for (int k = 0; k < 3; ++k) {
+                a.phases = ph[k];
+                ck(hipMemsetAsync(a.abort_flag, 0, 256, st), "memset");
+                ck(hipMemsetAsync(a.err, 0, 256, st), "memset");
+                ck(hipStreamSynchronize(st), "sync");
+                void* args[] = {&a};
+                ck(hipEventRecord(e0, st), "record");
+                ck(hipLaunchCooperativeKernel((const void*)k_pb_xcd, dim3(wgs), dim3(PB_WG), args, 0, st),
+                   "cooperative launch");
+                ck(hipEventRecord(e1, st), "record");
+                ck(hipEventSynchronize(e1), "sync");
+                ck(hipEventElapsedTime(&t[k], e0, e1), "elapsed");
+                uint32_t h[3];
+                ck(hipMemcpy(h, a.err, 8, hipMemcpyDeviceToHost), "copy");
+                ck(hipMemcpy(h + 2, a.abort_flag, 4, hipMemcpyDeviceToHost), "copy");
+                *errors += h[0] + h[1] * 1000u + (h[2] ? 1000000u : 0u);
+            }
+            ms = (t[2] - t[1]) * (float)phases / (float)(ph[2] - ph[1]);
         } else if (mode == 5) {
             // float atomics: wgs workgroups x bytes_per_phase/4 adds each over
             // a window of `phases` addresses (phases = contention spread)
@@ -263,7 +350,7 @@ extern "C" int chk_phase_bench(int mode, uint32_t wgs, uint32_t phases, uint64_t
             (void)hipStreamDestroy(st);
             return 0;
         } else {
-            throw std::runtime_error("mode must be 0..5");
+            throw std::runtime_error("mode must be 0..6");
         }
         *us_per_phase = ms * 1e3 / phases;
         ck(hipGetLastError(), "kernel");

@@ -78,6 +78,7 @@ PHASE_MODES = {
     2: "persistent kernel, grid barrier only",
     3: "persistent kernel, barrier then weights",
     4: "persistent kernel, next weights issued before the barrier",
+    6: "persistent kernel, XCD-local barrier in L2",
 }
 
 
@@ -92,7 +93,9 @@ def phases(wgs_list, mbytes_list, n: int) -> None:
 
     us, err = C.c_double(), C.c_uint32()
     for wgs in wgs_list:
-        for mode in (0, 2):
+        for mode in (0, 2, 6):
+            if mode == 6 and wgs % 8:
+                continue
             check(lib().chk_phase_bench(mode, wgs, n, 0, C.byref(us), C.byref(err)))
             print(f"phase mode={mode} wgs={wgs} mbytes=0 us_per_phase={us.value:.3f} errors={err.value}  # {PHASE_MODES[mode]}",
                   flush=True)

@@ -183,6 +183,10 @@ int chk_profile_graph(ChkEngine* e, int kind, uint32_t reps, double* ms_total, u
  *   mode 5  float atomicAdd without return: wgs workgroups x
  *           bytes_per_phase / 4 adds over a window of `phases` addresses;
  *           us_per_phase = microseconds per launch.
+ *   mode 6  XCD-local barrier: wgs (a multiple of 8) workgroups, those of
+ *           one XCD meeting at a counter in that XCD's L2 each phase and
+ *           reading two others' values (errors: +1000 per workgroup not on
+ *           XCD id % 8).
  * us_per_phase receives the time per phase (modes 2-4: the slope between
  * a quarter-length and a full-length run); errors counts values read back
  * wrong across workgroups (+1e6 if a barrier gave up: every spin is
