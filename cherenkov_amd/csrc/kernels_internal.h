@@ -321,6 +321,7 @@ struct PfGemmArgs {
     const uint16_t* norm;    // [hc H]
     float* out;              // [M][H]
     uint32_t H, hc;
+    uint32_t vec4;           // set by the launcher: outputs leave as 16-byte stores
 };
 
 // DeltaNet prefill (conv, decay/beta, sequential scan) over T rows.

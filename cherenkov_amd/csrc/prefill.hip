@@ -254,6 +254,7 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
     __shared__ __align__(16) u32x4 sA[2][2][64 * PF_AROW];
     __shared__ __align__(16) float sX[2][64];
     __shared__ uint32_t sSB[SBL ? 2 : 1][SBL ? 256 * SBR : 1];
+    __shared__ uint32_t sRow[2][64];  // per tile row: A row of its group sums, Y row
     const int tid = threadIdx.x, lane = tid & 63, col = lane & 15, kq = lane >> 4;
     const uint32_t wn = wave_id();
     uint32_t bx = blockIdx.x, by = blockIdx.y;
@@ -330,11 +331,9 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
         os = ms + rr * G;
         ob = mb + rr * G;
     };
-    uint32_t nout[NJ];  // output index of tile j (PE_HC_UP: the output i)
     uint32_t wo[NMAT][NJ], so[NMAT][NJ], bo[NMAT][NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-        nout[j] = out_of(wn, j, col);
         const uint32_t r = row_of(wn, j, col);
 #pragma unroll
         for (int q = 0; q < NMAT; ++q) offs(q, r, wo[q][j], so[q][j], bo[q][j]);
@@ -356,7 +355,12 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
         const uint32_t m = min(m0 + lrow, M - 1);
         arow_ld = list ? list[m] / a.div : m;
         const uint32_t mx = min(m0 + (tid & 63), M - 1);
-        arow_xs = list ? list[mx] / a.div : mx;
+        const uint32_t e = list ? list[mx] : mx;
+        arow_xs = list ? e / a.div : mx;
+        if (tid < 64) {
+            sRow[0][tid] = arow_xs;
+            sRow[1][tid] = e;
+        }
     }
     const u32x4* ghi = reinterpret_cast<const u32x4*>(a.xhi) + (size_t)arow_ld * KB + lkb;
     const u32x4* glo = reinterpret_cast<const u32x4*>(a.xlo) + (size_t)arow_ld * KB + lkb;
@@ -563,12 +567,17 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
                     const u32x4 v = *reinterpret_cast<const u32x4*>(sbase + bo[q][j] + kc);
                     bbv[q][j] = __builtin_bit_cast(b8, live ? v : u32x4{0u, 0u, 0u, 0u});
                 }
+            // every slice's group sums in flight before any is split
+            float4 xg[NI][2];
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
-                const uint32_t m = min(m0 + i * 16 + col, M - 1);
-                const uint32_t ar = list ? list[m] / a.div : m;
-                const float4* xp = reinterpret_cast<const float4*>(a.xs + (size_t)ar * G + kc);
-                const float4 x0 = xp[0], x1 = xp[1];
+                const float4* xp = reinterpret_cast<const float4*>(a.xs + (size_t)sRow[0][i * 16 + col] * G + kc);
+                xg[i][0] = xp[0];
+                xg[i][1] = xp[1];
+            }
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const float4 x0 = xg[i][0], x1 = xg[i][1];
                 const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
                 uint32_t hw[4], mw[4], lw[4];
 #pragma unroll
@@ -608,50 +617,189 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
         if (g < ge) step(I0{}, g);
     }
 
-    // ---- epilogue
+    // ---- epilogue: the tile leaves through LDS (the A staging buffers) in
+    // two 32-row halves.  Each lane parks its accumulators (one value per
+    // output: silu(gate) * up already formed for PE_SILU_MUL), then thread
+    // t finishes column t (PE_HC_UP: output t % 64 of row t / 64 + 4 k), so
+    // the per-output code is one loop body rather than one unrolled copy
+    // per accumulator, and a wave's stores cover consecutive outputs.
+    float* sO = reinterpret_cast<float*>(&sA[0][0][0]);
+    constexpr uint32_t OS = 260;  // floats per staged row (256 + pad: the four kq rows of a write hit distinct banks)
+    static_assert(32 * OS * sizeof(float) <= sizeof(sA), "a staged half fits the A buffers");
+    constexpr uint32_t NC = 256 / NMAT;  // staged columns
+    const uint32_t gcol = bx * NC + (uint32_t)tid % NC;  // PE_STORE / PE_SILU_MUL / PE_INJECT output column
+    PfSeg sg = a.seg[0];
+    if (EPI == PE_STORE) {
 #pragma unroll
-    for (int i = 0; i < NI; ++i)
+        for (int sgi = 1; sgi < 4; ++sgi)
+            if ((uint32_t)sgi < a.nseg && gcol >= a.seg[sgi].n0) sg = a.seg[sgi];
+    }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint32_t m = m0 + i * 16 + kq * 4 + r;
-            if (m >= M) continue;
-            const uint32_t yrow = list ? list[m] : m;
-            if (EPI == PE_HC_UP) {
-                const uint32_t o = nout[0];
-                if (o >= a.H) continue;
-                const float* hy = a.hyper + (size_t)m * a.hc * a.H;
-                float sum = 0.0f;
+    for (int h = 0; h < 2; ++h) {
+        __syncthreads();
 #pragma unroll
-                for (int j = 0; j < NJ; ++j) {
-                    if ((uint32_t)j >= a.hc) continue;
-                    const size_t k = (size_t)j * a.H + o;
-                    sum += sigmoidf_(acc[0][i][j][r]) * (hy[k] * a.inv[(size_t)m * a.hc + j] * bf16f(a.norm[k]));
+        for (int ii = 0; ii < 2; ++ii) {
+            const int i = 2 * h + ii;
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float v = EPI == PE_SILU_MUL ? siluf_(acc[0][i][j][r]) * acc[NMAT - 1][i][j][r] : acc[0][i][j][r];
+                    sO[(ii * 16 + kq * 4 + r) * OS + wn * (64 / NMAT) + j * 16 + col] = v;
                 }
-                a.out[(size_t)m * a.H + o] = sum / (float)a.hc;
-                continue;
+        }
+        __syncthreads();
+        const uint32_t mh = m0 + 32 * h;
+        if (EPI == PE_HC_UP) {
+            // thread: outputs 4 c4 .. + 3 of the 64, rows r0 + 16 k
+            const uint32_t c4 = (uint32_t)tid & 15, r0 = (uint32_t)tid >> 4, ol = 4 * c4;
+            const uint32_t o = bx * 64 + ol, sc0 = (ol >> 4) * 64 + (ol & 15);
+            const bool ook = o < a.H;  // H % 4 == 0: the group is whole or out
+            const uint32_t oc = ook ? o : 0;
+            float nw[4][4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint2 q = (uint32_t)j < a.hc ? *reinterpret_cast<const uint2*>(a.norm + (size_t)j * a.H + oc)
+                                                   : uint2{0u, 0u};
+                nw[j][0] = __uint_as_float(q.x << 16);
+                nw[j][1] = __uint_as_float(q.x & 0xffff0000u);
+                nw[j][2] = __uint_as_float(q.y << 16);
+                nw[j][3] = __uint_as_float(q.y & 0xffff0000u);
             }
 #pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-                const uint32_t n = nout[j];
-                if (n >= a.N) continue;
-                if (EPI == PE_SILU_MUL) {
-                    a.seg[0].y[(size_t)yrow * a.seg[0].ldy + n] = siluf_(acc[0][i][j][r]) * acc[1][i][j][r];
-                } else if (EPI == PE_INJECT) {
-                    const float v = acc[0][i][j][r];
-                    float* hy = a.hyper + (size_t)m * a.hc * a.H + n;
-                    for (uint32_t g = 0; g < a.hc; ++g) hy[(size_t)g * a.H] += v * a.inj[(size_t)m * a.hc + g];
-                } else {
-                    PfSeg sg = a.seg[0];
+            for (int k = 0; k < 2; ++k) {
+                const uint32_t rr = r0 + 16 * k, m = mh + rr, mc = min(m, M - 1);
+                const float* hy = a.hyper + (size_t)mc * a.hc * a.H + oc;
+                float4 hv[4], uv[4];
+                float iv[4];
 #pragma unroll
-                    for (int sgi = 1; sgi < 4; ++sgi)
-                        if ((uint32_t)sgi < a.nseg && n >= a.seg[sgi].n0) sg = a.seg[sgi];
-                    float v = acc[0][i][j][r];
-                    if (sg.act == PA_SILU) v = siluf_(v * a.alpha);
-                    else if (sg.act == PA_2SIG) v = 2.0f * sigmoidf_(v * a.alpha);
-                    sg.y[(size_t)blockIdx.z * a.zstride + (size_t)yrow * sg.ldy + (n - sg.n0)] = v;
+                for (int j = 0; j < 4; ++j) {
+                    const bool on = (uint32_t)j < a.hc;
+                    hv[j] = on ? *reinterpret_cast<const float4*>(hy + (size_t)j * a.H) : make_float4(0.f, 0.f, 0.f, 0.f);
+                    iv[j] = on ? a.inv[(size_t)mc * a.hc + j] : 0.0f;
+                    uv[j] = *reinterpret_cast<const float4*>(&sO[rr * OS + sc0 + j * 16]);
+                }
+                if (m >= M || !ook) continue;
+                float sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if ((uint32_t)j >= a.hc) continue;
+                    const float hj[4] = {hv[j].x, hv[j].y, hv[j].z, hv[j].w};
+                    const float uj[4] = {uv[j].x, uv[j].y, uv[j].z, uv[j].w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) sum[e] += sigmoidf_(uj[e]) * (hj[e] * iv[j] * nw[j][e]);
+                }
+                const float ih = (float)a.hc;
+                *reinterpret_cast<float4*>(a.out + (size_t)m * a.H + o) =
+                    make_float4(sum[0] / ih, sum[1] / ih, sum[2] / ih, sum[3] / ih);
+            }
+        } else if (a.vec4) {
+            // thread: columns 4 c4 .. + 3, rows r0 + RPP k (16-byte
+            // aligned rows and segments, N % 4 == 0: checked at launch)
+            constexpr uint32_t G4 = NC / 4, RPP = 256 / G4, KB = 32 / RPP;
+            const uint32_t c4 = (uint32_t)tid % G4, r0 = (uint32_t)tid / G4;
+            const uint32_t n4 = bx * NC + 4 * c4;
+            const bool nok = n4 < a.N;
+            PfSeg s4 = a.seg[0];
+            if (EPI == PE_STORE) {
+#pragma unroll
+                for (int sgi = 1; sgi < 4; ++sgi)
+                    if ((uint32_t)sgi < a.nseg && n4 >= a.seg[sgi].n0) s4 = a.seg[sgi];
+            }
+            if (EPI == PE_INJECT) {
+                float4 v[KB];
+#pragma unroll
+                for (int k = 0; k < (int)KB; ++k) v[k] = *reinterpret_cast<const float4*>(&sO[(r0 + RPP * k) * OS + 4 * c4]);
+                const uint32_t nc = nok ? n4 : 0;
+#pragma unroll
+                for (int k = 0; k < (int)KB; ++k) {
+                    const uint32_t m = mh + r0 + RPP * k, mc = min(m, M - 1);
+                    float* hy = a.hyper + (size_t)mc * a.hc * a.H + nc;
+                    float4 hv[4];
+#pragma unroll
+                    for (int g = 0; g < 4; ++g)
+                        hv[g] = (uint32_t)g < a.hc ? *reinterpret_cast<const float4*>(hy + (size_t)g * a.H)
+                                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (m >= M || !nok) continue;
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        if ((uint32_t)g >= a.hc) continue;
+                        const float ij = a.inj[(size_t)m * a.hc + g];
+                        *reinterpret_cast<float4*>(hy + (size_t)g * a.H) =
+                            make_float4(hv[g].x + v[k].x * ij, hv[g].y + v[k].y * ij, hv[g].z + v[k].z * ij,
+                                        hv[g].w + v[k].w * ij);
+                    }
+                }
+            } else {
+                // one row per iteration, the next row's LDS read issued
+                // before this row's activation and store
+                float4 vn = *reinterpret_cast<const float4*>(&sO[r0 * OS + 4 * c4]);
+                uint32_t yn = sRow[1][32 * h + r0];
+#pragma unroll 1
+                for (uint32_t k = 0; k < KB; ++k) {
+                    const uint32_t rr = r0 + RPP * k, m = mh + rr;
+                    const float4 v = vn;
+                    const uint32_t yr = yn;
+                    if (k + 1 < KB) {
+                        vn = *reinterpret_cast<const float4*>(&sO[(rr + RPP) * OS + 4 * c4]);
+                        yn = sRow[1][32 * h + rr + RPP];
+                    }
+                    if (m >= M) break;
+                    if (!nok) continue;
+                    float u[4] = {v.x, v.y, v.z, v.w};
+                    float* dst;
+                    if (EPI == PE_SILU_MUL) {
+                        dst = a.seg[0].y + (size_t)yr * a.seg[0].ldy + n4;
+                    } else {
+                        if (s4.act != PA_NONE) {
+                            // silu(x) = x / (1 + e^-x), 2 sigmoid(x) = 2 / (1 + e^-x)
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) {
+                                const float x = u[e] * a.alpha;
+                                u[e] = (s4.act == PA_SILU ? x : 2.0f) / (1.0f + expf(-x));
+                            }
+                        }
+                        dst = s4.y + (size_t)blockIdx.z * a.zstride + (size_t)yr * s4.ldy + (n4 - s4.n0);
+                    }
+                    *reinterpret_cast<float4*>(dst) = make_float4(u[0], u[1], u[2], u[3]);
+                }
+            }
+        } else {
+            // unaligned outputs (PE_STORE, PE_SILU_MUL): thread t takes
+            // column t % NC, rows in batches of 8 whose reads are all
+            // issued before the first store
+            constexpr uint32_t RPP = 256 / NC;  // rows per pass
+            constexpr int B = 8;
+            const uint32_t lc = (uint32_t)tid % NC, r0 = (uint32_t)tid / NC;
+            const bool nok = gcol < a.N;
+#pragma unroll 1
+            for (uint32_t rb = 0; rb < 32; rb += B * RPP) {
+                float v[B];
+                uint32_t yr[B];
+#pragma unroll
+                for (int k = 0; k < B; ++k) {
+                    const uint32_t rr = rb + r0 + k * RPP;
+                    v[k] = sO[rr * OS + lc];
+                    yr[k] = sRow[1][32 * h + rr];
+                }
+#pragma unroll
+                for (int k = 0; k < B; ++k) {
+                    const uint32_t m = mh + rb + r0 + k * RPP;
+                    if (m >= M || !nok) continue;
+                    if (EPI == PE_SILU_MUL) {
+                        a.seg[0].y[(size_t)yr[k] * a.seg[0].ldy + gcol] = v[k];
+                    } else if (EPI == PE_STORE) {
+                        float u = v[k];
+                        if (sg.act != PA_NONE) {
+                            const float x = u * a.alpha;
+                            u = (sg.act == PA_SILU ? x : 2.0f) / (1.0f + expf(-x));
+                        }
+                        sg.y[(size_t)blockIdx.z * a.zstride + (size_t)yr[k] * sg.ldy + (gcol - sg.n0)] = u;
+                    }
                 }
             }
         }
+    }
 }
 
 // Split-K hyper-connection read: the [down; inject] partials of the hc
@@ -1117,6 +1265,18 @@ void launch_pf_gemm_args(const PfGemmArgs& args, int epi, uint32_t grid_y, hipSt
               a.X.gate_b % 16 == 0 && a.X.up_s % 16 == 0 && a.X.up_b % 16 == 0 && a.X.down_s % 16 == 0 &&
               a.X.down_b % 16 == 0;
     if (epi == PE_HC_UP && a.hc > 4) throw std::runtime_error("prefill mix needs hc <= 4");
+    // 16-byte output stores: N, every output row and every segment start on
+    // a 4-float boundary.  The hc-stream epilogues (inject, mix) have only
+    // that form.
+    bool v4 = a.N % 4 == 0 && (ksplit == 1 || a.zstride % 4 == 0);
+    for (uint32_t q = 0; q < (epi == PE_STORE ? a.nseg : 1u); ++q)
+        v4 = v4 && (uintptr_t)a.seg[q].y % 16 == 0 && a.seg[q].ldy % 4 == 0 && a.seg[q].n0 % 4 == 0;
+    if (epi == PE_INJECT || epi == PE_HC_UP) {
+        v4 = a.H % 4 == 0 && a.N % 4 == 0 && (uintptr_t)a.hyper % 16 == 0 &&
+             (epi == PE_INJECT || ((uintptr_t)a.out % 16 == 0 && (uintptr_t)a.norm % 8 == 0));
+        if (!v4) throw std::runtime_error("prefill hyper-connection GEMMs need 16-byte aligned streams");
+    }
+    a.vec4 = v4 ? 1u : 0u;
 #define PF_GEMM(NM, E, GX)                                                             \
     do {                                                                               \
         if (sbl) k_pf_gemm<NM, E, true><<<dim3(GX, grid_y, ksplit), PF_WG, 0, st>>>(a); \
