@@ -1620,7 +1620,7 @@ uint64_t ChkEngine::prefill_scratch_bytes(uint64_t C, bool all_logits) const {
     const uint64_t at = C * (2ull * D.nh * D.hd + 2ull * D.kv_row + D.idx_out + 2ull * D.nh * D.hd);
     b += std::max(dn, at) * f;
     b += C * (D.E + 1 + 2ull * D.topk) * f + (D.E + 1ull) * C * 4 + (D.E + 1) * 4;
-    b += (uint64_t)pf_tile_bound((uint32_t)C, D.topk, D.E) * 4 + C * slots * (D.I + D.H) * f;
+    b += (uint64_t)(pf_tile_bound((uint32_t)C, D.topk, D.E, 48) + pf_tile_bound((uint32_t)C, D.topk, D.E, 64)) * 4 + C * slots * (D.I + D.H) * f;
     if (dc_supported(D.nk, D.nv, D.dk, D.dv)) b += dc_work_floats((uint32_t)C, D.nv, D.dv) * f;
     if (all_logits) b += C * D.V * f;
     if (ple_l >= 0) b += C * (ngram_heads + c.ple_embed_dim + 3ull * D.hh + D.H) * 4;
@@ -1722,8 +1722,8 @@ void ChkEngine::pf_alloc() {
     pf.ids = pfalloc<uint32_t>(C * D.topk);
     pf.list = pfalloc<uint32_t>((D.E + 1) * C);
     pf.count = pfalloc<uint32_t>(D.E + 1);
-    pf.tiles = pfalloc<uint32_t>(pf_tile_bound((uint32_t)C, D.topk, D.E));
-    pf.ntiles = pfalloc<uint32_t>(1);
+    pf.tiles = pfalloc<uint32_t>(pf_tile_bound((uint32_t)C, D.topk, D.E, 48) + pf_tile_bound((uint32_t)C, D.topk, D.E, 64));
+    pf.ntiles = pfalloc<uint32_t>(2);
     pf.act = pfalloc<float>(C * slots * D.I);
     pf.yd = pfalloc<float>(C * slots * D.H);
     pf.dcw = dc_supported(D.nk, D.nv, D.dk, D.dv) ? pfalloc<float>(dc_work_floats((uint32_t)C, D.nv, D.dv)) : nullptr;
@@ -1755,8 +1755,8 @@ void ChkEngine::pf_hc_read(const HcDev& w, float* inj, uint32_t T, bool for_moe)
     // split K by stream, partials summed in stream order by the finisher
     const uint32_t N = D.lowrank + D.hc;
     PfGemmArgs g{};
-    g.seg[0] = PfSeg{w.down, pf.hc_part, N, 0, PA_NONE};
-    g.seg[1] = PfSeg{w.inject, pf.hc_part + D.lowrank, N, D.lowrank, PA_NONE};
+    g.seg[0] = PfSeg{w.down, pf.hc_part, N, 0};
+    g.seg[1] = PfSeg{w.inject, pf.hc_part + D.lowrank, N, D.lowrank};
     g.nseg = 2;
     g.N = N;
     g.K = D.hh;
@@ -1808,10 +1808,10 @@ void ChkEngine::pf_hc_read(const HcDev& w, float* inj, uint32_t T, bool for_moe)
 void ChkEngine::pf_deltanet(const LayerDev& L, uint32_t T) {
     const uint32_t mt = (T + 63) / 64, di = (uint32_t)L.dn_idx;
     PfGemmArgs g{};
-    g.seg[0] = PfSeg{L.dn.qkv, pf.raw, D.conv_dim, 0, PA_NONE};
-    g.seg[1] = PfSeg{L.dn.z, pf.z, D.v_dim, D.conv_dim, PA_NONE};
-    g.seg[2] = PfSeg{L.dn.a, pf.a, D.nv, D.conv_dim + D.v_dim, PA_NONE};
-    g.seg[3] = PfSeg{L.dn.b, pf.b, D.nv, D.conv_dim + D.v_dim + D.nv, PA_NONE};
+    g.seg[0] = PfSeg{L.dn.qkv, pf.raw, D.conv_dim, 0};
+    g.seg[1] = PfSeg{L.dn.z, pf.z, D.v_dim, D.conv_dim};
+    g.seg[2] = PfSeg{L.dn.a, pf.a, D.nv, D.conv_dim + D.v_dim};
+    g.seg[3] = PfSeg{L.dn.b, pf.b, D.nv, D.conv_dim + D.v_dim + D.nv};
     g.nseg = 4;
     g.N = D.conv_dim + D.v_dim + 2 * D.nv;
     g.K = D.H;
@@ -1881,10 +1881,10 @@ void ChkEngine::pf_attention(const LayerDev& L, uint32_t T, uint32_t pos0, const
     const KvDev& kvl = kvo ? *kvo : kv[L.at_idx];
     const uint32_t mt = (T + 63) / 64;
     PfGemmArgs g{};
-    g.seg[0] = PfSeg{L.at.q, pf.q_raw, 2 * D.nh * D.hd, 0, PA_NONE};
-    g.seg[1] = PfSeg{L.at.k, pf.k_raw, D.kv_row, 2 * D.nh * D.hd, PA_NONE};
-    g.seg[2] = PfSeg{L.at.v, pf.v_raw, D.kv_row, 2 * D.nh * D.hd + D.kv_row, PA_NONE};
-    g.seg[3] = PfSeg{L.at.idx, pf.idx_raw, D.idx_out, 2 * D.nh * D.hd + 2 * D.kv_row, PA_NONE};
+    g.seg[0] = PfSeg{L.at.q, pf.q_raw, 2 * D.nh * D.hd, 0};
+    g.seg[1] = PfSeg{L.at.k, pf.k_raw, D.kv_row, 2 * D.nh * D.hd};
+    g.seg[2] = PfSeg{L.at.v, pf.v_raw, D.kv_row, 2 * D.nh * D.hd + D.kv_row};
+    g.seg[3] = PfSeg{L.at.idx, pf.idx_raw, D.idx_out, 2 * D.nh * D.hd + 2 * D.kv_row};
     g.nseg = 4;
     g.N = 2 * D.nh * D.hd + 2 * D.kv_row + D.idx_out;
     g.K = D.H;
@@ -1975,12 +1975,8 @@ void ChkEngine::pf_moe(const LayerDev& L, uint32_t T) {
     // the chunk's last row also as this layer's "last routes", as a row step leaves them
     const uint64_t roff = (uint64_t)L.moe.record_layer * MAX_NB * D.topk;
     launch_pf_route(pf.logits, T, D.E, D.topk, D.norm_topk, pf.ids, pf.wts, s.route_ids + roff, s.route_w + roff, st);
-    // (also counts the layer's expert activity)
-    launch_pf_group(pf.ids, T, D.topk, D.E, pf.cap, pf.list, pf.count, pf.tiles, pf.ntiles, act,
-                    L.moe.record_layer, st);
-    const uint32_t bound = pf_tile_bound(T, D.topk, D.E);
     PfGemmArgs gu{};
-    gu.seg[0] = PfSeg{L.moe.sh_gate, pf.act, D.I, 0, PA_NONE};
+    gu.seg[0] = PfSeg{L.moe.sh_gate, pf.act, D.I, 0};
     gu.seg[1].m = L.moe.sh_up;
     gu.nseg = 1;
     gu.N = D.I;
@@ -1996,15 +1992,25 @@ void ChkEngine::pf_moe(const LayerDev& L, uint32_t T) {
     gu.div = slots;
     gu.X = experts_dev();
     gu.record_layer = L.moe.record_layer;
-    launch_pf_gemm_args(gu, PE_SILU_MUL, bound, st);
-    launch_pf_xprep(pf.act, D.I, T * slots, D.I, pf.hi, pf.lo, pf.xs, st);
     PfGemmArgs dn = gu;
-    dn.seg[0] = PfSeg{L.moe.sh_down, pf.yd, D.H, 0, PA_NONE};
+    dn.seg[0] = PfSeg{L.moe.sh_down, pf.yd, D.H, 0};
     dn.seg[1] = PfSeg{};
     dn.N = D.H;
     dn.K = D.I;
     dn.div = 1;
-    launch_pf_gemm_args(dn, PE_STORE, bound, st);
+    // experts hold ~T k / E rows: gate/up in 48-row tiles where it takes
+    // the staged-scale form (Q4 records); the down GEMM, 8 groups deep,
+    // keeps 64-row tiles (fewer workgroups to start and finish)
+    const uint32_t tr = pf_gemm_staged(gu, PE_SILU_MUL) ? 48 : 64;
+    gu.tile_rows = tr;
+    dn.tiles = pf.tiles + pf_tile_bound(T, D.topk, D.E, tr);
+    dn.ntiles = pf.ntiles + 1;
+    // (also counts the layer's expert activity)
+    launch_pf_group(pf.ids, T, D.topk, D.E, pf.cap, pf.list, pf.count, pf.tiles, pf.ntiles, act,
+                    L.moe.record_layer, tr, st);
+    launch_pf_gemm_args(gu, PE_SILU_MUL, pf_tile_bound(T, D.topk, D.E, tr), st);
+    launch_pf_xprep(pf.act, D.I, T * slots, D.I, pf.hi, pf.lo, pf.xs, st);
+    launch_pf_gemm_args(dn, PE_STORE, pf_tile_bound(T, D.topk, D.E, 64), st);
     launch_pf_moe_combine(pf.yd, pf.wts, pf.sg, pf.inj_m, pf.hyper, T, D.H, D.topk, D.hc, st);
 }
 

@@ -268,7 +268,6 @@ struct AttnArgs {
 
 // ------------------------------------------------------------- prefill
 enum PfEpi { PE_STORE = 0, PE_INJECT = 1, PE_HC_UP = 2, PE_SILU_MUL = 3 };
-enum PfAct { PA_NONE = 0, PA_SILU = 1, PA_2SIG = 2 };
 
 // Operand preparation of one activation matrix (k_pf_prep).
 struct PfPrepArgs {
@@ -291,14 +290,12 @@ struct PfSeg {
     Q4Mat m;
     float* y;
     uint32_t ldy, n0;
-    int act;  // PfAct of alpha * v
     uint32_t wo, so, bo;  // set by the launcher: element offsets of m from wbase / sbase
 };
 
 struct PfGemmArgs {
     PfSeg seg[4];      // PE_SILU_MUL: seg[0].m gate, seg[1].m up (shared expert), output seg[0].y
     uint32_t nseg, N, K, M;
-    float alpha;
     uint32_t ksplit;         // K chunks (grid z); PE_STORE then writes chunk z at y + z zstride
     uint64_t zstride;
     const uint4* xhi;
@@ -322,6 +319,7 @@ struct PfGemmArgs {
     float* out;              // [M][H]
     uint32_t H, hc;
     uint32_t vec4;           // set by the launcher: outputs leave as 16-byte stores
+    uint32_t tile_rows;      // rows per tile: 64 (0) or 48 (grouped gate/up)
 };
 
 // DeltaNet prefill (conv, decay/beta, sequential scan) over T rows.
@@ -379,6 +377,8 @@ void launch_pf_xprep(const float* x, uint32_t ldx, uint32_t T, uint32_t K, uint4
 void launch_pf_hc_prep(const float* hyper, const uint16_t* norm, uint32_t H, uint32_t hc, float eps, float* inv,
                        uint4* hi, uint4* lo, float* xs, uint32_t T, hipStream_t st);
 void launch_pf_gemm_args(const PfGemmArgs& a, int epi, uint32_t grid_y, hipStream_t st);
+// whether a GEMM takes the staged-scale form (needed by tiles under 64 rows)
+bool pf_gemm_staged(const PfGemmArgs& a, int epi);
 void launch_pf_flash(const float* q_ready, const float* q_raw, const KvDev& kv, float* out, uint32_t T, uint32_t pos0,
                      uint32_t nh, uint32_t nkv, uint32_t hd, float scale, hipStream_t st);
 void launch_pf_gemm(const Q4Mat& w, const uint4* xhi, const uint4* xlo, const float* xs, float* y, uint32_t T,
@@ -390,9 +390,9 @@ void launch_pf_router(const uint16_t* router, const uint16_t* shared_gate, const
 void launch_pf_route(const float* logits, uint32_t T, uint32_t E, uint32_t topk, int norm_topk, uint32_t* ids,
                      float* wts, uint32_t* last_ids, float* last_wts, hipStream_t st);
 void launch_pf_group(const uint32_t* ids, uint32_t T, uint32_t topk, uint32_t E, uint32_t cap, uint32_t* list,
-                     uint32_t* count, uint32_t* tiles, uint32_t* ntiles, uint64_t* act, uint32_t layer,
+                     uint32_t* count, uint32_t* tiles, uint32_t* ntiles, uint64_t* act, uint32_t layer, uint32_t tr,
                      hipStream_t st);
-uint32_t pf_tile_bound(uint32_t T, uint32_t topk, uint32_t E);
+uint32_t pf_tile_bound(uint32_t T, uint32_t topk, uint32_t E, uint32_t tr);
 void launch_pf_moe_combine(const float* yd, const float* wts, const float* sg, const float* inj, float* hyper,
                            uint32_t T, uint32_t H, uint32_t topk, uint32_t hc, hipStream_t st);
 void launch_pf_embed(const uint32_t* tokens, const Q4Mat& emb, float* hyper, uint32_t H, uint32_t hc, uint32_t T,

@@ -196,10 +196,10 @@ __global__ void __launch_bounds__(256) k_pf_hc_prep(const float* __restrict__ hy
 }
 
 // --------------------------------------------------------------- GEMM
-// Tile: a workgroup of 4 waves covers 64 rows x 256 / NMAT outputs of every
-// matrix; wave w takes all 64 rows and outputs 64 w / NMAT .. (four 16-wide
-// MFMA tiles per 16 rows in all), so every unpacked weight word feeds 4 x 2
-// MFMAs.  The 64-row A tile of each quant group (hi and lo planes, 16 KiB)
+// Tile: a workgroup of 4 waves covers 16 NI (64) rows x 256 / NMAT outputs
+// of every matrix; wave w takes all rows and outputs 64 w / NMAT .. (four
+// 16-wide MFMA tiles per 16 rows in all), so every unpacked weight word
+// feeds NI x 2 MFMAs.  The A tile of each quant group (hi and lo planes)
 // is staged through LDS once for the 4 waves, double-buffered with the
 // next group's global loads; every wave streams its own weight words one
 // group ahead.  Per group and 16-row slice the MFMA partial sums start from
@@ -207,17 +207,16 @@ __global__ void __launch_bounds__(256) k_pf_hc_prep(const float* __restrict__ hy
 // the group's scale.  Two workgroups share a CU.
 //
 // Rows: dense (row m of A and Y), or grouped: a tile list names (group,
-// 64-row tile); list[group][m] is an entry e, A row e / div, Y row e.  The
+// tile); list[group][m] is an entry e, A row e / div, Y row e.  The
 // routed-expert GEMMs group the (token, slot) entries e = t (k+1) + slot
 // by expert (gate/up read token t, down reads the entry's activation);
 // group == X.experts is the shared expert.
 //
-// Epilogues: PE_STORE (concatenated segments, each with its own output,
-// optional silu / 2 sigmoid of alpha v), PE_INJECT (hyper[t][g H + n] +=
-// v inj[t][g], inject, cpu.rs:971-979), PE_HC_UP (the four 16-wide tiles of
-// a wave are the hc streams of the same 16 outputs: mixed = (1/hc) sum_g
-// sigmoid(v_g) normed_g, cpu.rs:477-491), PE_SILU_MUL (NMAT 2:
-// silu(gate) * up, mlp, cpu.rs:981-992).
+// Epilogues: PE_STORE (concatenated segments, each with its own output),
+// PE_INJECT (hyper[t][g H + n] += v inj[t][g], inject, cpu.rs:971-979),
+// PE_HC_UP (the four 16-wide tiles of a wave are the hc streams of the same
+// 16 outputs: mixed = (1/hc) sum_g sigmoid(v_g) normed_g, cpu.rs:477-491),
+// PE_SILU_MUL (NMAT 2: silu(gate) * up, mlp, cpu.rs:981-992).
 constexpr int PF_WG = 256;  // threads per GEMM workgroup
 constexpr int PF_AROW = 9;  // uint4 per staged A row (8 + 1 pad: bank spread)
 
@@ -230,31 +229,36 @@ CHK_DEV h8 pf_unpack(uint32_t w, const Q4Consts& qk) {
     return h8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
 }
 
-// SBL: the scales and biases of the workgroup's 256 weight rows are staged
-// through LDS in blocks of 8 groups (thread t loads row t's 8 scales and 8
-// biases with two 16-byte loads per block and interleaves them into
-// (scale | bias << 16) words); the main loop then folds only s * partial,
-// and the bias term sum_g b[n][g] xs[m][g] runs after it as its own small
-// MFMA contraction over the groups (bf16, with xs split into three bf16
-// terms so every product is exact).  Needs G % 8 == 0 and 16-byte aligned
-// rows; otherwise each lane loads its scale and bias per group and folds
-// both in the loop.
+// SBL: the scales of the workgroup's 256 weight rows are staged through LDS
+// in blocks of 8 groups (thread t loads row t's 8 scales with one 16-byte
+// load per block and stores them as f32, group-major); the main loop then
+// folds only s * partial, and the bias term sum_g b[n][g] xs[m][g] opens
+// the accumulation as its own small MFMA contraction over the groups (bf16,
+// with xs split into three bf16 terms so every product is exact).  Needs
+// G % 8 == 0 and 16-byte aligned rows; otherwise each lane loads its scale
+// and bias per group and folds both in the loop.  SBL launches also take
+// the transposed tile and may use tiles of NI = 3 slices (48 rows).
 // BITS: the routed-expert records' precision.  Q3 / Q2 rows (lowbit.rs
 // chunks of 32 codes in 3 / 2 words) load, per group and lane, the word of
 // the lane's 16 inputs (and Q3's low-bit word) and expand it to the two
 // Q4-order nibble words the unpack expects; their scale and bias carry the
 // midpoint rule (step s, half s + b), folded per lane in f32, so such
 // launches run without staged scales.
-template <int NMAT, int EPI, bool SBL, int BITS = 4>
+template <int NMAT, int EPI, bool SBL, int BITS = 4, int NI = 4>
 __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
     static_assert(BITS == 4 || !SBL, "low-bit records fold their scales per lane");
-    constexpr int NJ = 4 / NMAT;  // 16-wide output tiles per matrix per wave
-    constexpr int NI = 4;         // 16-row slices per wave
-    constexpr int SBR = 9;        // words per staged scale row (8 groups + pad)
+    static_assert(NI == 4 || SBL, "tiles of fewer than 64 rows take the transposed (staged-scale) form");
+    constexpr int NJ = 4 / NMAT;       // 16-wide output tiles per matrix per wave
+    constexpr uint32_t TR = 16 * NI;   // tile rows: NI 16-row slices per wave
+    // SBL launches compute the transposed tile (weights as the MFMA's A
+    // operand): a lane then holds 4 consecutive outputs of one row, so the
+    // scales it folds are 4 consecutive staged rows and its results leave
+    // as 16-byte stores straight from registers
+    constexpr bool SW = SBL;
     __shared__ __align__(16) u32x4 sA[2][2][64 * PF_AROW];
     __shared__ __align__(16) float sX[2][64];
-    __shared__ uint32_t sSB[SBL ? 2 : 1][SBL ? 256 * SBR : 1];
-    __shared__ uint32_t sRow[2][64];  // per tile row: A row of its group sums, Y row
+    __shared__ __align__(16) float sSB[SBL ? 2 : 1][SBL ? 8 * 256 : 1];  // [block][group % 8][local row]
+    __shared__ uint32_t sRow[64];  // Y row of each tile row (staged epilogue)
     const int tid = threadIdx.x, lane = tid & 63, col = lane & 15, kq = lane >> 4;
     const uint32_t wn = wave_id();
     uint32_t bx = blockIdx.x, by = blockIdx.y;
@@ -279,7 +283,7 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
         mt = tv & 0xffffu;
     }
     const uint32_t M = a.list ? a.count[grp] : a.M;
-    const uint32_t m0 = mt * 64;
+    const uint32_t m0 = mt * TR;
     if (m0 >= M) return;
     const uint32_t* list = a.list ? a.list + (size_t)grp * a.cap : nullptr;
     const uint32_t K = a.K, G = K >> 6, KB = K >> 3;
@@ -339,28 +343,28 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
         for (int q = 0; q < NMAT; ++q) offs(q, r, wo[q][j], so[q][j], bo[q][j]);
     }
     // scale loader (SBL): thread tid stages local row tid
-    uint32_t ld_so = 0, ld_bo = 0;
+    uint32_t ld_so = 0;
     if (SBL) {
         const uint32_t wn_ = (uint32_t)tid >> 6, rem = (uint32_t)tid & 63;
         const int q = (int)(rem / (NJ * 16)), j = (int)((rem >> 4) % NJ);
-        uint32_t ow;
-        offs(q, row_of(wn_, j, rem & 15), ow, ld_so, ld_bo);
+        uint32_t ow, ob;
+        offs(q, row_of(wn_, j, rem & 15), ow, ld_so, ob);
     }
 
     // ---- A staging: thread tid loads 8-blocks 2 (tid % 4) + {0, 1} of row
     // tid / 4 (hi, lo planes) and the group sum of row tid % 64
+    // (tiles under 64 rows: the threads past the tile re-read its last row,
+    // into buffer rows nobody reads; no branch keeps the pipeline's
+    // registers in one straight schedule)
     const uint32_t lrow = tid >> 2, lkb = (tid & 3) * 2;
     uint32_t arow_ld, arow_xs;
     {
-        const uint32_t m = min(m0 + lrow, M - 1);
+        const uint32_t m = min(m0 + min(lrow, TR - 1), M - 1);
         arow_ld = list ? list[m] / a.div : m;
         const uint32_t mx = min(m0 + (tid & 63), M - 1);
         const uint32_t e = list ? list[mx] : mx;
         arow_xs = list ? e / a.div : mx;
-        if (tid < 64) {
-            sRow[0][tid] = arow_xs;
-            sRow[1][tid] = e;
-        }
+        if (tid < 64) sRow[tid] = e;
     }
     const u32x4* ghi = reinterpret_cast<const u32x4*>(a.xhi) + (size_t)arow_ld * KB + lkb;
     const u32x4* glo = reinterpret_cast<const u32x4*>(a.xlo) + (size_t)arow_ld * KB + lkb;
@@ -376,13 +380,13 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
     u32x2 bw[2][NMAT][NJ];                         // words 2 kq, 2 kq + 1: K-steps 0, 1
     uint16_t bs[2][SBL ? 1 : NMAT][SBL ? 1 : NJ];  // per-lane scale, bias (not SBL)
     uint16_t bb[2][SBL ? 1 : NMAT][SBL ? 1 : NJ];
-    u32x4 sreg_s, sreg_b;                          // SBL: the next block's 8 scales, 8 biases
+    u32x4 sreg_s;                                  // SBL: the next block's 8 scales
     auto fetch = [&](int slot, uint32_t g) __attribute__((always_inline)) {
         rah0[slot] = ghi[g * 8];
         rah1[slot] = ghi[g * 8 + 1];
         ral0[slot] = glo[g * 8];
         ral1[slot] = glo[g * 8 + 1];
-        rx[slot] = gxs[g];
+        if (!SBL) rx[slot] = gxs[g];
 #pragma unroll
         for (int q = 0; q < NMAT; ++q)
 #pragma unroll
@@ -409,20 +413,18 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
         sA[buf][0][lrow * PF_AROW + lkb + 1] = rah1[slot];
         sA[buf][1][lrow * PF_AROW + lkb] = ral0[slot];
         sA[buf][1][lrow * PF_AROW + lkb + 1] = ral1[slot];
-        sX[buf][tid & 63] = rx[slot];  // four identical writes per row: no branch
+        if (!SBL) sX[buf][tid & 63] = rx[slot];  // four identical writes per row: no branch
     };
     auto sb_fetch = [&](uint32_t g0) __attribute__((always_inline)) {
         sreg_s = *reinterpret_cast<const u32x4*>(sbase + ld_so + g0);
-        sreg_b = *reinterpret_cast<const u32x4*>(sbase + ld_bo + g0);
     };
     auto sb_store = [&](uint32_t buf) __attribute__((always_inline)) {
-        uint32_t* d = &sSB[buf][tid * SBR];
+        float* d = &sSB[buf][tid];
         const uint32_t sv[4] = {sreg_s.x, sreg_s.y, sreg_s.z, sreg_s.w};
-        const uint32_t bv[4] = {sreg_b.x, sreg_b.y, sreg_b.z, sreg_b.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            d[2 * e] = (sv[e] & 0xffffu) | (bv[e] << 16);
-            d[2 * e + 1] = (sv[e] >> 16) | (bv[e] & 0xffff0000u);
+            d[(2 * e) * 256] = __uint_as_float(sv[e] << 16);
+            d[(2 * e + 1) * 256] = __uint_as_float(sv[e] & 0xffff0000u);
         }
     };
 
@@ -467,14 +469,15 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
                 bq[q][j][1] = pf_unpack(w1, qk);
             }
         float sc[NMAT][NJ], bi[NMAT][NJ];
+        float4 sc4[NMAT][NJ];  // SW: the scales of the lane's 4 outputs
 #pragma unroll
         for (int q = 0; q < NMAT; ++q)
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
                 if (SBL) {
-                    const uint32_t v = sSB[((g - gb) >> 3) & 1][(((wn * NMAT + q) * NJ + j) * 16 + col) * SBR + S];
-                    sc[q][j] = __uint_as_float(v << 16);
-                    bi[q][j] = 0.0f;
+                    sc4[q][j] = *reinterpret_cast<const float4*>(
+                        &sSB[((g - gb) >> 3) & 1][S * 256 + ((wn * NMAT + q) * NJ + j) * 16 + kq * 4]);
+                    sc[q][j] = bi[q][j] = 0.0f;
                 } else {
                     sc[q][j] = bf16f(bs[P][SBL ? 0 : q][SBL ? 0 : j]);
                     bi[q][j] = bf16f(bb[P][SBL ? 0 : q][SBL ? 0 : j]);
@@ -498,8 +501,13 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
 #pragma unroll
                     for (int j = 0; j < NJ; ++j) {
                         const f4 c0 = s == 0 ? f4{0.0f, 0.0f, 0.0f, 0.0f} : accg[q][j];
-                        accg[q][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq[q][j][s], c0, 0, 0, 0);
-                        accg[q][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bq[q][j][s], accg[q][j], 0, 0, 0);
+                        if (SW) {
+                            accg[q][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bq[q][j][s], ah, c0, 0, 0, 0);
+                            accg[q][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bq[q][j][s], al, accg[q][j], 0, 0, 0);
+                        } else {
+                            accg[q][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq[q][j][s], c0, 0, 0, 0);
+                            accg[q][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bq[q][j][s], accg[q][j], 0, 0, 0);
+                        }
                     }
             }
             if (SBL) {
@@ -508,7 +516,7 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
 #pragma unroll
                     for (int j = 0; j < NJ; ++j)
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) acc[q][i][j][r] = fmaf(sc[q][j], accg[q][j][r], acc[q][i][j][r]);
+                        for (int r = 0; r < 4; ++r) acc[q][i][j][r] = fmaf(sc4[q][j][r], accg[q][j][r], acc[q][i][j][r]);
             } else {
                 const float4 xv = *reinterpret_cast<const float4*>(&sX[P][i * 16 + kq * 4]);
                 const float xr[4] = {xv.x, xv.y, xv.z, xv.w};
@@ -532,9 +540,70 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
 
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
+    // bias term (SBL): acc[n][m] = sum_{g in [gb, ge)} b[n][g] xs[m][g], a
+    // small MFMA contraction over the groups (bf16, with xs split into three
+    // bf16 terms so every product is exact), 32 groups per K-step: lane
+    // (col, kq) takes groups k0 + 8 kq .. + 8 (whole 8-blocks: zero past
+    // ge).  It opens the accumulation, its loads in flight with the first
+    // group's, so its latency overlaps theirs rather than trailing the loop.
+    auto bias_pass = [&](uint32_t k0) __attribute__((always_inline)) {
+        const uint32_t kg = k0 + 8 * kq;
+        const bool live = kg < ge;
+        const uint32_t kc = live ? kg : gb;
+        b8 bbv[NMAT][NJ];
+#pragma unroll
+        for (int q = 0; q < NMAT; ++q)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                const u32x4 v = *reinterpret_cast<const u32x4*>(sbase + bo[q][j] + kc);
+                bbv[q][j] = __builtin_bit_cast(b8, live ? v : u32x4{0u, 0u, 0u, 0u});
+            }
+        float4 xg[NI][2];
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const uint32_t m = min(m0 + i * 16 + col, M - 1);
+            const uint32_t ar = list ? list[m] / a.div : m;
+            const float4* xp = reinterpret_cast<const float4*>(a.xs + (size_t)ar * G + kc);
+            xg[i][0] = xp[0];
+            xg[i][1] = xp[1];
+        }
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const float4 x0 = xg[i][0], x1 = xg[i][1];
+            const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            uint32_t hw[4], mw[4], lw[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                uint32_t h2_[2], m2_[2], l2_[2];
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const float xx = live ? xv[2 * e + u] : 0.0f;
+                    h2_[u] = f2bf_rne(xx);
+                    const float r1 = xx - __uint_as_float(h2_[u] << 16);
+                    m2_[u] = f2bf_rne(r1);
+                    l2_[u] = f2bf_rne(r1 - __uint_as_float(m2_[u] << 16));
+                }
+                hw[e] = h2_[0] | h2_[1] << 16;
+                mw[e] = m2_[0] | m2_[1] << 16;
+                lw[e] = l2_[0] | l2_[1] << 16;
+            }
+            const b8 xh = __builtin_bit_cast(b8, u32x4{hw[0], hw[1], hw[2], hw[3]});
+            const b8 xm = __builtin_bit_cast(b8, u32x4{mw[0], mw[1], mw[2], mw[3]});
+            const b8 xl = __builtin_bit_cast(b8, u32x4{lw[0], lw[1], lw[2], lw[3]});
+#pragma unroll
+            for (int q = 0; q < NMAT; ++q)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    acc[q][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bbv[q][j], xl, acc[q][i][j], 0, 0, 0);
+                    acc[q][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bbv[q][j], xm, acc[q][i][j], 0, 0, 0);
+                    acc[q][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bbv[q][j], xh, acc[q][i][j], 0, 0, 0);
+                }
+        }
+    };
     fetch(0, gb);
     if (SBL) {
         sb_fetch(gb);
+        for (uint32_t k0 = gb; k0 < ge; k0 += 32) bias_pass(k0);
         sb_store(0);
     }
     a_store(0, 0);
@@ -550,64 +619,6 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
             step(std::integral_constant<int, 6>{}, g + 6);
             step(std::integral_constant<int, 7>{}, g + 7);
         }
-        // bias term: acc[m][n] += sum_{g in [gb, ge)} b[n][g] xs[m][g], 32
-        // groups per bf16 MFMA K-step; lane (col, kq) takes groups
-        // k0 + 8 kq .. + 8 (whole 8-blocks: zero past ge)
-        const uint16_t zero16 = 0;
-        (void)zero16;
-        for (uint32_t k0 = gb; k0 < ge; k0 += 32) {
-            const uint32_t kg = k0 + 8 * kq;
-            const bool live = kg < ge;
-            const uint32_t kc = live ? kg : gb;
-            b8 bbv[NMAT][NJ];
-#pragma unroll
-            for (int q = 0; q < NMAT; ++q)
-#pragma unroll
-                for (int j = 0; j < NJ; ++j) {
-                    const u32x4 v = *reinterpret_cast<const u32x4*>(sbase + bo[q][j] + kc);
-                    bbv[q][j] = __builtin_bit_cast(b8, live ? v : u32x4{0u, 0u, 0u, 0u});
-                }
-            // every slice's group sums in flight before any is split
-            float4 xg[NI][2];
-#pragma unroll
-            for (int i = 0; i < NI; ++i) {
-                const float4* xp = reinterpret_cast<const float4*>(a.xs + (size_t)sRow[0][i * 16 + col] * G + kc);
-                xg[i][0] = xp[0];
-                xg[i][1] = xp[1];
-            }
-#pragma unroll
-            for (int i = 0; i < NI; ++i) {
-                const float4 x0 = xg[i][0], x1 = xg[i][1];
-                const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-                uint32_t hw[4], mw[4], lw[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    uint32_t h2_[2], m2_[2], l2_[2];
-#pragma unroll
-                    for (int u = 0; u < 2; ++u) {
-                        const float xx = live ? xv[2 * e + u] : 0.0f;
-                        h2_[u] = f2bf_rne(xx);
-                        const float r1 = xx - __uint_as_float(h2_[u] << 16);
-                        m2_[u] = f2bf_rne(r1);
-                        l2_[u] = f2bf_rne(r1 - __uint_as_float(m2_[u] << 16));
-                    }
-                    hw[e] = h2_[0] | h2_[1] << 16;
-                    mw[e] = m2_[0] | m2_[1] << 16;
-                    lw[e] = l2_[0] | l2_[1] << 16;
-                }
-                const b8 xh = __builtin_bit_cast(b8, u32x4{hw[0], hw[1], hw[2], hw[3]});
-                const b8 xm = __builtin_bit_cast(b8, u32x4{mw[0], mw[1], mw[2], mw[3]});
-                const b8 xl = __builtin_bit_cast(b8, u32x4{lw[0], lw[1], lw[2], lw[3]});
-#pragma unroll
-                for (int q = 0; q < NMAT; ++q)
-#pragma unroll
-                    for (int j = 0; j < NJ; ++j) {
-                        acc[q][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, bbv[q][j], acc[q][i][j], 0, 0, 0);
-                        acc[q][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xm, bbv[q][j], acc[q][i][j], 0, 0, 0);
-                        acc[q][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, bbv[q][j], acc[q][i][j], 0, 0, 0);
-                    }
-            }
-        }
     } else {
         uint32_t g = gb;
         for (; g + 2 <= ge; g += 2) {
@@ -617,45 +628,24 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
         if (g < ge) step(I0{}, g);
     }
 
-    // ---- epilogue: the tile leaves through LDS (the A staging buffers) in
-    // two 32-row halves.  Each lane parks its accumulators (one value per
-    // output: silu(gate) * up already formed for PE_SILU_MUL), then thread
-    // t finishes column t (PE_HC_UP: output t % 64 of row t / 64 + 4 k), so
-    // the per-output code is one loop body rather than one unrolled copy
-    // per accumulator, and a wave's stores cover consecutive outputs.
-    float* sO = reinterpret_cast<float*>(&sA[0][0][0]);
-    constexpr uint32_t OS = 260;  // floats per staged row (256 + pad: the four kq rows of a write hit distinct banks)
-    static_assert(32 * OS * sizeof(float) <= sizeof(sA), "a staged half fits the A buffers");
-    constexpr uint32_t NC = 256 / NMAT;  // staged columns
-    const uint32_t gcol = bx * NC + (uint32_t)tid % NC;  // PE_STORE / PE_SILU_MUL / PE_INJECT output column
-    PfSeg sg = a.seg[0];
-    if (EPI == PE_STORE) {
+    // ---- epilogue, transposed tile (SW): lane (col, kq) of tile (i, j)
+    // holds outputs tile base + 4 kq .. + 3 of row m0 + 16 i + col, which
+    // leave as one 16-byte store (four scalar ones where rows or segments
+    // are not 16-byte aligned)
+    if constexpr (SW) {
+        constexpr uint32_t NC = 256 / NMAT;
+        uint32_t yrow[NI];
+        bool mok[NI];
 #pragma unroll
-        for (int sgi = 1; sgi < 4; ++sgi)
-            if ((uint32_t)sgi < a.nseg && gcol >= a.seg[sgi].n0) sg = a.seg[sgi];
-    }
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        __syncthreads();
-#pragma unroll
-        for (int ii = 0; ii < 2; ++ii) {
-            const int i = 2 * h + ii;
-#pragma unroll
-            for (int j = 0; j < NJ; ++j)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float v = EPI == PE_SILU_MUL ? siluf_(acc[0][i][j][r]) * acc[NMAT - 1][i][j][r] : acc[0][i][j][r];
-                    sO[(ii * 16 + kq * 4 + r) * OS + wn * (64 / NMAT) + j * 16 + col] = v;
-                }
+        for (int i = 0; i < NI; ++i) {
+            mok[i] = m0 + i * 16 + col < M;
+            yrow[i] = sRow[i * 16 + col];
         }
-        __syncthreads();
-        const uint32_t mh = m0 + 32 * h;
         if (EPI == PE_HC_UP) {
-            // thread: outputs 4 c4 .. + 3 of the 64, rows r0 + 16 k
-            const uint32_t c4 = (uint32_t)tid & 15, r0 = (uint32_t)tid >> 4, ol = 4 * c4;
-            const uint32_t o = bx * 64 + ol, sc0 = (ol >> 4) * 64 + (ol & 15);
-            const bool ook = o < a.H;  // H % 4 == 0: the group is whole or out
-            const uint32_t oc = ook ? o : 0;
+            // the four tiles of a wave are the hc streams of the same outputs
+            const uint32_t o4 = bx * 64 + wn * 16 + kq * 4;
+            const bool ook = o4 < a.H;  // H % 4 == 0
+            const uint32_t oc = ook ? o4 : 0;
             float nw[4][4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -667,134 +657,260 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
                 nw[j][3] = __uint_as_float(q.y & 0xffff0000u);
             }
 #pragma unroll
-            for (int k = 0; k < 2; ++k) {
-                const uint32_t rr = r0 + 16 * k, m = mh + rr, mc = min(m, M - 1);
-                const float* hy = a.hyper + (size_t)mc * a.hc * a.H + oc;
-                float4 hv[4], uv[4];
+            for (int i = 0; i < NI; ++i) {
+                const uint32_t m = min(m0 + i * 16 + col, M - 1);
+                const float* hy = a.hyper + (size_t)m * a.hc * a.H + oc;
+                float4 hv[4];
                 float iv[4];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const bool on = (uint32_t)j < a.hc;
                     hv[j] = on ? *reinterpret_cast<const float4*>(hy + (size_t)j * a.H) : make_float4(0.f, 0.f, 0.f, 0.f);
-                    iv[j] = on ? a.inv[(size_t)mc * a.hc + j] : 0.0f;
-                    uv[j] = *reinterpret_cast<const float4*>(&sO[rr * OS + sc0 + j * 16]);
+                    iv[j] = on ? a.inv[(size_t)m * a.hc + j] : 0.0f;
                 }
-                if (m >= M || !ook) continue;
+                if (!mok[i] || !ook) continue;
                 float sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     if ((uint32_t)j >= a.hc) continue;
                     const float hj[4] = {hv[j].x, hv[j].y, hv[j].z, hv[j].w};
-                    const float uj[4] = {uv[j].x, uv[j].y, uv[j].z, uv[j].w};
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) sum[e] += sigmoidf_(uj[e]) * (hj[e] * iv[j] * nw[j][e]);
+                    for (int r = 0; r < 4; ++r) sum[r] += sigmoidf_(acc[0][i][j][r]) * (hj[r] * iv[j] * nw[j][r]);
                 }
                 const float ih = (float)a.hc;
-                *reinterpret_cast<float4*>(a.out + (size_t)m * a.H + o) =
+                *reinterpret_cast<float4*>(a.out + (size_t)m * a.H + o4) =
                     make_float4(sum[0] / ih, sum[1] / ih, sum[2] / ih, sum[3] / ih);
             }
-        } else if (a.vec4) {
-            // thread: columns 4 c4 .. + 3, rows r0 + RPP k (16-byte
-            // aligned rows and segments, N % 4 == 0: checked at launch)
-            constexpr uint32_t G4 = NC / 4, RPP = 256 / G4, KB = 32 / RPP;
-            const uint32_t c4 = (uint32_t)tid % G4, r0 = (uint32_t)tid / G4;
-            const uint32_t n4 = bx * NC + 4 * c4;
-            const bool nok = n4 < a.N;
-            PfSeg s4 = a.seg[0];
-            if (EPI == PE_STORE) {
+        } else {
+            uint32_t n4[NJ];
+            PfSeg sj[NJ];
 #pragma unroll
-                for (int sgi = 1; sgi < 4; ++sgi)
-                    if ((uint32_t)sgi < a.nseg && n4 >= a.seg[sgi].n0) s4 = a.seg[sgi];
+            for (int j = 0; j < NJ; ++j) {
+                n4[j] = bx * NC + wn * (64 / NMAT) + j * 16 + kq * 4;
+                sj[j] = a.seg[0];
+                if (EPI == PE_STORE) {
+#pragma unroll
+                    for (int sgi = 1; sgi < 4; ++sgi)
+                        if ((uint32_t)sgi < a.nseg && n4[j] >= a.seg[sgi].n0) sj[j] = a.seg[sgi];
+                }
             }
-            if (EPI == PE_INJECT) {
-                float4 v[KB];
 #pragma unroll
-                for (int k = 0; k < (int)KB; ++k) v[k] = *reinterpret_cast<const float4*>(&sO[(r0 + RPP * k) * OS + 4 * c4]);
-                const uint32_t nc = nok ? n4 : 0;
+            for (int i = 0; i < NI; ++i) {
+                const uint32_t m = m0 + i * 16 + col;
+                if (EPI == PE_INJECT) {
+                    const uint32_t mc = min(m, M - 1);
+                    float4 hv[NJ][4];
 #pragma unroll
-                for (int k = 0; k < (int)KB; ++k) {
-                    const uint32_t m = mh + r0 + RPP * k, mc = min(m, M - 1);
-                    float* hy = a.hyper + (size_t)mc * a.hc * a.H + nc;
-                    float4 hv[4];
+                    for (int j = 0; j < NJ; ++j) {
+                        const float* hy = a.hyper + (size_t)mc * a.hc * a.H + min(n4[j], a.N - 4);
 #pragma unroll
-                    for (int g = 0; g < 4; ++g)
-                        hv[g] = (uint32_t)g < a.hc ? *reinterpret_cast<const float4*>(hy + (size_t)g * a.H)
-                                                   : make_float4(0.f, 0.f, 0.f, 0.f);
-                    if (m >= M || !nok) continue;
+                        for (int g = 0; g < 4; ++g)
+                            hv[j][g] = (uint32_t)g < a.hc ? *reinterpret_cast<const float4*>(hy + (size_t)g * a.H)
+                                                          : make_float4(0.f, 0.f, 0.f, 0.f);
+                    }
+                    if (!mok[i]) continue;
 #pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        if ((uint32_t)g >= a.hc) continue;
-                        const float ij = a.inj[(size_t)m * a.hc + g];
-                        *reinterpret_cast<float4*>(hy + (size_t)g * a.H) =
-                            make_float4(hv[g].x + v[k].x * ij, hv[g].y + v[k].y * ij, hv[g].z + v[k].z * ij,
-                                        hv[g].w + v[k].w * ij);
+                    for (int j = 0; j < NJ; ++j) {
+                        if (n4[j] >= a.N) continue;
+                        float* hy = a.hyper + (size_t)m * a.hc * a.H + n4[j];
+                        const f4 v = acc[0][i][j];
+#pragma unroll
+                        for (int g = 0; g < 4; ++g) {
+                            if ((uint32_t)g >= a.hc) continue;
+                            const float ij = a.inj[(size_t)m * a.hc + g];
+                            *reinterpret_cast<float4*>(hy + (size_t)g * a.H) =
+                                make_float4(hv[j][g].x + v[0] * ij, hv[j][g].y + v[1] * ij, hv[j][g].z + v[2] * ij,
+                                            hv[j][g].w + v[3] * ij);
+                        }
+                    }
+                    continue;
+                }
+                if (!mok[i]) continue;
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    float u[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        u[r] = EPI == PE_SILU_MUL ? siluf_(acc[0][i][j][r]) * acc[NMAT - 1][i][j][r] : acc[0][i][j][r];
+                    float* dst = sj[j].y + (size_t)blockIdx.z * a.zstride + (size_t)yrow[i] * sj[j].ldy + (n4[j] - sj[j].n0);
+                    if (a.vec4) {
+                        if (n4[j] < a.N) *reinterpret_cast<float4*>(dst) = make_float4(u[0], u[1], u[2], u[3]);
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            if (n4[j] + r < a.N) dst[r] = u[r];
+                    }
+                }
+            }
+        }
+    } else {
+    // ---- epilogue: the tile leaves through LDS (the A staging buffers) in
+        // two 32-row halves.  Each lane parks its accumulators (one value per
+        // output: silu(gate) * up already formed for PE_SILU_MUL), then thread
+        // t finishes column t (PE_HC_UP: output t % 64 of row t / 64 + 4 k), so
+        // the per-output code is one loop body rather than one unrolled copy
+        // per accumulator, and a wave's stores cover consecutive outputs.
+        float* sO = reinterpret_cast<float*>(&sA[0][0][0]);
+        constexpr uint32_t OS = 260;  // floats per staged row (256 + pad: the four kq rows of a write hit distinct banks)
+        static_assert(32 * OS * sizeof(float) <= sizeof(sA), "a staged half fits the A buffers");
+        constexpr uint32_t NC = 256 / NMAT;  // staged columns
+        const uint32_t gcol = bx * NC + (uint32_t)tid % NC;  // PE_STORE / PE_SILU_MUL / PE_INJECT output column
+        PfSeg sg = a.seg[0];
+        if (EPI == PE_STORE) {
+    #pragma unroll
+            for (int sgi = 1; sgi < 4; ++sgi)
+                if ((uint32_t)sgi < a.nseg && gcol >= a.seg[sgi].n0) sg = a.seg[sgi];
+        }
+    #pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            __syncthreads();
+    #pragma unroll
+            for (int ii = 0; ii < 2; ++ii) {
+                const int i = 2 * h + ii;
+    #pragma unroll
+                for (int j = 0; j < NJ; ++j)
+    #pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float v = EPI == PE_SILU_MUL ? siluf_(acc[0][i][j][r]) * acc[NMAT - 1][i][j][r] : acc[0][i][j][r];
+                        sO[(ii * 16 + kq * 4 + r) * OS + wn * (64 / NMAT) + j * 16 + col] = v;
+                    }
+            }
+            __syncthreads();
+            const uint32_t mh = m0 + 32 * h;
+            if (EPI == PE_HC_UP) {
+                // thread: outputs 4 c4 .. + 3 of the 64, rows r0 + 16 k
+                const uint32_t c4 = (uint32_t)tid & 15, r0 = (uint32_t)tid >> 4, ol = 4 * c4;
+                const uint32_t o = bx * 64 + ol, sc0 = (ol >> 4) * 64 + (ol & 15);
+                const bool ook = o < a.H;  // H % 4 == 0: the group is whole or out
+                const uint32_t oc = ook ? o : 0;
+                float nw[4][4];
+    #pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint2 q = (uint32_t)j < a.hc ? *reinterpret_cast<const uint2*>(a.norm + (size_t)j * a.H + oc)
+                                                       : uint2{0u, 0u};
+                    nw[j][0] = __uint_as_float(q.x << 16);
+                    nw[j][1] = __uint_as_float(q.x & 0xffff0000u);
+                    nw[j][2] = __uint_as_float(q.y << 16);
+                    nw[j][3] = __uint_as_float(q.y & 0xffff0000u);
+                }
+    #pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    const uint32_t rr = r0 + 16 * k, m = mh + rr, mc = min(m, M - 1);
+                    const float* hy = a.hyper + (size_t)mc * a.hc * a.H + oc;
+                    float4 hv[4], uv[4];
+                    float iv[4];
+    #pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const bool on = (uint32_t)j < a.hc;
+                        hv[j] = on ? *reinterpret_cast<const float4*>(hy + (size_t)j * a.H) : make_float4(0.f, 0.f, 0.f, 0.f);
+                        iv[j] = on ? a.inv[(size_t)mc * a.hc + j] : 0.0f;
+                        uv[j] = *reinterpret_cast<const float4*>(&sO[rr * OS + sc0 + j * 16]);
+                    }
+                    if (m >= M || !ook) continue;
+                    float sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    #pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        if ((uint32_t)j >= a.hc) continue;
+                        const float hj[4] = {hv[j].x, hv[j].y, hv[j].z, hv[j].w};
+                        const float uj[4] = {uv[j].x, uv[j].y, uv[j].z, uv[j].w};
+    #pragma unroll
+                        for (int e = 0; e < 4; ++e) sum[e] += sigmoidf_(uj[e]) * (hj[e] * iv[j] * nw[j][e]);
+                    }
+                    const float ih = (float)a.hc;
+                    *reinterpret_cast<float4*>(a.out + (size_t)m * a.H + o) =
+                        make_float4(sum[0] / ih, sum[1] / ih, sum[2] / ih, sum[3] / ih);
+                }
+            } else if (a.vec4) {
+                // thread: columns 4 c4 .. + 3, rows r0 + RPP k (16-byte
+                // aligned rows and segments, N % 4 == 0: checked at launch)
+                constexpr uint32_t G4 = NC / 4, RPP = 256 / G4, KB = 32 / RPP;
+                const uint32_t c4 = (uint32_t)tid % G4, r0 = (uint32_t)tid / G4;
+                const uint32_t n4 = bx * NC + 4 * c4;
+                const bool nok = n4 < a.N;
+                PfSeg s4 = a.seg[0];
+                if (EPI == PE_STORE) {
+    #pragma unroll
+                    for (int sgi = 1; sgi < 4; ++sgi)
+                        if ((uint32_t)sgi < a.nseg && n4 >= a.seg[sgi].n0) s4 = a.seg[sgi];
+                }
+                if (EPI == PE_INJECT) {
+                    float4 v[KB];
+    #pragma unroll
+                    for (int k = 0; k < (int)KB; ++k) v[k] = *reinterpret_cast<const float4*>(&sO[(r0 + RPP * k) * OS + 4 * c4]);
+                    const uint32_t nc = nok ? n4 : 0;
+    #pragma unroll
+                    for (int k = 0; k < (int)KB; ++k) {
+                        const uint32_t m = mh + r0 + RPP * k, mc = min(m, M - 1);
+                        float* hy = a.hyper + (size_t)mc * a.hc * a.H + nc;
+                        float4 hv[4];
+    #pragma unroll
+                        for (int g = 0; g < 4; ++g)
+                            hv[g] = (uint32_t)g < a.hc ? *reinterpret_cast<const float4*>(hy + (size_t)g * a.H)
+                                                       : make_float4(0.f, 0.f, 0.f, 0.f);
+                        if (m >= M || !nok) continue;
+    #pragma unroll
+                        for (int g = 0; g < 4; ++g) {
+                            if ((uint32_t)g >= a.hc) continue;
+                            const float ij = a.inj[(size_t)m * a.hc + g];
+                            *reinterpret_cast<float4*>(hy + (size_t)g * a.H) =
+                                make_float4(hv[g].x + v[k].x * ij, hv[g].y + v[k].y * ij, hv[g].z + v[k].z * ij,
+                                            hv[g].w + v[k].w * ij);
+                        }
+                    }
+                } else {
+                    // one row per iteration, the next row's LDS read issued
+                    // before this row's activation and store
+                    float4 vn = *reinterpret_cast<const float4*>(&sO[r0 * OS + 4 * c4]);
+                    uint32_t yn = sRow[32 * h + r0];
+    #pragma unroll 1
+                    for (uint32_t k = 0; k < KB; ++k) {
+                        const uint32_t rr = r0 + RPP * k, m = mh + rr;
+                        const float4 v = vn;
+                        const uint32_t yr = yn;
+                        if (k + 1 < KB) {
+                            vn = *reinterpret_cast<const float4*>(&sO[(rr + RPP) * OS + 4 * c4]);
+                            yn = sRow[32 * h + rr + RPP];
+                        }
+                        if (m >= M) break;
+                        if (!nok) continue;
+                        float u[4] = {v.x, v.y, v.z, v.w};
+                        float* dst;
+                        if (EPI == PE_SILU_MUL) {
+                            dst = a.seg[0].y + (size_t)yr * a.seg[0].ldy + n4;
+                        } else {
+                            dst = s4.y + (size_t)blockIdx.z * a.zstride + (size_t)yr * s4.ldy + (n4 - s4.n0);
+                        }
+                        *reinterpret_cast<float4*>(dst) = make_float4(u[0], u[1], u[2], u[3]);
                     }
                 }
             } else {
-                // one row per iteration, the next row's LDS read issued
-                // before this row's activation and store
-                float4 vn = *reinterpret_cast<const float4*>(&sO[r0 * OS + 4 * c4]);
-                uint32_t yn = sRow[1][32 * h + r0];
-#pragma unroll 1
-                for (uint32_t k = 0; k < KB; ++k) {
-                    const uint32_t rr = r0 + RPP * k, m = mh + rr;
-                    const float4 v = vn;
-                    const uint32_t yr = yn;
-                    if (k + 1 < KB) {
-                        vn = *reinterpret_cast<const float4*>(&sO[(rr + RPP) * OS + 4 * c4]);
-                        yn = sRow[1][32 * h + rr + RPP];
+                // unaligned outputs (PE_STORE, PE_SILU_MUL): thread t takes
+                // column t % NC, rows in batches of 8 whose reads are all
+                // issued before the first store
+                constexpr uint32_t RPP = 256 / NC;  // rows per pass
+                constexpr int B = 8;
+                const uint32_t lc = (uint32_t)tid % NC, r0 = (uint32_t)tid / NC;
+                const bool nok = gcol < a.N;
+    #pragma unroll 1
+                for (uint32_t rb = 0; rb < 32; rb += B * RPP) {
+                    float v[B];
+                    uint32_t yr[B];
+    #pragma unroll
+                    for (int k = 0; k < B; ++k) {
+                        const uint32_t rr = rb + r0 + k * RPP;
+                        v[k] = sO[rr * OS + lc];
+                        yr[k] = sRow[32 * h + rr];
                     }
-                    if (m >= M) break;
-                    if (!nok) continue;
-                    float u[4] = {v.x, v.y, v.z, v.w};
-                    float* dst;
-                    if (EPI == PE_SILU_MUL) {
-                        dst = a.seg[0].y + (size_t)yr * a.seg[0].ldy + n4;
-                    } else {
-                        if (s4.act != PA_NONE) {
-                            // silu(x) = x / (1 + e^-x), 2 sigmoid(x) = 2 / (1 + e^-x)
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) {
-                                const float x = u[e] * a.alpha;
-                                u[e] = (s4.act == PA_SILU ? x : 2.0f) / (1.0f + expf(-x));
-                            }
+    #pragma unroll
+                    for (int k = 0; k < B; ++k) {
+                        const uint32_t m = mh + rb + r0 + k * RPP;
+                        if (m >= M || !nok) continue;
+                        if (EPI == PE_SILU_MUL) {
+                            a.seg[0].y[(size_t)yr[k] * a.seg[0].ldy + gcol] = v[k];
+                        } else if (EPI == PE_STORE) {
+                            const float u = v[k];
+                            sg.y[(size_t)blockIdx.z * a.zstride + (size_t)yr[k] * sg.ldy + (gcol - sg.n0)] = u;
                         }
-                        dst = s4.y + (size_t)blockIdx.z * a.zstride + (size_t)yr * s4.ldy + (n4 - s4.n0);
-                    }
-                    *reinterpret_cast<float4*>(dst) = make_float4(u[0], u[1], u[2], u[3]);
-                }
-            }
-        } else {
-            // unaligned outputs (PE_STORE, PE_SILU_MUL): thread t takes
-            // column t % NC, rows in batches of 8 whose reads are all
-            // issued before the first store
-            constexpr uint32_t RPP = 256 / NC;  // rows per pass
-            constexpr int B = 8;
-            const uint32_t lc = (uint32_t)tid % NC, r0 = (uint32_t)tid / NC;
-            const bool nok = gcol < a.N;
-#pragma unroll 1
-            for (uint32_t rb = 0; rb < 32; rb += B * RPP) {
-                float v[B];
-                uint32_t yr[B];
-#pragma unroll
-                for (int k = 0; k < B; ++k) {
-                    const uint32_t rr = rb + r0 + k * RPP;
-                    v[k] = sO[rr * OS + lc];
-                    yr[k] = sRow[1][32 * h + rr];
-                }
-#pragma unroll
-                for (int k = 0; k < B; ++k) {
-                    const uint32_t m = mh + rb + r0 + k * RPP;
-                    if (m >= M || !nok) continue;
-                    if (EPI == PE_SILU_MUL) {
-                        a.seg[0].y[(size_t)yr[k] * a.seg[0].ldy + gcol] = v[k];
-                    } else if (EPI == PE_STORE) {
-                        float u = v[k];
-                        if (sg.act != PA_NONE) {
-                            const float x = u * a.alpha;
-                            u = (sg.act == PA_SILU ? x : 2.0f) / (1.0f + expf(-x));
-                        }
-                        sg.y[(size_t)blockIdx.z * a.zstride + (size_t)yr[k] * sg.ldy + (gcol - sg.n0)] = u;
                     }
                 }
             }
@@ -937,10 +1053,13 @@ __global__ void __launch_bounds__(256) k_pf_route(const float* __restrict__ logi
 // Entries grouped by expert (the CSR lists of gpu/prefill/experts.rs:29-137):
 // list[e][0..count[e]) holds the entries t (k+1) + slot routed to e (any
 // order: every GEMM row is independent), list[E] every token's shared
-// slot t (k+1) + k, and tiles[] the (group, 64-row tile) pairs, *ntiles of
+// slot t (k+1) + k, and tiles[] the (group, tr-row tile) pairs, *ntiles of
 // them: first every group of two or more tiles, its count rounded up to
 // even (the extra tile has no rows), so each starts at an even position
 // (the GEMMs run tiles 2c and 2c + 1 on one XCD), then the one-tile groups.
+// A second such list of 64-row tiles follows at tiles + pf_tile_bound(T,
+// topk, E, tr), ntiles[1] of them (the gate/up and down GEMMs tile the same
+// entries differently).
 // With `act`, also the expert activity counters of `layer` (selected rows
 // and selections, as k_expert_activity counts them).  One workgroup.
 constexpr uint32_t PG_WG = 1024;  // threads of the grouping workgroup (one group each)
@@ -949,7 +1068,8 @@ __global__ void __launch_bounds__(PG_WG) k_pf_group(const uint32_t* __restrict__
                                                     uint32_t E, uint32_t cap, uint32_t* __restrict__ list,
                                                     uint32_t* __restrict__ count, uint32_t* __restrict__ tiles,
                                                     uint32_t* __restrict__ ntiles,
-                                                    unsigned long long* __restrict__ act, uint32_t layer) {
+                                                    unsigned long long* __restrict__ act, uint32_t layer,
+                                                    uint32_t tr) {
     __shared__ uint32_t cnt[PG_WG];
     __shared__ uint32_t wsum[PG_WG / 64];
     const uint32_t tau = threadIdx.x, lane = tau & 63, wv = tau >> 6;
@@ -969,28 +1089,38 @@ __global__ void __launch_bounds__(PG_WG) k_pf_group(const uint32_t* __restrict__
     // tiles per group (thread e takes group e): multi-tile counts in the
     // high half-word, single tiles in the low one, one workgroup prefix sum
     const uint32_t e = tau;
-    const uint32_t nt0 = e <= E ? (cnt[e] + 63) / 64 : 0;
-    const uint32_t nt = nt0 > 1 ? (nt0 + 1) & ~1u : nt0;
     if (e <= E) count[e] = cnt[e];
     if (act && e < E && cnt[e]) {
         unsigned long long* ae = act + ((size_t)layer * E + e) * 2;
         ae[0] += cnt[e];
         ae[1] += 1;
     }
-    const uint32_t packed = nt > 1 ? nt << 16 : nt;
-    uint32_t incl = packed;
-    for (int d = 1; d < 64; d <<= 1) {
-        const uint32_t o = __shfl_up(incl, d, 64);
-        if ((int)lane >= d) incl += o;
+    // one tile list per tile height: tr-row tiles at tiles, 64-row tiles
+    // at tiles + pf_tile_bound(T, topk, E, tr) (*ntiles, ntiles[1] of them)
+    const uint32_t trs[2] = {tr, 64u};
+    uint32_t* dst = tiles;
+    for (int h = 0; h < 2; ++h) {
+        const uint32_t nt0 = e <= E ? (cnt[e] + trs[h] - 1) / trs[h] : 0;
+        const uint32_t nt = nt0 > 1 ? (nt0 + 1) & ~1u : nt0;
+        const uint32_t packed = nt > 1 ? nt << 16 : nt;
+        uint32_t incl = packed;
+        for (int d = 1; d < 64; d <<= 1) {
+            const uint32_t o = __shfl_up(incl, d, 64);
+            if ((int)lane >= d) incl += o;
+        }
+        __syncthreads();  // the previous list's wsum reads are done
+        if (lane == 63) wsum[wv] = incl;
+        __syncthreads();
+        uint32_t off = incl - packed, all = 0;
+        for (uint32_t k = 0; k < wv; ++k) off += wsum[k];
+        for (uint32_t k = 0; k < PG_WG / 64; ++k) all += wsum[k];
+        const uint32_t start = nt > 1 ? off >> 16 : (all >> 16) + (off & 0xffffu);
+        for (uint32_t q = 0; q < nt; ++q) dst[start + q] = e << 16 | q;
+        if (tau == PG_WG - 1) ntiles[h] = (all >> 16) + (all & 0xffffu);
+        // bound of the first list, as pf_tile_bound computes it
+        const uint32_t n = (T * topk + tr - 1) / tr + E + (T + tr - 1) / tr + 1 + (E + 1);
+        dst = tiles + ((n + 15) & ~15u);
     }
-    if (lane == 63) wsum[wv] = incl;
-    __syncthreads();
-    uint32_t off = incl - packed, all = 0;
-    for (uint32_t k = 0; k < wv; ++k) off += wsum[k];
-    for (uint32_t k = 0; k < PG_WG / 64; ++k) all += wsum[k];
-    const uint32_t start = nt > 1 ? off >> 16 : (all >> 16) + (off & 0xffffu);
-    for (uint32_t q = 0; q < nt; ++q) tiles[start + q] = e << 16 | q;
-    if (tau == PG_WG - 1) *ntiles = (all >> 16) + (all & 0xffffu);
 }
 
 // out[t][n] = sum_r w[t][r] yd[t][r][n] + sigmoid(sg[t]) yd[t][k][n]
@@ -1231,11 +1361,11 @@ void launch_pf_hc_prep(const float* hyper, const uint16_t* norm, uint32_t H, uin
     if (T) k_pf_hc_prep<<<T, CHK_WG, 0, st>>>(hyper, norm, H, hc, eps, inv, hi, lo, xs);
 }
 
-void launch_pf_gemm_args(const PfGemmArgs& args, int epi, uint32_t grid_y, hipStream_t st) {
-    if (args.K % 64 || !args.K) throw std::runtime_error("prefill GEMM needs K a multiple of 64");
-    if (!grid_y) return;
-    // 32-bit element offsets of the dense matrices from the lowest base
-    PfGemmArgs a = args;
+// The launch form of a GEMM: 32-bit element offsets of the dense matrices
+// from their lowest base, and whether its scales can be staged (whole
+// blocks of 8 groups on 16-byte aligned rows), the form every tile height
+// under 64 rows needs.
+static bool pf_gemm_prepare(PfGemmArgs& a, int epi) {
     const int nm = std::max<int>(a.nseg, epi == PE_SILU_MUL ? 2 : 1);
     uintptr_t wmin = UINTPTR_MAX, smin = UINTPTR_MAX;
     for (int q = 0; q < nm; ++q) {
@@ -1255,15 +1385,29 @@ void launch_pf_gemm_args(const PfGemmArgs& args, int epi, uint32_t grid_y, hipSt
         a.seg[q].bo = (uint32_t)b;
     }
     const uint32_t ksplit = std::max<uint32_t>(1, a.ksplit);
-    if ((a.K / 64) % ksplit || (ksplit > 1 && epi != PE_STORE))
-        throw std::runtime_error("split K needs whole groups per chunk and a plain store");
-    // staged scales need whole blocks of 8 groups on 16-byte aligned rows
     bool sbl = (a.K / 64 / ksplit) % 8 == 0 && smin % 16 == 0;
     for (int q = 0; q < nm; ++q) sbl = sbl && a.seg[q].so % 8 == 0 && a.seg[q].bo % 8 == 0;
     if (a.X.base)
-        sbl = sbl && (uintptr_t)a.X.base % 16 == 0 && a.X.stride % 16 == 0 && a.X.gate_s % 16 == 0 &&
-              a.X.gate_b % 16 == 0 && a.X.up_s % 16 == 0 && a.X.up_b % 16 == 0 && a.X.down_s % 16 == 0 &&
-              a.X.down_b % 16 == 0;
+        sbl = sbl && a.X.bits == 4 && (uintptr_t)a.X.base % 16 == 0 && a.X.stride % 16 == 0 &&
+              a.X.gate_s % 16 == 0 && a.X.gate_b % 16 == 0 && a.X.up_s % 16 == 0 && a.X.up_b % 16 == 0 &&
+              a.X.down_s % 16 == 0 && a.X.down_b % 16 == 0;
+    return sbl;
+}
+
+bool pf_gemm_staged(const PfGemmArgs& args, int epi) {
+    if (args.K % 64 || !args.K) return false;
+    PfGemmArgs a = args;
+    return pf_gemm_prepare(a, epi);
+}
+
+void launch_pf_gemm_args(const PfGemmArgs& args, int epi, uint32_t grid_y, hipStream_t st) {
+    if (args.K % 64 || !args.K) throw std::runtime_error("prefill GEMM needs K a multiple of 64");
+    if (!grid_y) return;
+    PfGemmArgs a = args;
+    const bool sbl = pf_gemm_prepare(a, epi);
+    const uint32_t ksplit = std::max<uint32_t>(1, a.ksplit);
+    if ((a.K / 64) % ksplit || (ksplit > 1 && epi != PE_STORE))
+        throw std::runtime_error("split K needs whole groups per chunk and a plain store");
     if (epi == PE_HC_UP && a.hc > 4) throw std::runtime_error("prefill mix needs hc <= 4");
     // 16-byte output stores: N, every output row and every segment start on
     // a 4-float boundary.  The hc-stream epilogues (inject, mix) have only
@@ -1283,6 +1427,16 @@ void launch_pf_gemm_args(const PfGemmArgs& args, int epi, uint32_t grid_y, hipSt
         else k_pf_gemm<NM, E, false><<<dim3(GX, grid_y, ksplit), PF_WG, 0, st>>>(a);    \
     } while (0)
     const uint32_t xbits = a.X.base ? a.X.bits : 4;
+    const uint32_t tr = a.tile_rows ? a.tile_rows : 64;
+    if (tr != 64) {
+        // 48-row tiles (grouped experts: ~40 rows each)
+        if (!sbl || xbits != 4) throw std::runtime_error("prefill GEMM tiles under 64 rows need staged scales over Q4 rows");
+        const uint32_t gx = epi == PE_SILU_MUL ? (a.N + 127) / 128 : (a.N + 255) / 256;
+        const dim3 grid(gx, grid_y, ksplit);
+        if (tr == 48 && epi == PE_SILU_MUL) k_pf_gemm<2, PE_SILU_MUL, true, 4, 3><<<grid, PF_WG, 0, st>>>(a);
+        else throw std::runtime_error("prefill GEMM: no such tile height for this epilogue");
+        return;
+    }
     if (xbits != 4) {
         // grouped expert GEMMs over Q3 / Q2 records (scales folded per lane)
         if (epi != PE_STORE && epi != PE_SILU_MUL) throw std::runtime_error("low-bit records: gate/up and down only");
@@ -1307,7 +1461,7 @@ void launch_pf_gemm_args(const PfGemmArgs& args, int epi, uint32_t grid_y, hipSt
 void launch_pf_gemm(const Q4Mat& w, const uint4* xhi, const uint4* xlo, const float* xs, float* y, uint32_t T,
                     uint32_t ldy, hipStream_t st) {
     PfGemmArgs a{};
-    a.seg[0] = PfSeg{w, y, ldy, 0, PA_NONE};
+    a.seg[0] = PfSeg{w, y, ldy, 0};
     a.nseg = 1;
     a.N = w.out;
     a.K = w.in;
@@ -1338,18 +1492,20 @@ void launch_pf_route(const float* logits, uint32_t T, uint32_t E, uint32_t topk,
 }
 
 void launch_pf_group(const uint32_t* ids, uint32_t T, uint32_t topk, uint32_t E, uint32_t cap, uint32_t* list,
-                     uint32_t* count, uint32_t* tiles, uint32_t* ntiles, uint64_t* act, uint32_t layer,
+                     uint32_t* count, uint32_t* tiles, uint32_t* ntiles, uint64_t* act, uint32_t layer, uint32_t tr,
                      hipStream_t st) {
     if (E + 1 > PG_WG) throw std::runtime_error("prefill grouping supports at most 1023 experts");
-    if (pf_tile_bound(T, topk, E) >= 0x10000u) throw std::runtime_error("prefill grouping: too many tiles");
+    if (tr != 48 && tr != 64) throw std::runtime_error("prefill grouping: tiles of 48 or 64 rows");
+    if (pf_tile_bound(T, topk, E, tr) >= 0x10000u || pf_tile_bound(T, topk, E, 64) >= 0x10000u)
+        throw std::runtime_error("prefill grouping: too many tiles");
     k_pf_group<<<1, PG_WG, 0, st>>>(ids, T, topk, E, cap, list, count, tiles, ntiles,
-                                    reinterpret_cast<unsigned long long*>(act), layer);
+                                    reinterpret_cast<unsigned long long*>(act), layer, tr);
 }
 
-// Tiles of a grouped GEMM: every group's rows in 64-row tiles, one more
+// Tiles of a grouped GEMM: every group's rows in tr-row tiles, one more
 // per group for the even rounding, the grid rounded up to 16 tiles.
-uint32_t pf_tile_bound(uint32_t T, uint32_t topk, uint32_t E) {
-    const uint32_t n = (T * topk + 63) / 64 + E + (T + 63) / 64 + 1 + (E + 1);
+uint32_t pf_tile_bound(uint32_t T, uint32_t topk, uint32_t E, uint32_t tr) {
+    const uint32_t n = (T * topk + tr - 1) / tr + E + (T + tr - 1) / tr + 1 + (E + 1);
     return (n + 15) & ~15u;
 }
 
