@@ -89,17 +89,30 @@ __global__ void __launch_bounds__(PB_WG) k_pb_persistent(PbArgs a) {
     __syncthreads();
     uint32_t bad = 0, x = 0;
     uint4 wr[PB_WORDS];
-    const uint32_t words = a.words < PB_WORDS ? a.words : PB_WORDS;
+    const uint32_t words = a.words, w0 = words < PB_WORDS ? words : PB_WORDS;
+    // the first round of phase p: words 0 .. w0 of this workgroup's slice
     auto issue = [&](uint32_t p) {
         const uint4* src = a.w + ((size_t)(p % a.nrot) * nwg + wg) * PB_WG * words + t;
 #pragma unroll
         for (int i = 0; i < PB_WORDS; ++i)
-            if ((uint32_t)i < words) wr[i] = src[(size_t)i * PB_WG];
+            if ((uint32_t)i < w0) wr[i] = src[(size_t)i * PB_WG];
     };
     auto consume = [&]() {
 #pragma unroll
         for (int i = 0; i < PB_WORDS; ++i)
-            if ((uint32_t)i < words) x ^= wr[i].x + wr[i].y + wr[i].z + wr[i].w;
+            if ((uint32_t)i < w0) x ^= wr[i].x + wr[i].y + wr[i].z + wr[i].w;
+    };
+    // the rest of phase p's slice, round by round
+    auto rest = [&](uint32_t p) {
+        const uint4* src = a.w + ((size_t)(p % a.nrot) * nwg + wg) * PB_WG * words + t;
+        for (uint32_t r0 = PB_WORDS; r0 < words; r0 += PB_WORDS) {
+            uint4 v[PB_WORDS];
+#pragma unroll
+            for (int i = 0; i < PB_WORDS; ++i) v[i] = src[(size_t)min(r0 + i, words - 1) * PB_WG];
+#pragma unroll
+            for (int i = 0; i < PB_WORDS; ++i)
+                if (r0 + i < words) x ^= v[i].x + v[i].y + v[i].z + v[i].w;
+        }
     };
     if (a.prefetch) issue(0);
     for (uint32_t p = 0; p < a.phases; ++p) {
@@ -127,8 +140,11 @@ __global__ void __launch_bounds__(PB_WG) k_pb_persistent(PbArgs a) {
             const float v1 = ldf_sys(buf + o1 * 64 + lane), v2 = ldf_sys(buf + o2 * 64 + lane);
             bad += (v1 != (float)(p * 7 + o1)) + (v2 != (float)(p * 7 + o2));
         }
+        // the first round (issued before the wait under prefetch), then the
+        // rest of the slice
         if (!a.prefetch) issue(p);
         consume();
+        rest(p);
         if (a.prefetch && p + 1 < a.phases) issue(p + 1);
     }
     if (wave == 1 && bad) atomicAdd(a.err, bad);
@@ -230,7 +246,6 @@ extern "C" int chk_phase_bench(int mode, uint32_t wgs, uint32_t phases, uint64_t
         if (mode != 5 && (phases < 8 || phases > 20000)) throw std::runtime_error("8..=20000 phases");
         if (mode == 5 && (phases < 1 || phases > (1u << 24))) throw std::runtime_error("1..=2^24 addresses");
         uint32_t words = (uint32_t)std::max<uint64_t>(1, bytes_per_phase / ((uint64_t)wgs * PB_WG * 16));
-        if (mode >= 2 && mode <= 4) words = std::min<uint32_t>(words, PB_WORDS);
         // weights rotate over enough slices (>= 512 MB) that they come from
         // HBM, not from the memory-side cache
         const uint64_t slice = (uint64_t)wgs * PB_WG * words * 16;

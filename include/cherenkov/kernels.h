@@ -179,7 +179,8 @@ int chk_profile_graph(ChkEngine* e, int kind, uint32_t reps, double* ms_total, u
  *           system scope;
  *   mode 3  mode 2 + each phase streams its weights after the barrier;
  *   mode 4  mode 2 + the next phase's weights issued before the wait;
- *           (modes 3-4 hold at most 16 uint4 = 256 B per thread per phase)
+ *           (modes 3-4 stream a phase's slice in rounds of 16 uint4 per
+ *           thread; under mode 4 only the first round precedes the wait)
  *   mode 5  float atomicAdd without return: wgs workgroups x
  *           bytes_per_phase / 4 adds over a window of `phases` addresses;
  *           us_per_phase = microseconds per launch.
