@@ -2,6 +2,7 @@
 
     python3 -m cherenkov_amd.rocprof_summary steps <kernel_trace.csv> [first last]
     python3 -m cherenkov_amd.rocprof_summary pmc <counter_collection.csv> <kernel-name-prefix>
+    python3 -m cherenkov_amd.rocprof_summary mfma <counter_collection.csv> [rows] [name-prefixes]
 
 steps: splits the trace into decode steps (each from a `k_embed` to the
 following `k_argmax_final`) and prints kernels per step, kernel busy time
@@ -11,6 +12,15 @@ first..last (1-based, inclusive; negative counts from the end).
 
 pmc: the average of each counter over the dispatches of one kernel (e.g.
 FETCH_SIZE and WRITE_SIZE in KiB per dispatch).
+
+mfma: from a pass of SQ_VALU_MFMA_BUSY_CYCLES, GRBM_GUI_ACTIVE,
+SQ_INSTS_VALU_MFMA_MOPS_F16 and SQ_INSTS_VALU_MFMA_MOPS_BF16, per kernel
+and launch grid (the `rows` largest by total time, default 12, of the
+kernels whose names start with one of the comma-separated prefixes, if
+given): launches,
+average dispatch duration, MFMA busy = busy cycles / (GRBM_GUI_ACTIVE / 8
+XCDs x 1024 SIMDs) and MFMA TFLOP/s = (MOPS_F16 + MOPS_BF16) x 512 /
+duration.
 """
 
 from __future__ import annotations
@@ -80,6 +90,30 @@ def pmc(path: str, prefix: str) -> None:
         print(f"{prefix} {k}: dispatches {len(v)}, mean {statistics.mean(v):.1f}")
 
 
+def mfma(path: str, rows: int = 12, prefixes: str = "") -> None:
+    keep = tuple(x for x in prefixes.split(",") if x)
+    disp: dict[str, dict] = {}
+    for r in csv.DictReader(open(path)):
+        if keep and not _name(r).startswith(keep):
+            continue
+        d = disp.setdefault(r["Dispatch_Id"], {"name": _name(r), "grid": r["Grid_Size"], "c": {},
+                                               "us": (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3})
+        d["c"][r["Counter_Name"]] = float(r["Counter_Value"])
+    agg = collections.defaultdict(list)
+    for d in disp.values():
+        agg[(d["name"], d["grid"])].append(d)
+    print("| kernel | grid (threads) | launches | avg us | MFMA busy | MFMA TFLOP/s |")
+    print("|---|---:|---:|---:|---:|---:|")
+    for (name, grid), ds in sorted(agg.items(), key=lambda kv: -sum(d["us"] for d in kv[1]))[:rows]:
+        us = statistics.mean(d["us"] for d in ds)
+        busy = statistics.mean(d["c"].get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) /
+                               max(d["c"].get("GRBM_GUI_ACTIVE", 0.0) / 8 * 1024, 1.0) for d in ds)
+        ops = statistics.mean(d["c"].get("SQ_INSTS_VALU_MFMA_MOPS_F16", 0.0) +
+                              d["c"].get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0.0) for d in ds)
+        tf = ops * 512 / (us * 1e-6) / 1e12 if us > 0 else 0.0
+        print(f"| `{name}` | {grid} | {len(ds)} | {us:.1f} | {100 * busy:.0f}% | {tf:.0f} |")
+
+
 def main() -> None:
     if len(sys.argv) >= 5 and sys.argv[1] == "steps":
         steps(sys.argv[2], int(sys.argv[3]), int(sys.argv[4]))
@@ -87,6 +121,8 @@ def main() -> None:
         steps(sys.argv[2])
     elif len(sys.argv) >= 4 and sys.argv[1] == "pmc":
         pmc(sys.argv[2], sys.argv[3])
+    elif len(sys.argv) >= 3 and sys.argv[1] == "mfma":
+        mfma(sys.argv[2], int(sys.argv[3]) if len(sys.argv) >= 4 else 12, sys.argv[4] if len(sys.argv) >= 5 else "")
     else:
         print(__doc__)
         sys.exit(2)
