@@ -541,9 +541,14 @@ CHK_DEV void epi_prefetch(const SegArgs& a, const Seg& sg, uint32_t r, EpiIn& e)
 #pragma unroll
         for (uint32_t j = 0; j < 9; ++j)
             if (j < a.ck) e.cw[j] = a.conv_w[(size_t)r * a.ck + j];
+        // compiler-only, in each branch: without it the two branches' last
+        // load-and-store (cw[8] here, p1 below) are merged into one store
+        // through a pointer phi, which keeps EpiIn in scratch memory
+        asm volatile("" ::: "memory");
     } else if (sg.epi == EPI_DN_DECAY) {
         e.p0 = a.a_log[r];
         e.p1 = a.dt_bias[r];
+        asm volatile("" ::: "memory");
     }
     asm volatile("" ::: "memory");  // compiler-only: later loads stay behind these
     __builtin_amdgcn_sched_barrier(0);
@@ -1410,24 +1415,22 @@ void launch_qmv(const SegArgs& a, int nb, hipStream_t st) {
         return;
     }
     const size_t lds = xq_bytes(nb, in);
-#define QMV(C, R) CHK_NB_SWITCH(nb, (k_qmv<C, R, NB><<<grid_for((a.total + R - 1) / R), 256, lds, st>>>(a)))
+    // 1-2 rows take R rows per wave, 3-4 rows half that (only the row
+    // counts each shape serves are instantiated)
+#define QMV(C, R, NB) k_qmv<C, R, NB><<<grid_for((a.total + R - 1) / R), 256, lds, st>>>(a)
+#define QMV_LO(C, R) (nb == 1 ? (void)QMV(C, R, 1) : (void)QMV(C, R, 2))
+#define QMV_HI(C, R) (nb == 3 ? (void)QMV(C, R, 3) : (void)QMV(C, R, 4))
     if (nb <= 2) {
-        if (cpl <= 1) {
-            QMV(1, 4);
-        } else if (cpl == 2) {
-            QMV(2, 4);
-        } else {
-            QMV(4, 2);
-        }
+        if (cpl <= 1) QMV_LO(1, 4);
+        else if (cpl == 2) QMV_LO(2, 4);
+        else QMV_LO(4, 2);
     } else {
-        if (cpl <= 1) {
-            QMV(1, 2);
-        } else if (cpl == 2) {
-            QMV(2, 2);
-        } else {
-            QMV(4, 1);
-        }
+        if (cpl <= 1) QMV_HI(1, 2);
+        else if (cpl == 2) QMV_HI(2, 2);
+        else QMV_HI(4, 1);
     }
+#undef QMV_HI
+#undef QMV_LO
 #undef QMV
 }
 
