@@ -1125,19 +1125,57 @@ __global__ void __launch_bounds__(PG_WG) k_pf_group(const uint32_t* __restrict__
 
 // out[t][n] = sum_r w[t][r] yd[t][r][n] + sigmoid(sg[t]) yd[t][k][n]
 // (cpu.rs:527-540), then hyper[t][g H + n] += out inj[t][g].
+// K > 0: K routed slots known at compile time, a thread takes outputs
+// 4 n .. + 3 with every slot's values in flight before the first is summed;
+// K = 0: any topk, one output per thread.  Slots are summed in order either
+// way.
+template <int K>
 __global__ void __launch_bounds__(256) k_pf_moe_combine(const float* __restrict__ yd, const float* __restrict__ wts,
                                                         const float* __restrict__ sg, const float* __restrict__ inj,
                                                         float* __restrict__ hyper, uint32_t H, uint32_t topk,
                                                         uint32_t hc) {
-    const uint32_t t = blockIdx.y, n = blockIdx.x * CHK_WG + threadIdx.x;
-    if (n >= H) return;
-    const uint32_t slots = topk + 1;
-    const float* y = yd + (size_t)t * slots * H + n;
-    float out = 0.0f;
-    for (uint32_t r = 0; r < topk; ++r) out += wts[(size_t)t * topk + r] * y[(size_t)r * H];
-    out += sigmoidf_(sg[t]) * y[(size_t)topk * H];
-    float* hy = hyper + (size_t)t * hc * H + n;
-    for (uint32_t g = 0; g < hc; ++g) hy[(size_t)g * H] += out * inj[(size_t)t * hc + g];
+    const uint32_t t = blockIdx.y, slots = topk + 1;
+    if constexpr (K == 0) {
+        const uint32_t n = blockIdx.x * CHK_WG + threadIdx.x;
+        if (n >= H) return;
+        const float* y = yd + (size_t)t * slots * H + n;
+        float out = 0.0f;
+        for (uint32_t r = 0; r < topk; ++r) out += wts[(size_t)t * topk + r] * y[(size_t)r * H];
+        out += sigmoidf_(sg[t]) * y[(size_t)topk * H];
+        float* hy = hyper + (size_t)t * hc * H + n;
+        for (uint32_t g = 0; g < hc; ++g) hy[(size_t)g * H] += out * inj[(size_t)t * hc + g];
+    } else {
+        const uint32_t n = (blockIdx.x * CHK_WG + threadIdx.x) * 4;
+        if (n >= H) return;
+        const float* y = yd + (size_t)t * slots * H + n;
+        float4 v[K + 1];
+#pragma unroll
+        for (int r = 0; r <= K; ++r) v[r] = *reinterpret_cast<const float4*>(y + (size_t)r * H);
+        float out[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int r = 0; r < K; ++r) {
+            const float w = wts[(size_t)t * K + r];
+            out[0] += w * v[r].x;
+            out[1] += w * v[r].y;
+            out[2] += w * v[r].z;
+            out[3] += w * v[r].w;
+        }
+        const float sgv = sigmoidf_(sg[t]);
+        out[0] += sgv * v[K].x;
+        out[1] += sgv * v[K].y;
+        out[2] += sgv * v[K].z;
+        out[3] += sgv * v[K].w;
+        float* hy = hyper + (size_t)t * hc * H + n;
+        for (uint32_t g = 0; g < hc; ++g) {
+            float4 h = *reinterpret_cast<const float4*>(hy + (size_t)g * H);
+            const float ij = inj[(size_t)t * hc + g];
+            h.x += out[0] * ij;
+            h.y += out[1] * ij;
+            h.z += out[2] * ij;
+            h.w += out[3] * ij;
+            *reinterpret_cast<float4*>(hy + (size_t)g * H) = h;
+        }
+    }
 }
 
 // ------------------------------------------------------------- embed
@@ -1511,7 +1549,11 @@ uint32_t pf_tile_bound(uint32_t T, uint32_t topk, uint32_t E, uint32_t tr) {
 
 void launch_pf_moe_combine(const float* yd, const float* wts, const float* sg, const float* inj, float* hyper,
                            uint32_t T, uint32_t H, uint32_t topk, uint32_t hc, hipStream_t st) {
-    if (T) k_pf_moe_combine<<<dim3((H + 255) / 256, T), CHK_WG, 0, st>>>(yd, wts, sg, inj, hyper, H, topk, hc);
+    if (!T) return;
+    if (topk == 10 && H % 4 == 0)
+        k_pf_moe_combine<10><<<dim3((H / 4 + 255) / 256, T), CHK_WG, 0, st>>>(yd, wts, sg, inj, hyper, H, topk, hc);
+    else
+        k_pf_moe_combine<0><<<dim3((H + 255) / 256, T), CHK_WG, 0, st>>>(yd, wts, sg, inj, hyper, H, topk, hc);
 }
 
 void launch_pf_embed(const uint32_t* tokens, const Q4Mat& emb, float* hyper, uint32_t H, uint32_t hc, uint32_t T,
