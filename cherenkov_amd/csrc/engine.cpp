@@ -146,6 +146,11 @@ struct PfBufs {
     float* xs;
     float *inv, *d, *inj_a, *inj_m, *mixed, *hc_part;
     float *raw, *z, *a, *b, *conv, *decay, *beta, *y;
+    uint32_t ab_split = 1;  // K chunks of the a / b projections
+    // the block's out-projection, left as K-chunk partials (in yd) for the
+    // next hyper-connection read to inject
+    const float* pend = nullptr;
+    uint32_t pend_split = 0;
     float* dcw;  // chunked-scan workspace (null: sequential scan)
     float *q_raw, *k_raw, *v_raw, *idx_raw, *q_ready, *attn_out;
     float *logits, *sg, *wts;
@@ -1401,6 +1406,7 @@ struct ChkEngine {
     uint32_t pf_qsa_rows() const;
     void pf_alloc();
     void pf_hc_read(const HcDev& w, float* inj, uint32_t T, bool for_moe);
+    void pf_out_proj(const Q4Mat& m, uint32_t K, uint32_t T);
     void pf_deltanet(const LayerDev& L, uint32_t T);
     void pf_attention(const LayerDev& L, uint32_t T, uint32_t pos0, const KvDev* kvo = nullptr);
     void pf_mtp(const uint32_t* toks, uint32_t c0, uint32_t T, uint32_t pos0, bool last, uint32_t next_after);
@@ -1607,6 +1613,14 @@ void ChkEngine::prefill_rows(const uint32_t* toks, uint32_t n, uint32_t next_aft
     if (!has_mtp) *draft = 0xffffffffu;
 }
 
+// K chunks of the prefill's DeltaNet a / b projections: the most (4 or 2)
+// that keep whole 8-group scale blocks per chunk, else 1.
+static uint32_t pf_ab_split(uint32_t H) {
+    for (uint32_t ks : {4u, 2u})
+        if ((H / 64) % ks == 0 && (H / 64 / ks) % 8 == 0) return ks;
+    return 1;
+}
+
 // Scratch a prefill of `rows` rows per GEMM chunk allocates (pf_alloc's
 // buffers, plus the all-logits rows).
 uint64_t ChkEngine::prefill_scratch_bytes(uint64_t C, bool all_logits) const {
@@ -1616,7 +1630,7 @@ uint64_t ChkEngine::prefill_scratch_bytes(uint64_t C, bool all_logits) const {
     const uint64_t plane = std::max({C * D.hh, C * D.v_dim, C * D.nh * D.hd, C * slots * D.I, C * D.H});
     b += plane * 2 * 2 + plane / 64 * f + 3 * C * D.H * 2;
     b += C * (3ull * D.hc + D.lowrank + D.H + (uint64_t)D.hc * (D.lowrank + D.hc)) * f;
-    const uint64_t dn = C * (2ull * D.conv_dim + 2ull * D.v_dim + 4ull * D.nv);
+    const uint64_t dn = C * (2ull * D.conv_dim + 2ull * D.v_dim + (2ull * pf_ab_split(D.H) + 2) * D.nv);
     const uint64_t at = C * (2ull * D.nh * D.hd + 2ull * D.kv_row + D.idx_out + 2ull * D.nh * D.hd);
     b += std::max(dn, at) * f;
     b += C * (D.E + 1 + 2ull * D.topk) * f + (D.E + 1ull) * C * 4 + (D.E + 1) * 4;
@@ -1697,7 +1711,7 @@ void ChkEngine::pf_alloc() {
     pf.inj_m = pfalloc<float>(C * D.hc);
     pf.mixed = pfalloc<float>(C * D.H);
     // DeltaNet / attention arena
-    const uint64_t dn = C * (2ull * D.conv_dim + 2ull * D.v_dim + 4ull * D.nv);
+    const uint64_t dn = C * (2ull * D.conv_dim + 2ull * D.v_dim + (2ull * pf_ab_split(D.H) + 2) * D.nv);
     const uint64_t at = C * (2ull * D.nh * D.hd + 2ull * D.kv_row + D.idx_out + 2ull * D.nh * D.hd);
     float* arena = pfalloc<float>(std::max(dn, at));
     float* q = arena;
@@ -1705,8 +1719,10 @@ void ChkEngine::pf_alloc() {
     pf.conv = q; q += C * D.conv_dim;
     pf.z = q; q += C * D.v_dim;
     pf.y = q; q += C * D.v_dim;
-    pf.a = q; q += C * D.nv;
-    pf.b = q; q += C * D.nv;
+    pf.ab_split = pf_ab_split(D.H);
+    pf.a = q;  // K chunk z of a at a + z 2 C nv, of b at b + z 2 C nv
+    pf.b = q + C * D.nv;
+    q += 2 * C * D.nv * pf.ab_split;
     pf.decay = q; q += C * D.nv;
     pf.beta = q;
     q = arena;
@@ -1750,7 +1766,9 @@ void ChkEngine::pf_alloc() {
 // up GEMM with the sigmoid mix, then the mixed rows as the next operands.
 void ChkEngine::pf_hc_read(const HcDev& w, float* inj, uint32_t T, bool for_moe) {
     const uint32_t mt = (T + 63) / 64;
-    launch_pf_hc_prep(pf.hyper, w.norm, D.H, D.hc, D.eps, pf.inv, pf.hi, pf.lo, pf.xs, T, st);
+    launch_pf_hc_prep(pf.hyper, w.norm, D.H, D.hc, D.eps, pf.inv, pf.hi, pf.lo, pf.xs, T, pf.pend,
+                      (uint64_t)pf.cap * D.H, pf.pend_split, pf.inj_a, st);
+    pf.pend = nullptr;
     // [down; inject] is narrow (lowrank + hc outputs) over a long K = hc H:
     // split K by stream, partials summed in stream order by the finisher
     const uint32_t N = D.lowrank + D.hc;
@@ -1801,31 +1819,67 @@ void ChkEngine::pf_hc_read(const HcDev& w, float* inj, uint32_t T, bool for_moe)
     launch_pf_prep(p, st);
 }
 
-// linear_attention (cpu.rs:745-826) over the chunk: the four input
-// projections as one GEMM, conv + norms, the scan (chunked, 64 rows per
-// chunk, for head dims of 128; else sequential), the gated norm into the
-// out-projection's operands, out-projection + inject.
+// A block's out-projection (K inputs -> H) over the chunk's staged
+// operands.  Its inject into the hc streams (cpu.rs:971-979) is left to the
+// next hyper-connection read, which reads and rewrites every stream anyway:
+// the GEMM stores K-chunk partials (two chunks: twice the workgroups of a
+// one-pass launch, whose 8 column blocks x 64-row tiles gave the CUs one
+// workgroup each) into yd, free until the expert down projection.
+void ChkEngine::pf_out_proj(const Q4Mat& m, uint32_t K, uint32_t T) {
+    if (pf.pend) throw std::runtime_error("an out-projection is already pending");
+    const uint32_t G = K / 64;
+    PfGemmArgs o{};
+    o.seg[0] = PfSeg{m, pf.yd, D.H, 0};
+    o.nseg = 1;
+    o.N = D.H;
+    o.K = K;
+    o.M = T;
+    o.ksplit = G % 2 == 0 && (G / 2) % 8 == 0 ? 2 : 1;
+    o.zstride = (uint64_t)pf.cap * D.H;
+    o.xhi = pf.hi;
+    o.xlo = pf.lo;
+    o.xs = pf.xs;
+    launch_pf_gemm_args(o, PE_STORE, (T + 63) / 64, st);
+    pf.pend = pf.yd;
+    pf.pend_split = o.ksplit;
+}
+
+// linear_attention (cpu.rs:745-826) over the chunk: the qkv and z input
+// projections as one GEMM and the narrow a / b projections as a split-K
+// one, conv + norms, the scan (chunked, 64 rows per chunk, for head dims of
+// 128; else sequential), the gated norm into the out-projection's
+// operands, out-projection + inject.
 void ChkEngine::pf_deltanet(const LayerDev& L, uint32_t T) {
     const uint32_t mt = (T + 63) / 64, di = (uint32_t)L.dn_idx;
     PfGemmArgs g{};
     g.seg[0] = PfSeg{L.dn.qkv, pf.raw, D.conv_dim, 0};
     g.seg[1] = PfSeg{L.dn.z, pf.z, D.v_dim, D.conv_dim};
-    g.seg[2] = PfSeg{L.dn.a, pf.a, D.nv, D.conv_dim + D.v_dim};
-    g.seg[3] = PfSeg{L.dn.b, pf.b, D.nv, D.conv_dim + D.v_dim + D.nv};
-    g.nseg = 4;
-    g.N = D.conv_dim + D.v_dim + 2 * D.nv;
+    g.nseg = 2;
+    g.N = D.conv_dim + D.v_dim;
     g.K = D.H;
     g.M = T;
     g.xhi = pf.hi;
     g.xlo = pf.lo;
     g.xs = pf.xs;
     launch_pf_gemm_args(g, PE_STORE, mt, st);
+    // a and b (2 nv outputs): as 64 more columns of the GEMM above they made
+    // a last column block of workgroups, a whole extra pass over the CUs
+    // at the 80B shape; split K, their workgroups are short
+    PfGemmArgs ab = g;
+    ab.seg[0] = PfSeg{L.dn.a, pf.a, D.nv, 0};
+    ab.seg[1] = PfSeg{L.dn.b, pf.b, D.nv, D.nv};
+    ab.N = 2 * D.nv;
+    ab.ksplit = pf.ab_split;
+    ab.zstride = 2ull * pf.cap * D.nv;
+    launch_pf_gemm_args(ab, PE_STORE, mt, st);
     PfDnArgs a{};
     a.raw = pf.raw;
     a.ld_raw = D.conv_dim;
     a.a_raw = pf.a;
     a.b_raw = pf.b;
     a.ld_ab = D.nv;
+    a.ab_split = pf.ab_split;
+    a.ab_zstride = ab.zstride;
     a.conv_w = L.dn.conv;
     a.a_log = L.dn.a_log;
     a.dt_bias = L.dn.dt_bias;
@@ -1857,20 +1911,7 @@ void ChkEngine::pf_deltanet(const LayerDev& L, uint32_t T) {
     p.norm = L.dn.norm;
     p.dv = D.dv;
     launch_pf_prep(p, st);
-    PfGemmArgs o2{};
-    o2.seg[0].m = L.dn.out;
-    o2.nseg = 1;
-    o2.N = D.H;
-    o2.K = D.v_dim;
-    o2.M = T;
-    o2.xhi = pf.hi;
-    o2.xlo = pf.lo;
-    o2.xs = pf.xs;
-    o2.hyper = pf.hyper;
-    o2.inj = pf.inj_a;
-    o2.H = D.H;
-    o2.hc = D.hc;
-    launch_pf_gemm_args(o2, PE_INJECT, mt, st);
+    pf_out_proj(L.dn.out, D.v_dim, T);
 }
 
 // attention (cpu.rs:544-641) over the chunk: projections as one GEMM, the
@@ -1950,20 +1991,7 @@ void ChkEngine::pf_attention(const LayerDev& L, uint32_t T, uint32_t pos0, const
         }
     }
     launch_pf_xprep(pf.attn_out, D.nh * D.hd, T, D.nh * D.hd, pf.hi, pf.lo, pf.xs, st);
-    PfGemmArgs o2{};
-    o2.seg[0].m = L.at.o;
-    o2.nseg = 1;
-    o2.N = D.H;
-    o2.K = D.nh * D.hd;
-    o2.M = T;
-    o2.xhi = pf.hi;
-    o2.xlo = pf.lo;
-    o2.xs = pf.xs;
-    o2.hyper = pf.hyper;
-    o2.inj = pf.inj_a;
-    o2.H = D.H;
-    o2.hc = D.hc;
-    launch_pf_gemm_args(o2, PE_INJECT, mt, st);
+    pf_out_proj(L.at.o, D.nh * D.hd, T);
 }
 
 // moe (cpu.rs:504-541) over the chunk: router GEMM, per-row top-k, entries
@@ -1971,10 +1999,11 @@ void ChkEngine::pf_attention(const LayerDev& L, uint32_t T, uint32_t pos0, const
 // group), grouped down GEMM per entry, weighted combine + inject.
 void ChkEngine::pf_moe(const LayerDev& L, uint32_t T) {
     const uint32_t slots = D.topk + 1;
-    launch_pf_router(L.moe.router, L.moe.shared_gate, pf.bhi, pf.bmid, pf.blo, pf.logits, pf.sg, T, D.E, D.H, st);
+    launch_pf_router(L.moe.router, pf.bhi, pf.bmid, pf.blo, pf.logits, T, D.E, D.H, st);
     // the chunk's last row also as this layer's "last routes", as a row step leaves them
     const uint64_t roff = (uint64_t)L.moe.record_layer * MAX_NB * D.topk;
-    launch_pf_route(pf.logits, T, D.E, D.topk, D.norm_topk, pf.ids, pf.wts, s.route_ids + roff, s.route_w + roff, st);
+    launch_pf_route(pf.logits, T, D.E, D.topk, D.norm_topk, pf.ids, pf.wts, s.route_ids + roff, s.route_w + roff,
+                    L.moe.shared_gate, pf.bhi, pf.bmid, pf.blo, pf.sg, D.H, st);
     PfGemmArgs gu{};
     gu.seg[0] = PfSeg{L.moe.sh_gate, pf.act, D.I, 0};
     gu.seg[1].m = L.moe.sh_up;
@@ -2033,6 +2062,7 @@ void ChkEngine::prefill_gemm(const uint32_t* toks, uint32_t n, uint32_t next_aft
             tokens.resize(pos0);
             HIPCHK(hipMemcpy(pf.ple_ids, ids.data(), ids.size() * 4, hipMemcpyHostToDevice));
         }
+        pf.pend = nullptr;  // (an earlier failed chunk may have left one)
         launch_pf_embed(pf.tokens, embed, pf.hyper, D.H, D.hc, T, st);
         for (uint32_t l = 0; l < c.num_hidden_layers; ++l) {
             const LayerDev& L = layers[l];

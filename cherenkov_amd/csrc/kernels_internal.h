@@ -267,7 +267,7 @@ struct AttnArgs {
 };
 
 // ------------------------------------------------------------- prefill
-enum PfEpi { PE_STORE = 0, PE_INJECT = 1, PE_HC_UP = 2, PE_SILU_MUL = 3 };
+enum PfEpi { PE_STORE = 0, PE_HC_UP = 2, PE_SILU_MUL = 3 };
 
 // Operand preparation of one activation matrix (k_pf_prep).
 struct PfPrepArgs {
@@ -311,9 +311,8 @@ struct PfGemmArgs {
     uint32_t record_layer;
     const uint32_t* wbase;   // set by the launcher (dense matrices' common bases)
     const uint16_t* sbase;
-    // PE_INJECT / PE_HC_UP
+    // PE_HC_UP
     float* hyper;            // [M][hc H]
-    const float* inj;        // [M][hc]
     const float* inv;        // [M][hc]
     const uint16_t* norm;    // [hc H]
     float* out;              // [M][H]
@@ -326,9 +325,10 @@ struct PfGemmArgs {
 struct PfDnArgs {
     const float* raw;      // [T][ld_raw] qkv projection (pre-conv)
     uint32_t ld_raw;
-    const float* a_raw;    // [T][ld_ab]
+    const float* a_raw;    // [ab_split][.. ab_zstride][T][ld_ab]: K-chunk partials, summed in order
     const float* b_raw;
-    uint32_t ld_ab;
+    uint32_t ld_ab, ab_split = 1;
+    uint64_t ab_zstride;
     const uint16_t* conv_w;
     const uint16_t* a_log;
     const uint16_t* dt_bias;
@@ -374,8 +374,9 @@ void launch_attn(const AttnArgs& a, int nb, hipStream_t st);
 void launch_pf_prep(const PfPrepArgs& a, hipStream_t st);
 void launch_pf_xprep(const float* x, uint32_t ldx, uint32_t T, uint32_t K, uint4* hi, uint4* lo, float* xs,
                      hipStream_t st);
-void launch_pf_hc_prep(const float* hyper, const uint16_t* norm, uint32_t H, uint32_t hc, float eps, float* inv,
-                       uint4* hi, uint4* lo, float* xs, uint32_t T, hipStream_t st);
+void launch_pf_hc_prep(float* hyper, const uint16_t* norm, uint32_t H, uint32_t hc, float eps, float* inv,
+                       uint4* hi, uint4* lo, float* xs, uint32_t T, const float* part, uint64_t pzs, uint32_t nsplit,
+                       const float* pinj, hipStream_t st);
 void launch_pf_gemm_args(const PfGemmArgs& a, int epi, uint32_t grid_y, hipStream_t st);
 // whether a GEMM takes the staged-scale form (needed by tiles under 64 rows)
 bool pf_gemm_staged(const PfGemmArgs& a, int epi);
@@ -385,10 +386,11 @@ void launch_pf_gemm(const Q4Mat& w, const uint4* xhi, const uint4* xlo, const fl
                     uint32_t ldy, hipStream_t st);
 void launch_pf_hc_down_finish(const float* part, uint32_t nsplit, uint32_t T, uint32_t lowrank, uint32_t hc,
                               float alpha, float* d, float* inj, hipStream_t st);
-void launch_pf_router(const uint16_t* router, const uint16_t* shared_gate, const uint4* bhi, const uint4* bmid,
-                      const uint4* blo, float* logits, float* sg, uint32_t T, uint32_t E, uint32_t H, hipStream_t st);
+void launch_pf_router(const uint16_t* router, const uint4* bhi, const uint4* bmid, const uint4* blo, float* logits,
+                      uint32_t T, uint32_t E, uint32_t H, hipStream_t st);
 void launch_pf_route(const float* logits, uint32_t T, uint32_t E, uint32_t topk, int norm_topk, uint32_t* ids,
-                     float* wts, uint32_t* last_ids, float* last_wts, hipStream_t st);
+                     float* wts, uint32_t* last_ids, float* last_wts, const uint16_t* shared_gate, const uint4* bhi,
+                     const uint4* bmid, const uint4* blo, float* sg, uint32_t H, hipStream_t st);
 void launch_pf_group(const uint32_t* ids, uint32_t T, uint32_t topk, uint32_t E, uint32_t cap, uint32_t* list,
                      uint32_t* count, uint32_t* tiles, uint32_t* ntiles, uint64_t* act, uint32_t layer, uint32_t tr,
                      hipStream_t st);

@@ -119,13 +119,33 @@ __global__ void __launch_bounds__(256) k_pf_prep(PfPrepArgs a) {
 // grouped RMSNorm of gated_residual, cpu.rs:461-475), prepared as GEMM
 // operands over K = hc H.  One workgroup per row; thread tau owns 8-blocks
 // tau and tau + 256 of every stream (H <= 4096).
-__global__ void __launch_bounds__(256) k_pf_hc_prep(const float* __restrict__ hyper, const uint16_t* __restrict__ norm,
+// With `part`, first the inject of the block before (cpu.rs:971-979) the
+// out-projection left as nsplit K-chunk partials: hyper[t][g H + n] +=
+// (sum_z part[z][t][n]) inj[t][g], written back to hyper.
+__global__ void __launch_bounds__(256) k_pf_hc_prep(float* __restrict__ hyper, const uint16_t* __restrict__ norm,
                                                     uint32_t H, uint32_t hc, float eps, float* __restrict__ inv_out,
                                                     uint4* __restrict__ hi, uint4* __restrict__ lo,
-                                                    float* __restrict__ xs) {
+                                                    float* __restrict__ xs, const float* __restrict__ part,
+                                                    uint64_t pzs, uint32_t nsplit, const float* __restrict__ pinj) {
     __shared__ float red[4][4];
     const uint32_t t = blockIdx.x, tau = threadIdx.x, bps = H >> 3, hh = H * hc;
-    const float* row = hyper + (size_t)t * hh;
+    float* row = hyper + (size_t)t * hh;
+    float pv[2][8];
+    if (part) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t kb = min(tau + 256 * j, bps - 1);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) pv[j][e] = 0.0f;
+            for (uint32_t z = 0; z < nsplit; ++z) {
+                const float4* p = reinterpret_cast<const float4*>(part + z * pzs + (size_t)t * H + kb * 8);
+                const float4 u0 = p[0], u1 = p[1];
+                const float w8[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) pv[j][e] += w8[e];
+            }
+        }
+    }
     float v[4][2][8];
     float sq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -134,8 +154,15 @@ __global__ void __launch_bounds__(256) k_pf_hc_prep(const float* __restrict__ hy
         for (int j = 0; j < 2; ++j) {
             const uint32_t kb = tau + 256 * j;
             const bool ok = (uint32_t)g < hc && kb < bps;
-            const float4* p = reinterpret_cast<const float4*>(row + (size_t)(ok ? g : 0) * H + (ok ? kb : 0) * 8);
-            const float4 u0 = p[0], u1 = p[1];
+            float4* p = reinterpret_cast<float4*>(row + (size_t)(ok ? g : 0) * H + (ok ? kb : 0) * 8);
+            float4 u0 = p[0], u1 = p[1];
+            if (part && ok) {
+                const float ij = pinj[(size_t)t * hc + g];
+                u0 = make_float4(u0.x + pv[j][0] * ij, u0.y + pv[j][1] * ij, u0.z + pv[j][2] * ij, u0.w + pv[j][3] * ij);
+                u1 = make_float4(u1.x + pv[j][4] * ij, u1.y + pv[j][5] * ij, u1.z + pv[j][6] * ij, u1.w + pv[j][7] * ij);
+                p[0] = u0;
+                p[1] = u1;
+            }
             const float w8[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
@@ -213,7 +240,6 @@ __global__ void __launch_bounds__(256) k_pf_hc_prep(const float* __restrict__ hy
 // group == X.experts is the shared expert.
 //
 // Epilogues: PE_STORE (concatenated segments, each with its own output),
-// PE_INJECT (hyper[t][g H + n] += v inj[t][g], inject, cpu.rs:971-979),
 // PE_HC_UP (the four 16-wide tiles of a wave are the hc streams of the same
 // 16 outputs: mixed = (1/hc) sum_g sigmoid(v_g) normed_g, cpu.rs:477-491),
 // PE_SILU_MUL (NMAT 2: silu(gate) * up, mlp, cpu.rs:981-992).
@@ -697,34 +723,6 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
                 const uint32_t m = m0 + i * 16 + col;
-                if (EPI == PE_INJECT) {
-                    const uint32_t mc = min(m, M - 1);
-                    float4 hv[NJ][4];
-#pragma unroll
-                    for (int j = 0; j < NJ; ++j) {
-                        const float* hy = a.hyper + (size_t)mc * a.hc * a.H + min(n4[j], a.N - 4);
-#pragma unroll
-                        for (int g = 0; g < 4; ++g)
-                            hv[j][g] = (uint32_t)g < a.hc ? *reinterpret_cast<const float4*>(hy + (size_t)g * a.H)
-                                                          : make_float4(0.f, 0.f, 0.f, 0.f);
-                    }
-                    if (!mok[i]) continue;
-#pragma unroll
-                    for (int j = 0; j < NJ; ++j) {
-                        if (n4[j] >= a.N) continue;
-                        float* hy = a.hyper + (size_t)m * a.hc * a.H + n4[j];
-                        const f4 v = acc[0][i][j];
-#pragma unroll
-                        for (int g = 0; g < 4; ++g) {
-                            if ((uint32_t)g >= a.hc) continue;
-                            const float ij = a.inj[(size_t)m * a.hc + g];
-                            *reinterpret_cast<float4*>(hy + (size_t)g * a.H) =
-                                make_float4(hv[j][g].x + v[0] * ij, hv[j][g].y + v[1] * ij, hv[j][g].z + v[2] * ij,
-                                            hv[j][g].w + v[3] * ij);
-                        }
-                    }
-                    continue;
-                }
                 if (!mok[i]) continue;
 #pragma unroll
                 for (int j = 0; j < NJ; ++j) {
@@ -754,7 +752,7 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
         constexpr uint32_t OS = 260;  // floats per staged row (256 + pad: the four kq rows of a write hit distinct banks)
         static_assert(32 * OS * sizeof(float) <= sizeof(sA), "a staged half fits the A buffers");
         constexpr uint32_t NC = 256 / NMAT;  // staged columns
-        const uint32_t gcol = bx * NC + (uint32_t)tid % NC;  // PE_STORE / PE_SILU_MUL / PE_INJECT output column
+        const uint32_t gcol = bx * NC + (uint32_t)tid % NC;  // PE_STORE / PE_SILU_MUL output column
         PfSeg sg = a.seg[0];
         if (EPI == PE_STORE) {
     #pragma unroll
@@ -833,31 +831,7 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
                     for (int sgi = 1; sgi < 4; ++sgi)
                         if ((uint32_t)sgi < a.nseg && n4 >= a.seg[sgi].n0) s4 = a.seg[sgi];
                 }
-                if (EPI == PE_INJECT) {
-                    float4 v[KB];
-    #pragma unroll
-                    for (int k = 0; k < (int)KB; ++k) v[k] = *reinterpret_cast<const float4*>(&sO[(r0 + RPP * k) * OS + 4 * c4]);
-                    const uint32_t nc = nok ? n4 : 0;
-    #pragma unroll
-                    for (int k = 0; k < (int)KB; ++k) {
-                        const uint32_t m = mh + r0 + RPP * k, mc = min(m, M - 1);
-                        float* hy = a.hyper + (size_t)mc * a.hc * a.H + nc;
-                        float4 hv[4];
-    #pragma unroll
-                        for (int g = 0; g < 4; ++g)
-                            hv[g] = (uint32_t)g < a.hc ? *reinterpret_cast<const float4*>(hy + (size_t)g * a.H)
-                                                       : make_float4(0.f, 0.f, 0.f, 0.f);
-                        if (m >= M || !nok) continue;
-    #pragma unroll
-                        for (int g = 0; g < 4; ++g) {
-                            if ((uint32_t)g >= a.hc) continue;
-                            const float ij = a.inj[(size_t)m * a.hc + g];
-                            *reinterpret_cast<float4*>(hy + (size_t)g * a.H) =
-                                make_float4(hv[g].x + v[k].x * ij, hv[g].y + v[k].y * ij, hv[g].z + v[k].z * ij,
-                                            hv[g].w + v[k].w * ij);
-                        }
-                    }
-                } else {
+                {
                     // one row per iteration, the next row's LDS read issued
                     // before this row's activation and store
                     float4 vn = *reinterpret_cast<const float4*>(&sO[r0 * OS + 4 * c4]);
@@ -937,34 +911,34 @@ __global__ void __launch_bounds__(256) k_pf_hc_down_finish(const float* __restri
 }
 
 // ------------------------------------------------------------- router
-// logits[t][e] = W_r[e] . x_t (bf16 [E][H], f32 sums) and the shared-expert
-// gate logit as output E (moe, cpu.rs:506-508, 534-535), on
-// v_mfma_f32_16x16x32_bf16 with x split into three bf16 terms (natural k
+// logits[t][e] = W_r[e] . x_t (bf16 [E][H], f32 sums) (moe, cpu.rs:506-508),
+// on v_mfma_f32_16x16x32_bf16 with x split into three bf16 terms (natural k
 // order): every product of bf16 values is exact in f32, so the logits keep
 // f32-grade accuracy and the top-k cut sees what an f32 dot would.
 // A workgroup covers 64 rows x 64 outputs, each wave one 16-output column
-// tile over the 64 rows.  Per 64-wide k block the three x planes of the 64
+// tile over the 64 rows (E / 64 column blocks: one workgroup per CU at
+// E = 512, T = 2048; the shared-expert gate logit is the routing wave's).  Per 64-wide k block the three x planes of the 64
 // rows are staged through LDS once for the four waves (double-buffered;
 // the next block's pieces and weight words load while this one computes).
 constexpr int RT_AROW = 9;  // uint4 per staged row (8 + 1 pad)
 
 __global__ void __launch_bounds__(256) k_pf_router(const uint16_t* __restrict__ router,
-                                                   const uint16_t* __restrict__ shared_gate,
                                                    const uint4* __restrict__ bhi, const uint4* __restrict__ bmid,
                                                    const uint4* __restrict__ blo, float* __restrict__ logits,
-                                                   float* __restrict__ sg, uint32_t T, uint32_t E, uint32_t H) {
+                                                   uint32_t T, uint32_t E, uint32_t H) {
     __shared__ __align__(16) u32x4 sA[2][3][64 * RT_AROW];
     const int tid = threadIdx.x, lane = tid & 63, col = lane & 15, kq = lane >> 4;
     const uint32_t m0 = blockIdx.y * 64, KB = H >> 3, NB = H >> 6;
     const uint32_t nn = blockIdx.x * 64 + wave_id() * 16 + col;
-    const uint32_t r = min(nn, E);
-    const u32x4* bp = reinterpret_cast<const u32x4*>(r < E ? router + (size_t)r * H : shared_gate);
+    const u32x4* bp = reinterpret_cast<const u32x4*>(router + (size_t)min(nn, E - 1) * H);
     // staging: piece u of thread tid is plane u / 2, row (tid + 256 (u % 2)) / 8, 8-block tid % 8
     const uint32_t srow = (uint32_t)tid >> 3, skb = (uint32_t)tid & 7;
     size_t soff[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) soff[h] = (size_t)min(m0 + srow + 32 * h, T - 1) * KB + skb;
-    u32x4 ra[2][6], rb[2][2];
+    // three register slots: block blk's loads are issued two blocks ahead
+    // (slot blk % 3), so each step's wait covers two steps of latency
+    u32x4 ra[3][6], rb[3][2];
     auto fetch = [&](int slot, uint32_t blk) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < 6; ++u) {
@@ -981,37 +955,43 @@ __global__ void __launch_bounds__(256) k_pf_router(const uint16_t* __restrict__ 
     f4 acc[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    // block blk: registers slot P = blk % 3, LDS buffer blk % 2
     auto step = [&](auto sc_, uint32_t blk) __attribute__((always_inline)) {
         constexpr int P = decltype(sc_)::value;
-        fetch(P ^ 1, min(blk + 1, NB - 1));
+        const uint32_t buf = blk & 1;
+        fetch((P + 2) % 3, min(blk + 2, NB - 1));
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
             const b8 bq = __builtin_bit_cast(b8, rb[P][s]);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const uint32_t ai = (16 * i + col) * RT_AROW + 4 * s + kq;
-                const b8 xh = __builtin_bit_cast(b8, sA[P][0][ai]);
-                const b8 xm = __builtin_bit_cast(b8, sA[P][1][ai]);
-                const b8 xl = __builtin_bit_cast(b8, sA[P][2][ai]);
+                const b8 xh = __builtin_bit_cast(b8, sA[buf][0][ai]);
+                const b8 xm = __builtin_bit_cast(b8, sA[buf][1][ai]);
+                const b8 xl = __builtin_bit_cast(b8, sA[buf][2][ai]);
                 acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, bq, acc[i], 0, 0, 0);
                 acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xm, bq, acc[i], 0, 0, 0);
                 acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, bq, acc[i], 0, 0, 0);
             }
         }
-        store(P ^ 1, P ^ 1);
+        store((P + 1) % 3, buf ^ 1);
         __syncthreads();
     };
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
     fetch(0, 0);
+    fetch(1, min(1u, NB - 1));
     store(0, 0);
     __syncthreads();
     uint32_t blk = 0;
-    for (; blk + 1 < NB; blk += 2) {
+    for (; blk + 2 < NB; blk += 3) {
         step(I0{}, blk);
         step(I1{}, blk + 1);
+        step(I2{}, blk + 2);
     }
     if (blk < NB) step(I0{}, blk);
+    if (blk + 1 < NB) step(I1{}, blk + 1);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -1019,7 +999,6 @@ __global__ void __launch_bounds__(256) k_pf_router(const uint16_t* __restrict__ 
             const uint32_t m = m0 + i * 16 + kq * 4 + rr;
             if (m >= T) continue;
             if (nn < E) logits[(size_t)m * E + nn] = acc[i][rr];
-            else if (nn == E) sg[m] = acc[i][rr];
         }
 }
 
@@ -1030,13 +1009,40 @@ __global__ void __launch_bounds__(256) k_pf_router(const uint16_t* __restrict__ 
 __global__ void __launch_bounds__(256) k_pf_route(const float* __restrict__ logits, uint32_t T, uint32_t E,
                                                   uint32_t topk, int norm_topk, uint32_t* __restrict__ ids,
                                                   float* __restrict__ wts, uint32_t* __restrict__ last_ids,
-                                                  float* __restrict__ last_wts) {
+                                                  float* __restrict__ last_wts, const uint16_t* __restrict__ shared_gate,
+                                                  const uint4* __restrict__ bhi, const uint4* __restrict__ bmid,
+                                                  const uint4* __restrict__ blo, float* __restrict__ sg, uint32_t H) {
     const int lane = threadIdx.x & 63;
     const uint32_t t = blockIdx.x * (CHK_WG >> 6) + wave_id();
     if (t >= T) return;
+    // the shared-expert gate logit sg[t] = w_sg . x_t (cpu.rs:534-535) from
+    // the same three bf16 terms of x, products exact in f32; its loads are
+    // in flight beside the routing's
+    const uint32_t KB = H >> 3;
+    float sgs = 0.0f;
+#pragma unroll 4
+    for (uint32_t kb = lane; kb < KB; kb += 64) {
+        const size_t xo = (size_t)t * KB + kb;
+        const u32x4 w4 = reinterpret_cast<const u32x4*>(shared_gate)[kb];
+        const u32x4 p4[3] = {__builtin_bit_cast(u32x4, bhi[xo]), __builtin_bit_cast(u32x4, bmid[xo]),
+                             __builtin_bit_cast(u32x4, blo[xo])};
+        const uint32_t wv[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float wl = __uint_as_float(wv[c] << 16), wh = __uint_as_float(wv[c] & 0xffff0000u);
+#pragma unroll
+            for (int u = 0; u < 3; ++u) {
+                const uint32_t xv = c == 0 ? p4[u].x : c == 1 ? p4[u].y : c == 2 ? p4[u].z : p4[u].w;
+                sgs = fmaf(wl, __uint_as_float(xv << 16), sgs);
+                sgs = fmaf(wh, __uint_as_float(xv & 0xffff0000u), sgs);
+            }
+        }
+    }
     uint32_t my_id;
     float my_p;
     route_row(logits + (size_t)t * E, E, topk, lane, nullptr, my_id, my_p);
+    sgs = wave_sum_dpp(sgs);
+    if (lane == 0) sg[t] = sgs;
     float topsum = 0.0f;
     for (uint32_t r = 0; r < topk; ++r) topsum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_p), (int)r));
     if ((uint32_t)lane < topk) {
@@ -1282,7 +1288,12 @@ __global__ void __launch_bounds__(256) k_pf_dn_misc(PfDnArgs a) {
     const uint32_t j = i - a.conv_dim;
     if (j >= a.T * a.nv) return;
     const uint32_t t = j / a.nv, hv = j % a.nv;
-    const float av = a.a_raw[(size_t)t * a.ld_ab + hv], bv = a.b_raw[(size_t)t * a.ld_ab + hv];
+    float av = 0.0f, bv = 0.0f;
+    for (uint32_t z = 0; z < a.ab_split; ++z) {
+        const size_t o = z * a.ab_zstride + (size_t)t * a.ld_ab + hv;
+        av += a.a_raw[o];
+        bv += a.b_raw[o];
+    }
     const float gg = -expf(bf16f(a.a_log[hv])) * softplusf_(av + bf16f(a.dt_bias[hv]));
     a.decay[(size_t)t * a.nv + hv] = expf(gg);
     a.beta[(size_t)t * a.nv + hv] = sigmoidf_(bv);
@@ -1393,10 +1404,13 @@ void launch_pf_xprep(const float* x, uint32_t ldx, uint32_t T, uint32_t K, uint4
     launch_pf_prep(a, st);
 }
 
-void launch_pf_hc_prep(const float* hyper, const uint16_t* norm, uint32_t H, uint32_t hc, float eps, float* inv,
-                       uint4* hi, uint4* lo, float* xs, uint32_t T, hipStream_t st) {
+void launch_pf_hc_prep(float* hyper, const uint16_t* norm, uint32_t H, uint32_t hc, float eps, float* inv,
+                       uint4* hi, uint4* lo, float* xs, uint32_t T, const float* part, uint64_t pzs, uint32_t nsplit,
+                       const float* pinj, hipStream_t st) {
     if (H > 4096 || hc > 4 || H % 64) throw std::runtime_error("prefill hyper-connection norm needs hidden <= 4096, hc <= 4");
-    if (T) k_pf_hc_prep<<<T, CHK_WG, 0, st>>>(hyper, norm, H, hc, eps, inv, hi, lo, xs);
+    if (part && (!nsplit || pzs % 4 || (uintptr_t)part % 16 || !pinj))
+        throw std::runtime_error("pending inject needs 16-byte aligned partials");
+    if (T) k_pf_hc_prep<<<T, CHK_WG, 0, st>>>(hyper, norm, H, hc, eps, inv, hi, lo, xs, part, pzs, nsplit, pinj);
 }
 
 // The launch form of a GEMM: 32-bit element offsets of the dense matrices
@@ -1448,14 +1462,13 @@ void launch_pf_gemm_args(const PfGemmArgs& args, int epi, uint32_t grid_y, hipSt
         throw std::runtime_error("split K needs whole groups per chunk and a plain store");
     if (epi == PE_HC_UP && a.hc > 4) throw std::runtime_error("prefill mix needs hc <= 4");
     // 16-byte output stores: N, every output row and every segment start on
-    // a 4-float boundary.  The hc-stream epilogues (inject, mix) have only
-    // that form.
+    // a 4-float boundary.  The hc-stream mix epilogue has only that form.
     bool v4 = a.N % 4 == 0 && (ksplit == 1 || a.zstride % 4 == 0);
     for (uint32_t q = 0; q < (epi == PE_STORE ? a.nseg : 1u); ++q)
         v4 = v4 && (uintptr_t)a.seg[q].y % 16 == 0 && a.seg[q].ldy % 4 == 0 && a.seg[q].n0 % 4 == 0;
-    if (epi == PE_INJECT || epi == PE_HC_UP) {
+    if (epi == PE_HC_UP) {
         v4 = a.H % 4 == 0 && a.N % 4 == 0 && (uintptr_t)a.hyper % 16 == 0 &&
-             (epi == PE_INJECT || ((uintptr_t)a.out % 16 == 0 && (uintptr_t)a.norm % 8 == 0));
+             (uintptr_t)a.out % 16 == 0 && (uintptr_t)a.norm % 8 == 0;
         if (!v4) throw std::runtime_error("prefill hyper-connection GEMMs need 16-byte aligned streams");
     }
     a.vec4 = v4 ? 1u : 0u;
@@ -1489,7 +1502,6 @@ void launch_pf_gemm_args(const PfGemmArgs& args, int epi, uint32_t grid_y, hipSt
     }
     switch (epi) {
     case PE_STORE: PF_GEMM(1, PE_STORE, (a.N + 255) / 256); break;
-    case PE_INJECT: PF_GEMM(1, PE_INJECT, (a.N + 255) / 256); break;
     case PE_HC_UP: PF_GEMM(1, PE_HC_UP, (a.H + 63) / 64); break;
     default: PF_GEMM(2, PE_SILU_MUL, (a.N + 127) / 128); break;
     }
@@ -1516,17 +1528,20 @@ void launch_pf_hc_down_finish(const float* part, uint32_t nsplit, uint32_t T, ui
     if (n) k_pf_hc_down_finish<<<(uint32_t)((n + CHK_WG - 1) / CHK_WG), CHK_WG, 0, st>>>(part, nsplit, n, T, lowrank, hc, alpha, d, inj);
 }
 
-void launch_pf_router(const uint16_t* router, const uint16_t* shared_gate, const uint4* bhi, const uint4* bmid,
-                      const uint4* blo, float* logits, float* sg, uint32_t T, uint32_t E, uint32_t H, hipStream_t st) {
+void launch_pf_router(const uint16_t* router, const uint4* bhi, const uint4* bmid, const uint4* blo, float* logits,
+                      uint32_t T, uint32_t E, uint32_t H, hipStream_t st) {
     if (H % 64) throw std::runtime_error("router width must be a multiple of 64");
     if (T)
-        k_pf_router<<<dim3((E + 1 + 63) / 64, (T + 63) / 64), CHK_WG, 0, st>>>(router, shared_gate, bhi, bmid, blo,
-                                                                               logits, sg, T, E, H);
+        k_pf_router<<<dim3((E + 63) / 64, (T + 63) / 64), CHK_WG, 0, st>>>(router, bhi, bmid, blo, logits, T, E, H);
 }
 
 void launch_pf_route(const float* logits, uint32_t T, uint32_t E, uint32_t topk, int norm_topk, uint32_t* ids,
-                     float* wts, uint32_t* last_ids, float* last_wts, hipStream_t st) {
-    if (T) k_pf_route<<<(T + 3) / 4, CHK_WG, 0, st>>>(logits, T, E, topk, norm_topk, ids, wts, last_ids, last_wts);
+                     float* wts, uint32_t* last_ids, float* last_wts, const uint16_t* shared_gate, const uint4* bhi,
+                     const uint4* bmid, const uint4* blo, float* sg, uint32_t H, hipStream_t st) {
+    if (H % 8 || (uintptr_t)shared_gate % 16) throw std::runtime_error("shared gate needs 16-byte rows");
+    if (T)
+        k_pf_route<<<(T + 3) / 4, CHK_WG, 0, st>>>(logits, T, E, topk, norm_topk, ids, wts, last_ids, last_wts,
+                                                   shared_gate, bhi, bmid, blo, sg, H);
 }
 
 void launch_pf_group(const uint32_t* ids, uint32_t T, uint32_t topk, uint32_t E, uint32_t cap, uint32_t* list,
