@@ -833,9 +833,12 @@ std::vector<size_t> qsa_pick(std::vector<std::pair<float, size_t>> bs, size_t to
 // select_tokens, src/qwen4_exp/cpu.rs:643-719: dense while the complete
 // blocks fit the budget, else block scores (pooled index keys,
 // index_k_norm, rope at the block start, relu dots with the normed and
-// roped index queries) and qsa_pick.  Scoring is pinned by its parts'
-// closed forms (rms_norm, rope_partial) and, end to end, only against the
-// GPU's independent implementation (tests/test_gpu_qsa.py).
+// roped index queries) and qsa_pick.  Scoring is pinned by closed forms
+// in tests/test_oracle_compositions.py: block keys along chosen directions
+// outside the rotated dims (a tie kept at the lower block, the relu's
+// effect), and index queries and keys inside them, where the kept blocks
+// follow the relative angle between the query rotated at pos and block b's
+// key rotated at b * ratio (and change if either position is wrong).
 std::vector<size_t> select_tokens(const OrcModel& m, const AttnW& w, const float* iq, const KvCache& cache,
                                   size_t pos) {
     const ChkConfig& c = m.c;

@@ -409,6 +409,155 @@ def test_select_tokens_block_scores(case):
     close(out, attn_out(cfg, vals, n_tok - 1, visible), f"{case}: attention over the kept blocks", rtol=1e-4)
 
 
+# ------------------------------------------- RoPE positions (relative angles)
+
+def rel_dot(a, b, shift, rot, theta):
+    """a . b after rotating a by position p_a and b by p_b under rotate-half
+    RoPE on the first `rot` dims, p_a - p_b = shift: pair j = (j, j + rot/2)
+    is a complex number turned by p * theta^(-2j/rot), so the pair's share of
+    the dot is Re(a_j conj(b_j) e^{i shift w_j}) (the rotation group's
+    relative-angle identity); dims past `rot` add their plain product."""
+    half = rot // 2
+    w = float(theta) ** (-2.0 * np.arange(half) / rot)
+    ac = a[:half] + 1j * a[half:rot]
+    bc = b[:half] + 1j * b[half:rot]
+    return float(np.sum((ac * np.conj(bc) * np.exp(1j * shift * w)).real) + a[rot:] @ b[rot:])
+
+
+def test_attention_rope_relative_positions():
+    """attention (cpu.rs:544-641) with q and k inside the rotated dims
+    (cpu.rs:575-587: q rotated at the query's position, k at its own, both
+    after the per-head norm): the score of query token p against key token t
+    is hd^-1/2 rel_dot(q^, k^, p - t), so the softmax weights depend on
+    p - t through every pair's frequency.  Six tokens, each attended over
+    its causal prefix; a rotation at the wrong position for q (p + 1, 0) or
+    k (unrotated, the query's position) moves the weights by orders of
+    magnitude more than the tolerance."""
+    cfg = presets.tiny(mtp=0)
+    m = OracleModel(cfg)
+    st = m.new_state()
+    nh, nkv, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    rot = int(hd * cfg.partial_rotary_factor)
+    inh, ihd = cfg.indexer_n_heads, cfg.indexer_head_dim
+    rng = np.random.default_rng(36)
+    n_tok = 6
+    toks = []
+    for t in range(n_tok):
+        q = rng.normal(0, 0.3, (nh, hd))
+        q[:, :rot] = rng.normal(0, 2.0, (nh, rot))
+        k = rng.normal(0, 0.3, (nkv, hd))
+        k[:, :rot] = rng.normal(0, 2.0, (nkv, rot))
+        toks.append((q, rng.normal(0, 1, (nh, hd)), k, rng.normal(0, 1, (nkv, hd)),
+                     rng.normal(0, 1, (inh + 1, ihd))))
+    layer = 3
+    vals = attn_setup(cfg, m, layer, rng, toks)
+    grp = nh // nkv
+    G = nh * hd // 64
+
+    def expect(p, q_shift=0, k_pos=None):
+        out = np.zeros((nh, hd))
+        for h in range(nh):
+            hk = h // grp
+            qh = rms(vals[p][0][h])
+            s = np.array([hd ** -0.5 * rel_dot(qh, rms(vals[t][2][hk]),
+                                               p + q_shift - (t if k_pos is None else k_pos(t, p)),
+                                               rot, cfg.rope_theta) for t in range(p + 1)])
+            pr = np.exp(s - s.max())
+            pr /= pr.sum()
+            out[h] = sum(pi * vals[t][3][hk] for pi, t in zip(pr, range(p + 1))) * sig(vals[p][1][h])
+        gs = out.ravel().reshape(G, 64).sum(1)
+        return gs[np.arange(cfg.hidden_size) % G]
+
+    for p in range(n_tok):
+        x = np.zeros(cfg.hidden_size, np.float32)
+        x[p * 64:(p + 1) * 64] = 1.0
+        o = st.attention(layer, x, p, kv_q8=False)
+        want = expect(p)
+        close(o, want, f"attention with rotated q/k, token {p}", rtol=1e-4)
+        if p >= 2:  # the same closed form with a slipped position is far off
+            scale = float(np.max(np.abs(want)))
+            for label, wrong in (("q at p+1", expect(p, q_shift=1)), ("q at 0", expect(p, q_shift=-p)),
+                                 ("k unrotated", expect(p, k_pos=lambda t, pp: 0)),
+                                 ("k at the query's position", expect(p, k_pos=lambda t, pp: pp))):
+                assert float(np.max(np.abs(wrong - want))) > 100 * 1e-4 * scale, label
+
+
+def test_select_tokens_rope_positions():
+    """select_tokens (cpu.rs:643-719) past the budget with the index query
+    and the block keys inside the rotated dims (cpu.rs:676-690): the index
+    query heads are rotated at the query's position p and block b's pooled,
+    normed key at b * ratio, so head h scores relu(ihd cos(psi_h + p -
+    phi_b - b ratio)) / sqrt(ihd) for a query of angle psi_h and a key of
+    angle phi_b in the first rotated pair (frequency 1 rad per position).
+    The angles are chosen so that the two kept blocks of four differ from
+    the correct ones (the test checks this) if the query is rotated at 0,
+    p - 1 or p + 1, or the keys at p, b, 0, (b + 1) ratio - 1 or
+    (b + 1) ratio; the query/key dots of the attention proper are 0, so the
+    output shows which blocks are kept."""
+    budget, ratio = 8, 4
+    cfg = presets.tiny(mtp=0, indexer_budget=budget)
+    assert cfg.indexer_compress_ratio == ratio
+    m = OracleModel(cfg)
+    st = m.new_state()
+    nh, nkv, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    inh, ihd = cfg.indexer_n_heads, cfg.indexer_head_dim
+    assert inh == 2
+    rot = int(hd * cfg.partial_rotary_factor)
+    half = rot // 2
+    psi = [1.11, -0.61]
+    phi = [2.11, 0.45, -2.7, -2.69]
+    nb = len(phi)
+    n_tok = ratio * nb + 1
+    p = n_tok - 1
+    rng = np.random.default_rng(37)
+    groups = []
+    for blk in range(nb + 1):
+        q = np.zeros((nh, hd))
+        q[:, hd - 1] = 1.0
+        k = np.zeros((nkv, hd))
+        k[:, hd - 2] = 1.0
+        v = (blk + 1) * (1.0 + 0.01 * np.arange(hd))[None, :].repeat(nkv, 0)
+        v[1] *= -0.5
+        idx = np.zeros((inh + 1, ihd))
+        for h in range(inh):
+            idx[h, 0], idx[h, half] = np.cos(psi[h]), np.sin(psi[h])
+        if blk < nb:
+            idx[inh, 0], idx[inh, half] = np.cos(phi[blk]), np.sin(phi[blk])
+        groups.append((q, rng.normal(0, 1, (nh, hd)), k, v, idx))
+    layer = 3
+    vals_g = attn_setup(cfg, m, layer, rng, groups)
+    vals = [vals_g[min(t // ratio, nb)] for t in range(n_tok)]
+    qn = [rms(vals[-1][4][h]) for h in range(inh)]
+
+    def kept(q_pos, k_pos):
+        scores = []
+        for blk in range(nb):
+            key = rms(vals[blk * ratio][4][inh])
+            scores.append(sum(max(0.0, rel_dot(qh, key, q_pos - k_pos(blk), rot, cfg.rope_theta)) for qh in qn)
+                          / np.sqrt(ihd))
+        order = sorted(range(nb), key=lambda b: (-scores[b], b))
+        s = sorted(scores, reverse=True)
+        assert s[budget // ratio - 1] - s[budget // ratio] > 1.0, scores  # no near-tie at the cut
+        return sorted(order[:budget // ratio])
+
+    keep = kept(p, lambda b: b * ratio)
+    for label, q_pos, k_pos in (("q at 0", 0, lambda b: b * ratio), ("q at p-1", p - 1, lambda b: b * ratio),
+                                ("q at p+1", p + 1, lambda b: b * ratio), ("keys at p", p, lambda b: p),
+                                ("keys at b", p, lambda b: b), ("keys at 0", p, lambda b: 0),
+                                ("keys at the block end", p, lambda b: (b + 1) * ratio - 1),
+                                ("keys at the next block", p, lambda b: (b + 1) * ratio)):
+        assert kept(q_pos, k_pos) != keep, label
+    out = None
+    for t in range(n_tok):
+        x = np.zeros(cfg.hidden_size, np.float32)
+        g = min(t // ratio, nb)
+        x[g * 64:(g + 1) * 64] = 1.0
+        out = st.attention(layer, x, t, kv_q8=False)
+    visible = [t for b in keep for t in range(b * ratio, (b + 1) * ratio)] + [n_tok - 1]
+    close(out, attn_out(cfg, vals, n_tok - 1, visible), "attention over the blocks kept by rotated scores",
+          rtol=1e-4)
+
+
 # ---------------------------------------------------------------- MTP head
 
 def zero_layer_outputs(cfg, m, layer):
