@@ -234,6 +234,7 @@ SIGNATURES = [
     ("chk_decode_new_sampling", i32, [P, C.POINTER(ChkSampling), C.POINTER(u32), u32, C.POINTER(f32), u32,
                                       C.POINTER(u32), u32, u32, u32, u32, C.POINTER(P)]),
     ("chk_decode_free", None, [P]),
+    ("chk_decode_set_eos", i32, [P, C.POINTER(u32), u32]),
     ("chk_decode_step", i32, [P, C.POINTER(u32), C.POINTER(u32)]),
     ("chk_decode_finished", i32, [P]),
     ("chk_decode_stats", i32, [P, C.POINTER(u32), C.POINTER(u32)]),

@@ -555,6 +555,8 @@ struct ChkEngine {
             ngram_mult = store_i64(pre + ".layer_multipliers", c.ngram_size);
             const std::vector<int64_t> offs = store_i64(pre + ".ngram_heads_offsets", heads);
             const std::vector<int64_t> sizes = store_i64(pre + ".ngram_heads_vocab_sizes", heads);
+            for (uint32_t h = 0; h < heads; ++h)
+                ensure(offs[h] >= 0 && sizes[h] >= 0, "n-gram heads exceed the table");
             ngram_offs.assign(offs.begin(), offs.end());
             ngram_sizes.assign(sizes.begin(), sizes.end());
             ensure(N.dim * heads == c.ple_embed_dim, "n-gram head layout mismatch");
@@ -575,7 +577,7 @@ struct ChkEngine {
             ngram_row_bytes = chk_ngram_row_bytes(ngram_dim, ngram_group);
         }
         for (uint32_t h = 0; h < heads; ++h)
-            ensure(ngram_sizes[h] >= 1 && ngram_sizes[h] < (1ull << 62) && ngram_offs[h] + ngram_sizes[h] <= ngram_rows,
+            ensure(ngram_sizes[h] >= 1 && ngram_offs[h] <= ngram_rows && ngram_sizes[h] <= ngram_rows - ngram_offs[h],
                    "n-gram heads exceed the table");
         ensure(ngram_rows < (1ull << 32), "n-gram table above 2^32 rows");
         ngram = dalloc<uint8_t>(ngram_rows * ngram_row_bytes);

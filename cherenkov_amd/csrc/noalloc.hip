@@ -7,9 +7,14 @@
 // The array is a host-side stand-in in host code: its device address is
 // looked up once per device (hipGetSymbolAddress, on the entry point's
 // first call with that device current) and only that address is passed to
-// kernels.  Every call on a device shares that device's array; the kernels
-// overwrite every partial they read, so nothing needs clearing, and calls
-// that overlap on one device race.
+// kernels.  That first call must not be under stream capture (it is
+// refused there); every later call only enqueues the two kernels on the
+// caller's stream and never waits on it, so it can be captured into a
+// graph.  Launch errors are reported; errors of the kernels themselves
+// surface at the caller's next synchronisation.  Every call on a device
+// shares that device's array; the kernels overwrite every partial they
+// read, so nothing needs clearing, and calls that overlap on one device
+// race.
 #include <hip/hip_runtime.h>
 
 #include <mutex>
@@ -23,6 +28,7 @@ namespace chk {
 
 constexpr uint32_t NOALLOC_PARTS = 1024;  // LM head workgroups (argmax partials per row)
 constexpr uint64_t NOALLOC_SCRATCH_BYTES = (uint64_t)MAX_NB * NOALLOC_PARTS * (sizeof(float) + sizeof(uint32_t));
+static_assert(NOALLOC_SCRATCH_BYTES == 32 * 1024, "argmax partials: 4 rows x 1024 workgroups x (f32 value, u32 row)");
 
 static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
 
@@ -30,14 +36,20 @@ constexpr int NOALLOC_MAX_DEVICES = 64;
 static void* g_scratch_dev[NOALLOC_MAX_DEVICES];
 static std::mutex g_scratch_mu;
 
-// The device address of `scratch` on the current device.
-static uint8_t* scratch_address() {
+// The device address of `scratch` on the current device; the lookup (first
+// call on a device) is refused while `st` is capturing.
+static uint8_t* scratch_address(hipStream_t st) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) throw std::runtime_error(std::string("hipGetDevice: ") + hipGetErrorString(e));
     if (dev < 0 || dev >= NOALLOC_MAX_DEVICES) throw std::runtime_error("device index out of range");
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (!g_scratch_dev[dev]) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        e = hipStreamIsCapturing(st, &cs);
+        if (e != hipSuccess) throw std::runtime_error(std::string("hipStreamIsCapturing: ") + hipGetErrorString(e));
+        if (cs != hipStreamCaptureStatusNone)
+            throw std::runtime_error("the first call on a device resolves the scratch address and must not be captured");
         void* p = nullptr;
         e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess || !p)
@@ -57,18 +69,14 @@ extern "C" int chk_lm_head_argmax_noalloc(const void* w, const void* s, const vo
         if (nb < 1 || nb > (uint32_t)MAX_NB) throw std::runtime_error("nb must be 1..=4");
         if (in % 64 || in == 0) throw std::runtime_error("in must be a positive multiple of 64");
         if (out == 0 || out % 8) throw std::runtime_error("out must be a positive multiple of 8");
-        if ((uint64_t)nb * NOALLOC_PARTS * 8 > NOALLOC_SCRATCH_BYTES)
-            throw std::runtime_error("argmax partials exceed the " + std::to_string(NOALLOC_SCRATCH_BYTES) +
-                                     "-byte scratch");
         hipStream_t st = (hipStream_t)stream;
-        uint8_t* base = scratch_address();
+        uint8_t* base = scratch_address(st);
         float* pv = reinterpret_cast<float*>(base);
         uint32_t* pi = reinterpret_cast<uint32_t*>(base + (uint64_t)MAX_NB * NOALLOC_PARTS * sizeof(float));
         launch_lm_head(Q4Mat{(const uint32_t*)w, (const uint16_t*)s, (const uint16_t*)b, out, in}, x, logits, pv, pi,
                        NOALLOC_PARTS, ids, (int)nb, st);
-        hipError_t e = hipStreamSynchronize(st);
-        if (e == hipSuccess) e = hipGetLastError();
-        if (e != hipSuccess) throw std::runtime_error(std::string("HIP error ") + hipGetErrorString(e));
+        hipError_t e = hipPeekAtLastError();
+        if (e != hipSuccess) throw std::runtime_error(std::string("HIP launch error ") + hipGetErrorString(e));
         return 0;
     } catch (const std::exception& ex) {
         g_err = ex.what();

@@ -326,11 +326,13 @@ extern "C" int chk_phase_bench(int mode, uint32_t wgs, uint32_t phases, uint64_t
             a.abort_flag = d.alloc<uint32_t>(256);
             a.err = d.alloc<uint32_t>(256);
             a.data = d.alloc<float>((size_t)2 * wgs * 64 * 4);
-            ck(hipMemsetAsync(a.bar, 0, 8 * 16 * 4, st), "memset");
             float t[3];
             const uint32_t ph[3] = {phases / 4, phases / 4, phases};
             for (int k = 0; k < 3; ++k) {
                 a.phases = ph[k];
+                // each run starts its counters at 0: a run that aborted at the
+                // spin limit leaves them off a multiple of the XCD's workgroups
+                ck(hipMemsetAsync(a.bar, 0, 8 * 16 * 4, st), "memset");
                 ck(hipMemsetAsync(a.abort_flag, 0, 256, st), "memset");
                 ck(hipMemsetAsync(a.err, 0, 256, st), "memset");
                 ck(hipStreamSynchronize(st), "sync");

@@ -27,7 +27,7 @@ struct ChkDecode {
     std::vector<uint32_t> drafts;
     uint32_t n_draft = 0;
     bool use_eos = true;
-    uint32_t eos = 0;
+    std::vector<uint32_t> eos;  // the stop ids (the reference's [im_end, endoftext])
     uint32_t limit = 0;
     std::vector<uint32_t> tokens;
     int finish = 0;  // 0 running, 1 stop, 2 length
@@ -36,7 +36,7 @@ struct ChkDecode {
 
     ~ChkDecode() { chk_sampler_free(sampler); }
 
-    bool is_eos(uint32_t t) const { return use_eos && t == eos; }
+    bool is_eos(uint32_t t) const { return use_eos && std::find(eos.begin(), eos.end(), t) != eos.end(); }
 
     static void check(int rc) {
         if (rc != 0) throw std::runtime_error(chk_last_error());
@@ -124,7 +124,7 @@ int chk_decode_new_sampling(ChkEngine* e, const ChkSampling* sampling, const uin
         d->e = e;
         d->limit = limit;
         d->use_eos = no_eos == 0;
-        d->eos = chk_eos_token(e);
+        d->eos.assign(1, chk_eos_token(e));
         if (chk_sampling_greedy(sampling)) {
             ChkDecode::check(chk_sampling_validate(sampling));
             d->cur = next;
@@ -146,6 +146,18 @@ int chk_decode_new_sampling(ChkEngine* e, const ChkSampling* sampling, const uin
 }
 
 void chk_decode_free(ChkDecode* d) { delete d; }
+
+// The stop ids: the reference stops on the tokenizer's [im_end, endoftext]
+// (decode.rs:64); the engine has no tokenizer, so the caller that owns it
+// passes them.  Until called, the config's eos_token_id alone.
+int chk_decode_set_eos(ChkDecode* d, const uint32_t* ids, uint32_t n) {
+    if (n < 1 || n > 16) {
+        g_runner_err = "EOS ids must be 1..=16";
+        return -1;
+    }
+    d->eos.assign(ids, ids + n);
+    return 0;
+}
 
 // One Decode::step; writes the tokens emitted by this step (at most 4).
 int chk_decode_step(ChkDecode* d, uint32_t* emitted, uint32_t* n_emitted) {

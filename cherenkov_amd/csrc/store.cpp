@@ -206,6 +206,9 @@ double Json::number() const {
 uint64_t Json::u64() const {
     const double v = number();
     if (v < 0 || v != std::floor(v)) fail("expected a non-negative integer");
+    // every integer up to 2^53 is exact in the double it was parsed into;
+    // above that the value is not the manifest's and the cast may overflow
+    if (v > 9007199254740992.0) fail("integer above 2^53");
     return (uint64_t)v;
 }
 const std::string& Json::string() const {
@@ -350,7 +353,12 @@ std::unique_ptr<Store> open_store(const std::string& model_dir) {
     if (X.layers == 0 || X.experts == 0) fail("expert layer dimensions must be nonzero");
     if (X.layer_prefixes.size() != X.layers) fail("expert layer count does not match layer prefixes");
     if (X.group != 64) fail("expert group size must be 64");
+    if (X.record_bytes == 0 || X.record_stride == 0) fail("expert record size must be nonzero");
     if (X.record_bytes > X.record_stride) fail("expert record larger than its stride");
+    uint64_t span = 0;
+    if (__builtin_mul_overflow(X.layers, X.experts, &span) || __builtin_mul_overflow(span, X.record_stride, &span) ||
+        span > (1ull << 62))
+        fail("expert records exceed the addressable file size");
     const ChkConfig& c = S->cfg;
     if (X.experts != c.num_experts || X.inter != c.moe_intermediate_size || X.hidden != c.hidden_size)
         fail("expert layout does not match config.json");
@@ -362,7 +370,8 @@ std::unique_ptr<Store> open_store(const std::string& model_dir) {
                                                     {X.up_b, sc_up},       {X.down_s, sc_down},
                                                     {X.down_b, sc_down}};
     for (const auto& f : fields)
-        if (f.first + f.second > X.record_bytes) fail("expert record field outside the record");
+        if (f.first > X.record_bytes || f.second > X.record_bytes - f.first)
+            fail("expert record field outside the record");
     // NgramLayout, read when the config has a PLE layer; the row group
     // reaches the config (ngram rows are not necessarily groups of 64)
     if (const Json* n = m.get("ngram"); n && c.ple_layer) {

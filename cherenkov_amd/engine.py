@@ -396,6 +396,13 @@ class Decode:
         if rc != 0:
             raise EngineError(eng.L.chk_decode_error().decode())
 
+    def set_eos(self, ids: Sequence[int]) -> None:
+        """The stop ids (the tokenizer's [im_end, endoftext] in the
+        reference); the config's eos_token_id alone until set."""
+        ids = list(ids)
+        if self.eng.L.chk_decode_set_eos(self._h, _u32(ids), len(ids)) != 0:
+            raise EngineError(self.eng.L.chk_decode_error().decode())
+
     def step(self) -> list[int]:
         em = (C.c_uint32 * 4)()
         n = C.c_uint32()

@@ -92,16 +92,22 @@ def phases(wgs_list, mbytes_list, n: int) -> None:
     from .abi import check, lib
 
     us, err = C.c_double(), C.c_uint32()
+
+    def bench(mode, wgs, n_ph, nbytes):
+        check(lib().chk_phase_bench(mode, wgs, n_ph, nbytes, C.byref(us), C.byref(err)))
+        if err.value:  # a barrier that saw wrong data or hit its spin limit measures nothing
+            raise RuntimeError(f"phase mode={mode} wgs={wgs} bytes={nbytes}: {err.value} errors, not reported")
+
     for wgs in wgs_list:
         for mode in (0, 2, 6):
             if mode == 6 and wgs % 8:
                 continue
-            check(lib().chk_phase_bench(mode, wgs, n, 0, C.byref(us), C.byref(err)))
+            bench(mode, wgs, n, 0)
             print(f"phase mode={mode} wgs={wgs} mbytes=0 us_per_phase={us.value:.3f} errors={err.value}  # {PHASE_MODES[mode]}",
                   flush=True)
         for mb in mbytes_list:
             for mode in (1, 3, 4):
-                check(lib().chk_phase_bench(mode, wgs, min(n, 400), int(mb * 1e6), C.byref(us), C.byref(err)))
+                bench(mode, wgs, min(n, 400), int(mb * 1e6))
                 print(f"phase mode={mode} wgs={wgs} mbytes={mb} us_per_phase={us.value:.3f} errors={err.value}  "
                       f"# {PHASE_MODES[mode]}", flush=True)
     for wgs, window, per_wg in ((256, 1 << 22, 1300), (256, 1300, 1300), (64, 1300, 1300), (256, 2048, 2048)):

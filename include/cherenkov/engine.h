@@ -327,6 +327,10 @@ int chk_decode_new_sampling(ChkEngine* e, const ChkSampling* sampling, const uin
                             const float* final_logits, uint32_t next, const uint32_t* drafts, uint32_t n_drafts,
                             uint32_t n_draft, uint32_t limit, uint32_t no_eos, ChkDecode** out);
 void chk_decode_free(ChkDecode* d);
+/* The ids that end generation (Decode.eos = [tok.im_end, tok.endoftext],
+ * src/runner/decode.rs:64): the caller that owns the tokenizer passes them
+ * (1..=16 ids); until then the config's eos_token_id alone. */
+int chk_decode_set_eos(ChkDecode* d, const uint32_t* ids, uint32_t n);
 /* One step: the tokens it emits (1 + accepted drafts, <= 4) go to emitted. */
 int chk_decode_step(ChkDecode* d, uint32_t* emitted, uint32_t* n_emitted);
 /* 0 running, 1 stopped at EOS, 2 length limit reached. */

@@ -49,7 +49,9 @@ int chk_lm_head_argmax(const void* w, const void* s, const void* b, uint32_t out
  * results; the argmax partials live in a 32 KiB file-scope device array of
  * the library (nb <= 4 rows of 1024 workgroup partials), one per device,
  * shared by every call on that device: calls that overlap on one device
- * race. */
+ * race.  It never waits on the stream, so it can be captured into a graph;
+ * the first call on each device (which looks the array's address up) must
+ * be made outside capture and is refused under it. */
 int chk_lm_head_argmax_noalloc(const void* w, const void* s, const void* b, uint32_t out, uint32_t in,
                                const float* x, uint32_t nb, float* logits, uint32_t* ids, void* stream);
 

@@ -146,6 +146,38 @@ def test_runner_accepts_drafts_and_equals_greedy(have_gpu):
     assert acc > 0
 
 
+def test_runner_stops_on_any_eos_id(have_gpu):
+    """The runner stops on any id of its EOS set (the reference's
+    [im_end, endoftext], runner/decode.rs:64,76-80): the stop id is not
+    emitted, a verify step accepts no draft past it, and the output is the
+    greedy tokens before the first stop id, with and without drafts."""
+    cfg = presets.tiny(seed=99)
+    cfg.vocab_size = 16
+    rng = np.random.default_rng(99)
+    prompt = rng.integers(0, cfg.vocab_size, size=8).tolist()
+    eng = Engine(cfg, experts=4, drafts=2, max_t=512)
+    try:
+        nxt, dr = eng.prefill_chunk(prompt)
+        cp = eng.save_prefix()
+        g = Decode(eng, nxt, [], 0, limit=64, no_eos=True).run()
+        first = {}
+        for i, t in enumerate(g):
+            first.setdefault(t, i)
+        (ta, ka), (tb, kb) = sorted(first.items(), key=lambda kv: kv[1])[-2:]
+        assert 1 <= ka < kb, (ka, kb)
+        for ids, stop in (([tb, ta], ka), ([tb], kb)):
+            for drafts in (0, 2):
+                eng.reset_request()
+                eng.restore_prefix(cp)
+                d = Decode(eng, nxt, [dr] if drafts else [], drafts, limit=64, no_eos=False)
+                d.set_eos(ids)
+                out = d.run()
+                assert out == g[:stop], (ids, drafts)
+                assert d.finished == 1
+    finally:
+        eng.close()
+
+
 def test_full_shape_mtp_draft_matches_oracle(have_gpu):
     """The 48-layer preset's MTP head (its own attention + MoE layer, the
     shared LM head) against the oracle's mtp_forward for a few positions."""

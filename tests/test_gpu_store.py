@@ -82,3 +82,19 @@ def test_store_missing_tensor_is_named(have_gpu, tmp_path):
     (path / "manifest.json").write_text(json.dumps(m))
     with pytest.raises(EngineError, match=f'dense tensor "{gone}" not in manifest'):
         Engine.load_store(path, experts=4, drafts=0, max_t=64)
+
+
+def test_store_negative_ngram_offset_is_refused(have_gpu, tmp_path):
+    """A store whose n-gram head offsets hold -1 (an I64 tensor) is refused
+    with the loader's message before any kernel reads the table: the
+    offset is not wrapped into a huge unsigned row."""
+    cfg = presets.with_ple(presets.tiny(mtp=0), layer=2)
+    path = write_store(cfg, tmp_path / "packed")
+    m = json.loads((path / "manifest.json").read_text())
+    ent = [d for d in m["dense"] if d["name"].endswith(".ngram_heads_offsets")]
+    assert len(ent) == 1
+    with open(path / "dense.bin", "r+b") as fh:
+        fh.seek(ent[0]["offset"])
+        fh.write(np.array([-1], np.int64).tobytes())
+    with pytest.raises(EngineError, match="n-gram heads exceed the table"):
+        Engine.load_store(path, experts=4, drafts=0, max_t=64)

@@ -94,6 +94,9 @@ def _edit(path, fname, fn):
     ("model_type", "unsupported model_type llama"),
     ("layer_types", "layer_types length mismatch"),
     ("gate", "output_gate_type must be sigmoid"),
+    ("huge", "integer above 2^53"),
+    ("stride0", "expert record size must be nonzero"),
+    ("field", "expert record field outside the record"),
 ])
 def test_malformed_stores_are_refused(tmp_path, case, msg):
     if not abi.LIB_PATH.exists():
@@ -108,6 +111,10 @@ def test_malformed_stores_are_refused(tmp_path, case, msg):
         "model_type": ("config.json", lambda d: d.update(model_type="llama")),
         "layer_types": ("config.json", lambda d: d["text_config"]["layer_types"].pop()),
         "gate": ("config.json", lambda d: d["text_config"].update(output_gate_type="silu")),
+        "huge": ("manifest.json", lambda d: d["experts"].update(record_stride=2.0 ** 64)),
+        "stride0": ("manifest.json", lambda d: d["experts"].update(record_bytes=0, record_stride=0)),
+        # a field that starts inside the record and runs past its end
+        "field": ("manifest.json", lambda d: d["experts"].update(down_b=d["experts"]["record_bytes"] - 2)),
     }
     fname, fn = edits[case]
     _edit(path, fname, fn)
