@@ -340,10 +340,16 @@ constexpr int HR = 2;
 template <int CPL, int NB>
 __global__ void __launch_bounds__(256) k_hc_down(HcDev w, const float* __restrict__ hyper, float* __restrict__ d,
                                                  float* __restrict__ inj, float* __restrict__ inv_out, uint32_t H,
-                                                 uint32_t hc, float eps) {
+                                                 uint32_t hc, float eps, ActivityArgs act) {
     __shared__ float red[4][HR][NB];
+    __shared__ uint32_t hist[ACT_MAX_E];
     const int lane = threadIdx.x & 63, g = (int)wave_id();
     const uint32_t total = w.down.out + (w.has_inject ? w.inject.out : 0u);
+    const uint32_t groups = (total + HR - 1) / HR;
+    if (blockIdx.x >= groups) {  // the expert-activity workgroups past the rows
+        expert_activity_layer(act, blockIdx.x - groups, threadIdx.x, blockDim.x, hist);
+        return;
+    }
     const uint32_t r0 = blockIdx.x * HR;
     const uint32_t hh = H * hc, nch = H >> 5;  // chunks per stream
     // this stream's inputs first, then every weight load of the HR rows:
@@ -1360,15 +1366,20 @@ void launch_embed(const StepIn* in, uint32_t* tokens, uint32_t* rowpos, const Q4
 }
 
 void launch_hc_down(const HcDev& w, const float* hyper, float* d, float* inj, float* inv, uint32_t H, uint32_t hc,
-                    float eps, int nb, hipStream_t st) {
+                    float eps, int nb, hipStream_t st, const ActivityArgs* act) {
     const uint32_t rows = w.down.out + (w.has_inject ? w.inject.out : 0);
     const uint32_t cpl = (H / 32 + 63) / 64;
     if (hc > 4 || cpl > 2) throw std::runtime_error("hyper-connection read supports hc <= 4 and hidden <= 4096");
-    const uint32_t grid = (rows + HR - 1) / HR;
+    ActivityArgs a{};
+    if (act && act->act && act->layers && act->rows) {
+        if (act->E > ACT_MAX_E) throw std::runtime_error("expert activity counts at most 512 experts per layer");
+        a = *act;
+    }
+    const uint32_t grid = (rows + HR - 1) / HR + a.layers;
     if (cpl <= 1) {
-        CHK_NB_SWITCH(nb, (k_hc_down<1, NB><<<grid, 64 * hc, 0, st>>>(w, hyper, d, inj, inv, H, hc, eps)))
+        CHK_NB_SWITCH(nb, (k_hc_down<1, NB><<<grid, 64 * hc, 0, st>>>(w, hyper, d, inj, inv, H, hc, eps, a)))
     } else {
-        CHK_NB_SWITCH(nb, (k_hc_down<2, NB><<<grid, 64 * hc, 0, st>>>(w, hyper, d, inj, inv, H, hc, eps)))
+        CHK_NB_SWITCH(nb, (k_hc_down<2, NB><<<grid, 64 * hc, 0, st>>>(w, hyper, d, inj, inv, H, hc, eps, a)))
     }
 }
 

@@ -904,8 +904,8 @@ struct ChkEngine {
     }
 
     // ----------------------------------------------------------- blocks
-    void hc_read(const HcDev& w, const float* hyper, float* inj, int nb) {
-        launch_hc_down(w, hyper, s.hc_d, inj, s.hc_inv, D.H, D.hc, D.eps, nb, st);
+    void hc_read(const HcDev& w, const float* hyper, float* inj, int nb, const ActivityArgs* activity = nullptr) {
+        launch_hc_down(w, hyper, s.hc_d, inj, s.hc_inv, D.H, D.hc, D.eps, nb, st, activity);
         launch_hc_up_mix(w, hyper, s.hc_inv, s.hc_d, s.mixed, D.H, D.hc, nb, st);
     }
 
@@ -1242,9 +1242,10 @@ struct ChkEngine {
                 HIPCHK(hipMemcpyAsync(s.trace + (uint64_t)l * MAX_NB * D.hh, s.hyper, (uint64_t)nb * D.hh * 4,
                                       hipMemcpyDeviceToDevice, st));
         }
-        launch_expert_activity(s.route_ids, (uint64_t)MAX_NB * D.topk, c.num_hidden_layers, (uint32_t)nb, D.topk, D.E,
-                               act, 0, st);
-        hc_read(final_mixer, s.hyper, nullptr, nb);
+        // the step's expert activity rides on the final read's launch
+        const ActivityArgs aa{s.route_ids, (uint64_t)MAX_NB * D.topk, c.num_hidden_layers, (uint32_t)nb, D.topk, D.E, 0,
+                              reinterpret_cast<unsigned long long*>(act)};
+        hc_read(final_mixer, s.hyper, nullptr, nb, &aa);
         prof_begin(PROF_LM_HEAD);
         launch_lm_head(lm_head, s.mixed, s.logits, s.pv, s.pi, lm_parts, s.d_out, nb, st);
         prof_end(PROF_LM_HEAD, q4_bytes(lm_head) + (uint64_t)nb * (D.H + D.V) * 4);
@@ -1459,9 +1460,9 @@ void ChkEngine::mtp_rows(int rows, const float* src_hyper, const uint32_t* d_tok
     attention(L, s.mixed, rows, kvs, s.rowpos_aux, s.mtp_hyper, s.inj_a, nullptr);
     hc_read(L.mlp_hc, s.mtp_hyper, s.inj_m, rows);
     moe(L, c.num_hidden_layers, s.mixed, rows, s.mtp_hyper, s.inj_m, nullptr);
-    launch_expert_activity(s.route_ids + (uint64_t)c.num_hidden_layers * MAX_NB * D.topk, 0, 1, (uint32_t)rows,
-                           D.topk, D.E, act, c.num_hidden_layers, st);
-    hc_read(mtp_mixer, s.mtp_hyper, nullptr, rows);
+    const ActivityArgs aa{s.route_ids + (uint64_t)c.num_hidden_layers * MAX_NB * D.topk, 0, 1, (uint32_t)rows, D.topk,
+                          D.E, c.num_hidden_layers, reinterpret_cast<unsigned long long*>(act)};
+    hc_read(mtp_mixer, s.mtp_hyper, nullptr, rows, &aa);
     launch_lm_head(lm_head, s.mixed, s.mtp_logits, s.pv, s.pi, lm_parts, s.mtp_out, rows, st);
 }
 

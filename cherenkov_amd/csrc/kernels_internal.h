@@ -355,8 +355,46 @@ struct StepIn {
 
 void launch_embed(const StepIn* in, uint32_t* tokens, uint32_t* rowpos, const Q4Mat& emb, float* hyper, uint32_t H,
                   uint32_t hc, int nb, hipStream_t st);
+
+// Cumulative routed-expert activity (ExpertCounters::lookup, activity.rs:
+// 31-35) of `layers` record layers from layer0 on: per layer, how many of
+// the step's `rows` rows chose each expert (ids [rows][topk] at
+// ids + l * layer_stride) goes to the expert's selected rows and, when
+// non-zero, one lookup (a hit: every record is resident).  act: [record
+// layers][E][2].  Null `act`: nothing to count.
+struct ActivityArgs {
+    const uint32_t* ids;
+    uint64_t layer_stride;
+    uint32_t layers, rows, topk, E, layer0;
+    unsigned long long* act;
+};
+constexpr uint32_t ACT_MAX_E = 512;
+
+// One workgroup's share: record layer layer0 + l, counted in `hist` (LDS,
+// ACT_MAX_E entries) by threads t < nt.
+CHK_DEV void expert_activity_layer(const ActivityArgs& a, uint32_t l, uint32_t t, uint32_t nt, uint32_t* hist) {
+    for (uint32_t e = t; e < a.E; e += nt) hist[e] = 0;
+    __syncthreads();
+    const uint32_t* li = a.ids + (uint64_t)l * a.layer_stride;
+    for (uint32_t i = t; i < a.rows * a.topk; i += nt) {
+        const uint32_t e = li[i];
+        if (e < a.E) atomicAdd(&hist[e], 1u);
+    }
+    __syncthreads();
+    unsigned long long* c = a.act + (uint64_t)(a.layer0 + l) * a.E * 2;
+    for (uint32_t e = t; e < a.E; e += nt)
+        if (hist[e]) {
+            c[2 * e] += hist[e];
+            c[2 * e + 1] += 1;
+        }
+}
+
+// The hyper-connection read's first half; with `act` set, `act.layers`
+// more workgroups count the step's expert activity alongside it (the
+// step's last read, after every layer's routing), so the count costs no
+// dependent launch of its own.
 void launch_hc_down(const HcDev& w, const float* hyper, float* d, float* inj, float* inv, uint32_t H, uint32_t hc,
-                    float eps, int nb, hipStream_t st);
+                    float eps, int nb, hipStream_t st, const ActivityArgs* act = nullptr);
 void launch_hc_up_mix(const HcDev& w, const float* hyper, const float* inv, const float* d, float* mixed,
                       uint32_t H, uint32_t hc, int nb, hipStream_t st);
 void launch_qmv(const SegArgs& a, int nb, hipStream_t st);
@@ -417,10 +455,6 @@ bool attn_shape_ok(uint32_t nh, uint32_t nkv, uint32_t hd);
 void launch_copy_f32(float* dst, const float* src, uint64_t n, hipStream_t st);
 void launch_kv_fill(const float* k, const float* v, KvDev kv, uint32_t kv_row, uint32_t T, hipStream_t st);
 void launch_zero_f32(float* dst, uint64_t n, hipStream_t st);
-// per-record selected rows and lookups of `layers` record layers from
-// layer0 on (misc.hip); act [record layers][E][2]
-void launch_expert_activity(const uint32_t* ids, uint64_t layer_stride, uint32_t layers, uint32_t rows,
-                            uint32_t topk, uint32_t E, uint64_t* act, uint32_t layer0, hipStream_t st);
 // dependent-FMA clock probe over 65536 threads (out: 65536 floats)
 void launch_clock_probe(float* out, uint32_t iters, hipStream_t st);
 // PLE n-gram block (ple.hip)

@@ -81,40 +81,6 @@ void launch_kv_fill(const float* k, const float* v, KvDev kv, uint32_t kv_row, u
 }
 
 
-// Cumulative routed-expert activity (ExpertCounters::lookup, activity.rs:
-// 31-35): workgroup l takes record layer layer0 + l, counts how many of its
-// `rows` rows chose each expert (ids [rows][topk] at ids + l * layer_stride)
-// and adds that to the expert's selected rows and, when non-zero, one
-// lookup (a hit: every record is resident).  act: [record layers][E][2].
-__global__ void __launch_bounds__(256) k_expert_activity(const uint32_t* __restrict__ ids, uint64_t layer_stride,
-                                                         uint32_t rows, uint32_t topk, uint32_t E,
-                                                         unsigned long long* __restrict__ act, uint32_t layer0) {
-    __shared__ uint32_t hist[512];
-    const uint32_t l = blockIdx.x;
-    for (uint32_t e = threadIdx.x; e < E; e += CHK_WG) hist[e] = 0;
-    __syncthreads();
-    const uint32_t* li = ids + (uint64_t)l * layer_stride;
-    for (uint32_t i = threadIdx.x; i < rows * topk; i += CHK_WG) {
-        const uint32_t e = li[i];
-        if (e < E) atomicAdd(&hist[e], 1u);
-    }
-    __syncthreads();
-    unsigned long long* a = act + (uint64_t)(layer0 + l) * E * 2;
-    for (uint32_t e = threadIdx.x; e < E; e += CHK_WG)
-        if (hist[e]) {
-            a[2 * e] += hist[e];
-            a[2 * e + 1] += 1;
-        }
-}
-
-void launch_expert_activity(const uint32_t* ids, uint64_t layer_stride, uint32_t layers, uint32_t rows,
-                            uint32_t topk, uint32_t E, uint64_t* act, uint32_t layer0, hipStream_t st) {
-    if (E > 512) throw std::runtime_error("expert activity counts at most 512 experts per layer");
-    if (layers && rows)
-        k_expert_activity<<<layers, CHK_WG, 0, st>>>(ids, layer_stride, rows, topk, E,
-                                                     reinterpret_cast<unsigned long long*>(act), layer0);
-}
-
 // Dependent-FMA clock probe (Gpu::throttle_ms, gpu.rs:596-599 over
 // MetalContext::throttle_probe, metal.rs:167-212): 65536 threads each run
 // `iters` pairs of dependent FMAs; a slower run means lower clocks.

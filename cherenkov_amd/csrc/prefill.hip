@@ -1067,7 +1067,7 @@ __global__ void __launch_bounds__(256) k_pf_route(const float* __restrict__ logi
 // topk, E, tr), ntiles[1] of them (the gate/up and down GEMMs tile the same
 // entries differently).
 // With `act`, also the expert activity counters of `layer` (selected rows
-// and selections, as k_expert_activity counts them).  One workgroup.
+// and selections, as the decode step's activity count does).  One workgroup.
 constexpr uint32_t PG_WG = 1024;  // threads of the grouping workgroup (one group each)
 
 __global__ void __launch_bounds__(PG_WG) k_pf_group(const uint32_t* __restrict__ ids, uint32_t T, uint32_t topk,
