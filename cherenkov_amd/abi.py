@@ -203,6 +203,7 @@ SIGNATURES = [
     ("chk_copy_f32", i32, [P, P, u64, P]),
     ("chk_profile_graph", i32, [P, i32, u32, C.POINTER(C.c_double), C.POINTER(u64), C.POINTER(u64)]),
     ("chk_time_decode", i32, [P, u32, u32, C.POINTER(f32), C.POINTER(u32)]),
+    ("chk_time_blocks", i32, [P, C.c_int, u32, C.POINTER(u32), u32, P, u32, C.POINTER(u32), u32, C.POINTER(f32)]),
     ("chk_phase_bench", i32, [i32, u32, u32, u64, C.POINTER(f64), C.POINTER(u32)]),
     # sampling
     ("chk_sampling_validate", i32, [C.POINTER(ChkSampling)]),

@@ -3007,6 +3007,80 @@ int chk_profile_read(ChkEngine* e, double* ms_total, uint64_t* launches, uint64_
     })
 }
 
+// One captured graph runs the block of kind `kind` (2 MoE, 3 DeltaNet, 4
+// attention) once for each of layers[0..n_layers), block i on input rows
+// x + (i % nx) * nb * H, the way the decode step launches it; the graph is
+// replayed `reps` times between two HIP events (after one untimed replay).
+// Attention rows attend at positions pos[0..nb) over the engine's
+// sequence (nb 1) or its two sequence slots (nb 2, chk_kv_fill seq 1);
+// DeltaNet blocks with nb > 1 take the verify form (snapshots).
+int chk_time_blocks(ChkEngine* e, int kind, uint32_t nb, const uint32_t* layers, uint32_t n_layers, const float* x,
+                    uint32_t nx, const uint32_t* pos, uint32_t reps, float* us_per_block) {
+    CHK_TRY({
+        ensure(kind >= 2 && kind <= 4, "block kind must be 2 (MoE), 3 (DeltaNet) or 4 (attention)");
+        ensure(nb >= 1 && nb <= e->trunk_rows, "rows per block must be 1..=" + std::to_string(e->trunk_rows));
+        ensure(n_layers >= 1 && nx >= 1 && reps >= 1, "need layers, inputs and repetitions");
+        ensure(!(kind == 4 && nb > 2), "attention blocks are timed at batch 1 or 2");
+        ensure(!(kind == 4 && nb == 2 && e->kv2.empty()), "second sequence slot not initialised (chk_kv_fill seq 1)");
+        for (uint32_t i = 0; i < n_layers; ++i) {
+            ensure(layers[i] < e->c.num_hidden_layers || (kind == 2 && layers[i] == e->c.num_hidden_layers && e->has_mtp),
+                   "layer out of range");
+            if (kind == 3) ensure(e->layers[layers[i]].linear, "not a DeltaNet layer");
+            if (kind == 4) ensure(!e->layers[layers[i]].linear, "not an attention layer");
+        }
+        if (kind == 4) {
+            for (uint32_t b = 0; b < nb; ++b) ensure(pos[b] < e->max_t, "context capacity exceeded");
+            HIPCHK(hipMemcpyAsync(e->s.rowpos_aux, pos, nb * 4, hipMemcpyHostToDevice, e->st));
+        }
+        float* out = e->s.mix_out;
+        HIPCHK(hipStreamSynchronize(e->st));
+        hipGraph_t g;
+        HIPCHK(hipStreamBeginCapture(e->st, hipStreamCaptureModeThreadLocal));
+        e->capturing = true;
+        try {
+            for (uint32_t i = 0; i < n_layers; ++i) {
+                const LayerDev& L = layers[i] < e->c.num_hidden_layers ? e->layers[layers[i]] : e->mtp_layer;
+                const float* xi = x + (uint64_t)(i % nx) * nb * e->D.H;
+                if (kind == 2) {
+                    e->moe(L, layers[i], xi, (int)nb, nullptr, nullptr, out);
+                } else if (kind == 3) {
+                    e->deltanet(L, xi, (int)nb, nb > 1, nullptr, nullptr, out);
+                } else {
+                    KvDev kvs[MAX_NB];
+                    kvs[0] = e->kv[L.at_idx];
+                    if (nb == 2) kvs[1] = e->kv2[L.at_idx];
+                    e->attention(L, xi, (int)nb, kvs, e->s.rowpos_aux, nullptr, nullptr, out);
+                }
+            }
+        } catch (...) {
+            e->capturing = false;
+            hipGraph_t dead;
+            (void)hipStreamEndCapture(e->st, &dead);
+            throw;
+        }
+        e->capturing = false;
+        HIPCHK(hipStreamEndCapture(e->st, &g));
+        hipGraphExec_t ge;
+        HIPCHK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+        hipEvent_t a, b;
+        HIPCHK(hipEventCreate(&a));
+        HIPCHK(hipEventCreate(&b));
+        HIPCHK(hipGraphLaunch(ge, e->st));  // warm
+        HIPCHK(hipEventRecord(a, e->st));
+        for (uint32_t r = 0; r < reps; ++r) HIPCHK(hipGraphLaunch(ge, e->st));
+        HIPCHK(hipEventRecord(b, e->st));
+        HIPCHK(hipEventSynchronize(b));
+        float ms = 0.0f;
+        HIPCHK(hipEventElapsedTime(&ms, a, b));
+        *us_per_block = ms * 1e3f / (float)((uint64_t)reps * n_layers);
+        (void)hipEventDestroy(a);
+        (void)hipEventDestroy(b);
+        HIPCHK(hipGraphExecDestroy(ge));
+        HIPCHK(hipGraphDestroy(g));
+        HIPCHK(hipGetLastError());
+    })
+}
+
 int chk_time_decode(ChkEngine* e, uint32_t first_token, uint32_t steps, float* ms_per_step, uint32_t* last_token) {
     CHK_TRY({
         ensure(e->pos + steps <= e->max_t, "context capacity exceeded");

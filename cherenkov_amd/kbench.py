@@ -19,6 +19,25 @@ attn: the q8 flash-decode core (chk_attn_decode_q8: partials + combine, no
 projections) at the 80B shape (16 query / 2 kv heads of 256) over a cache
 of each given length: int8 K/V uniform in [-127, 127], fp16 scales
 0.01 +- 0.005, q ~ N(0, 1), `--reps` calls per length.
+
+blocks: configs 2-4 as the decode step runs them (chk_time_blocks: one
+captured graph of blocks over a rotation of layers, each with its own
+weights, replayed between HIP events), on working sets past the 256 MB
+last-level cache:
+
+    python3 -m cherenkov_amd.kbench blocks --config 2 --bits 4 3 2
+    python3 -m cherenkov_amd.kbench blocks --config 3
+    python3 -m cherenkov_amd.kbench blocks --config 4 --ctx 1024 8192 32768
+
+config 2: the MoE block (router, routed top-10 + shared expert, combine)
+of all 48 layers of the 80B shape, 16 inputs rms_norm(N(0, 1)) in
+rotation, >= 1000 blocks; config 3: the DeltaNet layer of all 36 DeltaNet
+layers, the decode step (1 row) and the 3-row verify (snapshots); config
+4: the attention layer (projections, q8 cache, combine, o-projection) of
+the 16 attention layers of a 64-layer model of the same shape, at batch 1
+and 2 (two sequence slots), K/V ~ N(0, 1) through the q8 rule.  Prints a
+JSON line per case with the algorithmic bytes per block (the blueprint's
+per-config accounting) and the achieved rate.
 """
 
 from __future__ import annotations
@@ -72,6 +91,99 @@ def attn(ctxs, reps: int) -> None:
             print(f"attn ctx={T} wall_ms={1e3 * (time.perf_counter() - t0):.3f}", flush=True)
 
 
+def _time_blocks(eng, kind, nb, layers, x, nx, pos, reps):
+    import ctypes as C
+
+    from .abi import check
+
+    us = C.c_float()
+    la = (C.c_uint32 * len(layers))(*layers)
+    pa = (C.c_uint32 * max(1, len(pos)))(*(pos or [0]))
+    check(eng.L.chk_time_blocks(eng.handle, kind, nb, la, len(layers), x.data_ptr(), nx, pa, reps, C.byref(us)))
+    return us.value
+
+
+def _report(case: dict, us: float, nbytes: int, working_set: int) -> None:
+    import json
+
+    gbs = nbytes / (us * 1e-6) / 1e9
+    case.update(us_per_block=round(us, 3), bytes_per_block=nbytes, gb_s=round(gbs, 1),
+                frac_of_8tbs=round(gbs / 8000, 4), rotated_working_set_mb=round(working_set / 1e6, 1))
+    print(json.dumps(case), flush=True)
+
+
+def blocks(config: int, bits_list, ctxs, min_blocks: int) -> None:
+    import torch
+
+    from . import presets
+    from .abi import check
+    from .engine import Engine
+
+    H = 2048
+    g = torch.Generator(device="cuda").manual_seed(7)
+
+    def inputs(nx, nb):
+        x = torch.randn((nx, nb, H), generator=g, device="cuda")
+        return x / torch.sqrt((x * x).mean(-1, keepdim=True) + 1e-6)
+
+    if config == 2:
+        # router 2,097,152 + 10 records + shared expert 1,769,472 + gate
+        # vector + x / out (the shared expert stays Q4)
+        per = {4: 21565440, 3: 17633280, 2: 13701120}
+        for bits in bits_list:
+            eng = Engine(presets.qwen3next_80b_shape(mtp=0), experts=bits, drafts=0, max_t=64)
+            try:
+                layers = list(range(48))
+                x = inputs(16, 1)
+                reps = -(-min_blocks // len(layers))
+                us = _time_blocks(eng, 2, 1, layers, x, 16, [], reps)
+                _report({"config": 2, "block": "moe", "experts_bits": bits, "rows": 1, "blocks_timed": reps * 48}, us,
+                        per[bits], 48 * per[bits])
+            finally:
+                eng.close()
+    elif config == 3:
+        # Q4 projections 18,948,096 + state read + write 4,194,304 + conv
+        # history read + write 196,608 + conv weights 65,536; the 3-row
+        # verify adds two snapshot planes of state and history
+        step = 18948096 + 4194304 + 196608 + 65536
+        eng = Engine(presets.qwen3next_80b_shape(mtp=1), experts=4, drafts=2, max_t=64)
+        try:
+            layers = [l for l in range(48) if (l + 1) % 4]
+            for nb in (1, 3):
+                x = inputs(16, nb)
+                reps = -(-min_blocks // len(layers))
+                us = _time_blocks(eng, 3, nb, layers, x, 16, [], reps)
+                nbytes = step + (nb - 1) * (4194304 // 2 + 196608 // 2)
+                _report({"config": 3, "block": "deltanet", "rows": nb, "form": "decode" if nb == 1 else "verify",
+                         "blocks_timed": reps * len(layers)}, us, nbytes, len(layers) * nbytes)
+        finally:
+            eng.close()
+    else:
+        # q, k, v, o projections 15,335,424 + index projection 737,280 +
+        # (T + 1) x 1,088 q8 K/V bytes per request (the new row appended)
+        cfg = presets.qwen3next_80b_shape(layers=64, mtp=1)
+        eng = Engine(cfg, experts=4, drafts=1, max_t=max(ctxs) + 8)
+        try:
+            layers = [l for l in range(64) if (l + 1) % 4 == 0]
+            kv_row = cfg.num_key_value_heads * cfg.head_dim
+            for T in ctxs:
+                for seq in (0, 1):
+                    for l in layers:
+                        k = torch.randn((T, kv_row), generator=g, device="cuda")
+                        v = torch.randn((T, kv_row), generator=g, device="cuda")
+                        torch.cuda.synchronize()
+                        check(eng.L.chk_kv_fill(eng.handle, l, seq, k.data_ptr(), v.data_ptr(), T))
+                for nb in (1, 2):
+                    x = inputs(16, nb)
+                    reps = -(-min_blocks // len(layers))
+                    us = _time_blocks(eng, 4, nb, layers, x, 16, [T] * nb, reps)
+                    nbytes = 15335424 + 737280 + nb * (T + 1) * 1088
+                    _report({"config": 4, "block": "attention", "ctx": T, "batch": nb,
+                             "blocks_timed": reps * len(layers)}, us, nbytes, len(layers) * nbytes)
+        finally:
+            eng.close()
+
+
 PHASE_MODES = {
     0: "graph of empty dependent launches",
     1: "graph of dependent launches streaming weights",
@@ -119,7 +231,10 @@ def phases(wgs_list, mbytes_list, n: int) -> None:
 
 def main() -> None:
     ap = argparse.ArgumentParser()
-    ap.add_argument("case", choices=["dn_scan", "attn", "phases"])
+    ap.add_argument("case", choices=["dn_scan", "attn", "phases", "blocks"])
+    ap.add_argument("--config", type=int, choices=[2, 3, 4], default=2)
+    ap.add_argument("--bits", type=int, nargs="+", default=[4, 3, 2])
+    ap.add_argument("--min-blocks", type=int, default=1000)
     ap.add_argument("--wgs", type=int, nargs="+", default=[256])
     ap.add_argument("--mbytes", type=float, nargs="+", default=[1.5, 14.0])
     ap.add_argument("--phases", type=int, default=2000)
@@ -131,6 +246,8 @@ def main() -> None:
         dn_scan(args.rows, args.reps)
     elif args.case == "attn":
         attn(args.ctx, args.reps)
+    elif args.case == "blocks":
+        blocks(args.config, args.bits, args.ctx, args.min_blocks)
     else:
         phases(args.wgs, args.mbytes, args.phases)
 

@@ -3,6 +3,7 @@
     python3 -m cherenkov_amd.rocprof_summary steps <kernel_trace.csv> [first last]
     python3 -m cherenkov_amd.rocprof_summary pmc <counter_collection.csv> <kernel-name-prefix>
     python3 -m cherenkov_amd.rocprof_summary mfma <counter_collection.csv> [rows] [name-prefixes]
+    python3 -m cherenkov_amd.rocprof_summary traffic <fetch.csv> <write.csv> <fetch-scale> <write-scale> <name-prefixes>
 
 steps: splits the trace into decode steps (each from a `k_embed` to the
 following `k_argmax_final`) and prints kernels per step, kernel busy time
@@ -12,6 +13,11 @@ first..last (1-based, inclusive; negative counts from the end).
 
 pmc: the average of each counter over the dispatches of one kernel (e.g.
 FETCH_SIZE and WRITE_SIZE in KiB per dispatch).
+
+traffic: from a FETCH_SIZE pass and a WRITE_SIZE pass (KiB per dispatch)
+and the copy-calibration factors that turn each into bytes, per kernel
+and launch grid (kernels whose names start with one of the comma-separated
+prefixes): launches, average KiB of each counter, HBM bytes per launch.
 
 mfma: from a pass of SQ_VALU_MFMA_BUSY_CYCLES, GRBM_GUI_ACTIVE,
 SQ_INSTS_VALU_MFMA_MOPS_F16 and SQ_INSTS_VALU_MFMA_MOPS_BF16, per kernel
@@ -90,6 +96,22 @@ def pmc(path: str, prefix: str) -> None:
         print(f"{prefix} {k}: dispatches {len(v)}, mean {statistics.mean(v):.1f}")
 
 
+def traffic(fetch: str, write: str, fscale: float, wscale: float, prefixes: str) -> None:
+    keep = tuple(x for x in prefixes.split(",") if x)
+    per: dict[tuple, dict[str, list]] = collections.defaultdict(lambda: collections.defaultdict(list))
+    for path, counter in ((fetch, "FETCH_SIZE"), (write, "WRITE_SIZE")):
+        for r in csv.DictReader(open(path)):
+            if r["Counter_Name"] == counter and _name(r).startswith(keep):
+                per[(_name(r), r["Grid_Size"])][counter].append(float(r["Counter_Value"]))
+    print("| kernel | grid (threads) | launches | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM bytes per launch |")
+    print("|---|---:|---:|---:|---:|---:|")
+    for (name, grid), c in sorted(per.items()):
+        f = statistics.mean(c["FETCH_SIZE"]) if c["FETCH_SIZE"] else 0.0
+        w = statistics.mean(c["WRITE_SIZE"]) if c["WRITE_SIZE"] else 0.0
+        n = max(len(c["FETCH_SIZE"]), len(c["WRITE_SIZE"]))
+        print(f"| `{name}` | {grid} | {n} | {f:,.1f} | {w:,.1f} | {1024 * (f * fscale + w * wscale):,.0f} |")
+
+
 def mfma(path: str, rows: int = 12, prefixes: str = "") -> None:
     keep = tuple(x for x in prefixes.split(",") if x)
     disp: dict[str, dict] = {}
@@ -121,6 +143,8 @@ def main() -> None:
         steps(sys.argv[2])
     elif len(sys.argv) >= 4 and sys.argv[1] == "pmc":
         pmc(sys.argv[2], sys.argv[3])
+    elif len(sys.argv) >= 7 and sys.argv[1] == "traffic":
+        traffic(sys.argv[2], sys.argv[3], float(sys.argv[4]), float(sys.argv[5]), sys.argv[6])
     elif len(sys.argv) >= 3 and sys.argv[1] == "mfma":
         mfma(sys.argv[2], int(sys.argv[3]) if len(sys.argv) >= 4 else 12, sys.argv[4] if len(sys.argv) >= 5 else "")
     else:

@@ -197,6 +197,18 @@ int chk_profile_graph(ChkEngine* e, int kind, uint32_t reps, double* ms_total, u
 int chk_phase_bench(int mode, uint32_t wgs, uint32_t phases, uint64_t bytes_per_phase, double* us_per_phase,
                     uint32_t* errors);
 
+/* Time blocks as the decode step runs them (profiling support, no
+ * reference counterpart): one captured graph runs the block of `kind`
+ * (2 MoE, 3 DeltaNet, 4 attention) once per layer of layers[0..n_layers),
+ * block i on input rows x + (i % nx) * nb * H (device f32), and is
+ * replayed `reps` times between HIP events; us_per_block = elapsed /
+ * (reps * n_layers).  Attention rows sit at positions pos[0..nb) of the
+ * engine's sequence (nb 1) or of its two sequence slots (nb 2); DeltaNet
+ * blocks with nb > 1 take the verify form.  The blocks advance recurrent
+ * state and write K/V at those positions, like the block entry points. */
+int chk_time_blocks(ChkEngine* e, int kind, uint32_t nb, const uint32_t* layers, uint32_t n_layers, const float* x,
+                    uint32_t nx, const uint32_t* pos, uint32_t reps, float* us_per_block);
+
 /* Time the decode step on the engine's stream: runs `steps` step_rows(1)
  * + commit pairs, returns milliseconds per step (HIP events). */
 int chk_time_decode(ChkEngine* e, uint32_t first_token, uint32_t steps, float* ms_per_step, uint32_t* last_token);
