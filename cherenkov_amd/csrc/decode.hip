@@ -1050,24 +1050,42 @@ __global__ void __launch_bounds__(GU_WG) k_moe_gate_up(MoeArgs a) {
     XqStaged<2, GU_WG> xs;
     const bool staged = xs.fits(a.H, a.nb);
     if (staged) xs.load(a.x, a.H, a.H, a.nb);
+    // mixed stores: this lane's 8 experts' kinds (the lanes' expert split of
+    // route_row), in flight with the logits
+    uint32_t kw0 = 0, kw1 = 0;
+    if (BITS != 4 && routed && a.kinds) {
+        const uint2 kv = *reinterpret_cast<const uint2*>(a.kinds + (size_t)a.record_layer * a.E +
+                                                         min((uint32_t)lane * 8u, a.E - 8u));
+        kw0 = kv.x;
+        kw1 = kv.y;
+    }
     uint32_t my_id = 0;
     float my_p = 0.0f;
     if (routed)
         route_row(a.logits + (size_t)b * a.E, a.E, publish ? a.topk : slot + 1, lane,
                   publish && a.probs ? a.probs + (size_t)b * a.E : nullptr, my_id, my_p);
     const uint32_t e = routed ? min((uint32_t)__builtin_amdgcn_readlane((int)my_id, (int)slot), a.X.experts - 1) : 0u;
+    // a low-bit launch decodes routed records of kind != 0 at X.bits and the
+    // rest from their 4-bit copies (the kind byte of expert e: lane e / 8)
+    bool low = BITS != 4 && routed;
+    if (BITS != 4 && routed && a.kinds) {
+        const uint32_t kw = (uint32_t)__builtin_amdgcn_readlane((int)((e & 4u) ? kw1 : kw0), (int)(e >> 3));
+        low = ((kw >> (8u * (e & 3u))) & 0xffu) != 0u;
+    }
     const uint8_t* rec = a.X.base + ((size_t)a.record_layer * a.X.experts + e) * a.X.stride;
     float g[R][1], u[R][1];
     // Q4 routed and shared rows share one straight path (only the matrices
     // differ); low-bit routed rows take their own fragments.  The prep sits
     // outside both so every wave reaches its barrier at the same point.
-    const bool q4path = BITS == 4 || !routed;
+    const bool q4path = BITS == 4 || !low;
     Q4Frag<64, 1, R> fg, fu;
     ExpFrag<64, 1, R, BITS> lg, lu;
     if (q4path) {
         Q4Mat mg = a.sh_gate, mu = a.sh_up;
-        if (BITS == 4 && routed) {
-            const ExpMat eg = expert_mat(a.X, rec, 0, a.I, a.H), eu = expert_mat(a.X, rec, 1, a.I, a.H);
+        if (routed) {
+            const ExpertsDev& XQ = BITS == 4 ? a.X : a.X4;
+            const uint8_t* rq = XQ.base + ((size_t)a.record_layer * XQ.experts + e) * XQ.stride;
+            const ExpMat eg = expert_mat(XQ, rq, 0, a.I, a.H), eu = expert_mat(XQ, rq, 1, a.I, a.H);
             mg = Q4Mat{(const uint32_t*)eg.w, eg.s, eg.b, a.I, a.H};
             mu = Q4Mat{(const uint32_t*)eu.w, eu.s, eu.b, a.I, a.H};
         }
@@ -1135,6 +1153,14 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a) {
         rw[b] = a.w[bb * a.topk + rl];
         sgv[b] = a.sg[bb];
     }
+    // mixed stores: lane l holds the kinds of experts 8l..8l+7
+    uint32_t kw0 = 0, kw1 = 0;
+    if (BITS != 4 && a.kinds) {
+        const uint2 kv = *reinterpret_cast<const uint2*>(a.kinds + (size_t)a.record_layer * a.E +
+                                                         min((uint32_t)lane * 8u, a.E - 8u));
+        kw0 = kv.x;
+        kw1 = kv.y;
+    }
     const uint32_t gi0 = global_wave();
     // the first row's activation chunks do not depend on the routing either
     XqFrag<1, 1> xq0[PASSES];
@@ -1181,6 +1207,7 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a) {
             ExpFrag<LPR, 1, R, BITS> fl[PASSES];
             XqFrag<1, 1> xq[PASSES];
             float wgt[PASSES];
+            bool low[PASSES];  // a routed slot decoded at X.bits (its kind != 0)
 #pragma unroll
             for (int pass = 0; pass < PASSES; ++pass) {
                 const uint32_t slot = grp + pass * G;
@@ -1188,18 +1215,24 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a) {
                 const uint32_t e = __shfl(my_id, sl < a.topk ? sl : 0, 64);
                 wgt[pass] = __shfl(my_w, sl, 64);
                 if (slot >= slots) wgt[pass] = 0.0f;
+                low[pass] = BITS != 4 && sl < a.topk;
+                if (BITS != 4 && a.kinds) {
+                    const uint32_t k0 = __shfl(kw0, (int)(e >> 3), 64), k1 = __shfl(kw1, (int)(e >> 3), 64);
+                    low[pass] = low[pass] && ((((e & 4u) ? k1 : k0) >> (8u * (e & 3u))) & 0xffu) != 0u;
+                }
                 const uint8_t* rec = a.X.base + ((size_t)a.record_layer * a.X.experts + e) * a.X.stride;
-                if (BITS == 4) {
+                if (BITS != 4 && low[pass]) {
+                    fl[pass].issue(expert_mat(a.X, rec, 2, a.H, a.I), rows, lir);
+                } else {
+                    // the shared expert, or a routed record's 4-bit copy
                     Q4Mat mm = a.sh_down;
                     if (sl < a.topk) {
-                        const ExpMat em = expert_mat(a.X, rec, 2, a.H, a.I);
+                        const ExpertsDev& XQ = BITS == 4 ? a.X : a.X4;
+                        const uint8_t* rq = XQ.base + ((size_t)a.record_layer * XQ.experts + e) * XQ.stride;
+                        const ExpMat em = expert_mat(XQ, rq, 2, a.H, a.I);
                         mm = Q4Mat{(const uint32_t*)em.w, em.s, em.b, a.H, a.I};
                     }
                     fq[pass].issue(mm, rows, lir);
-                } else if (sl < a.topk) {
-                    fl[pass].issue(expert_mat(a.X, rec, 2, a.H, a.I), rows, lir);
-                } else {
-                    fq[pass].issue(a.sh_down, rows, lir);
                 }
                 if (gi == gi0 && b == 0) xq[pass] = xq0[pass];
                 else xq[pass].template read<LPR>(a.act_xq + ((size_t)b * slots + sl) * nch, nch, lir);
@@ -1209,11 +1242,9 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a) {
             for (int i = 0; i < R; ++i) tot[i] = 0.0f;
 #pragma unroll
             for (int pass = 0; pass < PASSES; ++pass) {
-                const uint32_t slot = grp + pass * G;
-                const uint32_t sl = slot < slots ? slot : slots - 1;
                 float acc[R][1];
                 if constexpr (BITS != 4) {
-                    if (sl < a.topk) fl[pass].template dot<1>(xq[pass], acc);
+                    if (low[pass]) fl[pass].template dot<1>(xq[pass], acc);
                     else fq[pass].template dot<1>(xq[pass], acc);
                 } else {
                     fq[pass].template dot<1>(xq[pass], acc);

@@ -185,6 +185,11 @@ struct ChkEngine {
     RecordLayout rl4{}, rllo{};
     uint8_t* experts4 = nullptr;
     uint8_t* experts_lo = nullptr;
+    // per-record precision (residency.rs:290-310): kind of record rid (0
+    // 4-bit, else the low-bit store's kind), on the device for the expert
+    // kernels and in pinned host memory, from which each change is copied
+    uint8_t* rec_kind = nullptr;
+    uint8_t* rec_kind_host = nullptr;
     uint32_t record_layers = 0;
     uint64_t state_bytes = 0, kv_bytes = 0, scratch_bytes = 0;
     Q4Mat embed{}, lm_head{};
@@ -338,6 +343,7 @@ struct ChkEngine {
         if (dense_fd >= 0) close(dense_fd);
         if (experts_fd >= 0) close(experts_fd);
         if (ngram_fd >= 0) close(ngram_fd);
+        if (rec_kind_host) hipHostFree(rec_kind_host);
         if (s.h_in) hipHostFree(s.h_in);
         if (s.h_out) hipHostFree(s.h_out);
         for (void* p : allocs) hipFree(p);
@@ -606,12 +612,16 @@ struct ChkEngine {
         }
     }
 
-    ExpertsDev experts_dev() const {
+    // the store the expert kernels decode at its precision (bits 4: the
+    // 4-bit store; 3 / 2: the low-bit store, whose records of kind 0 come
+    // from the 4-bit one)
+    ExpertsDev experts_dev(bool q4 = false) const {
         ExpertsDev X{};
-        const RecordLayout& R = o.experts == 4 ? rl4 : rllo;
-        X.base = o.experts == 4 ? experts4 : experts_lo;
+        q4 = q4 || o.experts == 4;
+        const RecordLayout& R = q4 ? rl4 : rllo;
+        X.base = q4 ? experts4 : experts_lo;
         X.stride = R.stride;
-        X.bits = o.experts;
+        X.bits = q4 ? 4 : o.experts;
         X.experts = D.E;
         X.gate_w = R.gate_w; X.up_w = R.up_w; X.down_w = R.down_w;
         X.gate_s = R.gate_s; X.gate_b = R.gate_b; X.up_s = R.up_s; X.up_b = R.up_b;
@@ -757,6 +767,13 @@ struct ChkEngine {
             experts_lo = dalloc<uint8_t>(n_rec * rllo.stride);
             HIPCHK(hipMemsetAsync(experts_lo, 0, n_rec * rllo.stride, st));
             repack_lowbit(experts4, rl4, experts_lo, rllo, (uint32_t)n_rec, (uint64_t)D.I * D.H, st);
+            // every record starts at the low-bit store's kind (8 bytes of
+            // slack: the kernels read a layer's kinds 8 at a time)
+            const uint8_t kind0 = o.experts == 3 ? 1 : 2;
+            rec_kind = dalloc<uint8_t>(n_rec + 8);
+            HIPCHK(hipHostMalloc((void**)&rec_kind_host, n_rec + 8, hipHostMallocDefault));
+            memset(rec_kind_host, kind0, n_rec + 8);
+            HIPCHK(hipMemcpyAsync(rec_kind, rec_kind_host, n_rec + 8, hipMemcpyHostToDevice, st));
         }
 
         // recurrent state, snapshots, KV
@@ -1045,6 +1062,8 @@ struct ChkEngine {
                      float* raw_out) {
         MoeArgs m{};
         m.X = experts_dev();
+        m.X4 = experts_dev(true);
+        m.kinds = o.experts == 4 ? nullptr : rec_kind;
         m.record_layer = L.moe.record_layer;
         m.sh_gate = L.moe.sh_gate;
         m.sh_up = L.moe.sh_up;
@@ -2023,6 +2042,8 @@ void ChkEngine::pf_moe(const LayerDev& L, uint32_t T) {
     gu.cap = pf.cap;
     gu.div = slots;
     gu.X = experts_dev();
+    gu.X4 = experts_dev(true);
+    gu.kinds = o.experts == 4 ? nullptr : rec_kind;
     gu.record_layer = L.moe.record_layer;
     PfGemmArgs dn = gu;
     dn.seg[0] = PfSeg{L.moe.sh_down, pf.yd, D.H, 0};
@@ -2476,32 +2497,48 @@ int chk_pool_finish(ChkEngine* e, const uint32_t* rids, uint32_t n) {
     })
 }
 
+// Kind of record rid: 0 (4-bit) unless a low-bit store is attached and the
+// record uses it (Pool::kind, residency.rs:290-296).
+static uint32_t pool_rec_kind(const ChkEngine* e, uint32_t rid) {
+    return e->rec_kind_host ? e->rec_kind_host[rid] : 0u;
+}
+
+// Pool::addr (residency.rs:437-451): the record's device address in the
+// store of its kind, tagged bit 63 for 3-bit and bit 62 for 2-bit.
 uint64_t chk_pool_addr(const ChkEngine* e, uint32_t rid) {
     if (rid >= pool_records(e)) return 0;
-    if (e->o.experts == 4) return (uint64_t)(uintptr_t)e->experts4 + (uint64_t)rid * e->rl4.stride;
-    uint64_t tag = e->o.experts == 3 ? (1ull << 63) : (1ull << 62);
+    const uint32_t k = pool_rec_kind(e, rid);
+    if (k == 0) return (uint64_t)(uintptr_t)e->experts4 + (uint64_t)rid * e->rl4.stride;
+    const uint64_t tag = k == 1 ? (1ull << 63) : (1ull << 62);
     return ((uint64_t)(uintptr_t)e->experts_lo + (uint64_t)rid * e->rllo.stride) | tag;
 }
 
 int chk_pool_buf(const ChkEngine* e, uint32_t rid, void** base, uint64_t* offset) {
     CHK_TRY({
         ensure(rid < pool_records(e), "record id out of range");
-        const bool q4 = e->o.experts == 4;
+        const bool q4 = pool_rec_kind(e, rid) == 0;
         *base = q4 ? (void*)e->experts4 : (void*)e->experts_lo;
         *offset = (uint64_t)rid * (q4 ? e->rl4.stride : e->rllo.stride);
     })
 }
 
 uint32_t chk_pool_kind(const ChkEngine* e, uint32_t rid) {
-    return rid < pool_records(e) ? pool_store_kind(e) : 0u;
+    return rid < pool_records(e) ? pool_rec_kind(e, rid) : 0u;
 }
 
+// Pool::set_kind (residency.rs:298-306): the store a record is decoded
+// from, 0 (4-bit) or the attached low-bit store's kind; every record is
+// resident, so any record may change.  The change reaches the device on
+// the engine's stream ahead of the next step or prefill.
 int chk_pool_set_kind(ChkEngine* e, uint32_t rid, uint32_t kind) {
     CHK_TRY({
         ensure(rid < pool_records(e), "record id out of range");
         ensure(kind <= 2, "kind must be 0 (4-bit), 1 (3-bit) or 2 (2-bit)");
-        ensure(kind == pool_store_kind(e),
-               "every record of this store has the store's precision (per-record precision is not supported)");
+        if (kind == 0 && !e->rec_kind_host) return 0;  // 4-bit store only: every record is kind 0
+        ensure(e->rec_kind_host && (kind == 0 || kind == pool_store_kind(e)), "low-bit store of that kind not attached");
+        if (e->rec_kind_host[rid] == kind) return 0;
+        e->rec_kind_host[rid] = (uint8_t)kind;
+        HIPCHK(hipMemcpyAsync(e->rec_kind + rid, e->rec_kind_host + rid, 1, hipMemcpyHostToDevice, e->st));
     })
 }
 
@@ -2518,9 +2555,11 @@ int chk_pool_store(const ChkEngine* e, uint32_t kind, void** base, uint64_t* str
     })
 }
 
+// The bytes of every record in the store of its kind.
 uint64_t chk_pool_bytes(const ChkEngine* e) {
-    uint64_t nrec = pool_records(e);
-    return nrec * (e->o.experts == 4 ? e->rl4.stride : e->rllo.stride);
+    uint64_t n = 0;
+    for (uint32_t rid = 0; rid < pool_records(e); ++rid) n += pool_rec_kind(e, rid) ? e->rllo.stride : e->rl4.stride;
+    return n;
 }
 
 // Gpu::throttle_ms (gpu.rs:596-599): the wall time in ms of the second of

@@ -81,8 +81,15 @@ struct RouterArgs {
     uint32_t E, H;
 };
 
+// Routed-expert records of mixed precision (residency.rs:290-310, 437-451):
+// X is the store the launch decodes at X.bits; with a low-bit X, kinds
+// [record layers][experts] (0 = 4-bit, else X's low-bit kind) sends each
+// record with kind 0 to its 4-bit copy in X4 instead.  kinds is null for
+// 4-bit launches.
 struct MoeArgs {
     ExpertsDev X;
+    ExpertsDev X4;
+    const uint8_t* kinds;
     uint32_t record_layer;
     Q4Mat sh_gate, sh_up, sh_down;
     const float* x;        // [nb][H]
@@ -308,6 +315,8 @@ struct PfGemmArgs {
     const uint32_t* ntiles;
     uint32_t cap, div;
     ExpertsDev X;            // routed-expert records for groups < X.experts
+    ExpertsDev X4;           // their 4-bit copies, for records whose kind is 0
+    const uint8_t* kinds;    // [record layers][experts] with a low-bit X (else null)
     uint32_t record_layer;
     const uint32_t* wbase;   // set by the launcher (dense matrices' common bases)
     const uint16_t* sbase;

@@ -321,9 +321,13 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
     // segment matrix).  Local row lr = ((w NMAT + q) NJ + j) 16 + col of the
     // workgroup's 256 is matrix q, tile j of wave w.
     const bool expert = a.X.base && grp < a.X.experts;
-    const bool lowbit = BITS != 4 && expert;
+    // a low-bit launch decodes the group's record at X.bits unless its kind
+    // is 0, then from its 4-bit copy in X4 (workgroup-uniform)
+    bool lowbit = BITS != 4 && expert;
+    if (BITS != 4 && expert && a.kinds) lowbit = a.kinds[(size_t)a.record_layer * a.X.experts + grp] != 0;
+    const ExpertsDev& XR = (BITS == 4 || lowbit) ? a.X : a.X4;
     constexpr uint32_t CW = BITS == 2 ? 2 : 3;  // words per 32-code low-bit chunk
-    const uint8_t* rec = a.X.base + ((size_t)a.record_layer * a.X.experts + grp) * a.X.stride;
+    const uint8_t* rec = XR.base + ((size_t)a.record_layer * XR.experts + grp) * XR.stride;
     const uint32_t* wb = expert ? reinterpret_cast<const uint32_t*>(rec) : a.wbase;
     const uint16_t* sbase = expert ? reinterpret_cast<const uint16_t*>(rec) : a.sbase;
     auto out_of = [&](uint32_t wn_, int j, uint32_t col_) __attribute__((always_inline)) -> uint32_t {
@@ -337,10 +341,10 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
     auto offs = [&](int q, uint32_t r, uint32_t& ow, uint32_t& os, uint32_t& ob) __attribute__((always_inline)) {
         if (expert) {
             const int part = EPI == PE_SILU_MUL ? q : 2;
-            const uint64_t w0 = part == 0 ? a.X.gate_w : part == 1 ? a.X.up_w : a.X.down_w;
-            const uint64_t s0 = part == 0 ? a.X.gate_s : part == 1 ? a.X.up_s : a.X.down_s;
-            const uint64_t b0 = part == 0 ? a.X.gate_b : part == 1 ? a.X.up_b : a.X.down_b;
-            ow = (uint32_t)(w0 / 4) + r * (BITS == 4 ? KB : (K >> 5) * CW);
+            const uint64_t w0 = part == 0 ? XR.gate_w : part == 1 ? XR.up_w : XR.down_w;
+            const uint64_t s0 = part == 0 ? XR.gate_s : part == 1 ? XR.up_s : XR.down_s;
+            const uint64_t b0 = part == 0 ? XR.gate_b : part == 1 ? XR.up_b : XR.down_b;
+            ow = (uint32_t)(w0 / 4) + r * (lowbit ? (K >> 5) * CW : KB);
             os = (uint32_t)(s0 / 2) + r * G;
             ob = (uint32_t)(b0 / 2) + r * G;
             return;

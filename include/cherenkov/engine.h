@@ -176,12 +176,17 @@ uint32_t chk_prefix_tokens(const ChkPrefixState* state, uint32_t* out, uint32_t 
 /* Expert-cache interface (residency::Pool, gpu/residency.rs:255-460) over
  * the all-resident HBM store: every record is a member from load on, so
  * acquire(rids, step) never needs a read (n_need = 0), plan_reads plans no
- * read (warm = n) and finish waits for nothing; addr(rid) = base + rid *
- * stride with the kind tag in bits 62-63 (1 = Q3, 2 = Q2;
- * residency.rs:437-451); buf(rid) = (store base, byte offset); every record
- * has the store's kind (set_kind accepts only that kind); chk_pool_store
- * gives the device store behind a kind (store_file, residency.rs:300-311;
- * the low-bit store is attached at load time by ChkOptions.experts). */
+ * read (warm = n) and finish waits for nothing.  Each record has a kind
+ * (Pool::kind / set_kind, residency.rs:290-306): 0 (4-bit) or, when a
+ * low-bit store is attached (ChkOptions.experts 3 or 2, which is also every
+ * record's starting kind), that store's kind (1 = Q3, 2 = Q2); set_kind
+ * switches one record between the two, refuses any other kind, and the
+ * next step or prefill decodes the record from the store of its kind (one
+ * launch mixes both).  addr(rid) = that store's base + rid * stride with
+ * the kind tag in bits 62-63 (residency.rs:437-451); buf(rid) = (store
+ * base, byte offset); bytes = the records' bytes in the stores of their
+ * kinds; chk_pool_store gives the device store behind a kind (store_file,
+ * residency.rs:300-311). */
 uint32_t chk_pool_slots(const ChkEngine* e);
 uint32_t chk_pool_budget(const ChkEngine* e);
 uint32_t chk_pool_resident(const ChkEngine* e);

@@ -383,6 +383,10 @@ struct OrcState {
 struct OrcModel {
     ChkConfig c{};
     uint32_t expert_bits = 4;
+    // per-record precision of the routed experts ([record layer][expert];
+    // 0 = expert_bits), the mixed stores of Pool::set_kind
+    // (src/qwen4_exp/gpu/residency.rs:298-306)
+    std::vector<uint8_t> rec_bits;
     QStore embed, lm_head;
     std::vector<LayerW> layers;
     HcW final_mixer;
@@ -800,8 +804,9 @@ std::vector<float> moe(OrcModel& m, const MoeW& w, const float* x, uint32_t* top
         if (top_out) top_out[i] = ei;
         if (w_out) w_out[i] = weight;
         const uint8_t* rec = m.record(w.record_layer, ei);
-        std::vector<float> y = mlp(m.expert_view(rec, 0), m.expert_view(rec, 1), m.expert_view(rec, 2), x,
-                                   m.expert_bits);
+        const size_t ri = (size_t)w.record_layer * E + ei;
+        const uint32_t bits = ri < m.rec_bits.size() && m.rec_bits[ri] ? m.rec_bits[ri] : m.expert_bits;
+        std::vector<float> y = mlp(m.expert_view(rec, 0), m.expert_view(rec, 1), m.expert_view(rec, 2), x, bits);
         for (size_t o = 0; o < h; ++o) out[o] += weight * y[o];
     }
     std::vector<float> shared = mlp(w.sh_gate.view, w.sh_up.view, w.sh_down.view, x, 4);
@@ -1433,6 +1438,20 @@ static LayerW* layer_of(OrcModel* m, uint32_t layer) {
 }
 
 // The MoE block on an already-normalised input x[h]; reports routing.
+// The precision of one routed-expert record (4, 3 or 2 bits; 0 restores
+// the model's expert_bits).
+int orc_set_record_bits(void* mp, uint32_t record_layer, uint32_t e, uint32_t bits) {
+    OrcModel* m = (OrcModel*)mp;
+    const size_t E = m->c.num_experts, n = (m->c.num_hidden_layers + 1) * E;
+    if (record_layer > m->c.num_hidden_layers || e >= E || (bits && bits != 2 && bits != 3 && bits != 4)) {
+        g_err = "record or bits out of range";
+        return -1;
+    }
+    if (m->rec_bits.size() != n) m->rec_bits.assign(n, 0);
+    m->rec_bits[(size_t)record_layer * E + e] = (uint8_t)bits;
+    return 0;
+}
+
 int orc_moe(void* mp, uint32_t layer, const float* x, float* out, uint32_t* top_idx, float* top_w, float* probs) {
     OrcModel* m = (OrcModel*)mp;
     LayerW* L = layer_of(m, layer);

@@ -29,6 +29,7 @@ _SIGS = [
     ("orc_state_last_hyper", i32, [P, P, C.c_size_t]),
     ("orc_mtp_forward", i32, [P, P, u32, P, u32, i32, P, P]),
     ("orc_moe", i32, [P, u32, P, P, P, P, P]),
+    ("orc_set_record_bits", i32, [P, u32, u32, u32]),
     ("orc_gated_residual", i32, [P, u32, u32, P, P, P]),
     ("orc_deltanet", i32, [P, P, u32, P, P]),
     ("orc_delta_state", i32, [P, P, u32, P, P]),
@@ -117,6 +118,10 @@ class OracleModel:
 
     def new_state(self) -> "OracleState":
         return OracleState(self)
+
+    def set_record_bits(self, record_layer: int, expert: int, bits: int) -> None:
+        """One routed-expert record's precision (4, 3 or 2; 0: the model's)."""
+        _check(self.L.orc_set_record_bits(self.h, record_layer, expert, bits))
 
     def moe(self, layer: int, x: np.ndarray):
         c = self.cfg

@@ -249,7 +249,18 @@ def test_expert_pool_interface(have_gpu, bits):
             layer, e = divmod(rid, E)
             np.testing.assert_array_equal(got, eng.expert_record(layer, e, bits))
         eng.pool_set_kind(rids[0], kind)
-        with pytest.raises(EngineError, match="precision"):
-            eng.pool_set_kind(rids[0], (kind + 1) % 3)
+        other = {0: 1, 1: 2, 2: 1}[kind]
+        with pytest.raises(EngineError, match="low-bit store of that kind not attached"):
+            eng.pool_set_kind(rids[0], other)
+        if kind:
+            # a record switched to 4-bit moves to the 4-bit store, untagged
+            b4, s4 = eng.pool_store(0)
+            eng.pool_set_kind(rids[1], 0)
+            assert eng.pool_kind(rids[1]) == 0
+            assert eng.pool_addr(rids[1]) == b4 + rids[1] * s4
+            assert eng.pool_buf(rids[1]) == (b4, rids[1] * s4)
+            assert eng.L.chk_pool_bytes(eng.handle) == (n_rec - 1) * stride + s4
+            eng.pool_set_kind(rids[1], kind)
+            assert eng.pool_addr(rids[1]) == (base + rids[1] * stride) | tag
     finally:
         eng.close()

@@ -402,3 +402,35 @@ def test_qsa_pick_random_with_duplicates(seed):
     scores = rng.choice(np.float32([0.0, 0.25, 0.5, 1.5, 2.0]), size=n) + (rng.random(n) < 0.3) * rng.random(n).astype(np.float32)
     got = O.qsa_pick(scores.astype(np.float32), t_len, k, ratio)
     assert got.tolist() == _qsa_expect(scores.astype(np.float32), t_len, k, ratio)
+
+
+@pytest.mark.parametrize("base,override", [(2, 4), (4, 3), (4, 2)])
+def test_per_record_bits_select_each_records_reconstruction(base, override):
+    """The oracle's per-record precision (Pool::set_kind, residency.rs:
+    298-306): a model of expert_bits `base` whose every record is set to
+    `override` gives exactly the MoE output of a model of expert_bits
+    `override`; one chosen record set alone changes the output, and 0
+    restores the model's own precision exactly."""
+    from cherenkov_amd import presets
+
+    cfg = presets.tiny(mtp=0)
+    E, k = cfg.num_experts, cfg.num_experts_per_tok
+    x = np.random.default_rng(5).normal(0, 1, cfg.hidden_size).astype(np.float32)
+    x /= np.sqrt(np.mean(x * x))
+    m = O.OracleModel(cfg, expert_bits=base)
+    ref_o = O.OracleModel(cfg, expert_bits=override)
+    out_base, ids, w, _ = m.moe(1, x)
+    out_ref, ids_r, _, _ = ref_o.moe(1, x)
+    assert list(ids) == list(ids_r)
+    # one chosen expert switched: only its term changes
+    m.set_record_bits(1, int(ids[0]), override)
+    one, _, _, _ = m.moe(1, x)
+    assert not np.array_equal(one, out_base)
+    for e in range(E):
+        m.set_record_bits(1, e, override)
+    np.testing.assert_array_equal(m.moe(1, x)[0], out_ref)
+    # 0 restores the model's own precision
+    for e in range(E):
+        m.set_record_bits(1, e, 0)
+    np.testing.assert_array_equal(m.moe(1, x)[0], out_base)
+    assert len(ids) == k
