@@ -1029,7 +1029,8 @@ CHK_DEV void publish_routing(const MoeArgs& a, uint32_t b, int lane, uint32_t my
 constexpr uint32_t GU_WAVES = CHK_GU_WAVES;
 constexpr uint32_t GU_WG = 64 * GU_WAVES;
 
-template <int R, int BITS>
+// CPL: input chunks per lane (hidden sizes up to 2048 CPL).
+template <int R, int BITS, int CPL>
 __global__ void __launch_bounds__(GU_WG) k_moe_gate_up(MoeArgs a) {
     static_assert(R * GU_WAVES == 32, "a workgroup covers one 32-row chunk");
     __shared__ float act_s[32];
@@ -1078,8 +1079,8 @@ __global__ void __launch_bounds__(GU_WG) k_moe_gate_up(MoeArgs a) {
     // differ); low-bit routed rows take their own fragments.  The prep sits
     // outside both so every wave reaches its barrier at the same point.
     const bool q4path = BITS == 4 || !low;
-    Q4Frag<64, 1, R> fg, fu;
-    ExpFrag<64, 1, R, BITS> lg, lu;
+    Q4Frag<64, CPL, R> fg, fu;
+    ExpFrag<64, CPL, R, BITS> lg, lu;
     if (q4path) {
         Q4Mat mg = a.sh_gate, mu = a.sh_up;
         if (routed) {
@@ -1098,7 +1099,7 @@ __global__ void __launch_bounds__(GU_WG) k_moe_gate_up(MoeArgs a) {
     if (publish) publish_routing(a, b, lane, my_id, my_p);
     if (staged) xs.store(a.H, a.nb, xq_lds, XqIdentity{});
     else xq_prep<GU_WG>(a.x, a.H, a.H, a.nb, xq_lds, XqIdentity{});
-    XqFrag<1, 1> xq;
+    XqFrag<1, CPL> xq;
     xq.template read<64>(xq_lds + b * nch, nch, lane);
     if (q4path) {
         fg.template dot<1>(xq, g);
@@ -1270,7 +1271,8 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a) {
 // ------------------------------------------------------- LM head + argmax
 // logits = W_lm mixed; greedy argmax with the lowest index winning ties
 // (argmax_partial/argmax_final, kernels/common/sampling.metal:10-84).
-template <int R, int NB>
+// CPL: input chunks per lane (inputs up to 2048 CPL).
+template <int R, int NB, int CPL>
 __global__ void __launch_bounds__(256) k_lm_head(Q4Mat m, const float* __restrict__ x, float* __restrict__ logits, float* __restrict__ pv,
                           uint32_t* __restrict__ pi) {
     __shared__ float sv[NB][4];
@@ -1291,18 +1293,18 @@ __global__ void __launch_bounds__(256) k_lm_head(Q4Mat m, const float* __restric
     uint32_t rows[R];
 #pragma unroll
     for (int i = 0; i < R; ++i) rows[i] = grp * R + i;
-    Q4Frag<64, 1, R> f;
+    Q4Frag<64, CPL, R> f;
     if (grp < groups) f.issue(m, rows, lane);
     if (staged) xs.store(m.in, NB, xq_lds, XqIdentity{});
     else xq_prep(x, m.in, m.in, NB, xq_lds, XqIdentity{});
-    XqFrag<NB, 1> xr;
+    XqFrag<NB, CPL> xr;
     xr.template read<64>(xq_lds, nch, lane);
     while (grp < groups) {
         const uint32_t nxt = grp + total_waves();
         uint32_t nrows[R];
 #pragma unroll
         for (int i = 0; i < R; ++i) nrows[i] = nxt * R + i;
-        Q4Frag<64, 1, R> fn;
+        Q4Frag<64, CPL, R> fn;
         if (nxt < groups) fn.issue(m, nrows, lane);
         float acc[R][NB];
         f.template dot<NB>(xr, acc);
@@ -1419,6 +1421,9 @@ void launch_hc_up_mix(const HcDev& w, const float* hyper, const float* inv, cons
     const uint32_t nch = w.up.in / 32;
     int lpr = 2;
     while (lpr < (int)nch) lpr <<= 1;
+    // a wave holds 64 / lpr row slots, one per stream at least
+    if (w.up.in % 32 || lpr > 16 || (uint32_t)lpr * hc > 64)
+        throw std::runtime_error("hyper-connection low rank must be a multiple of 32 up to 512 (16 lanes a stream)");
     constexpr int R = 2;
     const uint32_t outs_pw = (64 / lpr) / hc * R;
     const uint32_t grid = grid_for((H + outs_pw - 1) / outs_pw, 1u << 20);
@@ -1478,6 +1483,22 @@ void launch_qmv(const SegArgs& a, int nb, hipStream_t st) {
 
 void launch_qmv_inject(const InjArgs& a, int nb, hipStream_t st) {
     const uint32_t cpl = (a.m.in / 32 + 63) / 64;
+    if (a.m.in % 32 || cpl > 4) throw std::runtime_error("out-projection input must be a multiple of 32 up to 8192");
+    if (cpl > 2 && nb > 2) {
+        // inputs past 4096 take four chunks per lane, whose 3-4 row forms
+        // would spill: rows are independent, so two launches of <= 2 rows
+        InjArgs hi = a;
+        hi.x += (size_t)2 * a.xs;
+        if (hi.z) hi.z += (size_t)2 * a.xs;
+        if (hi.x_xq) hi.x_xq += (size_t)2 * (a.m.in / 32);
+        if (hi.ssq) hi.ssq += (size_t)2 * a.nheads * a.ssq_blocks;
+        if (hi.hyper) hi.hyper += (size_t)2 * a.m.out * a.hc;
+        if (hi.inj) hi.inj += (size_t)2 * a.hc;
+        if (hi.raw_out) hi.raw_out += (size_t)2 * a.m.out;
+        launch_qmv_inject(a, 2, st);
+        launch_qmv_inject(hi, nb - 2, st);
+        return;
+    }
     constexpr int R = 2;
     const uint32_t grid = grid_for(a.m.out / R);
     if (a.xmode == XM_DN_GATED && !a.x_xq)
@@ -1485,17 +1506,27 @@ void launch_qmv_inject(const InjArgs& a, int nb, hipStream_t st) {
     const size_t lds = (a.xmode == XM_DN_GATED && a.x_xq) ? 0 : xq_bytes(nb, a.m.in);
     if (a.x_xq && a.xs != a.m.in) throw std::runtime_error("chunked inputs must be dense rows");
 #define INJ(C, X) CHK_NB_SWITCH(nb, (k_qmv_inject<C, R, NB, X><<<grid, 256, lds, st>>>(a)))
+    // one, two or four 32-input chunks per lane (lanes past the last chunk
+    // are masked)
     if (a.xmode == XM_DN_GATED) {
         if (cpl <= 1) {
             INJ(1, XM_DN_GATED);
-        } else {
+        } else if (cpl == 2) {
             INJ(2, XM_DN_GATED);
+        } else if (nb == 1) {
+            k_qmv_inject<4, R, 1, XM_DN_GATED><<<grid, 256, lds, st>>>(a);
+        } else {
+            k_qmv_inject<4, R, 2, XM_DN_GATED><<<grid, 256, lds, st>>>(a);
         }
     } else {
         if (cpl <= 1) {
             INJ(1, XM_PLAIN);
-        } else {
+        } else if (cpl == 2) {
             INJ(2, XM_PLAIN);
+        } else if (nb == 1) {
+            k_qmv_inject<4, R, 1, XM_PLAIN><<<grid, 256, lds, st>>>(a);
+        } else {
+            k_qmv_inject<4, R, 2, XM_PLAIN><<<grid, 256, lds, st>>>(a);
         }
     }
 #undef INJ
@@ -1522,24 +1553,19 @@ void launch_moe_gate_up(const MoeArgs& a, hipStream_t st, hipEvent_t ev_start, h
     (void)tasks;
     if (a.I % 32) throw std::runtime_error("expert width must be a multiple of 32");
     if (!a.act_xq) throw std::runtime_error("the gate/up kernel needs the act chunk buffer");
+    if (a.H % 32 || a.H > 4096) throw std::runtime_error("expert input width must be a multiple of 32 up to 4096");
     const uint32_t grid = a.nb * (a.topk + 1) * (a.I / 32);  // one 32-row chunk per workgroup
     const size_t lds = xq_bytes(a.nb, a.H);
-    if (ev_start) {
-        // events recorded by the dispatch itself: the kernel's own start and end
-        const void* fn = a.X.bits == 3   ? (const void*)k_moe_gate_up<RG, 3>
-                         : a.X.bits == 2 ? (const void*)k_moe_gate_up<RG, 2>
-                                         : (const void*)k_moe_gate_up<RG, 4>;
-        MoeArgs arg = a;
-        void* args[] = {&arg};
-        const hipError_t e = hipExtLaunchKernel(fn, dim3(grid), dim3(GU_WG), args, lds, st, ev_start, ev_stop, 0);
-        if (e != hipSuccess) throw std::runtime_error(std::string("gate/up launch: ") + hipGetErrorString(e));
-        return;
-    }
-    switch (a.X.bits) {
-    case 3: k_moe_gate_up<RG, 3><<<grid, GU_WG, lds, st>>>(a); break;
-    case 2: k_moe_gate_up<RG, 2><<<grid, GU_WG, lds, st>>>(a); break;
-    default: k_moe_gate_up<RG, 4><<<grid, GU_WG, lds, st>>>(a); break;
-    }
+    const bool wide = a.H > 2048;
+    const void* fn = a.X.bits == 3   ? (wide ? (const void*)k_moe_gate_up<RG, 3, 2> : (const void*)k_moe_gate_up<RG, 3, 1>)
+                     : a.X.bits == 2 ? (wide ? (const void*)k_moe_gate_up<RG, 2, 2> : (const void*)k_moe_gate_up<RG, 2, 1>)
+                                     : (wide ? (const void*)k_moe_gate_up<RG, 4, 2> : (const void*)k_moe_gate_up<RG, 4, 1>);
+    MoeArgs arg = a;
+    void* args[] = {&arg};
+    // with events: recorded by the dispatch itself (the kernel's own start and end)
+    const hipError_t e = ev_start ? hipExtLaunchKernel(fn, dim3(grid), dim3(GU_WG), args, lds, st, ev_start, ev_stop, 0)
+                                  : hipLaunchKernel(fn, dim3(grid), dim3(GU_WG), args, lds, st);
+    if (e != hipSuccess) throw std::runtime_error(std::string("gate/up launch: ") + hipGetErrorString(e));
 }
 
 void launch_moe_down(const MoeArgs& a, hipStream_t st) {
@@ -1584,8 +1610,12 @@ void launch_lm_head(const Q4Mat& m, const float* x, float* logits, float* pv, ui
                     uint32_t* out, int nb, hipStream_t st) {
     if (m.out % 4) throw std::runtime_error("LM head rows must be a multiple of 4");
     const size_t lds = xq_bytes(nb, m.in);
-    constexpr int R = 4;
-    CHK_NB_SWITCH(nb, (k_lm_head<R, NB><<<nparts, 256, lds, st>>>(m, x, logits, pv, pi)));
+    if (m.in > 4096) throw std::runtime_error("LM head input wider than 4096");
+    if (m.in <= 2048) {
+        CHK_NB_SWITCH(nb, (k_lm_head<4, NB, 1><<<nparts, 256, lds, st>>>(m, x, logits, pv, pi)));
+    } else {  // two chunks per lane: two rows per wave keep the registers
+        CHK_NB_SWITCH(nb, (k_lm_head<2, NB, 2><<<nparts, 256, lds, st>>>(m, x, logits, pv, pi)));
+    }
     k_argmax_final<<<nb, 256, 0, st>>>(pv, pi, nparts, out);
 }
 

@@ -653,10 +653,12 @@ struct ChkEngine {
         ensure(c.full_attention_interval >= 1 && c.num_hidden_layers >= 1, "layer pattern");
         ensure(c.hc_count >= 2 && c.hc_count <= 4, "hc_count must be 2..=4 (one hyper-connection stream per wave)");
         ensure(c.hidden_size % 256 == 0, "hidden % 256 == 0 (gpu/load.rs:25-28)");
-        // the batch-1 expert kernels hold one 32-input chunk per lane of a
-        // wave (64 chunks)
-        ensure(c.hidden_size <= 2048, "hidden size must be at most 2048 (one 32-input chunk per lane)");
-        ensure(c.hc_lowrank % 32 == 0 && c.hc_lowrank <= 2048, "hc_lowrank must be a multiple of 32");
+        // the batch-1 kernels hold one or two 32-input chunks per lane of a
+        // wave (64 lanes)
+        ensure(c.hidden_size <= 4096, "hidden size must be at most 4096 (two 32-input chunks per lane)");
+        // the up + mix kernel keeps one row slot per stream in a wave's 64
+        // lanes (<= 16 lanes a slot at hc 4), each lane one 32-input chunk
+        ensure(c.hc_lowrank % 32 == 0 && c.hc_lowrank <= 512, "hc_lowrank must be a multiple of 32 up to 512");
         ensure(c.moe_intermediate_size % 64 == 0, "expert width must be a multiple of 64 (gpu/load.rs:37-40)");
         ensure(c.shared_expert_intermediate_size == c.moe_intermediate_size,
                "shared expert width must equal the routed expert width");

@@ -93,6 +93,90 @@ def tiny(seed: int = 1234, layers: int = 4, mtp: int = 1, indexer_budget: int = 
     )
 
 
+def qwen4_exp_fixture(seed: int = 1234) -> ChkConfig:
+    """The qwen4_exp test checkpoint's text_config (the reference's
+    tests/fixtures/qwen4_exp/config.json: 4 layers with the attention
+    layer last, hidden 256, hc 4 / low rank 320, 8 experts top-4 of width
+    256 plus a shared expert of 256, DeltaNet 16 key / 48 value heads of
+    128, attention 8 q / 2 kv heads of 256, the QSA indexer 4 x 128 with
+    budget 2048, vocab 248,320, one MTP layer, a PLE block before layer 2
+    with 3-grams, 8 heads per order, embed dim 256 and conv kernel 4),
+    on synthetic weights; the n-gram rows are groups of 16
+    (tests/import.rs:52) and the synthetic table holds 1021 - h rows in
+    head h."""
+    return with_ple(make_config(
+        hidden_size=256,
+        num_hidden_layers=4,
+        full_attention_interval=4,
+        vocab_size=248320,
+        num_attention_heads=8,
+        num_key_value_heads=2,
+        head_dim=256,
+        linear_num_key_heads=16,
+        linear_num_value_heads=48,
+        linear_key_head_dim=128,
+        linear_value_head_dim=128,
+        linear_conv_kernel_dim=4,
+        hc_count=4,
+        hc_lowrank=320,
+        num_experts=8,
+        num_experts_per_tok=4,
+        moe_intermediate_size=256,
+        shared_expert_intermediate_size=256,
+        norm_topk_prob=1,
+        indexer_n_heads=4,
+        indexer_head_dim=128,
+        indexer_budget=2048,
+        indexer_compress_ratio=4,
+        mtp_num_hidden_layers=1,
+        eos_token_id=248044,
+        ple_layer=0,
+        rms_norm_eps=1e-6,
+        partial_rotary_factor=0.25,
+        rope_theta=1e7,
+        seed=seed,
+    ), layer=2, embed_dim=256, ngram_size=3, heads_per_ngram=8, group=16, head_rows=1021, kernel=4)
+
+
+def wide(seed: int = 4096, layers: int = 4) -> ChkConfig:
+    """A 4096-wide model for parity at the engine's widest hidden size:
+    the 80B shape's DeltaNet (16 / 32 heads of 128) and attention (16 q /
+    2 kv heads of 256) with hidden 4096, 32 experts top-4 of width 512
+    plus a shared expert, vocab 4096, one MTP layer."""
+    return make_config(
+        hidden_size=4096,
+        num_hidden_layers=layers,
+        full_attention_interval=4,
+        vocab_size=4096,
+        num_attention_heads=16,
+        num_key_value_heads=2,
+        head_dim=256,
+        linear_num_key_heads=16,
+        linear_num_value_heads=32,
+        linear_key_head_dim=128,
+        linear_value_head_dim=128,
+        linear_conv_kernel_dim=4,
+        hc_count=4,
+        hc_lowrank=320,
+        num_experts=32,
+        num_experts_per_tok=4,
+        moe_intermediate_size=512,
+        shared_expert_intermediate_size=512,
+        norm_topk_prob=1,
+        indexer_n_heads=4,
+        indexer_head_dim=128,
+        indexer_budget=QSA_DENSE_BUDGET,
+        indexer_compress_ratio=4,
+        mtp_num_hidden_layers=1,
+        eos_token_id=4095,
+        ple_layer=0,
+        rms_norm_eps=1e-6,
+        partial_rotary_factor=0.25,
+        rope_theta=1e7,
+        seed=seed,
+    )
+
+
 def with_ple(c: ChkConfig, layer: int = 2, embed_dim: int = 256, ngram_size: int = 3, heads_per_ngram: int = 8,
              group: int = 16, head_rows: int = 1021, kernel: int = 4) -> ChkConfig:
     """`c` with a PLE n-gram block before decoder layer `layer` (1-based, as

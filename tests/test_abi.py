@@ -51,9 +51,10 @@ def test_python_signatures_match_headers():
 
 def test_load_validates_before_touching_the_device():
     """Configs the kernels cannot run are refused by chk_engine_load before
-    any device call (so this runs without a GPU): hidden sizes above 2048
-    (one 32-input chunk per lane in the batch-1 expert kernels), more than
-    3 drafts, PLE blocks the kernels cannot lay out."""
+    any device call (so this runs without a GPU): hidden sizes above 4096
+    (two 32-input chunks per lane in the batch-1 kernels), hyper-connection
+    low ranks past 16 lanes a stream, more than 3 drafts, PLE blocks the
+    kernels cannot lay out."""
     if not abi.LIB_PATH.exists():
         pytest.skip("libcherenkov.so not built (run __graft_entry__.build())")
     from cherenkov_amd import presets
@@ -61,8 +62,11 @@ def test_load_validates_before_touching_the_device():
     L = abi.lib()
     cases = []
     c = presets.tiny()
-    c.hidden_size = 2304
-    cases.append((c, abi.ChkOptions(4, 0, 64, 0), "hidden size must be at most 2048"))
+    c.hidden_size = 4352
+    cases.append((c, abi.ChkOptions(4, 0, 64, 0), "hidden size must be at most 4096"))
+    c = presets.tiny()
+    c.hc_lowrank = 544
+    cases.append((c, abi.ChkOptions(4, 0, 64, 0), "hc_lowrank must be a multiple of 32 up to 512"))
     c = presets.tiny()
     cases.append((c, abi.ChkOptions(4, 4, 64, 0), "drafts must be 0..=3"))
     c = presets.tiny()

@@ -1,0 +1,61 @@
+"""Parity at model shapes other than the 80B preset and the tiny model:
+
+- the reference's qwen4_exp test checkpoint shape (tests/fixtures/qwen4_exp/
+  config.json: hidden 256, 48 DeltaNet value heads over 16 key heads,
+  8 experts top-4, vocab 248,320, the PLE block before layer 2, QSA budget
+  2048), on synthetic weights;
+- hidden 4096, the widest the batch-1 kernels take (two 32-input chunks
+  per lane in the expert gate/up and LM head kernels).
+
+Each runs a GEMM prefill and batch-1 decode steps against the oracle run
+token by token (forward_token, cpu.rs, q8 KV rule) at the north-star bar:
+every decode position's logits, the prefill's last row, and the greedy
+token where the margin exceeds 1e-3."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from cherenkov_amd import presets
+from cherenkov_amd.engine import Engine
+from oracle.oracle import OracleModel
+from tests.gpu_util import argmax_margin, assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def prefill_then_decode(cfg, label, prompt_len, steps, seed):
+    rng = np.random.default_rng(seed)
+    prompt = rng.integers(0, cfg.vocab_size, size=prompt_len).tolist()
+    eng = Engine(cfg, experts=4, drafts=0, max_t=prompt_len + steps + 8)
+    st = OracleModel(cfg).new_state()
+    try:
+        nxt, _ = eng.prefill_chunk(prompt)
+        got = eng.logits_row(0)
+        ref = None
+        for t in prompt:
+            ref = st.forward_token(t, True)
+        assert_close(got, ref, f"{label}: prefill last row")
+        if argmax_margin(ref) > 1e-3:
+            assert nxt == int(np.argmax(ref)), f"{label}: prefill greedy"
+        tok = nxt
+        for i in range(steps):
+            out = eng.step_rows([tok])
+            got = eng.logits_row(0)
+            eng.commit(1)
+            ref = st.forward_token(tok, True)
+            assert_close(got, ref, f"{label}: decode position {prompt_len + i}")
+            if argmax_margin(ref) > 1e-3:
+                assert out[0] == int(np.argmax(ref)), f"{label}: decode greedy {i}"
+            tok = out[0]
+    finally:
+        eng.close()
+
+
+def test_reference_fixture_shape_matches_oracle(have_gpu):
+    prefill_then_decode(presets.qwen4_exp_fixture(), "fixture shape", prompt_len=24, steps=6, seed=121)
+
+
+def test_hidden_4096_matches_oracle(have_gpu):
+    prefill_then_decode(presets.wide(), "hidden 4096", prompt_len=20, steps=5, seed=122)

@@ -120,3 +120,35 @@ def test_malformed_stores_are_refused(tmp_path, case, msg):
     _edit(path, fname, fn)
     rc, _, err = store_config(path)
     assert rc != 0 and msg in err, err
+
+
+def test_reference_fixture_config_is_parsed(tmp_path):
+    """The reference's own qwen4_exp test checkpoint config (tests/fixtures/
+    qwen4_exp/config.json, committed as tests/golden/qwen4_exp_fixture_config.json)
+    in a store of its shape: chk_store_config reads every field the engine
+    uses (config.rs:9-126: layer_types, the hyper-connection, indexer, MTP
+    and PLE settings, rope_parameters.rope_theta, eos_token_id) to the
+    values the fixture states, and the n-gram row group from the manifest."""
+    import shutil
+    from pathlib import Path
+
+    if not abi.LIB_PATH.exists():
+        pytest.skip("libcherenkov.so not built")
+    want = presets.qwen4_exp_fixture()
+    path = write_store(want, tmp_path / "s")
+    golden = Path(__file__).resolve().parent / "golden" / "qwen4_exp_fixture_config.json"
+    shutil.copyfile(golden, path / "config.json")
+    rc, got, err = store_config(path)
+    assert rc == 0, err
+    for k, _ in want._fields_:
+        if k not in ("seed", "ngram_head_rows"):
+            assert getattr(got, k) == getattr(want, k), k
+    t = json.loads(golden.read_text())["text_config"]
+    assert got.hidden_size == t["hidden_size"] == 256
+    assert got.linear_num_value_heads == t["linear_num_value_heads"] == 48
+    assert got.vocab_size == t["vocab_size"] == 248320
+    assert got.ple_layer == t["ple_layer_ids"][0] == 2
+    assert got.indexer_budget == t["indexer_budget"] == 2048
+    assert got.rope_theta == t["rope_parameters"]["rope_theta"]
+    assert got.eos_token_id == t["eos_token_id"]
+    assert got.ngram_group == 16
