@@ -119,6 +119,8 @@ SIGNATURES = [
     ("chk_engine_load", i32, [C.POINTER(ChkConfig), C.POINTER(ChkOptions), C.POINTER(P)]),
     ("chk_engine_free", None, [P]),
     ("chk_engine_load_store", i32, [C.c_char_p, C.POINTER(ChkOptions), C.POINTER(P)]),
+    ("chk_engine_load_bounded", i32, [C.POINTER(ChkConfig), C.POINTER(ChkOptions), u64, u64, u32, C.POINTER(P)]),
+    ("chk_engine_load_store_bounded", i32, [C.c_char_p, C.POINTER(ChkOptions), u64, u64, u32, C.POINTER(P)]),
     ("chk_store_config", i32, [C.c_char_p, C.POINTER(ChkConfig)]),
     ("chk_step_rows", i32, [P, C.POINTER(u32), u32, i32, i32, C.POINTER(u32)]),
     ("chk_step", i32, [P, u32, C.POINTER(u32)]),

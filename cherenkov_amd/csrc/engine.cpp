@@ -355,10 +355,19 @@ struct ChkEngine {
     // (`pf_allocs`, dropped by prefill_release); `alloc_bytes` counts both.
     std::vector<void*> pf_allocs;
     uint64_t alloc_bytes = 0, pf_alloc_bytes = 0;
+    // Gpu::load_bounded (gpu/load.rs:12-63): the server's memory budget
+    // (memory_bytes - reserve) every device buffer of the engine counts
+    // against (0: no budget), and the prefill rows whose scratch the load
+    // keeps room for
+    uint64_t mem_limit = 0;
+    uint32_t budget_prefill_rows = 0;
     template <class T>
     T* dalloc(uint64_t n, bool prefill_scratch = false) {
         void* p = nullptr;
         const uint64_t bytes = std::max<uint64_t>(n * sizeof(T), 256);
+        // MetalContext::check_allocation (metal.rs:145-156)
+        ensure(!mem_limit || alloc_bytes + bytes <= mem_limit,
+               "allocation would exceed the server memory budget; reduce pool or prefill chunk size");
         HIPCHK(hipMalloc(&p, bytes));
         (prefill_scratch ? pf_allocs : allocs).push_back(p);
         alloc_bytes += bytes;
@@ -875,6 +884,23 @@ struct ChkEngine {
         reset_state();
         HIPCHK(hipStreamSynchronize(st));
         HIPCHK(hipGetLastError());
+        // PoolMemory::bytes (budget.rs:14-40): with every record resident the
+        // pool is the whole store, an explicit size that must leave room for
+        // the prefill scratch of budget_prefill_rows rows
+        if (mem_limit) {
+            const uint64_t rows = std::max<uint32_t>(1, std::min(budget_prefill_rows, max_t));
+            ensure(alloc_bytes + prefill_scratch_bytes(rows, false) <= mem_limit,
+                   "explicit expert pool exceeds server memory budget after fixed buffers and prefill scratch");
+        }
+    }
+
+    // Gpu::load_bounded (gpu/load.rs:12-63): the budget is memory_bytes -
+    // reserve (memory_bytes 0: no budget, as load's None).
+    void set_budget(uint64_t reserve, uint64_t memory_bytes, uint32_t prefill_rows) {
+        if (!memory_bytes) return;
+        ensure(reserve <= memory_bytes, "cache exceeds memory budget");
+        mem_limit = memory_bytes - reserve;
+        budget_prefill_rows = prefill_rows;
     }
 
     // Gpu::load over a packed store (gpu/load.rs:8-19 with Packed::open):
@@ -1675,7 +1701,9 @@ uint64_t ChkEngine::prefill_scratch_bytes(uint64_t C, bool all_logits) const {
 uint32_t ChkEngine::prefill_rows_fit(bool all_logits) const {
     size_t free_b = 0, total_b = 0;
     HIPCHK(hipMemGetInfo(&free_b, &total_b));
-    const uint64_t avail = (uint64_t)free_b + pf_alloc_bytes;
+    uint64_t avail = (uint64_t)free_b + pf_alloc_bytes;
+    // under a server budget, what the budget leaves (allocation.rs:154)
+    if (mem_limit) avail = std::min<uint64_t>(avail, mem_limit - std::min(mem_limit, alloc_bytes - pf_alloc_bytes));
     uint32_t lo = 0, hi = std::min<uint32_t>(max_t, 4096);
     while (lo < hi) {
         const uint32_t mid = lo + (hi - lo + 1) / 2;
@@ -1708,7 +1736,10 @@ uint32_t ChkEngine::pf_qsa_rows() const {
 
 void ChkEngine::pf_alloc() {
     if (pf.cap) return;
-    const uint64_t C = std::min<uint32_t>(max_t, PF_MAX_ROWS);
+    // chunks of up to 4096 rows (prefill.rs:116); under a server budget, of
+    // the rows the load kept room for (the prompt then runs in more chunks)
+    uint64_t C = std::min<uint32_t>(max_t, PF_MAX_ROWS);
+    if (mem_limit) C = std::min<uint64_t>(C, std::max<uint32_t>(1, budget_prefill_rows));
     const uint64_t slots = D.topk + 1;
     pf.tokens = pfalloc<uint32_t>(C);
     pf.pos = pfalloc<uint32_t>(C);
@@ -2280,6 +2311,20 @@ int chk_engine_load_store(const char* dir, const ChkOptions* opt, ChkEngine** ou
     *out = nullptr;
     auto e = std::make_unique<ChkEngine>();
     CHK_TRY(e->load_store(dir, opt); *out = e.release())
+}
+
+int chk_engine_load_bounded(const ChkConfig* cfg, const ChkOptions* opt, uint64_t reserve, uint64_t memory_bytes,
+                            uint32_t prefill_rows, ChkEngine** out) {
+    *out = nullptr;
+    auto e = std::make_unique<ChkEngine>();
+    CHK_TRY(e->set_budget(reserve, memory_bytes, prefill_rows); e->load(cfg, opt); *out = e.release())
+}
+
+int chk_engine_load_store_bounded(const char* dir, const ChkOptions* opt, uint64_t reserve, uint64_t memory_bytes,
+                                  uint32_t prefill_rows, ChkEngine** out) {
+    *out = nullptr;
+    auto e = std::make_unique<ChkEngine>();
+    CHK_TRY(e->set_budget(reserve, memory_bytes, prefill_rows); e->load_store(dir, opt); *out = e.release())
 }
 
 int chk_store_config(const char* dir, ChkConfig* out) { CHK_TRY(*out = chk::open_store(dir)->cfg) }

@@ -34,6 +34,21 @@ class Engine:
         self.L = L
 
     @classmethod
+    def load_bounded(cls, cfg: ChkConfig, reserve: int, memory_bytes: int, prefill_rows: int, experts: int = 4,
+                     drafts: int = 0, max_t: int = 2048, no_eos: bool = False) -> "Engine":
+        """Gpu::load_bounded: the engine under a server memory budget of
+        memory_bytes - reserve (chk_engine_load_bounded)."""
+        self = cls.__new__(cls)
+        self.cfg = cfg
+        self.opt = ChkOptions(experts, drafts, max_t, 1 if no_eos else 0)
+        self._h = C.c_void_p()
+        L = lib()
+        check(L.chk_engine_load_bounded(C.byref(cfg), C.byref(self.opt), reserve, memory_bytes, prefill_rows,
+                                        C.byref(self._h)))
+        self.L = L
+        return self
+
+    @classmethod
     def load_store(cls, path, experts: int = 4, drafts: int = 0, max_t: int = 2048,
                    no_eos: bool = False) -> "Engine":
         """Gpu::load over a packed store directory (chk_engine_load_store)."""

@@ -51,6 +51,22 @@ void chk_engine_free(ChkEngine* e);
  * missing or mismatched tensor. */
 int chk_engine_load_store(const char* dir, const ChkOptions* opt, ChkEngine** out);
 
+/* Gpu::load_bounded (gpu/load.rs:12-63; src/server.rs:90-97): the loads
+ * above under a server memory budget of memory_bytes - reserve (memory_bytes
+ * 0: no budget, as load passes None; reserve above memory_bytes: "cache
+ * exceeds memory budget").  Every device buffer the engine allocates then,
+ * and later (prefill scratch), counts against it ("allocation would exceed
+ * the server memory budget; reduce pool or prefill chunk size"); the load
+ * fails unless the prefill scratch of prefill_rows rows (at most max_t, at
+ * least 1) still fits beside the resident store (budget.rs:14-40), and
+ * chk_prefill_rows_fit answers within the budget.  Checkpoints
+ * (chk_save_prefix / chk_save_into) are the caller's objects and are not
+ * counted. */
+int chk_engine_load_bounded(const ChkConfig* cfg, const ChkOptions* opt, uint64_t reserve, uint64_t memory_bytes,
+                            uint32_t prefill_rows, ChkEngine** out);
+int chk_engine_load_store_bounded(const char* dir, const ChkOptions* opt, uint64_t reserve, uint64_t memory_bytes,
+                                  uint32_t prefill_rows, ChkEngine** out);
+
 /* The ChkConfig of a packed store's config.json after the manifest checks
  * of chk_engine_load_store (file reads only, no device work). */
 int chk_store_config(const char* dir, ChkConfig* out);

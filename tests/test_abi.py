@@ -84,3 +84,19 @@ def test_load_validates_before_touching_the_device():
         rc = L.chk_engine_load(C.byref(cfg), C.byref(opt), C.byref(h))
         assert rc != 0 and not h.value
         assert msg in L.chk_last_error().decode()
+
+
+def test_bounded_load_refuses_a_reserve_above_the_budget():
+    """Gpu::load_bounded (gpu/load.rs:55-61): a reserve larger than the
+    memory budget is refused before any device call."""
+    if not abi.LIB_PATH.exists():
+        pytest.skip("libcherenkov.so not built (run __graft_entry__.build())")
+    from cherenkov_amd import presets
+
+    L = abi.lib()
+    cfg = presets.tiny()
+    opt = abi.ChkOptions(4, 0, 64, 0)
+    h = C.c_void_p()
+    assert L.chk_engine_load_bounded(C.byref(cfg), C.byref(opt), 2 << 30, 1 << 30, 64, C.byref(h)) != 0
+    assert not h.value
+    assert "cache exceeds memory budget" in L.chk_last_error().decode()
