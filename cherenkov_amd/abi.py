@@ -131,6 +131,8 @@ SIGNATURES = [
     ("chk_prefill_chunk", i32, [P, C.POINTER(u32), u32, u32, i32, C.POINTER(u32), C.POINTER(u32)]),
     ("chk_prefill_release", None, [P]),
     ("chk_prefill_rows_fit", i32, [P, i32, C.POINTER(u32)]),
+    ("chk_debug_engine_blocks", i32, [P, u32, C.POINTER(u32), u32, C.POINTER(u32)]),
+    ("chk_debug_row_vis", i32, [P, u32, C.POINTER(u32), u32, C.POINTER(u32)]),
     ("chk_pf_logits_row", C.POINTER(f32), [P, u32]),
     ("chk_logits_row", C.POINTER(f32), [P, u32]),
     ("chk_logits", C.POINTER(f32), [P]),

@@ -165,6 +165,11 @@ struct PfBufs {
     float *iq_ready, *qsa_bscore, *qsa_part;
     uint32_t* qsa_vmask;
     uint32_t qsa_rows;
+    // every row's block mask of the chunk's latest attention layer (rows
+    // that attend densely: no bits), for the debug_engine_blocks view;
+    // rows of the latest chunk
+    uint32_t* qsa_rows_mask;
+    uint32_t last_rows;
     // PLE over a chunk: table rows of each row's token, then as Scratch
     uint32_t* ple_ids;
     float *ple_e, *ple_key, *ple_value, *ple_gated, *ple_gvn;
@@ -1689,8 +1694,8 @@ uint64_t ChkEngine::prefill_scratch_bytes(uint64_t C, bool all_logits) const {
     if (all_logits) b += C * D.V * f;
     if (ple_l >= 0) b += C * (ngram_heads + c.ple_embed_dim + 3ull * D.hh + D.H) * 4;
     if (D.qsa)
-        b += (C * D.inh * D.ihd + (uint64_t)pf_qsa_rows() * (D.max_blocks + D.mask_words +
-                                                             (uint64_t)D.nh * max_chunks * (D.hd + 2))) * 4;
+        b += (C * (D.inh * D.ihd + D.mask_words) +
+              (uint64_t)pf_qsa_rows() * (D.max_blocks + D.mask_words + (uint64_t)D.nh * max_chunks * (D.hd + 2))) * 4;
     return b;
 }
 
@@ -1803,6 +1808,7 @@ void ChkEngine::pf_alloc() {
         pf.iq_ready = pfalloc<float>(C * D.inh * D.ihd);
         pf.qsa_bscore = pfalloc<float>((uint64_t)pf.qsa_rows * D.max_blocks);
         pf.qsa_vmask = pfalloc<uint32_t>((uint64_t)pf.qsa_rows * D.mask_words);
+        pf.qsa_rows_mask = pfalloc<uint32_t>(C * D.mask_words);
         pf.qsa_part = pfalloc<float>((uint64_t)pf.qsa_rows * D.nh * max_chunks * (D.hd + 2));
     }
     if (ple_l >= 0) {
@@ -2027,8 +2033,10 @@ void ChkEngine::pf_attention(const LayerDev& L, uint32_t T, uint32_t pos0, const
         launch_qsa_block_keys(aa, pos0 / D.ratio, (pos0 + T) / D.ratio, st);
         const uint32_t first_sel = (D.kblk + 1) * D.ratio - 1;  // first position with nblk > kblk
         const uint32_t td = first_sel <= pos0 ? 0 : std::min(T, first_sel - pos0);
-        if (td)
+        if (td) {
             launch_pf_flash(pf.q_ready, pf.q_raw, kvl, pf.attn_out, td, pos0, D.nh, D.nkv, D.hd, D.attn_scale, st);
+            launch_zero_f32(reinterpret_cast<float*>(pf.qsa_rows_mask), (uint64_t)td * D.mask_words, st);
+        }
         for (uint32_t r0 = td; r0 < T; r0 += pf.qsa_rows) {
             const uint32_t nr = std::min(pf.qsa_rows, T - r0);
             AttnArgs ag = aa;
@@ -2042,6 +2050,8 @@ void ChkEngine::pf_attention(const LayerDev& L, uint32_t T, uint32_t pos0, const
             ag.part = pf.qsa_part;
             ag.max_chunks = (pos0 + r0 + nr - 1) / ATTN_CHUNK + 1;
             launch_qsa(ag, (int)nr, st);
+            launch_copy_f32(reinterpret_cast<float*>(pf.qsa_rows_mask) + (uint64_t)r0 * D.mask_words,
+                            reinterpret_cast<const float*>(pf.qsa_vmask), (uint64_t)nr * D.mask_words, st);
             launch_attn_core(ag, (int)nr, st);
         }
     }
@@ -2107,6 +2117,7 @@ void ChkEngine::prefill_gemm(const uint32_t* toks, uint32_t n, uint32_t next_aft
     tokens.resize(pos);
     for (uint32_t c0 = 0; c0 < n; c0 += pf.cap) {
         const uint32_t T = std::min(pf.cap, n - c0), pos0 = pos;
+        pf.last_rows = T;
         std::vector<uint32_t> rp(T);
         for (uint32_t t = 0; t < T; ++t) rp[t] = pos0 + t;
         HIPCHK(hipMemcpy(pf.tokens, toks + c0, T * 4, hipMemcpyHostToDevice));
@@ -2365,6 +2376,56 @@ int chk_prefill_chunk(ChkEngine* e, const uint32_t* tokens, uint32_t n, uint32_t
 }
 
 void chk_prefill_release(ChkEngine* e) { e->prefill_release(); }
+
+// Gpu::debug_engine_blocks (gpu/prefill.rs:471-484): the blocks selected for
+// row r of the last prefill chunk at its latest attention layer, from the
+// block mask; rows that attend densely (within the budget) select none.
+int chk_debug_engine_blocks(const ChkEngine* e, uint32_t r, uint32_t* out, uint32_t cap, uint32_t* n) {
+    CHK_TRY({
+        *n = 0;
+        ensure(e->pf.cap, "prefill scratch released");
+        ensure(r < e->pf.last_rows, "row out of range");
+        if (!e->D.qsa) return 0;  // the budget covers every context: no selection
+        std::vector<uint32_t> m(e->D.mask_words);
+        HIPCHK(hipMemcpy(m.data(), e->pf.qsa_rows_mask + (uint64_t)r * e->D.mask_words, m.size() * 4,
+                         hipMemcpyDeviceToHost));
+        uint32_t k = 0;
+        for (uint32_t j = 0; j < e->D.max_blocks; ++j)
+            if ((m[j / 32] >> (j % 32)) & 1u) {
+                if (k < cap) out[k] = j;
+                ++k;
+            }
+        *n = k;
+    })
+}
+
+// Gpu::debug_row_vis (gpu/prefill.rs:486-494): the tokens row r of the last
+// row step attended to at its latest attention layer, ascending: every
+// token while the row's complete blocks fit the budget, else the selected
+// blocks' tokens and the incomplete tail (select_tokens, cpu.rs:643-719).
+int chk_debug_row_vis(const ChkEngine* e, uint32_t r, uint32_t* out, uint32_t cap, uint32_t* n) {
+    CHK_TRY({
+        *n = 0;
+        ensure(r < e->batch_nb, "row out of range");
+        const Dims& D = e->D;
+        const uint32_t t_len = e->batch_pos + r + 1, nblk = t_len / D.ratio;
+        std::vector<uint32_t> m;
+        const bool dense = !D.qsa || nblk <= D.kblk;
+        if (!dense) {
+            m.resize(D.mask_words);
+            HIPCHK(hipMemcpy(m.data(), e->s.vmask + (uint64_t)r * D.mask_words, m.size() * 4, hipMemcpyDeviceToHost));
+        }
+        uint32_t k = 0;
+        for (uint32_t t = 0; t < t_len; ++t) {
+            const uint32_t j = t / D.ratio;
+            if (dense || j >= nblk || ((m[j / 32] >> (j % 32)) & 1u)) {
+                if (k < cap) out[k] = t;
+                ++k;
+            }
+        }
+        *n = k;
+    })
+}
 
 int chk_prefill_rows_fit(const ChkEngine* e, int all_logits, uint32_t* rows) {
     CHK_TRY(*rows = e->prefill_rows_fit(all_logits != 0))

@@ -117,6 +117,23 @@ class Engine:
     def prefill_release(self) -> None:
         self.L.chk_prefill_release(self._h)
 
+    def _ids(self, fn, r: int) -> list[int]:
+        n = C.c_uint32()
+        check(fn(self._h, r, None, 0, C.byref(n)))
+        out = (C.c_uint32 * max(1, n.value))()
+        check(fn(self._h, r, out, n.value, C.byref(n)))
+        return list(out[: n.value])
+
+    def debug_engine_blocks(self, r: int) -> list[int]:
+        """Gpu::debug_engine_blocks: QSA blocks selected for row r of the last
+        prefill chunk (its latest attention layer)."""
+        return self._ids(self.L.chk_debug_engine_blocks, r)
+
+    def debug_row_vis(self, r: int) -> list[int]:
+        """Gpu::debug_row_vis: tokens row r of the last row step attended to
+        (its latest attention layer)."""
+        return self._ids(self.L.chk_debug_row_vis, r)
+
     def prefill_rows_fit(self, all_logits: bool = False) -> int:
         r = C.c_uint32()
         check(self.L.chk_prefill_rows_fit(self._h, int(all_logits), C.byref(r)))

@@ -117,6 +117,14 @@ void chk_prefill_release(ChkEngine* e);
  * at most min(max_t, 4096) rows, whose prefill scratch fits the device
  * memory free now (errors when not even one row fits). */
 int chk_prefill_rows_fit(const ChkEngine* e, int all_logits, uint32_t* rows);
+/* Gpu::debug_engine_blocks (gpu/prefill.rs:471-484): the QSA blocks
+ * selected for row r of the last prefill chunk at its latest attention
+ * layer (rows within the budget, which attend densely, select none); and
+ * Gpu::debug_row_vis (gpu/prefill.rs:486-494): the tokens row r of the last
+ * row step attended to at its latest attention layer, ascending.  Up to cap
+ * ids go to out, n receives the count. */
+int chk_debug_engine_blocks(const ChkEngine* e, uint32_t r, uint32_t* out, uint32_t cap, uint32_t* n);
+int chk_debug_row_vis(const ChkEngine* e, uint32_t r, uint32_t* out, uint32_t cap, uint32_t* n);
 
 /* Gpu::pf_logits_row (gpu/prefill.rs:496-507): row r of the last prefill
  * chunk's logits (all-logits mode only; NULL + error otherwise). */

@@ -344,6 +344,9 @@ struct LayerW {
 struct KvCache {
     std::vector<float> k, v, index_k;
     size_t len = 0;
+    // the tokens the latest query attended to (select_tokens' result), for
+    // the tests of the engine's selection views
+    std::vector<size_t> last_selected;
 };
 struct DeltaState {
     std::vector<float> s, conv;
@@ -1040,6 +1043,7 @@ std::vector<float> attention(const OrcModel& m, const AttnW& w, const float* x, 
     size_t t_len = cache.len;
     if (t_len != pos + 1) throw std::runtime_error("attention cache out of step");
     std::vector<size_t> selected = select_tokens(m, w, qk.data(), cache, pos);
+    cache.last_selected = selected;
     std::vector<float> out(nh * hd, 0.0f);
     attend(qg.data(), cache.k.data(), cache.v.data(), selected, nh, nkv, hd, out.data());
     std::vector<float> o(w.o.view.out);
@@ -1350,6 +1354,27 @@ int orc_forward_token(void* mp, void* sp, uint32_t token, int kv_q8, float* logi
         g_err = ex.what();
         return -1;
     }
+}
+
+// The tokens the latest query of attention layer `layer` (a decoder layer
+// index; num_hidden_layers: the MTP layer) attended to, ascending.
+int orc_state_last_selection(void* mp, void* sp, uint32_t layer, uint32_t* out, uint32_t cap, uint32_t* n) {
+    OrcModel* m = (OrcModel*)mp;
+    OrcState* st = (OrcState*)sp;
+    const KvCache* kc = nullptr;
+    if (layer == m->c.num_hidden_layers && m->has_mtp) {
+        kc = &st->mtp_kv;
+    } else if (layer < m->c.num_hidden_layers && !m->layers[layer].linear) {
+        size_t ki = 0;
+        for (uint32_t l = 0; l < layer; ++l) ki += m->layers[l].linear ? 0 : 1;
+        kc = &st->kv[ki];
+    } else {
+        g_err = "not an attention layer";
+        return -1;
+    }
+    *n = (uint32_t)kc->last_selected.size();
+    for (uint32_t i = 0; i < std::min<uint32_t>(*n, cap); ++i) out[i] = (uint32_t)kc->last_selected[i];
+    return 0;
 }
 
 // Near-tie route hints for the next forward_token / mtp_forward (see

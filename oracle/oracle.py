@@ -30,6 +30,7 @@ _SIGS = [
     ("orc_mtp_forward", i32, [P, P, u32, P, u32, i32, P, P]),
     ("orc_moe", i32, [P, u32, P, P, P, P, P]),
     ("orc_set_record_bits", i32, [P, u32, u32, u32]),
+    ("orc_state_last_selection", i32, [P, P, u32, P, u32, P]),
     ("orc_gated_residual", i32, [P, u32, u32, P, P, P]),
     ("orc_deltanet", i32, [P, P, u32, P, P]),
     ("orc_delta_state", i32, [P, P, u32, P, P]),
@@ -271,6 +272,15 @@ class OracleState:
         out = np.empty(self.m.cfg.vocab_size, np.float32)
         _check(self.m.L.orc_forward_token(self.m.h, self.h, token, int(kv_q8), _p(out)))
         return out
+
+    def last_selection(self, layer: int) -> list[int]:
+        """The tokens the latest query of attention layer `layer` attended
+        to (select_tokens, cpu.rs:643-719), ascending."""
+        n = C.c_uint32()
+        _check(self.m.L.orc_state_last_selection(self.m.h, self.h, layer, None, 0, C.byref(n)))
+        out = np.empty(max(1, n.value), np.uint32)
+        _check(self.m.L.orc_state_last_selection(self.m.h, self.h, layer, _p(out), n.value, C.byref(n)))
+        return out[: n.value].tolist()
 
     def fill_prefix(self, n: int, seed: int = 1) -> None:
         """Jump to position n with seeded synthetic caches (timing only)."""

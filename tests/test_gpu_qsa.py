@@ -164,3 +164,42 @@ def test_tiny_qsa_gemm_prefill_matches_oracle(have_gpu, splits):
             assert_close(eng.logits_row(0), st.forward_token(t, True), "decode after prefill")
     finally:
         eng.close()
+
+
+def test_selection_debug_views_match_oracle(have_gpu):
+    """Gpu::debug_engine_blocks (gpu/prefill.rs:471-484) after a GEMM
+    prefill past the budget, for every row of the chunk, and Gpu::
+    debug_row_vis (gpu/prefill.rs:486-494) after each decode step: the
+    blocks and tokens the engine's last attention layer selected equal the
+    oracle's select_tokens (cpu.rs:643-719) at the same positions; rows
+    within the budget select no block in the prefill view and every token
+    in the row view."""
+    cfg = presets.tiny(indexer_budget=16, mtp=0)
+    ratio, kblk = cfg.indexer_compress_ratio, 16 // cfg.indexer_compress_ratio
+    layer = cfg.num_hidden_layers - 1
+    assert (layer + 1) % cfg.full_attention_interval == 0
+    rng = np.random.default_rng(29)
+    prompt = rng.integers(0, cfg.vocab_size, size=50).tolist()
+    eng = Engine(cfg, experts=4, drafts=0, max_t=128)
+    st = OracleModel(cfg).new_state()
+    try:
+        eng.prefill_chunk(prompt)
+        selective = 0
+        for p, t in enumerate(prompt):
+            st.forward_token(t, True)
+            sel = st.last_selection(layer)
+            nblk = (p + 1) // ratio
+            got = eng.debug_engine_blocks(p)
+            if nblk <= kblk:
+                assert sel == list(range(p + 1)) and got == [], f"row {p}"
+            else:
+                selective += 1
+                assert got == sorted({t_ // ratio for t_ in sel if t_ < nblk * ratio}), f"row {p}"
+        assert selective > 20
+        for t in rng.integers(0, cfg.vocab_size, size=4).tolist():
+            eng.step_rows([t])
+            eng.commit(1)
+            st.forward_token(t, True)
+            assert eng.debug_row_vis(0) == st.last_selection(layer)
+    finally:
+        eng.close()
