@@ -169,7 +169,7 @@ struct PfBufs {
     // that attend densely: no bits), for the debug_engine_blocks view;
     // rows of the latest chunk
     uint32_t* qsa_rows_mask;
-    uint32_t last_rows;
+    uint32_t last_rows, last_pos0;
     // PLE over a chunk: table rows of each row's token, then as Scratch
     uint32_t* ple_ids;
     float *ple_e, *ple_key, *ple_value, *ple_gated, *ple_gvn;
@@ -2118,6 +2118,7 @@ void ChkEngine::prefill_gemm(const uint32_t* toks, uint32_t n, uint32_t next_aft
     for (uint32_t c0 = 0; c0 < n; c0 += pf.cap) {
         const uint32_t T = std::min(pf.cap, n - c0), pos0 = pos;
         pf.last_rows = T;
+        pf.last_pos0 = pos0;
         std::vector<uint32_t> rp(T);
         for (uint32_t t = 0; t < T; ++t) rp[t] = pos0 + t;
         HIPCHK(hipMemcpy(pf.tokens, toks + c0, T * 4, hipMemcpyHostToDevice));
@@ -2389,8 +2390,11 @@ int chk_debug_engine_blocks(const ChkEngine* e, uint32_t r, uint32_t* out, uint3
         std::vector<uint32_t> m(e->D.mask_words);
         HIPCHK(hipMemcpy(m.data(), e->pf.qsa_rows_mask + (uint64_t)r * e->D.mask_words, m.size() * 4,
                          hipMemcpyDeviceToHost));
+        // the selection writes the mask words of the row's complete blocks
+        // only (the attention reads no bit past them)
+        const uint32_t nblk = std::min(e->D.max_blocks, (e->pf.last_pos0 + r + 1) / e->D.ratio);
         uint32_t k = 0;
-        for (uint32_t j = 0; j < e->D.max_blocks; ++j)
+        for (uint32_t j = 0; j < nblk; ++j)
             if ((m[j / 32] >> (j % 32)) & 1u) {
                 if (k < cap) out[k] = j;
                 ++k;
