@@ -10,6 +10,7 @@
 // Reference semantics: /root/reference/src/qwen4_exp/cpu.rs (forward_token
 // and the blocks it calls); the Metal dispatch plan this replaces:
 // src/qwen4_exp/gpu/decode.rs:13-294 and kernels/{common,qwen4_exp}/*.metal.
+#include <algorithm>
 #include <stdexcept>
 #include <type_traits>
 
@@ -1036,9 +1037,15 @@ __global__ void __launch_bounds__(GU_WG) k_moe_gate_up(MoeArgs a) {
     __shared__ float act_s[32];
     const int lane = threadIdx.x & 63;
     const uint32_t w = wave_id();
-    const uint32_t slots = a.topk + 1, cpr = a.I / 32;
+    // a row's tasks: topk routed slots of cpr chunks, then the shared
+    // expert's cps chunks
+    const uint32_t cpr = a.I / 32, cps = a.SI / 32, per_row = a.topk * cpr + cps;
     const uint32_t task = blockIdx.x;
-    const uint32_t b = task / (slots * cpr), slot = (task / cpr) % slots, c = task % cpr;
+    const uint32_t b = task / per_row, t = task % per_row;
+    const bool shared_task = t >= a.topk * cpr;
+    const uint32_t slot = shared_task ? a.topk : t / cpr, c = shared_task ? t - a.topk * cpr : t % cpr;
+    const size_t act_off = (size_t)b * (a.topk * a.I + a.SI) + slot * a.I;  // this slot's act values
+    const size_t xq_off = (size_t)b * per_row + slot * cpr;                  // and its chunks
     const uint32_t i0 = c * 32 + w * R;
     uint32_t rows[R];
 #pragma unroll
@@ -1117,11 +1124,11 @@ __global__ void __launch_bounds__(GU_WG) k_moe_gate_up(MoeArgs a) {
                 uv = u[i][0];
             }
         const float act = siluf_(gv) * uv;
-        a.act[((size_t)b * slots + slot) * a.I + i0 + lane] = act;
+        a.act[act_off + i0 + lane] = act;
         act_s[w * R + lane] = act;
     }
     __syncthreads();
-    if (w == 0) xq_chunk_store(act_s, a.act_xq + ((size_t)b * slots + slot) * cpr + c, lane);
+    if (w == 0) xq_chunk_store(act_s, a.act_xq + xq_off + c, lane);
 }
 
 // ------------------------------------------------- experts: down + combine
@@ -1135,7 +1142,9 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a) {
     constexpr int G = 64 / LPR;
     const int lane = threadIdx.x & 63, grp = lane / LPR, lir = lane % LPR;
     const uint32_t slots = a.topk + 1;
-    const uint32_t groups = a.H / R, nch = a.I >> 5;
+    // act_xq rows: topk routed slots of nch chunks, then the shared
+    // expert's nchs
+    const uint32_t groups = a.H / R, nch = a.I >> 5, nchs = a.SI >> 5, xrow = a.topk * nch + nchs;
     const uint32_t li = lane / a.hc, lg = lane % a.hc;
     const bool owner = li < (uint32_t)R && a.hyper;
     // routing of every row (lane j < topk: slot j's id and weight; lane
@@ -1168,7 +1177,7 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a) {
 #pragma unroll
     for (int pass = 0; pass < PASSES; ++pass) {
         const uint32_t slot = grp + pass * G, sl = slot < slots ? slot : slots - 1;
-        xq0[pass].template read<LPR>(a.act_xq + (size_t)sl * nch, nch, lir);
+        xq0[pass].template read<LPR>(a.act_xq + (size_t)sl * nch, sl < a.topk ? nch : nchs, lir);
     }
     float hy0 = 0.0f, ij0 = 0.0f;
     if (a.hyper) {
@@ -1236,7 +1245,7 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a) {
                     fq[pass].issue(mm, rows, lir);
                 }
                 if (gi == gi0 && b == 0) xq[pass] = xq0[pass];
-                else xq[pass].template read<LPR>(a.act_xq + ((size_t)b * slots + sl) * nch, nch, lir);
+                else xq[pass].template read<LPR>(a.act_xq + (size_t)b * xrow + sl * nch, sl < a.topk ? nch : nchs, lir);
             }
             float tot[R];
 #pragma unroll
@@ -1549,12 +1558,11 @@ void launch_router(const RouterArgs& a, int nb, hipStream_t st) {
 void launch_moe_gate_up(const MoeArgs& a, hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop) {
     constexpr int RG = 32 / GU_WAVES;
     if (a.topk >= 64 || a.E > 512 || a.E % 8 || a.I % RG) throw std::runtime_error("routing too wide");
-    const uint32_t tasks = a.nb * (a.topk + 1) * (a.I / RG);
-    (void)tasks;
     if (a.I % 32) throw std::runtime_error("expert width must be a multiple of 32");
     if (!a.act_xq) throw std::runtime_error("the gate/up kernel needs the act chunk buffer");
     if (a.H % 32 || a.H > 4096) throw std::runtime_error("expert input width must be a multiple of 32 up to 4096");
-    const uint32_t grid = a.nb * (a.topk + 1) * (a.I / 32);  // one 32-row chunk per workgroup
+    if (a.SI % 32) throw std::runtime_error("shared expert width must be a multiple of 32");
+    const uint32_t grid = a.nb * (a.topk * (a.I / 32) + a.SI / 32);  // one 32-row chunk per workgroup
     const size_t lds = xq_bytes(a.nb, a.H);
     const bool wide = a.H > 2048;
     const void* fn = a.X.bits == 3   ? (wide ? (const void*)k_moe_gate_up<RG, 3, 2> : (const void*)k_moe_gate_up<RG, 3, 1>)
@@ -1570,7 +1578,8 @@ void launch_moe_gate_up(const MoeArgs& a, hipStream_t st, hipEvent_t ev_start, h
 
 void launch_moe_down(const MoeArgs& a, hipStream_t st) {
     constexpr int RD = 2;
-    const uint32_t nch = a.I / 32;
+    if (a.I % 32 || a.SI % 32) throw std::runtime_error("expert widths must be multiples of 32");
+    const uint32_t nch = std::max(a.I, a.SI) / 32;  // lanes of a row: the wider expert's chunks
     int lpr = 2;
     while (lpr < (int)nch) lpr <<= 1;
     if (lpr > 32) throw std::runtime_error("expert width above 1024 is not supported");

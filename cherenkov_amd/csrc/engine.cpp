@@ -156,6 +156,7 @@ struct PfBufs {
     float *logits, *sg, *wts;
     uint32_t *ids, *list, *count, *tiles, *ntiles;
     float *act, *yd;
+    float* act_sh;  // [T][SI] the shared expert's activations when SI != I (else null)
     // MTP head over a chunk: the tokens after each row, rms_norm_shift(e),
     // the normed trunk streams, fc_e / fc_h outputs and the head's residual
     uint32_t* mtp_tok;
@@ -674,8 +675,9 @@ struct ChkEngine {
         // lanes (<= 16 lanes a slot at hc 4), each lane one 32-input chunk
         ensure(c.hc_lowrank % 32 == 0 && c.hc_lowrank <= 512, "hc_lowrank must be a multiple of 32 up to 512");
         ensure(c.moe_intermediate_size % 64 == 0, "expert width must be a multiple of 64 (gpu/load.rs:37-40)");
-        ensure(c.shared_expert_intermediate_size == c.moe_intermediate_size,
-               "shared expert width must equal the routed expert width");
+        ensure(c.shared_expert_intermediate_size % 64 == 0 && c.shared_expert_intermediate_size >= 64 &&
+                   c.shared_expert_intermediate_size <= 1024,
+               "shared expert width must be a multiple of 64 up to 1024");
         ensure(c.linear_key_head_dim == 128, "DeltaNet key head dim must be 128");
         ensure(c.linear_value_head_dim * 4 <= 1024, "DeltaNet value head dim too wide");
         ensure(c.linear_num_value_heads % c.linear_num_key_heads == 0, "value heads must group key heads");
@@ -848,8 +850,9 @@ struct ChkEngine {
         s.route_ids = dalloc<uint32_t>((uint64_t)LR * NB * D.topk);
         s.route_w = dalloc<float>((uint64_t)LR * NB * D.topk);
         s.sg = dalloc<float>(NB);
-        s.act = dalloc<float>((uint64_t)NB * (D.topk + 1) * D.I);
-        s.act_xq = dalloc<XqChunk>((uint64_t)NB * (D.topk + 1) * (D.I / 32));
+        // a row: topk routed slots of I activations, then the shared expert's SI
+        s.act = dalloc<float>((uint64_t)NB * (D.topk * D.I + D.SI));
+        s.act_xq = dalloc<XqChunk>((uint64_t)NB * (D.topk * D.I + D.SI) / 32);
         s.mix_out = dalloc<float>(NB * D.H);
         act = dalloc<uint64_t>((uint64_t)LR * D.E * 2);
         HIPCHK(hipMemsetAsync(act, 0, (uint64_t)LR * D.E * 2 * 8, st));
@@ -1119,6 +1122,7 @@ struct ChkEngine {
         m.nb = nb;
         m.H = D.H;
         m.I = D.I;
+        m.SI = D.SI;
         m.topk = D.topk;
         m.hc = D.hc;
         return m;
@@ -1131,8 +1135,8 @@ struct ChkEngine {
     // in f32 and as nibble-plane chunks)
     uint64_t gate_up_bytes(const LayerDev& L, int nb) const {
         return (uint64_t)nb * D.topk * 2 * expert_mat_bytes() + 2 * q4_bytes(L.moe.sh_gate) +
-               (uint64_t)nb * (D.E * 4 + D.H * 4 + (D.topk + 1) * D.I * 4 +
-                               (uint64_t)(D.topk + 1) * (D.I / 32) * sizeof(XqChunk));
+               (uint64_t)nb * (D.E * 4 + D.H * 4 + (D.topk * D.I + D.SI) * 4 +
+                               (uint64_t)((D.topk * D.I + D.SI) / 32) * sizeof(XqChunk));
     }
 
     void moe(const LayerDev& L, uint32_t route_slot, const float* x, int nb, float* hyper, const float* inj,
@@ -1682,7 +1686,7 @@ uint64_t ChkEngine::prefill_scratch_bytes(uint64_t C, bool all_logits) const {
     const uint64_t slots = D.topk + 1, f = 4;
     uint64_t b = C * 8 + C * D.hh * f;
     if (has_mtp) b += C * 4 + C * (2ull * D.H + 3ull * D.hh) * f;
-    const uint64_t plane = std::max({C * D.hh, C * D.v_dim, C * D.nh * D.hd, C * slots * D.I, C * D.H});
+    const uint64_t plane = std::max({C * D.hh, C * D.v_dim, C * D.nh * D.hd, C * slots * D.I, C * D.SI, C * D.H});
     b += plane * 2 * 2 + plane / 64 * f + 3 * C * D.H * 2;
     b += C * (3ull * D.hc + D.lowrank + D.H + (uint64_t)D.hc * (D.lowrank + D.hc)) * f;
     const uint64_t dn = C * (2ull * D.conv_dim + 2ull * D.v_dim + (2ull * pf_ab_split(D.H) + 2) * D.nv);
@@ -1690,6 +1694,7 @@ uint64_t ChkEngine::prefill_scratch_bytes(uint64_t C, bool all_logits) const {
     b += std::max(dn, at) * f;
     b += C * (D.E + 1 + 2ull * D.topk) * f + (D.E + 1ull) * C * 4 + (D.E + 1) * 4;
     b += (uint64_t)(pf_tile_bound((uint32_t)C, D.topk, D.E, 48) + pf_tile_bound((uint32_t)C, D.topk, D.E, 64)) * 4 + C * slots * (D.I + D.H) * f;
+    if (D.SI != D.I) b += C * D.SI * f;
     if (dc_supported(D.nk, D.nv, D.dk, D.dv)) b += dc_work_floats((uint32_t)C, D.nv, D.dv) * f;
     if (all_logits) b += C * D.V * f;
     if (ple_l >= 0) b += C * (ngram_heads + c.ple_embed_dim + 3ull * D.hh + D.H) * 4;
@@ -1757,7 +1762,7 @@ void ChkEngine::pf_alloc() {
         pf.mtp_fh = pfalloc<float>(C * D.hh);
         pf.mtp_hyper = pfalloc<float>(C * D.hh);
     }
-    const uint64_t plane = std::max({C * D.hh, C * D.v_dim, C * D.nh * D.hd, C * slots * D.I, C * D.H});
+    const uint64_t plane = std::max({C * D.hh, C * D.v_dim, C * D.nh * D.hd, C * slots * D.I, C * D.SI, C * D.H});
     pf.hi = pfalloc<uint4>(plane / 8);
     pf.lo = pfalloc<uint4>(plane / 8);
     pf.xs = pfalloc<float>(plane / 64);
@@ -1801,6 +1806,7 @@ void ChkEngine::pf_alloc() {
     pf.tiles = pfalloc<uint32_t>(pf_tile_bound((uint32_t)C, D.topk, D.E, 48) + pf_tile_bound((uint32_t)C, D.topk, D.E, 64));
     pf.ntiles = pfalloc<uint32_t>(2);
     pf.act = pfalloc<float>(C * slots * D.I);
+    pf.act_sh = D.SI != D.I ? pfalloc<float>(C * D.SI) : nullptr;
     pf.yd = pfalloc<float>(C * slots * D.H);
     pf.dcw = dc_supported(D.nk, D.nv, D.dk, D.dv) ? pfalloc<float>(dc_work_floats((uint32_t)C, D.nv, D.dv)) : nullptr;
     if (D.qsa) {
@@ -2061,7 +2067,9 @@ void ChkEngine::pf_attention(const LayerDev& L, uint32_t T, uint32_t pos0, const
 
 // moe (cpu.rs:504-541) over the chunk: router GEMM, per-row top-k, entries
 // grouped by expert, grouped gate/up GEMM (shared expert as the last
-// group), grouped down GEMM per entry, weighted combine + inject.
+// group), grouped down GEMM per entry, weighted combine + inject.  A shared
+// expert narrower or wider than the routed ones runs as two dense GEMMs of
+// its own (gate/up over every row, then down into each row's shared slot).
 void ChkEngine::pf_moe(const LayerDev& L, uint32_t T) {
     const uint32_t slots = D.topk + 1;
     launch_pf_router(L.moe.router, pf.bhi, pf.bmid, pf.blo, pf.logits, T, D.E, D.H, st);
@@ -2102,11 +2110,34 @@ void ChkEngine::pf_moe(const LayerDev& L, uint32_t T) {
     dn.tiles = pf.tiles + pf_tile_bound(T, D.topk, D.E, tr);
     dn.ntiles = pf.ntiles + 1;
     // (also counts the layer's expert activity)
+    const bool shared_grouped = D.SI == D.I;
     launch_pf_group(pf.ids, T, D.topk, D.E, pf.cap, pf.list, pf.count, pf.tiles, pf.ntiles, act,
-                    L.moe.record_layer, tr, st);
+                    L.moe.record_layer, tr, shared_grouped, st);
     launch_pf_gemm_args(gu, PE_SILU_MUL, pf_tile_bound(T, D.topk, D.E, tr), st);
+    PfGemmArgs sh{};
+    if (!shared_grouped) {
+        sh.seg[0] = PfSeg{L.moe.sh_gate, pf.act_sh, D.SI, 0};
+        sh.seg[1].m = L.moe.sh_up;
+        sh.nseg = 1;
+        sh.N = D.SI;
+        sh.K = D.H;
+        sh.M = T;
+        sh.xhi = pf.hi;
+        sh.xlo = pf.lo;
+        sh.xs = pf.xs;
+        launch_pf_gemm_args(sh, PE_SILU_MUL, (T + 63) / 64, st);
+    }
     launch_pf_xprep(pf.act, D.I, T * slots, D.I, pf.hi, pf.lo, pf.xs, st);
     launch_pf_gemm_args(dn, PE_STORE, pf_tile_bound(T, D.topk, D.E, 64), st);
+    if (!shared_grouped) {
+        // row t's shared slot of yd: t (k + 1) + k
+        launch_pf_xprep(pf.act_sh, D.SI, T, D.SI, pf.hi, pf.lo, pf.xs, st);
+        sh.seg[0] = PfSeg{L.moe.sh_down, pf.yd + (uint64_t)D.topk * D.H, slots * D.H, 0};
+        sh.seg[1] = PfSeg{};
+        sh.N = D.H;
+        sh.K = D.SI;
+        launch_pf_gemm_args(sh, PE_STORE, (T + 63) / 64, st);
+    }
     launch_pf_moe_combine(pf.yd, pf.wts, pf.sg, pf.inj_m, pf.hyper, T, D.H, D.topk, D.hc, st);
 }
 

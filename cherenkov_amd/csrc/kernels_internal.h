@@ -104,12 +104,16 @@ struct MoeArgs {
     const uint32_t* ids;   // [nb][topk]
     const float* w;        // [nb][topk]
     const float* sg;       // [nb] shared gate logit
-    float* act;            // [nb][topk + 1][I]
-    XqChunk* act_xq;       // [nb][topk + 1][I / 32] act in nibble planes
+    // a row's act: topk routed slots of I values, then the shared
+    // expert's SI (rows of topk I + SI values; act_xq likewise in 32-value
+    // chunks)
+    float* act;            // [nb][topk I + SI]
+    XqChunk* act_xq;       // [nb][(topk I + SI) / 32] act in nibble planes
     float* hyper;          // [nb][hc H] (null: no inject)
     const float* inj;      // [nb][hc]
     float* raw_out;        // [nb][H] (optional)
     uint32_t nb, H, I, topk, hc;
+    uint32_t SI;           // the shared expert's width
 };
 
 // Wave64 reductions through DPP (quad_perm, row_ror, row_bcast): no LDS
@@ -440,7 +444,7 @@ void launch_pf_route(const float* logits, uint32_t T, uint32_t E, uint32_t topk,
                      const uint4* bmid, const uint4* blo, float* sg, uint32_t H, hipStream_t st);
 void launch_pf_group(const uint32_t* ids, uint32_t T, uint32_t topk, uint32_t E, uint32_t cap, uint32_t* list,
                      uint32_t* count, uint32_t* tiles, uint32_t* ntiles, uint64_t* act, uint32_t layer, uint32_t tr,
-                     hipStream_t st);
+                     bool shared, hipStream_t st);
 uint32_t pf_tile_bound(uint32_t T, uint32_t topk, uint32_t E, uint32_t tr);
 void launch_pf_moe_combine(const float* yd, const float* wts, const float* sg, const float* inj, float* hyper,
                            uint32_t T, uint32_t H, uint32_t topk, uint32_t hc, hipStream_t st);

@@ -1071,7 +1071,9 @@ __global__ void __launch_bounds__(256) k_pf_route(const float* __restrict__ logi
 // topk, E, tr), ntiles[1] of them (the gate/up and down GEMMs tile the same
 // entries differently).
 // With `act`, also the expert activity counters of `layer` (selected rows
-// and selections, as the decode step's activity count does).  One workgroup.
+// and selections, as the decode step's activity count does).  Without
+// `shared`, group E gets no rows or tiles (a shared expert of another width
+// runs as dense GEMMs of its own).  One workgroup.
 constexpr uint32_t PG_WG = 1024;  // threads of the grouping workgroup (one group each)
 
 __global__ void __launch_bounds__(PG_WG) k_pf_group(const uint32_t* __restrict__ ids, uint32_t T, uint32_t topk,
@@ -1079,7 +1081,7 @@ __global__ void __launch_bounds__(PG_WG) k_pf_group(const uint32_t* __restrict__
                                                     uint32_t* __restrict__ count, uint32_t* __restrict__ tiles,
                                                     uint32_t* __restrict__ ntiles,
                                                     unsigned long long* __restrict__ act, uint32_t layer,
-                                                    uint32_t tr) {
+                                                    uint32_t tr, uint32_t shared) {
     __shared__ uint32_t cnt[PG_WG];
     __shared__ uint32_t wsum[PG_WG / 64];
     const uint32_t tau = threadIdx.x, lane = tau & 63, wv = tau >> 6;
@@ -1092,9 +1094,10 @@ __global__ void __launch_bounds__(PG_WG) k_pf_group(const uint32_t* __restrict__
         const uint32_t p = atomicAdd(&cnt[e], 1u);
         list[(size_t)e * cap + p] = t * slots + r;
     }
-    for (uint32_t t = tau; t < T; t += PG_WG) list[(size_t)E * cap + t] = t * slots + topk;
+    if (shared)
+        for (uint32_t t = tau; t < T; t += PG_WG) list[(size_t)E * cap + t] = t * slots + topk;
     __syncthreads();
-    if (tau == 0) cnt[E] = T;
+    if (tau == 0) cnt[E] = shared ? T : 0;
     __syncthreads();
     // tiles per group (thread e takes group e): multi-tile counts in the
     // high half-word, single tiles in the low one, one workgroup prefix sum
@@ -1550,13 +1553,13 @@ void launch_pf_route(const float* logits, uint32_t T, uint32_t E, uint32_t topk,
 
 void launch_pf_group(const uint32_t* ids, uint32_t T, uint32_t topk, uint32_t E, uint32_t cap, uint32_t* list,
                      uint32_t* count, uint32_t* tiles, uint32_t* ntiles, uint64_t* act, uint32_t layer, uint32_t tr,
-                     hipStream_t st) {
+                     bool shared, hipStream_t st) {
     if (E + 1 > PG_WG) throw std::runtime_error("prefill grouping supports at most 1023 experts");
     if (tr != 48 && tr != 64) throw std::runtime_error("prefill grouping: tiles of 48 or 64 rows");
     if (pf_tile_bound(T, topk, E, tr) >= 0x10000u || pf_tile_bound(T, topk, E, 64) >= 0x10000u)
         throw std::runtime_error("prefill grouping: too many tiles");
     k_pf_group<<<1, PG_WG, 0, st>>>(ids, T, topk, E, cap, list, count, tiles, ntiles,
-                                    reinterpret_cast<unsigned long long*>(act), layer, tr);
+                                    reinterpret_cast<unsigned long long*>(act), layer, tr, shared ? 1u : 0u);
 }
 
 // Tiles of a grouped GEMM: every group's rows in tr-row tiles, one more

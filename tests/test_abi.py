@@ -67,6 +67,10 @@ def test_load_validates_before_touching_the_device():
     c = presets.tiny()
     c.hc_lowrank = 544
     cases.append((c, abi.ChkOptions(4, 0, 64, 0), "hc_lowrank must be a multiple of 32 up to 512"))
+    for si in (96, 1088):
+        c = presets.tiny()
+        c.shared_expert_intermediate_size = si
+        cases.append((c, abi.ChkOptions(4, 0, 64, 0), "shared expert width must be a multiple of 64 up to 1024"))
     c = presets.tiny()
     cases.append((c, abi.ChkOptions(4, 4, 64, 0), "drafts must be 0..=3"))
     c = presets.tiny()
