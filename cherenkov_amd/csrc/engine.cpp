@@ -155,6 +155,9 @@ struct PfBufs {
     float *q_raw, *k_raw, *v_raw, *idx_raw, *q_ready, *attn_out;
     float *logits, *sg, *wts;
     uint32_t *ids, *list, *count, *tiles, *ntiles;
+    uint2* tinfo;   // per tile of both lists: (group's first grouped row, group's rows)
+    uint32_t* goff;  // [E + 1] each group's first grouped row of act / yd
+    uint32_t* gpos;  // [T][k + 1] each entry's group << 22 | place in the group
     float *act, *yd;
     float* act_sh;  // [T][SI] the shared expert's activations when SI != I (else null)
     // MTP head over a chunk: the tokens after each row, rms_norm_shift(e),
@@ -1693,7 +1696,8 @@ uint64_t ChkEngine::prefill_scratch_bytes(uint64_t C, bool all_logits) const {
     const uint64_t at = C * (2ull * D.nh * D.hd + 2ull * D.kv_row + D.idx_out + 2ull * D.nh * D.hd);
     b += std::max(dn, at) * f;
     b += C * (D.E + 1 + 2ull * D.topk) * f + (D.E + 1ull) * C * 4 + (D.E + 1) * 4;
-    b += (uint64_t)(pf_tile_bound((uint32_t)C, D.topk, D.E, 48) + pf_tile_bound((uint32_t)C, D.topk, D.E, 64)) * 4 + C * slots * (D.I + D.H) * f;
+    b += (uint64_t)(pf_tile_bound((uint32_t)C, D.topk, D.E, 48) + pf_tile_bound((uint32_t)C, D.topk, D.E, 64)) * 12 +
+         C * slots * (D.I + D.H) * f + C * slots * 4 + (D.E + 1) * 4;
     if (D.SI != D.I) b += C * D.SI * f;
     if (dc_supported(D.nk, D.nv, D.dk, D.dv)) b += dc_work_floats((uint32_t)C, D.nv, D.dv) * f;
     if (all_logits) b += C * D.V * f;
@@ -1804,6 +1808,9 @@ void ChkEngine::pf_alloc() {
     pf.list = pfalloc<uint32_t>((D.E + 1) * C);
     pf.count = pfalloc<uint32_t>(D.E + 1);
     pf.tiles = pfalloc<uint32_t>(pf_tile_bound((uint32_t)C, D.topk, D.E, 48) + pf_tile_bound((uint32_t)C, D.topk, D.E, 64));
+    pf.tinfo = pfalloc<uint2>(pf_tile_bound((uint32_t)C, D.topk, D.E, 48) + pf_tile_bound((uint32_t)C, D.topk, D.E, 64));
+    pf.goff = pfalloc<uint32_t>(D.E + 1);
+    pf.gpos = pfalloc<uint32_t>(C * slots);
     pf.ntiles = pfalloc<uint32_t>(2);
     pf.act = pfalloc<float>(C * slots * D.I);
     pf.act_sh = D.SI != D.I ? pfalloc<float>(C * D.SI) : nullptr;
@@ -2067,7 +2074,10 @@ void ChkEngine::pf_attention(const LayerDev& L, uint32_t T, uint32_t pos0, const
 
 // moe (cpu.rs:504-541) over the chunk: router GEMM, per-row top-k, entries
 // grouped by expert, grouped gate/up GEMM (shared expert as the last
-// group), grouped down GEMM per entry, weighted combine + inject.  A shared
+// group), grouped down GEMM per entry, weighted combine + inject.  The
+// activations and down outputs are stored in grouped order (each expert's
+// rows together), so the down GEMM's tiles read and write row ranges; the
+// combine gathers each token's rows by their grouped positions.  A shared
 // expert narrower or wider than the routed ones runs as two dense GEMMs of
 // its own (gate/up over every row, then down into each row's shared slot).
 void ChkEngine::pf_moe(const LayerDev& L, uint32_t T) {
@@ -2087,8 +2097,8 @@ void ChkEngine::pf_moe(const LayerDev& L, uint32_t T) {
     gu.xlo = pf.lo;
     gu.xs = pf.xs;
     gu.list = pf.list;
-    gu.count = pf.count;
     gu.tiles = pf.tiles;
+    gu.tinfo = pf.tinfo;
     gu.ntiles = pf.ntiles;
     gu.cap = pf.cap;
     gu.div = slots;
@@ -2101,6 +2111,7 @@ void ChkEngine::pf_moe(const LayerDev& L, uint32_t T) {
     dn.seg[1] = PfSeg{};
     dn.N = D.H;
     dn.K = D.I;
+    dn.list = nullptr;  // rows in grouped order: the tile's own range
     dn.div = 1;
     // experts hold ~T k / E rows: gate/up in 48-row tiles where it takes
     // the staged-scale form (Q4 records); the down GEMM, 8 groups deep,
@@ -2108,10 +2119,11 @@ void ChkEngine::pf_moe(const LayerDev& L, uint32_t T) {
     const uint32_t tr = pf_gemm_staged(gu, PE_SILU_MUL) ? 48 : 64;
     gu.tile_rows = tr;
     dn.tiles = pf.tiles + pf_tile_bound(T, D.topk, D.E, tr);
+    dn.tinfo = pf.tinfo + pf_tile_bound(T, D.topk, D.E, tr);
     dn.ntiles = pf.ntiles + 1;
     // (also counts the layer's expert activity)
     const bool shared_grouped = D.SI == D.I;
-    launch_pf_group(pf.ids, T, D.topk, D.E, pf.cap, pf.list, pf.count, pf.tiles, pf.ntiles, act,
+    launch_pf_group(pf.ids, T, D.topk, D.E, pf.cap, pf.list, pf.count, pf.tiles, pf.ntiles, pf.tinfo, pf.goff, pf.gpos, act,
                     L.moe.record_layer, tr, shared_grouped, st);
     launch_pf_gemm_args(gu, PE_SILU_MUL, pf_tile_bound(T, D.topk, D.E, tr), st);
     PfGemmArgs sh{};
@@ -2130,15 +2142,15 @@ void ChkEngine::pf_moe(const LayerDev& L, uint32_t T) {
     launch_pf_xprep(pf.act, D.I, T * slots, D.I, pf.hi, pf.lo, pf.xs, st);
     launch_pf_gemm_args(dn, PE_STORE, pf_tile_bound(T, D.topk, D.E, 64), st);
     if (!shared_grouped) {
-        // row t's shared slot of yd: t (k + 1) + k
+        // token t's shared slot of yd: grouped row T k + t, after the routed rows
         launch_pf_xprep(pf.act_sh, D.SI, T, D.SI, pf.hi, pf.lo, pf.xs, st);
-        sh.seg[0] = PfSeg{L.moe.sh_down, pf.yd + (uint64_t)D.topk * D.H, slots * D.H, 0};
+        sh.seg[0] = PfSeg{L.moe.sh_down, pf.yd + (uint64_t)T * D.topk * D.H, D.H, 0};
         sh.seg[1] = PfSeg{};
         sh.N = D.H;
         sh.K = D.SI;
         launch_pf_gemm_args(sh, PE_STORE, (T + 63) / 64, st);
     }
-    launch_pf_moe_combine(pf.yd, pf.wts, pf.sg, pf.inj_m, pf.hyper, T, D.H, D.topk, D.hc, st);
+    launch_pf_moe_combine(pf.yd, pf.goff, pf.gpos, pf.wts, pf.sg, pf.inj_m, pf.hyper, T, D.H, D.topk, D.hc, st);
 }
 
 void ChkEngine::prefill_gemm(const uint32_t* toks, uint32_t n, uint32_t next_after, bool all_logits,

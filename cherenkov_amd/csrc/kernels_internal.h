@@ -312,10 +312,10 @@ struct PfGemmArgs {
     const uint4* xhi;
     const uint4* xlo;
     const float* xs;
-    // grouped rows (list non-null)
-    const uint32_t* list;    // [groups][cap] entries
-    const uint32_t* count;   // [groups]
-    const uint32_t* tiles;   // (group << 16 | 64-row tile)
+    // grouped rows (tinfo non-null)
+    const uint32_t* list;    // [groups][cap] entries: A row list[g][m] / div (else off + m)
+    const uint32_t* tiles;   // (group << 16 | tile)
+    const uint2* tinfo;      // per tile: (group's first row in grouped order, group's row count)
     const uint32_t* ntiles;
     uint32_t cap, div;
     ExpertsDev X;            // routed-expert records for groups < X.experts
@@ -443,11 +443,12 @@ void launch_pf_route(const float* logits, uint32_t T, uint32_t E, uint32_t topk,
                      float* wts, uint32_t* last_ids, float* last_wts, const uint16_t* shared_gate, const uint4* bhi,
                      const uint4* bmid, const uint4* blo, float* sg, uint32_t H, hipStream_t st);
 void launch_pf_group(const uint32_t* ids, uint32_t T, uint32_t topk, uint32_t E, uint32_t cap, uint32_t* list,
-                     uint32_t* count, uint32_t* tiles, uint32_t* ntiles, uint64_t* act, uint32_t layer, uint32_t tr,
-                     bool shared, hipStream_t st);
+                     uint32_t* count, uint32_t* tiles, uint32_t* ntiles, uint2* tinfo, uint32_t* goff, uint32_t* pos,
+                     uint64_t* act, uint32_t layer, uint32_t tr, bool shared, hipStream_t st);
 uint32_t pf_tile_bound(uint32_t T, uint32_t topk, uint32_t E, uint32_t tr);
-void launch_pf_moe_combine(const float* yd, const float* wts, const float* sg, const float* inj, float* hyper,
-                           uint32_t T, uint32_t H, uint32_t topk, uint32_t hc, hipStream_t st);
+void launch_pf_moe_combine(const float* yd, const uint32_t* goff, const uint32_t* pos, const float* wts, const float* sg,
+                           const float* inj, float* hyper, uint32_t T, uint32_t H, uint32_t topk, uint32_t hc,
+                           hipStream_t st);
 void launch_pf_embed(const uint32_t* tokens, const Q4Mat& emb, float* hyper, uint32_t H, uint32_t hc, uint32_t T,
                      hipStream_t st);
 // conv + norms, decay / beta, then the scan: chunked (dnscan.hip) when

@@ -234,10 +234,13 @@ __global__ void __launch_bounds__(256) k_pf_hc_prep(float* __restrict__ hyper, c
 // the group's scale.  Two workgroups share a CU.
 //
 // Rows: dense (row m of A and Y), or grouped: a tile list names (group,
-// tile); list[group][m] is an entry e, A row e / div, Y row e.  The
-// routed-expert GEMMs group the (token, slot) entries e = t (k+1) + slot
-// by expert (gate/up read token t, down reads the entry's activation);
-// group == X.experts is the shared expert.
+// tile) and, per tile, the group's first row in grouped order (off) and
+// its row count; Y row off + m, A row off + m, or, with a list,
+// list[group][m] / div.  The routed-expert GEMMs group the (token, slot)
+// entries e = t (k+1) + slot by expert: gate/up reads token t (list entry
+// e, div k+1) and writes the entry's activation at its grouped position,
+// down reads and writes grouped rows; group == X.experts is the shared
+// expert.
 //
 // Epilogues: PE_STORE (concatenated segments, each with its own output),
 // PE_HC_UP (the four 16-wide tiles of a wave are the hc streams of the same
@@ -288,7 +291,8 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, col = lane & 15, kq = lane >> 4;
     const uint32_t wn = wave_id();
     uint32_t bx = blockIdx.x, by = blockIdx.y;
-    if (a.list) {
+    const bool grouped = a.tinfo != nullptr;
+    if (grouped) {
         // XCD-aware order: workgroups are dealt to the 8 XCDs round-robin
         // by linear id, so linear ids L = 8 s + x map to items w = x C + s
         // % C of chunk s / C (C = 2 gridDim.x items: every column block of
@@ -301,14 +305,18 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
         bx = w % gridDim.x;
         by = w / gridDim.x;
     }
-    uint32_t grp = 0, mt = by;
-    if (a.list) {
+    // grouped: the tile's group, its first row in grouped order and the
+    // group's row count come with the tile (one round trip)
+    uint32_t grp = 0, mt = by, toff = 0, M = a.M;
+    if (grouped) {
         if (by >= *a.ntiles) return;
         const uint32_t tv = a.tiles[by];
+        const uint2 ti = a.tinfo[by];
         grp = tv >> 16;
         mt = tv & 0xffffu;
+        toff = ti.x;
+        M = ti.y;
     }
-    const uint32_t M = a.list ? a.count[grp] : a.M;
     const uint32_t m0 = mt * TR;
     if (m0 >= M) return;
     const uint32_t* list = a.list ? a.list + (size_t)grp * a.cap : nullptr;
@@ -390,11 +398,10 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
     uint32_t arow_ld, arow_xs;
     {
         const uint32_t m = min(m0 + min(lrow, TR - 1), M - 1);
-        arow_ld = list ? list[m] / a.div : m;
+        arow_ld = list ? list[m] / a.div : toff + m;
         const uint32_t mx = min(m0 + (tid & 63), M - 1);
-        const uint32_t e = list ? list[mx] : mx;
-        arow_xs = list ? e / a.div : mx;
-        if (tid < 64) sRow[tid] = e;
+        arow_xs = list ? list[mx] / a.div : toff + mx;
+        if (tid < 64) sRow[tid] = toff + mx;
     }
     const u32x4* ghi = reinterpret_cast<const u32x4*>(a.xhi) + (size_t)arow_ld * KB + lkb;
     const u32x4* glo = reinterpret_cast<const u32x4*>(a.xlo) + (size_t)arow_ld * KB + lkb;
@@ -592,7 +599,7 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             const uint32_t m = min(m0 + i * 16 + col, M - 1);
-            const uint32_t ar = list ? list[m] / a.div : m;
+            const uint32_t ar = list ? list[m] / a.div : toff + m;
             const float4* xp = reinterpret_cast<const float4*>(a.xs + (size_t)ar * G + kc);
             xg[i][0] = xp[0];
             xg[i][1] = xp[1];
@@ -1070,6 +1077,11 @@ __global__ void __launch_bounds__(256) k_pf_route(const float* __restrict__ logi
 // A second such list of 64-row tiles follows at tiles + pf_tile_bound(T,
 // topk, E, tr), ntiles[1] of them (the gate/up and down GEMMs tile the same
 // entries differently).
+// Per tile also tinfo[] = (the group's first row in grouped order, its row
+// count), per group goff[] = that first row, and per entry pos[] = its
+// group << 22 | its place in the group (grouped row goff[group] + place;
+// every token's shared slot is place t of group E, whose rows start where
+// the routed entries end, at T k).
 // With `act`, also the expert activity counters of `layer` (selected rows
 // and selections, as the decode step's activity count does).  Without
 // `shared`, group E gets no rows or tiles (a shared expert of another width
@@ -1079,10 +1091,12 @@ constexpr uint32_t PG_WG = 1024;  // threads of the grouping workgroup (one grou
 __global__ void __launch_bounds__(PG_WG) k_pf_group(const uint32_t* __restrict__ ids, uint32_t T, uint32_t topk,
                                                     uint32_t E, uint32_t cap, uint32_t* __restrict__ list,
                                                     uint32_t* __restrict__ count, uint32_t* __restrict__ tiles,
-                                                    uint32_t* __restrict__ ntiles,
+                                                    uint32_t* __restrict__ ntiles, uint2* __restrict__ tinfo,
+                                                    uint32_t* __restrict__ goff, uint32_t* __restrict__ pos,
                                                     unsigned long long* __restrict__ act, uint32_t layer,
                                                     uint32_t tr, uint32_t shared) {
     __shared__ uint32_t cnt[PG_WG];
+    __shared__ uint32_t offs[PG_WG];
     __shared__ uint32_t wsum[PG_WG / 64];
     const uint32_t tau = threadIdx.x, lane = tau & 63, wv = tau >> 6;
     cnt[tau] = 0;
@@ -1093,15 +1107,34 @@ __global__ void __launch_bounds__(PG_WG) k_pf_group(const uint32_t* __restrict__
         const uint32_t e = min(ids[i], E - 1);
         const uint32_t p = atomicAdd(&cnt[e], 1u);
         list[(size_t)e * cap + p] = t * slots + r;
+        pos[t * slots + r] = e << 22 | p;
     }
-    if (shared)
-        for (uint32_t t = tau; t < T; t += PG_WG) list[(size_t)E * cap + t] = t * slots + topk;
+    for (uint32_t t = tau; t < T; t += PG_WG) {
+        if (shared) list[(size_t)E * cap + t] = t * slots + topk;
+        pos[t * slots + topk] = E << 22 | t;
+    }
     __syncthreads();
     if (tau == 0) cnt[E] = shared ? T : 0;
     __syncthreads();
+    const uint32_t e = tau;
+    // grouped order: group e's rows start at the sum of the counts before it
+    {
+        const uint32_t c = e <= E ? cnt[e] : 0u;
+        uint32_t incl = c;
+        for (int d = 1; d < 64; d <<= 1) {
+            const uint32_t o = __shfl_up(incl, d, 64);
+            if ((int)lane >= d) incl += o;
+        }
+        if (lane == 63) wsum[wv] = incl;
+        __syncthreads();
+        uint32_t off = incl - c;
+        for (uint32_t k = 0; k < wv; ++k) off += wsum[k];
+        offs[e] = off;
+        if (e <= E) goff[e] = off;
+        __syncthreads();  // offs complete; wsum free again
+    }
     // tiles per group (thread e takes group e): multi-tile counts in the
     // high half-word, single tiles in the low one, one workgroup prefix sum
-    const uint32_t e = tau;
     if (e <= E) count[e] = cnt[e];
     if (act && e < E && cnt[e]) {
         unsigned long long* ae = act + ((size_t)layer * E + e) * 2;
@@ -1128,7 +1161,11 @@ __global__ void __launch_bounds__(PG_WG) k_pf_group(const uint32_t* __restrict__
         for (uint32_t k = 0; k < wv; ++k) off += wsum[k];
         for (uint32_t k = 0; k < PG_WG / 64; ++k) all += wsum[k];
         const uint32_t start = nt > 1 ? off >> 16 : (all >> 16) + (off & 0xffffu);
-        for (uint32_t q = 0; q < nt; ++q) dst[start + q] = e << 16 | q;
+        uint2* tdst = tinfo + (dst - tiles);
+        for (uint32_t q = 0; q < nt; ++q) {
+            dst[start + q] = e << 16 | q;
+            tdst[start + q] = make_uint2(offs[e], cnt[e]);
+        }
         if (tau == PG_WG - 1) ntiles[h] = (all >> 16) + (all & 0xffffu);
         // bound of the first list, as pf_tile_bound computes it
         const uint32_t n = (T * topk + tr - 1) / tr + E + (T + tr - 1) / tr + 1 + (E + 1);
@@ -1137,13 +1174,17 @@ __global__ void __launch_bounds__(PG_WG) k_pf_group(const uint32_t* __restrict__
 }
 
 // out[t][n] = sum_r w[t][r] yd[t][r][n] + sigmoid(sg[t]) yd[t][k][n]
-// (cpu.rs:527-540), then hyper[t][g H + n] += out inj[t][g].
+// (cpu.rs:527-540), then hyper[t][g H + n] += out inj[t][g].  Slot r of
+// token t is yd row goff[q >> 22] + (q & 0x3fffff), q = pos[t (k+1) + r]
+// (the down GEMM's grouped order).
 // K > 0: K routed slots known at compile time, a thread takes outputs
 // 4 n .. + 3 with every slot's values in flight before the first is summed;
 // K = 0: any topk, one output per thread.  Slots are summed in order either
 // way.
 template <int K>
-__global__ void __launch_bounds__(256) k_pf_moe_combine(const float* __restrict__ yd, const float* __restrict__ wts,
+__global__ void __launch_bounds__(256) k_pf_moe_combine(const float* __restrict__ yd, const uint32_t* __restrict__ goff,
+                                                        const uint32_t* __restrict__ pos,
+                                                        const float* __restrict__ wts,
                                                         const float* __restrict__ sg, const float* __restrict__ inj,
                                                         float* __restrict__ hyper, uint32_t H, uint32_t topk,
                                                         uint32_t hc) {
@@ -1151,19 +1192,24 @@ __global__ void __launch_bounds__(256) k_pf_moe_combine(const float* __restrict_
     if constexpr (K == 0) {
         const uint32_t n = blockIdx.x * CHK_WG + threadIdx.x;
         if (n >= H) return;
-        const float* y = yd + (size_t)t * slots * H + n;
+        const uint32_t* pt = pos + (size_t)t * slots;
+        auto row = [&](uint32_t r) { return (size_t)(goff[pt[r] >> 22] + (pt[r] & 0x3fffffu)); };
         float out = 0.0f;
-        for (uint32_t r = 0; r < topk; ++r) out += wts[(size_t)t * topk + r] * y[(size_t)r * H];
-        out += sigmoidf_(sg[t]) * y[(size_t)topk * H];
+        for (uint32_t r = 0; r < topk; ++r) out += wts[(size_t)t * topk + r] * yd[row(r) * H + n];
+        out += sigmoidf_(sg[t]) * yd[row(topk) * H + n];
         float* hy = hyper + (size_t)t * hc * H + n;
         for (uint32_t g = 0; g < hc; ++g) hy[(size_t)g * H] += out * inj[(size_t)t * hc + g];
     } else {
         const uint32_t n = (blockIdx.x * CHK_WG + threadIdx.x) * 4;
         if (n >= H) return;
-        const float* y = yd + (size_t)t * slots * H + n;
+        uint32_t pr[K + 1];
+#pragma unroll
+        for (int r = 0; r <= K; ++r) pr[r] = pos[(size_t)t * slots + r];
+#pragma unroll
+        for (int r = 0; r <= K; ++r) pr[r] = goff[pr[r] >> 22] + (pr[r] & 0x3fffffu);
         float4 v[K + 1];
 #pragma unroll
-        for (int r = 0; r <= K; ++r) v[r] = *reinterpret_cast<const float4*>(y + (size_t)r * H);
+        for (int r = 0; r <= K; ++r) v[r] = *reinterpret_cast<const float4*>(yd + (size_t)pr[r] * H + n);
         float out[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int r = 0; r < K; ++r) {
@@ -1552,13 +1598,14 @@ void launch_pf_route(const float* logits, uint32_t T, uint32_t E, uint32_t topk,
 }
 
 void launch_pf_group(const uint32_t* ids, uint32_t T, uint32_t topk, uint32_t E, uint32_t cap, uint32_t* list,
-                     uint32_t* count, uint32_t* tiles, uint32_t* ntiles, uint64_t* act, uint32_t layer, uint32_t tr,
-                     bool shared, hipStream_t st) {
+                     uint32_t* count, uint32_t* tiles, uint32_t* ntiles, uint2* tinfo, uint32_t* goff, uint32_t* pos,
+                     uint64_t* act, uint32_t layer, uint32_t tr, bool shared, hipStream_t st) {
     if (E + 1 > PG_WG) throw std::runtime_error("prefill grouping supports at most 1023 experts");
+    if ((uint64_t)T * (topk + 1) >= (1u << 22)) throw std::runtime_error("prefill grouping: too many entries");
     if (tr != 48 && tr != 64) throw std::runtime_error("prefill grouping: tiles of 48 or 64 rows");
     if (pf_tile_bound(T, topk, E, tr) >= 0x10000u || pf_tile_bound(T, topk, E, 64) >= 0x10000u)
         throw std::runtime_error("prefill grouping: too many tiles");
-    k_pf_group<<<1, PG_WG, 0, st>>>(ids, T, topk, E, cap, list, count, tiles, ntiles,
+    k_pf_group<<<1, PG_WG, 0, st>>>(ids, T, topk, E, cap, list, count, tiles, ntiles, tinfo, goff, pos,
                                     reinterpret_cast<unsigned long long*>(act), layer, tr, shared ? 1u : 0u);
 }
 
@@ -1569,13 +1616,14 @@ uint32_t pf_tile_bound(uint32_t T, uint32_t topk, uint32_t E, uint32_t tr) {
     return (n + 15) & ~15u;
 }
 
-void launch_pf_moe_combine(const float* yd, const float* wts, const float* sg, const float* inj, float* hyper,
-                           uint32_t T, uint32_t H, uint32_t topk, uint32_t hc, hipStream_t st) {
+void launch_pf_moe_combine(const float* yd, const uint32_t* goff, const uint32_t* pos, const float* wts, const float* sg,
+                           const float* inj, float* hyper, uint32_t T, uint32_t H, uint32_t topk, uint32_t hc,
+                           hipStream_t st) {
     if (!T) return;
     if (topk == 10 && H % 4 == 0)
-        k_pf_moe_combine<10><<<dim3((H / 4 + 255) / 256, T), CHK_WG, 0, st>>>(yd, wts, sg, inj, hyper, H, topk, hc);
+        k_pf_moe_combine<10><<<dim3((H / 4 + 255) / 256, T), CHK_WG, 0, st>>>(yd, goff, pos, wts, sg, inj, hyper, H, topk, hc);
     else
-        k_pf_moe_combine<0><<<dim3((H + 255) / 256, T), CHK_WG, 0, st>>>(yd, wts, sg, inj, hyper, H, topk, hc);
+        k_pf_moe_combine<0><<<dim3((H + 255) / 256, T), CHK_WG, 0, st>>>(yd, goff, pos, wts, sg, inj, hyper, H, topk, hc);
 }
 
 void launch_pf_embed(const uint32_t* tokens, const Q4Mat& emb, float* hyper, uint32_t H, uint32_t hc, uint32_t T,
