@@ -316,11 +316,16 @@ __global__ void __launch_bounds__(256) k_attn_part(AttnArgs a) {
     __shared__ float sp[G][CH];
     __shared__ float sml[G][2];
     __shared__ __align__(16) float so[NS][G][HD];
-    // blockIdx.x = (kv head, slice of G of its query heads): a kv head's
-    // query heads may be split over several workgroups for parallelism
+    // x = (kv head, slice of G of its query heads): a kv head's query heads
+    // may be split over several workgroups for parallelism.  Workgroups are
+    // dealt to the 8 XCDs round-robin by linear id; the ids are remapped so
+    // that the gridDim.x workgroups of one (chunk, row) sit 8 apart, on one
+    // XCD, and the kv heads' chunks come from HBM once into that XCD's L2
+    // (the ids past the last whole span of 8 gridDim.x keep their places).
+    uint32_t x = blockIdx.x, yz = blockIdx.z * gridDim.y + blockIdx.y;
     const uint32_t split = (a.nh / a.nkv) / G;
-    const uint32_t hk = blockIdx.x / split, h0 = hk * (a.nh / a.nkv) + (blockIdx.x % split) * G;
-    const uint32_t c = blockIdx.y, b = blockIdx.z, t = threadIdx.x;
+    const uint32_t hk = x / split, h0 = hk * (a.nh / a.nkv) + (x % split) * G;
+    const uint32_t c = yz % gridDim.y, b = yz / gridDim.y, t = threadIdx.x;
     const uint32_t T = a.pos[b] + 1;  // causal: rows see positions <= their own
     const uint32_t t0 = c * CH;
     if (t0 >= T) return;
@@ -519,6 +524,15 @@ __global__ void __launch_bounds__(256) k_attn_combine(AttnArgs a) {
 #pragma unroll
             for (int k = 0; k < 8; ++k) o += v0[k] * sw[c + 4 * k];
             c += 32;
+        }
+        // long contexts: 32 loads in flight per round trip (the same
+        // ascending chunk order as the 8-wide rounds)
+        for (; c + 124 < nc; c += 128) {
+            float v[32];
+#pragma unroll
+            for (int k = 0; k < 32; ++k) v[k] = pd[(size_t)(c + 4 * k) * (hd + 2)];
+#pragma unroll
+            for (int k = 0; k < 32; ++k) o += v[k] * sw[c + 4 * k];
         }
         for (; c + 28 < nc; c += 32) {
             float v[8];
