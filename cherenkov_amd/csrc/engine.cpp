@@ -2113,11 +2113,10 @@ void ChkEngine::pf_moe(const LayerDev& L, uint32_t T) {
     dn.K = D.I;
     dn.list = nullptr;  // rows in grouped order: the tile's own range
     dn.div = 1;
-    // experts hold ~T k / E rows: gate/up in 48-row tiles where it takes
-    // the staged-scale form (Q4 records); the down GEMM, 8 groups deep,
-    // keeps 64-row tiles (fewer workgroups to start and finish)
-    const uint32_t tr = pf_gemm_staged(gu, PE_SILU_MUL) ? 48 : 64;
-    gu.tile_rows = tr;
+    // experts hold from one row to over a thousand (T k / E on average):
+    // both GEMMs take 64-row tiles, whose empty 16-row slices the kernel
+    // skips
+    const uint32_t tr = 64;
     dn.tiles = pf.tiles + pf_tile_bound(T, D.topk, D.E, tr);
     dn.tinfo = pf.tinfo + pf_tile_bound(T, D.topk, D.E, tr);
     dn.ntiles = pf.ntiles + 1;

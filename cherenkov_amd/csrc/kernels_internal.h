@@ -331,7 +331,6 @@ struct PfGemmArgs {
     float* out;              // [M][H]
     uint32_t H, hc;
     uint32_t vec4;           // set by the launcher: outputs leave as 16-byte stores
-    uint32_t tile_rows;      // rows per tile: 64 (0) or 48 (grouped gate/up)
 };
 
 // DeltaNet prefill (conv, decay/beta, sequential scan) over T rows.

@@ -266,7 +266,8 @@ CHK_DEV h8 pf_unpack(uint32_t w, const Q4Consts& qk) {
 // with xs split into three bf16 terms so every product is exact).  Needs
 // G % 8 == 0 and 16-byte aligned rows; otherwise each lane loads its scale
 // and bias per group and folds both in the loop.  SBL launches also take
-// the transposed tile and may use tiles of NI = 3 slices (48 rows).
+// the transposed tile.  NI: 16-row slices per tile (a tile computes only
+// the slices that hold rows).
 // BITS: the routed-expert records' precision.  Q3 / Q2 rows (lowbit.rs
 // chunks of 32 codes in 3 / 2 words) load, per group and lane, the word of
 // the lane's 16 inputs (and Q3's low-bit word) and expand it to the two
@@ -319,6 +320,10 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
     }
     const uint32_t m0 = mt * TR;
     if (m0 >= M) return;
+    // 16-row slices holding rows (a grouped tile is often short: expert
+    // row counts run from 1 to over 1000): the MFMAs, folds and bias terms
+    // of the empty slices are skipped, a uniform branch per slice
+    const uint32_t ni = min((uint32_t)NI, (M - m0 + 15) / 16);
     const uint32_t* list = a.list ? a.list + (size_t)grp * a.cap : nullptr;
     const uint32_t K = a.K, G = K >> 6, KB = K >> 3;
     // split K: this workgroup's groups [gb, ge)
@@ -527,6 +532,7 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
             }
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
+            if ((uint32_t)i >= ni) break;
             f4 accg[NMAT][NJ];
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
@@ -598,6 +604,7 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
         float4 xg[NI][2];
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
+            if ((uint32_t)i >= ni) break;
             const uint32_t m = min(m0 + i * 16 + col, M - 1);
             const uint32_t ar = list ? list[m] / a.div : toff + m;
             const float4* xp = reinterpret_cast<const float4*>(a.xs + (size_t)ar * G + kc);
@@ -606,6 +613,7 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
         }
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
+            if ((uint32_t)i >= ni) break;
             const float4 x0 = xg[i][0], x1 = xg[i][1];
             const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
             uint32_t hw[4], mw[4], lw[4];
@@ -1531,16 +1539,6 @@ void launch_pf_gemm_args(const PfGemmArgs& args, int epi, uint32_t grid_y, hipSt
         else k_pf_gemm<NM, E, false><<<dim3(GX, grid_y, ksplit), PF_WG, 0, st>>>(a);    \
     } while (0)
     const uint32_t xbits = a.X.base ? a.X.bits : 4;
-    const uint32_t tr = a.tile_rows ? a.tile_rows : 64;
-    if (tr != 64) {
-        // 48-row tiles (grouped experts: ~40 rows each)
-        if (!sbl || xbits != 4) throw std::runtime_error("prefill GEMM tiles under 64 rows need staged scales over Q4 rows");
-        const uint32_t gx = epi == PE_SILU_MUL ? (a.N + 127) / 128 : (a.N + 255) / 256;
-        const dim3 grid(gx, grid_y, ksplit);
-        if (tr == 48 && epi == PE_SILU_MUL) k_pf_gemm<2, PE_SILU_MUL, true, 4, 3><<<grid, PF_WG, 0, st>>>(a);
-        else throw std::runtime_error("prefill GEMM: no such tile height for this epilogue");
-        return;
-    }
     if (xbits != 4) {
         // grouped expert GEMMs over Q3 / Q2 records (scales folded per lane)
         if (epi != PE_STORE && epi != PE_SILU_MUL) throw std::runtime_error("low-bit records: gate/up and down only");
