@@ -164,6 +164,12 @@ struct PfBufs {
     // the normed trunk streams, fc_e / fc_h outputs and the head's residual
     uint32_t* mtp_tok;
     float *mtp_en, *mtp_hn, *mtp_fe, *mtp_fh, *mtp_hyper;
+    // the flash attention plan (pf_flash_plan) for the chunk's dense rows,
+    // uploaded for the (rows, first position) key it was made for
+    uint4 *fa_seg, *fa_merge;
+    float* fa_part;
+    uint64_t fa_key = ~0ull;
+    uint32_t fa_W = 0, fa_nslots = 0, fa_nmerge = 0;
     // QSA past the budget: every row's index queries; scores, selections
     // and attention partials of qsa_rows rows at a time
     float *iq_ready, *qsa_bscore, *qsa_part;
@@ -200,6 +206,7 @@ struct ChkEngine {
     uint8_t* rec_kind = nullptr;
     uint8_t* rec_kind_host = nullptr;
     uint32_t record_layers = 0;
+    uint32_t ncu = 256;  // compute units of the device (flash attention plans)
     uint64_t state_bytes = 0, kv_bytes = 0, scratch_bytes = 0;
     Q4Mat embed{}, lm_head{};
     std::vector<LayerDev> layers;
@@ -760,6 +767,12 @@ struct ChkEngine {
         max_t = o.max_t;
         trunk_rows = 1 + o.drafts;
         HIPCHK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+        {
+            int dev = 0, n = 0;
+            HIPCHK(hipGetDevice(&dev));
+            HIPCHK(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev));
+            ncu = n > 0 ? (uint32_t)n : 256u;
+        }
 
         // dense store: dry run for the size, then allocate and generate
         Bump dry;
@@ -1465,6 +1478,14 @@ struct ChkEngine {
     uint32_t prefill_rows_fit(bool all_logits) const;
     // ------------------------------------------------- GEMM prefill
     bool pf_supported() const;
+    // flash attention plans: workgroups per kv head, partial floats (at most
+    // two pieces per workgroup of a kv head)
+    uint64_t fa_wmax(uint64_t C) const {
+        return std::min<uint64_t>((C + 15) / 16, std::max<uint32_t>(1, ncu / D.nkv));
+    }
+    uint64_t fa_part_floats(uint64_t C) const { return (uint64_t)D.nkv * 2 * fa_wmax(C) * 16 * (D.nh / D.nkv) * (2 + D.hd); }
+    uint32_t pf_dense_rows(uint32_t T, uint32_t pos0) const;
+    PfFlashLaunch pf_flash_launch(uint32_t T, uint32_t pos0);
     uint32_t pf_qsa_rows() const;
     void pf_alloc();
     void pf_hc_read(const HcDev& w, float* inj, uint32_t T, bool for_moe);
@@ -1701,6 +1722,10 @@ uint64_t ChkEngine::prefill_scratch_bytes(uint64_t C, bool all_logits) const {
     if (D.SI != D.I) b += C * D.SI * f;
     if (dc_supported(D.nk, D.nv, D.dk, D.dv)) b += dc_work_floats((uint32_t)C, D.nv, D.dv) * f;
     if (all_logits) b += C * D.V * f;
+    {
+        const uint64_t rmax = (C + 15) / 16, wmax = fa_wmax(C);
+        b += (rmax * FA_MAXSEG + wmax) * 16 + fa_part_floats(C) * f;
+    }
     if (ple_l >= 0) b += C * (ngram_heads + c.ple_embed_dim + 3ull * D.hh + D.H) * 4;
     if (D.qsa)
         b += (C * (D.inh * D.ihd + D.mask_words) +
@@ -1779,6 +1804,10 @@ void ChkEngine::pf_alloc() {
     pf.inj_a = pfalloc<float>(C * D.hc);
     pf.inj_m = pfalloc<float>(C * D.hc);
     pf.mixed = pfalloc<float>(C * D.H);
+    pf.fa_seg = pfalloc<uint4>((C + 15) / 16 * FA_MAXSEG);
+    pf.fa_merge = pfalloc<uint4>(fa_wmax(C));
+    pf.fa_part = pfalloc<float>(fa_part_floats(C));
+    pf.fa_key = ~0ull;
     // DeltaNet / attention arena
     const uint64_t dn = C * (2ull * D.conv_dim + 2ull * D.v_dim + (2ull * pf_ab_split(D.H) + 2) * D.nv);
     const uint64_t at = C * (2ull * D.nh * D.hd + 2ull * D.kv_row + D.idx_out + 2ull * D.nh * D.hd);
@@ -2032,7 +2061,8 @@ void ChkEngine::pf_attention(const LayerDev& L, uint32_t T, uint32_t pos0, const
     aa.max_chunks = (pos0 + T - 1) / ATTN_CHUNK + 1;
     if (!D.qsa) {
         launch_attn_prep(aa, (int)T, st);
-        launch_pf_flash(pf.q_ready, pf.q_raw, kvl, pf.attn_out, T, pos0, D.nh, D.nkv, D.hd, D.attn_scale, st);
+        launch_pf_flash(pf.q_ready, pf.q_raw, kvl, pf.attn_out, T, pos0, D.nh, D.nkv, D.hd, D.attn_scale,
+                        pf_flash_launch(T, pos0), st);
     } else {
         // select_tokens (cpu.rs:643-719) over the chunk: every row's KV,
         // index key and index queries first, then the pooled keys of the
@@ -2044,10 +2074,10 @@ void ChkEngine::pf_attention(const LayerDev& L, uint32_t T, uint32_t pos0, const
         aa.iq_ready = pf.iq_ready;
         launch_attn_prep(aa, (int)T, st);
         launch_qsa_block_keys(aa, pos0 / D.ratio, (pos0 + T) / D.ratio, st);
-        const uint32_t first_sel = (D.kblk + 1) * D.ratio - 1;  // first position with nblk > kblk
-        const uint32_t td = first_sel <= pos0 ? 0 : std::min(T, first_sel - pos0);
+        const uint32_t td = pf_dense_rows(T, pos0);
         if (td) {
-            launch_pf_flash(pf.q_ready, pf.q_raw, kvl, pf.attn_out, td, pos0, D.nh, D.nkv, D.hd, D.attn_scale, st);
+            launch_pf_flash(pf.q_ready, pf.q_raw, kvl, pf.attn_out, td, pos0, D.nh, D.nkv, D.hd, D.attn_scale,
+                            pf_flash_launch(td, pos0), st);
             launch_zero_f32(reinterpret_cast<float*>(pf.qsa_rows_mask), (uint64_t)td * D.mask_words, st);
         }
         for (uint32_t r0 = td; r0 < T; r0 += pf.qsa_rows) {
@@ -2070,6 +2100,37 @@ void ChkEngine::pf_attention(const LayerDev& L, uint32_t T, uint32_t pos0, const
     }
     launch_pf_xprep(pf.attn_out, D.nh * D.hd, T, D.nh * D.hd, pf.hi, pf.lo, pf.xs, st);
     pf_out_proj(L.at.o, D.nh * D.hd, T);
+}
+
+// Rows of a chunk that attend densely (the flash kernel): all of them, or
+// with QSA those before the first position whose blocks exceed the budget.
+uint32_t ChkEngine::pf_dense_rows(uint32_t T, uint32_t pos0) const {
+    if (!D.qsa) return T;
+    const uint32_t first_sel = (D.kblk + 1) * D.ratio - 1;  // first position with nblk > kblk
+    return first_sel <= pos0 ? 0 : std::min(T, first_sel - pos0);
+}
+
+// The flash plan for (T dense rows at pos0), made and uploaded when the key
+// changes: at the start of a chunk, whose stream is then idle (the previous
+// chunk ended with a stream synchronisation); a change within a chunk waits
+// for the launches that may still read the old plan.
+PfFlashLaunch ChkEngine::pf_flash_launch(uint32_t T, uint32_t pos0) {
+    const uint64_t key = (uint64_t)T << 32 | pos0;
+    if (key != pf.fa_key) {
+        const PfFlashPlan p = pf_flash_plan(T, pos0, std::max<uint32_t>(1, ncu / D.nkv));
+        const uint64_t rmax = (pf.cap + 15) / 16, wmax = fa_wmax(pf.cap);
+        if (p.seg.size() > rmax * FA_MAXSEG || p.merge.size() > wmax || p.nslots > 2 * wmax)
+            throw std::runtime_error("flash attention plan exceeds its buffers");
+        HIPCHK(hipStreamSynchronize(st));
+        HIPCHK(hipMemcpy(pf.fa_seg, p.seg.data(), p.seg.size() * sizeof(uint4), hipMemcpyHostToDevice));
+        if (!p.merge.empty())
+            HIPCHK(hipMemcpy(pf.fa_merge, p.merge.data(), p.merge.size() * sizeof(uint4), hipMemcpyHostToDevice));
+        pf.fa_key = key;
+        pf.fa_W = p.W;
+        pf.fa_nslots = p.nslots;
+        pf.fa_nmerge = (uint32_t)p.merge.size();
+    }
+    return PfFlashLaunch{pf.fa_seg, pf.fa_merge, pf.fa_part, pf.fa_W, pf.fa_nslots, pf.fa_nmerge};
 }
 
 // moe (cpu.rs:504-541) over the chunk: router GEMM, per-row top-k, entries
@@ -2174,6 +2235,8 @@ void ChkEngine::prefill_gemm(const uint32_t* toks, uint32_t n, uint32_t next_aft
             HIPCHK(hipMemcpy(pf.ple_ids, ids.data(), ids.size() * 4, hipMemcpyHostToDevice));
         }
         pf.pend = nullptr;  // (an earlier failed chunk may have left one)
+        // the chunk's flash plan, while the stream is idle
+        if (const uint32_t td = pf_dense_rows(T, pos0)) pf_flash_launch(td, pos0);
         launch_pf_embed(pf.tokens, embed, pf.hyper, D.H, D.hc, T, st);
         for (uint32_t l = 0; l < c.num_hidden_layers; ++l) {
             const LayerDev& L = layers[l];

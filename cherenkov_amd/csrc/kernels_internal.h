@@ -1,6 +1,8 @@
 // Argument blocks and launchers of the decode kernels (internal).
 #pragma once
 
+#include <vector>
+
 #include "internal.h"
 
 namespace chk {
@@ -428,10 +430,29 @@ void launch_pf_hc_prep(float* hyper, const uint16_t* norm, uint32_t H, uint32_t 
                        uint4* hi, uint4* lo, float* xs, uint32_t T, const float* part, uint64_t pzs, uint32_t nsplit,
                        const float* pinj, hipStream_t st);
 void launch_pf_gemm_args(const PfGemmArgs& a, int epi, uint32_t grid_y, hipStream_t st);
-// whether a GEMM takes the staged-scale form (needed by tiles under 64 rows)
-bool pf_gemm_staged(const PfGemmArgs& a, int epi);
+// Causal flash attention over a prefill chunk.  Its (row block, token
+// tile) steps are dealt to the workgroups by a plan made on the host
+// (pf_flash_plan, the same for every kv head): per workgroup up to
+// FA_MAXSEG segments (row block, first tile, end tile, partial slot or ~0
+// for a whole block; row block ~0 ends the list), and per split row block
+// a merge entry (row block, first slot, pieces, 0).
+constexpr uint32_t FA_MAXSEG = 6;
+constexpr int FA_MAXP = 4;  // pieces of a split row block
+struct PfFlashPlan {
+    uint32_t W = 0;            // workgroups per kv head
+    uint32_t nslots = 0;       // partial slots per kv head
+    std::vector<uint4> seg;    // [W][FA_MAXSEG]
+    std::vector<uint4> merge;  // [split row blocks]
+};
+PfFlashPlan pf_flash_plan(uint32_t T, uint32_t pos0, uint32_t max_wg);
+struct PfFlashLaunch {         // a plan uploaded to the device
+    const uint4* seg;
+    const uint4* merge;
+    float* part;               // [nkv][nslots][16][nh / nkv][2 + hd]
+    uint32_t W, nslots, nmerge;
+};
 void launch_pf_flash(const float* q_ready, const float* q_raw, const KvDev& kv, float* out, uint32_t T, uint32_t pos0,
-                     uint32_t nh, uint32_t nkv, uint32_t hd, float scale, hipStream_t st);
+                     uint32_t nh, uint32_t nkv, uint32_t hd, float scale, const PfFlashLaunch& plan, hipStream_t st);
 void launch_pf_gemm(const Q4Mat& w, const uint4* xhi, const uint4* xlo, const float* xs, float* y, uint32_t T,
                     uint32_t ldy, hipStream_t st);
 void launch_pf_hc_down_finish(const float* part, uint32_t nsplit, uint32_t T, uint32_t lowrank, uint32_t hc,

@@ -1476,8 +1476,7 @@ void launch_pf_hc_prep(float* hyper, const uint16_t* norm, uint32_t H, uint32_t 
 
 // The launch form of a GEMM: 32-bit element offsets of the dense matrices
 // from their lowest base, and whether its scales can be staged (whole
-// blocks of 8 groups on 16-byte aligned rows), the form every tile height
-// under 64 rows needs.
+// blocks of 8 groups on 16-byte aligned rows).
 static bool pf_gemm_prepare(PfGemmArgs& a, int epi) {
     const int nm = std::max<int>(a.nseg, epi == PE_SILU_MUL ? 2 : 1);
     uintptr_t wmin = UINTPTR_MAX, smin = UINTPTR_MAX;
@@ -1507,11 +1506,6 @@ static bool pf_gemm_prepare(PfGemmArgs& a, int epi) {
     return sbl;
 }
 
-bool pf_gemm_staged(const PfGemmArgs& args, int epi) {
-    if (args.K % 64 || !args.K) return false;
-    PfGemmArgs a = args;
-    return pf_gemm_prepare(a, epi);
-}
 
 void launch_pf_gemm_args(const PfGemmArgs& args, int epi, uint32_t grid_y, hipStream_t st) {
     if (args.K % 64 || !args.K) throw std::runtime_error("prefill GEMM needs K a multiple of 64");
@@ -1660,8 +1654,15 @@ namespace chk {
 // for every prompt row r at position pos0 + r and query head h,
 //   o = softmax_t(scale q . k_t) . v_t over t <= pos0 + r, times sigmoid(gate).
 //
-// A workgroup takes 16 rows and one kv head; wave w serves that kv head's
-// query head w (GQA: the group's waves share every staged K/V tile).  Per
+// Work: per kv head, (16-row block, 32-token tile) steps; row block rb
+// needs tiles 0 .. (pos0 + 16 rb + 15) / 32, so late blocks hold up to
+// twice the average.  A plan (pf_flash_plan, on the host) deals the steps
+// to the workgroups in equal shares: row blocks in zigzag order (first,
+// last, second, ...), the sequence cut into W equal ranges, so a workgroup
+// runs a few segments (row block, tile range); a row block cut between
+// workgroups leaves unnormalised partials (m, l, o) that k_pf_flash_merge
+// joins.  Within a segment, wave w serves the kv head's query head w
+// (GQA: the group's waves share every staged K/V tile).  Per
 // 32-token tile the workgroup dequantises K and V (int8 x fp16 scale,
 // exact in f32) into LDS as fp16 hi + lo planes (V transposed), then each
 // wave runs S = Q K^T and O += P V on v_mfma_f32_16x16x32_f16 with three
@@ -1678,6 +1679,9 @@ struct PfFlashArgs {
     float* out;            // [T][nh * hd]
     uint32_t T, pos0, nh, nkv;
     float scale;
+    const uint4* seg;      // [W][FA_MAXSEG] the plan's segments (pf_flash_plan)
+    float* part;           // [nkv][nslots][FA_ROWS][G][2 + hd] partials of split row blocks
+    uint32_t nslots;
 };
 
 CHK_DEV h8 split_hi(const float (&v)[8], h8& lo) {
@@ -1704,10 +1708,15 @@ __global__ void __launch_bounds__(64 * G) k_pf_flash(PfFlashArgs a) {
     constexpr int IPT = (FA_TOK * HD / 16 + nthr - 1) / nthr;  // staging items per thread
     const uint32_t tid = threadIdx.x, lane = tid & 63, w = wave_id();
     const uint32_t col = lane & 15, kq = lane >> 4;
-    // heavy (late) row blocks first
-    const uint32_t rb = gridDim.x - 1 - blockIdx.x, hk = blockIdx.y, h = hk * G + w;
-    const uint32_t r0 = rb * FA_ROWS, rlast = min(r0 + FA_ROWS, a.T) - 1;
+    const uint32_t hk = blockIdx.y, h = hk * G + w;
     const uint32_t kv_row = a.nkv * HD, last_tok = a.pos0 + a.T - 1;
+    const uint4* segs = a.seg + (size_t)blockIdx.x * FA_MAXSEG;
+    for (uint32_t sgi = 0; sgi < FA_MAXSEG; ++sgi) {
+    const uint4 sg = segs[sgi];  // (row block, first tile, end tile, slot or ~0: the whole block)
+    if (sg.x == ~0u) break;
+    if (sgi) __syncthreads();  // every wave is done with the previous segment's tiles
+    const uint32_t rb = sg.x, ta = sg.y, tb = sg.z;
+    const uint32_t r0 = rb * FA_ROWS;
     // this wave's queries as A operands
     h8 qh[KS], ql[KS];
     {
@@ -1735,7 +1744,6 @@ __global__ void __launch_bounds__(64 * G) k_pf_flash(PfFlashArgs a) {
         m[i] = -INFINITY;
         l[i] = 0.0f;
     }
-    const uint32_t ntile = (a.pos0 + rlast) / FA_TOK + 1;
     // Staging: K as (token tid % 32, 16 dims), V as (token pair tid % 16,
     // 8 dims) so that the transposed V writes are whole dwords in
     // consecutive banks; a tile's raw bytes are loaded one tile ahead.
@@ -1797,12 +1805,12 @@ __global__ void __launch_bounds__(64 * G) k_pf_flash(PfFlashArgs a) {
             }
         }
     };
-    load_raw(0);
+    load_raw(ta * FA_TOK);
     store_tile();
     __syncthreads();
-    for (uint32_t tile = 0; tile < ntile; ++tile) {
+    for (uint32_t tile = ta; tile < tb; ++tile) {
         const uint32_t t0 = tile * FA_TOK;
-        if (tile + 1 < ntile) load_raw(t0 + FA_TOK);
+        if (tile + 1 < tb) load_raw(t0 + FA_TOK);
         // ---- S = Q K^T for 2 token tiles
         f4 s[2];
 #pragma unroll
@@ -1869,42 +1877,190 @@ __global__ void __launch_bounds__(64 * G) k_pf_flash(PfFlashArgs a) {
             o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pah, bl, o[d], 0, 0, 0);
             o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pah, bh, o[d], 0, 0, 0);
         }
-        if (tile + 1 < ntile) {
+        if (tile + 1 < tb) {
             __syncthreads();  // every wave is done with this tile's K and V
             store_tile();
             __syncthreads();
         }
     }
-    // ---- o / l times the per-dim sigmoid gate (cpu.rs:629-633)
+    if (sg.w == ~0u) {
+        // ---- o / l times the per-dim sigmoid gate (cpu.rs:629-633)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t r = r0 + kq * 4 + i;
-        if (r >= a.T) continue;
-        const float inv = 1.0f / l[i];
-        const float* gp = a.q_raw + ((size_t)r * a.nh + h) * 2 * HD + HD;
-        float* op = a.out + (size_t)r * a.nh * HD + (size_t)h * HD;
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t r = r0 + kq * 4 + i;
+            if (r >= a.T) continue;
+            const float inv = 1.0f / l[i];
+            const float* gp = a.q_raw + ((size_t)r * a.nh + h) * 2 * HD + HD;
+            float* op = a.out + (size_t)r * a.nh * HD + (size_t)h * HD;
 #pragma unroll
-        for (int d = 0; d < DT; ++d) {
-            const uint32_t dd = d * 16 + col;
-            op[dd] = o[d][i] * inv * sigmoidf_(gp[dd]);
+            for (int d = 0; d < DT; ++d) {
+                const uint32_t dd = d * 16 + col;
+                op[dd] = o[d][i] * inv * sigmoidf_(gp[dd]);
+            }
+        }
+    } else {
+        // ---- a piece of a split row block: (m, l, unnormalised o) per row
+        float* pp = a.part + ((size_t)hk * a.nslots + sg.w) * FA_ROWS * G * (2 + HD);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float* q = pp + ((size_t)(kq * 4 + i) * G + w) * (2 + HD);
+            if (col == 0) {
+                q[0] = m[i];
+                q[1] = l[i];
+            }
+#pragma unroll
+            for (int d = 0; d < DT; ++d) q[2 + d * 16 + col] = o[d][i];
+        }
+    }
+    }
+}
+
+// Joins the pieces of the row blocks a flash plan split: per row, head and
+// dim, o = sum_k o_k e^(m_k - M) / sum_k l_k e^(m_k - M) with M = max_k m_k
+// (a piece whose tokens a row cannot see holds m = -inf, l = 0), times the
+// sigmoid gate.  Workgroup (entry, row) of kv head blockIdx.z; thread d
+// takes dims d, d + 256 of every head, all loads issued before the sums.
+template <int G, int HD>
+__global__ void __launch_bounds__(256) k_pf_flash_merge(PfFlashArgs a, const uint4* __restrict__ merge) {
+    constexpr int DPT = (HD + CHK_WG - 1) / CHK_WG;
+    const uint4 me = merge[blockIdx.x];  // (row block, first slot, pieces, 0)
+    const uint32_t row = blockIdx.y, hk = blockIdx.z, r = me.x * FA_ROWS + row, np = me.z;
+    if (r >= a.T) return;
+    const float* __restrict__ part = a.part;
+    const float* __restrict__ qraw = a.q_raw;
+    float* __restrict__ outp = a.out;
+    const size_t ps = (size_t)FA_ROWS * G * (2 + HD);  // floats per slot
+    const float* p0 = part + ((size_t)hk * a.nslots + me.y) * ps + (size_t)row * G * (2 + HD);
+    float mk[G][FA_MAXP], lk[G][FA_MAXP], ok[G][FA_MAXP][DPT], gate[G][DPT];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const float* q = p0 + (size_t)g * (2 + HD);
+#pragma unroll
+        for (int k = 0; k < FA_MAXP; ++k) {
+            const bool on = (uint32_t)k < np;
+            mk[g][k] = on ? q[k * ps] : -INFINITY;
+            lk[g][k] = on ? q[k * ps + 1] : 0.0f;
+#pragma unroll
+            for (int j = 0; j < DPT; ++j) {
+                const uint32_t d = threadIdx.x + j * CHK_WG;
+                ok[g][k][j] = on && d < (uint32_t)HD ? q[k * ps + 2 + d] : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < DPT; ++j) {
+            const uint32_t d = min(threadIdx.x + j * CHK_WG, (uint32_t)HD - 1);
+            gate[g][j] = qraw[((size_t)r * a.nh + hk * G + g) * 2 * HD + HD + d];
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < FA_MAXP; ++k) M = fmaxf(M, mk[g][k]);
+        float e[FA_MAXP], L = 0.0f;
+#pragma unroll
+        for (int k = 0; k < FA_MAXP; ++k) {
+            e[k] = mk[g][k] == -INFINITY ? 0.0f : expf(mk[g][k] - M);
+            L += lk[g][k] * e[k];
+        }
+        const float inv = 1.0f / L;
+#pragma unroll
+        for (int j = 0; j < DPT; ++j) {
+            const uint32_t d = threadIdx.x + j * CHK_WG;
+            if (d >= (uint32_t)HD) continue;
+            float O = 0.0f;
+#pragma unroll
+            for (int k = 0; k < FA_MAXP; ++k) O += ok[g][k][j] * e[k];
+            outp[(size_t)r * a.nh * HD + (size_t)(hk * G + g) * HD + d] = O * inv * sigmoidf_(gate[g][j]);
         }
     }
 }
 
+// Deals every kv head's (row block, tile) steps to max_wg workgroups in
+// equal shares (see k_pf_flash); one whole row block per workgroup, heavy
+// ones first, where the blocks' work is within 15% of even or a share
+// would need more than FA_MAXSEG segments.
+PfFlashPlan pf_flash_plan(uint32_t T, uint32_t pos0, uint32_t max_wg) {
+    PfFlashPlan p;
+    const uint32_t R = (T + FA_ROWS - 1) / FA_ROWS;
+    std::vector<uint32_t> tiles(R);
+    uint64_t total = 0;
+    uint32_t most = 0;
+    for (uint32_t rb = 0; rb < R; ++rb) {
+        tiles[rb] = (pos0 + std::min(rb * FA_ROWS + FA_ROWS - 1, T - 1)) / FA_TOK + 1;
+        total += tiles[rb];
+        most = std::max(most, tiles[rb]);
+    }
+    const uint32_t W = std::max<uint32_t>(1, std::min(R, max_wg));
+    auto whole = [&]() {
+        p = PfFlashPlan{};
+        p.W = R;
+        p.seg.assign((size_t)R * FA_MAXSEG, make_uint4(~0u, 0, 0, 0));
+        for (uint32_t x = 0; x < R; ++x) {
+            const uint32_t rb = R - 1 - x;
+            p.seg[(size_t)x * FA_MAXSEG] = make_uint4(rb, 0, tiles[rb], ~0u);
+        }
+        return p;
+    };
+    if ((double)most <= 1.15 * (double)total / W) return whole();
+    p.W = W;
+    p.seg.assign((size_t)W * FA_MAXSEG, make_uint4(~0u, 0, 0, 0));
+    std::vector<uint32_t> order;
+    for (uint32_t i = 0, j = R; i < j;) {
+        order.push_back(i++);
+        if (i < j) order.push_back(--j);
+    }
+    uint64_t start = 0;
+    std::vector<uint32_t> nseg(W, 0);
+    for (uint32_t rb : order) {
+        const uint64_t end = start + tiles[rb];
+        // workgroups whose range [k total / W, (k + 1) total / W) meets [start, end)
+        uint32_t k = (uint32_t)(start * W / total);
+        while (k > 0 && k * total / W > start) --k;
+        while (k + 1 < W && (k + 1) * total / W <= start) ++k;  // the range holding tile `start`
+        const bool split = (k + 1) * total / W < end;
+        uint32_t pieces = 0;
+        const uint32_t first_slot = p.nslots;
+        for (; k < W && k * total / W < end; ++k) {
+            const uint64_t lo = std::max<uint64_t>(start, k * total / W), hi = std::min<uint64_t>(end, (k + 1) * total / W);
+            if (lo >= hi) continue;
+            if (nseg[k] == FA_MAXSEG) return whole();
+            const uint32_t slot = split ? p.nslots++ : ~0u;
+            p.seg[(size_t)k * FA_MAXSEG + nseg[k]++] = make_uint4(rb, (uint32_t)(lo - start), (uint32_t)(hi - start), slot);
+            ++pieces;
+        }
+        if (split) {
+            if (pieces > FA_MAXP) return whole();
+            p.merge.push_back(make_uint4(rb, first_slot, pieces, 0));
+        }
+        start = end;
+    }
+    return p;
+}
+
 void launch_pf_flash(const float* q_ready, const float* q_raw, const KvDev& kv, float* out, uint32_t T, uint32_t pos0,
-                     uint32_t nh, uint32_t nkv, uint32_t hd, float scale, hipStream_t st) {
+                     uint32_t nh, uint32_t nkv, uint32_t hd, float scale, const PfFlashLaunch& plan, hipStream_t st) {
     if (nkv == 0 || nh % nkv || nh / nkv > 8 || (hd != 128 && hd != 256))
         throw std::runtime_error("flash prefill takes head_dim 128 or 256 and up to 8 query heads per kv head");
     if (!T) return;
-    PfFlashArgs a{q_ready, q_raw, kv, out, T, pos0, nh, nkv, scale};
-    const dim3 grid((T + FA_ROWS - 1) / FA_ROWS, nkv);
-#define CHK_FA(HDV)                                                           \
-    switch (nh / nkv) {                                                       \
-    case 1: k_pf_flash<HDV, 1><<<grid, 64, 0, st>>>(a); break;                \
-    case 2: k_pf_flash<HDV, 2><<<grid, 128, 0, st>>>(a); break;               \
-    case 3: case 4: k_pf_flash<HDV, 4><<<grid, 256, 0, st>>>(a); break;       \
-    default: k_pf_flash<HDV, 8><<<grid, 512, 0, st>>>(a); break;              \
-    }
+    if (!plan.seg || !plan.W || (plan.nmerge && (!plan.merge || !plan.part)))
+        throw std::runtime_error("flash prefill needs its plan");
+    PfFlashArgs a{q_ready, q_raw, kv, out, T, pos0, nh, nkv, scale, plan.seg, plan.part, plan.nslots};
+    const dim3 grid(plan.W, nkv);
+    const dim3 mgrid(plan.nmerge, FA_ROWS, nkv);
+#define CHK_FA(HDV)                                                                                      \
+    switch (nh / nkv) {                                                                                  \
+    case 1: k_pf_flash<HDV, 1><<<grid, 64, 0, st>>>(a); break;                                           \
+    case 2: k_pf_flash<HDV, 2><<<grid, 128, 0, st>>>(a); break;                                          \
+    case 3: case 4: k_pf_flash<HDV, 4><<<grid, 256, 0, st>>>(a); break;                                  \
+    default: k_pf_flash<HDV, 8><<<grid, 512, 0, st>>>(a); break;                                         \
+    }                                                                                                    \
+    if (plan.nmerge) switch (nh / nkv) {                                                                 \
+        case 1: k_pf_flash_merge<1, HDV><<<mgrid, CHK_WG, 0, st>>>(a, plan.merge); break;                \
+        case 2: k_pf_flash_merge<2, HDV><<<mgrid, CHK_WG, 0, st>>>(a, plan.merge); break;                \
+        case 3: case 4: k_pf_flash_merge<4, HDV><<<mgrid, CHK_WG, 0, st>>>(a, plan.merge); break;        \
+        default: k_pf_flash_merge<8, HDV><<<mgrid, CHK_WG, 0, st>>>(a, plan.merge); break;               \
+        }
     if (nh / nkv != 1 && nh / nkv != 2 && nh / nkv != 4 && nh / nkv != 8)
         throw std::runtime_error("flash prefill takes 1, 2, 4 or 8 query heads per kv head");
     if (hd == 256) {
