@@ -1031,7 +1031,9 @@ constexpr uint32_t GU_WAVES = CHK_GU_WAVES;
 constexpr uint32_t GU_WG = 64 * GU_WAVES;
 
 // CPL: input chunks per lane (hidden sizes up to 2048 CPL).
-template <int R, int BITS, int CPL>
+// MIXED: a low-bit launch whose records may be switched to their 4-bit
+// copies (a.kinds set); else every routed record is decoded at X.bits.
+template <int R, int BITS, int CPL, bool MIXED>
 __global__ void __launch_bounds__(GU_WG) k_moe_gate_up(MoeArgs a) {
     static_assert(R * GU_WAVES == 32, "a workgroup covers one 32-row chunk");
     __shared__ float act_s[32];
@@ -1061,7 +1063,7 @@ __global__ void __launch_bounds__(GU_WG) k_moe_gate_up(MoeArgs a) {
     // mixed stores: this lane's 8 experts' kinds (the lanes' expert split of
     // route_row), in flight with the logits
     uint32_t kw0 = 0, kw1 = 0;
-    if (BITS != 4 && routed && a.kinds) {
+    if (MIXED && routed) {
         const uint2 kv = *reinterpret_cast<const uint2*>(a.kinds + (size_t)a.record_layer * a.E +
                                                          min((uint32_t)lane * 8u, a.E - 8u));
         kw0 = kv.x;
@@ -1076,7 +1078,7 @@ __global__ void __launch_bounds__(GU_WG) k_moe_gate_up(MoeArgs a) {
     // a low-bit launch decodes routed records of kind != 0 at X.bits and the
     // rest from their 4-bit copies (the kind byte of expert e: lane e / 8)
     bool low = BITS != 4 && routed;
-    if (BITS != 4 && routed && a.kinds) {
+    if (MIXED && routed) {
         const uint32_t kw = (uint32_t)__builtin_amdgcn_readlane((int)((e & 4u) ? kw1 : kw0), (int)(e >> 3));
         low = ((kw >> (8u * (e & 3u))) & 0xffu) != 0u;
     }
@@ -1090,7 +1092,7 @@ __global__ void __launch_bounds__(GU_WG) k_moe_gate_up(MoeArgs a) {
     ExpFrag<64, CPL, R, BITS> lg, lu;
     if (q4path) {
         Q4Mat mg = a.sh_gate, mu = a.sh_up;
-        if (routed) {
+        if ((BITS == 4 || MIXED) && routed) {
             const ExpertsDev& XQ = BITS == 4 ? a.X : a.X4;
             const uint8_t* rq = XQ.base + ((size_t)a.record_layer * XQ.experts + e) * XQ.stride;
             const ExpMat eg = expert_mat(XQ, rq, 0, a.I, a.H), eu = expert_mat(XQ, rq, 1, a.I, a.H);
@@ -1137,7 +1139,7 @@ __global__ void __launch_bounds__(GU_WG) k_moe_gate_up(MoeArgs a) {
 // output rows; its 64/LPR lane groups take one expert slot each per pass.
 // Two dependent round trips: the routing (ids, weights), then every pass's
 // weight rows and activations at once.
-template <int LPR, int R, int BITS, int PASSES>
+template <int LPR, int R, int BITS, int PASSES, bool MIXED>
 __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a) {
     constexpr int G = 64 / LPR;
     const int lane = threadIdx.x & 63, grp = lane / LPR, lir = lane % LPR;
@@ -1165,7 +1167,7 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a) {
     }
     // mixed stores: lane l holds the kinds of experts 8l..8l+7
     uint32_t kw0 = 0, kw1 = 0;
-    if (BITS != 4 && a.kinds) {
+    if (MIXED) {
         const uint2 kv = *reinterpret_cast<const uint2*>(a.kinds + (size_t)a.record_layer * a.E +
                                                          min((uint32_t)lane * 8u, a.E - 8u));
         kw0 = kv.x;
@@ -1226,7 +1228,7 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a) {
                 wgt[pass] = __shfl(my_w, sl, 64);
                 if (slot >= slots) wgt[pass] = 0.0f;
                 low[pass] = BITS != 4 && sl < a.topk;
-                if (BITS != 4 && a.kinds) {
+                if (MIXED) {
                     const uint32_t k0 = __shfl(kw0, (int)(e >> 3), 64), k1 = __shfl(kw1, (int)(e >> 3), 64);
                     low[pass] = low[pass] && ((((e & 4u) ? k1 : k0) >> (8u * (e & 3u))) & 0xffu) != 0u;
                 }
@@ -1236,7 +1238,7 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a) {
                 } else {
                     // the shared expert, or a routed record's 4-bit copy
                     Q4Mat mm = a.sh_down;
-                    if (sl < a.topk) {
+                    if ((BITS == 4 || MIXED) && sl < a.topk) {
                         const ExpertsDev& XQ = BITS == 4 ? a.X : a.X4;
                         const uint8_t* rq = XQ.base + ((size_t)a.record_layer * XQ.experts + e) * XQ.stride;
                         const ExpMat em = expert_mat(XQ, rq, 2, a.H, a.I);
@@ -1565,9 +1567,12 @@ void launch_moe_gate_up(const MoeArgs& a, hipStream_t st, hipEvent_t ev_start, h
     const uint32_t grid = a.nb * (a.topk * (a.I / 32) + a.SI / 32);  // one 32-row chunk per workgroup
     const size_t lds = xq_bytes(a.nb, a.H);
     const bool wide = a.H > 2048;
-    const void* fn = a.X.bits == 3   ? (wide ? (const void*)k_moe_gate_up<RG, 3, 2> : (const void*)k_moe_gate_up<RG, 3, 1>)
-                     : a.X.bits == 2 ? (wide ? (const void*)k_moe_gate_up<RG, 2, 2> : (const void*)k_moe_gate_up<RG, 2, 1>)
-                                     : (wide ? (const void*)k_moe_gate_up<RG, 4, 2> : (const void*)k_moe_gate_up<RG, 4, 1>);
+    const bool mixed = a.kinds != nullptr;
+#define GU_FN(B, M) (wide ? (const void*)k_moe_gate_up<RG, B, 2, M> : (const void*)k_moe_gate_up<RG, B, 1, M>)
+    const void* fn = a.X.bits == 3   ? (mixed ? GU_FN(3, true) : GU_FN(3, false))
+                     : a.X.bits == 2 ? (mixed ? GU_FN(2, true) : GU_FN(2, false))
+                                     : GU_FN(4, false);
+#undef GU_FN
     MoeArgs arg = a;
     void* args[] = {&arg};
     // with events: recorded by the dispatch itself (the kernel's own start and end)
@@ -1589,26 +1594,31 @@ void launch_moe_down(const MoeArgs& a, hipStream_t st) {
     if (a.topk >= 64 || a.hc * RD > 64) throw std::runtime_error("routing too wide");
     const uint32_t gdown = grid_for(a.H / RD, 1024);
     if (a.nb > 4) throw std::runtime_error("the down kernel takes at most 4 rows");
-#define DOWN(L, B, P) k_moe_down<L, RD, B, P><<<gdown, 256, 0, st>>>(a)
-#define DOWNP(L, B)                           \
+#define DOWN(L, B, P, M) k_moe_down<L, RD, B, P, M><<<gdown, 256, 0, st>>>(a)
+#define DOWNP(L, B, M)                        \
     switch (passes) {                         \
-    case 1: DOWN(L, B, 1); break;             \
-    case 2: DOWN(L, B, 2); break;             \
-    case 3: DOWN(L, B, 3); break;             \
-    default: DOWN(L, B, 4); break;            \
+    case 1: DOWN(L, B, 1, M); break;          \
+    case 2: DOWN(L, B, 2, M); break;          \
+    case 3: DOWN(L, B, 3, M); break;          \
+    default: DOWN(L, B, 4, M); break;         \
     }
-#define DOWNB(B)                              \
+#define DOWNB(B, M)                           \
     switch (lpr) {                            \
-    case 2: DOWNP(2, B); break;               \
-    case 4: DOWNP(4, B); break;               \
-    case 8: DOWNP(8, B); break;               \
-    case 16: DOWNP(16, B); break;             \
-    default: DOWNP(32, B); break;             \
+    case 2: DOWNP(2, B, M); break;            \
+    case 4: DOWNP(4, B, M); break;            \
+    case 8: DOWNP(8, B, M); break;            \
+    case 16: DOWNP(16, B, M); break;          \
+    default: DOWNP(32, B, M); break;          \
     }
+    const bool mixed = a.kinds != nullptr;
     switch (a.X.bits) {
-    case 3: DOWNB(3); break;
-    case 2: DOWNB(2); break;
-    default: DOWNB(4); break;
+    case 3:
+        if (mixed) DOWNB(3, true) else DOWNB(3, false)
+        break;
+    case 2:
+        if (mixed) DOWNB(2, true) else DOWNB(2, false)
+        break;
+    default: DOWNB(4, false); break;
     }
 #undef DOWNB
 #undef DOWNP

@@ -205,6 +205,10 @@ struct ChkEngine {
     // kernels and in pinned host memory, from which each change is copied
     uint8_t* rec_kind = nullptr;
     uint8_t* rec_kind_host = nullptr;
+    // records of a low-bit store switched to their 4-bit copy: while none
+    // is, the expert kernels take the kind table as absent (their pure
+    // low-bit form); the step graphs are recaptured when that changes
+    uint32_t kinds_q4 = 0;
     uint32_t record_layers = 0;
     uint32_t ncu = 256;  // compute units of the device (flash attention plans)
     uint64_t state_bytes = 0, kv_bytes = 0, scratch_bytes = 0;
@@ -346,6 +350,13 @@ struct ChkEngine {
         uint64_t codes = (uint64_t)D.I * D.H;
         if (o.experts == 4) return codes / 2 + 4 * (codes / 64);
         return codes * o.experts / 8 + 4 * (codes / 64);
+    }
+
+    // drops the captured step graphs (recaptured on their next use)
+    void drop_graphs() {
+        HIPCHK(hipStreamSynchronize(st));
+        for (auto& kv : graphs) HIPCHK(hipGraphExecDestroy(kv.second.exec));
+        graphs.clear();
     }
 
     ~ChkEngine() {
@@ -1115,7 +1126,7 @@ struct ChkEngine {
         MoeArgs m{};
         m.X = experts_dev();
         m.X4 = experts_dev(true);
-        m.kinds = o.experts == 4 ? nullptr : rec_kind;
+        m.kinds = o.experts == 4 || kinds_q4 == 0 ? nullptr : rec_kind;
         m.record_layer = L.moe.record_layer;
         m.sh_gate = L.moe.sh_gate;
         m.sh_up = L.moe.sh_up;
@@ -2165,7 +2176,7 @@ void ChkEngine::pf_moe(const LayerDev& L, uint32_t T) {
     gu.div = slots;
     gu.X = experts_dev();
     gu.X4 = experts_dev(true);
-    gu.kinds = o.experts == 4 ? nullptr : rec_kind;
+    gu.kinds = o.experts == 4 || kinds_q4 == 0 ? nullptr : rec_kind;
     gu.record_layer = L.moe.record_layer;
     PfGemmArgs dn = gu;
     dn.seg[0] = PfSeg{L.moe.sh_down, pf.yd, D.H, 0};
@@ -2753,9 +2764,14 @@ int chk_pool_set_kind(ChkEngine* e, uint32_t rid, uint32_t kind) {
         ensure(kind <= 2, "kind must be 0 (4-bit), 1 (3-bit) or 2 (2-bit)");
         if (kind == 0 && !e->rec_kind_host) return 0;  // 4-bit store only: every record is kind 0
         ensure(e->rec_kind_host && (kind == 0 || kind == pool_store_kind(e)), "low-bit store of that kind not attached");
-        if (e->rec_kind_host[rid] == kind) return 0;
+        const uint32_t was = e->rec_kind_host[rid];
+        if (was == kind) return 0;
         e->rec_kind_host[rid] = (uint8_t)kind;
         HIPCHK(hipMemcpyAsync(e->rec_kind + rid, e->rec_kind_host + rid, 1, hipMemcpyHostToDevice, e->st));
+        const uint32_t before = e->kinds_q4;
+        e->kinds_q4 += kind == 0 ? 1 : 0;
+        e->kinds_q4 -= was == 0 ? 1 : 0;
+        if ((before == 0) != (e->kinds_q4 == 0)) e->drop_graphs();  // the kernels' form changes
     })
 }
 
