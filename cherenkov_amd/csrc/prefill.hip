@@ -276,7 +276,6 @@ CHK_DEV h8 pf_unpack(uint32_t w, const Q4Consts& qk) {
 // launches run without staged scales.
 template <int NMAT, int EPI, bool SBL, int BITS = 4, int NI = 4>
 __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
-    static_assert(BITS == 4 || !SBL, "low-bit records fold their scales per lane");
     static_assert(NI == 4 || SBL, "tiles of fewer than 64 rows take the transposed (staged-scale) form");
     constexpr int NJ = 4 / NMAT;       // 16-wide output tiles per matrix per wave
     constexpr uint32_t TR = 16 * NI;   // tile rows: NI 16-row slices per wave
@@ -460,13 +459,17 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
     auto sb_fetch = [&](uint32_t g0) __attribute__((always_inline)) {
         sreg_s = *reinterpret_cast<const u32x4*>(sbase + ld_so + g0);
     };
+    // low-bit records: the midpoint rule's step (w = (step q + half) s + b)
+    // rides on the staged scale, exact as a power of two; half s joins the
+    // bias contraction
+    const float sstep = BITS != 4 && lowbit ? (BITS == 2 ? 4.0f : 2.0f) : 1.0f;
     auto sb_store = [&](uint32_t buf) __attribute__((always_inline)) {
         float* d = &sSB[buf][tid];
         const uint32_t sv[4] = {sreg_s.x, sreg_s.y, sreg_s.z, sreg_s.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            d[(2 * e) * 256] = __uint_as_float(sv[e] << 16);
-            d[(2 * e + 1) * 256] = __uint_as_float(sv[e] & 0xffff0000u);
+            d[(2 * e) * 256] = __uint_as_float(sv[e] << 16) * sstep;
+            d[(2 * e + 1) * 256] = __uint_as_float(sv[e] & 0xffff0000u) * sstep;
         }
     };
 
@@ -593,13 +596,19 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
         const uint32_t kg = k0 + 8 * kq;
         const bool live = kg < ge;
         const uint32_t kc = live ? kg : gb;
+        const bool lowb = BITS != 4 && lowbit;
         b8 bbv[NMAT][NJ];
+        u32x4 ssv[BITS == 4 ? 1 : NMAT][BITS == 4 ? 1 : NJ];  // low-bit: the scales (half s term)
 #pragma unroll
         for (int q = 0; q < NMAT; ++q)
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
                 const u32x4 v = *reinterpret_cast<const u32x4*>(sbase + bo[q][j] + kc);
                 bbv[q][j] = __builtin_bit_cast(b8, live ? v : u32x4{0u, 0u, 0u, 0u});
+                if constexpr (BITS != 4) {
+                    const u32x4 sv = lowb ? *reinterpret_cast<const u32x4*>(sbase + so[q][j] + kc) : u32x4{0u, 0u, 0u, 0u};
+                    ssv[q][j] = live ? sv : u32x4{0u, 0u, 0u, 0u};
+                }
             }
         float4 xg[NI][2];
 #pragma unroll
@@ -642,6 +651,27 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs a) {
                     acc[q][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bbv[q][j], xl, acc[q][i][j], 0, 0, 0);
                     acc[q][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bbv[q][j], xm, acc[q][i][j], 0, 0, 0);
                     acc[q][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bbv[q][j], xh, acc[q][i][j], 0, 0, 0);
+                    if constexpr (BITS != 4) {
+                        if (lowb) {
+                            // half s = s / 2 (Q3) or s + s / 2 (Q2), each exact in bf16
+                            const uint32_t sw[4] = {ssv[q][j].x, ssv[q][j].y, ssv[q][j].z, ssv[q][j].w};
+                            uint32_t hs[4];
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                hs[e] = f2bf_rne(__uint_as_float(sw[e] << 16) * 0.5f) |
+                                        f2bf_rne(__uint_as_float(sw[e] & 0xffff0000u) * 0.5f) << 16;
+                            const b8 sh = __builtin_bit_cast(b8, u32x4{hs[0], hs[1], hs[2], hs[3]});
+                            acc[q][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(sh, xl, acc[q][i][j], 0, 0, 0);
+                            acc[q][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(sh, xm, acc[q][i][j], 0, 0, 0);
+                            acc[q][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(sh, xh, acc[q][i][j], 0, 0, 0);
+                            if (BITS == 2) {
+                                const b8 sf = __builtin_bit_cast(b8, ssv[q][j]);
+                                acc[q][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(sf, xl, acc[q][i][j], 0, 0, 0);
+                                acc[q][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(sf, xm, acc[q][i][j], 0, 0, 0);
+                                acc[q][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(sf, xh, acc[q][i][j], 0, 0, 0);
+                            }
+                        }
+                    }
                 }
         }
     };
@@ -1499,10 +1529,11 @@ static bool pf_gemm_prepare(PfGemmArgs& a, int epi) {
     const uint32_t ksplit = std::max<uint32_t>(1, a.ksplit);
     bool sbl = (a.K / 64 / ksplit) % 8 == 0 && smin % 16 == 0;
     for (int q = 0; q < nm; ++q) sbl = sbl && a.seg[q].so % 8 == 0 && a.seg[q].bo % 8 == 0;
-    if (a.X.base)
-        sbl = sbl && a.X.bits == 4 && (uintptr_t)a.X.base % 16 == 0 && a.X.stride % 16 == 0 &&
-              a.X.gate_s % 16 == 0 && a.X.gate_b % 16 == 0 && a.X.up_s % 16 == 0 && a.X.up_b % 16 == 0 &&
-              a.X.down_s % 16 == 0 && a.X.down_b % 16 == 0;
+    auto aligned = [](const ExpertsDev& X) {
+        return (uintptr_t)X.base % 16 == 0 && X.stride % 16 == 0 && X.gate_s % 16 == 0 && X.gate_b % 16 == 0 &&
+               X.up_s % 16 == 0 && X.up_b % 16 == 0 && X.down_s % 16 == 0 && X.down_b % 16 == 0;
+    };
+    if (a.X.base) sbl = sbl && aligned(a.X) && (a.X.bits == 4 || (a.X4.base && aligned(a.X4)));
     return sbl;
 }
 
@@ -1534,15 +1565,22 @@ void launch_pf_gemm_args(const PfGemmArgs& args, int epi, uint32_t grid_y, hipSt
     } while (0)
     const uint32_t xbits = a.X.base ? a.X.bits : 4;
     if (xbits != 4) {
-        // grouped expert GEMMs over Q3 / Q2 records (scales folded per lane)
+        // grouped expert GEMMs over Q3 / Q2 records (scales staged where
+        // the groups come in blocks of 8, else folded per lane)
         if (epi != PE_STORE && epi != PE_SILU_MUL) throw std::runtime_error("low-bit records: gate/up and down only");
         const uint32_t gx = epi == PE_STORE ? (a.N + 255) / 256 : (a.N + 127) / 128;
         const dim3 grid(gx, grid_y, ksplit);
-        if (xbits == 3 && epi == PE_STORE) k_pf_gemm<1, PE_STORE, false, 3><<<grid, PF_WG, 0, st>>>(a);
-        else if (xbits == 3) k_pf_gemm<2, PE_SILU_MUL, false, 3><<<grid, PF_WG, 0, st>>>(a);
-        else if (xbits == 2 && epi == PE_STORE) k_pf_gemm<1, PE_STORE, false, 2><<<grid, PF_WG, 0, st>>>(a);
-        else if (xbits == 2) k_pf_gemm<2, PE_SILU_MUL, false, 2><<<grid, PF_WG, 0, st>>>(a);
+#define PF_LB(B, S)                                                                       \
+    do {                                                                                  \
+        if (epi == PE_STORE) k_pf_gemm<1, PE_STORE, S, B><<<grid, PF_WG, 0, st>>>(a);     \
+        else k_pf_gemm<2, PE_SILU_MUL, S, B><<<grid, PF_WG, 0, st>>>(a);                  \
+    } while (0)
+        if (xbits == 3 && sbl) PF_LB(3, true);
+        else if (xbits == 3) PF_LB(3, false);
+        else if (xbits == 2 && sbl) PF_LB(2, true);
+        else if (xbits == 2) PF_LB(2, false);
         else throw std::runtime_error("expert records of 4, 3 or 2 bits");
+#undef PF_LB
         return;
     }
     switch (epi) {
