@@ -205,6 +205,7 @@ SIGNATURES = [
     ("chk_prefix_read", i32, [P, u32, P, u64]),
     ("chk_fill_u8", i32, [P, u32, u64, P]),
     ("chk_copy_f32", i32, [P, P, u64, P]),
+    ("chk_pf_flash_plan", i32, [u32, u32, u32, C.POINTER(u32), C.POINTER(u32), P, u64, P, u64, C.POINTER(u32)]),
     ("chk_profile_graph", i32, [P, i32, u32, C.POINTER(C.c_double), C.POINTER(u64), C.POINTER(u64)]),
     ("chk_time_decode", i32, [P, u32, u32, C.POINTER(f32), C.POINTER(u32)]),
     ("chk_time_blocks", i32, [P, C.c_int, u32, C.POINTER(u32), u32, P, u32, C.POINTER(u32), u32, C.POINTER(f32)]),

@@ -3256,6 +3256,20 @@ int chk_fill_u8(void* dst, uint32_t value, uint64_t n, void* stream) {
     })
 }
 
+int chk_pf_flash_plan(uint32_t T, uint32_t pos0, uint32_t max_wg, uint32_t* W, uint32_t* nslots, uint32_t* seg,
+                      uint64_t seg_cap, uint32_t* merge, uint64_t merge_cap, uint32_t* nmerge) {
+    CHK_TRY({
+        ensure(T >= 1 && max_wg >= 1, "T and max_wg must be positive");
+        const PfFlashPlan p = pf_flash_plan(T, pos0, max_wg);
+        ensure(p.seg.size() * 4 <= seg_cap && p.merge.size() * 4 <= merge_cap, "plan buffers too small");
+        *W = p.W;
+        *nslots = p.nslots;
+        *nmerge = (uint32_t)p.merge.size();
+        memcpy(seg, p.seg.data(), p.seg.size() * sizeof(uint4));
+        if (!p.merge.empty()) memcpy(merge, p.merge.data(), p.merge.size() * sizeof(uint4));
+    })
+}
+
 int chk_copy_f32(float* dst, const float* src, uint64_t n, void* stream) {
     CHK_TRY({
         hipStream_t st = (hipStream_t)stream;

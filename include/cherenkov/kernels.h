@@ -209,6 +209,17 @@ int chk_phase_bench(int mode, uint32_t wgs, uint32_t phases, uint64_t bytes_per_
 int chk_time_blocks(ChkEngine* e, int kind, uint32_t nb, const uint32_t* layers, uint32_t n_layers, const float* x,
                     uint32_t nx, const uint32_t* pos, uint32_t reps, float* us_per_block);
 
+/* The prefill attention's work plan for T dense rows at pos0 over max_wg
+ * workgroups per kv head (host code, no device call; a test entry point,
+ * no reference counterpart): *W workgroups, each with up to FA_MAXSEG (6)
+ * segments of 4 u32 (row block, first tile, end tile, partial slot or
+ * 0xffffffff for a whole row block; row block 0xffffffff ends the list),
+ * written to seg[W * 6 * 4] (seg_cap u32); merge entries (row block, first
+ * slot, pieces, 0) to merge (merge_cap u32), *nmerge of them; *nslots
+ * partial slots. */
+int chk_pf_flash_plan(uint32_t T, uint32_t pos0, uint32_t max_wg, uint32_t* W, uint32_t* nslots, uint32_t* seg,
+                      uint64_t seg_cap, uint32_t* merge, uint64_t merge_cap, uint32_t* nmerge);
+
 /* Time the decode step on the engine's stream: runs `steps` step_rows(1)
  * + commit pairs, returns milliseconds per step (HIP events). */
 int chk_time_decode(ChkEngine* e, uint32_t first_token, uint32_t steps, float* ms_per_step, uint32_t* last_token);
