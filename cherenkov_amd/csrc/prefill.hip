@@ -1153,7 +1153,7 @@ __global__ void __launch_bounds__(PG_WG) k_pf_group(const uint32_t* __restrict__
                                                     uint32_t tr, uint32_t shared) {
     __shared__ uint32_t cnt[PG_WG];
     __shared__ uint32_t offs[PG_WG];
-    __shared__ uint32_t wsum[PG_WG / 64];
+    __shared__ unsigned long long wsum[PG_WG / 64];
     const uint32_t tau = threadIdx.x, lane = tau & 63, wv = tau >> 6;
     cnt[tau] = 0;
     __syncthreads();
@@ -1198,31 +1198,44 @@ __global__ void __launch_bounds__(PG_WG) k_pf_group(const uint32_t* __restrict__
         ae[1] += 1;
     }
     // one tile list per tile height: tr-row tiles at tiles, 64-row tiles
-    // at tiles + pf_tile_bound(T, topk, E, tr) (*ntiles, ntiles[1] of them)
+    // at tiles + pf_tile_bound(T, topk, E, tr) (*ntiles, ntiles[1] of
+    // them).  Tiles come in five classes, in this order: the tiles of the
+    // longer groups, then the one-tile groups by their 16-row slices, most
+    // first (the GEMMs deal workgroups in list order, so a launch ends on
+    // its shortest ones); per group a count in the 12-bit field of its
+    // class of one 64-bit workgroup prefix sum (the launcher keeps the
+    // counts under 4096).
     const uint32_t trs[2] = {tr, 64u};
     uint32_t* dst = tiles;
+    auto field = [](unsigned long long v, uint32_t k) { return (uint32_t)(v >> (12 * k)) & 0xfffu; };
     for (int h = 0; h < 2; ++h) {
-        const uint32_t nt0 = e <= E ? (cnt[e] + trs[h] - 1) / trs[h] : 0;
+        const uint32_t c = e <= E ? cnt[e] : 0u;
+        const uint32_t nt0 = (c + trs[h] - 1) / trs[h];
         const uint32_t nt = nt0 > 1 ? (nt0 + 1) & ~1u : nt0;
-        const uint32_t packed = nt > 1 ? nt << 16 : nt;
-        uint32_t incl = packed;
+        const uint32_t cls = nt > 1 ? 0u : 5u - min((c + 15) / 16, 4u);
+        const unsigned long long packed = (unsigned long long)nt << (12 * cls);
+        unsigned long long incl = packed;
         for (int d = 1; d < 64; d <<= 1) {
-            const uint32_t o = __shfl_up(incl, d, 64);
+            const unsigned long long o = __shfl_up(incl, d, 64);
             if ((int)lane >= d) incl += o;
         }
         __syncthreads();  // the previous list's wsum reads are done
         if (lane == 63) wsum[wv] = incl;
         __syncthreads();
-        uint32_t off = incl - packed, all = 0;
+        unsigned long long off = incl - packed, all = 0;
         for (uint32_t k = 0; k < wv; ++k) off += wsum[k];
         for (uint32_t k = 0; k < PG_WG / 64; ++k) all += wsum[k];
-        const uint32_t start = nt > 1 ? off >> 16 : (all >> 16) + (off & 0xffffu);
+        uint32_t start = field(off, cls), total = 0;
+        for (uint32_t k = 0; k < 5; ++k) {
+            if (k < cls) start += field(all, k);
+            total += field(all, k);
+        }
         uint2* tdst = tinfo + (dst - tiles);
         for (uint32_t q = 0; q < nt; ++q) {
             dst[start + q] = e << 16 | q;
             tdst[start + q] = make_uint2(offs[e], cnt[e]);
         }
-        if (tau == PG_WG - 1) ntiles[h] = (all >> 16) + (all & 0xffffu);
+        if (tau == PG_WG - 1) ntiles[h] = total;
         // bound of the first list, as pf_tile_bound computes it
         const uint32_t n = (T * topk + tr - 1) / tr + E + (T + tr - 1) / tr + 1 + (E + 1);
         dst = tiles + ((n + 15) & ~15u);
@@ -1651,7 +1664,7 @@ void launch_pf_group(const uint32_t* ids, uint32_t T, uint32_t topk, uint32_t E,
     if (E + 1 > PG_WG) throw std::runtime_error("prefill grouping supports at most 1023 experts");
     if ((uint64_t)T * (topk + 1) >= (1u << 22)) throw std::runtime_error("prefill grouping: too many entries");
     if (tr != 48 && tr != 64) throw std::runtime_error("prefill grouping: tiles of 48 or 64 rows");
-    if (pf_tile_bound(T, topk, E, tr) >= 0x10000u || pf_tile_bound(T, topk, E, 64) >= 0x10000u)
+    if (pf_tile_bound(T, topk, E, tr) >= 0x1000u || pf_tile_bound(T, topk, E, 64) >= 0x1000u)
         throw std::runtime_error("prefill grouping: too many tiles");
     k_pf_group<<<1, PG_WG, 0, st>>>(ids, T, topk, E, cap, list, count, tiles, ntiles, tinfo, goff, pos,
                                     reinterpret_cast<unsigned long long*>(act), layer, tr, shared ? 1u : 0u);
