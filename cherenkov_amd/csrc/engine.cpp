@@ -1899,8 +1899,7 @@ void ChkEngine::pf_hc_read(const HcDev& w, float* inj, uint32_t T, bool for_moe)
     g.xlo = pf.lo;
     g.xs = pf.xs;
     launch_pf_gemm_args(g, PE_STORE, mt, st);
-    launch_pf_hc_down_finish(pf.hc_part, D.hc, T, D.lowrank, D.hc, 1.0f / (float)D.hc, pf.d, inj, st);
-    launch_pf_xprep(pf.d, D.lowrank, T, D.lowrank, pf.hi, pf.lo, pf.xs, st);
+    launch_pf_hc_down_finish(pf.hc_part, D.hc, T, D.lowrank, D.hc, 1.0f / (float)D.hc, pf.d, inj, pf.hi, pf.lo, pf.xs, st);
     PfGemmArgs u{};
     u.seg[0].m = w.up;
     u.nseg = 1;

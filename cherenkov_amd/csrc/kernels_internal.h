@@ -455,8 +455,10 @@ void launch_pf_flash(const float* q_ready, const float* q_raw, const KvDev& kv, 
                      uint32_t nh, uint32_t nkv, uint32_t hd, float scale, const PfFlashLaunch& plan, hipStream_t st);
 void launch_pf_gemm(const Q4Mat& w, const uint4* xhi, const uint4* xlo, const float* xs, float* y, uint32_t T,
                     uint32_t ldy, hipStream_t st);
+// [down; inject] partials -> inj and d, d staged as the up GEMM's operands
+// (hi, lo, xs) with d as the scratch of the unfused form
 void launch_pf_hc_down_finish(const float* part, uint32_t nsplit, uint32_t T, uint32_t lowrank, uint32_t hc,
-                              float alpha, float* d, float* inj, hipStream_t st);
+                              float alpha, float* d, float* inj, uint4* hi, uint4* lo, float* xs, hipStream_t st);
 void launch_pf_router(const uint16_t* router, const uint4* bhi, const uint4* bmid, const uint4* blo, float* logits,
                       uint32_t T, uint32_t E, uint32_t H, hipStream_t st);
 void launch_pf_route(const float* logits, uint32_t T, uint32_t E, uint32_t topk, int norm_topk, uint32_t* ids,

@@ -977,6 +977,57 @@ __global__ void __launch_bounds__(256) k_pf_hc_down_finish(const float* __restri
     else inj[(size_t)t * hc + (n - lowrank)] = 2.0f * sigmoidf_(v);
 }
 
+// The same finisher with d staged straight into the up GEMM's operands
+// (k_pf_prep's planes: fp16 hi / lo in the permuted 8-block order and the
+// per-group sums, summed in k_pf_prep's order), so d itself is never
+// written: thread i < T (lowrank / 8) takes 8-block i % (lowrank / 8) of
+// row i / (lowrank / 8), the T hc threads after them the inject values.
+// lowrank % 64 == 0 keeps every 64-group's eight threads in one aligned
+// lane group.
+__global__ void __launch_bounds__(256) k_pf_hc_down_finish_q(const float* __restrict__ part, uint32_t nsplit,
+                                                             uint64_t zstride, uint32_t T, uint32_t lowrank,
+                                                             uint32_t hc, float alpha, uint4* __restrict__ hi,
+                                                             uint4* __restrict__ lo, float* __restrict__ xs,
+                                                             float* __restrict__ inj) {
+    const uint32_t N = lowrank + hc, blocks = lowrank >> 3;
+    const uint64_t i = (uint64_t)blockIdx.x * CHK_WG + threadIdx.x, nb = (uint64_t)T * blocks;
+    if (i >= nb) {
+        const uint64_t j = i - nb;
+        if (j >= (uint64_t)T * hc) return;
+        const uint32_t t = (uint32_t)(j / hc), g = (uint32_t)(j % hc);
+        float v = 0.0f;
+        for (uint32_t z = 0; z < nsplit; ++z) v += part[z * zstride + (size_t)t * N + lowrank + g];
+        v *= alpha;
+        inj[(size_t)t * hc + g] = 2.0f * sigmoidf_(v);
+        return;
+    }
+    const uint32_t t = (uint32_t)(i / blocks), kb = (uint32_t)(i % blocks);
+    float v[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t z = 0; z < nsplit; ++z) {
+        const float4* p = reinterpret_cast<const float4*>(part + z * zstride + (size_t)t * N + kb * 8);
+        const float4 u0 = p[0], u1 = p[1];
+        v[0] += u0.x; v[1] += u0.y; v[2] += u0.z; v[3] += u0.w;
+        v[4] += u1.x; v[5] += u1.y; v[6] += u1.z; v[7] += u1.w;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = siluf_(v[j] * alpha);
+    float s = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    s += __shfl_xor(s, 4, 64);
+    const float o[8] = {v[0], v[4], v[1] * 0.0625f, v[5] * 0.0625f, v[2], v[6], v[3] * 0.0625f, v[7] * 0.0625f};
+    h8 h, l;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const _Float16 hj = (_Float16)o[j];
+        h[j] = hj;
+        l[j] = (_Float16)(o[j] - (float)hj);
+    }
+    hi[i] = __builtin_bit_cast(uint4, h);
+    lo[i] = __builtin_bit_cast(uint4, l);
+    if ((kb & 7) == 0) xs[(size_t)t * (lowrank >> 6) + (kb >> 3)] = s;
+}
+
 // ------------------------------------------------------------- router
 // logits[t][e] = W_r[e] . x_t (bf16 [E][H], f32 sums) (moe, cpu.rs:506-508),
 // on v_mfma_f32_16x16x32_bf16 with x split into three bf16 terms (natural k
@@ -1637,9 +1688,18 @@ void launch_pf_gemm(const Q4Mat& w, const uint4* xhi, const uint4* xlo, const fl
 }
 
 void launch_pf_hc_down_finish(const float* part, uint32_t nsplit, uint32_t T, uint32_t lowrank, uint32_t hc,
-                              float alpha, float* d, float* inj, hipStream_t st) {
+                              float alpha, float* d, float* inj, uint4* hi, uint4* lo, float* xs, hipStream_t st) {
     const uint64_t n = (uint64_t)T * (lowrank + hc);
-    if (n) k_pf_hc_down_finish<<<(uint32_t)((n + CHK_WG - 1) / CHK_WG), CHK_WG, 0, st>>>(part, nsplit, n, T, lowrank, hc, alpha, d, inj);
+    if (!n) return;
+    if (lowrank % 64 == 0 && (lowrank + hc) % 4 == 0) {
+        // d staged straight into the up GEMM's operands
+        const uint64_t m = (uint64_t)T * (lowrank / 8 + hc);
+        k_pf_hc_down_finish_q<<<(uint32_t)((m + CHK_WG - 1) / CHK_WG), CHK_WG, 0, st>>>(part, nsplit, n, T, lowrank, hc, alpha,
+                                                                                    hi, lo, xs, inj);
+        return;
+    }
+    k_pf_hc_down_finish<<<(uint32_t)((n + CHK_WG - 1) / CHK_WG), CHK_WG, 0, st>>>(part, nsplit, n, T, lowrank, hc, alpha, d, inj);
+    launch_pf_xprep(d, lowrank, T, lowrank, hi, lo, xs, st);
 }
 
 void launch_pf_router(const uint16_t* router, const uint4* bhi, const uint4* bmid, const uint4* blo, float* logits,
