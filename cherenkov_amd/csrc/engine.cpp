@@ -145,6 +145,8 @@ struct PfBufs {
     uint4 *hi, *lo, *bhi, *bmid, *blo;
     float* xs;
     float *inv, *d, *inj_a, *inj_m, *mixed, *hc_part;
+    uint4 *dhi, *dlo;  // d staged as the hyper-connection up GEMM's operands
+    float* dxs;
     float *raw, *z, *a, *b, *conv, *decay, *beta, *y;
     uint32_t ab_split = 1;  // K chunks of the a / b projections
     // the block's out-projection, left as K-chunk partials (in yd) for the
@@ -1724,6 +1726,7 @@ uint64_t ChkEngine::prefill_scratch_bytes(uint64_t C, bool all_logits) const {
     const uint64_t plane = std::max({C * D.hh, C * D.v_dim, C * D.nh * D.hd, C * slots * D.I, C * D.SI, C * D.H});
     b += plane * 2 * 2 + plane / 64 * f + 3 * C * D.H * 2;
     b += C * (3ull * D.hc + D.lowrank + D.H + (uint64_t)D.hc * (D.lowrank + D.hc)) * f;
+    b += C * D.lowrank / 8 * 32 + (C * D.lowrank / 64 + 1) * f;
     const uint64_t dn = C * (2ull * D.conv_dim + 2ull * D.v_dim + (2ull * pf_ab_split(D.H) + 2) * D.nv);
     const uint64_t at = C * (2ull * D.nh * D.hd + 2ull * D.kv_row + D.idx_out + 2ull * D.nh * D.hd);
     b += std::max(dn, at) * f;
@@ -1811,6 +1814,9 @@ void ChkEngine::pf_alloc() {
     pf.blo = pfalloc<uint4>(C * D.H / 8);
     pf.inv = pfalloc<float>(C * D.hc);
     pf.d = pfalloc<float>(C * D.lowrank);
+    pf.dhi = pfalloc<uint4>(C * D.lowrank / 8);
+    pf.dlo = pfalloc<uint4>(C * D.lowrank / 8);
+    pf.dxs = pfalloc<float>(C * D.lowrank / 64 + 1);
     pf.hc_part = pfalloc<float>(C * D.hc * (D.lowrank + D.hc));
     pf.inj_a = pfalloc<float>(C * D.hc);
     pf.inj_m = pfalloc<float>(C * D.hc);
@@ -1899,22 +1905,36 @@ void ChkEngine::pf_hc_read(const HcDev& w, float* inj, uint32_t T, bool for_moe)
     g.xlo = pf.lo;
     g.xs = pf.xs;
     launch_pf_gemm_args(g, PE_STORE, mt, st);
-    launch_pf_hc_down_finish(pf.hc_part, D.hc, T, D.lowrank, D.hc, 1.0f / (float)D.hc, pf.d, inj, pf.hi, pf.lo, pf.xs, st);
+    launch_pf_hc_down_finish(pf.hc_part, D.hc, T, D.lowrank, D.hc, 1.0f / (float)D.hc, pf.d, inj, pf.dhi, pf.dlo, pf.dxs,
+                             st);
     PfGemmArgs u{};
     u.seg[0].m = w.up;
     u.nseg = 1;
     u.N = D.hh;
     u.K = D.lowrank;
     u.M = T;
-    u.xhi = pf.hi;
-    u.xlo = pf.lo;
-    u.xs = pf.xs;
+    u.xhi = pf.dhi;
+    u.xlo = pf.dlo;
+    u.xs = pf.dxs;
     u.hyper = pf.hyper;
     u.inv = pf.inv;
     u.norm = w.norm;
     u.out = pf.mixed;
     u.H = D.H;
     u.hc = D.hc;
+    if (D.H % 64 == 0 && (uintptr_t)w.norm % 16 == 0) {
+        // the mixed rows leave as the next GEMM's operands (and the router's)
+        u.phi = pf.hi;
+        u.plo = pf.lo;
+        u.pxs = pf.xs;
+        if (for_moe) {
+            u.pbhi = pf.bhi;
+            u.pbmid = pf.bmid;
+            u.pblo = pf.blo;
+        }
+        launch_pf_gemm_args(u, PE_HC_UP, mt, st);
+        return;
+    }
     launch_pf_gemm_args(u, PE_HC_UP, mt, st);
     PfPrepArgs p{};
     p.x = pf.mixed;

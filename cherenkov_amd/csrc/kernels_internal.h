@@ -332,6 +332,11 @@ struct PfGemmArgs {
     const uint16_t* norm;    // [hc H]
     float* out;              // [M][H]
     uint32_t H, hc;
+    // PE_HC_UP with phi set: the mixed rows leave as the next GEMM's
+    // operands (k_pf_prep's planes: hi, lo, xs; with pbhi also the router's
+    // three bf16 planes) instead of f32 rows in out
+    uint4 *phi, *plo, *pbhi, *pbmid, *pblo;
+    float* pxs;
     uint32_t vec4;           // set by the launcher: outputs leave as 16-byte stores
 };
 

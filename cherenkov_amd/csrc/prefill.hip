@@ -842,7 +842,80 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs ka) {
             }
             __syncthreads();
             const uint32_t mh = m0 + 32 * h;
-            if (EPI == PE_HC_UP) {
+            if (EPI == PE_HC_UP && a.phi) {
+                // thread: 8-block tid % 8 (outputs 8 (tid % 8) .. + 7 of the
+                // 64, one quant group of the next GEMM's K) of row tid / 8;
+                // the mixed values leave as that GEMM's operands, summed and
+                // split as k_pf_prep does (the row's eight threads are one
+                // aligned lane group)
+                const uint32_t rr = (uint32_t)tid >> 3, b8 = (uint32_t)tid & 7, ol = 8 * b8;
+                const uint32_t o = bx * 64 + ol, sc0 = (ol >> 4) * 64 + (ol & 15);
+                const uint32_t m = mh + rr, mc = min(m, M - 1);
+                const float* hy = a.hyper + (size_t)mc * a.hc * a.H + o;
+                float4 hv[4][2], uv[4][2];
+                uint4 nq[4];
+                float iv[4];
+    #pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const bool on = (uint32_t)j < a.hc;
+                    hv[j][0] = on ? *reinterpret_cast<const float4*>(hy + (size_t)j * a.H) : make_float4(0.f, 0.f, 0.f, 0.f);
+                    hv[j][1] = on ? *reinterpret_cast<const float4*>(hy + (size_t)j * a.H + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+                    nq[j] = on ? *reinterpret_cast<const uint4*>(a.norm + (size_t)j * a.H + o) : make_uint4(0u, 0u, 0u, 0u);
+                    iv[j] = on ? a.inv[(size_t)mc * a.hc + j] : 0.0f;
+                    uv[j][0] = *reinterpret_cast<const float4*>(&sO[rr * OS + sc0 + j * 16]);
+                    uv[j][1] = *reinterpret_cast<const float4*>(&sO[rr * OS + sc0 + j * 16 + 4]);
+                }
+                float v[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    #pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if ((uint32_t)j >= a.hc) continue;
+                    const float hj[8] = {hv[j][0].x, hv[j][0].y, hv[j][0].z, hv[j][0].w,
+                                         hv[j][1].x, hv[j][1].y, hv[j][1].z, hv[j][1].w};
+                    const float uj[8] = {uv[j][0].x, uv[j][0].y, uv[j][0].z, uv[j][0].w,
+                                         uv[j][1].x, uv[j][1].y, uv[j][1].z, uv[j][1].w};
+                    const uint32_t nw[4] = {nq[j].x, nq[j].y, nq[j].z, nq[j].w};
+    #pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float we = __uint_as_float(e & 1 ? nw[e >> 1] & 0xffff0000u : nw[e >> 1] << 16);
+                        v[e] += sigmoidf_(uj[e]) * (hj[e] * iv[j] * we);
+                    }
+                }
+                const float ih = (float)a.hc;
+    #pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = v[e] / ih;
+                float gs = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+                gs += __shfl_xor(gs, 1, 64);
+                gs += __shfl_xor(gs, 2, 64);
+                gs += __shfl_xor(gs, 4, 64);
+                if (m < M) {
+                    const float op[8] = {v[0], v[4], v[1] * 0.0625f, v[5] * 0.0625f, v[2], v[6], v[3] * 0.0625f, v[7] * 0.0625f};
+                    h8 hh, hl;
+    #pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const _Float16 he = (_Float16)op[e];
+                        hh[e] = he;
+                        hl[e] = (_Float16)(op[e] - (float)he);
+                    }
+                    const size_t bi = (size_t)m * (a.H >> 3) + (o >> 3);
+                    a.phi[bi] = __builtin_bit_cast(uint4, hh);
+                    a.plo[bi] = __builtin_bit_cast(uint4, hl);
+                    if (b8 == 0) a.pxs[(size_t)m * (a.H >> 6) + bx] = gs;
+                    if (a.pbhi) {
+                        // three bf16 terms in natural order (the router's)
+                        uint32_t bh[8], bm[8], bl[8];
+    #pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            bh[e] = f2bf_rne(v[e]);
+                            const float r1 = v[e] - __uint_as_float(bh[e] << 16);
+                            bm[e] = f2bf_rne(r1);
+                            bl[e] = f2bf_rne(r1 - __uint_as_float(bm[e] << 16));
+                        }
+                        a.pbhi[bi] = make_uint4(bh[0] | bh[1] << 16, bh[2] | bh[3] << 16, bh[4] | bh[5] << 16, bh[6] | bh[7] << 16);
+                        a.pbmid[bi] = make_uint4(bm[0] | bm[1] << 16, bm[2] | bm[3] << 16, bm[4] | bm[5] << 16, bm[6] | bm[7] << 16);
+                        a.pblo[bi] = make_uint4(bl[0] | bl[1] << 16, bl[2] | bl[3] << 16, bl[4] | bl[5] << 16, bl[6] | bl[7] << 16);
+                    }
+                }
+            } else if (EPI == PE_HC_UP) {
                 // thread: outputs 4 c4 .. + 3 of the 64, rows r0 + 16 k
                 const uint32_t c4 = (uint32_t)tid & 15, r0 = (uint32_t)tid >> 4, ol = 4 * c4;
                 const uint32_t o = bx * 64 + ol, sc0 = (ol >> 4) * 64 + (ol & 15);
@@ -1638,6 +1711,8 @@ void launch_pf_gemm_args(const PfGemmArgs& args, int epi, uint32_t grid_y, hipSt
         v4 = a.H % 4 == 0 && a.N % 4 == 0 && (uintptr_t)a.hyper % 16 == 0 &&
              (uintptr_t)a.out % 16 == 0 && (uintptr_t)a.norm % 8 == 0;
         if (!v4) throw std::runtime_error("prefill hyper-connection GEMMs need 16-byte aligned streams");
+        if (a.phi && (a.H % 64 || (uintptr_t)a.norm % 16 || !a.plo || !a.pxs || (a.pbhi && (!a.pbmid || !a.pblo))))
+            throw std::runtime_error("prefill mix into operands needs hidden % 64 == 0 and 16-byte aligned norms");
     }
     a.vec4 = v4 ? 1u : 0u;
 #define PF_GEMM(NM, E, GX)                                                             \
