@@ -147,6 +147,8 @@ struct PfBufs {
     float *inv, *d, *inj_a, *inj_m, *mixed, *hc_part;
     uint4 *dhi, *dlo;  // d staged as the hyper-connection up GEMM's operands
     float* dxs;
+    uint4 *ahi, *alo;  // the expert activations staged as the down GEMM's operands
+    float* axs;
     float *raw, *z, *a, *b, *conv, *decay, *beta, *y;
     uint32_t ab_split = 1;  // K chunks of the a / b projections
     // the block's out-projection, left as K-chunk partials (in yd) for the
@@ -1727,6 +1729,7 @@ uint64_t ChkEngine::prefill_scratch_bytes(uint64_t C, bool all_logits) const {
     b += plane * 2 * 2 + plane / 64 * f + 3 * C * D.H * 2;
     b += C * (3ull * D.hc + D.lowrank + D.H + (uint64_t)D.hc * (D.lowrank + D.hc)) * f;
     b += C * D.lowrank / 8 * 32 + (C * D.lowrank / 64 + 1) * f;
+    b += C * slots * D.I / 8 * 32 + (C * slots * D.I / 64 + 1) * f;
     const uint64_t dn = C * (2ull * D.conv_dim + 2ull * D.v_dim + (2ull * pf_ab_split(D.H) + 2) * D.nv);
     const uint64_t at = C * (2ull * D.nh * D.hd + 2ull * D.kv_row + D.idx_out + 2ull * D.nh * D.hd);
     b += std::max(dn, at) * f;
@@ -1817,6 +1820,9 @@ void ChkEngine::pf_alloc() {
     pf.dhi = pfalloc<uint4>(C * D.lowrank / 8);
     pf.dlo = pfalloc<uint4>(C * D.lowrank / 8);
     pf.dxs = pfalloc<float>(C * D.lowrank / 64 + 1);
+    pf.ahi = pfalloc<uint4>(C * slots * D.I / 8);
+    pf.alo = pfalloc<uint4>(C * slots * D.I / 8);
+    pf.axs = pfalloc<float>(C * slots * D.I / 64 + 1);
     pf.hc_part = pfalloc<float>(C * D.hc * (D.lowrank + D.hc));
     pf.inj_a = pfalloc<float>(C * D.hc);
     pf.inj_m = pfalloc<float>(C * D.hc);
@@ -2204,6 +2210,9 @@ void ChkEngine::pf_moe(const LayerDev& L, uint32_t T) {
     dn.K = D.I;
     dn.list = nullptr;  // rows in grouped order: the tile's own range
     dn.div = 1;
+    dn.xhi = pf.ahi;
+    dn.xlo = pf.alo;
+    dn.xs = pf.axs;
     // experts hold from one row to over a thousand (T k / E on average):
     // both GEMMs take 64-row tiles, whose empty 16-row slices the kernel
     // skips
@@ -2215,7 +2224,12 @@ void ChkEngine::pf_moe(const LayerDev& L, uint32_t T) {
     const bool shared_grouped = D.SI == D.I;
     launch_pf_group(pf.ids, T, D.topk, D.E, pf.cap, pf.list, pf.count, pf.tiles, pf.ntiles, pf.tinfo, pf.goff, pf.gpos, act,
                     L.moe.record_layer, tr, shared_grouped, st);
-    launch_pf_gemm_args(gu, PE_SILU_MUL, pf_tile_bound(T, D.topk, D.E, tr), st);
+    // the activations leave as the down GEMM's operands where the form
+    // allows, else as f32 rows staged by xprep
+    gu.phi = pf.ahi;
+    gu.plo = pf.alo;
+    gu.pxs = pf.axs;
+    const bool staged = launch_pf_gemm_args(gu, PE_SILU_MUL, pf_tile_bound(T, D.topk, D.E, tr), st);
     PfGemmArgs sh{};
     if (!shared_grouped) {
         sh.seg[0] = PfSeg{L.moe.sh_gate, pf.act_sh, D.SI, 0};
@@ -2229,7 +2243,7 @@ void ChkEngine::pf_moe(const LayerDev& L, uint32_t T) {
         sh.xs = pf.xs;
         launch_pf_gemm_args(sh, PE_SILU_MUL, (T + 63) / 64, st);
     }
-    launch_pf_xprep(pf.act, D.I, T * slots, D.I, pf.hi, pf.lo, pf.xs, st);
+    if (!staged) launch_pf_xprep(pf.act, D.I, T * slots, D.I, pf.ahi, pf.alo, pf.axs, st);
     launch_pf_gemm_args(dn, PE_STORE, pf_tile_bound(T, D.topk, D.E, 64), st);
     if (!shared_grouped) {
         // token t's shared slot of yd: grouped row T k + t, after the routed rows

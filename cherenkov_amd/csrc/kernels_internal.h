@@ -332,9 +332,9 @@ struct PfGemmArgs {
     const uint16_t* norm;    // [hc H]
     float* out;              // [M][H]
     uint32_t H, hc;
-    // PE_HC_UP with phi set: the mixed rows leave as the next GEMM's
-    // operands (k_pf_prep's planes: hi, lo, xs; with pbhi also the router's
-    // three bf16 planes) instead of f32 rows in out
+    // PE_HC_UP / PE_SILU_MUL with phi set: the rows leave as the next
+    // GEMM's operands (k_pf_prep's planes: hi, lo, xs; with pbhi also the
+    // router's three bf16 planes, PE_HC_UP) instead of f32 rows
     uint4 *phi, *plo, *pbhi, *pbmid, *pblo;
     float* pxs;
     uint32_t vec4;           // set by the launcher: outputs leave as 16-byte stores
@@ -434,7 +434,9 @@ void launch_pf_xprep(const float* x, uint32_t ldx, uint32_t T, uint32_t K, uint4
 void launch_pf_hc_prep(float* hyper, const uint16_t* norm, uint32_t H, uint32_t hc, float eps, float* inv,
                        uint4* hi, uint4* lo, float* xs, uint32_t T, const float* part, uint64_t pzs, uint32_t nsplit,
                        const float* pinj, hipStream_t st);
-void launch_pf_gemm_args(const PfGemmArgs& a, int epi, uint32_t grid_y, hipStream_t st);
+// false when the caller asked for operand planes (phi) and the launch wrote
+// its f32 rows instead
+bool launch_pf_gemm_args(const PfGemmArgs& a, int epi, uint32_t grid_y, hipStream_t st);
 // Causal flash attention over a prefill chunk.  Its (row block, token
 // tile) steps are dealt to the workgroups by a plan made on the host
 // (pf_flash_plan, the same for every kv head): per workgroup up to

@@ -774,6 +774,61 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs ka) {
                 *reinterpret_cast<float4*>(a.out + (size_t)m * a.H + o4) =
                     make_float4(sum[0] / ih, sum[1] / ih, sum[2] / ih, sum[3] / ih);
             }
+        } else if (EPI == PE_SILU_MUL && a.phi) {
+            // the activations leave as the down GEMM's operands (k_pf_prep's
+            // planes, summed and split as it does): an 8-block's outputs sit
+            // in lanes kq, kq + 1 (the even one writes it), a 64-group's in
+            // waves 2 g, 2 g + 1 (its sum meets in LDS, the A buffers, free
+            // after the main loop's last barrier)
+            float* sG = reinterpret_cast<float*>(&sA[0][0][0]);  // [wave][slice][col]
+            const uint32_t K8 = a.N >> 3, K64 = a.N >> 6;
+            const uint32_t nw0 = bx * NC + wn * (NC / 4);  // the wave's first output
+            const bool ev = (kq & 1) == 0;
+            float X[NI];
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                float P[NJ];
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    float u[4], pv[4], v[8];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) u[r] = siluf_(acc[0][i][j][r]) * acc[NMAT - 1][i][j][r];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) pv[r] = __shfl_xor(u[r], 16, 64);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        v[r] = ev ? u[r] : pv[r];
+                        v[4 + r] = ev ? pv[r] : u[r];
+                    }
+                    float bs = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+                    bs += __shfl_xor(bs, 32, 64);
+                    P[j] = bs;
+                    if (ev && mok[i]) {
+                        const float op[8] = {v[0], v[4], v[1] * 0.0625f, v[5] * 0.0625f,
+                                             v[2], v[6], v[3] * 0.0625f, v[7] * 0.0625f};
+                        h8 hh, hl;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            const _Float16 he = (_Float16)op[e];
+                            hh[e] = he;
+                            hl[e] = (_Float16)(op[e] - (float)he);
+                        }
+                        const size_t bi = (size_t)yrow[i] * K8 + (nw0 + j * 16 + (kq >> 1) * 8) / 8;
+                        a.phi[bi] = __builtin_bit_cast(uint4, hh);
+                        a.plo[bi] = __builtin_bit_cast(uint4, hl);
+                    }
+                }
+                X[i] = P[0] + P[NJ - 1];
+            }
+            __syncthreads();
+            if (kq == 0)
+#pragma unroll
+                for (int i = 0; i < NI; ++i) sG[(wn * NI + i) * 16 + col] = X[i];
+            __syncthreads();
+            if (kq == 0 && (wn & 1) == 0)
+#pragma unroll
+                for (int i = 0; i < NI; ++i)
+                    if (mok[i]) a.pxs[(size_t)yrow[i] * K64 + nw0 / 64] = X[i] + sG[((wn + 1) * NI + i) * 16 + col];
         } else {
             uint32_t n4[NJ];
             PfSeg sj[NJ];
@@ -1693,11 +1748,17 @@ static bool pf_gemm_prepare(PfGemmArgs& a, int epi) {
 }
 
 
-void launch_pf_gemm_args(const PfGemmArgs& args, int epi, uint32_t grid_y, hipStream_t st) {
+bool launch_pf_gemm_args(const PfGemmArgs& args, int epi, uint32_t grid_y, hipStream_t st) {
     if (args.K % 64 || !args.K) throw std::runtime_error("prefill GEMM needs K a multiple of 64");
-    if (!grid_y) return;
+    if (!grid_y) return true;
     PfGemmArgs a = args;
     const bool sbl = pf_gemm_prepare(a, epi);
+    // the epilogue writes the next GEMM's operands (phi) where it can: the
+    // mix always, gate/up in its transposed (staged-scale) form; else its
+    // f32 rows, and the caller stages them
+    if (a.phi && epi == PE_SILU_MUL && (!sbl || a.N % 64 || (uintptr_t)a.phi % 16 || (uintptr_t)a.plo % 16 || !a.pxs))
+        a.phi = nullptr;
+    const bool fused = !args.phi || a.phi;
     const uint32_t ksplit = std::max<uint32_t>(1, a.ksplit);
     if ((a.K / 64) % ksplit || (ksplit > 1 && epi != PE_STORE))
         throw std::runtime_error("split K needs whole groups per chunk and a plain store");
@@ -1738,7 +1799,7 @@ void launch_pf_gemm_args(const PfGemmArgs& args, int epi, uint32_t grid_y, hipSt
         else if (xbits == 2) PF_LB(2, false);
         else throw std::runtime_error("expert records of 4, 3 or 2 bits");
 #undef PF_LB
-        return;
+        return fused;
     }
     switch (epi) {
     case PE_STORE: PF_GEMM(1, PE_STORE, (a.N + 255) / 256); break;
@@ -1746,6 +1807,7 @@ void launch_pf_gemm_args(const PfGemmArgs& args, int epi, uint32_t grid_y, hipSt
     default: PF_GEMM(2, PE_SILU_MUL, (a.N + 127) / 128); break;
     }
 #undef PF_GEMM
+    return fused;
 }
 
 void launch_pf_gemm(const Q4Mat& w, const uint4* xhi, const uint4* xlo, const float* xs, float* y, uint32_t T,
