@@ -1938,10 +1938,9 @@ void ChkEngine::pf_hc_read(const HcDev& w, float* inj, uint32_t T, bool for_moe)
             u.pbmid = pf.bmid;
             u.pblo = pf.blo;
         }
-        launch_pf_gemm_args(u, PE_HC_UP, mt, st);
-        return;
     }
-    launch_pf_gemm_args(u, PE_HC_UP, mt, st);
+    // (false: the launch wrote the f32 rows, staged below)
+    if (launch_pf_gemm_args(u, PE_HC_UP, mt, st) && u.phi) return;
     PfPrepArgs p{};
     p.x = pf.mixed;
     p.ldx = D.H;

@@ -1754,10 +1754,11 @@ bool launch_pf_gemm_args(const PfGemmArgs& args, int epi, uint32_t grid_y, hipSt
     PfGemmArgs a = args;
     const bool sbl = pf_gemm_prepare(a, epi);
     // the epilogue writes the next GEMM's operands (phi) where it can: the
-    // mix always, gate/up in its transposed (staged-scale) form; else its
-    // f32 rows, and the caller stages them
+    // mix in its staged form, gate/up in its transposed (staged-scale)
+    // form; else its f32 rows, and the caller stages them
     if (a.phi && epi == PE_SILU_MUL && (!sbl || a.N % 64 || (uintptr_t)a.phi % 16 || (uintptr_t)a.plo % 16 || !a.pxs))
         a.phi = nullptr;
+    if (a.phi && epi == PE_HC_UP && sbl) a.phi = nullptr;
     const bool fused = !args.phi || a.phi;
     const uint32_t ksplit = std::max<uint32_t>(1, a.ksplit);
     if ((a.K / 64) % ksplit || (ksplit > 1 && epi != PE_STORE))

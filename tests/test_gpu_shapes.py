@@ -64,6 +64,14 @@ def test_hidden_4096_matches_oracle(have_gpu):
     prefill_then_decode(presets.wide(), "hidden 4096", prompt_len=20, steps=5, seed=122)
 
 
+def test_hc_lowrank_512_matches_oracle(have_gpu):
+    """A hyper-connection low rank of 512 (8 quant groups: the up GEMM runs
+    its staged-scale form, whose rows are then staged by their own pass)."""
+    cfg = presets.tiny(mtp=0)
+    cfg.hc_lowrank = 512
+    prefill_then_decode(cfg, "hc low rank 512", prompt_len=40, steps=3, seed=123)
+
+
 @pytest.mark.parametrize("si", [512, 128])
 def test_shared_expert_width_differs_from_routed(have_gpu, si):
     """Routed experts of width 256 with a shared expert of `si`: GEMM
