@@ -155,10 +155,15 @@ struct PfBufs {
     // next hyper-connection read to inject
     const float* pend = nullptr;
     uint32_t pend_split = 0;
+    // the expert block's combine and inject, left (in yd) for the next
+    // hyper-connection read: the streams it goes into, and the rows
+    float* moe_pend = nullptr;
+    uint32_t moe_pend_T = 0;
     float* dcw;  // chunked-scan workspace (null: sequential scan)
     float *q_raw, *k_raw, *v_raw, *idx_raw, *q_ready, *attn_out;
     float *logits, *sg, *wts;
     uint32_t *ids, *list, *count, *tiles, *ntiles;
+    uint32_t* gcnt;  // [E][PF_GCNT_STRIDE] per-expert entry counts, zero between layers
     uint2* tinfo;   // per tile of both lists: (group's first grouped row, group's rows)
     uint32_t* goff;  // [E + 1] each group's first grouped row of act / yd
     uint32_t* gpos;  // [T][k + 1] each entry's group << 22 | place in the group
@@ -1509,6 +1514,7 @@ struct ChkEngine {
     void pf_attention(const LayerDev& L, uint32_t T, uint32_t pos0, const KvDev* kvo = nullptr);
     void pf_mtp(const uint32_t* toks, uint32_t c0, uint32_t T, uint32_t pos0, bool last, uint32_t next_after);
     void pf_moe(const LayerDev& L, uint32_t T);
+    void pf_moe_flush();
     void prefill_gemm(const uint32_t* toks, uint32_t n, uint32_t next_after, bool all_logits, uint32_t* next);
     void mtp_draft(const uint32_t* next, uint32_t n, uint32_t chain, uint32_t* drafts, uint32_t* nd);
 };
@@ -1733,7 +1739,7 @@ uint64_t ChkEngine::prefill_scratch_bytes(uint64_t C, bool all_logits) const {
     const uint64_t dn = C * (2ull * D.conv_dim + 2ull * D.v_dim + (2ull * pf_ab_split(D.H) + 2) * D.nv);
     const uint64_t at = C * (2ull * D.nh * D.hd + 2ull * D.kv_row + D.idx_out + 2ull * D.nh * D.hd);
     b += std::max(dn, at) * f;
-    b += C * (D.E + 1 + 2ull * D.topk) * f + (D.E + 1ull) * C * 4 + (D.E + 1) * 4;
+    b += C * (D.E + 1 + 2ull * D.topk) * f + (D.E + 1ull) * C * 4 + (PF_GCNT_STRIDE + 1ull) * (D.E + 1) * 4;
     b += (uint64_t)(pf_tile_bound((uint32_t)C, D.topk, D.E, 48) + pf_tile_bound((uint32_t)C, D.topk, D.E, 64)) * 12 +
          C * slots * (D.I + D.H) * f + C * slots * 4 + (D.E + 1) * 4;
     if (D.SI != D.I) b += C * D.SI * f;
@@ -1859,6 +1865,8 @@ void ChkEngine::pf_alloc() {
     pf.ids = pfalloc<uint32_t>(C * D.topk);
     pf.list = pfalloc<uint32_t>((D.E + 1) * C);
     pf.count = pfalloc<uint32_t>(D.E + 1);
+    pf.gcnt = pfalloc<uint32_t>((D.E + 1) * PF_GCNT_STRIDE);
+    HIPCHK(hipMemset(pf.gcnt, 0, (D.E + 1) * PF_GCNT_STRIDE * 4));
     pf.tiles = pfalloc<uint32_t>(pf_tile_bound((uint32_t)C, D.topk, D.E, 48) + pf_tile_bound((uint32_t)C, D.topk, D.E, 64));
     pf.tinfo = pfalloc<uint2>(pf_tile_bound((uint32_t)C, D.topk, D.E, 48) + pf_tile_bound((uint32_t)C, D.topk, D.E, 64));
     pf.goff = pfalloc<uint32_t>(D.E + 1);
@@ -1892,8 +1900,16 @@ void ChkEngine::pf_alloc() {
 // up GEMM with the sigmoid mix, then the mixed rows as the next operands.
 void ChkEngine::pf_hc_read(const HcDev& w, float* inj, uint32_t T, bool for_moe) {
     const uint32_t mt = (T + 63) / 64;
+    // a pending expert combine joins the norm pass (which reads and
+    // rewrites every stream anyway) unless an out-projection is pending too
+    PfCombine mc{};
+    if (pf.moe_pend && pf.moe_pend == pf.hyper && pf.moe_pend_T == T && !pf.pend) {
+        mc = PfCombine{pf.yd, pf.goff, pf.gpos, pf.wts, pf.sg, pf.inj_m, D.topk};
+        pf.moe_pend = nullptr;
+    }
+    pf_moe_flush();
     launch_pf_hc_prep(pf.hyper, w.norm, D.H, D.hc, D.eps, pf.inv, pf.hi, pf.lo, pf.xs, T, pf.pend,
-                      (uint64_t)pf.cap * D.H, pf.pend_split, pf.inj_a, st);
+                      (uint64_t)pf.cap * D.H, pf.pend_split, pf.inj_a, st, mc);
     pf.pend = nullptr;
     // [down; inject] is narrow (lowrank + hc outputs) over a long K = hc H:
     // split K by stream, partials summed in stream order by the finisher
@@ -1965,6 +1981,7 @@ void ChkEngine::pf_hc_read(const HcDev& w, float* inj, uint32_t T, bool for_moe)
 // workgroup each) into yd, free until the expert down projection.
 void ChkEngine::pf_out_proj(const Q4Mat& m, uint32_t K, uint32_t T) {
     if (pf.pend) throw std::runtime_error("an out-projection is already pending");
+    pf_moe_flush();  // (its partials take yd)
     const uint32_t G = K / 64;
     PfGemmArgs o{};
     o.seg[0] = PfSeg{m, pf.yd, D.H, 0};
@@ -2181,8 +2198,11 @@ void ChkEngine::pf_moe(const LayerDev& L, uint32_t T) {
     launch_pf_router(L.moe.router, pf.bhi, pf.bmid, pf.blo, pf.logits, T, D.E, D.H, st);
     // the chunk's last row also as this layer's "last routes", as a row step leaves them
     const uint64_t roff = (uint64_t)L.moe.record_layer * MAX_NB * D.topk;
+    const bool shared_grouped = D.SI == D.I;
+    // (also places every entry in its expert's group: list, gpos)
     launch_pf_route(pf.logits, T, D.E, D.topk, D.norm_topk, pf.ids, pf.wts, s.route_ids + roff, s.route_w + roff,
-                    L.moe.shared_gate, pf.bhi, pf.bmid, pf.blo, pf.sg, D.H, st);
+                    L.moe.shared_gate, pf.bhi, pf.bmid, pf.blo, pf.sg, D.H, pf.gcnt, pf.list, pf.gpos, pf.cap,
+                    shared_grouped, st);
     PfGemmArgs gu{};
     gu.seg[0] = PfSeg{L.moe.sh_gate, pf.act, D.I, 0};
     gu.seg[1].m = L.moe.sh_up;
@@ -2220,8 +2240,7 @@ void ChkEngine::pf_moe(const LayerDev& L, uint32_t T) {
     dn.tinfo = pf.tinfo + pf_tile_bound(T, D.topk, D.E, tr);
     dn.ntiles = pf.ntiles + 1;
     // (also counts the layer's expert activity)
-    const bool shared_grouped = D.SI == D.I;
-    launch_pf_group(pf.ids, T, D.topk, D.E, pf.cap, pf.list, pf.count, pf.tiles, pf.ntiles, pf.tinfo, pf.goff, pf.gpos, act,
+    launch_pf_group(pf.gcnt, T, D.topk, D.E, pf.cap, pf.count, pf.tiles, pf.ntiles, pf.tinfo, pf.goff, act,
                     L.moe.record_layer, tr, shared_grouped, st);
     // the activations leave as the down GEMM's operands where the form
     // allows, else as f32 rows staged by xprep
@@ -2253,7 +2272,18 @@ void ChkEngine::pf_moe(const LayerDev& L, uint32_t T) {
         sh.K = D.SI;
         launch_pf_gemm_args(sh, PE_STORE, (T + 63) / 64, st);
     }
-    launch_pf_moe_combine(pf.yd, pf.goff, pf.gpos, pf.wts, pf.sg, pf.inj_m, pf.hyper, T, D.H, D.topk, D.hc, st);
+    // the weighted combine and its inject (cpu.rs:527-540, 971-979) are
+    // left to the next hyper-connection read; other readers of the streams
+    // flush them first
+    pf.moe_pend = pf.hyper;
+    pf.moe_pend_T = T;
+}
+
+void ChkEngine::pf_moe_flush() {
+    if (!pf.moe_pend) return;
+    launch_pf_moe_combine(pf.yd, pf.goff, pf.gpos, pf.wts, pf.sg, pf.inj_m, pf.moe_pend, pf.moe_pend_T, D.H, D.topk,
+                          D.hc, st);
+    pf.moe_pend = nullptr;
 }
 
 void ChkEngine::prefill_gemm(const uint32_t* toks, uint32_t n, uint32_t next_after, bool all_logits,
@@ -2278,20 +2308,25 @@ void ChkEngine::prefill_gemm(const uint32_t* toks, uint32_t n, uint32_t next_aft
             HIPCHK(hipMemcpy(pf.ple_ids, ids.data(), ids.size() * 4, hipMemcpyHostToDevice));
         }
         pf.pend = nullptr;  // (an earlier failed chunk may have left one)
+        pf.moe_pend = nullptr;
+        HIPCHK(hipMemsetAsync(pf.gcnt, 0, (D.E + 1) * PF_GCNT_STRIDE * 4, st));  // (and its expert counts)
         // the chunk's flash plan, while the stream is idle
         if (const uint32_t td = pf_dense_rows(T, pos0)) pf_flash_launch(td, pos0);
         launch_pf_embed(pf.tokens, embed, pf.hyper, D.H, D.hc, T, st);
         for (uint32_t l = 0; l < c.num_hidden_layers; ++l) {
             const LayerDev& L = layers[l];
-            if (L.has_ple)
+            if (L.has_ple) {
+                pf_moe_flush();
                 ple_rows(L.ple, pf.ple_ids, ngram_heads, pf.hyper, pf.pos, T, pf.ple_e, pf.ple_key, pf.ple_value, pf.ple_gated,
                          pf.ple_gvn, nullptr, true);
+            }
             pf_hc_read(L.attn_hc, pf.inj_a, T, false);
             if (L.linear) pf_deltanet(L, T);
             else pf_attention(L, T, pos0);
             pf_hc_read(L.mlp_hc, pf.inj_m, T, true);
             pf_moe(L, T);
         }
+        pf_moe_flush();
         if (all_logits) {
             // every row through the final mixer and the LM head, four rows
             // per launch pair (the decode kernels; a checking mode)
@@ -2351,8 +2386,10 @@ void ChkEngine::pf_mtp(const uint32_t* toks, uint32_t c0, uint32_t T, uint32_t p
         pf_attention(L, T, pos0, &mtp_kv);
         pf_hc_read(L.mlp_hc, pf.inj_m, T, true);
         pf_moe(L, T);
+        pf_moe_flush();
     } catch (...) {
         pf.hyper = trunk;
+        pf.moe_pend = nullptr;
         throw;
     }
     pf.hyper = trunk;

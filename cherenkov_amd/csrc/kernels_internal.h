@@ -431,9 +431,20 @@ void launch_attn(const AttnArgs& a, int nb, hipStream_t st);
 void launch_pf_prep(const PfPrepArgs& a, hipStream_t st);
 void launch_pf_xprep(const float* x, uint32_t ldx, uint32_t T, uint32_t K, uint4* hi, uint4* lo, float* xs,
                      hipStream_t st);
+// An expert block's output left for the next hyper-connection read to
+// combine and inject (launch_pf_moe_combine's inputs); yd null: none.
+struct PfCombine {
+    const float* yd = nullptr;
+    const uint32_t* goff = nullptr;
+    const uint32_t* pos = nullptr;
+    const float* wts = nullptr;
+    const float* sg = nullptr;
+    const float* inj = nullptr;
+    uint32_t topk = 0;
+};
 void launch_pf_hc_prep(float* hyper, const uint16_t* norm, uint32_t H, uint32_t hc, float eps, float* inv,
                        uint4* hi, uint4* lo, float* xs, uint32_t T, const float* part, uint64_t pzs, uint32_t nsplit,
-                       const float* pinj, hipStream_t st);
+                       const float* pinj, hipStream_t st, const PfCombine& mc = PfCombine{});
 // false when the caller asked for operand planes (phi) and the launch wrote
 // its f32 rows instead
 bool launch_pf_gemm_args(const PfGemmArgs& a, int epi, uint32_t grid_y, hipStream_t st);
@@ -470,10 +481,13 @@ void launch_pf_router(const uint16_t* router, const uint4* bhi, const uint4* bmi
                       uint32_t T, uint32_t E, uint32_t H, hipStream_t st);
 void launch_pf_route(const float* logits, uint32_t T, uint32_t E, uint32_t topk, int norm_topk, uint32_t* ids,
                      float* wts, uint32_t* last_ids, float* last_wts, const uint16_t* shared_gate, const uint4* bhi,
-                     const uint4* bmid, const uint4* blo, float* sg, uint32_t H, hipStream_t st);
-void launch_pf_group(const uint32_t* ids, uint32_t T, uint32_t topk, uint32_t E, uint32_t cap, uint32_t* list,
-                     uint32_t* count, uint32_t* tiles, uint32_t* ntiles, uint2* tinfo, uint32_t* goff, uint32_t* pos,
-                     uint64_t* act, uint32_t layer, uint32_t tr, bool shared, hipStream_t st);
+                     const uint4* bmid, const uint4* blo, float* sg, uint32_t H, uint32_t* gcnt, uint32_t* list,
+                     uint32_t* pos, uint32_t cap, bool shared, hipStream_t st);
+// words between two experts' entry counters of the routing pass (gcnt)
+constexpr uint32_t PF_GCNT_STRIDE = 32;
+void launch_pf_group(uint32_t* gcnt, uint32_t T, uint32_t topk, uint32_t E, uint32_t cap, uint32_t* count,
+                     uint32_t* tiles, uint32_t* ntiles, uint2* tinfo, uint32_t* goff, uint64_t* act, uint32_t layer,
+                     uint32_t tr, bool shared, hipStream_t st);
 uint32_t pf_tile_bound(uint32_t T, uint32_t topk, uint32_t E, uint32_t tr);
 void launch_pf_moe_combine(const float* yd, const uint32_t* goff, const uint32_t* pos, const float* wts, const float* sg,
                            const float* inj, float* hyper, uint32_t T, uint32_t H, uint32_t topk, uint32_t hc,

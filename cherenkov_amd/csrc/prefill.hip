@@ -122,16 +122,68 @@ __global__ void __launch_bounds__(256) k_pf_prep(PfPrepArgs a) {
 // With `part`, first the inject of the block before (cpu.rs:971-979) the
 // out-projection left as nsplit K-chunk partials: hyper[t][g H + n] +=
 // (sum_z part[z][t][n]) inj[t][g], written back to hyper.
+// MK >= 0: instead the expert block before, left as its down rows (mc,
+// k_pf_moe_combine's inputs and sums: the routed slots in rank order,
+// then the gated shared slot; MK routed slots at compile time, 0: mc.topk
+// at run time), injected the same way.
+template <int MK>
 __global__ void __launch_bounds__(256) k_pf_hc_prep(float* __restrict__ hyper, const uint16_t* __restrict__ norm,
                                                     uint32_t H, uint32_t hc, float eps, float* __restrict__ inv_out,
                                                     uint4* __restrict__ hi, uint4* __restrict__ lo,
                                                     float* __restrict__ xs, const float* __restrict__ part,
-                                                    uint64_t pzs, uint32_t nsplit, const float* __restrict__ pinj) {
+                                                    uint64_t pzs, uint32_t nsplit, const float* __restrict__ pinj,
+                                                    PfCombine mc) {
     __shared__ float red[4][4];
     const uint32_t t = blockIdx.x, tau = threadIdx.x, bps = H >> 3, hh = H * hc;
     float* row = hyper + (size_t)t * hh;
     float pv[2][8];
-    if (part) {
+    if constexpr (MK >= 0) {
+        const uint32_t K = MK > 0 ? (uint32_t)MK : mc.topk, slots = K + 1;
+        const uint32_t* pt = mc.pos + (size_t)t * slots;
+        auto grow = [&](uint32_t r) {
+            const uint32_t q = pt[r];
+            return (size_t)(mc.goff[q >> 22] + (q & 0x3fffffu)) * H;
+        };
+        const float sgv = sigmoidf_(mc.sg[t]);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t kb = min(tau + 256 * j, bps - 1);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) pv[j][e] = 0.0f;
+            if (256 * j >= bps) continue;  // uniform
+            auto add = [&](size_t ro, float w) {
+                const float4* p = reinterpret_cast<const float4*>(mc.yd + ro + kb * 8);
+                const float4 u0 = p[0], u1 = p[1];
+                const float w8[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) pv[j][e] += w * w8[e];
+            };
+            if constexpr (MK > 0) {
+                size_t ro[MK + 1];
+#pragma unroll
+                for (int r = 0; r <= MK; ++r) ro[r] = grow(r);
+                float4 u[MK + 1][2];
+#pragma unroll
+                for (int r = 0; r <= MK; ++r) {
+                    const float4* p = reinterpret_cast<const float4*>(mc.yd + ro[r] + kb * 8);
+                    u[r][0] = p[0];
+                    u[r][1] = p[1];
+                }
+#pragma unroll
+                for (int r = 0; r <= MK; ++r) {
+                    const float w = r < MK ? mc.wts[(size_t)t * MK + r] : sgv;
+                    const float w8[8] = {u[r][0].x, u[r][0].y, u[r][0].z, u[r][0].w,
+                                         u[r][1].x, u[r][1].y, u[r][1].z, u[r][1].w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) pv[j][e] += w * w8[e];
+                }
+            } else {
+                for (uint32_t r = 0; r < K; ++r) add(grow(r), mc.wts[(size_t)t * K + r]);
+                add(grow(K), sgv);
+            }
+        }
+        pinj = mc.inj;
+    } else if (part) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const uint32_t kb = min(tau + 256 * j, bps - 1);
@@ -156,7 +208,7 @@ __global__ void __launch_bounds__(256) k_pf_hc_prep(float* __restrict__ hyper, c
             const bool ok = (uint32_t)g < hc && kb < bps;
             float4* p = reinterpret_cast<float4*>(row + (size_t)(ok ? g : 0) * H + (ok ? kb : 0) * 8);
             float4 u0 = p[0], u1 = p[1];
-            if (part && ok) {
+            if ((MK >= 0 || part) && ok) {
                 const float ij = pinj[(size_t)t * hc + g];
                 u0 = make_float4(u0.x + pv[j][0] * ij, u0.y + pv[j][1] * ij, u0.z + pv[j][2] * ij, u0.w + pv[j][3] * ij);
                 u1 = make_float4(u1.x + pv[j][4] * ij, u1.y + pv[j][5] * ij, u1.z + pv[j][6] * ij, u1.w + pv[j][7] * ij);
@@ -1252,12 +1304,21 @@ __global__ void __launch_bounds__(256) k_pf_router(const uint16_t* __restrict__ 
 // One wave per token: softmax top-k (route_row) and the renormalised
 // weights in rank order (cpu.rs:508-525); the last token's routing also
 // goes to last_ids / last_wts (the layer's "last routes").
+// Each entry t (k+1) + r also takes its place in its expert's group here
+// (the grouping pass's list and pos, below): an atomic count per expert
+// in gcnt, one 128-byte line each (PF_GCNT_STRIDE words apart; zero on
+// entry; the grouping pass reads and clears them), so the entries'
+// scattered stores are spread over the launch's workgroups.
+// Places within a group come in arrival order, which only moves rows
+// (every GEMM row is computed on its own).
 __global__ void __launch_bounds__(256) k_pf_route(const float* __restrict__ logits, uint32_t T, uint32_t E,
                                                   uint32_t topk, int norm_topk, uint32_t* __restrict__ ids,
                                                   float* __restrict__ wts, uint32_t* __restrict__ last_ids,
                                                   float* __restrict__ last_wts, const uint16_t* __restrict__ shared_gate,
                                                   const uint4* __restrict__ bhi, const uint4* __restrict__ bmid,
-                                                  const uint4* __restrict__ blo, float* __restrict__ sg, uint32_t H) {
+                                                  const uint4* __restrict__ blo, float* __restrict__ sg, uint32_t H,
+                                                  uint32_t* __restrict__ gcnt, uint32_t* __restrict__ list,
+                                                  uint32_t* __restrict__ pos, uint32_t cap, uint32_t shared) {
     const int lane = threadIdx.x & 63;
     const uint32_t t = blockIdx.x * (CHK_WG >> 6) + wave_id();
     if (t >= T) return;
@@ -1299,13 +1360,28 @@ __global__ void __launch_bounds__(256) k_pf_route(const float* __restrict__ logi
             last_ids[lane] = my_id;
             last_wts[lane] = w;
         }
+        // route_row's ids are distinct and below E: a group holds at most
+        // one entry per token, so p < T <= cap
+        const uint32_t e = min(my_id, E - 1), slots = topk + 1;
+        const uint32_t p = atomicAdd(&gcnt[(size_t)e * PF_GCNT_STRIDE], 1u);
+        if (p < cap) {
+            list[(size_t)e * cap + p] = t * slots + lane;
+            pos[(size_t)t * slots + lane] = e << 22 | p;
+        }
+    }
+    if (lane == 0) {
+        // the shared slot: place t of group E
+        if (shared) list[(size_t)E * cap + t] = t * (topk + 1) + topk;
+        pos[(size_t)t * (topk + 1) + topk] = E << 22 | t;
     }
 }
 
 // Entries grouped by expert (the CSR lists of gpu/prefill/experts.rs:29-137):
 // list[e][0..count[e]) holds the entries t (k+1) + slot routed to e (any
 // order: every GEMM row is independent), list[E] every token's shared
-// slot t (k+1) + k, and tiles[] the (group, tr-row tile) pairs, *ntiles of
+// slot t (k+1) + k (both, and pos below, stored by the routing pass, which
+// leaves the per-expert counts in gcnt; this pass clears them for the
+// next layer), and tiles[] the (group, tr-row tile) pairs, *ntiles of
 // them: first every group of two or more tiles, its count rounded up to
 // even (the extra tile has no rows), so each starts at an even position
 // (the GEMMs run tiles 2c and 2c + 1 on one XCD), then the one-tile groups.
@@ -1323,33 +1399,18 @@ __global__ void __launch_bounds__(256) k_pf_route(const float* __restrict__ logi
 // runs as dense GEMMs of its own).  One workgroup.
 constexpr uint32_t PG_WG = 1024;  // threads of the grouping workgroup (one group each)
 
-__global__ void __launch_bounds__(PG_WG) k_pf_group(const uint32_t* __restrict__ ids, uint32_t T, uint32_t topk,
-                                                    uint32_t E, uint32_t cap, uint32_t* __restrict__ list,
-                                                    uint32_t* __restrict__ count, uint32_t* __restrict__ tiles,
-                                                    uint32_t* __restrict__ ntiles, uint2* __restrict__ tinfo,
-                                                    uint32_t* __restrict__ goff, uint32_t* __restrict__ pos,
+__global__ void __launch_bounds__(PG_WG) k_pf_group(uint32_t* __restrict__ gcnt, uint32_t T, uint32_t E,
+                                                    uint32_t cap, uint32_t* __restrict__ count,
+                                                    uint32_t* __restrict__ tiles, uint32_t* __restrict__ ntiles,
+                                                    uint2* __restrict__ tinfo, uint32_t* __restrict__ goff,
                                                     unsigned long long* __restrict__ act, uint32_t layer,
-                                                    uint32_t tr, uint32_t shared) {
+                                                    uint32_t tr, uint32_t topk, uint32_t shared) {
     __shared__ uint32_t cnt[PG_WG];
     __shared__ uint32_t offs[PG_WG];
     __shared__ unsigned long long wsum[PG_WG / 64];
     const uint32_t tau = threadIdx.x, lane = tau & 63, wv = tau >> 6;
-    cnt[tau] = 0;
-    __syncthreads();
-    const uint32_t slots = topk + 1;
-    for (uint32_t i = tau; i < T * topk; i += PG_WG) {
-        const uint32_t t = i / topk, r = i % topk;
-        const uint32_t e = min(ids[i], E - 1);
-        const uint32_t p = atomicAdd(&cnt[e], 1u);
-        list[(size_t)e * cap + p] = t * slots + r;
-        pos[t * slots + r] = e << 22 | p;
-    }
-    for (uint32_t t = tau; t < T; t += PG_WG) {
-        if (shared) list[(size_t)E * cap + t] = t * slots + topk;
-        pos[t * slots + topk] = E << 22 | t;
-    }
-    __syncthreads();
-    if (tau == 0) cnt[E] = shared ? T : 0;
+    cnt[tau] = tau < E ? min(gcnt[(size_t)tau * PF_GCNT_STRIDE], cap) : tau == E && shared ? T : 0u;
+    if (tau < E) gcnt[(size_t)tau * PF_GCNT_STRIDE] = 0;
     __syncthreads();
     const uint32_t e = tau;
     // grouped order: group e's rows start at the sum of the counts before it
@@ -1707,11 +1768,19 @@ void launch_pf_xprep(const float* x, uint32_t ldx, uint32_t T, uint32_t K, uint4
 
 void launch_pf_hc_prep(float* hyper, const uint16_t* norm, uint32_t H, uint32_t hc, float eps, float* inv,
                        uint4* hi, uint4* lo, float* xs, uint32_t T, const float* part, uint64_t pzs, uint32_t nsplit,
-                       const float* pinj, hipStream_t st) {
+                       const float* pinj, hipStream_t st, const PfCombine& mc) {
     if (H > 4096 || hc > 4 || H % 64) throw std::runtime_error("prefill hyper-connection norm needs hidden <= 4096, hc <= 4");
     if (part && (!nsplit || pzs % 4 || (uintptr_t)part % 16 || !pinj))
         throw std::runtime_error("pending inject needs 16-byte aligned partials");
-    if (T) k_pf_hc_prep<<<T, CHK_WG, 0, st>>>(hyper, norm, H, hc, eps, inv, hi, lo, xs, part, pzs, nsplit, pinj);
+    if (mc.yd) {
+        if (part) throw std::runtime_error("prefill hyper-connection norm: one pending inject at a time");
+        if ((uintptr_t)mc.yd % 16 || !mc.inj || !mc.topk) throw std::runtime_error("pending combine needs 16-byte rows");
+        if (!T) return;
+        if (mc.topk == 10) k_pf_hc_prep<10><<<T, CHK_WG, 0, st>>>(hyper, norm, H, hc, eps, inv, hi, lo, xs, part, pzs, nsplit, pinj, mc);
+        else k_pf_hc_prep<0><<<T, CHK_WG, 0, st>>>(hyper, norm, H, hc, eps, inv, hi, lo, xs, part, pzs, nsplit, pinj, mc);
+        return;
+    }
+    if (T) k_pf_hc_prep<-1><<<T, CHK_WG, 0, st>>>(hyper, norm, H, hc, eps, inv, hi, lo, xs, part, pzs, nsplit, pinj, mc);
 }
 
 // The launch form of a GEMM: 32-bit element offsets of the dense matrices
@@ -1849,23 +1918,27 @@ void launch_pf_router(const uint16_t* router, const uint4* bhi, const uint4* bmi
 
 void launch_pf_route(const float* logits, uint32_t T, uint32_t E, uint32_t topk, int norm_topk, uint32_t* ids,
                      float* wts, uint32_t* last_ids, float* last_wts, const uint16_t* shared_gate, const uint4* bhi,
-                     const uint4* bmid, const uint4* blo, float* sg, uint32_t H, hipStream_t st) {
+                     const uint4* bmid, const uint4* blo, float* sg, uint32_t H, uint32_t* gcnt, uint32_t* list,
+                     uint32_t* pos, uint32_t cap, bool shared, hipStream_t st) {
     if (H % 8 || (uintptr_t)shared_gate % 16) throw std::runtime_error("shared gate needs 16-byte rows");
+    if (E > 512 || topk > 64 || topk >= E) throw std::runtime_error("prefill routing: at most 512 experts");
+    if (T > cap || (uint64_t)T * (topk + 1) >= (1u << 22)) throw std::runtime_error("prefill grouping: too many entries");
     if (T)
         k_pf_route<<<(T + 3) / 4, CHK_WG, 0, st>>>(logits, T, E, topk, norm_topk, ids, wts, last_ids, last_wts,
-                                                   shared_gate, bhi, bmid, blo, sg, H);
+                                                   shared_gate, bhi, bmid, blo, sg, H, gcnt, list, pos, cap,
+                                                   shared ? 1u : 0u);
 }
 
-void launch_pf_group(const uint32_t* ids, uint32_t T, uint32_t topk, uint32_t E, uint32_t cap, uint32_t* list,
-                     uint32_t* count, uint32_t* tiles, uint32_t* ntiles, uint2* tinfo, uint32_t* goff, uint32_t* pos,
-                     uint64_t* act, uint32_t layer, uint32_t tr, bool shared, hipStream_t st) {
+void launch_pf_group(uint32_t* gcnt, uint32_t T, uint32_t topk, uint32_t E, uint32_t cap, uint32_t* count,
+                     uint32_t* tiles, uint32_t* ntiles, uint2* tinfo, uint32_t* goff, uint64_t* act, uint32_t layer,
+                     uint32_t tr, bool shared, hipStream_t st) {
     if (E + 1 > PG_WG) throw std::runtime_error("prefill grouping supports at most 1023 experts");
-    if ((uint64_t)T * (topk + 1) >= (1u << 22)) throw std::runtime_error("prefill grouping: too many entries");
+    if (T > cap || (uint64_t)T * (topk + 1) >= (1u << 22)) throw std::runtime_error("prefill grouping: too many entries");
     if (tr != 48 && tr != 64) throw std::runtime_error("prefill grouping: tiles of 48 or 64 rows");
     if (pf_tile_bound(T, topk, E, tr) >= 0x1000u || pf_tile_bound(T, topk, E, 64) >= 0x1000u)
         throw std::runtime_error("prefill grouping: too many tiles");
-    k_pf_group<<<1, PG_WG, 0, st>>>(ids, T, topk, E, cap, list, count, tiles, ntiles, tinfo, goff, pos,
-                                    reinterpret_cast<unsigned long long*>(act), layer, tr, shared ? 1u : 0u);
+    k_pf_group<<<1, PG_WG, 0, st>>>(gcnt, T, E, cap, count, tiles, ntiles, tinfo, goff,
+                                    reinterpret_cast<unsigned long long*>(act), layer, tr, topk, shared ? 1u : 0u);
 }
 
 // Tiles of a grouped GEMM: every group's rows in tr-row tiles, one more
