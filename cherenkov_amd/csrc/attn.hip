@@ -12,88 +12,129 @@
 
 namespace chk {
 
-// rms_norm then rope_partial at position `pos` of one vector held one
-// element per thread (d < n live), as cpu.rs:575-587 and 676-681 apply them
-// to q/k heads and to the indexer's query heads.
-CHK_DEV float norm_rope(float x, bool live, uint32_t d, uint32_t n, const uint16_t* w, float eps, uint32_t rot,
-                        float theta, uint32_t pos, float* red, float* sx) {
-    // the norm weight (raw bf16 in a 32-bit register) and the rotation
-    // are fetched and computed ahead of the reduction, not after it
-    const uint32_t wv = w[min(d, n - 1)];
-    const uint32_t half = rot / 2, j = d < half ? d : d - half;
-    float sn = 0.0f, cs = 1.0f;
-    if (d < rot) {
-        const float inv_freq = powf(theta, -(2.0f * (float)j) / (float)rot);
-        const float ang = (float)pos * inv_freq;
-        sn = sinf(ang);
-        cs = cosf(ang);
+// rms_norm then rope_partial at position `pos` of one vector of n <= 256
+// dims held by a wave, lane l holding dims l + 64 i in x[i] (0 past n), as
+// cpu.rs:575-587 and 676-681 apply them to q/k heads and to the indexer's
+// query heads.  The sum of squares is summed per 64-dim slab, slabs in
+// order; a rotated dim's partner (d -+ rot / 2) comes by a lane permute.
+CHK_DEV void wave_norm_rope(float (&x)[4], uint32_t n, const uint16_t* __restrict__ w, float eps, uint32_t rot,
+                            float theta, uint32_t pos, uint32_t lane) {
+    uint32_t wv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wv[i] = w[min(64 * i + lane, n - 1)];
+    // the rotations, computed ahead of the reduction
+    const uint32_t half = rot / 2;
+    float sn[4], cs[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t d = 64 * i + lane, j = d < half ? d : d - half;
+        sn[i] = 0.0f;
+        cs[i] = 1.0f;
+        if (64 * i < rot && d < rot) {
+            const float inv_freq = powf(theta, -(2.0f * (float)j) / (float)rot);
+            const float ang = (float)pos * inv_freq;
+            sn[i] = sinf(ang);
+            cs[i] = cosf(ang);
+        }
     }
-    const float ss = block_sum(live ? x * x : 0.0f, red);
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ss += wave_sum(64 * i + lane < n ? x[i] * x[i] : 0.0f);
     const float inv = 1.0f / sqrtf(ss / (float)n + eps);
-    if (live) {
-        x = x * inv * __uint_as_float(wv << 16);
-        sx[d] = x;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        if (64 * i + lane < n) x[i] = x[i] * inv * __uint_as_float(wv[i] << 16);
+    float y[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        y[i] = x[i];
+        if (64 * i >= rot) continue;  // uniform
+        const uint32_t d = 64 * i + lane, p = d < half ? d + half : d - half;
+        const int lp = (int)(p & 63u);
+        // every lane takes part in the permutes; only d < rot uses them
+        float xp = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            if (64 * q >= rot) break;  // uniform: partners lie below rot
+            const float v = __shfl(x[q], lp, 64);
+            if ((p >> 6) == (uint32_t)q) xp = v;
+        }
+        if (d < rot) {
+            const float av = d < half ? x[i] : xp, bv = d < half ? xp : x[i];
+            y[i] = d < half ? av * cs[i] - bv * sn[i] : bv * cs[i] + av * sn[i];
+        }
     }
-    __syncthreads();
-    if (d < rot) {
-        const float av = sx[j], bv = sx[j + half];
-        x = d < half ? av * cs - bv * sn : bv * cs + av * sn;
-    }
-    return x;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = y[i];
 }
 
 // Per head: q RMSNorm + partial RoPE -> q_ready; k RMSNorm + RoPE -> q8 K
 // row; v -> q8 V row; the raw indexer key -> index cache; with QSA the
-// indexer's query heads, normed and roped -> iq_ready.  One CHK_WG-thread
-// workgroup per (row, item), thread d < hd owning dim d: items [0, nh) q
-// heads, [nh, nh + nkv) k heads, [nh + nkv, nh + 2 nkv) v heads,
-// nh + 2 nkv the index key, then inh index query heads.
+// indexer's query heads, normed and roped -> iq_ready.  One wave per (row,
+// item), four items per workgroup: items [0, nh) q heads, [nh, nh + nkv) k
+// heads, [nh + nkv, nh + 2 nkv) v heads, nh + 2 nkv the index key, then inh
+// index query heads.  Lane l holds dims l + 64 i, so a q8 block of 32 dims
+// is a half-wave.
 __global__ void __launch_bounds__(256) k_attn_prep(AttnArgs a) {
-    __shared__ float red[8];
-    __shared__ float sx[512];
-    const uint32_t b = blockIdx.y, item = blockIdx.x, d = threadIdx.x, hd = a.hd;
-    const bool live = d < hd;
+    const uint32_t b = blockIdx.y, lane = threadIdx.x & 63, hd = a.hd;
+    const uint32_t item = blockIdx.x * (CHK_WG >> 6) + wave_id();
+    const uint32_t nkey = a.nh + 2 * a.nkv;
+    if (item > nkey + (a.qsa ? a.inh : 0)) return;
     const uint32_t pos = a.pos[b];
     const KvDev& kv = a.kv[a.one_kv ? 0 : b];
-    if (item == a.nh + 2 * a.nkv) {
-        if (d < a.ihd) kv.index_k[(size_t)pos * a.ihd + d] = a.idx_raw[(size_t)b * (a.inh + 1) * a.ihd + a.inh * a.ihd + d];
+    const size_t irow = (size_t)b * (a.inh + 1) * a.ihd;
+    float x[4];
+    if (item == nkey) {
+        for (uint32_t d = lane; d < a.ihd; d += 64) kv.index_k[(size_t)pos * a.ihd + d] = a.idx_raw[irow + a.inh * a.ihd + d];
         return;
     }
-    if (item > a.nh + 2 * a.nkv) {
+    if (item > nkey) {
         // select_tokens' query heads (cpu.rs:676-681): index_q_norm, rope at pos
-        const uint32_t h = item - (a.nh + 2 * a.nkv + 1);
-        const bool il = d < a.ihd;
-        const float x0 = il ? a.idx_raw[(size_t)b * (a.inh + 1) * a.ihd + h * a.ihd + d] : 0.0f;
-        const float x = norm_rope(x0, il, d, a.ihd, a.iq_norm, a.eps, a.rot, a.theta, pos, red, sx);
-        if (il) a.iq_ready[((size_t)b * a.inh + h) * a.ihd + d] = x;
+        const uint32_t h = item - (nkey + 1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t d = 64 * i + lane;
+            x[i] = d < a.ihd ? a.idx_raw[irow + h * a.ihd + d] : 0.0f;
+        }
+        wave_norm_rope(x, a.ihd, a.iq_norm, a.eps, a.rot, a.theta, pos, lane);
+        float* dst = a.iq_ready + ((size_t)b * a.inh + h) * a.ihd;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (64 * i + lane < a.ihd) dst[64 * i + lane] = x[i];
         return;
     }
     const bool is_q = item < a.nh, is_k = !is_q && item < a.nh + a.nkv;
-    float x = 0.0f;
-    if (live) {
-        if (is_q) x = a.q_raw[(size_t)b * a.nh * 2 * hd + item * 2 * hd + d];
-        else if (is_k) x = a.k_raw[(size_t)b * a.nkv * hd + (item - a.nh) * hd + d];
-        else x = a.v_raw[(size_t)b * a.nkv * hd + (item - a.nh - a.nkv) * hd + d];
-    }
+    const float* src = is_q   ? a.q_raw + (size_t)b * a.nh * 2 * hd + item * 2 * hd
+                       : is_k ? a.k_raw + (size_t)b * a.nkv * hd + (item - a.nh) * hd
+                              : a.v_raw + (size_t)b * a.nkv * hd + (item - a.nh - a.nkv) * hd;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = 64 * i + lane < hd ? src[64 * i + lane] : 0.0f;
     if (is_q || is_k)
         // nn::rms_norm (nn.rs:6-15) then rope_partial (cpu.rs:1051-1063)
-        x = norm_rope(x, live, d, hd, is_q ? a.q_norm : a.k_norm, a.eps, a.rot, a.theta, pos, red, sx);
+        wave_norm_rope(x, hd, is_q ? a.q_norm : a.k_norm, a.eps, a.rot, a.theta, pos, lane);
     if (is_q) {
-        if (live) a.q_ready[((size_t)b * a.nh + item) * hd + d] = x;
+        float* dst = a.q_ready + ((size_t)b * a.nh + item) * hd;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (64 * i + lane < hd) dst[64 * i + lane] = x[i];
         return;
     }
-    // q8: 32-lane blocks are half-waves (dims past hd hold 0 and write nothing)
-    float amax = group_max<32>(fabsf(x));
-    float dq = amax / 127.0f;
-    float qv = dq > 0.0f ? rintf(x / dq) : 0.0f;
-    qv = fminf(fmaxf(qv, -127.0f), 127.0f);
-    if (!live) return;
     const uint32_t kvh = is_k ? item - a.nh : item - a.nh - a.nkv;
     const uint32_t kv_row = a.nkv * hd;
     int8_t* plane = is_k ? kv.k : kv.v;
     uint16_t* sc = is_k ? kv.ks : kv.vs;
-    plane[(size_t)pos * kv_row + kvh * hd + d] = (int8_t)qv;
-    if ((d & 31) == 0) sc[(size_t)pos * (kv_row / 32) + (kvh * hd + d) / 32] = __half_as_ushort(__float2half_rn(dq));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if (64 * i >= hd) break;  // uniform; hd is a multiple of 64
+        // q8 over the half-wave's 32 dims
+        const float amax = group_max<32>(fabsf(x[i]));
+        const float dq = amax / 127.0f;
+        float qv = dq > 0.0f ? rintf(x[i] / dq) : 0.0f;
+        qv = fminf(fmaxf(qv, -127.0f), 127.0f);
+        const uint32_t d = 64 * i + lane;
+        plane[(size_t)pos * kv_row + kvh * hd + d] = (int8_t)qv;
+        if ((d & 31) == 0) sc[(size_t)pos * (kv_row / 32) + (kvh * hd + d) / 32] = __half_as_ushort(__float2half_rn(dq));
+    }
 }
 
 
@@ -599,7 +640,10 @@ void launch_attn_core(const AttnArgs& a, int nb, hipStream_t st) {
 
 void launch_attn_prep(const AttnArgs& a, int nb, hipStream_t st) {
     if (nb > MAX_NB && !a.one_kv) throw std::runtime_error("rows beyond the step batch must share one sequence");
-    k_attn_prep<<<dim3(a.nh + 2 * a.nkv + 1 + (a.qsa ? a.inh : 0), nb), CHK_WG, 0, st>>>(a);
+    if (a.hd > 256 || a.hd % 64 || a.ihd > 256 || a.rot > a.hd || (a.qsa && a.rot > a.ihd))
+        throw std::runtime_error("attention heads of at most 256 dims (a multiple of 64), rotation within the head");
+    const uint32_t items = a.nh + 2 * a.nkv + 1 + (a.qsa ? a.inh : 0);
+    k_attn_prep<<<dim3((items + 3) / 4, nb), CHK_WG, 0, st>>>(a);
 }
 
 // Block keys, scores and selection; a no-op for rows still within the budget
