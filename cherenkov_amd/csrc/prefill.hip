@@ -113,6 +113,14 @@ __global__ void __launch_bounds__(256) k_pf_prep(PfPrepArgs a) {
     }
 }
 
+// The mix epilogues' sigmoid (T hc H of them per hyper-connection read):
+// e^-v as 2^(-v log2 e) on the transcendental unit and one hardware
+// reciprocal, a few instructions against ~25 for 1 / (1 + expf(-v)).
+// Absolute error below 3e-7 for |v| <= 16, exact limits 0 and 1 beyond.
+CHK_DEV float sigmoid_mix(float v) {
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(v * -1.44269504088896341f));
+}
+
 // ----------------------------------------------- hyper-connection norm
 // normed[t][g H + k] = hyper[t][g H + k] * inv[t][g] * w[g H + k] with
 // inv = 1/sqrt(mean_k(hyper[t][g H + k]^2) + eps) per stream g (the
@@ -820,7 +828,7 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs ka) {
                     if ((uint32_t)j >= a.hc) continue;
                     const float hj[4] = {hv[j].x, hv[j].y, hv[j].z, hv[j].w};
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) sum[r] += sigmoidf_(acc[0][i][j][r]) * (hj[r] * iv[j] * nw[j][r]);
+                    for (int r = 0; r < 4; ++r) sum[r] += sigmoid_mix(acc[0][i][j][r]) * (hj[r] * iv[j] * nw[j][r]);
                 }
                 const float ih = (float)a.hc;
                 *reinterpret_cast<float4*>(a.out + (size_t)m * a.H + o4) =
@@ -933,6 +941,31 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs ka) {
             for (int sgi = 1; sgi < 4; ++sgi)
                 if ((uint32_t)sgi < a.nseg && gcol >= a.seg[sgi].n0) sg = a.seg[sgi];
         }
+        // the mix's stream values, norm weights and RMS factors for both
+        // halves, requested before the first half is staged (their one
+        // round trip overlaps the staging rather than following it)
+        float4 mhv[2][4][2];
+        uint4 mnq[4];
+        float miv[2][4];
+        if (EPI == PE_HC_UP && a.phi) {
+            const uint32_t o = bx * 64 + 8 * ((uint32_t)tid & 7);
+    #pragma unroll
+            for (int j = 0; j < 4; ++j)
+                mnq[j] = (uint32_t)j < a.hc ? *reinterpret_cast<const uint4*>(a.norm + (size_t)j * a.H + o)
+                                            : make_uint4(0u, 0u, 0u, 0u);
+    #pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t mc = min(m0 + 32 * h + ((uint32_t)tid >> 3), M - 1);
+                const float* hy = a.hyper + (size_t)mc * a.hc * a.H + o;
+    #pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const bool on = (uint32_t)j < a.hc;
+                    mhv[h][j][0] = on ? *reinterpret_cast<const float4*>(hy + (size_t)j * a.H) : make_float4(0.f, 0.f, 0.f, 0.f);
+                    mhv[h][j][1] = on ? *reinterpret_cast<const float4*>(hy + (size_t)j * a.H + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+                    miv[h][j] = on ? a.inv[(size_t)mc * a.hc + j] : 0.0f;
+                }
+            }
+        }
     #pragma unroll
         for (int h = 0; h < 2; ++h) {
             __syncthreads();
@@ -957,18 +990,13 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs ka) {
                 // aligned lane group)
                 const uint32_t rr = (uint32_t)tid >> 3, b8 = (uint32_t)tid & 7, ol = 8 * b8;
                 const uint32_t o = bx * 64 + ol, sc0 = (ol >> 4) * 64 + (ol & 15);
-                const uint32_t m = mh + rr, mc = min(m, M - 1);
-                const float* hy = a.hyper + (size_t)mc * a.hc * a.H + o;
-                float4 hv[4][2], uv[4][2];
-                uint4 nq[4];
-                float iv[4];
+                const uint32_t m = mh + rr;
+                float4 uv[4][2];
+                const auto& hv = mhv[h];
+                const auto& nq = mnq;
+                const auto& iv = miv[h];
     #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const bool on = (uint32_t)j < a.hc;
-                    hv[j][0] = on ? *reinterpret_cast<const float4*>(hy + (size_t)j * a.H) : make_float4(0.f, 0.f, 0.f, 0.f);
-                    hv[j][1] = on ? *reinterpret_cast<const float4*>(hy + (size_t)j * a.H + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
-                    nq[j] = on ? *reinterpret_cast<const uint4*>(a.norm + (size_t)j * a.H + o) : make_uint4(0u, 0u, 0u, 0u);
-                    iv[j] = on ? a.inv[(size_t)mc * a.hc + j] : 0.0f;
                     uv[j][0] = *reinterpret_cast<const float4*>(&sO[rr * OS + sc0 + j * 16]);
                     uv[j][1] = *reinterpret_cast<const float4*>(&sO[rr * OS + sc0 + j * 16 + 4]);
                 }
@@ -984,12 +1012,19 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs ka) {
     #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         const float we = __uint_as_float(e & 1 ? nw[e >> 1] & 0xffff0000u : nw[e >> 1] << 16);
-                        v[e] += sigmoidf_(uj[e]) * (hj[e] * iv[j] * we);
+                        v[e] += sigmoid_mix(uj[e]) * (hj[e] * iv[j] * we);
                     }
                 }
+                // / hc: a product by the exact reciprocal for a power of two
                 const float ih = (float)a.hc;
+                if ((a.hc & (a.hc - 1)) == 0) {
+                    const float rh = 1.0f / ih;
     #pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = v[e] / ih;
+                    for (int e = 0; e < 8; ++e) v[e] = v[e] * rh;
+                } else {
+    #pragma unroll
+                    for (int e = 0; e < 8; ++e) v[e] = v[e] / ih;
+                }
                 float gs = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
                 gs += __shfl_xor(gs, 1, 64);
                 gs += __shfl_xor(gs, 2, 64);
@@ -1059,7 +1094,7 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs ka) {
                         const float hj[4] = {hv[j].x, hv[j].y, hv[j].z, hv[j].w};
                         const float uj[4] = {uv[j].x, uv[j].y, uv[j].z, uv[j].w};
     #pragma unroll
-                        for (int e = 0; e < 4; ++e) sum[e] += sigmoidf_(uj[e]) * (hj[e] * iv[j] * nw[j][e]);
+                        for (int e = 0; e < 4; ++e) sum[e] += sigmoid_mix(uj[e]) * (hj[e] * iv[j] * nw[j][e]);
                     }
                     const float ih = (float)a.hc;
                     *reinterpret_cast<float4*>(a.out + (size_t)m * a.H + o) =
