@@ -113,13 +113,15 @@ __global__ void __launch_bounds__(256) k_pf_prep(PfPrepArgs a) {
     }
 }
 
-// The mix epilogues' sigmoid (T hc H of them per hyper-connection read):
-// e^-v as 2^(-v log2 e) on the transcendental unit and one hardware
-// reciprocal, a few instructions against ~25 for 1 / (1 + expf(-v)).
-// Absolute error below 3e-7 for |v| <= 16, exact limits 0 and 1 beyond.
-CHK_DEV float sigmoid_mix(float v) {
+// The GEMM epilogues' sigmoid and SiLU (T hc H sigmoids per
+// hyper-connection read, T (k+1) I SiLUs per expert gate/up): e^-v as
+// 2^(-v log2 e) on the transcendental unit and one hardware reciprocal, a
+// few instructions against ~25 for 1 / (1 + expf(-v)).  Absolute error of
+// the sigmoid below 3e-7 for |v| <= 16, exact limits 0 and 1 beyond.
+CHK_DEV float sigmoid_hw(float v) {
     return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(v * -1.44269504088896341f));
 }
+CHK_DEV float silu_hw(float v) { return v * sigmoid_hw(v); }
 
 // ----------------------------------------------- hyper-connection norm
 // normed[t][g H + k] = hyper[t][g H + k] * inv[t][g] * w[g H + k] with
@@ -828,7 +830,7 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs ka) {
                     if ((uint32_t)j >= a.hc) continue;
                     const float hj[4] = {hv[j].x, hv[j].y, hv[j].z, hv[j].w};
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) sum[r] += sigmoid_mix(acc[0][i][j][r]) * (hj[r] * iv[j] * nw[j][r]);
+                    for (int r = 0; r < 4; ++r) sum[r] += sigmoid_hw(acc[0][i][j][r]) * (hj[r] * iv[j] * nw[j][r]);
                 }
                 const float ih = (float)a.hc;
                 *reinterpret_cast<float4*>(a.out + (size_t)m * a.H + o4) =
@@ -852,7 +854,7 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs ka) {
                 for (int j = 0; j < NJ; ++j) {
                     float u[4], pv[4], v[8];
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) u[r] = siluf_(acc[0][i][j][r]) * acc[NMAT - 1][i][j][r];
+                    for (int r = 0; r < 4; ++r) u[r] = silu_hw(acc[0][i][j][r]) * acc[NMAT - 1][i][j][r];
 #pragma unroll
                     for (int r = 0; r < 4; ++r) pv[r] = __shfl_xor(u[r], 16, 64);
 #pragma unroll
@@ -911,7 +913,7 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs ka) {
                     float u[4];
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        u[r] = EPI == PE_SILU_MUL ? siluf_(acc[0][i][j][r]) * acc[NMAT - 1][i][j][r] : acc[0][i][j][r];
+                        u[r] = EPI == PE_SILU_MUL ? silu_hw(acc[0][i][j][r]) * acc[NMAT - 1][i][j][r] : acc[0][i][j][r];
                     float* dst = sj[j].y + (size_t)blockIdx.z * a.zstride + (size_t)yrow[i] * sj[j].ldy + (n4[j] - sj[j].n0);
                     if (a.vec4) {
                         if (n4[j] < a.N) *reinterpret_cast<float4*>(dst) = make_float4(u[0], u[1], u[2], u[3]);
@@ -976,7 +978,7 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs ka) {
                 for (int j = 0; j < NJ; ++j)
     #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const float v = EPI == PE_SILU_MUL ? siluf_(acc[0][i][j][r]) * acc[NMAT - 1][i][j][r] : acc[0][i][j][r];
+                        const float v = EPI == PE_SILU_MUL ? silu_hw(acc[0][i][j][r]) * acc[NMAT - 1][i][j][r] : acc[0][i][j][r];
                         sO[(ii * 16 + kq * 4 + r) * OS + wn * (64 / NMAT) + j * 16 + col] = v;
                     }
             }
@@ -1012,7 +1014,7 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs ka) {
     #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         const float we = __uint_as_float(e & 1 ? nw[e >> 1] & 0xffff0000u : nw[e >> 1] << 16);
-                        v[e] += sigmoid_mix(uj[e]) * (hj[e] * iv[j] * we);
+                        v[e] += sigmoid_hw(uj[e]) * (hj[e] * iv[j] * we);
                     }
                 }
                 // / hc: a product by the exact reciprocal for a power of two
@@ -1094,7 +1096,7 @@ __global__ void __launch_bounds__(PF_WG, 2) k_pf_gemm(PfGemmArgs ka) {
                         const float hj[4] = {hv[j].x, hv[j].y, hv[j].z, hv[j].w};
                         const float uj[4] = {uv[j].x, uv[j].y, uv[j].z, uv[j].w};
     #pragma unroll
-                        for (int e = 0; e < 4; ++e) sum[e] += sigmoid_mix(uj[e]) * (hj[e] * iv[j] * nw[j][e]);
+                        for (int e = 0; e < 4; ++e) sum[e] += sigmoid_hw(uj[e]) * (hj[e] * iv[j] * nw[j][e]);
                     }
                     const float ih = (float)a.hc;
                     *reinterpret_cast<float4*>(a.out + (size_t)m * a.H + o) =
