@@ -12,6 +12,89 @@
 
 namespace chk {
 
+// rms_norm then rope_partial at position `pos` of one vector held one
+// element per thread (d < n live), as cpu.rs:575-587 and 676-681 apply them
+// to q/k heads and to the indexer's query heads.
+CHK_DEV float norm_rope(float x, bool live, uint32_t d, uint32_t n, const uint16_t* w, float eps, uint32_t rot,
+                        float theta, uint32_t pos, float* red, float* sx) {
+    // the norm weight (raw bf16 in a 32-bit register) and the rotation
+    // are fetched and computed ahead of the reduction, not after it
+    const uint32_t wv = w[min(d, n - 1)];
+    const uint32_t half = rot / 2, j = d < half ? d : d - half;
+    float sn = 0.0f, cs = 1.0f;
+    if (d < rot) {
+        const float inv_freq = powf(theta, -(2.0f * (float)j) / (float)rot);
+        const float ang = (float)pos * inv_freq;
+        sn = sinf(ang);
+        cs = cosf(ang);
+    }
+    const float ss = block_sum(live ? x * x : 0.0f, red);
+    const float inv = 1.0f / sqrtf(ss / (float)n + eps);
+    if (live) {
+        x = x * inv * __uint_as_float(wv << 16);
+        sx[d] = x;
+    }
+    __syncthreads();
+    if (d < rot) {
+        const float av = sx[j], bv = sx[j + half];
+        x = d < half ? av * cs - bv * sn : bv * cs + av * sn;
+    }
+    return x;
+}
+
+// The step batch's form of k_attn_prep below (the same items and the same
+// arithmetic, sums in the same order): one CHK_WG-thread
+// workgroup per (row, item), thread d < hd owning dim d, which gives a
+// decode step's single row the shortest path (a wave per 64 dims).
+__global__ void __launch_bounds__(256) k_attn_prep_wg(AttnArgs a) {
+    __shared__ float red[8];
+    __shared__ float sx[512];
+    const uint32_t b = blockIdx.y, item = blockIdx.x, d = threadIdx.x, hd = a.hd;
+    const bool live = d < hd;
+    const uint32_t pos = a.pos[b];
+    const KvDev& kv = a.kv[a.one_kv ? 0 : b];
+    if (item == a.nh + 2 * a.nkv) {
+        if (d < a.ihd) kv.index_k[(size_t)pos * a.ihd + d] = a.idx_raw[(size_t)b * (a.inh + 1) * a.ihd + a.inh * a.ihd + d];
+        return;
+    }
+    if (item > a.nh + 2 * a.nkv) {
+        // select_tokens' query heads (cpu.rs:676-681): index_q_norm, rope at pos
+        const uint32_t h = item - (a.nh + 2 * a.nkv + 1);
+        const bool il = d < a.ihd;
+        const float x0 = il ? a.idx_raw[(size_t)b * (a.inh + 1) * a.ihd + h * a.ihd + d] : 0.0f;
+        const float x = norm_rope(x0, il, d, a.ihd, a.iq_norm, a.eps, a.rot, a.theta, pos, red, sx);
+        if (il) a.iq_ready[((size_t)b * a.inh + h) * a.ihd + d] = x;
+        return;
+    }
+    const bool is_q = item < a.nh, is_k = !is_q && item < a.nh + a.nkv;
+    float x = 0.0f;
+    if (live) {
+        if (is_q) x = a.q_raw[(size_t)b * a.nh * 2 * hd + item * 2 * hd + d];
+        else if (is_k) x = a.k_raw[(size_t)b * a.nkv * hd + (item - a.nh) * hd + d];
+        else x = a.v_raw[(size_t)b * a.nkv * hd + (item - a.nh - a.nkv) * hd + d];
+    }
+    if (is_q || is_k)
+        // nn::rms_norm (nn.rs:6-15) then rope_partial (cpu.rs:1051-1063)
+        x = norm_rope(x, live, d, hd, is_q ? a.q_norm : a.k_norm, a.eps, a.rot, a.theta, pos, red, sx);
+    if (is_q) {
+        if (live) a.q_ready[((size_t)b * a.nh + item) * hd + d] = x;
+        return;
+    }
+    // q8: 32-lane blocks are half-waves (dims past hd hold 0 and write nothing)
+    float amax = group_max<32>(fabsf(x));
+    float dq = amax / 127.0f;
+    float qv = dq > 0.0f ? rintf(x / dq) : 0.0f;
+    qv = fminf(fmaxf(qv, -127.0f), 127.0f);
+    if (!live) return;
+    const uint32_t kvh = is_k ? item - a.nh : item - a.nh - a.nkv;
+    const uint32_t kv_row = a.nkv * hd;
+    int8_t* plane = is_k ? kv.k : kv.v;
+    uint16_t* sc = is_k ? kv.ks : kv.vs;
+    plane[(size_t)pos * kv_row + kvh * hd + d] = (int8_t)qv;
+    if ((d & 31) == 0) sc[(size_t)pos * (kv_row / 32) + (kvh * hd + d) / 32] = __half_as_ushort(__float2half_rn(dq));
+}
+
+
 // rms_norm then rope_partial at position `pos` of one vector of n <= 256
 // dims held by a wave, lane l holding dims l + 64 i in x[i] (0 past n), as
 // cpu.rs:575-587 and 676-681 apply them to q/k heads and to the indexer's
@@ -643,7 +726,10 @@ void launch_attn_prep(const AttnArgs& a, int nb, hipStream_t st) {
     if (a.hd > 256 || a.hd % 64 || a.ihd > 256 || a.rot > a.hd || (a.qsa && a.rot > a.ihd))
         throw std::runtime_error("attention heads of at most 256 dims (a multiple of 64), rotation within the head");
     const uint32_t items = a.nh + 2 * a.nkv + 1 + (a.qsa ? a.inh : 0);
-    k_attn_prep<<<dim3((items + 3) / 4, nb), CHK_WG, 0, st>>>(a);
+    // a step batch: a workgroup per item (latency); prefill rows: a wave per
+    // item (four per workgroup)
+    if (nb <= MAX_NB) k_attn_prep_wg<<<dim3(items, nb), CHK_WG, 0, st>>>(a);
+    else k_attn_prep<<<dim3((items + 3) / 4, nb), CHK_WG, 0, st>>>(a);
 }
 
 // Block keys, scores and selection; a no-op for rows still within the budget
