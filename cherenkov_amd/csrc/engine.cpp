@@ -1739,7 +1739,8 @@ uint64_t ChkEngine::prefill_scratch_bytes(uint64_t C, bool all_logits) const {
     const uint64_t dn = C * (2ull * D.conv_dim + 2ull * D.v_dim + (2ull * pf_ab_split(D.H) + 2) * D.nv);
     const uint64_t at = C * (2ull * D.nh * D.hd + 2ull * D.kv_row + D.idx_out + 2ull * D.nh * D.hd);
     b += std::max(dn, at) * f;
-    b += C * (D.E + 1 + 2ull * D.topk) * f + (D.E + 1ull) * C * 4 + (PF_GCNT_STRIDE + 1ull) * (D.E + 1) * 4;
+    b += C * (PF_ROUTER_CHUNKS * D.E + 1 + 2ull * D.topk) * f + (D.E + 1ull) * C * 4 +
+         (PF_GCNT_STRIDE + 1ull) * (D.E + 1) * 4;
     b += (uint64_t)(pf_tile_bound((uint32_t)C, D.topk, D.E, 48) + pf_tile_bound((uint32_t)C, D.topk, D.E, 64)) * 12 +
          C * slots * (D.I + D.H) * f + C * slots * 4 + (D.E + 1) * 4;
     if (D.SI != D.I) b += C * D.SI * f;
@@ -1859,7 +1860,7 @@ void ChkEngine::pf_alloc() {
     pf.idx_raw = q; q += C * D.idx_out;
     pf.q_ready = q; q += C * D.nh * D.hd;
     pf.attn_out = q;
-    pf.logits = pfalloc<float>(C * D.E);
+    pf.logits = pfalloc<float>(C * D.E * PF_ROUTER_CHUNKS);  // (K-chunk partials)
     pf.sg = pfalloc<float>(C);
     pf.wts = pfalloc<float>(C * D.topk);
     pf.ids = pfalloc<uint32_t>(C * D.topk);

@@ -186,13 +186,23 @@ CHK_DEV void rank_swap(float& va, uint32_t& ia, float& vb, uint32_t& ib) {
     ia = ti;
 }
 
+// NZ > 1: the logits arrive as NZ K-chunk partials zs floats apart,
+// summed here in chunk order.
+template <int NZ = 1>
 CHK_DEV void route_row(const float* __restrict__ l, uint32_t E, uint32_t need, int lane, float* probs,
-                       uint32_t& my_id, float& my_p) {
+                       uint32_t& my_id, float& my_p, size_t zs = 0) {
     constexpr int PER = 8;
     const uint32_t base = (uint32_t)lane * PER;
     const bool live = base < E;
     const float4* lp = reinterpret_cast<const float4*>(l + (live ? base : 0));
-    const float4 l0 = lp[0], l1 = lp[1];
+    float4 l0 = lp[0], l1 = lp[1];
+#pragma unroll
+    for (int z = 1; z < NZ; ++z) {
+        const float4* q = reinterpret_cast<const float4*>(l + z * zs + (live ? base : 0));
+        const float4 q0 = q[0], q1 = q[1];
+        l0 = make_float4(l0.x + q0.x, l0.y + q0.y, l0.z + q0.z, l0.w + q0.w);
+        l1 = make_float4(l1.x + q1.x, l1.y + q1.y, l1.z + q1.z, l1.w + q1.w);
+    }
     float v[PER] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
     uint32_t ix[PER];
     float mx = -INFINITY;
@@ -477,6 +487,13 @@ void launch_pf_gemm(const Q4Mat& w, const uint4* xhi, const uint4* xlo, const fl
 // (hi, lo, xs) with d as the scratch of the unfused form
 void launch_pf_hc_down_finish(const float* part, uint32_t nsplit, uint32_t T, uint32_t lowrank, uint32_t hc,
                               float alpha, float* d, float* inj, uint4* hi, uint4* lo, float* xs, hipStream_t st);
+// The prefill router's plan: column blocks of 64 PF_ROUTER_CT experts and
+// PF_ROUTER_CHUNKS K chunks where the shape allows (the logits then leave
+// as that many partials, T E floats apart, summed by the routing pass),
+// else 64-expert blocks over the whole K (grid z = 1).
+constexpr uint32_t PF_ROUTER_CT = 2;
+constexpr uint32_t PF_ROUTER_CHUNKS = 2;
+dim3 pf_router_plan(uint32_t T, uint32_t E, uint32_t H);
 void launch_pf_router(const uint16_t* router, const uint4* bhi, const uint4* bmid, const uint4* blo, float* logits,
                       uint32_t T, uint32_t E, uint32_t H, hipStream_t st);
 void launch_pf_route(const float* logits, uint32_t T, uint32_t E, uint32_t topk, int norm_topk, uint32_t* ids,

@@ -1257,15 +1257,25 @@ __global__ void __launch_bounds__(256) k_pf_hc_down_finish_q(const float* __rest
 // the next block's pieces and weight words load while this one computes).
 constexpr int RT_AROW = 9;  // uint4 per staged row (8 + 1 pad)
 
+template <int CT>
 __global__ void __launch_bounds__(256) k_pf_router(const uint16_t* __restrict__ router,
                                                    const uint4* __restrict__ bhi, const uint4* __restrict__ bmid,
                                                    const uint4* __restrict__ blo, float* __restrict__ logits,
                                                    uint32_t T, uint32_t E, uint32_t H) {
     __shared__ __align__(16) u32x4 sA[2][3][64 * RT_AROW];
     const int tid = threadIdx.x, lane = tid & 63, col = lane & 15, kq = lane >> 4;
-    const uint32_t m0 = blockIdx.y * 64, KB = H >> 3, NB = H >> 6;
-    const uint32_t nn = blockIdx.x * 64 + wave_id() * 16 + col;
-    const u32x4* bp = reinterpret_cast<const u32x4*>(router + (size_t)min(nn, E - 1) * H);
+    const uint32_t m0 = blockIdx.y * 64, KB = H >> 3;
+    // K chunk blockIdx.z: 64-wide blocks b0 .. NB - 1, partials at logits + z T E
+    const uint32_t NBc = (H >> 6) / gridDim.z, b0 = blockIdx.z * NBc, NB = b0 + NBc;
+    logits += (size_t)blockIdx.z * T * E;
+    // wave w: CT 16-expert column tiles
+    uint32_t nn[CT];
+    const u32x4* bp[CT];
+#pragma unroll
+    for (int c = 0; c < CT; ++c) {
+        nn[c] = (blockIdx.x * 4 + wave_id()) * 16 * CT + 16 * c + col;
+        bp[c] = reinterpret_cast<const u32x4*>(router + (size_t)min(nn[c], E - 1) * H);
+    }
     // staging: piece u of thread tid is plane u / 2, row (tid + 256 (u % 2)) / 8, 8-block tid % 8
     const uint32_t srow = (uint32_t)tid >> 3, skb = (uint32_t)tid & 7;
     size_t soff[2];
@@ -1273,40 +1283,48 @@ __global__ void __launch_bounds__(256) k_pf_router(const uint16_t* __restrict__ 
     for (int h = 0; h < 2; ++h) soff[h] = (size_t)min(m0 + srow + 32 * h, T - 1) * KB + skb;
     // three register slots: block blk's loads are issued two blocks ahead
     // (slot blk % 3), so each step's wait covers two steps of latency
-    u32x4 ra[3][6], rb[3][2];
+    u32x4 ra[3][6], rb[3][CT][2];
     auto fetch = [&](int slot, uint32_t blk) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < 6; ++u) {
             const u32x4* pl = reinterpret_cast<const u32x4*>(u < 2 ? bhi : u < 4 ? bmid : blo);
             ra[slot][u] = pl[soff[u & 1] + blk * 8];
         }
-        rb[slot][0] = bp[blk * 8 + kq];
-        rb[slot][1] = bp[blk * 8 + 4 + kq];
+#pragma unroll
+        for (int c = 0; c < CT; ++c) {
+            rb[slot][c][0] = bp[c][blk * 8 + kq];
+            rb[slot][c][1] = bp[c][blk * 8 + 4 + kq];
+        }
     };
     auto store = [&](int slot, int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < 6; ++u) sA[buf][u >> 1][(srow + 32 * (u & 1)) * RT_AROW + skb] = ra[slot][u];
     };
-    f4 acc[4];
+    f4 acc[CT][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    // block blk: registers slot P = blk % 3, LDS buffer blk % 2
+    for (int c = 0; c < CT; ++c)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[c][i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    // block blk: registers slot P = (blk - b0) % 3, LDS buffer (blk - b0) % 2
     auto step = [&](auto sc_, uint32_t blk) __attribute__((always_inline)) {
         constexpr int P = decltype(sc_)::value;
-        const uint32_t buf = blk & 1;
+        const uint32_t buf = (blk - b0) & 1;
         fetch((P + 2) % 3, min(blk + 2, NB - 1));
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-            const b8 bq = __builtin_bit_cast(b8, rb[P][s]);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const uint32_t ai = (16 * i + col) * RT_AROW + 4 * s + kq;
                 const b8 xh = __builtin_bit_cast(b8, sA[buf][0][ai]);
                 const b8 xm = __builtin_bit_cast(b8, sA[buf][1][ai]);
                 const b8 xl = __builtin_bit_cast(b8, sA[buf][2][ai]);
-                acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, bq, acc[i], 0, 0, 0);
-                acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xm, bq, acc[i], 0, 0, 0);
-                acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, bq, acc[i], 0, 0, 0);
+#pragma unroll
+                for (int c = 0; c < CT; ++c) {
+                    const b8 bq = __builtin_bit_cast(b8, rb[P][c][s]);
+                    acc[c][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, bq, acc[c][i], 0, 0, 0);
+                    acc[c][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xm, bq, acc[c][i], 0, 0, 0);
+                    acc[c][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, bq, acc[c][i], 0, 0, 0);
+                }
             }
         }
         store((P + 1) % 3, buf ^ 1);
@@ -1315,11 +1333,11 @@ __global__ void __launch_bounds__(256) k_pf_router(const uint16_t* __restrict__ 
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
     using I2 = std::integral_constant<int, 2>;
-    fetch(0, 0);
-    fetch(1, min(1u, NB - 1));
+    fetch(0, b0);
+    fetch(1, min(b0 + 1, NB - 1));
     store(0, 0);
     __syncthreads();
-    uint32_t blk = 0;
+    uint32_t blk = b0;
     for (; blk + 2 < NB; blk += 3) {
         step(I0{}, blk);
         step(I1{}, blk + 1);
@@ -1328,13 +1346,15 @@ __global__ void __launch_bounds__(256) k_pf_router(const uint16_t* __restrict__ 
     if (blk < NB) step(I0{}, blk);
     if (blk + 1 < NB) step(I1{}, blk + 1);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int c = 0; c < CT; ++c)
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-            const uint32_t m = m0 + i * 16 + kq * 4 + rr;
-            if (m >= T) continue;
-            if (nn < E) logits[(size_t)m * E + nn] = acc[i][rr];
-        }
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const uint32_t m = m0 + i * 16 + kq * 4 + rr;
+                if (m >= T) continue;
+                if (nn[c] < E) logits[(size_t)m * E + nn[c]] = acc[c][i][rr];
+            }
 }
 
 // ------------------------------------------------------------ routing
@@ -1348,6 +1368,7 @@ __global__ void __launch_bounds__(256) k_pf_router(const uint16_t* __restrict__ 
 // scattered stores are spread over the launch's workgroups.
 // Places within a group come in arrival order, which only moves rows
 // (every GEMM row is computed on its own).
+template <int NZ>
 __global__ void __launch_bounds__(256) k_pf_route(const float* __restrict__ logits, uint32_t T, uint32_t E,
                                                   uint32_t topk, int norm_topk, uint32_t* __restrict__ ids,
                                                   float* __restrict__ wts, uint32_t* __restrict__ last_ids,
@@ -1384,7 +1405,7 @@ __global__ void __launch_bounds__(256) k_pf_route(const float* __restrict__ logi
     }
     uint32_t my_id;
     float my_p;
-    route_row(logits + (size_t)t * E, E, topk, lane, nullptr, my_id, my_p);
+    route_row<NZ>(logits + (size_t)t * E, E, topk, lane, nullptr, my_id, my_p, (size_t)T * E);
     sgs = wave_sum_dpp(sgs);
     if (lane == 0) sg[t] = sgs;
     float topsum = 0.0f;
@@ -1946,11 +1967,26 @@ void launch_pf_hc_down_finish(const float* part, uint32_t nsplit, uint32_t T, ui
     launch_pf_xprep(d, lowrank, T, lowrank, hi, lo, xs, st);
 }
 
+// The router's grid: x = column blocks of 64 PF_ROUTER_CT experts, z = K
+// chunks.  Wide blocks (the x planes are re-read once per column block)
+// with PF_ROUTER_CHUNKS chunks where every chunk keeps whole 64-wide
+// blocks, at least three (the staging runs two blocks ahead), E % 4 == 0
+// (16-byte partials) and E fills the blocks; else 64-expert blocks over
+// the whole K.
+dim3 pf_router_plan(uint32_t T, uint32_t E, uint32_t H) {
+    const uint32_t NB = H / 64;
+    if (NB % PF_ROUTER_CHUNKS == 0 && NB / PF_ROUTER_CHUNKS >= 3 && E % 4 == 0 && E % (64 * PF_ROUTER_CT) == 0)
+        return dim3(E / (64 * PF_ROUTER_CT), (T + 63) / 64, PF_ROUTER_CHUNKS);
+    return dim3((E + 63) / 64, (T + 63) / 64, 1);
+}
+
 void launch_pf_router(const uint16_t* router, const uint4* bhi, const uint4* bmid, const uint4* blo, float* logits,
                       uint32_t T, uint32_t E, uint32_t H, hipStream_t st) {
     if (H % 64) throw std::runtime_error("router width must be a multiple of 64");
-    if (T)
-        k_pf_router<<<dim3((E + 63) / 64, (T + 63) / 64), CHK_WG, 0, st>>>(router, bhi, bmid, blo, logits, T, E, H);
+    if (!T) return;
+    const dim3 g = pf_router_plan(T, E, H);
+    if (g.z > 1) k_pf_router<PF_ROUTER_CT><<<g, CHK_WG, 0, st>>>(router, bhi, bmid, blo, logits, T, E, H);
+    else k_pf_router<1><<<g, CHK_WG, 0, st>>>(router, bhi, bmid, blo, logits, T, E, H);
 }
 
 void launch_pf_route(const float* logits, uint32_t T, uint32_t E, uint32_t topk, int norm_topk, uint32_t* ids,
@@ -1960,10 +1996,17 @@ void launch_pf_route(const float* logits, uint32_t T, uint32_t E, uint32_t topk,
     if (H % 8 || (uintptr_t)shared_gate % 16) throw std::runtime_error("shared gate needs 16-byte rows");
     if (E > 512 || topk > 64 || topk >= E) throw std::runtime_error("prefill routing: at most 512 experts");
     if (T > cap || (uint64_t)T * (topk + 1) >= (1u << 22)) throw std::runtime_error("prefill grouping: too many entries");
-    if (T)
-        k_pf_route<<<(T + 3) / 4, CHK_WG, 0, st>>>(logits, T, E, topk, norm_topk, ids, wts, last_ids, last_wts,
-                                                   shared_gate, bhi, bmid, blo, sg, H, gcnt, list, pos, cap,
-                                                   shared ? 1u : 0u);
+    if (!T) return;
+    // the router's K-chunk partials, summed in chunk order
+    const uint32_t nz = pf_router_plan(T, E, H).z;
+    if (nz == PF_ROUTER_CHUNKS)
+        k_pf_route<PF_ROUTER_CHUNKS><<<(T + 3) / 4, CHK_WG, 0, st>>>(logits, T, E, topk, norm_topk, ids, wts, last_ids,
+                                                                     last_wts, shared_gate, bhi, bmid, blo, sg, H,
+                                                                     gcnt, list, pos, cap, shared ? 1u : 0u);
+    else
+        k_pf_route<1><<<(T + 3) / 4, CHK_WG, 0, st>>>(logits, T, E, topk, norm_topk, ids, wts, last_ids, last_wts,
+                                                      shared_gate, bhi, bmid, blo, sg, H, gcnt, list, pos, cap,
+                                                      shared ? 1u : 0u);
 }
 
 void launch_pf_group(uint32_t* gcnt, uint32_t T, uint32_t topk, uint32_t E, uint32_t cap, uint32_t* count,
